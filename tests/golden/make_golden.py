@@ -1,0 +1,159 @@
+"""Writes tests/golden/*.json from the REFERENCE's own sampling.cpp and speculator.cpp.
+
+The reference sources are compiled by oracle/Makefile (target `ref`) into oracle/_ref/libref.so
+in this container; this script calls that build and commits only small fixtures: parameters,
+generator seeds, SHA-256 digests of the large input rows, and the reference's outputs.
+
+Input rows are regenerated at test time by oracle/gen_std.cpp (std::mt19937 through
+std::normal_distribution<float>, the generator the reference's own tests use) and by the
+counter formulas documented in oracle/oracle.h, so the fixtures stay a few KB.
+
+Run:  make -C oracle all ref && python tests/golden/make_golden.py
+"""
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "..", "..", "oracle"))
+import oracle as O  # noqa: E402
+
+V_FULL = 262144
+
+
+def sha(a: np.ndarray) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def f32_hex(a) -> list[str]:
+    return [f"{int(x):08x}" for x in np.asarray(a, np.float32).view(np.uint32)]
+
+
+def main() -> None:
+    R = O.Reference()
+    out: dict = {"source": "reference src/sampling.cpp + src/speculator.cpp via oracle/_ref"}
+
+    # ---- seeding (sampling.cpp:85-101) --------------------------------------------------------
+    xs = [0, 1, 2, 3, 0x9E3779B97F4A7C15, 0xFFFFFFFFFFFFFFFF, 12345, 1 << 63]
+    out["splitmix64"] = [[str(x), str(R.splitmix64(x))] for x in xs]
+    seeds = []
+    for has_seed, seed in [(True, 12345), (True, 0), (True, 20260721), (False, 0), (False, 99)]:
+        for pos in [0, 1, 2, 7, 100, 4095, 65535, -1]:
+            seeds.append([int(has_seed), str(seed), pos, str(R.seed_for(has_seed, seed, pos))])
+    out["seed_for"] = seeds
+
+    # ---- validate_sampling (sampling.cpp:61-83) ------------------------------------------------
+    grid = []
+    for t in [0.0, 0.2, -0.1, float("inf"), float("nan"), 1.5]:
+        for p in [1.0, 0.95, 0.0, 1.5, float("nan")]:
+            for k in [0, 1, 64, 256, 257, -1]:
+                for rp in [1.0, 1.1, 0.0, -1.0]:
+                    grid.append([t, p, k, rp, R.validate_sampling(t, p, k, rp)])
+    out["validate_sampling"] = [[repr(a), repr(b), c, repr(d), e] for a, b, c, d, e in grid]
+
+    # ---- repetition penalty (sampling.cpp:103-119) ----------------------------------------------
+    pen = []
+    rng = np.random.default_rng(7)
+    for case, (vocab, nhist, rp, cap, dup) in enumerate([
+        (64, 40, 1.1, 30.0, True), (64, 200, 2.0, 30.0, True), (64, 50, 0.5, 30.0, True),
+        (64, 50, 0.7, 0.0, True), (4096, 4096, 1.1, 30.0, False), (4096, 300, 1.3, 30.0, True),
+    ]):
+        logits = O.gen_mt19937_normal(1000 + case, 0.0, 12.0, vocab)
+        logits = O.softcap(logits, 30.0)
+        if dup:
+            hist = rng.integers(0, vocab + 8, size=nhist, dtype=np.uint32)  # some out of range
+        else:
+            hist = rng.integers(0, vocab, size=nhist, dtype=np.uint32)
+        got = R.apply_repetition_penalty(logits, hist, rp, cap)
+        pen.append({
+            "gen": ["mt19937_normal", 1000 + case, 0.0, 12.0, vocab, "softcap", 30.0],
+            "history": [int(x) for x in hist], "penalty": rp, "softcap": cap,
+            "in_sha256": sha(logits), "out_sha256": sha(got),
+            "out_f32_hex": f32_hex(got) if vocab <= 64 else None,
+        })
+    out["penalty"] = pen
+
+    # ---- sample_token, the reference test's own rows ---------------------------------------------
+    # tests/test_sampling.cpp:238-265: mt19937(20260723), N(0, 6^2), V=262144, 5 configs x 40.
+    lg = O.gen_mt19937_normal(20260723, 0.0, 6.0, V_FULL)
+    cfgs = [(0.2, 0.95, 64, 1), (1.0, 0.90, 8, 2), (0.7, 1.00, 256, 3), (0.5, 1.00, 0, 4),
+            (1.5, 0.99, 1, 5)]
+    rows = []
+    for t, p, k, s in cfgs:
+        ids = []
+        for i in range(40):
+            sd = R.seed_for(True, s, i)
+            ids.append([str(sd), R.sample_token(lg, t, p, k, sd)])
+        rows.append({"t": t, "p": p, "k": k, "seed": s, "draws": ids})
+    out["shortlist_vs_full_sort"] = {"gen": ["mt19937_normal", 20260723, 0.0, 6.0, V_FULL],
+                                     "logits_sha256": sha(lg), "configs": rows}
+
+    # ---- N(0, 4^2) row, softcap 30, greedy then T=.8/k=64/p=.95 -----------
+    z = O.gen_mt19937_normal(1, 0.0, 4.0, V_FULL)
+    zc = O.softcap(z, 30.0)
+    c1 = {"gen": ["mt19937_normal", 1, 0.0, 4.0, V_FULL, "softcap", 30.0],
+          "logits_sha256": sha(zc),
+          "greedy": R.sample_token(zc, 0.0, 1.0, 0, 1),
+          "sampled": []}
+    for i in range(64):
+        sd = R.seed_for(True, 20260801, i)
+        c1["sampled"].append([str(sd), R.sample_token(zc, 0.8, 0.95, 64, sd)])
+    out["config1"] = c1
+
+    # ---- BASELINE config 3/5 style rows: softcapped, penalised, sampled ---------------------------
+    c3 = []
+    for case in range(6):
+        zz = O.softcap(O.gen_mt19937_normal(300 + case, 0.0, 4.0, V_FULL), 30.0)
+        hist = np.random.default_rng(300 + case).integers(0, V_FULL, size=4096, dtype=np.uint32)
+        rp, t, p, k = [(1.1, 0.7, 0.9, 40), (1.1, 0.8, 0.95, 64), (1.3, 1.2, 0.98, 100),
+                       (1.1, 0.5, 0.8, 20), (0.9, 0.7, 0.9, 40), (1.1, 0.0, 1.0, 0)][case]
+        pz = R.apply_repetition_penalty(zz, hist, rp, 30.0)
+        draws = []
+        for i in range(16):
+            sd = R.seed_for(True, 77 + case, i)
+            draws.append([str(sd), R.sample_token(pz, t, p, k, sd)])
+        c3.append({"gen": ["mt19937_normal", 300 + case, 0.0, 4.0, V_FULL, "softcap", 30.0],
+                   "history_gen": ["numpy_default_rng_integers", 300 + case, 4096],
+                   "history_sha256": sha(hist),
+                   "rp": rp, "t": t, "p": p, "k": k, "penalised_sha256": sha(pz),
+                   "draws": draws})
+    out["penalised_sampling"] = c3
+
+    # ---- greedy speculative verify (speculator.cpp:79-198) ------------------------------------
+    ver = []
+    vrng = np.random.default_rng(44)
+    vocab = 4096
+    for case in range(24):
+        nrows = int(vrng.integers(1, 9))
+        ndraft = int(vrng.integers(0, 9))
+        rws = [O.softcap(O.gen_mt19937_normal(5000 + 16 * case + j, 0.0, 4.0, vocab), 30.0)
+               for j in range(nrows)]
+        arg = [int(np.argmax(r)) for r in rws]
+        drafts = []
+        for i in range(ndraft):
+            if i < nrows and vrng.random() < 0.6:
+                drafts.append(arg[i])
+            else:
+                drafts.append(int(vrng.integers(0, vocab)))
+        t, p, k = [(0.0, 1.0, 0), (0.7, 0.9, 40)][case % 2]
+        base = int(vrng.integers(0, 2**63))
+        res = R.verify(drafts, rws, t, p, k, 1.0, base)
+        ver.append({"rows_gen": ["mt19937_normal", 5000 + 16 * case, 0.0, 4.0, vocab, "softcap",
+                                 30.0, nrows],
+                    "drafts": drafts, "t": t, "p": p, "k": k, "base_seed": str(base),
+                    "result": res})
+    out["verify"] = ver
+
+    path = os.path.join(HERE, "sampling_golden.json")
+    with open(path, "w") as f:
+        json.dump(out, f, indent=0, separators=(",", ":"))
+    print("wrote", path, os.path.getsize(path), "bytes")
+
+
+if __name__ == "__main__":
+    main()
