@@ -1,0 +1,325 @@
+"""LM-head + token-selection throughput on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--configs 1,2,3,4,5]
+
+Headline (`value`): BASELINE config 2 -- the INT4 g64 LM head at M=1 (V=262144, d=5376, bf16 h)
+with the softcap and greedy argmax fused, rows/s with every input already resident in HBM.
+One step = one launch over one hidden row. The other BASELINE configs are timed the same way and
+reported under "configs". `roofline` is the dominant kernel (the head pass of config 2): its
+algorithmic bytes per launch divided by its mean launch duration, measured with HIP events on
+the stream the kernel runs on. `cpu_baseline` times the scalar CPU LM head of
+src/cpu_reference.cpp:643-665 (restated in oracle/) on a bounded sample of vocabulary rows.
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+V, D, G, CAP = 262144, 5376, 64, 30.0
+HEAD_BYTES = V * (D // 2 + 4 * D // 64)  # 792,723,456
+PEAK_HBM = 8.0e12
+PEAK_BF16 = 2.5e15
+SEED = 20260801
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes(rows: int, hist_per_row: int = 0) -> int:
+    """Weights once per pass + bf16 h per row + history ids + one id out per row."""
+    return HEAD_BYTES + rows * D * 2 + rows * 4 * hist_per_row + rows * 4
+
+
+def bf16_rne(x):
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def hidden_pool(torch, dev, n, rows, seed):
+    h = bf16_rne(np.random.default_rng(seed).standard_normal((n, rows, D)).astype(np.float32))
+    return torch.from_numpy(h.view(np.int16)).to(dev)
+
+
+class Timer:
+    """Per-launch HIP events on the current stream plus a region pair around the loop."""
+
+    def __init__(self, torch, n):
+        self.torch = torch
+        E = torch.cuda.Event
+        self.starts = [E(enable_timing=True) for _ in range(n)]
+        self.ends = [E(enable_timing=True) for _ in range(n)]
+        self.r0, self.r1 = E(enable_timing=True), E(enable_timing=True)
+
+    def launch_ms(self, n):
+        return [self.starts[i].elapsed_time(self.ends[i]) for i in range(n)]
+
+
+def time_loop(torch, steps, warmup, step_fn, kernel_fn=None):
+    """Runs warmup untimed steps, then `steps` timed ones. Returns (region_s, step launch ms
+    list). kernel_fn(i, start_evt, end_evt) brackets the dominant kernel when given."""
+    for i in range(warmup):
+        step_fn(i, None, None)
+    torch.cuda.synchronize()
+    t = Timer(torch, steps)
+    t.r0.record()
+    wall0 = time.perf_counter()
+    for i in range(steps):
+        step_fn(warmup + i, t.starts[i], t.ends[i])
+    t.r1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    region_s = t.r0.elapsed_time(t.r1) / 1e3
+    return region_s, wall, t.launch_ms(steps)
+
+
+def cpu_baseline(wsb_dev, hidden_rows, n_rows: int):
+    """Scalar single-thread LM head + softcap + greedy argmax over `n_rows` full rows (every
+    vocabulary row each), the oracle's restatement of cpu_reference.cpp:643-665 and
+    sampling.cpp:126-133, on the same weights and hidden states the GPU uses."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    host = wsb_dev.cpu().numpy()
+    wpr, gpr = D // 8, D // G
+    W = host[: V * wpr * 4].view(np.uint32).reshape(V, wpr)
+    S = host[V * wpr * 4: V * wpr * 4 + V * gpr * 2].view(np.uint16).reshape(V, gpr)
+    B = host[V * wpr * 4 + V * gpr * 2:].view(np.uint16).reshape(V, gpr)
+    t0 = time.perf_counter()
+    for m in range(n_rows):
+        hf = (hidden_rows[m].astype(np.uint32) << 16).view(np.float32)
+        lg = O.lm_head(W, S, B, hf, D, softcap=CAP)
+        _ = O.argmax(lg)
+    dt = time.perf_counter() - t0
+    return {"value": n_rows / dt, "unit": "rows/s", "cores": 1, "kind": "port",
+            "sample": f"{n_rows} full rows of BASELINE config 2 (all {V} vocabulary rows, fp32 "
+                      f"scalar dot as cpu_reference.cpp:643-665, softcap, argmax) in {dt:.1f} s, "
+                      f"one thread of {platform.processor() or platform.machine()}, "
+                      f"nproc={os.cpu_count()}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--configs", default="1,2,3,4,5")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=3, help="full rows in the CPU baseline")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device copy (FETCH_SIZE/WRITE_SIZE calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the sharded design is described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    if args.copy_calibration:
+        n = 1 << 30
+        a = torch.empty(n, dtype=torch.uint8, device=dev)
+        b = torch.empty(n, dtype=torch.uint8, device=dev)
+        a.fill_(1)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": n, "launches": 5}))
+        return
+
+    sys.path.insert(0, ROOT)
+    twd = importlib.import_module("turbo-winfare-dense_amd")
+    cfgs = {int(c) for c in args.configs.split(",") if c}
+    cfgs.add(2)
+
+    log(f"generating the synthetic head V={V} d={D} ({HEAD_BYTES / 1e6:.1f} MB) on {dev}")
+    wsb = torch.empty(HEAD_BYTES, dtype=torch.uint8, device=dev)
+    twd.generate_head(wsb, V, D, SEED)
+    head = twd.LMHead(wsb, V, D, CAP)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream().cuda_stream
+    results = {}
+
+    # ---- config 2: M=1, fused head + softcap + greedy argmax -------------------------------------
+    log("config 2: M=1 greedy")
+    hp = hidden_pool(torch, dev, 64, 1, 2)
+    tok = torch.empty(1, dtype=torch.int32, device=dev)
+
+    def step2(i, e0, e1):
+        if e0 is not None:
+            e0.record()
+        head.greedy(hp[i % 64], tokens=tok, stream=stream)
+        if e1 is not None:
+            e1.record()
+
+    region_s, wall, launch_ms = time_loop(torch, args.steps, args.warmup, step2)
+    kern_s = float(np.mean(launch_ms)) / 1e3
+    rows_s = args.steps / region_s
+    bytes2 = algorithmic_bytes(1)
+    results[2] = {"rows_per_s": rows_s, "ms_per_step": region_s * 1e3 / args.steps,
+                  "kernel_us_mean": kern_s * 1e6,
+                  "kernel_us_p10_p90": [float(np.percentile(launch_ms, 10)) * 1e3,
+                                        float(np.percentile(launch_ms, 90)) * 1e3],
+                  "hbm_frac": bytes2 / kern_s / PEAK_HBM}
+    log(f"config 2: {rows_s:.1f} rows/s, kernel {kern_s * 1e6:.1f} us, "
+        f"{bytes2 / kern_s / 1e12:.2f} TB/s")
+
+    # ---- config 1: selection only over one fp32 row (1 MB): greedy, then T=.8 k=64 p=.95 u=.37 ----
+    if 1 in cfgs:
+        log("config 1: select on one 1 MB row")
+        sel = twd.Selector(V, 1)
+        z = np.random.default_rng(1).standard_normal(V).astype(np.float32) * 4.0
+        z = (30.0 * np.tanh(z / 30.0)).astype(np.float32)
+        zr = torch.from_numpy(z).to(dev).view(1, V)
+        t1 = torch.empty(1, dtype=torch.int32, device=dev)
+        p_g = [twd.RowParams(0.0, 1.0, 0, 1.0, 0.0, CAP, 0, 0)]
+        p_s = [twd.RowParams(0.8, 0.95, 64, 1.0, 0.37, CAP, 0, 0)]
+        out = {}
+        for name, pr in (("greedy", p_g), ("sampled", p_s)):
+            def step1(i, e0, e1, pr=pr):
+                if e0 is not None:
+                    e0.record()
+                sel.select(zr, pr, tokens=t1, stream=stream)
+                if e1 is not None:
+                    e1.record()
+            n1 = max(50, args.steps // 4)
+            r_s, _, lm = time_loop(torch, n1, 10, step1)
+            out[name] = {"us_per_row": r_s / n1 * 1e6, "kernel_us_mean": float(np.mean(lm)) * 1e3}
+        results[1] = out
+
+    # ---- config 3: M=1 full chain, rp 1.1 over a 4096-id history, T=.7 k=40 p=.9, 1000 steps --
+    if 3 in cfgs:
+        log("config 3: M=1 sampled chain, 1000 steps")
+        n3 = 1000
+        hp3 = hidden_pool(torch, dev, n3, 1, 3)
+        rng = np.random.default_rng(33)
+        hist = torch.from_numpy(rng.integers(0, V, 4096 + n3 + 20, dtype=np.int64).astype(np.int32)).to(dev)
+        lg3 = torch.empty(1, V, dtype=torch.float32, device=dev)
+        t3 = torch.empty(1, dtype=torch.int32, device=dev)
+        sp = twd.SamplingParams(0.7, 0.9, 40, 1.1, True, 12345)
+        # the history is a sliding 4096-id window; uniforms follow seed_for(sp, position)
+        prm = [[twd.RowParams(0.7, 0.9, 40, 1.1, twd.uniform_from_seed(twd.seed_for(sp, 4096 + i)),
+                              CAP, i, 4096)] for i in range(n3 + 20)]
+
+        def step3(i, e0, e1):
+            if e0 is not None:
+                e0.record()
+            head.sample(hp3[i % n3], prm[i % len(prm)], history=hist, logits=lg3, tokens=t3,
+                        stream=stream)
+            if e1 is not None:
+                e1.record()
+
+        r_s, _, lm = time_loop(torch, n3, 20, step3)
+        b3 = algorithmic_bytes(1, 4096)
+        results[3] = {"rows_per_s": n3 / r_s, "ms_per_step": r_s * 1e3 / n3,
+                      "step_us_mean": float(np.mean(lm)) * 1e3,
+                      "hbm_frac": b3 / (r_s / n3) / PEAK_HBM}
+
+    # ---- config 4: M=5 greedy verify of 4 drafts ------------------------------------------------
+    if 4 in cfgs:
+        log("config 4: M=5 verify")
+        hp4 = hidden_pool(torch, dev, 64, 5, 4)
+        drafts = torch.from_numpy(np.random.default_rng(4).integers(0, V, (64, 4)).astype(np.int32)).to(dev)
+        res4 = torch.zeros(twd.twd.VERIFY_WORDS, dtype=torch.int32, device=dev)
+
+        def step4(i, e0, e1):
+            if e0 is not None:
+                e0.record()
+            head.verify_greedy(hp4[i % 64], drafts[i % 64], result=res4, stream=stream)
+            if e1 is not None:
+                e1.record()
+
+        n4 = max(100, args.steps // 2)
+        r_s, _, lm = time_loop(torch, n4, 20, step4)
+        k4 = float(np.mean(lm)) / 1e3
+        results[4] = {"rows_per_s": 5 * n4 / r_s, "ms_per_step": r_s * 1e3 / n4,
+                      "kernel_us_mean": k4 * 1e6,
+                      "hbm_frac": algorithmic_bytes(5) / k4 / PEAK_HBM}
+
+    # ---- config 5: M=64 rows, each with own T/k/p, rp 1.1 over its own 2048-id history ---------
+    if 5 in cfgs:
+        log("config 5: M=64 sampled, MFMA path")
+        hp5 = hidden_pool(torch, dev, 8, 64, 5)
+        rng = np.random.default_rng(55)
+        hist5 = torch.from_numpy(rng.integers(0, V, 64 * 2048, dtype=np.int64).astype(np.int32)).to(dev)
+        prm5 = [twd.RowParams(float(rng.uniform(0.5, 1.2)), float(rng.uniform(0.8, 0.98)),
+                              int(rng.integers(20, 101)), 1.1,
+                              twd.uniform_from_seed(twd.splitmix64(m)), CAP, 2048 * m, 2048)
+                for m in range(64)]
+        lg5 = torch.empty(64, V, dtype=torch.float32, device=dev)
+        t5 = torch.empty(64, dtype=torch.int32, device=dev)
+        kt0, kt1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+        def step5(i, e0, e1):
+            if e0 is not None:
+                e0.record()
+            head.sample(hp5[i % 8], prm5, history=hist5, logits=lg5, tokens=t5, stream=stream)
+            if e1 is not None:
+                e1.record()
+
+        n5 = max(50, args.steps // 8)
+        r_s, _, lm = time_loop(torch, n5, 10, step5)
+
+        def head5(i, e0, e1):
+            if e0 is not None:
+                e0.record()
+            head.logits(hp5[i % 8], out=lg5, stream=stream)
+            if e1 is not None:
+                e1.record()
+
+        _, _, lmh = time_loop(torch, n5, 5, head5)
+        kh = float(np.mean(lmh)) / 1e3
+        b5 = algorithmic_bytes(64, 2048) + 64 * V * 4  # the fp32 logits are written
+        results[5] = {"rows_per_s": 64 * n5 / r_s, "ms_per_step": r_s * 1e3 / n5,
+                      "head_kernel_us_mean": kh * 1e6,
+                      "hbm_frac_full_step": b5 / (r_s / n5) / PEAK_HBM,
+                      "head_hbm_frac": (HEAD_BYTES + 64 * D * 2 + 64 * V * 4) / kh / PEAK_HBM,
+                      "head_mfma_frac": 2.0 * 64 * V * D / kh / PEAK_BF16}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log(f"cpu baseline: scalar LM head, {args.cpu_rows} full rows")
+        cpu = cpu_baseline(wsb, hp[: args.cpu_rows].cpu().numpy().view(np.uint16).reshape(-1, D),
+                           args.cpu_rows)
+
+    achieved = bytes2 / kern_s
+    line = {
+        "metric": "LM-head+sample rows/s at d=5376,V=262144 INT4; % HBM roofline",
+        "value": results[2]["rows_per_s"],
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": results[2]["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "BASELINE config 2: INT4 g64 LM head M=1, V=262144, d=5376, bf16 h "
+                               "~N(0,1), fused softcap 30 + greedy argmax",
+                   "vocab": V, "d_model": D, "group": G, "rows_per_step": 1,
+                   "weights": "q~U{0..15}, s~U(1e-3,1e-2) bf16, b=-8s (twd_generate_head seed "
+                              f"{SEED})"},
+        "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9,
+                     "unit": "GB/s", "frac": achieved / PEAK_HBM, "traffic": None,
+                     "kernel": "head_kernel<1,1,4,1> (M=1 greedy)",
+                     "bytes_per_launch": bytes2},
+        "cpu_baseline": cpu,
+        "configs": {str(k): results[k] for k in sorted(results)},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

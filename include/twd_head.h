@@ -1,0 +1,173 @@
+/*
+ * twd_head.h -- C-ABI of the MI355X (gfx950) token-selection path for Turbo-WinFare Dense.
+ *
+ * Covers the tied INT4 group-64 affine LM head and everything after it: the tanh logit softcap,
+ * greedy argmax, the sampling chain (repetition penalty, then top-p over the full distribution,
+ * then top-k, then the temperature draw), and greedy speculative verify/accept.
+ *
+ * Conventions (mirroring the reference's C-ABI, include/g4dense/c_api.h:18-49 and
+ * src/c_api.cpp:82-93):
+ *   - every entry point returns 0 on success and a negative TWD_E_* code on failure, never
+ *     throws, and leaves a message for twd_last_error() (thread-local, valid until the next
+ *     call on the same thread);
+ *   - device pointers are plain pointers into HBM; `stream` is a hipStream_t passed as void*
+ *     (NULL = the legacy default stream). Work is enqueued on that stream and the call returns
+ *     without waiting, except where a comment says otherwise;
+ *   - token ids are uint32; logits are fp32 rows of `vocab` entries; hidden states are bf16
+ *     bit patterns (uint16) laid out [rows][d_model].
+ *
+ * A selected id of TWD_TOKEN_DEGENERATE (0xFFFFFFFF) in a token output marks a row whose
+ * distribution the reference rejects: sample_token throws when sum(exp(l - max)) is not
+ * > 0, e.g. NaN logits (src/sampling.cpp:141-147).
+ */
+#ifndef TWD_HEAD_H
+#define TWD_HEAD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TWD_API __attribute__((visibility("default")))
+
+#define TWD_OK 0
+#define TWD_E_INVALID (-1)  /* bad argument (null handle, size out of range, ...) */
+#define TWD_E_HIP (-2)      /* a HIP runtime call failed */
+#define TWD_E_DEGENERATE (-3)
+#define TWD_E_UNSUPPORTED (-4)
+
+#define TWD_TOKEN_DEGENERATE 0xFFFFFFFFu
+#define TWD_MAX_ROWS 64u     /* rows per LM-head call (M) */
+#define TWD_MAX_WANT 256u    /* largest shortlist (top_k, or 256 when top_k == 0) */
+
+/* Per-row selection parameters. temperature/top_p/top_k/repetition_penalty have the meaning of
+ * g4dense::SamplingParams (include/g4dense/sampling.hpp:9-18). `uniform` is the draw in [0,1):
+ * sample_token derives it as next_uniform(seed) (src/sampling.cpp:54-57,190-191); the host
+ * supplies it here (twd_uniform_from_seed computes the reference's value). `softcap` is the
+ * clamp bound handed to apply_repetition_penalty (src/sampling.cpp:103-119). The history is
+ * history_ids[history_offset .. history_offset + history_len). */
+typedef struct {
+    float temperature;
+    float top_p;
+    int32_t top_k;
+    float repetition_penalty;
+    float uniform;
+    float softcap;
+    uint32_t history_offset;
+    uint32_t history_len;
+} twd_row_params;
+
+/* Greedy verify result, mirroring g4dense::SpeculativeEvaluation
+ * (include/g4dense/speculator.hpp:10-17). Written to device memory. */
+typedef struct {
+    uint32_t n_tokens;             /* accepted drafts + 1 correction/bonus token */
+    uint32_t num_accepted;
+    uint32_t total_drafted;
+    uint32_t bonus_token_sampled;
+    uint32_t bonus_token;
+    uint32_t tokens[TWD_MAX_ROWS + 1];
+} twd_verify_result;
+
+typedef struct twd_head twd_head;
+typedef struct twd_selector twd_selector;
+
+/* Message of the last failed call on this thread (g4dense_engine_last_error, c_api.h:47). */
+TWD_API const char* twd_last_error(void);
+
+/* ---- the LM head ---------------------------------------------------------------------------
+ * Uploads the tied head once, as the runner does at load time (src/runner.cpp:423-443): `wsb`
+ * is the container's contiguous LM-head slice [W u32 V x d/8 | S bf16 V x d/64 | B bf16 V x d/64]
+ * (include/g4dense/format.hpp:60-61), element c of row r being nibble c%8 (low first) of word
+ * r*d/8 + c/8 and w = q*s + b (shaders/Common.hlsli:163-222). The head is repacked once into
+ * the HBM layout the kernels stream. group_size must be 64, d_model a multiple of 128, and the
+ * call is synchronous. */
+TWD_API int twd_head_create(const void* wsb_host, uint64_t wsb_bytes, uint32_t vocab,
+                            uint32_t d_model, uint32_t group_size, float softcap,
+                            twd_head** out);
+/* Same, from a copy of the slice that is already in device memory (left untouched). */
+TWD_API int twd_head_create_device(const void* wsb_dev, uint64_t wsb_bytes, uint32_t vocab,
+                                   uint32_t d_model, uint32_t group_size, float softcap,
+                                   void* stream, twd_head** out);
+TWD_API void twd_head_destroy(twd_head* head);
+TWD_API int twd_head_info(const twd_head* head, uint32_t* vocab, uint32_t* d_model,
+                          float* softcap, uint64_t* device_bytes);
+
+/* logits[m][v] = softcap(sum_c w[v][c] * h[m][c]) for m < rows, row stride `vocab`.
+ * Replaces GemvInt4 (rows == 1) / GemmInt4Batch (rows > 1) followed by Softcap
+ * (src/runner.cpp:1958-2022; shaders/GemvInt4.hlsl:31-53, GemmInt4Batch.hlsl:65-143,
+ * Softcap.hlsl:16-30). rows <= TWD_MAX_ROWS. */
+TWD_API int twd_head_logits(twd_head* head, const uint16_t* hidden_bf16, uint32_t rows,
+                            float* logits, void* stream);
+
+/* tokens[m] = greedy sample_token of row m's softcapped logits (strict '>' argmax, lowest index
+ * on ties, -0 == +0), fused into the head pass. `logits` may be NULL (not materialised).
+ * Replaces LMHeadGreedy + ArgmaxReduce (shaders/LMHeadGreedy.hlsl:28-72,
+ * ArgmaxReduce.hlsl:21-61) with the softcap the reference's sample_token sees
+ * (src/sampling.cpp:126-133). */
+TWD_API int twd_head_greedy(twd_head* head, const uint16_t* hidden_bf16, uint32_t rows,
+                            float* logits, uint32_t* tokens, void* stream);
+
+/* The decode-loop order of src/runner.cpp:2314-2326 per row m: softcapped logits, then
+ * apply_repetition_penalty over the row's history (in place on `logits`, when
+ * repetition_penalty != 1), then sample_token with params[m].uniform as the draw.
+ * `params` is a host array of `rows` entries; `history_ids` is device memory. `logits` is
+ * required (rows x vocab). */
+TWD_API int twd_head_sample(twd_head* head, const uint16_t* hidden_bf16, uint32_t rows,
+                            const twd_row_params* params, const uint32_t* history_ids,
+                            float* logits, uint32_t* tokens, void* stream);
+
+/* Greedy speculative verify over rows = n_drafts + 1 target rows [pending, d1..dK]:
+ * SpeculativeCoordinator::evaluate_verification's greedy branch (src/speculator.cpp:95-114,
+ * 183-195) fused into the head pass. `drafts` is device memory (n_drafts ids), `result` a
+ * device twd_verify_result. `logits` may be NULL. */
+TWD_API int twd_head_verify_greedy(twd_head* head, const uint16_t* hidden_bf16, uint32_t rows,
+                                   const uint32_t* drafts, uint32_t n_drafts, float* logits,
+                                   twd_verify_result* result, void* stream);
+
+/* ---- selection over caller-owned logits ----------------------------------------------------
+ * A selector owns the scratch for up to max_rows rows of up to max_vocab entries. */
+TWD_API int twd_selector_create(uint32_t max_vocab, uint32_t max_rows, twd_selector** out);
+TWD_API void twd_selector_destroy(twd_selector* sel);
+
+/* Per row m of `logits` (device, row stride `row_stride` floats): apply_repetition_penalty in
+ * place (src/sampling.cpp:103-119), then sample_token (src/sampling.cpp:121-198) with
+ * params[m].uniform. tokens[m] receives the id (device). */
+TWD_API int twd_select(twd_selector* sel, float* logits, uint32_t vocab, uint32_t rows,
+                       uint64_t row_stride, const twd_row_params* params,
+                       const uint32_t* history_ids, uint32_t* tokens, void* stream);
+
+/* evaluate_verification without draft logits (src/speculator.cpp:79-198 minus :116-167): row i
+ * is sampled with uniform next_uniform(splitmix64(base_seed + i)) and compared with draft i;
+ * the first mismatch emits the target token, a full match adds the bonus row. Greedy params
+ * (temperature <= 0) give the greedy branch. `params` applies to every row and its history
+ * fields are ignored (the reference's verify applies no penalty). */
+TWD_API int twd_verify(twd_selector* sel, const float* logits, uint32_t vocab, uint32_t rows,
+                       uint64_t row_stride, const twd_row_params* params, uint64_t base_seed,
+                       const uint32_t* drafts, uint32_t n_drafts, twd_verify_result* result,
+                       void* stream);
+
+/* ---- the reference's seeding, for callers that keep seeds (src/sampling.cpp:47-101) -------- */
+TWD_API uint64_t twd_splitmix64(uint64_t x);
+TWD_API uint64_t twd_seed_for(int has_seed, uint64_t seed, int position);
+TWD_API float twd_uniform_from_seed(uint64_t seed);
+/* 0 when validate_sampling accepts the parameters, TWD_E_INVALID (with a message) otherwise
+ * (src/sampling.cpp:61-83). */
+TWD_API int twd_validate_sampling(float temperature, float top_p, int32_t top_k,
+                                  float repetition_penalty);
+
+/* ---- synthetic data (benchmarks and tests) -------------------------------------------------
+ * Fills a device buffer with the reference layout [W|S|B] of a V x d head, rows drawn from the
+ * counter formula: W[i] = hi32(splitmix64(seed + 2^60 + i)), u_j = (splitmix64(seed + 2^61 + j)
+ * >> 40) / 2^24, S[j] = bf16_rne(fmaf(9e-3, u_j, 1e-3)), B[j] = -8 * S[j]. */
+TWD_API int twd_generate_head(void* wsb_dev, uint32_t vocab, uint32_t d_model,
+                              uint32_t group_size, uint64_t seed, void* stream);
+/* Bytes of the reference layout for a V x d head with 64-wide groups. */
+TWD_API uint64_t twd_head_bytes(uint32_t vocab, uint32_t d_model, uint32_t group_size);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TWD_HEAD_H */

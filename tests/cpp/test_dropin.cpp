@@ -1,0 +1,137 @@
+// Drives the drop-in C++ API (include/g4dense/sampling.hpp, speculator.hpp) through
+// libtwd_head.so on the GPU, with the assertions of the reference's own tests:
+// tests/test_sampling.cpp:92-265 and tests/test_speculative.cpp:29-77.
+// Prints one line per block and exits nonzero on the first failure.
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <random>
+#include <set>
+#include <vector>
+
+#include "g4dense/sampling.hpp"
+#include "g4dense/speculator.hpp"
+
+using namespace g4dense;
+
+#define CHECK(cond)                                                          \
+    do {                                                                     \
+        if (!(cond)) {                                                       \
+            std::fprintf(stderr, "FAIL %s:%d: %s\n", __FILE__, __LINE__, #cond); \
+            std::exit(1);                                                    \
+        }                                                                    \
+    } while (0)
+
+static bool rejects(const SamplingParams& p) {
+    try {
+        validate_sampling(p);
+        return false;
+    } catch (const G4DenseFormatError&) {
+        return true;
+    }
+}
+
+int main() {
+    // validation matrix
+    CHECK(!rejects(SamplingParams{0.2f, 0.95f, 64, 1.0f, false, 0}));
+    CHECK(!rejects(SamplingParams{0.0f, 1.0f, 0, 1.0f, false, 0}));
+    CHECK(rejects(SamplingParams{-0.1f, 1.0f, 0, 1.0f, false, 0}));
+    CHECK(rejects(SamplingParams{0.2f, 0.0f, 64, 1.0f, false, 0}));
+    CHECK(rejects(SamplingParams{0.2f, 1.5f, 64, 1.0f, false, 0}));
+    CHECK(rejects(SamplingParams{0.2f, 0.95f, 257, 1.0f, false, 0}));
+    CHECK(rejects(SamplingParams{0.2f, 0.95f, -1, 1.0f, false, 0}));
+    CHECK(rejects(SamplingParams{0.2f, 0.95f, 64, 0.0f, false, 0}));
+    CHECK(rejects(SamplingParams{0.7f, 0.9f, 0, 1.0f, false, 0}));
+    CHECK(!rejects(SamplingParams{0.7f, 1.0f, 0, 1.0f, false, 0}));
+    CHECK(!rejects(SamplingParams{0.0f, 0.9f, 0, 1.0f, false, 0}));
+    std::puts("validation ok");
+
+    CHECK(splitmix64(0) == 0xE220A8397B1DCDAFULL);
+    CHECK(splitmix64(3) == 0x1D0B14E4DB018FEDULL);
+    SamplingParams seeded{0.7f, 1.0f, 0, 1.0f, true, 12345};
+    for (int pos = 0; pos < 1000; ++pos) CHECK(seed_for(seeded, pos) != 0);
+    std::puts("seeding ok");
+
+    {
+        std::vector<float> lg{1.0f, 5.0f, 3.0f, 5.0f, 2.0f};
+        SamplingParams greedy{0.0f, 1.0f, 0, 1.0f, false, 0};
+        CHECK(sample_token(lg.data(), 5, greedy, 1) == 1);
+        std::vector<float> one{7.0f};
+        CHECK(sample_token(one.data(), 1, greedy, 1) == 0);
+    }
+    std::puts("greedy ok");
+
+    {
+        std::vector<float> lg{3.0f, 2.5f, 2.0f, 1.5f, -1.0f, -2.0f, -3.0f, -4.0f};
+        SamplingParams p{1.0f, 0.9f, 2, 1.0f, true, 7};
+        std::set<uint32_t> seen;
+        for (int i = 0; i < 300; ++i) seen.insert(sample_token(lg.data(), 8, p, seed_for(p, i)));
+        CHECK(seen.size() == 2 && seen.count(0) && seen.count(1));
+    }
+    std::puts("truncation order ok");
+
+    {
+        std::vector<float> lg{10.0f, -10.0f, 0.0f, 29.999f};
+        std::vector<uint32_t> hist{0, 1, 3, 99999};
+        auto v = lg;
+        apply_repetition_penalty(v.data(), 4, hist, 2.0f, 30.0f);
+        CHECK(std::fabs(v[0] - 5.0f) < 1e-5f && std::fabs(v[1] + 20.0f) < 1e-5f && v[2] == 0.0f);
+        CHECK(v[3] < 15.1f && v[3] > 14.9f);
+        auto w = lg;
+        apply_repetition_penalty(w.data(), 4, hist, 1.0f, 30.0f);
+        CHECK(w == lg);
+        std::vector<float> g{9.0f, 8.0f};
+        SamplingParams greedy{0.0f, 1.0f, 0, 1.0f, false, 0};
+        apply_repetition_penalty(g.data(), 2, {0}, 2.0f, 30.0f);
+        CHECK(sample_token(g.data(), 2, greedy, 1) == 1);
+    }
+    std::puts("penalty ok");
+
+    {
+        std::vector<float> bad(16, -INFINITY);
+        SamplingParams p{0.7f, 1.0f, 0, 1.0f, false, 0};
+        bool threw = false;
+        try {
+            sample_token(bad.data(), 16, p, 1);
+        } catch (const G4DenseFormatError&) {
+            threw = true;
+        }
+        CHECK(threw);
+    }
+    std::puts("degenerate ok");
+
+    {
+        std::mt19937 rng(4242);
+        std::normal_distribution<float> nd(0.0f, 4.0f);
+        std::vector<float> lg(4096);
+        for (auto& x : lg) x = nd(rng);
+        SamplingParams p{0.8f, 0.95f, 64, 1.0f, true, 20260721};
+        std::vector<uint32_t> a, b;
+        for (int i = 0; i < 32; ++i) a.push_back(sample_token(lg.data(), 4096, p, seed_for(p, i)));
+        for (int i = 0; i < 32; ++i) b.push_back(sample_token(lg.data(), 4096, p, seed_for(p, i)));
+        CHECK(a == b);
+    }
+    std::puts("determinism ok");
+
+    {
+        SpeculativeCoordinator spec;
+        const uint32_t V = 1024;
+        SamplingParams greedy;
+        std::vector<std::vector<float>> rows(5, std::vector<float>(V, 0.0f));
+        rows[0][42] = rows[1][100] = rows[2][200] = rows[3][300] = rows[4][400] = 10.0f;
+        std::vector<const float*> ptrs;
+        for (auto& r : rows) ptrs.push_back(r.data());
+        auto e1 = spec.evaluate_verification({42, 100, 200, 300}, ptrs, V, greedy, 12345);
+        CHECK(e1.num_accepted == 4 && e1.bonus_token_sampled && e1.bonus_token == 400);
+        CHECK((e1.accepted_tokens == std::vector<uint32_t>{42, 100, 200, 300, 400}));
+        auto e2 = spec.evaluate_verification({42, 100, 999, 300}, ptrs, V, greedy, 12345);
+        CHECK(e2.num_accepted == 2 && e2.bonus_token == 200);
+        CHECK((e2.accepted_tokens == std::vector<uint32_t>{42, 100, 200}));
+        auto e3 = spec.evaluate_verification({999, 100}, ptrs, V, greedy, 12345);
+        CHECK(e3.num_accepted == 0 && e3.accepted_tokens.size() == 1 && e3.accepted_tokens[0] == 42);
+        CHECK(spec.total_draft_tokens() == 10 && spec.total_accepted_tokens() == 6);
+    }
+    std::puts("speculative verify ok");
+    std::puts("ALL OK");
+    return 0;
+}

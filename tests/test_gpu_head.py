@@ -1,0 +1,256 @@
+"""GPU parity of the fused INT4 LM head (logits, softcap, greedy argmax, greedy verify) against
+the CPU oracle. Logit tolerance follows tests/test_gpu_kernels.cpp of the reference (atol 1e-3,
+rtol 1e-3 for GemvInt4 :345; 1e-3/1e-2 for GemmInt4Batch :584; 1e-4/1e-3 for Softcap :491);
+token ids are compared bit-exactly with the oracle run on the GPU's own logits."""
+import numpy as np
+import pytest
+
+from helpers import allclose_report, bf16_to_f32, hidden_bf16, twd, wsb_bytes
+
+pytestmark = pytest.mark.gpu
+
+D = 5376
+CAP = 30.0
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    assert torch.cuda.is_available(), "GPU test run without a GPU"
+    return torch, torch.device("cuda:0")
+
+
+def make_head(torch_dev, W, S, B, vocab, d, cap):
+    torch, dev = torch_dev
+    buf = torch.from_numpy(wsb_bytes(W, S, B)).to(dev)
+    return twd().LMHead(buf, vocab, d, cap)
+
+
+def to_dev_bf16(torch_dev, h16):
+    torch, dev = torch_dev
+    return torch.from_numpy(np.ascontiguousarray(h16).view(np.int16)).to(dev)
+
+
+def oracle_rows(oracle, W, S, B, hb, cap, rows=None):
+    """Oracle logits [M, rows] for bf16 hidden rows hb [M, d]."""
+    out = []
+    for m in range(hb.shape[0]):
+        hf = bf16_to_f32(hb[m])
+        if rows is None:
+            out.append(oracle.lm_head(W, S, B, hf, hb.shape[1], softcap=cap))
+        else:
+            out.append(np.array([oracle.lm_head(W, S, B, hf, hb.shape[1], row0=int(r), nrows=1,
+                                                softcap=cap)[0] for r in rows], np.float32))
+    return np.stack(out)
+
+
+def test_layout_single_unit(torch_dev, oracle):
+    # one 16x128 unit with structured nibbles: catches a wrong lane/slot mapping at once
+    torch, dev = torch_dev
+    V, d = 16, 128
+    q = (np.arange(V)[:, None] * 7 + np.arange(d)[None, :] * 3) % 16
+    W = np.zeros((V, d // 8), np.uint32)
+    for j in range(8):
+        W |= (q[:, j::8].astype(np.uint32) << (4 * j))
+    S = np.full((V, 2), 0x3F80, np.uint16)  # 1.0
+    B = np.zeros((V, 2), np.uint16)
+    head = make_head(torch_dev, W, S, B, V, d, 0.0)
+    for col in range(0, d, 37):
+        h = np.zeros((1, d), np.uint16)
+        h[0, col] = 0x3F80
+        lg = head.logits(to_dev_bf16(torch_dev, h)).cpu().numpy()[0]
+        assert np.array_equal(lg, q[:, col].astype(np.float32)), col
+    h = hidden_bf16(3, 1, d)
+    lg = head.logits(to_dev_bf16(torch_dev, h)).cpu().numpy()[0]
+    want = q.astype(np.float64) @ bf16_to_f32(h[0]).astype(np.float64)
+    assert np.allclose(lg, want, rtol=1e-5, atol=1e-4)
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 5, 16, 17, 33, 64])
+def test_logits_parity(torch_dev, oracle, M):
+    V = 1000  # not a multiple of 16: the last row tile is partial
+    W, S, B = oracle.gen_lm_head(100 + M, V, D)
+    head = make_head(torch_dev, W, S, B, V, D, CAP)
+    hb = hidden_bf16(M, M, D)
+    got = head.logits(to_dev_bf16(torch_dev, hb)).cpu().numpy()
+    want = oracle_rows(oracle, W, S, B, hb, CAP)
+    ratio, err, i = allclose_report(got, want, 1e-3, 1e-3)
+    print(f"M={M} max|err|={err:.3e} worst tolerance ratio {ratio:.3f}")
+    assert ratio <= 1.0
+
+
+def _reference_test_weights(rows, d, seed):
+    # the value ranges of tests/test_gpu_kernels.cpp:272-275 and :532-535
+    rng = np.random.default_rng(seed)
+    W = rng.integers(0, 2**32, size=(rows, d // 8), dtype=np.uint64).astype(np.uint32)
+    s = (np.abs(rng.uniform(-2, 2, size=(rows, d // 64))) * 0.05 + 0.01).astype(np.float32)
+    b = (rng.uniform(-2, 2, size=(rows, d // 64)) * 0.05).astype(np.float32)
+    S = (s.view(np.uint32) >> 16).astype(np.uint16)
+    B = (b.view(np.uint32) >> 16).astype(np.uint16)
+    return W, S, B, rng
+
+
+@pytest.mark.parametrize("M,rtol", [(1, 1e-3), (5, 1e-2)])
+def test_reference_kernel_test_shape(torch_dev, oracle, M, rtol):
+    W, S, B, rng = _reference_test_weights(256, D, 42 + M)
+    head = make_head(torch_dev, W, S, B, 256, D, 0.0)
+    x = (rng.uniform(-2, 2, size=(M, D)) * 0.1).astype(np.float32)
+    hb = (x.view(np.uint32) >> 16).astype(np.uint16)  # the activations as bf16
+    got = head.logits(to_dev_bf16(torch_dev, hb)).cpu().numpy()
+    want = oracle_rows(oracle, W, S, B, hb, 0.0)
+    ratio, err, _ = allclose_report(got, want, 1e-3, rtol)
+    assert ratio <= 1.0, (ratio, err)
+
+
+def test_softcap_matches_tanh(torch_dev, oracle):
+    V = 2048
+    W, S, B = oracle.gen_lm_head(7, V, D)
+    hb = hidden_bf16(8, 3, D)
+    # scale the activations so the pre-cap logits span the saturated region too
+    hb = (hb.astype(np.uint32) + (5 << 7)).astype(np.uint16)  # x32
+    raw = make_head(torch_dev, W, S, B, V, D, 0.0).logits(to_dev_bf16(torch_dev, hb)).cpu().numpy()
+    capped = make_head(torch_dev, W, S, B, V, D, CAP).logits(to_dev_bf16(torch_dev, hb)).cpu().numpy()
+    assert np.abs(raw).max() > 40.0
+    want = oracle.softcap(raw.reshape(-1), CAP).reshape(raw.shape)
+    ratio, err, _ = allclose_report(capped, want, 1e-4, 1e-3)
+    assert ratio <= 1.0, (ratio, err)
+    assert np.all(np.abs(capped) <= CAP)
+
+
+@pytest.mark.parametrize("M", [1, 3, 5, 16, 20, 64])
+def test_greedy_fused_is_argmax_of_own_logits(torch_dev, oracle, M):
+    torch, dev = torch_dev
+    V = 3000
+    W, S, B = oracle.gen_lm_head(200 + M, V, D)
+    # exact duplicate rows -> exactly tied logits; the lower index must win
+    W[17] = W[2900]
+    S[17] = S[2900]
+    B[17] = B[2900]
+    head = make_head(torch_dev, W, S, B, V, D, CAP)
+    hb = hidden_bf16(300 + M, M, D)
+    h = to_dev_bf16(torch_dev, hb)
+    logits = torch.empty(M, V, dtype=torch.float32, device=dev)
+    tok = head.greedy(h, logits=logits).cpu().numpy().astype(np.int64) & 0xFFFFFFFF
+    lg = logits.cpu().numpy()
+    assert np.array_equal(lg.view(np.uint32), head.logits(h).cpu().numpy().view(np.uint32))
+    for m in range(M):
+        assert tok[m] == oracle.argmax(lg[m])
+    tok2 = head.greedy(h).cpu().numpy().astype(np.int64) & 0xFFFFFFFF  # logits not materialised
+    assert np.array_equal(tok, tok2)
+
+
+def test_greedy_tie_goes_to_lower_index(torch_dev, oracle):
+    V = 64
+    W, S, B = oracle.gen_lm_head(9, V, D)
+    for r in (5, 40, 63):  # three identical rows, all the maximum
+        W[r], S[r], B[r] = W[0] * 0 + 0xFFFFFFFF, S[0] * 0 + 0x3F80, B[0] * 0
+    hb = np.full((1, D), 0x3F80, np.uint16)  # h = 1: rows 5, 40, 63 give 15 * 5376
+    head = make_head(torch_dev, W, S, B, V, D, CAP)
+    assert int(head.greedy(to_dev_bf16(torch_dev, hb)).item()) == 5
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_verify_greedy_fused(torch_dev, oracle, case):
+    torch, dev = torch_dev
+    V = 4096
+    W, S, B = oracle.gen_lm_head(500, V, D)
+    head = make_head(torch_dev, W, S, B, V, D, CAP)
+    rng = np.random.default_rng(case)
+    K = [4, 4, 4, 1, 7, 0, 2, 4][case]
+    rows = K + 1 if case != 6 else K  # case 6: no bonus row
+    hb = hidden_bf16(600 + case, rows, D)
+    h = to_dev_bf16(torch_dev, hb)
+    logits = torch.empty(rows, V, dtype=torch.float32, device=dev)
+    target = head.greedy(h, logits=logits).cpu().numpy().astype(np.int64)
+    drafts = [int(target[i]) if (i < rows and rng.random() < 0.6) else int(rng.integers(0, V))
+              for i in range(K)]
+    if case == 0:
+        drafts = [int(t) for t in target[:K]]  # full accept + bonus
+    d_dev = torch.tensor(drafts if drafts else [0], dtype=torch.int32, device=dev)[:K]
+    res = head.verify_greedy(h, d_dev if K else None, logits=logits)
+    got = twd().decode_verify(res)
+    want = oracle.verify(drafts, list(logits.cpu().numpy()), base_seed=0)
+    for key in ("tokens", "num_accepted", "total_drafted", "bonus_token_sampled"):
+        assert got[key] == want[key], (key, got, want)
+    if want["bonus_token_sampled"]:
+        assert got["bonus_token"] == want["bonus_token"]
+
+
+# ---- the BASELINE geometry: V = 262144, d = 5376 --------------------------------------------------
+
+V_FULL = 262144
+SEED_FULL = 20260801
+
+
+@pytest.fixture(scope="module")
+def full_head(torch_dev):
+    torch, dev = torch_dev
+    t = twd()
+    nbytes = t.head_bytes(V_FULL, D)
+    wsb = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    t.generate_head(wsb, V_FULL, D, SEED_FULL)
+    head = t.LMHead(wsb, V_FULL, D, CAP)
+    yield head, wsb
+    head.close()
+
+
+def test_device_generator_matches_oracle(full_head, oracle):
+    _, wsb = full_head
+    rows = [0, 1, 777, 131071, V_FULL - 1]
+    wpr, gpr = D // 8, D // 64
+    host = wsb.cpu().numpy()
+    Wd = host[: V_FULL * wpr * 4].view(np.uint32).reshape(V_FULL, wpr)
+    Sd = host[V_FULL * wpr * 4: V_FULL * wpr * 4 + V_FULL * gpr * 2].view(np.uint16).reshape(V_FULL, gpr)
+    Bd = host[V_FULL * wpr * 4 + V_FULL * gpr * 2:].view(np.uint16).reshape(V_FULL, gpr)
+    for r in rows:
+        W, S, B = oracle.gen_lm_head(SEED_FULL, 1, D, row0=r)
+        assert np.array_equal(Wd[r], W[0]) and np.array_equal(Sd[r], S[0])
+        assert np.array_equal(Bd[r], B[0])
+
+
+def _check_full_rows(oracle, head_logits, hb, sample_rows):
+    W, S, B = zip(*[oracle.gen_lm_head(SEED_FULL, 1, D, row0=int(r)) for r in sample_rows])
+    W, S, B = np.concatenate(W), np.concatenate(S), np.concatenate(B)
+    for m in range(hb.shape[0]):
+        want = oracle.lm_head(W, S, B, bf16_to_f32(hb[m]), D, softcap=CAP)
+        ratio, err, _ = allclose_report(head_logits[m, sample_rows], want, 1e-3, 1e-3)
+        assert ratio <= 1.0, (m, ratio, err)
+
+
+@pytest.mark.parametrize("M", [1, 5, 64])
+def test_full_geometry_greedy(torch_dev, full_head, oracle, M):
+    # configs 2 (M=1), 4 (M=5) and 5 (M=64): softcap 30, greedy argmax per row
+    torch, dev = torch_dev
+    head, _ = full_head
+    hb = hidden_bf16(1000 + M, M, D)
+    h = to_dev_bf16(torch_dev, hb)
+    logits = torch.empty(M, V_FULL, dtype=torch.float32, device=dev)
+    tok = head.greedy(h, logits=logits).cpu().numpy().astype(np.int64) & 0xFFFFFFFF
+    lg = logits.cpu().numpy()
+    rng = np.random.default_rng(M)
+    sample_rows = np.unique(np.concatenate([rng.integers(0, V_FULL, 96), tok[: min(M, 8)],
+                                            [0, V_FULL - 1]]))
+    _check_full_rows(oracle, lg[: min(M, 4)], hb[: min(M, 4)], sample_rows)
+    for m in range(M):
+        assert tok[m] == oracle.argmax(lg[m])
+    assert np.all(np.abs(lg) <= CAP)
+    assert 1.0 < float(lg.std()) < 4.0  # sd ~ 2.1 by construction (no saturation)
+
+
+def test_full_geometry_verify_config4(torch_dev, full_head, oracle):
+    torch, dev = torch_dev
+    head, _ = full_head
+    rng = np.random.default_rng(4)
+    for trial in range(3):
+        hb = hidden_bf16(4000 + trial, 5, D)
+        h = to_dev_bf16(torch_dev, hb)
+        logits = torch.empty(5, V_FULL, dtype=torch.float32, device=dev)
+        target = head.greedy(h, logits=logits).cpu().numpy().astype(np.int64)
+        drafts, ok = [], True
+        for i in range(4):  # sequential Bernoulli(0.6) matches, else a random id
+            ok = ok and rng.random() < 0.6
+            drafts.append(int(target[i]) if ok else int(rng.integers(0, V_FULL)))
+        res = head.verify_greedy(h, torch.tensor(drafts, dtype=torch.int32, device=dev))
+        got = twd().decode_verify(res)
+        want = oracle.verify(drafts, list(logits.cpu().numpy()), base_seed=0)
+        assert got["tokens"] == want["tokens"] and got["num_accepted"] == want["num_accepted"]

@@ -1,0 +1,232 @@
+"""GPU parity of the selection kernel (repetition penalty, greedy, top-p -> top-k -> temperature
+draw, verify) against the reference's golden ids and the CPU oracle. Token ids and penalised
+logits are compared bit-exactly. For sampled draws the oracle's cut and draw margins are
+printed: a mismatch could only come from libm/summation-order differences within that margin."""
+import hashlib
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from helpers import ROOT, twd
+
+pytestmark = pytest.mark.gpu
+
+V = 262144
+
+
+def sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+@pytest.fixture(scope="module")
+def env():
+    import torch
+    assert torch.cuda.is_available(), "GPU test run without a GPU"
+    t = twd()
+    return torch, torch.device("cuda:0"), t, t.Selector(V, 65)
+
+
+def select_rows(env, rows_np, params, history=None):
+    torch, dev, t, sel = env
+    lg = torch.from_numpy(np.ascontiguousarray(rows_np, np.float32)).to(dev)
+    hist = None if history is None else torch.from_numpy(
+        np.ascontiguousarray(history, np.uint32).view(np.int32)).to(dev)
+    tok = sel.select(lg, params, hist)
+    return (tok.cpu().numpy().astype(np.int64) & 0xFFFFFFFF), lg.cpu().numpy()
+
+
+def rp(t, T, p, k, u, rep=1.0, cap=0.0, off=0, n=0):
+    return t.RowParams(T, p, k, rep, u, cap, off, n)
+
+
+def test_golden_shortlist_full_vocab(env, oracle, golden):
+    # tests/test_sampling.cpp:238-265: 5 configs x 40 seeds at V=262144, ids from the reference
+    torch, dev, t, sel = env
+    g = golden["shortlist_vs_full_sort"]
+    lg = oracle.gen_mt19937_normal(*g["gen"][1:])
+    assert sha(lg) == g["logits_sha256"]
+    for cfg in g["configs"]:
+        draws = cfg["draws"]
+        for start in range(0, len(draws), 20):  # 20 rows per launch
+            chunk = draws[start:start + 20]
+            params = [rp(t, cfg["t"], cfg["p"], cfg["k"], t.uniform_from_seed(int(s)))
+                      for s, _ in chunk]
+            tok, _ = select_rows(env, np.tile(lg, (len(chunk), 1)), params)
+            assert [int(x) for x in tok] == [w for _, w in chunk], cfg
+
+
+def test_golden_config1(env, oracle, golden):
+    torch, dev, t, sel = env
+    c1 = golden["config1"]
+    _, seed, mean, sd, n, _, cap = c1["gen"]
+    z = oracle.softcap(oracle.gen_mt19937_normal(seed, mean, sd, n), cap)
+    assert sha(z) == c1["logits_sha256"]
+    tok, _ = select_rows(env, z[None], [rp(t, 0.0, 1.0, 0, 0.0)])
+    assert int(tok[0]) == c1["greedy"]
+    draws = c1["sampled"]
+    for start in range(0, len(draws), 32):
+        chunk = draws[start:start + 32]
+        params = [rp(t, 0.8, 0.95, 64, t.uniform_from_seed(int(s))) for s, _ in chunk]
+        tok, _ = select_rows(env, np.tile(z, (len(chunk), 1)), params)
+        assert [int(x) for x in tok] == [w for _, w in chunk]
+    # the fixed-uniform pass of BASELINE config 1 (u = 0.37): oracle through the u seam
+    tok, _ = select_rows(env, z[None], [rp(t, 0.8, 0.95, 64, 0.37)])
+    want, diag = oracle.sample_token(z, 0.8, 0.95, 64, u=0.37, diag=True)
+    print("config1 u=0.37 margins", diag["cut_margin"], diag["draw_margin"])
+    assert int(tok[0]) == want
+
+
+def test_golden_penalised_sampling(env, oracle, golden):
+    torch, dev, t, sel = env
+    for case in golden["penalised_sampling"]:
+        _, seed, mean, sd, n, _, cap = case["gen"]
+        z = oracle.softcap(oracle.gen_mt19937_normal(seed, mean, sd, n), cap)
+        hist = np.random.default_rng(case["history_gen"][1]).integers(
+            0, n, size=case["history_gen"][2], dtype=np.uint32)
+        draws = case["draws"]
+        params = [rp(t, case["t"], case["p"], case["k"], t.uniform_from_seed(int(s)), case["rp"],
+                     cap, 0, len(hist)) for s, _ in draws]
+        tok, pen = select_rows(env, np.tile(z, (len(draws), 1)), params, hist)
+        for r in range(len(draws)):
+            assert sha(pen[r]) == case["penalised_sha256"], "penalised logits differ"
+        assert [int(x) for x in tok] == [w for _, w in draws], case["gen"]
+
+
+def test_penalty_bit_exact_random(env, oracle):
+    torch, dev, t, sel = env
+    rng = np.random.default_rng(5)
+    rows, params, hist_all, off = [], [], [], 0
+    for r in range(24):
+        n = int(rng.choice([1, 7, 1000, 16384, 16385, 40000]))
+        row = (rng.standard_normal(n) * rng.uniform(1, 20)).astype(np.float32)
+        row = oracle.softcap(row, 30.0) if r % 2 else row
+        hlen = int(rng.integers(0, 3000))
+        h = rng.integers(0, n + 3, size=hlen, dtype=np.uint32)  # out-of-range ids included
+        if hlen and r % 3 == 0:
+            h[: hlen // 2] = h[0]  # heavy duplicates compound
+        rows.append(row)
+        rep = float(rng.choice([1.1, 0.7, 2.0, 1.0]))
+        cap = float(rng.choice([30.0, 0.0]))
+        params.append((rep, cap, off, hlen, n))
+        hist_all.append(h)
+        off += hlen
+    hist = np.concatenate(hist_all) if off else np.zeros(1, np.uint32)
+    for row, (rep, cap, o, hlen, n), h in zip(rows, params, hist_all):
+        p = rp(t, 0.0, 1.0, 0, 0.0, rep, cap, o, hlen)
+        tok, pen = select_rows(env, row[None], [p], hist)
+        want = oracle.apply_repetition_penalty(row, h, rep, cap)
+        assert np.array_equal(pen[0].view(np.uint32), want.view(np.uint32))
+        assert int(tok[0]) == oracle.argmax(want)
+
+
+@pytest.mark.parametrize("n", [1, 5, 100, 16384, 16385, 50000, V])
+def test_select_random_vs_oracle(env, oracle, n):
+    torch, dev, t, sel = env
+    rng = np.random.default_rng(n)
+    configs = [(0.7, 0.9, 40), (0.8, 0.95, 64), (1.0, 1.0, 0), (0.5, 1.0, 256), (1.2, 0.98, 100),
+               (0.3, 0.5, 1), (2.0, 0.999, 256), (0.0, 1.0, 0), (1.0, 0.9, 8), (0.9, 1.0, 3)]
+    rows, params, want = [], [], []
+    worst = np.inf
+    for i, (T, p, k) in enumerate(configs * 2):
+        row = (rng.standard_normal(n) * rng.uniform(0.5, 8)).astype(np.float32)
+        if i % 4 == 1 and n > 10:
+            row[rng.integers(0, n, size=max(2, n // 50))] = row.max()  # ties at the top
+        if i % 4 == 2 and n > 10:
+            row[:5] = 0.0
+            row[5:10] = -0.0
+        if i % 4 == 3:
+            row = np.round(row)  # many exact ties everywhere
+        u = t.uniform_from_seed(t.splitmix64(1000 * n + i))
+        rows.append(row)
+        params.append(rp(t, T, p, k, u))
+        w, diag = oracle.sample_token(row, T, p, k, u=u, diag=True)
+        want.append(w)
+        worst = min(worst, diag["cut_margin"], diag["draw_margin"])
+    tok, _ = select_rows(env, np.stack(rows), params)
+    print(f"n={n} smallest oracle margin {worst:.3e}")
+    assert [int(x) for x in tok] == want
+
+
+def test_rows_with_own_params_and_histories(env, oracle):
+    # config 5 style: 64 rows, own T/k/p, own 2048-id history with rp 1.1, own uniform
+    torch, dev, t, sel = env
+    rng = np.random.default_rng(55)
+    rows = oracle.softcap((rng.standard_normal((64, V)) * 2.5).astype(np.float32), 30.0)
+    hists = [rng.integers(0, V, 2048, dtype=np.uint32) for _ in range(64)]
+    params = []
+    for m in range(64):
+        params.append(rp(t, float(np.float32(rng.uniform(0.5, 1.2))), float(np.float32(rng.uniform(0.8, 0.98))),
+                         int(rng.integers(20, 101)), t.uniform_from_seed(t.splitmix64(m)), 1.1,
+                         30.0, 2048 * m, 2048))
+    tok, pen = select_rows(env, rows, params, np.concatenate(hists))
+    for m in range(64):
+        want_pen = oracle.apply_repetition_penalty(rows[m], hists[m], 1.1, 30.0)
+        assert np.array_equal(pen[m].view(np.uint32), want_pen.view(np.uint32))
+        p = params[m]
+        assert int(tok[m]) == oracle.sample_token(want_pen, p.temperature, p.top_p, p.top_k,
+                                                  u=p.uniform)
+
+
+def test_degenerate_rows(env):
+    torch, dev, t, sel = env
+    nan_row = np.zeros(5000, np.float32)
+    nan_row[1234] = np.nan
+    inf_row = np.full(5000, -np.inf, np.float32)
+    nan0 = np.full(300, 2.0, np.float32)
+    nan0[0] = np.nan
+    nan_mid = np.arange(300, dtype=np.float32)
+    nan_mid[299] = np.nan
+    tok, _ = select_rows(env, nan_row[None], [rp(t, 0.7, 1.0, 0, 0.5)])
+    assert int(tok[0]) == t.twd.TOKEN_DEGENERATE
+    tok, _ = select_rows(env, inf_row[None], [rp(t, 0.7, 1.0, 0, 0.5)])
+    assert int(tok[0]) == t.twd.TOKEN_DEGENERATE
+    # greedy follows the reference's strict '>' scan: all -inf -> 0, NaN at 0 -> 0, NaN skipped
+    tok, _ = select_rows(env, inf_row[None], [rp(t, 0.0, 1.0, 0, 0.0)])
+    assert int(tok[0]) == 0
+    tok, _ = select_rows(env, nan0[None], [rp(t, 0.0, 1.0, 0, 0.0)])
+    assert int(tok[0]) == 0
+    tok, _ = select_rows(env, nan_mid[None], [rp(t, 0.0, 1.0, 0, 0.0)])
+    assert int(tok[0]) == 298
+
+
+def test_verify_selector_golden(env, oracle, golden):
+    torch, dev, t, sel = env
+    for case in golden["verify"]:
+        _, seed0, mean, sd, vocab, _, cap, nrows = case["rows_gen"]
+        rows = np.stack([oracle.softcap(oracle.gen_mt19937_normal(seed0 + j, mean, sd, vocab), cap)
+                         for j in range(nrows)])
+        lg = torch.from_numpy(rows).to(dev)
+        drafts = case["drafts"]
+        d = torch.tensor(drafts if drafts else [0], dtype=torch.int32, device=dev)[: len(drafts)]
+        p = rp(t, case["t"], case["p"], case["k"], 0.0)
+        got = t.decode_verify(sel.verify(lg, p, int(case["base_seed"]), d if drafts else None))
+        want = case["result"]
+        for key in ("tokens", "num_accepted", "total_drafted", "bonus_token_sampled"):
+            assert got[key] == want[key], (key, got, want)
+
+
+def test_python_mirror_api(env, oracle):
+    torch, dev, t, sel = env
+    lg = torch.tensor([1.0, 5.0, 3.0, 5.0, 2.0], device=dev)
+    assert t.sample_token(lg, 5, t.SamplingParams(), 1) == 1
+    v = torch.tensor([10.0, -10.0, 0.0, 29.999], device=dev)
+    t.apply_repetition_penalty(v, 4, [0, 1, 3, 99999], 2.0, 30.0)
+    want = oracle.apply_repetition_penalty(np.array([10.0, -10.0, 0.0, 29.999], np.float32),
+                                           [0, 1, 3, 99999], 2.0, 30.0)
+    assert np.array_equal(v.cpu().numpy(), want)
+    rows = torch.zeros(5, 1024, device=dev)
+    for i, j in enumerate((42, 100, 200, 300, 400)):
+        rows[i, j] = 10.0
+    sc = t.SpeculativeCoordinator()
+    r = sc.evaluate_verification([42, 100, 999, 300], rows, 1024, t.SamplingParams(), 12345)
+    assert r["tokens"] == [42, 100, 200] and r["num_accepted"] == 2
+
+
+def test_cpp_dropin_program():
+    exe = os.path.join(ROOT, "tests", "cpp", "test_dropin")
+    assert os.path.exists(exe), "build() compiles tests/cpp/test_dropin"
+    res = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    print(res.stdout, res.stderr)
+    assert res.returncode == 0 and "ALL OK" in res.stdout

@@ -1,0 +1,196 @@
+// The reference's C++ sampling/speculator API (include/g4dense/sampling.hpp:20-27,
+// include/g4dense/speculator.hpp:24-31 in the reference checkout) implemented on the GPU.
+//
+// These entry points take HOST logits, as the reference's do. Each call stages the rows into
+// device memory, runs the same selection kernel as the device C-ABI, and copies the result
+// back, so the host-pointer API and twd_select give identical ids on identical logits. A
+// caller that already holds logits in HBM should use twd_select / twd_head_* directly and skip
+// the copies.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "g4dense/sampling.hpp"
+#include "g4dense/speculator.hpp"
+#include "twd_internal.h"
+
+#define G4_API __attribute__((visibility("default")))
+
+namespace {
+
+// Device staging shared by the host-pointer entry points; grown on demand, serialised.
+struct Staging {
+    std::mutex mu;
+    twd_selector* sel = nullptr;
+    uint32_t sel_vocab = 0, sel_rows = 0;
+    float* logits = nullptr;
+    size_t logits_cap = 0;
+    uint32_t* history = nullptr;
+    size_t history_cap = 0;
+    uint32_t* drafts = nullptr;
+    uint32_t* tokens = nullptr;
+    twd_verify_result* vres = nullptr;
+
+    ~Staging() = default;  // released with the process, like the reference's device context
+};
+
+Staging& staging() {
+    static Staging* s = new Staging();
+    return *s;
+}
+
+[[noreturn]] void throw_last(const char* what) {
+    throw g4dense::G4DenseFormatError(std::string(what) + ": " + twd_last_error());
+}
+
+void check_hip(hipError_t e, const char* what) {
+    if (e != hipSuccess)
+        throw g4dense::G4DenseFormatError(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+void ensure(Staging& s, uint32_t vocab, uint32_t rows, size_t history_len) {
+    if (!s.sel || s.sel_vocab < vocab || s.sel_rows < rows) {
+        if (s.sel) twd_selector_destroy(s.sel);
+        s.sel = nullptr;
+        const uint32_t v = std::max(vocab, s.sel_vocab);
+        const uint32_t r = std::max<uint32_t>(std::max(rows, s.sel_rows), 8);
+        if (twd_selector_create(v, r, &s.sel) != TWD_OK) throw_last("twd_selector_create");
+        s.sel_vocab = v;
+        s.sel_rows = r;
+    }
+    const size_t need = static_cast<size_t>(vocab) * rows;
+    if (s.logits_cap < need) {
+        if (s.logits) check_hip(hipFree(s.logits), "hipFree");
+        s.logits = nullptr;
+        check_hip(hipMalloc(&s.logits, need * sizeof(float)), "hipMalloc logits");
+        s.logits_cap = need;
+    }
+    if (s.history_cap < history_len) {
+        if (s.history) check_hip(hipFree(s.history), "hipFree");
+        s.history = nullptr;
+        check_hip(hipMalloc(&s.history, history_len * sizeof(uint32_t)), "hipMalloc history");
+        s.history_cap = history_len;
+    }
+    if (!s.tokens) {
+        check_hip(hipMalloc(&s.tokens, (TWD_MAX_ROWS + 1) * sizeof(uint32_t)), "hipMalloc tokens");
+        check_hip(hipMalloc(&s.drafts, (TWD_MAX_ROWS + 1) * sizeof(uint32_t)), "hipMalloc drafts");
+        check_hip(hipMalloc(&s.vres, sizeof(twd_verify_result)), "hipMalloc verify result");
+    }
+}
+
+twd_row_params row_params(const g4dense::SamplingParams& p, float uniform) {
+    twd_row_params r{};
+    r.temperature = p.temperature;
+    r.top_p = p.top_p;
+    r.top_k = p.top_k;
+    r.repetition_penalty = 1.0f;  // sample_token itself never penalises
+    r.uniform = uniform;
+    r.softcap = 0.0f;
+    r.history_offset = 0;
+    r.history_len = 0;
+    return r;
+}
+
+}  // namespace
+
+namespace g4dense {
+
+G4_API void validate_sampling(const SamplingParams& p) {
+    if (twd_validate_sampling(p.temperature, p.top_p, p.top_k, p.repetition_penalty) != TWD_OK)
+        throw G4DenseFormatError(twd_last_error());
+}
+
+G4_API uint64_t splitmix64(uint64_t x) { return twd_splitmix64(x); }
+
+G4_API uint64_t seed_for(const SamplingParams& p, int position) {
+    return twd_seed_for(p.has_seed ? 1 : 0, p.seed, position);
+}
+
+G4_API void apply_repetition_penalty(float* logits, uint32_t vocab,
+                                     const std::vector<uint32_t>& history, float penalty,
+                                     float softcap) {
+    if (penalty == 1.0f || history.empty() || vocab == 0) return;
+    Staging& s = staging();
+    std::lock_guard<std::mutex> lock(s.mu);
+    ensure(s, vocab, 1, history.size());
+    check_hip(hipMemcpy(s.logits, logits, vocab * sizeof(float), hipMemcpyHostToDevice), "upload");
+    check_hip(hipMemcpy(s.history, history.data(), history.size() * sizeof(uint32_t),
+                        hipMemcpyHostToDevice), "upload history");
+    twd_row_params r{};
+    r.temperature = 0.0f;
+    r.top_p = 1.0f;
+    r.repetition_penalty = penalty;
+    r.softcap = softcap;
+    r.history_len = static_cast<uint32_t>(history.size());
+    if (twd::launch_select(s.sel->scratch, s.logits, vocab, 1, vocab, &r, s.history, nullptr,
+                           nullptr, /*penalty_only=*/true) != TWD_OK)
+        throw_last("apply_repetition_penalty");
+    check_hip(hipMemcpy(logits, s.logits, vocab * sizeof(float), hipMemcpyDeviceToHost), "download");
+}
+
+G4_API uint32_t sample_token(const float* logits, uint32_t vocab, const SamplingParams& p,
+                             uint64_t seed) {
+    if (vocab == 0) throw G4DenseFormatError("sample_token: empty vocabulary");
+    Staging& s = staging();
+    std::lock_guard<std::mutex> lock(s.mu);
+    ensure(s, vocab, 1, 0);
+    check_hip(hipMemcpy(s.logits, logits, vocab * sizeof(float), hipMemcpyHostToDevice), "upload");
+    const twd_row_params r = row_params(p, twd_uniform_from_seed(seed));
+    if (twd_select(s.sel, s.logits, vocab, 1, vocab, &r, nullptr, s.tokens, nullptr) != TWD_OK)
+        throw_last("sample_token");
+    uint32_t tok = 0;
+    check_hip(hipMemcpy(&tok, s.tokens, sizeof(uint32_t), hipMemcpyDeviceToHost), "download");
+    if (tok == TWD_TOKEN_DEGENERATE)
+        throw G4DenseFormatError("sample_token: logit distribution is degenerate");
+    return tok;
+}
+
+G4_API SpeculativeEvaluation SpeculativeCoordinator::evaluate_verification(
+    const std::vector<uint32_t>& draft_tokens, const std::vector<const float*>& target_logits_per_pos,
+    uint32_t vocab_size, const SamplingParams& sampling, uint64_t base_seed,
+    const std::vector<std::vector<float>>& draft_logits) {
+    SpeculativeEvaluation eval{};
+    eval.total_drafted = static_cast<uint32_t>(draft_tokens.size());
+    total_draft_tokens_ += eval.total_drafted;
+    if (draft_tokens.empty() || target_logits_per_pos.empty()) return eval;
+    if (!sampling.is_greedy()) {
+        for (const auto& d : draft_logits)
+            if (!d.empty())
+                throw G4DenseFormatError(
+                    "evaluate_verification: rejection sampling with draft logits is not "
+                    "implemented on the device path");
+    }
+    const size_t k = std::min(draft_tokens.size(), target_logits_per_pos.size());
+    if (k > TWD_MAX_ROWS) throw G4DenseFormatError("evaluate_verification: more than 64 drafts");
+    const uint32_t rows = static_cast<uint32_t>(std::min(target_logits_per_pos.size(), k + 1));
+
+    Staging& s = staging();
+    std::lock_guard<std::mutex> lock(s.mu);
+    ensure(s, vocab_size, rows, 0);
+    for (uint32_t i = 0; i < rows; ++i)
+        check_hip(hipMemcpy(s.logits + static_cast<size_t>(i) * vocab_size, target_logits_per_pos[i],
+                            vocab_size * sizeof(float), hipMemcpyHostToDevice), "upload rows");
+    check_hip(hipMemcpy(s.drafts, draft_tokens.data(), k * sizeof(uint32_t), hipMemcpyHostToDevice),
+              "upload drafts");
+    const twd_row_params r = row_params(sampling, 0.0f);
+    if (twd_verify(s.sel, s.logits, vocab_size, rows, vocab_size, &r, base_seed, s.drafts,
+                   static_cast<uint32_t>(k), s.vres, nullptr) != TWD_OK)
+        throw_last("evaluate_verification");
+    twd_verify_result v{};
+    check_hip(hipMemcpy(&v, s.vres, sizeof(v), hipMemcpyDeviceToHost), "download result");
+    if (v.n_tokens == TWD_TOKEN_DEGENERATE)
+        throw G4DenseFormatError("sample_token: logit distribution is degenerate");
+    eval.accepted_tokens.assign(v.tokens, v.tokens + v.n_tokens);
+    eval.num_accepted = v.num_accepted;
+    eval.bonus_token_sampled = v.bonus_token_sampled != 0;
+    eval.bonus_token = v.bonus_token;
+    total_accepted_tokens_ += eval.num_accepted;
+    eval.acceptance_rate =
+        eval.total_drafted == 0 ? 0.0 : static_cast<double>(eval.num_accepted) / eval.total_drafted;
+    return eval;
+}
+
+}  // namespace g4dense

@@ -1,0 +1,628 @@
+// The tied INT4 group-64 LM head on gfx950: layout repack, synthetic generator, and the fused
+// dequant-GEMM kernel (softcap, greedy argmax and greedy verify in its epilogue).
+//
+// Arithmetic (reference: shaders/Common.hlsli:163-222, src/cpu_reference.cpp:643-665):
+//   logit[m][r] = sum_g s[r][g] * sum_{c in g} q[r][c] * h[m][c]  +  b[r][g] * X[m][g],
+//   X[m][g] = sum_{c in g} h[m][c],  then softcap*tanh(logit/softcap).
+// The inner sums run on MFMA (v_mfma_f32_16x16x32_bf16): nibbles become the exact bf16 values
+// 128 + q with one and-or per pair, h is already bf16, so every product is exact and the
+// accumulation is fp32. The +128 offset is removed per group through X:
+//   sum (128+q) h = 128 X + sum q h  =>  logit += s * acc + (b - 128 s) * X.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <string>
+
+#include "twd_internal.h"
+
+namespace twd {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+enum HeadMode { kModeLogits = 0, kModeGreedy = 1, kModeVerify = 2 };
+
+constexpr int kHeadThreads = 256;
+constexpr int kHeadWaves = 4;
+
+struct HeadArgs {
+    const uint8_t* tiled;
+    uint32_t ntiles, nunits;
+    const uint16_t* h;
+    uint32_t M, d;
+    float softcap;
+    float* logits;
+    uint32_t vocab;
+    uint64_t* partial;  // [TWD_MAX_ROWS][gridDim.x]
+    uint32_t* counter;
+    uint32_t* tokens;
+    const uint32_t* drafts;
+    uint32_t n_drafts;
+    twd_verify_result* vres;
+};
+
+// 8 nibbles of one word -> 8 bf16 values 128+q, in k-slot order [0,4,1,5,2,6,3,7].
+__device__ __forceinline__ bf16x8_t nibbles_to_bf16(uint32_t w) {
+    const uint32_t m = 0x000F000Fu, e = 0x43004300u;
+    u32x4_t p;
+    p.x = (w & m) | e;
+    p.y = ((w >> 4) & m) | e;
+    p.z = ((w >> 8) & m) | e;
+    p.w = ((w >> 12) & m) | e;
+    return __builtin_bit_cast(bf16x8_t, p);
+}
+
+// One 16-byte slice of h (8 bf16 values e0..e7) permuted into the same k-slot order.
+__device__ __forceinline__ u32x4_t permute_h(u32x4_t v) {
+    u32x4_t o;
+    o.x = (v.x & 0xFFFFu) | (v.z << 16);
+    o.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
+    o.z = (v.y & 0xFFFFu) | (v.w << 16);
+    o.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
+    return o;
+}
+
+__device__ __forceinline__ float sum8_bf16(u32x4_t v) {
+    float s = bf16_lo(v.x);
+    s += bf16_hi(v.x);
+    s += bf16_lo(v.y);
+    s += bf16_hi(v.y);
+    s += bf16_lo(v.z);
+    s += bf16_hi(v.z);
+    s += bf16_lo(v.w);
+    s += bf16_hi(v.w);
+    return s;
+}
+
+// Block = 4 waves; wave w owns RT consecutive 16-row tiles. NMT = number of 16-wide m tiles
+// (1 for M <= 16, 4 for M <= 64); NI = accumulator lanes per m tile that can hold a live row
+// (1 when M == 1, else 4).
+template <int NMT, int NI, int RT, int MODE>
+__global__ __launch_bounds__(kHeadThreads) void head_kernel(HeadArgs a) {
+    __shared__ u32x4_t sA[2][NMT][4][64];
+    __shared__ float sX[2][2][NMT * 16];
+    __shared__ uint64_t sRed[kHeadWaves][NMT * 16];
+    __shared__ uint32_t sTok[TWD_MAX_ROWS];
+    __shared__ int sLast;
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const uint32_t tile0 = (blockIdx.x * kHeadWaves + wave) * RT;
+
+    // ---- h staging: chunk U of every live row, permuted, plus its two group sums ----
+    u32x4_t hv[NMT];
+    auto stage_load = [&](uint32_t U) {
+#pragma unroll
+        for (int it = 0; it < NMT; ++it) {
+            const int task = tid + kHeadThreads * it;
+            const int m = task >> 4, c = task & 15;
+            hv[it] = u32x4_t{0u, 0u, 0u, 0u};
+            if (m < static_cast<int>(a.M))
+                hv[it] = *reinterpret_cast<const u32x4_t*>(a.h + static_cast<size_t>(m) * a.d +
+                                                           U * kChunkK + c * 8);
+        }
+    };
+    auto stage_store = [&](int buf) {
+#pragma unroll
+        for (int it = 0; it < NMT; ++it) {
+            const int task = tid + kHeadThreads * it;
+            const int m = task >> 4, c = task & 15;
+            float s = sum8_bf16(hv[it]);
+            s += __shfl_xor(s, 1);
+            s += __shfl_xor(s, 2);
+            s += __shfl_xor(s, 4);
+            sA[buf][m >> 4][c >> 2][(c & 3) * 16 + (m & 15)] = permute_h(hv[it]);
+            if ((c & 7) == 0) sX[buf][c >> 3][m] = s;
+        }
+    };
+
+    // ---- weight units (nibbles + scales/biases) of this wave's tiles ----
+    u32x4_t wq[RT];
+    u32x2_t sq[RT];
+    auto load_unit = [&](uint32_t U, u32x4_t* w, u32x2_t* sb) {
+#pragma unroll
+        for (int j = 0; j < RT; ++j) {
+            const uint32_t T = tile0 + j;
+            if (T < a.ntiles) {
+                const uint8_t* base =
+                    a.tiled + (static_cast<size_t>(T) * a.nunits + U) * kUnitBytes;
+                w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(base) + lane);
+                sb[j] = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x2_t*>(base + kUnitNibbleBytes) + (lane & 15));
+            } else {
+                w[j] = u32x4_t{0u, 0u, 0u, 0u};
+                sb[j] = u32x2_t{0u, 0u};
+            }
+        }
+    };
+
+    f32x4_t tot[RT][NMT];
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt) tot[j][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    stage_load(0);
+    stage_store(0);
+    load_unit(0, wq, sq);
+
+    for (uint32_t U = 0; U < a.nunits; ++U) {
+        __syncthreads();
+        const int buf = U & 1;
+        const bool more = (U + 1) < a.nunits;
+        u32x4_t wn[RT];
+        u32x2_t sn[RT];
+        if (more) {
+            stage_load(U + 1);
+            load_unit(U + 1, wn, sn);
+        }
+
+        bf16x8_t av[NMT][4];
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) av[mt][t] = __builtin_bit_cast(bf16x8_t, sA[buf][mt][t][lane]);
+        f32x4_t xv[2][NMT];
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+            for (int mt = 0; mt < NMT; ++mt)
+                xv[g][mt] = *reinterpret_cast<const f32x4_t*>(&sX[buf][g][mt * 16 + 4 * (lane >> 4)]);
+
+#pragma unroll
+        for (int j = 0; j < RT; ++j) {
+            bf16x8_t bv[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) bv[t] = nibbles_to_bf16(wq[j][t]);
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                const float s = g == 0 ? bf16_lo(sq[j].x) : bf16_hi(sq[j].x);
+                const float b = g == 0 ? bf16_lo(sq[j].y) : bf16_hi(sq[j].y);
+                const float tb = fmaf(-128.0f, s, b);
+#pragma unroll
+                for (int mt = 0; mt < NMT; ++mt) {
+                    f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt][2 * g], bv[2 * g], acc,
+                                                                  0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt][2 * g + 1],
+                                                                  bv[2 * g + 1], acc, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < NI; ++i)
+                        tot[j][mt][i] = fmaf(s, acc[i], fmaf(tb, xv[g][mt][i], tot[j][mt][i]));
+                }
+            }
+        }
+
+        if (more) {
+            stage_store(buf ^ 1);
+#pragma unroll
+            for (int j = 0; j < RT; ++j) {
+                wq[j] = wn[j];
+                sq[j] = sn[j];
+            }
+        }
+    }
+
+    // ---- epilogue: softcap, store, greedy ranks ----
+    uint64_t best[NMT][NI];
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+        for (int i = 0; i < NI; ++i) best[mt][i] = 0;
+
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+        const uint32_t r = (tile0 + j) * kTileRows + (lane & 15);
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const uint32_t m = mt * 16 + 4 * (lane >> 4) + i;
+                float v = tot[j][mt][i];
+                if (a.softcap > 0.0f) v = a.softcap * tanhf(v / a.softcap);
+                const bool live = (m < a.M) && (r < a.vocab);
+                if (live && a.logits) a.logits[static_cast<size_t>(m) * a.vocab + r] = v;
+                if (MODE != kModeLogits) {
+                    const uint64_t k = live ? rank_key(v, r) : 0ull;
+                    best[mt][i] = k > best[mt][i] ? k : best[mt][i];
+                }
+            }
+    }
+    if (MODE == kModeLogits) return;
+
+    // rows sharing m are the 16 lanes with the same lane>>4
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            uint64_t k = best[mt][i];
+#pragma unroll
+            for (int msk = 1; msk < 16; msk <<= 1) {
+                const uint64_t o = shfl_xor_u64(k, msk);
+                k = o > k ? o : k;
+            }
+            const uint32_t m = mt * 16 + 4 * (lane >> 4) + i;
+            if ((lane & 15) == 0) sRed[wave][m] = k;
+        }
+    __syncthreads();
+    const uint32_t nb = gridDim.x;
+    if (tid < NMT * 16) {
+        uint64_t k = sRed[0][tid];
+#pragma unroll
+        for (int w = 1; w < kHeadWaves; ++w) k = sRed[w][tid] > k ? sRed[w][tid] : k;
+        if (static_cast<uint32_t>(tid) < a.M) a.partial[static_cast<size_t>(tid) * nb + blockIdx.x] = k;
+    }
+
+    // ---- the last block to finish reduces every block's ranks ----
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) sLast = (atomicAdd(a.counter, 1u) == nb - 1);
+    __syncthreads();
+    if (!sLast) return;
+    __threadfence();
+    for (uint32_t m = wave; m < a.M; m += kHeadWaves) {
+        uint64_t k = 0;
+        for (uint32_t b = lane; b < nb; b += 64) {
+            const uint64_t o = __builtin_nontemporal_load(a.partial + static_cast<size_t>(m) * nb + b);
+            k = o > k ? o : k;
+        }
+        k = wave_max_u64(k);
+        if (lane == 0) {
+            const uint32_t tok = rank_index(k);
+            sTok[m] = tok;
+            if (a.tokens) a.tokens[m] = tok;
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        *a.counter = 0u;  // ready for the next launch on this head
+        if (MODE == kModeVerify) {
+            // speculator.cpp:91-114 and :183-195, greedy branch
+            twd_verify_result* v = a.vres;
+            const uint32_t nd = a.n_drafts, rows = a.M;
+            uint32_t n = 0, acc = 0, bonus = 0, sampled = 0;
+            if (nd != 0 && rows != 0) {
+                const uint32_t k = nd < rows ? nd : rows;
+                bool rejected = false;
+                for (uint32_t i = 0; i < k; ++i) {
+                    const uint32_t t = sTok[i];
+                    if (a.drafts[i] == t) {
+                        v->tokens[n++] = t;
+                        ++acc;
+                    } else {
+                        bonus = t;
+                        sampled = 1;
+                        v->tokens[n++] = t;
+                        rejected = true;
+                        break;
+                    }
+                }
+                if (!rejected && rows > k) {
+                    bonus = sTok[k];
+                    sampled = 1;
+                    v->tokens[n++] = bonus;
+                }
+            }
+            v->n_tokens = n;
+            v->num_accepted = acc;
+            v->total_drafted = nd;
+            v->bonus_token_sampled = sampled;
+            v->bonus_token = bonus;
+        }
+    }
+}
+
+// ---- layout repack: reference [W|S|B] -> units ----------------------------------------------
+__global__ void repack_kernel(const uint32_t* __restrict__ W, const uint16_t* __restrict__ S,
+                              const uint16_t* __restrict__ B, uint32_t vocab, uint32_t d,
+                              uint32_t ntiles, uint32_t nunits, uint8_t* __restrict__ out) {
+    const uint64_t total = static_cast<uint64_t>(ntiles) * nunits * 64;
+    const uint32_t wpr = d / 8, gpr = d / kGroup;
+    for (uint64_t g = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; g < total;
+         g += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+        const uint32_t lane = static_cast<uint32_t>(g & 63);
+        const uint64_t unit = g >> 6;
+        const uint32_t U = static_cast<uint32_t>(unit % nunits);
+        const uint32_t T = static_cast<uint32_t>(unit / nunits);
+        const uint32_t r = T * kTileRows + (lane & 15), kg = lane >> 4;
+        u32x4_t w = u32x4_t{0u, 0u, 0u, 0u};
+        if (r < vocab) {
+            const uint32_t* row = W + static_cast<size_t>(r) * wpr + 16 * U + kg;
+            w = u32x4_t{row[0], row[4], row[8], row[12]};
+        }
+        uint8_t* ub = out + unit * kUnitBytes;
+        *reinterpret_cast<u32x4_t*>(ub + lane * 16) = w;
+        if (lane < 16) {
+            u32x2_t sb = u32x2_t{0u, 0u};
+            if (r < vocab) {
+                const uint16_t* sr = S + static_cast<size_t>(r) * gpr + 2 * U;
+                const uint16_t* br = B + static_cast<size_t>(r) * gpr + 2 * U;
+                sb.x = static_cast<uint32_t>(sr[0]) | (static_cast<uint32_t>(sr[1]) << 16);
+                sb.y = static_cast<uint32_t>(br[0]) | (static_cast<uint32_t>(br[1]) << 16);
+            }
+            *reinterpret_cast<u32x2_t*>(ub + kUnitNibbleBytes + lane * 8) = sb;
+        }
+    }
+}
+
+// ---- synthetic head in the reference layout (formula in twd_head.h) ---------------------------
+__device__ __forceinline__ uint64_t splitmix64_dev(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ULL;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBULL;
+    return x ^ (x >> 31);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+__global__ void generate_kernel(uint32_t* __restrict__ W, uint16_t* __restrict__ S,
+                                uint16_t* __restrict__ B, uint64_t n_words, uint64_t n_groups,
+                                uint64_t seed) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n_words;
+         i += stride)
+        W[i] = static_cast<uint32_t>(splitmix64_dev(seed + 0x1000000000000000ULL + i) >> 32);
+    for (uint64_t j = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; j < n_groups;
+         j += stride) {
+        const float u = static_cast<float>(splitmix64_dev(seed + 0x2000000000000000ULL + j) >> 40) *
+                        (1.0f / 16777216.0f);
+        const uint16_t s = f32_to_bf16_rne(fmaf(9e-3f, u, 1e-3f));
+        S[j] = s;
+        B[j] = f32_to_bf16_rne(-8.0f * __uint_as_float(static_cast<uint32_t>(s) << 16));
+    }
+}
+
+}  // namespace twd
+
+// =================================================================================================
+// C-ABI: the head object
+// =================================================================================================
+
+using namespace twd;
+
+struct twd_head {
+    uint32_t vocab = 0, d = 0, ntiles = 0, nunits = 0;
+    float softcap = 0.f;
+    uint8_t* tiled = nullptr;
+    uint64_t tiled_bytes = 0;
+    uint64_t* partial = nullptr;  // [TWD_MAX_ROWS][max blocks]
+    uint32_t* counter = nullptr;
+    uint32_t max_blocks = 0;
+    twd_selector* sel = nullptr;
+};
+
+namespace {
+
+constexpr int kRT1 = 4;  // row tiles per wave, M <= 16
+constexpr int kRT4 = 2;  // row tiles per wave, M <= 64
+
+uint32_t blocks_for(uint32_t ntiles, int rt) {
+    const uint32_t per = kHeadWaves * rt;
+    return (ntiles + per - 1) / per;
+}
+
+int check_geometry(uint32_t vocab, uint32_t d, uint32_t group) {
+    if (group != kGroup) return fail(TWD_E_UNSUPPORTED, "group_size must be 64");
+    if (vocab == 0) return fail(TWD_E_INVALID, "vocab must be > 0");
+    if (d == 0 || d % kChunkK != 0) return fail(TWD_E_UNSUPPORTED, "d_model must be a positive multiple of 128");
+    return TWD_OK;
+}
+
+int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
+    twd_head* h = new twd_head();
+    h->vocab = vocab;
+    h->d = d;
+    h->softcap = softcap;
+    h->ntiles = (vocab + kTileRows - 1) / kTileRows;
+    h->nunits = d / kChunkK;
+    h->tiled_bytes = static_cast<uint64_t>(h->ntiles) * h->nunits * kUnitBytes;
+    h->max_blocks = std::max(blocks_for(h->ntiles, kRT1), blocks_for(h->ntiles, kRT4));
+    hipError_t e = hipMalloc(&h->tiled, h->tiled_bytes);
+    if (e == hipSuccess) e = hipMalloc(&h->partial, sizeof(uint64_t) * TWD_MAX_ROWS * h->max_blocks);
+    if (e == hipSuccess) e = hipMalloc(&h->counter, sizeof(uint32_t) * 4);
+    if (e == hipSuccess) e = hipMemset(h->counter, 0, sizeof(uint32_t) * 4);
+    if (e != hipSuccess) {
+        twd_head_destroy(h);
+        return hip_fail(e, "allocating the LM head");
+    }
+    if (twd_selector_create(vocab, TWD_MAX_ROWS, &h->sel) != TWD_OK) {
+        twd_head_destroy(h);
+        return TWD_E_HIP;
+    }
+    *out = h;
+    return TWD_OK;
+}
+
+int head_repack(twd_head* h, const uint8_t* wsb_dev, hipStream_t stream) {
+    const uint64_t w_bytes = static_cast<uint64_t>(h->vocab) * (h->d / 8) * 4;
+    const uint64_t s_bytes = static_cast<uint64_t>(h->vocab) * (h->d / kGroup) * 2;
+    const uint32_t* W = reinterpret_cast<const uint32_t*>(wsb_dev);
+    const uint16_t* S = reinterpret_cast<const uint16_t*>(wsb_dev + w_bytes);
+    const uint16_t* B = reinterpret_cast<const uint16_t*>(wsb_dev + w_bytes + s_bytes);
+    const uint64_t work = static_cast<uint64_t>(h->ntiles) * h->nunits * 64;
+    const uint32_t grid = static_cast<uint32_t>(std::min<uint64_t>((work + 255) / 256, 1u << 16));
+    repack_kernel<<<grid, 256, 0, stream>>>(W, S, B, h->vocab, h->d, h->ntiles, h->nunits, h->tiled);
+    TWD_HIP(hipGetLastError());
+    return TWD_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <int MODE>
+int launch_head(twd_head* h, const uint16_t* hidden, uint32_t rows, float* logits,
+                uint32_t* tokens, const uint32_t* drafts, uint32_t n_drafts,
+                twd_verify_result* vres, hipStream_t stream) {
+    if (!h) return fail(TWD_E_INVALID, "null head");
+    if (!hidden || !aligned16(hidden)) return fail(TWD_E_INVALID, "hidden must be a 16-byte aligned device pointer");
+    if (rows == 0 || rows > TWD_MAX_ROWS) return fail(TWD_E_INVALID, "rows must be in 1..64");
+    HeadArgs a{};
+    a.tiled = h->tiled;
+    a.ntiles = h->ntiles;
+    a.nunits = h->nunits;
+    a.h = hidden;
+    a.M = rows;
+    a.d = h->d;
+    a.softcap = h->softcap;
+    a.logits = logits;
+    a.vocab = h->vocab;
+    a.partial = h->partial;
+    a.counter = h->counter;
+    a.tokens = tokens;
+    a.drafts = drafts;
+    a.n_drafts = n_drafts;
+    a.vres = vres;
+    if (rows == 1) {
+        head_kernel<1, 1, kRT1, MODE><<<blocks_for(h->ntiles, kRT1), kHeadThreads, 0, stream>>>(a);
+    } else if (rows <= 16) {
+        head_kernel<1, 4, kRT1, MODE><<<blocks_for(h->ntiles, kRT1), kHeadThreads, 0, stream>>>(a);
+    } else {
+        head_kernel<4, 4, kRT4, MODE><<<blocks_for(h->ntiles, kRT4), kHeadThreads, 0, stream>>>(a);
+    }
+    TWD_HIP(hipGetLastError());
+    return TWD_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+TWD_API uint64_t twd_head_bytes(uint32_t vocab, uint32_t d_model, uint32_t group_size) {
+    if (group_size == 0) return 0;
+    return static_cast<uint64_t>(vocab) * (d_model / 8) * 4 +
+           2ull * static_cast<uint64_t>(vocab) * (d_model / group_size) * 2;
+}
+
+TWD_API int twd_head_create_device(const void* wsb_dev, uint64_t wsb_bytes, uint32_t vocab,
+                                   uint32_t d_model, uint32_t group_size, float softcap,
+                                   void* stream, twd_head** out) {
+    clear_error();
+    if (!out || !wsb_dev) return fail(TWD_E_INVALID, "null argument");
+    *out = nullptr;
+    int rc = check_geometry(vocab, d_model, group_size);
+    if (rc) return rc;
+    if (wsb_bytes < twd_head_bytes(vocab, d_model, group_size))
+        return fail(TWD_E_INVALID, "wsb_bytes is smaller than the [W|S|B] slice of this geometry");
+    twd_head* h = nullptr;
+    if ((rc = head_alloc(vocab, d_model, softcap, &h))) return rc;
+    if ((rc = head_repack(h, static_cast<const uint8_t*>(wsb_dev), static_cast<hipStream_t>(stream)))) {
+        twd_head_destroy(h);
+        return rc;
+    }
+    hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) {
+        twd_head_destroy(h);
+        return hip_fail(e, "repacking the LM head");
+    }
+    *out = h;
+    return TWD_OK;
+}
+
+TWD_API int twd_head_create(const void* wsb_host, uint64_t wsb_bytes, uint32_t vocab,
+                            uint32_t d_model, uint32_t group_size, float softcap,
+                            twd_head** out) {
+    clear_error();
+    if (!out || !wsb_host) return fail(TWD_E_INVALID, "null argument");
+    *out = nullptr;
+    int rc = check_geometry(vocab, d_model, group_size);
+    if (rc) return rc;
+    const uint64_t need = twd_head_bytes(vocab, d_model, group_size);
+    if (wsb_bytes < need)
+        return fail(TWD_E_INVALID, "wsb_bytes is smaller than the [W|S|B] slice of this geometry");
+    void* staging = nullptr;
+    TWD_HIP(hipMalloc(&staging, need));
+    hipError_t e = hipMemcpy(staging, wsb_host, need, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(staging);
+        return hip_fail(e, "uploading the LM head");
+    }
+    rc = twd_head_create_device(staging, need, vocab, d_model, group_size, softcap, nullptr, out);
+    (void)hipFree(staging);
+    return rc;
+}
+
+TWD_API void twd_head_destroy(twd_head* h) {
+    if (!h) return;
+    if (h->tiled) (void)hipFree(h->tiled);
+    if (h->partial) (void)hipFree(h->partial);
+    if (h->counter) (void)hipFree(h->counter);
+    if (h->sel) twd_selector_destroy(h->sel);
+    delete h;
+}
+
+TWD_API int twd_head_info(const twd_head* h, uint32_t* vocab, uint32_t* d_model, float* softcap,
+                          uint64_t* device_bytes) {
+    clear_error();
+    if (!h) return fail(TWD_E_INVALID, "null head");
+    if (vocab) *vocab = h->vocab;
+    if (d_model) *d_model = h->d;
+    if (softcap) *softcap = h->softcap;
+    if (device_bytes) *device_bytes = h->tiled_bytes;
+    return TWD_OK;
+}
+
+TWD_API int twd_head_logits(twd_head* h, const uint16_t* hidden, uint32_t rows, float* logits,
+                            void* stream) {
+    clear_error();
+    if (!logits) return fail(TWD_E_INVALID, "null logits");
+    return launch_head<kModeLogits>(h, hidden, rows, logits, nullptr, nullptr, 0, nullptr,
+                                    static_cast<hipStream_t>(stream));
+}
+
+TWD_API int twd_head_greedy(twd_head* h, const uint16_t* hidden, uint32_t rows, float* logits,
+                            uint32_t* tokens, void* stream) {
+    clear_error();
+    if (!tokens) return fail(TWD_E_INVALID, "null tokens");
+    return launch_head<kModeGreedy>(h, hidden, rows, logits, tokens, nullptr, 0, nullptr,
+                                    static_cast<hipStream_t>(stream));
+}
+
+TWD_API int twd_head_verify_greedy(twd_head* h, const uint16_t* hidden, uint32_t rows,
+                                   const uint32_t* drafts, uint32_t n_drafts, float* logits,
+                                   twd_verify_result* result, void* stream) {
+    clear_error();
+    if (!result) return fail(TWD_E_INVALID, "null result");
+    if (n_drafts > 0 && !drafts) return fail(TWD_E_INVALID, "null drafts");
+    if (n_drafts > TWD_MAX_ROWS) return fail(TWD_E_INVALID, "n_drafts must be <= 64");
+    return launch_head<kModeVerify>(h, hidden, rows, logits, nullptr, drafts, n_drafts, result,
+                                    static_cast<hipStream_t>(stream));
+}
+
+TWD_API int twd_head_sample(twd_head* h, const uint16_t* hidden, uint32_t rows,
+                            const twd_row_params* params, const uint32_t* history, float* logits,
+                            uint32_t* tokens, void* stream) {
+    clear_error();
+    if (!h) return fail(TWD_E_INVALID, "null head");
+    if (!logits || !tokens || !params) return fail(TWD_E_INVALID, "null logits, tokens or params");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    int rc = launch_head<kModeLogits>(h, hidden, rows, logits, nullptr, nullptr, 0, nullptr, s);
+    if (rc) return rc;
+    return launch_select(h->sel->scratch, logits, h->vocab, rows, h->vocab, params, history,
+                         tokens, s);
+}
+
+TWD_API int twd_generate_head(void* wsb_dev, uint32_t vocab, uint32_t d_model,
+                              uint32_t group_size, uint64_t seed, void* stream) {
+    clear_error();
+    if (!wsb_dev) return fail(TWD_E_INVALID, "null buffer");
+    if (group_size == 0 || d_model % group_size != 0 || d_model % 8 != 0)
+        return fail(TWD_E_INVALID, "d_model must be a multiple of 8 and of group_size");
+    const uint64_t n_words = static_cast<uint64_t>(vocab) * (d_model / 8);
+    const uint64_t n_groups = static_cast<uint64_t>(vocab) * (d_model / group_size);
+    uint32_t* W = static_cast<uint32_t*>(wsb_dev);
+    uint16_t* S = reinterpret_cast<uint16_t*>(W + n_words);
+    uint16_t* B = S + n_groups;
+    const uint32_t grid = static_cast<uint32_t>(std::min<uint64_t>((n_words + 255) / 256, 1u << 16));
+    generate_kernel<<<std::max(grid, 1u), 256, 0, static_cast<hipStream_t>(stream)>>>(W, S, B, n_words, n_groups, seed);
+    TWD_HIP(hipGetLastError());
+    return TWD_OK;
+}
+
+}  // extern "C"

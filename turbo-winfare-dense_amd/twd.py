@@ -1,0 +1,386 @@
+"""Python binding of libtwd_head.so, mirroring the reference's sampling/speculator interface.
+
+Names, argument meaning and error behaviour follow include/g4dense/sampling.hpp:9-27 and
+include/g4dense/speculator.hpp:10-43 of the reference (SamplingParams, validate_sampling,
+splitmix64, seed_for, apply_repetition_penalty, sample_token,
+SpeculativeCoordinator.evaluate_verification), plus LMHead for the fused INT4 head.
+
+Device memory and streams come from PyTorch (ROCm); every computation runs in the HIP library.
+If the library is missing this module raises at import -- there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import dataclasses
+import os
+from typing import Sequence
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtwd_head.so")
+
+TWD_OK, TWD_E_INVALID, TWD_E_HIP, TWD_E_DEGENERATE, TWD_E_UNSUPPORTED = 0, -1, -2, -3, -4
+TOKEN_DEGENERATE = 0xFFFFFFFF
+MAX_ROWS = 64
+MAX_WANT = 256
+
+
+class G4DenseFormatError(RuntimeError):
+    """The reference's G4DenseFormatError (include/g4dense/format.hpp:249-253)."""
+
+
+class TwdError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+class RowParams(C.Structure):
+    _fields_ = [
+        ("temperature", C.c_float),
+        ("top_p", C.c_float),
+        ("top_k", C.c_int32),
+        ("repetition_penalty", C.c_float),
+        ("uniform", C.c_float),
+        ("softcap", C.c_float),
+        ("history_offset", C.c_uint32),
+        ("history_len", C.c_uint32),
+    ]
+
+
+class VerifyResult(C.Structure):
+    _fields_ = [
+        ("n_tokens", C.c_uint32),
+        ("num_accepted", C.c_uint32),
+        ("total_drafted", C.c_uint32),
+        ("bonus_token_sampled", C.c_uint32),
+        ("bonus_token", C.c_uint32),
+        ("tokens", C.c_uint32 * (MAX_ROWS + 1)),
+    ]
+
+
+VERIFY_WORDS = C.sizeof(VerifyResult) // 4
+
+_vp, _u32, _u64, _f32, _i32 = C.c_void_p, C.c_uint32, C.c_uint64, C.c_float, C.c_int32
+
+_SIGS = {
+    "twd_last_error": (C.c_char_p, []),
+    "twd_head_create": (C.c_int, [_vp, _u64, _u32, _u32, _u32, _f32, C.POINTER(_vp)]),
+    "twd_head_create_device": (C.c_int, [_vp, _u64, _u32, _u32, _u32, _f32, _vp, C.POINTER(_vp)]),
+    "twd_head_destroy": (None, [_vp]),
+    "twd_head_info": (C.c_int, [_vp, C.POINTER(_u32), C.POINTER(_u32), C.POINTER(_f32),
+                                C.POINTER(_u64)]),
+    "twd_head_logits": (C.c_int, [_vp, _vp, _u32, _vp, _vp]),
+    "twd_head_greedy": (C.c_int, [_vp, _vp, _u32, _vp, _vp, _vp]),
+    "twd_head_sample": (C.c_int, [_vp, _vp, _u32, C.POINTER(RowParams), _vp, _vp, _vp, _vp]),
+    "twd_head_verify_greedy": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _vp]),
+    "twd_selector_create": (C.c_int, [_u32, _u32, C.POINTER(_vp)]),
+    "twd_selector_destroy": (None, [_vp]),
+    "twd_select": (C.c_int, [_vp, _vp, _u32, _u32, _u64, C.POINTER(RowParams), _vp, _vp, _vp]),
+    "twd_verify": (C.c_int, [_vp, _vp, _u32, _u32, _u64, C.POINTER(RowParams), _u64, _vp, _u32,
+                             _vp, _vp]),
+    "twd_splitmix64": (_u64, [_u64]),
+    "twd_seed_for": (_u64, [C.c_int, _u64, C.c_int]),
+    "twd_uniform_from_seed": (_f32, [_u64]),
+    "twd_validate_sampling": (C.c_int, [_f32, _f32, _i32, _f32]),
+    "twd_generate_head": (C.c_int, [_vp, _u32, _u32, _u32, _u64, _vp]),
+    "twd_head_bytes": (_u64, [_u32, _u32, _u32]),
+}
+
+
+def _load() -> C.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build() "
+                          "(or python turbo-winfare-dense_amd/build.py) first")
+    lib = C.CDLL(LIB_PATH)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def last_error() -> str:
+    return (lib.twd_last_error() or b"").decode()
+
+
+def _check(rc: int) -> None:
+    if rc != TWD_OK:
+        raise TwdError(rc, last_error())
+
+
+def _ptr(t) -> int | None:
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def _stream(stream=None) -> int | None:
+    if stream is not None:
+        return stream
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+# ---- sampling.hpp mirror --------------------------------------------------------------------------
+
+@dataclasses.dataclass
+class SamplingParams:
+    temperature: float = 0.0
+    top_p: float = 1.0
+    top_k: int = 0
+    repetition_penalty: float = 1.0
+    has_seed: bool = False
+    seed: int = 0
+
+    def is_greedy(self) -> bool:
+        import numpy as np
+        return (np.float32(self.temperature) <= 0.0
+                and np.float32(self.repetition_penalty) == np.float32(1.0))
+
+
+def validate_sampling(p: SamplingParams) -> None:
+    if lib.twd_validate_sampling(p.temperature, p.top_p, p.top_k, p.repetition_penalty) != TWD_OK:
+        raise G4DenseFormatError(last_error())
+
+
+def splitmix64(x: int) -> int:
+    return int(lib.twd_splitmix64(x & 0xFFFFFFFFFFFFFFFF))
+
+
+def seed_for(p: SamplingParams, position: int) -> int:
+    return int(lib.twd_seed_for(1 if p.has_seed else 0, p.seed & 0xFFFFFFFFFFFFFFFF, position))
+
+
+def uniform_from_seed(seed: int) -> float:
+    return float(lib.twd_uniform_from_seed(seed & 0xFFFFFFFFFFFFFFFF))
+
+
+def row_params(p: SamplingParams, uniform: float = 0.0, softcap: float = 0.0,
+               history_offset: int = 0, history_len: int = 0,
+               repetition_penalty: float | None = None) -> RowParams:
+    rp = p.repetition_penalty if repetition_penalty is None else repetition_penalty
+    return RowParams(p.temperature, p.top_p, p.top_k, rp, uniform, softcap, history_offset,
+                     history_len)
+
+
+def _params_array(params: Sequence[RowParams]):
+    arr = (RowParams * len(params))(*params)
+    return arr
+
+
+class Selector:
+    """Scratch for selection over caller-owned device logits (twd_selector)."""
+
+    def __init__(self, max_vocab: int, max_rows: int = MAX_ROWS):
+        h = C.c_void_p()
+        _check(lib.twd_selector_create(max_vocab, max_rows, C.byref(h)))
+        self.handle = h
+        self.max_vocab = max_vocab
+
+    def close(self):
+        if self.handle:
+            lib.twd_selector_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def select(self, logits, params: Sequence[RowParams], history=None, tokens=None,
+               stream=None):
+        """Penalty (in place) + sample_token per row of a [rows, vocab] float32 device tensor."""
+        import torch
+        rows, vocab = logits.shape
+        if tokens is None:
+            tokens = torch.empty(rows, dtype=torch.int32, device=logits.device)
+        arr = _params_array(params)
+        _check(lib.twd_select(self.handle, _ptr(logits), vocab, rows, logits.stride(0), arr,
+                              _ptr(history), _ptr(tokens), _stream(stream)))
+        return tokens
+
+    def verify(self, logits, params: RowParams, base_seed: int, drafts, result=None,
+               stream=None):
+        import torch
+        rows, vocab = logits.shape
+        if result is None:
+            result = torch.zeros(VERIFY_WORDS, dtype=torch.int32, device=logits.device)
+        _check(lib.twd_verify(self.handle, _ptr(logits), vocab, rows, logits.stride(0),
+                              C.byref(params), base_seed & 0xFFFFFFFFFFFFFFFF, _ptr(drafts),
+                              0 if drafts is None else drafts.numel(), _ptr(result),
+                              _stream(stream)))
+        return result
+
+
+_default_selector: Selector | None = None
+
+
+def _selector(vocab: int) -> Selector:
+    global _default_selector
+    if _default_selector is None or _default_selector.max_vocab < vocab:
+        _default_selector = Selector(max(vocab, 262144), MAX_ROWS + 1)
+    return _default_selector
+
+
+def apply_repetition_penalty(logits, vocab: int, history, penalty: float, softcap: float):
+    """In place on a float32 device tensor holding one row (sampling.cpp:103-119)."""
+    import torch
+    if float(penalty) == 1.0 or history is None or len(history) == 0:
+        return logits
+    hist = torch.as_tensor(history, dtype=torch.int64).to(torch.int32).to(logits.device)
+    p = RowParams(0.0, 1.0, 0, penalty, 0.0, softcap, 0, hist.numel())
+    sel = _selector(vocab)
+    tok = torch.empty(1, dtype=torch.int32, device=logits.device)
+    sel.select(logits.view(1, -1)[:, :vocab], [p], hist, tok)
+    return logits
+
+
+def sample_token(logits, vocab: int, p: SamplingParams, seed: int) -> int:
+    """sample_token (sampling.cpp:121-198) on a float32 device tensor holding one row."""
+    if vocab == 0:
+        raise G4DenseFormatError("sample_token: empty vocabulary")
+    sel = _selector(vocab)
+    rp = row_params(p, uniform_from_seed(seed), repetition_penalty=1.0)
+    tok = sel.select(logits.view(1, -1)[:, :vocab], [rp])
+    t = int(tok.cpu().item()) & 0xFFFFFFFF
+    if t == TOKEN_DEGENERATE:
+        raise G4DenseFormatError("sample_token: logit distribution is degenerate")
+    return t
+
+
+def decode_verify(result) -> dict:
+    v = [int(x) & 0xFFFFFFFF for x in result.cpu().tolist()]
+    n = v[0]
+    if n == TOKEN_DEGENERATE:
+        raise G4DenseFormatError("sample_token: logit distribution is degenerate")
+    total = v[2]
+    return {
+        "tokens": v[5:5 + n],
+        "num_accepted": v[1],
+        "total_drafted": total,
+        "bonus_token_sampled": bool(v[3]),
+        "bonus_token": v[4],
+        "acceptance_rate": 0.0 if total == 0 else v[1] / total,
+    }
+
+
+class SpeculativeCoordinator:
+    """speculator.hpp:19-43 over device logit rows."""
+
+    def __init__(self):
+        self.total_draft_tokens = 0
+        self.total_accepted_tokens = 0
+
+    def cumulative_acceptance_rate(self) -> float:
+        return 0.0 if self.total_draft_tokens == 0 else (
+            self.total_accepted_tokens / self.total_draft_tokens)
+
+    def evaluate_verification(self, draft_tokens, target_logits, vocab_size: int,
+                              sampling: SamplingParams, base_seed: int, draft_logits=()):
+        """target_logits: float32 device tensor [rows, vocab]."""
+        import torch
+        n = len(draft_tokens)
+        self.total_draft_tokens += n
+        if n == 0 or target_logits.shape[0] == 0:
+            return {"tokens": [], "num_accepted": 0, "total_drafted": n,
+                    "bonus_token_sampled": False, "bonus_token": 0, "acceptance_rate": 0.0}
+        if not sampling.is_greedy() and any(len(d) for d in draft_logits):
+            raise G4DenseFormatError("evaluate_verification: rejection sampling with draft "
+                                     "logits is not implemented on the device path")
+        drafts = torch.tensor(list(draft_tokens), dtype=torch.int64).to(torch.int32).to(
+            target_logits.device)
+        sel = _selector(vocab_size)
+        res = sel.verify(target_logits[:, :vocab_size], row_params(sampling), base_seed, drafts)
+        out = decode_verify(res)
+        self.total_accepted_tokens += out["num_accepted"]
+        return out
+
+
+# ---- the fused LM head --------------------------------------------------------------------------
+
+def head_bytes(vocab: int, d_model: int, group: int = 64) -> int:
+    return int(lib.twd_head_bytes(vocab, d_model, group))
+
+
+def generate_head(buf, vocab: int, d_model: int, seed: int, group: int = 64, stream=None):
+    """Fills a uint8 device tensor with the synthetic [W|S|B] head (formula in twd_head.h)."""
+    _check(lib.twd_generate_head(_ptr(buf), vocab, d_model, group,
+                                 seed & 0xFFFFFFFFFFFFFFFF, _stream(stream)))
+    return buf
+
+
+class LMHead:
+    """The tied INT4 g64 LM head resident in HBM (twd_head)."""
+
+    def __init__(self, wsb, vocab: int, d_model: int, softcap: float, group: int = 64,
+                 stream=None):
+        """wsb: the reference layout [W|S|B] as a uint8 device tensor (or host numpy array)."""
+        h = C.c_void_p()
+        nbytes = head_bytes(vocab, d_model, group)
+        if hasattr(wsb, "data_ptr") and wsb.is_cuda:
+            _check(lib.twd_head_create_device(_ptr(wsb), wsb.numel() * wsb.element_size(),
+                                              vocab, d_model, group, softcap, _stream(stream),
+                                              C.byref(h)))
+        else:
+            import numpy as np
+            arr = np.ascontiguousarray(wsb)
+            _check(lib.twd_head_create(arr.ctypes.data, arr.nbytes, vocab, d_model, group,
+                                       softcap, C.byref(h)))
+        self.handle = h
+        self.vocab, self.d_model, self.softcap = vocab, d_model, softcap
+        self.nbytes = nbytes
+
+    def close(self):
+        if self.handle:
+            lib.twd_head_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def logits(self, hidden, out=None, stream=None):
+        import torch
+        rows = hidden.shape[0]
+        if out is None:
+            out = torch.empty(rows, self.vocab, dtype=torch.float32, device=hidden.device)
+        _check(lib.twd_head_logits(self.handle, _ptr(hidden), rows, _ptr(out), _stream(stream)))
+        return out
+
+    def greedy(self, hidden, logits=None, tokens=None, stream=None):
+        import torch
+        rows = hidden.shape[0]
+        if tokens is None:
+            tokens = torch.empty(rows, dtype=torch.int32, device=hidden.device)
+        _check(lib.twd_head_greedy(self.handle, _ptr(hidden), rows, _ptr(logits), _ptr(tokens),
+                                   _stream(stream)))
+        return tokens
+
+    def sample(self, hidden, params: Sequence[RowParams], history=None, logits=None,
+               tokens=None, stream=None):
+        import torch
+        rows = hidden.shape[0]
+        if logits is None:
+            logits = torch.empty(rows, self.vocab, dtype=torch.float32, device=hidden.device)
+        if tokens is None:
+            tokens = torch.empty(rows, dtype=torch.int32, device=hidden.device)
+        arr = _params_array(params)
+        _check(lib.twd_head_sample(self.handle, _ptr(hidden), rows, arr, _ptr(history),
+                                   _ptr(logits), _ptr(tokens), _stream(stream)))
+        return tokens, logits
+
+    def verify_greedy(self, hidden, drafts, logits=None, result=None, stream=None):
+        import torch
+        rows = hidden.shape[0]
+        if result is None:
+            result = torch.zeros(VERIFY_WORDS, dtype=torch.int32, device=hidden.device)
+        nd = 0 if drafts is None else drafts.numel()
+        _check(lib.twd_head_verify_greedy(self.handle, _ptr(hidden), rows, _ptr(drafts), nd,
+                                          _ptr(logits), _ptr(result), _stream(stream)))
+        return result
