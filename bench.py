@@ -313,7 +313,7 @@ def main():
                               f"{SEED})"},
         "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9,
                      "unit": "GB/s", "frac": achieved / PEAK_HBM, "traffic": None,
-                     "kernel": "head_kernel<1,1,4,1> (M=1 greedy)",
+                     "kernel": "head_small_kernel<1,2,4,1> + head_finish_kernel (M=1 greedy)",
                      "bytes_per_launch": bytes2},
         "cpu_baseline": cpu,
         "configs": {str(k): results[k] for k in sorted(results)},

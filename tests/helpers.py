@@ -39,8 +39,8 @@ def wsb_bytes(W, S, B) -> np.ndarray:
 
 
 def allclose_report(got, want, atol, rtol):
-    got = np.asarray(got, np.float64)
-    want = np.asarray(want, np.float64)
+    got = np.asarray(got, np.float64).reshape(-1)
+    want = np.asarray(want, np.float64).reshape(-1)
     err = np.abs(got - want)
     ratio = err / (atol + rtol * np.abs(want))
     i = int(np.argmax(ratio))

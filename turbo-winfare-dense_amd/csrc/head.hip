@@ -23,7 +23,7 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
-enum HeadMode { kModeLogits = 0, kModeGreedy = 1, kModeVerify = 2 };
+enum HeadMode { kModeLogits = 0, kModeGreedy = 1 };  // greedy: also write block ranks
 
 constexpr int kHeadThreads = 256;
 constexpr int kHeadWaves = 4;
@@ -37,11 +37,6 @@ struct HeadArgs {
     float* logits;
     uint32_t vocab;
     uint64_t* partial;  // [TWD_MAX_ROWS][gridDim.x]
-    uint32_t* counter;
-    uint32_t* tokens;
-    const uint32_t* drafts;
-    uint32_t n_drafts;
-    twd_verify_result* vres;
 };
 
 // 8 nibbles of one word -> 8 bf16 values 128+q, in k-slot order [0,4,1,5,2,6,3,7].
@@ -77,16 +72,197 @@ __device__ __forceinline__ float sum8_bf16(u32x4_t v) {
     return s;
 }
 
+// Shared memory of the head epilogue (cross-wave greedy reduction).
+struct EpiShared {
+    uint64_t red[kHeadWaves][TWD_MAX_ROWS];
+};
+
+// Softcap, logits store, and -- for the greedy modes -- the block's per-row rank maximum,
+// written to partial[m][block]. head_finish_kernel reduces the blocks in a second launch: a
+// per-block device-scope fence plus a global counter (the "last block" pattern) serialises on
+// this part's memory-side atomics and costs more than the whole streaming pass.
+// tot[j][mt][i] holds row r = (tile0 + j) * 16 + lane % 16 of m = 16 mt + 4 (lane / 16) + i.
+template <int NMT, int NI, int RT, int MODE>
+__device__ __forceinline__ void head_epilogue(const HeadArgs& a, f32x4_t (&tot)[RT][NMT],
+                                              uint32_t tile0, EpiShared& se) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    uint64_t best[NMT][NI];
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+        for (int i = 0; i < NI; ++i) best[mt][i] = 0;
+
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+        const uint32_t r = (tile0 + j) * kTileRows + (lane & 15);
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const uint32_t m = mt * 16 + 4 * (lane >> 4) + i;
+                float v = tot[j][mt][i];
+                if (a.softcap > 0.0f) v = a.softcap * tanhf(v / a.softcap);
+                const bool live = (m < a.M) && (r < a.vocab);
+                if (live && a.logits) a.logits[static_cast<size_t>(m) * a.vocab + r] = v;
+                if (MODE != kModeLogits) {
+                    const uint64_t k = live ? rank_key(v, r) : 0ull;
+                    best[mt][i] = k > best[mt][i] ? k : best[mt][i];
+                }
+            }
+    }
+    if (MODE == kModeLogits) return;
+
+    // rows sharing m are the 16 lanes with the same lane >> 4
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            uint64_t k = best[mt][i];
+#pragma unroll
+            for (int msk = 1; msk < 16; msk <<= 1) {
+                const uint64_t o = shfl_xor_u64(k, msk);
+                k = o > k ? o : k;
+            }
+            const uint32_t m = mt * 16 + 4 * (lane >> 4) + i;
+            if ((lane & 15) == 0 && m < TWD_MAX_ROWS) se.red[wave][m] = k;
+        }
+    __syncthreads();
+    const uint32_t nb = gridDim.x;
+    if (static_cast<uint32_t>(tid) < a.M) {
+        uint64_t k = se.red[0][tid];
+#pragma unroll
+        for (int w = 1; w < kHeadWaves; ++w) k = se.red[w][tid] > k ? se.red[w][tid] : k;
+        a.partial[static_cast<size_t>(tid) * nb + blockIdx.x] = k;
+    }
+
+}
+
+// Per-chunk math shared by both kernels: one unit of one row tile (4 words per lane = 4 MFMA
+// k-steps, two groups) against A fragments av[mt][t] and group sums xv[g][mt].
+template <int NMT, int NI>
+__device__ __forceinline__ void unit_mac(const u32x4_t& w, const u32x2_t& sb,
+                                         const bf16x8_t (&av)[NMT][4],
+                                         const f32x4_t (&xv)[2][NMT], f32x4_t (&tot)[NMT]) {
+    bf16x8_t bv[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) bv[t] = nibbles_to_bf16(w[t]);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        const float s = g == 0 ? bf16_lo(sb.x) : bf16_hi(sb.x);
+        const float b = g == 0 ? bf16_lo(sb.y) : bf16_hi(sb.y);
+        const float tb = fmaf(-128.0f, s, b);
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt) {
+            f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt][2 * g], bv[2 * g], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt][2 * g + 1], bv[2 * g + 1], acc,
+                                                          0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < NI; ++i)
+                tot[mt][i] = fmaf(s, acc[i], fmaf(tb, xv[g][mt][i], tot[mt][i]));
+        }
+    }
+}
+
+template <int RT>
+__device__ __forceinline__ void load_unit(const HeadArgs& a, uint32_t tile0, uint32_t U, int lane,
+                                          u32x4_t (&w)[RT], u32x2_t (&sb)[RT]) {
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+        const uint32_t T = tile0 + j;
+        if (T < a.ntiles) {
+            const uint8_t* base = a.tiled + (static_cast<size_t>(T) * a.nunits + U) * kUnitBytes;
+            w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(base) + lane);
+            sb[j] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x2_t*>(base + kUnitNibbleBytes) + (lane & 15));
+        } else {
+            w[j] = u32x4_t{0u, 0u, 0u, 0u};
+            sb[j] = u32x2_t{0u, 0u};
+        }
+    }
+}
+
+// ---- M <= 8: the whole h resident in LDS, no barrier in the streaming loop ---------------------
+//
+// LDS holds h permuted into A-fragment order, [m][chunk U][k-step t][kg] of 16 B, plus the group
+// sums [g][16]. A-fragment rows m >= M only feed output rows that are never stored, so their
+// lanes simply read row 0. Each wave streams its RT row tiles through a PF-deep register ring
+// of weight units, with no synchronisation until the epilogue.
+template <int NI, int RT, int PF, int MODE>
+__global__ __launch_bounds__(kHeadThreads) void head_small_kernel(HeadArgs a) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    __shared__ EpiShared se;
+    u32x4_t* sH = reinterpret_cast<u32x4_t*>(smem_raw);
+    const uint32_t row_vecs = a.d / 8;  // 16 B vectors per h row
+    float* sX = reinterpret_cast<float*>(sH + a.M * row_vecs);  // [groups][16]
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t tile0 = (blockIdx.x * kHeadWaves + wave) * RT;
+    const uint32_t groups = a.d / kGroup;
+
+    // ---- stage h: 8 consecutive threads cover one 64-column group ----
+    const uint32_t tasks = a.M * row_vecs;
+    for (uint32_t base = 0; base < tasks; base += kHeadThreads) {
+        const uint32_t task = base + tid;
+        u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
+        if (task < tasks) v = *reinterpret_cast<const u32x4_t*>(a.h + static_cast<size_t>(task) * 8);
+        float s = sum8_bf16(v);
+        s += __shfl_xor(s, 1);
+        s += __shfl_xor(s, 2);
+        s += __shfl_xor(s, 4);
+        if (task < tasks) {
+            const uint32_t m = task / row_vecs, c8 = task % row_vecs;
+            const uint32_t U = c8 >> 4, c = c8 & 15;
+            sH[((m * (a.d / kChunkK) + U) * 4 + (c >> 2)) * 4 + (c & 3)] = permute_h(v);
+            if ((c8 & 7) == 0) sX[(c8 >> 3) * 16 + m] = s;
+        }
+    }
+    for (uint32_t i = tid; i < groups * 16; i += kHeadThreads)
+        if ((i & 15) >= a.M) sX[i] = 0.0f;
+    __syncthreads();
+
+    const uint32_t m_lane = lane & 15;
+    const u32x4_t* aRow = sH + (m_lane < a.M ? m_lane : 0u) * row_vecs + (lane >> 4);
+    const float* xLane = sX + 4 * (lane >> 4);
+
+    f32x4_t tot[RT][1];
+#pragma unroll
+    for (int j = 0; j < RT; ++j) tot[j][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    u32x4_t wq[PF][RT];
+    u32x2_t sq[PF][RT];
+#pragma unroll
+    for (int s = 0; s < PF; ++s)
+        if (static_cast<uint32_t>(s) < a.nunits) load_unit<RT>(a, tile0, s, lane, wq[s], sq[s]);
+
+    for (uint32_t U0 = 0; U0 < a.nunits; U0 += PF) {
+#pragma unroll
+        for (int s = 0; s < PF; ++s) {
+            const uint32_t U = U0 + s;
+            if (U >= a.nunits) break;
+            bf16x8_t av[1][4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) av[0][t] = __builtin_bit_cast(bf16x8_t, aRow[(U * 4 + t) * 4]);
+            f32x4_t xv[2][1];
+#pragma unroll
+            for (int g = 0; g < 2; ++g)
+                xv[g][0] = *reinterpret_cast<const f32x4_t*>(xLane + (2 * U + g) * 16);
+#pragma unroll
+            for (int j = 0; j < RT; ++j) unit_mac<1, NI>(wq[s][j], sq[s][j], av, xv, tot[j]);
+            if (U + PF < a.nunits) load_unit<RT>(a, tile0, U + PF, lane, wq[s], sq[s]);
+        }
+    }
+    head_epilogue<1, NI, RT, MODE>(a, tot, tile0, se);
+}
+
+// ---- any M <= 64: h staged through LDS one 128-column chunk at a time ---------------------------
+//
 // Block = 4 waves; wave w owns RT consecutive 16-row tiles. NMT = number of 16-wide m tiles
-// (1 for M <= 16, 4 for M <= 64); NI = accumulator lanes per m tile that can hold a live row
-// (1 when M == 1, else 4).
+// (1 for M <= 16, 4 for M <= 64); NI = accumulator lanes per m tile that can hold a live row.
 template <int NMT, int NI, int RT, int MODE>
 __global__ __launch_bounds__(kHeadThreads) void head_kernel(HeadArgs a) {
     __shared__ u32x4_t sA[2][NMT][4][64];
     __shared__ float sX[2][2][NMT * 16];
-    __shared__ uint64_t sRed[kHeadWaves][NMT * 16];
-    __shared__ uint32_t sTok[TWD_MAX_ROWS];
-    __shared__ int sLast;
+    __shared__ EpiShared se;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -120,26 +296,8 @@ __global__ __launch_bounds__(kHeadThreads) void head_kernel(HeadArgs a) {
         }
     };
 
-    // ---- weight units (nibbles + scales/biases) of this wave's tiles ----
     u32x4_t wq[RT];
     u32x2_t sq[RT];
-    auto load_unit = [&](uint32_t U, u32x4_t* w, u32x2_t* sb) {
-#pragma unroll
-        for (int j = 0; j < RT; ++j) {
-            const uint32_t T = tile0 + j;
-            if (T < a.ntiles) {
-                const uint8_t* base =
-                    a.tiled + (static_cast<size_t>(T) * a.nunits + U) * kUnitBytes;
-                w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(base) + lane);
-                sb[j] = __builtin_nontemporal_load(
-                    reinterpret_cast<const u32x2_t*>(base + kUnitNibbleBytes) + (lane & 15));
-            } else {
-                w[j] = u32x4_t{0u, 0u, 0u, 0u};
-                sb[j] = u32x2_t{0u, 0u};
-            }
-        }
-    };
-
     f32x4_t tot[RT][NMT];
 #pragma unroll
     for (int j = 0; j < RT; ++j)
@@ -148,7 +306,7 @@ __global__ __launch_bounds__(kHeadThreads) void head_kernel(HeadArgs a) {
 
     stage_load(0);
     stage_store(0);
-    load_unit(0, wq, sq);
+    load_unit<RT>(a, tile0, 0, lane, wq, sq);
 
     for (uint32_t U = 0; U < a.nunits; ++U) {
         __syncthreads();
@@ -158,9 +316,8 @@ __global__ __launch_bounds__(kHeadThreads) void head_kernel(HeadArgs a) {
         u32x2_t sn[RT];
         if (more) {
             stage_load(U + 1);
-            load_unit(U + 1, wn, sn);
+            load_unit<RT>(a, tile0, U + 1, lane, wn, sn);
         }
-
         bf16x8_t av[NMT][4];
 #pragma unroll
         for (int mt = 0; mt < NMT; ++mt)
@@ -172,31 +329,8 @@ __global__ __launch_bounds__(kHeadThreads) void head_kernel(HeadArgs a) {
 #pragma unroll
             for (int mt = 0; mt < NMT; ++mt)
                 xv[g][mt] = *reinterpret_cast<const f32x4_t*>(&sX[buf][g][mt * 16 + 4 * (lane >> 4)]);
-
 #pragma unroll
-        for (int j = 0; j < RT; ++j) {
-            bf16x8_t bv[4];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) bv[t] = nibbles_to_bf16(wq[j][t]);
-#pragma unroll
-            for (int g = 0; g < 2; ++g) {
-                const float s = g == 0 ? bf16_lo(sq[j].x) : bf16_hi(sq[j].x);
-                const float b = g == 0 ? bf16_lo(sq[j].y) : bf16_hi(sq[j].y);
-                const float tb = fmaf(-128.0f, s, b);
-#pragma unroll
-                for (int mt = 0; mt < NMT; ++mt) {
-                    f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt][2 * g], bv[2 * g], acc,
-                                                                  0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt][2 * g + 1],
-                                                                  bv[2 * g + 1], acc, 0, 0, 0);
-#pragma unroll
-                    for (int i = 0; i < NI; ++i)
-                        tot[j][mt][i] = fmaf(s, acc[i], fmaf(tb, xv[g][mt][i], tot[j][mt][i]));
-                }
-            }
-        }
-
+        for (int j = 0; j < RT; ++j) unit_mac<NMT, NI>(wq[j], sq[j], av, xv, tot[j]);
         if (more) {
             stage_store(buf ^ 1);
 #pragma unroll
@@ -206,114 +340,61 @@ __global__ __launch_bounds__(kHeadThreads) void head_kernel(HeadArgs a) {
             }
         }
     }
+    head_epilogue<NMT, NI, RT, MODE>(a, tot, tile0, se);
+}
 
-    // ---- epilogue: softcap, store, greedy ranks ----
-    uint64_t best[NMT][NI];
-#pragma unroll
-    for (int mt = 0; mt < NMT; ++mt)
-#pragma unroll
-        for (int i = 0; i < NI; ++i) best[mt][i] = 0;
-
-#pragma unroll
-    for (int j = 0; j < RT; ++j) {
-        const uint32_t r = (tile0 + j) * kTileRows + (lane & 15);
-#pragma unroll
-        for (int mt = 0; mt < NMT; ++mt)
-#pragma unroll
-            for (int i = 0; i < NI; ++i) {
-                const uint32_t m = mt * 16 + 4 * (lane >> 4) + i;
-                float v = tot[j][mt][i];
-                if (a.softcap > 0.0f) v = a.softcap * tanhf(v / a.softcap);
-                const bool live = (m < a.M) && (r < a.vocab);
-                if (live && a.logits) a.logits[static_cast<size_t>(m) * a.vocab + r] = v;
-                if (MODE != kModeLogits) {
-                    const uint64_t k = live ? rank_key(v, r) : 0ull;
-                    best[mt][i] = k > best[mt][i] ? k : best[mt][i];
-                }
-            }
-    }
-    if (MODE == kModeLogits) return;
-
-    // rows sharing m are the 16 lanes with the same lane>>4
-#pragma unroll
-    for (int mt = 0; mt < NMT; ++mt)
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            uint64_t k = best[mt][i];
-#pragma unroll
-            for (int msk = 1; msk < 16; msk <<= 1) {
-                const uint64_t o = shfl_xor_u64(k, msk);
-                k = o > k ? o : k;
-            }
-            const uint32_t m = mt * 16 + 4 * (lane >> 4) + i;
-            if ((lane & 15) == 0) sRed[wave][m] = k;
-        }
-    __syncthreads();
-    const uint32_t nb = gridDim.x;
-    if (tid < NMT * 16) {
-        uint64_t k = sRed[0][tid];
-#pragma unroll
-        for (int w = 1; w < kHeadWaves; ++w) k = sRed[w][tid] > k ? sRed[w][tid] : k;
-        if (static_cast<uint32_t>(tid) < a.M) a.partial[static_cast<size_t>(tid) * nb + blockIdx.x] = k;
-    }
-
-    // ---- the last block to finish reduces every block's ranks ----
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) sLast = (atomicAdd(a.counter, 1u) == nb - 1);
-    __syncthreads();
-    if (!sLast) return;
-    __threadfence();
-    for (uint32_t m = wave; m < a.M; m += kHeadWaves) {
+// Greedy tokens from the per-block ranks, then greedy verify bookkeeping
+// (speculator.cpp:91-114 and :183-195). One block; wave w reduces rows w, w+4, ...
+__global__ __launch_bounds__(kHeadThreads) void head_finish_kernel(
+    const uint64_t* __restrict__ partial, uint32_t nb, uint32_t M, uint32_t* tokens,
+    const uint32_t* drafts, uint32_t n_drafts, twd_verify_result* vres) {
+    __shared__ uint32_t sTok[TWD_MAX_ROWS];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    for (uint32_t m = wave; m < M; m += kHeadWaves) {
         uint64_t k = 0;
         for (uint32_t b = lane; b < nb; b += 64) {
-            const uint64_t o = __builtin_nontemporal_load(a.partial + static_cast<size_t>(m) * nb + b);
+            const uint64_t o = partial[static_cast<size_t>(m) * nb + b];
             k = o > k ? o : k;
         }
         k = wave_max_u64(k);
         if (lane == 0) {
             const uint32_t tok = rank_index(k);
             sTok[m] = tok;
-            if (a.tokens) a.tokens[m] = tok;
+            if (tokens) tokens[m] = tok;
         }
     }
     __syncthreads();
-    if (tid == 0) {
-        *a.counter = 0u;  // ready for the next launch on this head
-        if (MODE == kModeVerify) {
-            // speculator.cpp:91-114 and :183-195, greedy branch
-            twd_verify_result* v = a.vres;
-            const uint32_t nd = a.n_drafts, rows = a.M;
-            uint32_t n = 0, acc = 0, bonus = 0, sampled = 0;
-            if (nd != 0 && rows != 0) {
-                const uint32_t k = nd < rows ? nd : rows;
-                bool rejected = false;
-                for (uint32_t i = 0; i < k; ++i) {
-                    const uint32_t t = sTok[i];
-                    if (a.drafts[i] == t) {
-                        v->tokens[n++] = t;
-                        ++acc;
-                    } else {
-                        bonus = t;
-                        sampled = 1;
-                        v->tokens[n++] = t;
-                        rejected = true;
-                        break;
-                    }
-                }
-                if (!rejected && rows > k) {
-                    bonus = sTok[k];
-                    sampled = 1;
-                    v->tokens[n++] = bonus;
-                }
+    if (tid != 0 || !vres) return;
+    twd_verify_result* v = vres;
+    const uint32_t nd = n_drafts, rows = M;
+    uint32_t n = 0, acc = 0, bonus = 0, sampled = 0;
+    if (nd != 0 && rows != 0) {
+        const uint32_t k = nd < rows ? nd : rows;
+        bool rejected = false;
+        for (uint32_t i = 0; i < k; ++i) {
+            const uint32_t t = sTok[i];
+            if (drafts[i] == t) {
+                v->tokens[n++] = t;
+                ++acc;
+            } else {
+                bonus = t;
+                sampled = 1;
+                v->tokens[n++] = t;
+                rejected = true;
+                break;
             }
-            v->n_tokens = n;
-            v->num_accepted = acc;
-            v->total_drafted = nd;
-            v->bonus_token_sampled = sampled;
-            v->bonus_token = bonus;
+        }
+        if (!rejected && rows > k) {
+            bonus = sTok[k];
+            sampled = 1;
+            v->tokens[n++] = bonus;
         }
     }
+    v->n_tokens = n;
+    v->num_accepted = acc;
+    v->total_drafted = nd;
+    v->bonus_token_sampled = sampled;
+    v->bonus_token = bonus;
 }
 
 // ---- layout repack: reference [W|S|B] -> units ----------------------------------------------
@@ -394,15 +475,19 @@ struct twd_head {
     uint8_t* tiled = nullptr;
     uint64_t tiled_bytes = 0;
     uint64_t* partial = nullptr;  // [TWD_MAX_ROWS][max blocks]
-    uint32_t* counter = nullptr;
     uint32_t max_blocks = 0;
     twd_selector* sel = nullptr;
 };
 
 namespace {
 
-constexpr int kRT1 = 4;  // row tiles per wave, M <= 16
-constexpr int kRT4 = 2;  // row tiles per wave, M <= 64
+constexpr int kRT1 = 4;   // row tiles per wave, chunked kernel, M <= 16
+constexpr int kRT4 = 2;   // row tiles per wave, chunked kernel, M <= 64
+// resident-h kernel: row tiles per wave and weight units in flight (measured best on MI355X:
+// M = 1 -> 2 tiles x 4 units, 126 us; M = 5 -> 4 tiles x 2 units, 165 us)
+constexpr int kRTS1 = 2, kPFS1 = 4;  // M == 1
+constexpr int kRTS4 = 4, kPFS4 = 2;  // 2 <= M <= 8
+constexpr uint32_t kSmallMaxRows = 8;
 
 uint32_t blocks_for(uint32_t ntiles, int rt) {
     const uint32_t per = kHeadWaves * rt;
@@ -416,6 +501,32 @@ int check_geometry(uint32_t vocab, uint32_t d, uint32_t group) {
     return TWD_OK;
 }
 
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Dynamic LDS of the resident-h kernel: h permuted (M x d bf16) + group sums [d/64][16] fp32.
+size_t small_smem_bytes(uint32_t rows, uint32_t d) {
+    return static_cast<size_t>(rows) * d * 2 + static_cast<size_t>(d / kGroup) * 16 * 4;
+}
+
+template <typename K>
+hipError_t allow_smem(K kernel, size_t bytes) {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+}
+
+// Lets every resident-h instantiation use the LDS it needs for kSmallMaxRows rows of d.
+int enable_small_kernels(uint32_t d) {
+    const size_t bytes = small_smem_bytes(kSmallMaxRows, d);
+    if (bytes > 160 * 1024) return fail(TWD_E_UNSUPPORTED, "d_model too large for the LDS-resident head");
+    hipError_t e = hipSuccess;
+    if (e == hipSuccess) e = allow_smem(head_small_kernel<1, kRTS1, kPFS1, kModeLogits>, bytes);
+    if (e == hipSuccess) e = allow_smem(head_small_kernel<1, kRTS1, kPFS1, kModeGreedy>, bytes);
+    if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS4, kPFS4, kModeLogits>, bytes);
+    if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS4, kPFS4, kModeGreedy>, bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
+    return TWD_OK;
+}
+
 int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
     twd_head* h = new twd_head();
     h->vocab = vocab;
@@ -424,16 +535,15 @@ int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
     h->ntiles = (vocab + kTileRows - 1) / kTileRows;
     h->nunits = d / kChunkK;
     h->tiled_bytes = static_cast<uint64_t>(h->ntiles) * h->nunits * kUnitBytes;
-    h->max_blocks = std::max(blocks_for(h->ntiles, kRT1), blocks_for(h->ntiles, kRT4));
+    h->max_blocks = std::max({blocks_for(h->ntiles, kRT1), blocks_for(h->ntiles, kRT4),
+                              blocks_for(h->ntiles, kRTS1), blocks_for(h->ntiles, kRTS4)});
     hipError_t e = hipMalloc(&h->tiled, h->tiled_bytes);
     if (e == hipSuccess) e = hipMalloc(&h->partial, sizeof(uint64_t) * TWD_MAX_ROWS * h->max_blocks);
-    if (e == hipSuccess) e = hipMalloc(&h->counter, sizeof(uint32_t) * 4);
-    if (e == hipSuccess) e = hipMemset(h->counter, 0, sizeof(uint32_t) * 4);
     if (e != hipSuccess) {
         twd_head_destroy(h);
         return hip_fail(e, "allocating the LM head");
     }
-    if (twd_selector_create(vocab, TWD_MAX_ROWS, &h->sel) != TWD_OK) {
+    if (enable_small_kernels(d) != TWD_OK || twd_selector_create(vocab, TWD_MAX_ROWS, &h->sel) != TWD_OK) {
         twd_head_destroy(h);
         return TWD_E_HIP;
     }
@@ -454,7 +564,7 @@ int head_repack(twd_head* h, const uint8_t* wsb_dev, hipStream_t stream) {
     return TWD_OK;
 }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 
 template <int MODE>
 int launch_head(twd_head* h, const uint16_t* hidden, uint32_t rows, float* logits,
@@ -474,19 +584,29 @@ int launch_head(twd_head* h, const uint16_t* hidden, uint32_t rows, float* logit
     a.logits = logits;
     a.vocab = h->vocab;
     a.partial = h->partial;
-    a.counter = h->counter;
-    a.tokens = tokens;
-    a.drafts = drafts;
-    a.n_drafts = n_drafts;
-    a.vres = vres;
-    if (rows == 1) {
-        head_kernel<1, 1, kRT1, MODE><<<blocks_for(h->ntiles, kRT1), kHeadThreads, 0, stream>>>(a);
+    if (rows <= kSmallMaxRows) {
+        const size_t smem = small_smem_bytes(rows, h->d);
+        if (rows == 1)
+            head_small_kernel<1, kRTS1, kPFS1, MODE>
+                <<<blocks_for(h->ntiles, kRTS1), kHeadThreads, smem, stream>>>(a);
+        else
+            head_small_kernel<4, kRTS4, kPFS4, MODE>
+                <<<blocks_for(h->ntiles, kRTS4), kHeadThreads, smem, stream>>>(a);
     } else if (rows <= 16) {
         head_kernel<1, 4, kRT1, MODE><<<blocks_for(h->ntiles, kRT1), kHeadThreads, 0, stream>>>(a);
     } else {
         head_kernel<4, 4, kRT4, MODE><<<blocks_for(h->ntiles, kRT4), kHeadThreads, 0, stream>>>(a);
     }
     TWD_HIP(hipGetLastError());
+    if (MODE == kModeGreedy) {
+        const uint32_t nb = rows == 1             ? blocks_for(h->ntiles, kRTS1)
+                          : rows <= kSmallMaxRows ? blocks_for(h->ntiles, kRTS4)
+                          : rows <= 16            ? blocks_for(h->ntiles, kRT1)
+                                                  : blocks_for(h->ntiles, kRT4);
+        head_finish_kernel<<<1, kHeadThreads, 0, stream>>>(h->partial, nb, rows, tokens, drafts,
+                                                           n_drafts, vres);
+        TWD_HIP(hipGetLastError());
+    }
     return TWD_OK;
 }
 
@@ -552,7 +672,6 @@ TWD_API void twd_head_destroy(twd_head* h) {
     if (!h) return;
     if (h->tiled) (void)hipFree(h->tiled);
     if (h->partial) (void)hipFree(h->partial);
-    if (h->counter) (void)hipFree(h->counter);
     if (h->sel) twd_selector_destroy(h->sel);
     delete h;
 }
@@ -591,7 +710,7 @@ TWD_API int twd_head_verify_greedy(twd_head* h, const uint16_t* hidden, uint32_t
     if (!result) return fail(TWD_E_INVALID, "null result");
     if (n_drafts > 0 && !drafts) return fail(TWD_E_INVALID, "null drafts");
     if (n_drafts > TWD_MAX_ROWS) return fail(TWD_E_INVALID, "n_drafts must be <= 64");
-    return launch_head<kModeVerify>(h, hidden, rows, logits, nullptr, drafts, n_drafts, result,
+    return launch_head<kModeGreedy>(h, hidden, rows, logits, nullptr, drafts, n_drafts, result,
                                     static_cast<hipStream_t>(stream));
 }
 

@@ -1,11 +1,12 @@
 // Token selection over device logit rows on gfx950: repetition penalty, greedy argmax and the
 // sampled chain of sample_token (src/sampling.cpp:103-198), plus verify bookkeeping.
 //
-// One launch covers all rows: grid (parts, rows), each block owns a 16384-entry slice of one
-// row. Per block: penalty on the slice's history ids (occurrence counts in LDS, each applied
-// one occurrence at a time like the reference loop), then either the greedy rank maximum or
-// {slice max, sum exp(l - slice max) in double, the slice's top-`want` ranks by a radix select
-// on 64-bit (value desc, index asc) ranks}. The last block of a row (atomic counter) merges the
+// select_slice_kernel covers all rows: grid (parts, rows), each block owns a 16384-entry slice
+// of one row. Per block: penalty on the slice's history ids (occurrence counts in LDS, each
+// applied one occurrence at a time like the reference loop), then either the greedy rank
+// maximum or {slice max, sum exp(l - slice max) in double, the slice's top-`want` ranks by a
+// radix select on 64-bit (value desc, index asc) ranks}. A row held by one slice finishes in
+// the same block; otherwise select_merge_kernel (one block per row, second launch) merges the
 // slices, sorts the global top-`want`, and runs top-p, top-k and the draw in reference order.
 #include <hip/hip_runtime.h>
 
@@ -17,8 +18,8 @@
 
 namespace twd {
 
-constexpr uint32_t kMaxParts = 64;  // vocab <= 64 * 16384
-constexpr uint32_t kMergePerThread = kMaxParts * kMaxWant / kSelThreads;  // 16
+constexpr uint32_t kMaxParts = 32;  // vocab <= 32 * 16384 = 524288
+constexpr uint32_t kMergePerThread = kMaxParts * kMaxWant / kSelThreads;  // 8
 constexpr int kSelWaves = kSelThreads / 64;
 
 struct SelectArgs {
@@ -40,11 +41,14 @@ struct SelectBufs {
     uint32_t* part_count;
     uint64_t* part_key;
     uint64_t* cand;
-    uint32_t* row_counter;
 };
 
 struct SelectShared {
-    uint32_t cnt[kSlice];       // penalty occurrence counts of the slice
+    union {
+        uint32_t cnt[kSlice];                 // penalty occurrence counts of the slice
+        float val[kSlice];                    // then the slice's penalised values
+        uint64_t cand[kMaxParts * kMaxWant];  // then, in the merge kernel, every slice's ranks
+    } u;
     uint32_t hist[256];         // radix digit histogram
     uint32_t misc[8];
     uint64_t red64[kSelWaves];
@@ -57,7 +61,6 @@ struct SelectShared {
     float gmax;
     double total;
     uint32_t flag;
-    int last;
 };
 
 __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, SelectShared& sh) {
@@ -113,18 +116,20 @@ __device__ __forceinline__ uint32_t block_or_u32(uint32_t v, SelectShared& sh) {
 // The smallest rank T with exactly `want` of the block's ranks >= T (ranks are distinct; rank
 // 0 marks an empty slot and is never selected while want <= number of real ranks). Radix
 // descent over 8-bit digits from the top, stopping once a digit bin is taken whole.
-template <int E>
-__device__ uint64_t block_select(const uint64_t (&K)[E], uint32_t want, SelectShared& sh) {
+template <typename KeyAt>
+__device__ uint64_t block_select(uint32_t per_thread, KeyAt key_at, uint32_t want,
+                                 SelectShared& sh) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     uint64_t prefix = 0, mask = 0;
     uint32_t need = want;
     for (int shift = 56; shift >= 0; shift -= 8) {
         for (int i = tid; i < 256; i += kSelThreads) sh.hist[i] = 0;
         __syncthreads();
-#pragma unroll
-        for (int e = 0; e < E; ++e)
-            if ((K[e] & mask) == prefix && K[e] != 0)
-                atomicAdd(&sh.hist[(K[e] >> shift) & 255u], 1u);
+#pragma unroll 4
+        for (uint32_t e = 0; e < per_thread; ++e) {
+            const uint64_t k = key_at(e);
+            if (k != 0 && (k & mask) == prefix) atomicAdd(&sh.hist[(k >> shift) & 255u], 1u);
+        }
         __syncthreads();
         if (wave == 0) {
             uint32_t c[4];
@@ -228,13 +233,40 @@ __device__ uint32_t finish_sampled(SelectShared& sh, uint32_t want, const twd_ro
     return sh.misc[4];
 }
 
-__global__ __launch_bounds__(kSelThreads) void select_kernel(SelectBufs b, SelectArgs args) {
+// After sh.top[0..want) holds the row's shortlist and sh.gmax/total/flag its statistics:
+// the degenerate check of sampling.cpp:145-147, the shortlist sort, and steps 5-7.
+__device__ void finish_row(SelectShared& sh, uint32_t want, const twd_row_params& p,
+                           uint32_t* token_out) {
+    const int tid = threadIdx.x;
+    if (sh.flag != 0 || !(sh.total > 0.0)) {
+        if (tid == 0) *token_out = TWD_TOKEN_DEGENERATE;
+        return;
+    }
+    uint32_t n2 = 1;
+    while (n2 < want) n2 <<= 1;
+    if (static_cast<uint32_t>(tid) >= want && static_cast<uint32_t>(tid) < n2) sh.top[tid] = 0;
+    __syncthreads();
+    block_sort_desc(sh, n2);
+    const uint32_t tok = finish_sampled(sh, want, p);
+    if (tid == 0) *token_out = tok;
+}
+
+// SelectArgs is the first kernel argument, so it sits at offset 0 of the kernarg segment. The
+// row's parameters are read through that pointer: indexing the by-value argument with
+// blockIdx.y would make the compiler copy all of it into per-lane scratch memory.
+__global__ __launch_bounds__(kSelThreads) void select_slice_kernel(SelectArgs args_by_value, SelectBufs b) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     SelectShared& sh = *reinterpret_cast<SelectShared*>(smem_raw);
+#if __HIP_DEVICE_COMPILE__
+    const SelectArgs& args =
+        *reinterpret_cast<const SelectArgs*>(__builtin_amdgcn_kernarg_segment_ptr());
+#else
+    const SelectArgs& args = args_by_value;  // the host pass only parses kernel bodies
+#endif
     const int tid = threadIdx.x;
     const uint32_t part = blockIdx.x, row = blockIdx.y;
     const uint32_t parts = args.parts;
-    const twd_row_params& p = args.p[row];
+    const twd_row_params p = args.p[row];
     float* lg = b.logits + static_cast<size_t>(row) * b.stride;
     const uint32_t lo = part * kSlice;
     const uint32_t hi = min(b.vocab, lo + kSlice);
@@ -249,19 +281,19 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelectBufs b, Selec
     // ---- repetition penalty, sampling.cpp:103-119 ----
     if (p.repetition_penalty != 1.0f && p.history_len > 0) {
 #pragma unroll
-        for (int e = 0; e < kSelPerThread; ++e) sh.cnt[tid + kSelThreads * e] = 0;
+        for (int e = 0; e < kSelPerThread; ++e) sh.u.cnt[tid + kSelThreads * e] = 0;
         __syncthreads();
         const uint32_t* hist = b.history + p.history_offset;
         for (uint32_t j = tid; j < p.history_len; j += kSelThreads) {
             const uint32_t id = hist[j];
-            if (id >= lo && id < hi) atomicAdd(&sh.cnt[id - lo], 1u);
+            if (id >= lo && id < hi) atomicAdd(&sh.u.cnt[id - lo], 1u);
         }
         __syncthreads();
         const float rp = p.repetition_penalty;
         const float limit = (p.softcap > 0.0f) ? p.softcap * 0.9999f : 0.0f;
 #pragma unroll
         for (int e = 0; e < kSelPerThread; ++e) {
-            const uint32_t n = sh.cnt[tid + kSelThreads * e];
+            const uint32_t n = sh.u.cnt[tid + kSelThreads * e];
             if (n == 0) continue;
             float x = v[e];
             for (uint32_t t = 0; t < n; ++t) {
@@ -295,22 +327,6 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelectBufs b, Selec
             return;
         }
         if (tid == 0) b.part_key[static_cast<size_t>(row) * parts + part] = k;
-        __threadfence();
-        __syncthreads();
-        if (tid == 0) sh.last = (atomicAdd(&b.row_counter[row], 1u) == parts - 1);
-        __syncthreads();
-        if (!sh.last) return;
-        __threadfence();
-        uint64_t m = 0;
-        for (uint32_t q = tid; q < parts; q += kSelThreads) {
-            const uint64_t o = __builtin_nontemporal_load(&b.part_key[static_cast<size_t>(row) * parts + q]);
-            m = o > m ? o : m;
-        }
-        m = block_max_u64(m, sh);
-        if (tid == 0) {
-            b.tokens[row] = rank_index(m);
-            b.row_counter[row] = 0;
-        }
         return;
     }
 
@@ -327,36 +343,39 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelectBufs b, Selec
             any = true;
         }
     }
+    __syncthreads();  // the penalty's counts are dead from here on: the region now holds values
+#pragma unroll
+    for (int e = 0; e < kSelPerThread; ++e) sh.u.val[tid + kSelThreads * e] = v[e];
     nan_seen = block_or_u32(nan_seen, sh);
     mx = block_max_f32(any ? mx : -INFINITY, sh);
     const double dmx = static_cast<double>(mx);
     double s = 0.0;
-#pragma unroll
-    for (int e = 0; e < kSelPerThread; ++e) {
-        const uint32_t i = lo + tid + kSelThreads * e;
-        if (i < hi) s += exp(static_cast<double>(v[e]) - dmx);
+    const uint32_t n_here = hi - lo;
+#pragma unroll 2
+    for (uint32_t e = 0; e < kSelPerThread; ++e) {
+        const uint32_t i = tid + kSelThreads * e;
+        if (i < n_here) s += exp(static_cast<double>(sh.u.val[i]) - dmx);
     }
     s = block_sum_f64(s, sh);
 
     // ---- shortlist of this slice, sampling.cpp:149-166 ----
     const uint32_t want_row = (p.top_k > 0) ? min(static_cast<uint32_t>(p.top_k), b.vocab)
                                             : min(kMaxWant, b.vocab);
-    const uint32_t want = min(want_row, hi - lo);
-    uint64_t K[kSelPerThread];
-#pragma unroll
-    for (int e = 0; e < kSelPerThread; ++e) {
-        const uint32_t i = lo + tid + kSelThreads * e;
-        K[e] = i < hi ? rank_key(v[e], i) : 0ull;
-    }
-    const uint64_t thr = block_select(K, want, sh);
+    const uint32_t want = min(want_row, n_here);
+    auto local_key = [&](uint32_t e) -> uint64_t {
+        const uint32_t i = tid + kSelThreads * e;
+        return i < n_here ? rank_key(sh.u.val[i], lo + i) : 0ull;
+    };
+    const uint64_t thr = block_select(kSelPerThread, local_key, want, sh);
     if (tid == 0) sh.misc[3] = 0;
     __syncthreads();
     uint64_t* out = (parts == 1) ? sh.top : b.cand + (static_cast<size_t>(row) * parts + part) * kMaxWant;
-#pragma unroll
-    for (int e = 0; e < kSelPerThread; ++e) {
-        if (K[e] != 0 && K[e] >= thr) {
+#pragma unroll 4
+    for (uint32_t e = 0; e < kSelPerThread; ++e) {
+        const uint64_t k = local_key(e);
+        if (k != 0 && k >= thr) {
             const uint32_t pos = atomicAdd(&sh.misc[3], 1u);
-            if (pos < want) out[pos] = K[e];  // exactly `want` ranks pass; the bound is a guard
+            if (pos < want) out[pos] = k;  // exactly `want` ranks pass; the bound is a guard
         }
     }
 
@@ -368,78 +387,83 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelectBufs b, Selec
             b.part_flag[o] = nan_seen;
             b.part_count[o] = want;
         }
-        __threadfence();
-        __syncthreads();
-        if (tid == 0) sh.last = (atomicAdd(&b.row_counter[row], 1u) == parts - 1);
-        __syncthreads();
-        if (!sh.last) return;
-        __threadfence();
-        // ---- merge the slices: max, rescaled sum, global shortlist ----
-        if (tid == 0) {
-            const size_t o = static_cast<size_t>(row) * parts;
-            float gm = __builtin_nontemporal_load(&b.part_max[o]);
-            uint32_t fl = __builtin_nontemporal_load(&b.part_flag[o]);
-            for (uint32_t q = 1; q < parts; ++q) {
-                const float x = __builtin_nontemporal_load(&b.part_max[o + q]);
-                gm = (gm < x) ? x : gm;
-                fl |= __builtin_nontemporal_load(&b.part_flag[o + q]);
-            }
-            double tot = 0.0;
-            for (uint32_t q = 0; q < parts; ++q)
-                tot += __builtin_nontemporal_load(&b.part_sum[o + q]) *
-                       exp(static_cast<double>(__builtin_nontemporal_load(&b.part_max[o + q])) -
-                           static_cast<double>(gm));
-            sh.gmax = gm;
-            sh.total = tot;
-            sh.flag = fl;
-        }
-        uint64_t K2[kMergePerThread];
-#pragma unroll
-        for (int j = 0; j < static_cast<int>(kMergePerThread); ++j) {
-            const uint32_t f = tid + kSelThreads * j;
-            const uint32_t q = f / kMaxWant, slot = f % kMaxWant;
-            K2[j] = 0;
-            if (q < parts) {
-                const size_t o = static_cast<size_t>(row) * parts + q;
-                if (slot < __builtin_nontemporal_load(&b.part_count[o]))
-                    K2[j] = __builtin_nontemporal_load(&b.cand[o * kMaxWant + slot]);
-            }
-        }
-        __syncthreads();
-        const uint64_t thr2 = block_select(K2, want_row, sh);
-        if (tid == 0) sh.misc[3] = 0;
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < static_cast<int>(kMergePerThread); ++j)
-            if (K2[j] != 0 && K2[j] >= thr2) {
-                const uint32_t pos = atomicAdd(&sh.misc[3], 1u);
-                if (pos < want_row) sh.top[pos] = K2[j];
-            }
-    } else if (tid == 0) {
+        return;  // select_merge_kernel finishes the row
+    }
+    if (tid == 0) {
         sh.gmax = mx;
         sh.total = s;
         sh.flag = nan_seen;
     }
     __syncthreads();
+    finish_row(sh, want_row, p, b.tokens + row);
+}
 
-    const bool degenerate = sh.flag != 0 || !(sh.total > 0.0);
-    if (degenerate) {
-        if (tid == 0) {
-            b.tokens[row] = TWD_TOKEN_DEGENERATE;
-            if (parts > 1) b.row_counter[row] = 0;
+// Second launch when a row spans several slices: global max, the rescaled sum of exponentials,
+// the global shortlist from every slice's candidates, then the draw. One block per row.
+__global__ __launch_bounds__(kSelThreads) void select_merge_kernel(SelectArgs args_by_value, SelectBufs b) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    SelectShared& sh = *reinterpret_cast<SelectShared*>(smem_raw);
+#if __HIP_DEVICE_COMPILE__
+    const SelectArgs& args =
+        *reinterpret_cast<const SelectArgs*>(__builtin_amdgcn_kernarg_segment_ptr());
+#else
+    const SelectArgs& args = args_by_value;
+#endif
+    const int tid = threadIdx.x;
+    const uint32_t row = blockIdx.x;
+    const uint32_t parts = args.parts;
+    const twd_row_params p = args.p[row];
+    const size_t o = static_cast<size_t>(row) * parts;
+
+    if (!(p.temperature > 0.0f)) {  // greedy: the best rank over the slices
+        uint64_t m = 0;
+        for (uint32_t q = tid; q < parts; q += kSelThreads) {
+            const uint64_t x = b.part_key[o + q];
+            m = x > m ? x : m;
         }
+        m = block_max_u64(m, sh);
+        if (tid == 0) b.tokens[row] = rank_index(m);
         return;
     }
-    uint32_t n2 = 1;
-    while (n2 < want_row) n2 <<= 1;
-    if (static_cast<uint32_t>(tid) >= want_row && static_cast<uint32_t>(tid) < n2) sh.top[tid] = 0;
-    __syncthreads();
-    block_sort_desc(sh, n2);
-    const uint32_t tok = finish_sampled(sh, want_row, p);
+    const uint32_t want_row = (p.top_k > 0) ? min(static_cast<uint32_t>(p.top_k), b.vocab)
+                                            : min(kMaxWant, b.vocab);
     if (tid == 0) {
-        b.tokens[row] = tok;
-        if (parts > 1) b.row_counter[row] = 0;
+        float gm = b.part_max[o];
+        uint32_t fl = b.part_flag[o];
+        for (uint32_t q = 1; q < parts; ++q) {
+            const float x = b.part_max[o + q];
+            gm = (gm < x) ? x : gm;
+            fl |= b.part_flag[o + q];
+        }
+        double tot = 0.0;
+        for (uint32_t q = 0; q < parts; ++q)
+            tot += b.part_sum[o + q] *
+                   exp(static_cast<double>(b.part_max[o + q]) - static_cast<double>(gm));
+        sh.gmax = gm;
+        sh.total = tot;
+        sh.flag = fl;
     }
+    for (uint32_t f = tid; f < kMaxParts * kMaxWant; f += kSelThreads) {
+        const uint32_t q = f / kMaxWant, slot = f % kMaxWant;
+        uint64_t k = 0;
+        if (q < parts && slot < b.part_count[o + q]) k = b.cand[(o + q) * kMaxWant + slot];
+        sh.u.cand[f] = k;
+    }
+    __syncthreads();
+    auto merge_key = [&](uint32_t e) -> uint64_t { return sh.u.cand[tid + kSelThreads * e]; };
+    const uint64_t thr = block_select(kMergePerThread, merge_key, want_row, sh);
+    if (tid == 0) sh.misc[3] = 0;
+    __syncthreads();
+#pragma unroll 4
+    for (uint32_t e = 0; e < kMergePerThread; ++e) {
+        const uint64_t k = merge_key(e);
+        if (k != 0 && k >= thr) {
+            const uint32_t pos = atomicAdd(&sh.misc[3], 1u);
+            if (pos < want_row) sh.top[pos] = k;
+        }
+    }
+    __syncthreads();
+    finish_row(sh, want_row, p, b.tokens + row);
 }
 
 __global__ void verify_compare_kernel(const uint32_t* row_tokens, uint32_t rows,
@@ -497,8 +521,6 @@ int scratch_alloc(SelectScratch* s, uint32_t max_vocab, uint32_t max_rows) {
     if (e == hipSuccess) e = hipMalloc(&s->part_count, n * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMalloc(&s->part_key, n * sizeof(uint64_t));
     if (e == hipSuccess) e = hipMalloc(&s->cand, n * kMaxWant * sizeof(uint64_t));
-    if (e == hipSuccess) e = hipMalloc(&s->row_counter, max_rows * sizeof(uint32_t));
-    if (e == hipSuccess) e = hipMemset(s->row_counter, 0, max_rows * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMalloc(&s->verify_tokens, (max_rows + 1) * sizeof(uint32_t));
     if (e != hipSuccess) {
         scratch_free(s);
@@ -514,7 +536,6 @@ void scratch_free(SelectScratch* s) {
     (void)hipFree(s->part_count);
     (void)hipFree(s->part_key);
     (void)hipFree(s->cand);
-    (void)hipFree(s->row_counter);
     (void)hipFree(s->verify_tokens);
     *s = SelectScratch{};
 }
@@ -553,10 +574,13 @@ int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_
     b.part_count = s.part_count;
     b.part_key = s.part_key;
     b.cand = s.cand;
-    b.row_counter = s.row_counter;
     const size_t smem = sizeof(SelectShared);
-    select_kernel<<<dim3(parts, rows), kSelThreads, smem, stream>>>(b, a);
+    select_slice_kernel<<<dim3(parts, rows), kSelThreads, smem, stream>>>(a, b);
     TWD_HIP(hipGetLastError());
+    if (parts > 1 && !penalty_only) {
+        select_merge_kernel<<<rows, kSelThreads, smem, stream>>>(a, b);
+        TWD_HIP(hipGetLastError());
+    }
     return TWD_OK;
 }
 
@@ -582,7 +606,10 @@ TWD_API int twd_selector_create(uint32_t max_vocab, uint32_t max_rows, twd_selec
     if (parts_for(max_vocab) > kMaxParts) return fail(TWD_E_UNSUPPORTED, "max_vocab above 1048576");
     static bool attr_done = false;
     if (!attr_done) {
-        TWD_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(select_kernel),
+        TWD_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(select_slice_kernel),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    static_cast<int>(sizeof(SelectShared))));
+        TWD_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(select_merge_kernel),
                                     hipFuncAttributeMaxDynamicSharedMemorySize,
                                     static_cast<int>(sizeof(SelectShared))));
         attr_done = true;

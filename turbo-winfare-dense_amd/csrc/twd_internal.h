@@ -107,7 +107,6 @@ struct SelectScratch {
     uint32_t* part_count = nullptr; // [rows][parts] candidates written
     uint64_t* part_key = nullptr;   // [rows][parts] greedy best rank
     uint64_t* cand = nullptr;       // [rows][parts][kMaxWant]
-    uint32_t* row_counter = nullptr;  // [rows], zero between calls
     uint32_t* verify_tokens = nullptr;  // [max_rows] scratch for twd_verify
 };
 

@@ -199,7 +199,10 @@ class Selector:
         if tokens is None:
             tokens = torch.empty(rows, dtype=torch.int32, device=logits.device)
         arr = _params_array(params)
-        _check(lib.twd_select(self.handle, _ptr(logits), vocab, rows, logits.stride(0), arr,
+        if logits.stride(1) != 1:
+            raise ValueError("logit rows must be contiguous")
+        stride = logits.stride(0) if rows > 1 else vocab  # a size-1 dim may carry any stride
+        _check(lib.twd_select(self.handle, _ptr(logits), vocab, rows, stride, arr,
                               _ptr(history), _ptr(tokens), _stream(stream)))
         return tokens
 
@@ -209,7 +212,10 @@ class Selector:
         rows, vocab = logits.shape
         if result is None:
             result = torch.zeros(VERIFY_WORDS, dtype=torch.int32, device=logits.device)
-        _check(lib.twd_verify(self.handle, _ptr(logits), vocab, rows, logits.stride(0),
+        if logits.stride(1) != 1:
+            raise ValueError("logit rows must be contiguous")
+        stride = logits.stride(0) if rows > 1 else vocab
+        _check(lib.twd_verify(self.handle, _ptr(logits), vocab, rows, stride,
                               C.byref(params), base_seed & 0xFFFFFFFFFFFFFFFF, _ptr(drafts),
                               0 if drafts is None else drafts.numel(), _ptr(result),
                               _stream(stream)))
