@@ -50,36 +50,20 @@ def hidden_pool(torch, dev, n, rows, seed):
     return torch.from_numpy(h.view(np.int16)).to(dev)
 
 
-class Timer:
-    """Per-launch HIP events on the current stream plus a region pair around the loop."""
-
-    def __init__(self, torch, n):
-        self.torch = torch
-        E = torch.cuda.Event
-        self.starts = [E(enable_timing=True) for _ in range(n)]
-        self.ends = [E(enable_timing=True) for _ in range(n)]
-        self.r0, self.r1 = E(enable_timing=True), E(enable_timing=True)
-
-    def launch_ms(self, n):
-        return [self.starts[i].elapsed_time(self.ends[i]) for i in range(n)]
-
-
-def time_loop(torch, steps, warmup, step_fn, kernel_fn=None):
-    """Runs warmup untimed steps, then `steps` timed ones. Returns (region_s, step launch ms
-    list). kernel_fn(i, start_evt, end_evt) brackets the dominant kernel when given."""
+def time_loop(torch, steps, warmup, step_fn):
+    """Runs `warmup` untimed steps, then `steps` timed ones bracketed by synchronize + HIP events
+    on the current stream (the stream every launch below uses). Returns seconds on the GPU
+    clock between the two events."""
     for i in range(warmup):
-        step_fn(i, None, None)
+        step_fn(i)
     torch.cuda.synchronize()
-    t = Timer(torch, steps)
-    t.r0.record()
-    wall0 = time.perf_counter()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
     for i in range(steps):
-        step_fn(warmup + i, t.starts[i], t.ends[i])
-    t.r1.record()
+        step_fn(warmup + i)
+    e1.record()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    region_s = t.r0.elapsed_time(t.r1) / 1e3
-    return region_s, wall, t.launch_ms(steps)
+    return e0.elapsed_time(e1) / 1e3
 
 
 def cpu_baseline(wsb_dev, hidden_rows, n_rows: int):
@@ -155,24 +139,17 @@ def main():
     hp = hidden_pool(torch, dev, 64, 1, 2)
     tok = torch.empty(1, dtype=torch.int32, device=dev)
 
-    def step2(i, e0, e1):
-        if e0 is not None:
-            e0.record()
+    def step2(i):
         head.greedy(hp[i % 64], tokens=tok, stream=stream)
-        if e1 is not None:
-            e1.record()
 
-    region_s, wall, launch_ms = time_loop(torch, args.steps, args.warmup, step2)
-    kern_s = float(np.mean(launch_ms)) / 1e3
+    region_s = time_loop(torch, args.steps, args.warmup, step2)
+    step_s = region_s / args.steps  # one launch per step: the mean launch-to-launch time
     rows_s = args.steps / region_s
     bytes2 = algorithmic_bytes(1)
-    results[2] = {"rows_per_s": rows_s, "ms_per_step": region_s * 1e3 / args.steps,
-                  "kernel_us_mean": kern_s * 1e6,
-                  "kernel_us_p10_p90": [float(np.percentile(launch_ms, 10)) * 1e3,
-                                        float(np.percentile(launch_ms, 90)) * 1e3],
-                  "hbm_frac": bytes2 / kern_s / PEAK_HBM}
-    log(f"config 2: {rows_s:.1f} rows/s, kernel {kern_s * 1e6:.1f} us, "
-        f"{bytes2 / kern_s / 1e12:.2f} TB/s")
+    results[2] = {"rows_per_s": rows_s, "ms_per_step": step_s * 1e3,
+                  "kernel_us_mean": step_s * 1e6, "hbm_frac": bytes2 / step_s / PEAK_HBM}
+    log(f"config 2: {rows_s:.1f} rows/s, {step_s * 1e6:.1f} us per launch, "
+        f"{bytes2 / step_s / 1e12:.2f} TB/s")
 
     # ---- config 1: selection only over one fp32 row (1 MB): greedy, then T=.8 k=64 p=.95 u=.37 ----
     if 1 in cfgs:
@@ -186,15 +163,11 @@ def main():
         p_s = [twd.RowParams(0.8, 0.95, 64, 1.0, 0.37, CAP, 0, 0)]
         out = {}
         for name, pr in (("greedy", p_g), ("sampled", p_s)):
-            def step1(i, e0, e1, pr=pr):
-                if e0 is not None:
-                    e0.record()
+            def step1(i, pr=pr):
                 sel.select(zr, pr, tokens=t1, stream=stream)
-                if e1 is not None:
-                    e1.record()
             n1 = max(50, args.steps // 4)
-            r_s, _, lm = time_loop(torch, n1, 10, step1)
-            out[name] = {"us_per_row": r_s / n1 * 1e6, "kernel_us_mean": float(np.mean(lm)) * 1e3}
+            r_s = time_loop(torch, n1, 10, step1)
+            out[name] = {"us_per_row": r_s / n1 * 1e6}
         results[1] = out
 
     # ---- config 3: M=1 full chain, rp 1.1 over a 4096-id history, T=.7 k=40 p=.9, 1000 steps --
@@ -211,18 +184,13 @@ def main():
         prm = [[twd.RowParams(0.7, 0.9, 40, 1.1, twd.uniform_from_seed(twd.seed_for(sp, 4096 + i)),
                               CAP, i, 4096)] for i in range(n3 + 20)]
 
-        def step3(i, e0, e1):
-            if e0 is not None:
-                e0.record()
+        def step3(i):
             head.sample(hp3[i % n3], prm[i % len(prm)], history=hist, logits=lg3, tokens=t3,
                         stream=stream)
-            if e1 is not None:
-                e1.record()
 
-        r_s, _, lm = time_loop(torch, n3, 20, step3)
+        r_s = time_loop(torch, n3, 20, step3)
         b3 = algorithmic_bytes(1, 4096)
         results[3] = {"rows_per_s": n3 / r_s, "ms_per_step": r_s * 1e3 / n3,
-                      "step_us_mean": float(np.mean(lm)) * 1e3,
                       "hbm_frac": b3 / (r_s / n3) / PEAK_HBM}
 
     # ---- config 4: M=5 greedy verify of 4 drafts ------------------------------------------------
@@ -232,19 +200,14 @@ def main():
         drafts = torch.from_numpy(np.random.default_rng(4).integers(0, V, (64, 4)).astype(np.int32)).to(dev)
         res4 = torch.zeros(twd.twd.VERIFY_WORDS, dtype=torch.int32, device=dev)
 
-        def step4(i, e0, e1):
-            if e0 is not None:
-                e0.record()
+        def step4(i):
             head.verify_greedy(hp4[i % 64], drafts[i % 64], result=res4, stream=stream)
-            if e1 is not None:
-                e1.record()
 
         n4 = max(100, args.steps // 2)
-        r_s, _, lm = time_loop(torch, n4, 20, step4)
-        k4 = float(np.mean(lm)) / 1e3
-        results[4] = {"rows_per_s": 5 * n4 / r_s, "ms_per_step": r_s * 1e3 / n4,
-                      "kernel_us_mean": k4 * 1e6,
-                      "hbm_frac": algorithmic_bytes(5) / k4 / PEAK_HBM}
+        r_s = time_loop(torch, n4, 20, step4)
+        k4 = r_s / n4
+        results[4] = {"rows_per_s": 5 * n4 / r_s, "ms_per_step": k4 * 1e3,
+                      "kernel_us_mean": k4 * 1e6, "hbm_frac": algorithmic_bytes(5) / k4 / PEAK_HBM}
 
     # ---- config 5: M=64 rows, each with own T/k/p, rp 1.1 over its own 2048-id history ---------
     if 5 in cfgs:
@@ -258,27 +221,17 @@ def main():
                 for m in range(64)]
         lg5 = torch.empty(64, V, dtype=torch.float32, device=dev)
         t5 = torch.empty(64, dtype=torch.int32, device=dev)
-        kt0, kt1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
-        def step5(i, e0, e1):
-            if e0 is not None:
-                e0.record()
+        def step5(i):
             head.sample(hp5[i % 8], prm5, history=hist5, logits=lg5, tokens=t5, stream=stream)
-            if e1 is not None:
-                e1.record()
 
         n5 = max(50, args.steps // 8)
-        r_s, _, lm = time_loop(torch, n5, 10, step5)
+        r_s = time_loop(torch, n5, 10, step5)
 
-        def head5(i, e0, e1):
-            if e0 is not None:
-                e0.record()
+        def head5(i):
             head.logits(hp5[i % 8], out=lg5, stream=stream)
-            if e1 is not None:
-                e1.record()
 
-        _, _, lmh = time_loop(torch, n5, 5, head5)
-        kh = float(np.mean(lmh)) / 1e3
+        kh = time_loop(torch, n5, 5, head5) / n5
         b5 = algorithmic_bytes(64, 2048) + 64 * V * 4  # the fp32 logits are written
         results[5] = {"rows_per_s": 64 * n5 / r_s, "ms_per_step": r_s * 1e3 / n5,
                       "head_kernel_us_mean": kh * 1e6,
@@ -292,7 +245,7 @@ def main():
         cpu = cpu_baseline(wsb, hp[: args.cpu_rows].cpu().numpy().view(np.uint16).reshape(-1, D),
                            args.cpu_rows)
 
-    achieved = bytes2 / kern_s
+    achieved = bytes2 / step_s
     line = {
         "metric": "LM-head+sample rows/s at d=5376,V=262144 INT4; % HBM roofline",
         "value": results[2]["rows_per_s"],
@@ -313,7 +266,7 @@ def main():
                               f"{SEED})"},
         "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9,
                      "unit": "GB/s", "frac": achieved / PEAK_HBM, "traffic": None,
-                     "kernel": "head_small_kernel<1,2,4,1> + head_finish_kernel (M=1 greedy)",
+                     "kernel": "head_small_kernel<1,2,4,1> (M=1 greedy, single launch)",
                      "bytes_per_launch": bytes2},
         "cpu_baseline": cpu,
         "configs": {str(k): results[k] for k in sorted(results)},

@@ -36,8 +36,48 @@ struct HeadArgs {
     float softcap;
     float* logits;
     uint32_t vocab;
-    uint64_t* partial;  // [TWD_MAX_ROWS][gridDim.x]
+    // greedy finish: running per-row maxima and the arrival count, both zero between
+    // launches, and where the last block puts its results
+    uint64_t* gbest;    // [TWD_MAX_ROWS]
+    uint32_t* gcount;
+    uint32_t* tokens;
+    const uint32_t* drafts;
+    uint32_t n_drafts;
+    twd_verify_result* vres;
 };
+
+// speculator.cpp:91-114 and :183-195, greedy branch, over per-row target tokens tok[0..rows).
+__device__ void verify_bookkeeping(const uint32_t* tok, uint32_t rows, const uint32_t* drafts,
+                                   uint32_t nd, twd_verify_result* v) {
+    uint32_t n = 0, acc = 0, bonus = 0, sampled = 0;
+    if (nd != 0 && rows != 0) {
+        const uint32_t k = nd < rows ? nd : rows;
+        bool rejected = false;
+        for (uint32_t i = 0; i < k; ++i) {
+            const uint32_t t = tok[i];
+            if (drafts[i] == t) {
+                v->tokens[n++] = t;
+                ++acc;
+            } else {
+                bonus = t;
+                sampled = 1;
+                v->tokens[n++] = t;
+                rejected = true;
+                break;
+            }
+        }
+        if (!rejected && rows > k) {
+            bonus = tok[k];
+            sampled = 1;
+            v->tokens[n++] = bonus;
+        }
+    }
+    v->n_tokens = n;
+    v->num_accepted = acc;
+    v->total_drafted = nd;
+    v->bonus_token_sampled = sampled;
+    v->bonus_token = bonus;
+}
 
 // 8 nibbles of one word -> 8 bf16 values 128+q, in k-slot order [0,4,1,5,2,6,3,7].
 __device__ __forceinline__ bf16x8_t nibbles_to_bf16(uint32_t w) {
@@ -75,12 +115,21 @@ __device__ __forceinline__ float sum8_bf16(u32x4_t v) {
 // Shared memory of the head epilogue (cross-wave greedy reduction).
 struct EpiShared {
     uint64_t red[kHeadWaves][TWD_MAX_ROWS];
+    uint64_t seen[TWD_MAX_ROWS];
+    uint32_t tok[TWD_MAX_ROWS];
+    int last;
 };
 
-// Softcap, logits store, and -- for the greedy modes -- the block's per-row rank maximum,
-// written to partial[m][block]. head_finish_kernel reduces the blocks in a second launch: a
-// per-block device-scope fence plus a global counter (the "last block" pattern) serialises on
-// this part's memory-side atomics and costs more than the whole streaming pass.
+// Softcap, logits store, and -- for the greedy modes -- the per-row rank maximum over the
+// whole grid, finished by the last block to arrive (tokens, then greedy verify bookkeeping).
+//
+// Cross-block publication uses device-scope atomics only: each block folds its ranks into
+// gbest[m] with a returning atomic max, then counts itself in with an atomic add; the block that
+// sees the final count reads and clears gbest with atomic exchanges. Returning atomics are
+// performed at the memory-side coherence point before they return, so every block's maxima
+// precede its arrival, and the last block observes all of them. No data travels through plain
+// stores, so no device-scope fence is needed: on this part such a fence writes back the XCD's
+// L2 and, paid by each of ~1000 blocks, costs more than the streaming pass itself.
 // tot[j][mt][i] holds row r = (tile0 + j) * 16 + lane % 16 of m = 16 mt + 4 (lane / 16) + i.
 template <int NMT, int NI, int RT, int MODE>
 __device__ __forceinline__ void head_epilogue(const HeadArgs& a, f32x4_t (&tot)[RT][NMT],
@@ -132,9 +181,30 @@ __device__ __forceinline__ void head_epilogue(const HeadArgs& a, f32x4_t (&tot)[
         uint64_t k = se.red[0][tid];
 #pragma unroll
         for (int w = 1; w < kHeadWaves; ++w) k = se.red[w][tid] > k ? se.red[w][tid] : k;
-        a.partial[static_cast<size_t>(tid) * nb + blockIdx.x] = k;
+        // the returning form: the maximum is performed before this block counts itself in
+        se.seen[tid] = __hip_atomic_fetch_max(reinterpret_cast<unsigned long long*>(a.gbest + tid),
+                                              static_cast<unsigned long long>(k), __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
     }
-
+    __syncthreads();
+    if (tid == 0)
+        se.last = __hip_atomic_fetch_add(a.gcount, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                  nb - 1;
+    __syncthreads();
+    if (!se.last) return;
+    // every other block's maximum was performed before its arrival was counted
+    if (static_cast<uint32_t>(tid) < a.M) {
+        const uint64_t k = __hip_atomic_exchange(reinterpret_cast<unsigned long long*>(a.gbest + tid),
+                                                 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t t = rank_index(k);
+        se.tok[tid] = t;
+        if (a.tokens) a.tokens[tid] = t;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        __hip_atomic_exchange(a.gcount, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (a.vres) verify_bookkeeping(se.tok, a.M, a.drafts, a.n_drafts, a.vres);
+    }
 }
 
 // Per-chunk math shared by both kernels: one unit of one row tile (4 words per lane = 4 MFMA
@@ -161,6 +231,26 @@ __device__ __forceinline__ void unit_mac(const u32x4_t& w, const u32x2_t& sb,
             for (int i = 0; i < NI; ++i)
                 tot[mt][i] = fmaf(s, acc[i], fmaf(tb, xv[g][mt][i], tot[mt][i]));
         }
+    }
+}
+
+// One 64-column group (two MFMA k-steps) of one row tile: words w0, w1 of the unit, the
+// group's scale and bias from sb (g selects the half), A fragments av[mt][t] and X sums xv[mt].
+template <int NMT, int NI>
+__device__ __forceinline__ void group_mac(uint32_t w0, uint32_t w1, const u32x2_t& sb, int g,
+                                          const bf16x8_t (&av)[NMT][2], const f32x4_t (&xv)[NMT],
+                                          f32x4_t (&tot)[NMT]) {
+    const bf16x8_t b0 = nibbles_to_bf16(w0), b1 = nibbles_to_bf16(w1);
+    const float s = g == 0 ? bf16_lo(sb.x) : bf16_hi(sb.x);
+    const float b = g == 0 ? bf16_lo(sb.y) : bf16_hi(sb.y);
+    const float tb = fmaf(-128.0f, s, b);
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt) {
+        f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt][0], b0, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt][1], b1, acc, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) tot[mt][i] = fmaf(s, acc[i], fmaf(tb, xv[mt][i], tot[mt][i]));
     }
 }
 
@@ -254,14 +344,17 @@ __global__ __launch_bounds__(kHeadThreads) void head_small_kernel(HeadArgs a) {
     head_epilogue<1, NI, RT, MODE>(a, tot, tile0, se);
 }
 
-// ---- any M <= 64: h staged through LDS one 128-column chunk at a time ---------------------------
+// ---- any M <= 64: h staged through LDS, PF chunks of 128 columns at a time ---------------------
 //
 // Block = 4 waves; wave w owns RT consecutive 16-row tiles. NMT = number of 16-wide m tiles
 // (1 for M <= 16, 4 for M <= 64); NI = accumulator lanes per m tile that can hold a live row.
-template <int NMT, int NI, int RT, int MODE>
-__global__ __launch_bounds__(kHeadThreads) void head_kernel(HeadArgs a) {
-    __shared__ u32x4_t sA[2][NMT][4][64];
-    __shared__ float sX[2][2][NMT * 16];
+// A stage is PF chunks: one barrier per stage, h for the next stage loaded into registers while
+// this one computes, and a PF-deep register ring of weight units per row tile.
+template <int NMT, int NI, int RT, int PF, int MODE>
+__global__ __launch_bounds__(kHeadThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void head_kernel(HeadArgs a) {
+    __shared__ u32x4_t sA[2][PF][NMT][4][64];
+    __shared__ float sX[2][PF][2][NMT * 16];
     __shared__ EpiShared se;
 
     const int tid = threadIdx.x;
@@ -269,132 +362,84 @@ __global__ __launch_bounds__(kHeadThreads) void head_kernel(HeadArgs a) {
     const int lane = tid & 63;
     const uint32_t tile0 = (blockIdx.x * kHeadWaves + wave) * RT;
 
-    // ---- h staging: chunk U of every live row, permuted, plus its two group sums ----
-    u32x4_t hv[NMT];
-    auto stage_load = [&](uint32_t U) {
+    // ---- h staging: chunks [S*PF, S*PF + PF) of every live row, permuted, with group sums ----
+    u32x4_t hv[PF][NMT];
+    auto stage_load = [&](uint32_t S) {
 #pragma unroll
-        for (int it = 0; it < NMT; ++it) {
-            const int task = tid + kHeadThreads * it;
-            const int m = task >> 4, c = task & 15;
-            hv[it] = u32x4_t{0u, 0u, 0u, 0u};
-            if (m < static_cast<int>(a.M))
-                hv[it] = *reinterpret_cast<const u32x4_t*>(a.h + static_cast<size_t>(m) * a.d +
-                                                           U * kChunkK + c * 8);
-        }
+        for (int u = 0; u < PF; ++u)
+#pragma unroll
+            for (int it = 0; it < NMT; ++it) {
+                const int task = tid + kHeadThreads * it;
+                const int m = task >> 4, c = task & 15;
+                const uint32_t U = S * PF + u;
+                hv[u][it] = u32x4_t{0u, 0u, 0u, 0u};
+                if (m < static_cast<int>(a.M) && U < a.nunits)
+                    hv[u][it] = *reinterpret_cast<const u32x4_t*>(
+                        a.h + static_cast<size_t>(m) * a.d + U * kChunkK + c * 8);
+            }
     };
     auto stage_store = [&](int buf) {
 #pragma unroll
-        for (int it = 0; it < NMT; ++it) {
-            const int task = tid + kHeadThreads * it;
-            const int m = task >> 4, c = task & 15;
-            float s = sum8_bf16(hv[it]);
-            s += __shfl_xor(s, 1);
-            s += __shfl_xor(s, 2);
-            s += __shfl_xor(s, 4);
-            sA[buf][m >> 4][c >> 2][(c & 3) * 16 + (m & 15)] = permute_h(hv[it]);
-            if ((c & 7) == 0) sX[buf][c >> 3][m] = s;
-        }
+        for (int u = 0; u < PF; ++u)
+#pragma unroll
+            for (int it = 0; it < NMT; ++it) {
+                const int task = tid + kHeadThreads * it;
+                const int m = task >> 4, c = task & 15;
+                float s = sum8_bf16(hv[u][it]);
+                s += __shfl_xor(s, 1);
+                s += __shfl_xor(s, 2);
+                s += __shfl_xor(s, 4);
+                sA[buf][u][m >> 4][c >> 2][(c & 3) * 16 + (m & 15)] = permute_h(hv[u][it]);
+                if ((c & 7) == 0) sX[buf][u][c >> 3][m] = s;
+            }
     };
 
-    u32x4_t wq[RT];
-    u32x2_t sq[RT];
     f32x4_t tot[RT][NMT];
 #pragma unroll
     for (int j = 0; j < RT; ++j)
 #pragma unroll
         for (int mt = 0; mt < NMT; ++mt) tot[j][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+    u32x4_t wq[PF][RT];
+    u32x2_t sq[PF][RT];
+#pragma unroll
+    for (int u = 0; u < PF; ++u)
+        if (static_cast<uint32_t>(u) < a.nunits) load_unit<RT>(a, tile0, u, lane, wq[u], sq[u]);
     stage_load(0);
     stage_store(0);
-    load_unit<RT>(a, tile0, 0, lane, wq, sq);
 
-    for (uint32_t U = 0; U < a.nunits; ++U) {
+    const uint32_t nstages = (a.nunits + PF - 1) / PF;
+    for (uint32_t S = 0; S < nstages; ++S) {
         __syncthreads();
-        const int buf = U & 1;
-        const bool more = (U + 1) < a.nunits;
-        u32x4_t wn[RT];
-        u32x2_t sn[RT];
-        if (more) {
-            stage_load(U + 1);
-            load_unit<RT>(a, tile0, U + 1, lane, wn, sn);
-        }
-        bf16x8_t av[NMT][4];
+        const int buf = S & 1;
+        const bool more = (S + 1) < nstages;
+        if (more) stage_load(S + 1);
 #pragma unroll
-        for (int mt = 0; mt < NMT; ++mt)
+        for (int u = 0; u < PF; ++u) {
+            const uint32_t U = S * PF + u;
+            if (U >= a.nunits) break;
+            // one 64-column group at a time keeps only its two k-steps of A and X live
 #pragma unroll
-            for (int t = 0; t < 4; ++t) av[mt][t] = __builtin_bit_cast(bf16x8_t, sA[buf][mt][t][lane]);
-        f32x4_t xv[2][NMT];
+            for (int g = 0; g < 2; ++g) {
+                bf16x8_t av[NMT][2];
 #pragma unroll
-        for (int g = 0; g < 2; ++g)
+                for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
-            for (int mt = 0; mt < NMT; ++mt)
-                xv[g][mt] = *reinterpret_cast<const f32x4_t*>(&sX[buf][g][mt * 16 + 4 * (lane >> 4)]);
+                    for (int t = 0; t < 2; ++t)
+                        av[mt][t] = __builtin_bit_cast(bf16x8_t, sA[buf][u][mt][2 * g + t][lane]);
+                f32x4_t xv[NMT];
 #pragma unroll
-        for (int j = 0; j < RT; ++j) unit_mac<NMT, NI>(wq[j], sq[j], av, xv, tot[j]);
-        if (more) {
-            stage_store(buf ^ 1);
+                for (int mt = 0; mt < NMT; ++mt)
+                    xv[mt] = *reinterpret_cast<const f32x4_t*>(&sX[buf][u][g][mt * 16 + 4 * (lane >> 4)]);
 #pragma unroll
-            for (int j = 0; j < RT; ++j) {
-                wq[j] = wn[j];
-                sq[j] = sn[j];
+                for (int j = 0; j < RT; ++j)
+                    group_mac<NMT, NI>(wq[u][j][2 * g], wq[u][j][2 * g + 1], sq[u][j], g, av, xv, tot[j]);
             }
+            if (U + PF < a.nunits) load_unit<RT>(a, tile0, U + PF, lane, wq[u], sq[u]);
         }
+        if (more) stage_store(buf ^ 1);
     }
     head_epilogue<NMT, NI, RT, MODE>(a, tot, tile0, se);
-}
-
-// Greedy tokens from the per-block ranks, then greedy verify bookkeeping
-// (speculator.cpp:91-114 and :183-195). One block; wave w reduces rows w, w+4, ...
-__global__ __launch_bounds__(kHeadThreads) void head_finish_kernel(
-    const uint64_t* __restrict__ partial, uint32_t nb, uint32_t M, uint32_t* tokens,
-    const uint32_t* drafts, uint32_t n_drafts, twd_verify_result* vres) {
-    __shared__ uint32_t sTok[TWD_MAX_ROWS];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    for (uint32_t m = wave; m < M; m += kHeadWaves) {
-        uint64_t k = 0;
-        for (uint32_t b = lane; b < nb; b += 64) {
-            const uint64_t o = partial[static_cast<size_t>(m) * nb + b];
-            k = o > k ? o : k;
-        }
-        k = wave_max_u64(k);
-        if (lane == 0) {
-            const uint32_t tok = rank_index(k);
-            sTok[m] = tok;
-            if (tokens) tokens[m] = tok;
-        }
-    }
-    __syncthreads();
-    if (tid != 0 || !vres) return;
-    twd_verify_result* v = vres;
-    const uint32_t nd = n_drafts, rows = M;
-    uint32_t n = 0, acc = 0, bonus = 0, sampled = 0;
-    if (nd != 0 && rows != 0) {
-        const uint32_t k = nd < rows ? nd : rows;
-        bool rejected = false;
-        for (uint32_t i = 0; i < k; ++i) {
-            const uint32_t t = sTok[i];
-            if (drafts[i] == t) {
-                v->tokens[n++] = t;
-                ++acc;
-            } else {
-                bonus = t;
-                sampled = 1;
-                v->tokens[n++] = t;
-                rejected = true;
-                break;
-            }
-        }
-        if (!rejected && rows > k) {
-            bonus = sTok[k];
-            sampled = 1;
-            v->tokens[n++] = bonus;
-        }
-    }
-    v->n_tokens = n;
-    v->num_accepted = acc;
-    v->total_drafted = nd;
-    v->bonus_token_sampled = sampled;
-    v->bonus_token = bonus;
 }
 
 // ---- layout repack: reference [W|S|B] -> units ----------------------------------------------
@@ -474,17 +519,18 @@ struct twd_head {
     float softcap = 0.f;
     uint8_t* tiled = nullptr;
     uint64_t tiled_bytes = 0;
-    uint64_t* partial = nullptr;  // [TWD_MAX_ROWS][max blocks]
-    uint32_t max_blocks = 0;
+    uint64_t* gbest = nullptr;    // [TWD_MAX_ROWS] + arrival counter, zero between launches
     twd_selector* sel = nullptr;
 };
 
 namespace {
 
-constexpr int kRT1 = 4;   // row tiles per wave, chunked kernel, M <= 16
-constexpr int kRT4 = 2;   // row tiles per wave, chunked kernel, M <= 64
+// staged-h kernel: row tiles per wave, units per stage (measured: M = 16 -> 4 x 2, 155 us;
+// M = 64 -> 2 x 2, 446 us greedy)
+constexpr int kRT1 = 4, kPF1 = 2;  // M <= 16
+constexpr int kRT4 = 2, kPF4 = 2;  // M <= 64
 // resident-h kernel: row tiles per wave and weight units in flight (measured best on MI355X:
-// M = 1 -> 2 tiles x 4 units, 126 us; M = 5 -> 4 tiles x 2 units, 165 us)
+// M = 1 -> 2 tiles x 4 units, 122-136 us; M = 5 -> 4 tiles x 2 units, 155-165 us)
 constexpr int kRTS1 = 2, kPFS1 = 4;  // M == 1
 constexpr int kRTS4 = 4, kPFS4 = 2;  // 2 <= M <= 8
 constexpr uint32_t kSmallMaxRows = 8;
@@ -535,10 +581,9 @@ int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
     h->ntiles = (vocab + kTileRows - 1) / kTileRows;
     h->nunits = d / kChunkK;
     h->tiled_bytes = static_cast<uint64_t>(h->ntiles) * h->nunits * kUnitBytes;
-    h->max_blocks = std::max({blocks_for(h->ntiles, kRT1), blocks_for(h->ntiles, kRT4),
-                              blocks_for(h->ntiles, kRTS1), blocks_for(h->ntiles, kRTS4)});
     hipError_t e = hipMalloc(&h->tiled, h->tiled_bytes);
-    if (e == hipSuccess) e = hipMalloc(&h->partial, sizeof(uint64_t) * TWD_MAX_ROWS * h->max_blocks);
+    if (e == hipSuccess) e = hipMalloc(&h->gbest, sizeof(uint64_t) * (TWD_MAX_ROWS + 1));
+    if (e == hipSuccess) e = hipMemset(h->gbest, 0, sizeof(uint64_t) * (TWD_MAX_ROWS + 1));
     if (e != hipSuccess) {
         twd_head_destroy(h);
         return hip_fail(e, "allocating the LM head");
@@ -583,30 +628,24 @@ int launch_head(twd_head* h, const uint16_t* hidden, uint32_t rows, float* logit
     a.softcap = h->softcap;
     a.logits = logits;
     a.vocab = h->vocab;
-    a.partial = h->partial;
-    if (rows <= kSmallMaxRows) {
-        const size_t smem = small_smem_bytes(rows, h->d);
-        if (rows == 1)
-            head_small_kernel<1, kRTS1, kPFS1, MODE>
-                <<<blocks_for(h->ntiles, kRTS1), kHeadThreads, smem, stream>>>(a);
-        else
-            head_small_kernel<4, kRTS4, kPFS4, MODE>
-                <<<blocks_for(h->ntiles, kRTS4), kHeadThreads, smem, stream>>>(a);
+    a.gbest = h->gbest;
+    a.gcount = reinterpret_cast<uint32_t*>(h->gbest + TWD_MAX_ROWS);
+    a.tokens = tokens;
+    a.drafts = drafts;
+    a.n_drafts = n_drafts;
+    a.vres = vres;
+    if (rows == 1) {
+        head_small_kernel<1, kRTS1, kPFS1, MODE><<<blocks_for(h->ntiles, kRTS1), kHeadThreads,
+                                                   small_smem_bytes(rows, h->d), stream>>>(a);
+    } else if (rows <= kSmallMaxRows) {
+        head_small_kernel<4, kRTS4, kPFS4, MODE><<<blocks_for(h->ntiles, kRTS4), kHeadThreads,
+                                                   small_smem_bytes(rows, h->d), stream>>>(a);
     } else if (rows <= 16) {
-        head_kernel<1, 4, kRT1, MODE><<<blocks_for(h->ntiles, kRT1), kHeadThreads, 0, stream>>>(a);
+        head_kernel<1, 4, kRT1, kPF1, MODE><<<blocks_for(h->ntiles, kRT1), kHeadThreads, 0, stream>>>(a);
     } else {
-        head_kernel<4, 4, kRT4, MODE><<<blocks_for(h->ntiles, kRT4), kHeadThreads, 0, stream>>>(a);
+        head_kernel<4, 4, kRT4, kPF4, MODE><<<blocks_for(h->ntiles, kRT4), kHeadThreads, 0, stream>>>(a);
     }
     TWD_HIP(hipGetLastError());
-    if (MODE == kModeGreedy) {
-        const uint32_t nb = rows == 1             ? blocks_for(h->ntiles, kRTS1)
-                          : rows <= kSmallMaxRows ? blocks_for(h->ntiles, kRTS4)
-                          : rows <= 16            ? blocks_for(h->ntiles, kRT1)
-                                                  : blocks_for(h->ntiles, kRT4);
-        head_finish_kernel<<<1, kHeadThreads, 0, stream>>>(h->partial, nb, rows, tokens, drafts,
-                                                           n_drafts, vres);
-        TWD_HIP(hipGetLastError());
-    }
     return TWD_OK;
 }
 
@@ -671,7 +710,7 @@ TWD_API int twd_head_create(const void* wsb_host, uint64_t wsb_bytes, uint32_t v
 TWD_API void twd_head_destroy(twd_head* h) {
     if (!h) return;
     if (h->tiled) (void)hipFree(h->tiled);
-    if (h->partial) (void)hipFree(h->partial);
+    if (h->gbest) (void)hipFree(h->gbest);
     if (h->sel) twd_selector_destroy(h->sel);
     delete h;
 }
