@@ -90,6 +90,19 @@ def cpu_baseline(wsb_dev, hidden_rows, n_rows: int):
                       f"nproc={os.cpu_count()}"}
 
 
+def measured_traffic():
+    """HBM bytes per launch of the config-2 kernel from the committed PMC summary
+    (FETCH_SIZE and WRITE_SIZE passes, calibrated on a 1 GiB copy), or None."""
+    path = os.path.join(ROOT, "profiles", "head_m1_greedy_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1]), "profiles/head_m1_greedy_traffic.md"
+    except OSError:
+        pass
+    return None, None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -246,6 +259,7 @@ def main():
                            args.cpu_rows)
 
     achieved = bytes2 / step_s
+    traffic, traffic_src = measured_traffic()
     line = {
         "metric": "LM-head+sample rows/s at d=5376,V=262144 INT4; % HBM roofline",
         "value": results[2]["rows_per_s"],
@@ -265,7 +279,8 @@ def main():
                    "weights": "q~U{0..15}, s~U(1e-3,1e-2) bf16, b=-8s (twd_generate_head seed "
                               f"{SEED})"},
         "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9,
-                     "unit": "GB/s", "frac": achieved / PEAK_HBM, "traffic": None,
+                     "unit": "GB/s", "frac": achieved / PEAK_HBM, "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "kernel": "head_small_kernel<1,2,4,1> (M=1 greedy, single launch)",
                      "bytes_per_launch": bytes2},
         "cpu_baseline": cpu,
