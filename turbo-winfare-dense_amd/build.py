@@ -20,8 +20,11 @@ SOURCES = ["csrc/head.hip", "csrc/select.hip", "csrc/host.cpp", "csrc/g4dense_ap
 ARCH = os.environ.get("TWD_OFFLOAD_ARCH", "gfx950")
 
 # Packed-fp32 VALU forms are kept out of the code object: hipcc would otherwise pair fp32 adds
-# and multiplies into v_pk_* instructions on its own.
-DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# and multiplies into v_pk_* instructions on its own. MFMA results stay in ordinary VGPRs: the
+# head kernels read every accumulator back on the VALU, and accumulation registers would cost
+# a copy per read.
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                "-mllvm", "-amdgpu-mfma-vgpr-form"]
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden", "-Wall",
           f"--offload-arch={ARCH}", "-I" + os.path.join(ROOT, "include"),
           "-I" + os.path.join(HERE, "csrc")]

@@ -1,13 +1,17 @@
 // The tied INT4 group-64 LM head on gfx950: layout repack, synthetic generator, and the fused
-// dequant-GEMM kernel (softcap, greedy argmax and greedy verify in its epilogue).
+// dequant-GEMM kernels (softcap, greedy argmax and greedy verify in their epilogue).
 //
 // Arithmetic (reference: shaders/Common.hlsli:163-222, src/cpu_reference.cpp:643-665):
 //   logit[m][r] = sum_g s[r][g] * sum_{c in g} q[r][c] * h[m][c]  +  b[r][g] * X[m][g],
 //   X[m][g] = sum_{c in g} h[m][c],  then softcap*tanh(logit/softcap).
-// The inner sums run on MFMA (v_mfma_f32_16x16x32_bf16): nibbles become the exact bf16 values
-// 128 + q with one and-or per pair, h is already bf16, so every product is exact and the
-// accumulation is fp32. The +128 offset is removed per group through X:
-//   sum (128+q) h = 128 X + sum q h  =>  logit += s * acc + (b - 128 s) * X.
+// Both sums run on MFMA (v_mfma_f32_16x16x32_bf16) with fp32 accumulation and exact products:
+//   * weights: a nibble pair becomes the exact bf16 values 128 + q with one and-or;
+//   * h enters as -h/128 (exact), so one group's MFMA chain gives acc = -(128 X + sum q h)/128
+//     and, with t = -128 s stored in the unit, t * acc = s * sum q h + 128 s X;
+//   * the bias term (b - 128 s) X runs as a second MFMA stream: X is split into three bf16
+//     slices hi + mid + lo (exact to fp32), paired against the stored word {b, t}, four groups
+//     per K=32 MFMA.
+// Per group and output element that leaves one fp32 FMA on the VALU: tot += t * acc.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -79,24 +83,48 @@ __device__ void verify_bookkeeping(const uint32_t* tok, uint32_t rows, const uin
     v->bonus_token = bonus;
 }
 
-// 8 nibbles of one word -> 8 bf16 values 128+q, in k-slot order [0,4,1,5,2,6,3,7].
-__device__ __forceinline__ bf16x8_t nibbles_to_bf16(uint32_t w) {
-    const uint32_t m = 0x000F000Fu, e = 0x43004300u;
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+    if (f != f) return 0x7FC0u;
+    uint32_t u = __float_as_uint(f);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+// A VGPR holding c, opaque to constant folding. (w & mask) | c only becomes a single
+// v_and_or_b32 when c sits in a register: a VOP3 op on this target encodes no literal.
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t c) {
+    uint32_t r;
+    asm("v_mov_b32 %0, %1" : "=v"(r) : "i"(c));
+    return r;
+}
+
+// 8 nibbles of one word -> 8 bf16 values 128+q, in k-slot order [0,4,1,5,2,6,3,7]. magic holds
+// 0x43004300 (bf16 128.0 twice).
+__device__ __forceinline__ bf16x8_t nibbles_to_bf16(uint32_t w, uint32_t magic) {
+    const uint32_t m = 0x000F000Fu;
     u32x4_t p;
-    p.x = (w & m) | e;
-    p.y = ((w >> 4) & m) | e;
-    p.z = ((w >> 8) & m) | e;
-    p.w = ((w >> 12) & m) | e;
+    p.x = (w & m) | magic;
+    p.y = ((w >> 4) & m) | magic;
+    p.z = ((w >> 8) & m) | magic;
+    p.w = ((w >> 12) & m) | magic;
     return __builtin_bit_cast(bf16x8_t, p);
 }
 
-// One 16-byte slice of h (8 bf16 values e0..e7) permuted into the same k-slot order.
-__device__ __forceinline__ u32x4_t permute_h(u32x4_t v) {
+// -h/128 of a bf16 pair, exact for every |h| >= 2^-119.
+__device__ __forceinline__ uint32_t neg_over_128(uint32_t v) {
+    const uint32_t lo = f32_to_bf16_rne(bf16_lo(v) * -0.0078125f);
+    const uint32_t hi = f32_to_bf16_rne(bf16_hi(v) * -0.0078125f);
+    return lo | (hi << 16);
+}
+
+// One 16-byte slice of h (8 bf16 values e0..e7) as an A-fragment entry: permuted into the
+// nibbles' k-slot order and multiplied by -1/128.
+__device__ __forceinline__ u32x4_t prep_h(u32x4_t v) {
     u32x4_t o;
-    o.x = (v.x & 0xFFFFu) | (v.z << 16);
-    o.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
-    o.z = (v.y & 0xFFFFu) | (v.w << 16);
-    o.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
+    o.x = neg_over_128((v.x & 0xFFFFu) | (v.z << 16));
+    o.y = neg_over_128((v.x >> 16) | (v.z & 0xFFFF0000u));
+    o.z = neg_over_128((v.y & 0xFFFFu) | (v.w << 16));
+    o.w = neg_over_128((v.y >> 16) | (v.w & 0xFFFF0000u));
     return o;
 }
 
@@ -110,6 +138,26 @@ __device__ __forceinline__ float sum8_bf16(u32x4_t v) {
     s += bf16_lo(v.w);
     s += bf16_hi(v.w);
     return s;
+}
+
+// The bias MFMA of one super-unit (two chunks, groups 4P + c, c = 0..3).
+//   B fragment, lane (row r, k-group kg): the four {b, t} words of row r, one per group c,
+//     the same for every kg -- i.e. the two units' scale words side by side.
+//   A fragment, lane (row m, k-group kg): dword c = slice kg of X[m][4P + c], duplicated into
+//     a bf16 pair, with X = hi + mid + lo (slices kg = 0, 1, 2; slice 3 is zero).
+// Summed over k that is sum_c X_c * (b_c + t_c) = sum_c X_c * (b_c - 128 s_c).
+// bias_slices writes the four slice dwords of one (m, group) entry; at(kg) addresses them.
+template <typename At>
+__device__ __forceinline__ void bias_slices(float x, At at) {
+    const uint32_t hi = f32_to_bf16_rne(x);
+    const float r1 = x - __uint_as_float(hi << 16);  // exact
+    const uint32_t mid = f32_to_bf16_rne(r1);
+    const float r2 = r1 - __uint_as_float(mid << 16);  // exact
+    const uint32_t lo = f32_to_bf16_rne(r2);
+    *at(0) = hi * 0x10001u;
+    *at(1) = mid * 0x10001u;
+    *at(2) = lo * 0x10001u;
+    *at(3) = 0u;
 }
 
 // Shared memory of the head epilogue (cross-wave greedy reduction).
@@ -207,87 +255,62 @@ __device__ __forceinline__ void head_epilogue(const HeadArgs& a, f32x4_t (&tot)[
     }
 }
 
-// Per-chunk math shared by both kernels: one unit of one row tile (4 words per lane = 4 MFMA
-// k-steps, two groups) against A fragments av[mt][t] and group sums xv[g][mt].
-template <int NMT, int NI>
-__device__ __forceinline__ void unit_mac(const u32x4_t& w, const u32x2_t& sb,
-                                         const bf16x8_t (&av)[NMT][4],
-                                         const f32x4_t (&xv)[2][NMT], f32x4_t (&tot)[NMT]) {
-    bf16x8_t bv[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) bv[t] = nibbles_to_bf16(w[t]);
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-        const float s = g == 0 ? bf16_lo(sb.x) : bf16_hi(sb.x);
-        const float b = g == 0 ? bf16_lo(sb.y) : bf16_hi(sb.y);
-        const float tb = fmaf(-128.0f, s, b);
-#pragma unroll
-        for (int mt = 0; mt < NMT; ++mt) {
-            f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt][2 * g], bv[2 * g], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt][2 * g + 1], bv[2 * g + 1], acc,
-                                                          0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < NI; ++i)
-                tot[mt][i] = fmaf(s, acc[i], fmaf(tb, xv[g][mt][i], tot[mt][i]));
-        }
-    }
-}
-
-// One 64-column group (two MFMA k-steps) of one row tile: words w0, w1 of the unit, the
-// group's scale and bias from sb (g selects the half), A fragments av[mt][t] and X sums xv[mt].
-template <int NMT, int NI>
-__device__ __forceinline__ void group_mac(uint32_t w0, uint32_t w1, const u32x2_t& sb, int g,
-                                          const bf16x8_t (&av)[NMT][2], const f32x4_t (&xv)[NMT],
-                                          f32x4_t (&tot)[NMT]) {
-    const bf16x8_t b0 = nibbles_to_bf16(w0), b1 = nibbles_to_bf16(w1);
-    const float s = g == 0 ? bf16_lo(sb.x) : bf16_hi(sb.x);
-    const float b = g == 0 ? bf16_lo(sb.y) : bf16_hi(sb.y);
-    const float tb = fmaf(-128.0f, s, b);
-#pragma unroll
-    for (int mt = 0; mt < NMT; ++mt) {
-        f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt][0], b0, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt][1], b1, acc, 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < NI; ++i) tot[mt][i] = fmaf(s, acc[i], fmaf(tb, xv[mt][i], tot[mt][i]));
-    }
-}
+// Weight streams: one buffer descriptor per row tile covering its stripe of units, so a unit
+// load is one buffer_load with the unit offset in a scalar register and a fixed per-lane offset
+// -- no per-lane address arithmetic in the streaming loop. Tiles past the end (tile0 is
+// wave-uniform) re-read the last tile: their rows are >= vocab and never stored.
+constexpr int kBufferWord3 = 0x00020000;  // descriptor word 3: 32-bit data format
+constexpr int kNonTemporal = 2;           // cache-policy bit of a streaming load
 
 template <int RT>
-__device__ __forceinline__ void load_unit(const HeadArgs& a, uint32_t tile0, uint32_t U, int lane,
-                                          u32x4_t (&w)[RT], u32x2_t (&sb)[RT]) {
+__device__ __forceinline__ void tile_streams(const HeadArgs& a, uint32_t tile0,
+                                             __amdgpu_buffer_rsrc_t (&rs)[RT]) {
+    const uint32_t stripe = a.nunits * kUnitBytes;
 #pragma unroll
     for (int j = 0; j < RT; ++j) {
-        const uint32_t T = tile0 + j;
-        if (T < a.ntiles) {
-            const uint8_t* base = a.tiled + (static_cast<size_t>(T) * a.nunits + U) * kUnitBytes;
-            w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(base) + lane);
-            sb[j] = __builtin_nontemporal_load(
-                reinterpret_cast<const u32x2_t*>(base + kUnitNibbleBytes) + (lane & 15));
-        } else {
-            w[j] = u32x4_t{0u, 0u, 0u, 0u};
-            sb[j] = u32x2_t{0u, 0u};
-        }
+        const uint32_t T = min(tile0 + j, a.ntiles - 1);
+        rs[j] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.tiled) + static_cast<size_t>(T) * stripe,
+                                                  0, static_cast<int>(stripe), kBufferWord3);
     }
+}
+
+// Unit U of the RT row tiles: 16 B of nibbles (lane offset lane * 16) and the 8 B {b, t} pair
+// of the lane's row (lane offset 1024 + (lane % 16) * 8).
+template <int RT>
+__device__ __forceinline__ void load_unit(const __amdgpu_buffer_rsrc_t (&rs)[RT], uint32_t U,
+                                          uint32_t vo_w, uint32_t vo_s, u32x4_t (&w)[RT],
+                                          u32x2_t (&sb)[RT]) {
+    const int so = static_cast<int>(U * kUnitBytes);
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+        w[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs[j], vo_w, so, kNonTemporal));
+        sb[j] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rs[j], vo_s, so, kNonTemporal));
+    }
+}
+
+// Wave index as a scalar: keeps tile and address arithmetic on the scalar unit.
+__device__ __forceinline__ uint32_t wave_id() {
+    return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 }
 
 // ---- M <= 8: the whole h resident in LDS, no barrier in the streaming loop ---------------------
 //
-// LDS holds h permuted into A-fragment order, [m][chunk U][k-step t][kg] of 16 B, plus the group
-// sums [g][16]. A-fragment rows m >= M only feed output rows that are never stored, so their
-// lanes simply read row 0. Each wave streams its RT row tiles through a PF-deep register ring
-// of weight units, with no synchronisation until the epilogue.
+// LDS holds the prepared h in A-fragment order, [m][chunk U][k-step t][kg] of 16 B, and the bias
+// A-fragment entries [super-unit P][slice kg][m] of 16 B. A-fragment rows m >= M only feed output
+// rows that are never stored, so their lanes simply read row 0. Each wave streams its RT row
+// tiles through a PF-deep register ring of weight units, with no synchronisation until the
+// epilogue.
 template <int NI, int RT, int PF, int MODE>
 __global__ __launch_bounds__(kHeadThreads) void head_small_kernel(HeadArgs a) {
+    static_assert(PF % 2 == 0, "the ring holds whole super-units");
     extern __shared__ __align__(16) unsigned char smem_raw[];
     __shared__ EpiShared se;
     u32x4_t* sH = reinterpret_cast<u32x4_t*>(smem_raw);
     const uint32_t row_vecs = a.d / 8;  // 16 B vectors per h row
-    float* sX = reinterpret_cast<float*>(sH + a.M * row_vecs);  // [groups][16]
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const uint32_t tile0 = (blockIdx.x * kHeadWaves + wave) * RT;
-    const uint32_t groups = a.d / kGroup;
+    u32x4_t* sXF = sH + a.M * row_vecs;  // [super-units][4][M]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const uint32_t tile0 = (blockIdx.x * kHeadWaves + wave_id()) * RT;
+    const uint32_t magic = vgpr_const(0x43004300u);
 
     // ---- stage h: 8 consecutive threads cover one 64-column group ----
     const uint32_t tasks = a.M * row_vecs;
@@ -302,109 +325,196 @@ __global__ __launch_bounds__(kHeadThreads) void head_small_kernel(HeadArgs a) {
         if (task < tasks) {
             const uint32_t m = task / row_vecs, c8 = task % row_vecs;
             const uint32_t U = c8 >> 4, c = c8 & 15;
-            sH[((m * (a.d / kChunkK) + U) * 4 + (c >> 2)) * 4 + (c & 3)] = permute_h(v);
-            if ((c8 & 7) == 0) sX[(c8 >> 3) * 16 + m] = s;
+            sH[((m * a.nunits + U) * 4 + (c >> 2)) * 4 + (c & 3)] = prep_h(v);
+            if ((c8 & 7) == 0) {
+                const uint32_t g = c8 >> 3;
+                uint32_t* x = reinterpret_cast<uint32_t*>(sXF);
+                auto at = [&](int kg) { return x + (((g >> 2) * 4 + kg) * a.M + m) * 4 + (g & 3); };
+                bias_slices(s, at);
+                // an odd chunk count leaves groups 2, 3 of the last super-unit empty
+                if ((a.nunits & 1) && U == a.nunits - 1)
+                    bias_slices(0.0f, [&](int kg) { return at(kg) + 2; });
+            }
         }
     }
-    for (uint32_t i = tid; i < groups * 16; i += kHeadThreads)
-        if ((i & 15) >= a.M) sX[i] = 0.0f;
     __syncthreads();
 
-    const uint32_t m_lane = lane & 15;
-    const u32x4_t* aRow = sH + (m_lane < a.M ? m_lane : 0u) * row_vecs + (lane >> 4);
-    const float* xLane = sX + 4 * (lane >> 4);
+    const uint32_t m_lane = (lane & 15) < a.M ? (lane & 15) : 0u;
+    const u32x4_t* aRow = sH + m_lane * row_vecs + (lane >> 4);
+    const u32x4_t* xRow = sXF + (lane >> 4) * a.M + m_lane;
 
-    f32x4_t tot[RT][1];
+    f32x4_t tot[RT][1], bacc[RT];
 #pragma unroll
-    for (int j = 0; j < RT; ++j) tot[j][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < RT; ++j) {
+        tot[j][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        bacc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
 
+    __amdgpu_buffer_rsrc_t rs[RT];
+    tile_streams<RT>(a, tile0, rs);
+    const uint32_t vo_w = lane * 16, vo_s = kUnitNibbleBytes + (lane & 15) * 8;
     u32x4_t wq[PF][RT];
     u32x2_t sq[PF][RT];
 #pragma unroll
     for (int s = 0; s < PF; ++s)
-        if (static_cast<uint32_t>(s) < a.nunits) load_unit<RT>(a, tile0, s, lane, wq[s], sq[s]);
+        if (static_cast<uint32_t>(s) < a.nunits) load_unit<RT>(rs, s, vo_w, vo_s, wq[s], sq[s]);
 
+    u32x4_t bp[RT];  // {b, t} words of the super-unit's four groups: the bias B fragment
     for (uint32_t U0 = 0; U0 < a.nunits; U0 += PF) {
 #pragma unroll
         for (int s = 0; s < PF; ++s) {
             const uint32_t U = U0 + s;
             if (U >= a.nunits) break;
-            bf16x8_t av[1][4];
+            bf16x8_t av[4];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) av[0][t] = __builtin_bit_cast(bf16x8_t, aRow[(U * 4 + t) * 4]);
-            f32x4_t xv[2][1];
+            for (int t = 0; t < 4; ++t) av[t] = __builtin_bit_cast(bf16x8_t, aRow[(U * 4 + t) * 4]);
+            f32x4_t acc[RT][2];
 #pragma unroll
-            for (int g = 0; g < 2; ++g)
-                xv[g][0] = *reinterpret_cast<const f32x4_t*>(xLane + (2 * U + g) * 16);
+            for (int j = 0; j < RT; ++j)
 #pragma unroll
-            for (int j = 0; j < RT; ++j) unit_mac<1, NI>(wq[s][j], sq[s][j], av, xv, tot[j]);
-            if (U + PF < a.nunits) load_unit<RT>(a, tile0, U + PF, lane, wq[s], sq[s]);
+                for (int g = 0; g < 2; ++g) {
+                    const bf16x8_t b0 = nibbles_to_bf16(wq[s][j][2 * g], magic);
+                    const bf16x8_t b1 = nibbles_to_bf16(wq[s][j][2 * g + 1], magic);
+                    acc[j][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[2 * g], b0,
+                                                                        f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    acc[j][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[2 * g + 1], b1, acc[j][g], 0, 0, 0);
+                }
+#pragma unroll
+            for (int j = 0; j < RT; ++j)
+#pragma unroll
+                for (int g = 0; g < 2; ++g) {
+                    const float t = bf16_hi(g ? sq[s][j].y : sq[s][j].x);
+#pragma unroll
+                    for (int i = 0; i < NI; ++i) tot[j][0][i] = fmaf(t, acc[j][g][i], tot[j][0][i]);
+                }
+            const bool odd = (s & 1) != 0;
+#pragma unroll
+            for (int j = 0; j < RT; ++j) {
+                if (odd) {
+                    bp[j].z = sq[s][j].x;
+                    bp[j].w = sq[s][j].y;
+                } else {
+                    bp[j].x = sq[s][j].x;
+                    bp[j].y = sq[s][j].y;
+                }
+            }
+            if (odd || U + 1 == a.nunits) {
+                if (!odd) {
+#pragma unroll
+                    for (int j = 0; j < RT; ++j) bp[j].z = bp[j].w = 0u;  // no second unit
+                }
+                const bf16x8_t xa = __builtin_bit_cast(bf16x8_t, xRow[(U >> 1) * 4 * a.M]);
+#pragma unroll
+                for (int j = 0; j < RT; ++j)
+                    bacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        xa, __builtin_bit_cast(bf16x8_t, bp[j]), bacc[j], 0, 0, 0);
+            }
+            if (U + PF < a.nunits) load_unit<RT>(rs, U + PF, vo_w, vo_s, wq[s], sq[s]);
         }
     }
+#pragma unroll
+    for (int j = 0; j < RT; ++j) tot[j][0] += bacc[j];
     head_epilogue<1, NI, RT, MODE>(a, tot, tile0, se);
 }
 
-// ---- any M <= 64: h staged through LDS, PF chunks of 128 columns at a time ---------------------
+// ---- 9 <= M <= 64: h prepared once per call, staged through LDS by plain copies -------------------
 //
+// prep_hidden_kernel writes, once per call, the prepared h in A-fragment order,
+// hp[U][mt][t][lane] (16 B each, rows m >= M zero), and the bias A-fragment entries
+// hx[P][mt][lane] of super-unit P (groups past the end zero).
+template <int NMT>
+__global__ __launch_bounds__(kHeadThreads) void prep_hidden_kernel(const uint16_t* __restrict__ h,
+                                                                   uint32_t M, uint32_t d,
+                                                                   u32x4_t* __restrict__ hp,
+                                                                   u32x4_t* __restrict__ hx) {
+    const uint32_t per_chunk = NMT * 256;  // 16 B vectors per chunk (NMT*16 rows x 16)
+    const uint32_t nunits = d / kChunkK;
+    const uint32_t task = blockIdx.x * kHeadThreads + threadIdx.x;  // grid covers nunits chunks
+    const uint32_t U = task / per_chunk, rem = task % per_chunk;
+    const uint32_t m = rem >> 4, c = rem & 15;
+    u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
+    if (U < nunits && m < M)
+        v = *reinterpret_cast<const u32x4_t*>(h + static_cast<size_t>(m) * d + U * kChunkK + c * 8);
+    float s = sum8_bf16(v);
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    if (U < nunits) {
+        hp[((static_cast<size_t>(U) * NMT + (m >> 4)) * 4 + (c >> 2)) * 64 + (c & 3) * 16 + (m & 15)] =
+            prep_h(v);
+        if ((c & 7) == 0) {
+            const uint32_t g = 2 * U + (c >> 3);
+            uint32_t* x = reinterpret_cast<uint32_t*>(hx);
+            auto at = [&](int kg) {
+                return x + (((static_cast<size_t>(g >> 2) * NMT + (m >> 4)) * 4 + kg) * 16 + (m & 15)) * 4 +
+                       (g & 3);
+            };
+            bias_slices(s, at);
+            // an odd chunk count leaves groups 2, 3 of the last super-unit empty
+            if ((nunits & 1) && U == nunits - 1) bias_slices(0.0f, [&](int kg) { return at(kg) + 2; });
+        }
+    }
+}
+
 // Block = 4 waves; wave w owns RT consecutive 16-row tiles. NMT = number of 16-wide m tiles
 // (1 for M <= 16, 4 for M <= 64); NI = accumulator lanes per m tile that can hold a live row.
-// A stage is PF chunks: one barrier per stage, h for the next stage loaded into registers while
-// this one computes, and a PF-deep register ring of weight units per row tile.
-template <int NMT, int NI, int RT, int PF, int MODE>
+// A stage is one super-unit (two chunks): one barrier per stage, the next stage's h loaded into
+// registers while this one computes, and a two-deep register ring of weight units per row tile.
+// Each group runs all RT x NMT MFMA chains before its FMAs, so results are consumed well after
+// the MFMA pipe produced them. hp holds one chunk past the end, so stage loads are unconditional.
+template <int NMT, int NI, int RT, int MODE>
 __global__ __launch_bounds__(kHeadThreads) __attribute__((amdgpu_waves_per_eu(2)))
-void head_kernel(HeadArgs a) {
+void head_wide_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_t* __restrict__ hx) {
+    constexpr int PF = 2;
     __shared__ u32x4_t sA[2][PF][NMT][4][64];
-    __shared__ float sX[2][PF][2][NMT * 16];
+    __shared__ u32x4_t sXA[2][NMT][64];
     __shared__ EpiShared se;
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
     const int lane = tid & 63;
-    const uint32_t tile0 = (blockIdx.x * kHeadWaves + wave) * RT;
+    const uint32_t tile0 = (blockIdx.x * kHeadWaves + wave_id()) * RT;
+    const uint32_t magic = vgpr_const(0x43004300u);
+    constexpr int kVec = NMT * 4 * 64;  // 16 B vectors per chunk
+    constexpr int kXA = NMT * 64;       // 16 B bias vectors per super-unit
 
-    // ---- h staging: chunks [S*PF, S*PF + PF) of every live row, permuted, with group sums ----
-    u32x4_t hv[PF][NMT];
+    u32x4_t hv[PF][kVec / kHeadThreads];
+    u32x4_t xv_st = u32x4_t{0u, 0u, 0u, 0u};
     auto stage_load = [&](uint32_t S) {
+        const u32x4_t* src = hp + static_cast<size_t>(S) * PF * kVec;
 #pragma unroll
         for (int u = 0; u < PF; ++u)
 #pragma unroll
-            for (int it = 0; it < NMT; ++it) {
-                const int task = tid + kHeadThreads * it;
-                const int m = task >> 4, c = task & 15;
-                const uint32_t U = S * PF + u;
-                hv[u][it] = u32x4_t{0u, 0u, 0u, 0u};
-                if (m < static_cast<int>(a.M) && U < a.nunits)
-                    hv[u][it] = *reinterpret_cast<const u32x4_t*>(
-                        a.h + static_cast<size_t>(m) * a.d + U * kChunkK + c * 8);
-            }
+            for (int it = 0; it < kVec / kHeadThreads; ++it)
+                hv[u][it] = (src + u * kVec + kHeadThreads * it)[tid];
+        if (tid < kXA) xv_st = hx[static_cast<size_t>(S) * kXA + tid];
     };
     auto stage_store = [&](int buf) {
 #pragma unroll
-        for (int u = 0; u < PF; ++u)
+        for (int u = 0; u < PF; ++u) {
+            u32x4_t* dst = &sA[buf][u][0][0][0];
 #pragma unroll
-            for (int it = 0; it < NMT; ++it) {
-                const int task = tid + kHeadThreads * it;
-                const int m = task >> 4, c = task & 15;
-                float s = sum8_bf16(hv[u][it]);
-                s += __shfl_xor(s, 1);
-                s += __shfl_xor(s, 2);
-                s += __shfl_xor(s, 4);
-                sA[buf][u][m >> 4][c >> 2][(c & 3) * 16 + (m & 15)] = permute_h(hv[u][it]);
-                if ((c & 7) == 0) sX[buf][u][c >> 3][m] = s;
-            }
+            for (int it = 0; it < kVec / kHeadThreads; ++it) dst[tid + kHeadThreads * it] = hv[u][it];
+        }
+        if (tid < kXA) (&sXA[buf][0][0])[tid] = xv_st;
     };
 
-    f32x4_t tot[RT][NMT];
+    f32x4_t tot[RT][NMT], bacc[RT][NMT];
 #pragma unroll
     for (int j = 0; j < RT; ++j)
 #pragma unroll
-        for (int mt = 0; mt < NMT; ++mt) tot[j][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int mt = 0; mt < NMT; ++mt) {
+            tot[j][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            bacc[j][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
 
+    __amdgpu_buffer_rsrc_t rs[RT];
+    tile_streams<RT>(a, tile0, rs);
+    const uint32_t vo_w = lane * 16, vo_s = kUnitNibbleBytes + (lane & 15) * 8;
     u32x4_t wq[PF][RT];
     u32x2_t sq[PF][RT];
 #pragma unroll
     for (int u = 0; u < PF; ++u)
-        if (static_cast<uint32_t>(u) < a.nunits) load_unit<RT>(a, tile0, u, lane, wq[u], sq[u]);
+        if (static_cast<uint32_t>(u) < a.nunits) load_unit<RT>(rs, u, vo_w, vo_s, wq[u], sq[u]);
     stage_load(0);
     stage_store(0);
 
@@ -414,11 +524,15 @@ void head_kernel(HeadArgs a) {
         const int buf = S & 1;
         const bool more = (S + 1) < nstages;
         if (more) stage_load(S + 1);
+        u32x4_t bp[RT];  // {b, t} words of the super-unit's four groups: the bias B fragment
 #pragma unroll
         for (int u = 0; u < PF; ++u) {
             const uint32_t U = S * PF + u;
-            if (U >= a.nunits) break;
-            // one 64-column group at a time keeps only its two k-steps of A and X live
+            if (U >= a.nunits) {  // odd chunk count: no second unit
+#pragma unroll
+                for (int j = 0; j < RT; ++j) bp[j].z = bp[j].w = 0u;
+                break;
+            }
 #pragma unroll
             for (int g = 0; g < 2; ++g) {
                 bf16x8_t av[NMT][2];
@@ -427,25 +541,65 @@ void head_kernel(HeadArgs a) {
 #pragma unroll
                     for (int t = 0; t < 2; ++t)
                         av[mt][t] = __builtin_bit_cast(bf16x8_t, sA[buf][u][mt][2 * g + t][lane]);
-                f32x4_t xv[NMT];
+                f32x4_t acc[RT][NMT];
 #pragma unroll
-                for (int mt = 0; mt < NMT; ++mt)
-                    xv[mt] = *reinterpret_cast<const f32x4_t*>(&sX[buf][u][g][mt * 16 + 4 * (lane >> 4)]);
+                for (int j = 0; j < RT; ++j) {
+                    const bf16x8_t b0 = nibbles_to_bf16(wq[u][j][2 * g], magic);
+                    const bf16x8_t b1 = nibbles_to_bf16(wq[u][j][2 * g + 1], magic);
 #pragma unroll
-                for (int j = 0; j < RT; ++j)
-                    group_mac<NMT, NI>(wq[u][j][2 * g], wq[u][j][2 * g + 1], sq[u][j], g, av, xv, tot[j]);
+                    for (int mt = 0; mt < NMT; ++mt) {
+                        acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            av[mt][0], b0, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        acc[j][mt] =
+                            __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt][1], b1, acc[j][mt], 0, 0, 0);
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < RT; ++j) {
+                    const float t = bf16_hi(g ? sq[u][j].y : sq[u][j].x);
+#pragma unroll
+                    for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+                        for (int i = 0; i < NI; ++i) tot[j][mt][i] = fmaf(t, acc[j][mt][i], tot[j][mt][i]);
+                }
             }
-            if (U + PF < a.nunits) load_unit<RT>(a, tile0, U + PF, lane, wq[u], sq[u]);
+#pragma unroll
+            for (int j = 0; j < RT; ++j) {
+                if (u == 0) {
+                    bp[j].x = sq[u][j].x;
+                    bp[j].y = sq[u][j].y;
+                } else {
+                    bp[j].z = sq[u][j].x;
+                    bp[j].w = sq[u][j].y;
+                }
+            }
+            if (U + PF < a.nunits) load_unit<RT>(rs, U + PF, vo_w, vo_s, wq[u], sq[u]);
         }
+        // the super-unit's bias: one K=32 MFMA per row tile and m tile
+        bf16x8_t xa[NMT];
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt) xa[mt] = __builtin_bit_cast(bf16x8_t, sXA[buf][mt][lane]);
+#pragma unroll
+        for (int j = 0; j < RT; ++j)
+#pragma unroll
+            for (int mt = 0; mt < NMT; ++mt)
+                bacc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    xa[mt], __builtin_bit_cast(bf16x8_t, bp[j]), bacc[j][mt], 0, 0, 0);
         if (more) stage_store(buf ^ 1);
     }
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt) tot[j][mt] += bacc[j][mt];
     head_epilogue<NMT, NI, RT, MODE>(a, tot, tile0, se);
 }
 
 // ---- layout repack: reference [W|S|B] -> units ----------------------------------------------
+// Sets *bad when a scale's magnitude exceeds kMaxScale (t = -128 s would not be finite).
 __global__ void repack_kernel(const uint32_t* __restrict__ W, const uint16_t* __restrict__ S,
                               const uint16_t* __restrict__ B, uint32_t vocab, uint32_t d,
-                              uint32_t ntiles, uint32_t nunits, uint8_t* __restrict__ out) {
+                              uint32_t ntiles, uint32_t nunits, uint8_t* __restrict__ out,
+                              uint32_t* __restrict__ bad) {
     const uint64_t total = static_cast<uint64_t>(ntiles) * nunits * 64;
     const uint32_t wpr = d / 8, gpr = d / kGroup;
     for (uint64_t g = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; g < total;
@@ -467,8 +621,14 @@ __global__ void repack_kernel(const uint32_t* __restrict__ W, const uint16_t* __
             if (r < vocab) {
                 const uint16_t* sr = S + static_cast<size_t>(r) * gpr + 2 * U;
                 const uint16_t* br = B + static_cast<size_t>(r) * gpr + 2 * U;
-                sb.x = static_cast<uint32_t>(sr[0]) | (static_cast<uint32_t>(sr[1]) << 16);
-                sb.y = static_cast<uint32_t>(br[0]) | (static_cast<uint32_t>(br[1]) << 16);
+                uint32_t word[2];
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const float s = __uint_as_float(static_cast<uint32_t>(sr[k]) << 16);
+                    if (fabsf(s) > kMaxScale) __hip_atomic_fetch_or(bad, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    word[k] = static_cast<uint32_t>(br[k]) | (f32_to_bf16_rne(-128.0f * s) << 16);
+                }
+                sb = u32x2_t{word[0], word[1]};
             }
             *reinterpret_cast<u32x2_t*>(ub + kUnitNibbleBytes + lane * 8) = sb;
         }
@@ -483,12 +643,6 @@ __device__ __forceinline__ uint64_t splitmix64_dev(uint64_t x) {
     return x ^ (x >> 31);
 }
 
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-    uint32_t u = __float_as_uint(f);
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return static_cast<uint16_t>(u >> 16);
-}
-
 __global__ void generate_kernel(uint32_t* __restrict__ W, uint16_t* __restrict__ S,
                                 uint16_t* __restrict__ B, uint64_t n_words, uint64_t n_groups,
                                 uint64_t seed) {
@@ -500,9 +654,9 @@ __global__ void generate_kernel(uint32_t* __restrict__ W, uint16_t* __restrict__
          j += stride) {
         const float u = static_cast<float>(splitmix64_dev(seed + 0x2000000000000000ULL + j) >> 40) *
                         (1.0f / 16777216.0f);
-        const uint16_t s = f32_to_bf16_rne(fmaf(9e-3f, u, 1e-3f));
+        const uint16_t s = static_cast<uint16_t>(f32_to_bf16_rne(fmaf(9e-3f, u, 1e-3f)));
         S[j] = s;
-        B[j] = f32_to_bf16_rne(-8.0f * __uint_as_float(static_cast<uint32_t>(s) << 16));
+        B[j] = static_cast<uint16_t>(f32_to_bf16_rne(-8.0f * __uint_as_float(static_cast<uint32_t>(s) << 16)));
     }
 }
 
@@ -520,17 +674,18 @@ struct twd_head {
     uint8_t* tiled = nullptr;
     uint64_t tiled_bytes = 0;
     uint64_t* gbest = nullptr;    // [TWD_MAX_ROWS] + arrival counter, zero between launches
+    u32x4_t* hp = nullptr;        // prepared h in A-fragment order for M > 8 (prep_hidden_kernel)
+    u32x4_t* hx = nullptr;        // its bias A-fragment entries
     twd_selector* sel = nullptr;
 };
 
 namespace {
 
-// staged-h kernel: row tiles per wave, units per stage (measured: M = 16 -> 4 x 2, 155 us;
-// M = 64 -> 2 x 2, 446 us greedy)
-constexpr int kRT1 = 4, kPF1 = 2;  // M <= 16
-constexpr int kRT4 = 2, kPF4 = 2;  // M <= 64
+// staged-h kernel: row tiles per wave (measured on MI355X: M = 16 -> 4, M = 64 -> 2)
+constexpr int kRT1 = 4;  // M <= 16
+constexpr int kRT4 = 2;  // M <= 64
 // resident-h kernel: row tiles per wave and weight units in flight (measured best on MI355X:
-// M = 1 -> 2 tiles x 4 units, 122-136 us; M = 5 -> 4 tiles x 2 units, 155-165 us)
+// M = 1 -> 2 tiles x 4 units; M = 5 -> 4 tiles x 2 units)
 constexpr int kRTS1 = 2, kPFS1 = 4;  // M == 1
 constexpr int kRTS4 = 4, kPFS4 = 2;  // 2 <= M <= 8
 constexpr uint32_t kSmallMaxRows = 8;
@@ -539,6 +694,8 @@ uint32_t blocks_for(uint32_t ntiles, int rt) {
     const uint32_t per = kHeadWaves * rt;
     return (ntiles + per - 1) / per;
 }
+
+uint32_t super_units(uint32_t nunits) { return (nunits + 1) / 2; }
 
 int check_geometry(uint32_t vocab, uint32_t d, uint32_t group) {
     if (group != kGroup) return fail(TWD_E_UNSUPPORTED, "group_size must be 64");
@@ -549,9 +706,10 @@ int check_geometry(uint32_t vocab, uint32_t d, uint32_t group) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Dynamic LDS of the resident-h kernel: h permuted (M x d bf16) + group sums [d/64][16] fp32.
+// Dynamic LDS of the resident-h kernel: prepared h (M x d bf16) + bias entries [groups4][M].
 size_t small_smem_bytes(uint32_t rows, uint32_t d) {
-    return static_cast<size_t>(rows) * d * 2 + static_cast<size_t>(d / kGroup) * 16 * 4;
+    const size_t groups4 = ((d / kGroup) + 3) & ~size_t{3};
+    return static_cast<size_t>(rows) * d * 2 + groups4 * rows * 16;
 }
 
 template <typename K>
@@ -563,7 +721,8 @@ hipError_t allow_smem(K kernel, size_t bytes) {
 // Lets every resident-h instantiation use the LDS it needs for kSmallMaxRows rows of d.
 int enable_small_kernels(uint32_t d) {
     const size_t bytes = small_smem_bytes(kSmallMaxRows, d);
-    if (bytes > 160 * 1024) return fail(TWD_E_UNSUPPORTED, "d_model too large for the LDS-resident head");
+    if (bytes > 160 * 1024 - sizeof(EpiShared))
+        return fail(TWD_E_UNSUPPORTED, "d_model too large for the LDS-resident head");
     hipError_t e = hipSuccess;
     if (e == hipSuccess) e = allow_smem(head_small_kernel<1, kRTS1, kPFS1, kModeLogits>, bytes);
     if (e == hipSuccess) e = allow_smem(head_small_kernel<1, kRTS1, kPFS1, kModeGreedy>, bytes);
@@ -582,8 +741,11 @@ int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
     h->nunits = d / kChunkK;
     h->tiled_bytes = static_cast<uint64_t>(h->ntiles) * h->nunits * kUnitBytes;
     hipError_t e = hipMalloc(&h->tiled, h->tiled_bytes);
-    if (e == hipSuccess) e = hipMalloc(&h->gbest, sizeof(uint64_t) * (TWD_MAX_ROWS + 1));
-    if (e == hipSuccess) e = hipMemset(h->gbest, 0, sizeof(uint64_t) * (TWD_MAX_ROWS + 1));
+    // gbest: per-row maxima, the arrival counter, and the repack's bad-scale flag
+    if (e == hipSuccess) e = hipMalloc(&h->gbest, sizeof(uint64_t) * (TWD_MAX_ROWS + 2));
+    if (e == hipSuccess) e = hipMemset(h->gbest, 0, sizeof(uint64_t) * (TWD_MAX_ROWS + 2));
+    if (e == hipSuccess) e = hipMalloc(&h->hp, sizeof(u32x4_t) * (h->nunits + 1) * 4 * 4 * 64);
+    if (e == hipSuccess) e = hipMalloc(&h->hx, sizeof(u32x4_t) * super_units(h->nunits) * 4 * 64);
     if (e != hipSuccess) {
         twd_head_destroy(h);
         return hip_fail(e, "allocating the LM head");
@@ -596,6 +758,8 @@ int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
     return TWD_OK;
 }
 
+uint32_t* repack_flag(twd_head* h) { return reinterpret_cast<uint32_t*>(h->gbest + TWD_MAX_ROWS + 1); }
+
 int head_repack(twd_head* h, const uint8_t* wsb_dev, hipStream_t stream) {
     const uint64_t w_bytes = static_cast<uint64_t>(h->vocab) * (h->d / 8) * 4;
     const uint64_t s_bytes = static_cast<uint64_t>(h->vocab) * (h->d / kGroup) * 2;
@@ -604,12 +768,11 @@ int head_repack(twd_head* h, const uint8_t* wsb_dev, hipStream_t stream) {
     const uint16_t* B = reinterpret_cast<const uint16_t*>(wsb_dev + w_bytes + s_bytes);
     const uint64_t work = static_cast<uint64_t>(h->ntiles) * h->nunits * 64;
     const uint32_t grid = static_cast<uint32_t>(std::min<uint64_t>((work + 255) / 256, 1u << 16));
-    repack_kernel<<<grid, 256, 0, stream>>>(W, S, B, h->vocab, h->d, h->ntiles, h->nunits, h->tiled);
+    repack_kernel<<<grid, 256, 0, stream>>>(W, S, B, h->vocab, h->d, h->ntiles, h->nunits, h->tiled,
+                                            repack_flag(h));
     TWD_HIP(hipGetLastError());
     return TWD_OK;
 }
-
-
 
 template <int MODE>
 int launch_head(twd_head* h, const uint16_t* hidden, uint32_t rows, float* logits,
@@ -641,9 +804,13 @@ int launch_head(twd_head* h, const uint16_t* hidden, uint32_t rows, float* logit
         head_small_kernel<4, kRTS4, kPFS4, MODE><<<blocks_for(h->ntiles, kRTS4), kHeadThreads,
                                                    small_smem_bytes(rows, h->d), stream>>>(a);
     } else if (rows <= 16) {
-        head_kernel<1, 4, kRT1, kPF1, MODE><<<blocks_for(h->ntiles, kRT1), kHeadThreads, 0, stream>>>(a);
+        prep_hidden_kernel<1><<<h->nunits * 1, kHeadThreads, 0, stream>>>(hidden, rows, h->d, h->hp, h->hx);
+        head_wide_kernel<1, 4, kRT1, MODE>
+            <<<blocks_for(h->ntiles, kRT1), kHeadThreads, 0, stream>>>(a, h->hp, h->hx);
     } else {
-        head_kernel<4, 4, kRT4, kPF4, MODE><<<blocks_for(h->ntiles, kRT4), kHeadThreads, 0, stream>>>(a);
+        prep_hidden_kernel<4><<<h->nunits * 4, kHeadThreads, 0, stream>>>(hidden, rows, h->d, h->hp, h->hx);
+        head_wide_kernel<4, 4, kRT4, MODE>
+            <<<blocks_for(h->ntiles, kRT4), kHeadThreads, 0, stream>>>(a, h->hp, h->hx);
     }
     TWD_HIP(hipGetLastError());
     return TWD_OK;
@@ -671,14 +838,21 @@ TWD_API int twd_head_create_device(const void* wsb_dev, uint64_t wsb_bytes, uint
         return fail(TWD_E_INVALID, "wsb_bytes is smaller than the [W|S|B] slice of this geometry");
     twd_head* h = nullptr;
     if ((rc = head_alloc(vocab, d_model, softcap, &h))) return rc;
-    if ((rc = head_repack(h, static_cast<const uint8_t*>(wsb_dev), static_cast<hipStream_t>(stream)))) {
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if ((rc = head_repack(h, static_cast<const uint8_t*>(wsb_dev), s))) {
         twd_head_destroy(h);
         return rc;
     }
-    hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    uint32_t bad = 0;
+    hipError_t e = hipMemcpyAsync(&bad, repack_flag(h), sizeof(bad), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
         twd_head_destroy(h);
         return hip_fail(e, "repacking the LM head");
+    }
+    if (bad) {
+        twd_head_destroy(h);
+        return fail(TWD_E_UNSUPPORTED, "a group scale exceeds 2^100 in magnitude");
     }
     *out = h;
     return TWD_OK;
@@ -711,6 +885,8 @@ TWD_API void twd_head_destroy(twd_head* h) {
     if (!h) return;
     if (h->tiled) (void)hipFree(h->tiled);
     if (h->gbest) (void)hipFree(h->gbest);
+    if (h->hp) (void)hipFree(h->hp);
+    if (h->hx) (void)hipFree(h->hx);
     if (h->sel) twd_selector_destroy(h->sel);
     delete h;
 }

@@ -20,11 +20,15 @@ namespace twd {
 //   bytes [0, 1024)     64 lanes x 16 B of packed nibbles. Lane l = 16*kg + r holds row r of the
 //                       tile and the four words 16U + 4t + kg (t = 0..3) of that row, i.e. the
 //                       8 columns 128U + 32t + 8kg .. +7 for each of the four MFMA k-steps t.
-//   bytes [1024, 1152)  16 rows x 8 B: bf16 {s(2U), s(2U+1), b(2U), b(2U+1)} of the row.
+//   bytes [1024, 1152)  16 rows x 8 B: two words, one per group g = 2U, 2U+1 of the row, each
+//                       bf16 {b(g), t(g)} (low half b) with t = -128 * s(g), which is exact.
 //
 // Units are ordered [row tile T][chunk U], so a wave working through one row tile reads one
 // contiguous 48 KB stripe, and every load instruction moves 1 KB (nibbles) or 128 B (scales)
 // of contiguous memory. The total is exactly the reference's byte count: 3024 B per row.
+// Storing t instead of s lets the word {b, t} serve directly as an MFMA operand for the group's
+// bias term (b - 128 s) * X; s itself is t * (-1/128), folded into h ahead of time.
+constexpr float kMaxScale = 0x1p100f;  // |s| above this is rejected at load (t would overflow)
 constexpr uint32_t kGroup = 64;
 constexpr uint32_t kChunkK = 128;
 constexpr uint32_t kTileRows = 16;
