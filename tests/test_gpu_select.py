@@ -149,6 +149,51 @@ def test_select_random_vs_oracle(env, oracle, n):
     assert [int(x) for x in tok] == want
 
 
+def shaped_rows(rng, n):
+    """Rows whose values stress the distance-from-max shortlist: every branch of the kernel's
+    top-`want` (direct ranking of the boundary bin, radix inside an overfull bin, radix over an
+    unbinnable block, all entries) must give the oracle's ids."""
+    base = (rng.standard_normal(n) * 3).astype(np.float32)
+    out = {"all_equal": np.full(n, 1.25, np.float32)}
+    gap = base.copy()
+    gap[rng.integers(0, n, 3)] = 100.0  # a few entries far above the rest
+    out["huge_gap"] = gap
+    out["plateaus"] = np.round(base * 2) / 2  # every bin boundary holds exact ties
+    masked = np.full(n, -np.inf, np.float32)
+    keep = rng.integers(0, n, max(1, n // 10))
+    masked[keep] = base[keep]
+    out["mostly_minus_inf"] = masked
+    few = np.full(n, -np.inf, np.float32)
+    few[rng.integers(0, n, 7)] = rng.standard_normal(7).astype(np.float32)
+    out["seven_finite"] = few
+    out["narrow"] = (1.0 + rng.standard_normal(n) * 1e-4).astype(np.float32)
+    crowd = base.copy()
+    crowd[rng.integers(0, n, min(n, 5000))] = base.max()  # an overfull bin at the very top
+    out["crowded_top"] = crowd
+    wide = (rng.standard_normal(n) * 400).astype(np.float32)  # span far beyond the binned range
+    out["wide"] = wide
+    return out
+
+
+@pytest.mark.parametrize("n", [300, 16384, 50000, V])
+def test_select_shaped_rows_vs_oracle(env, oracle, n):
+    torch, dev, t, sel = env
+    rng = np.random.default_rng(77 + n)
+    configs = [(0.7, 1.0, 0), (0.8, 0.95, 64), (1.0, 0.9, 256), (0.5, 1.0, 1), (1.5, 0.999, 100)]
+    rows, params, want, names = [], [], [], []
+    for name, row in shaped_rows(rng, n).items():
+        for j, (T, p, k) in enumerate(configs):
+            u = t.uniform_from_seed(t.splitmix64(31 * n + 7 * j + len(rows)))
+            rows.append(row)
+            params.append(rp(t, T, p, k, u))
+            want.append(oracle.sample_token(row, T, p, k, u=u))
+            names.append((name, T, p, k))
+    for start in range(0, len(rows), 64):
+        tok, _ = select_rows(env, np.stack(rows[start:start + 64]), params[start:start + 64])
+        for got, w, nm in zip(tok, want[start:start + 64], names[start:start + 64]):
+            assert int(got) == w, nm
+
+
 def test_rows_with_own_params_and_histories(env, oracle):
     # config 5 style: 64 rows, own T/k/p, own 2048-id history with rp 1.1, own uniform
     torch, dev, t, sel = env

@@ -1,13 +1,20 @@
 // Token selection over device logit rows on gfx950: repetition penalty, greedy argmax and the
 // sampled chain of sample_token (src/sampling.cpp:103-198), plus verify bookkeeping.
 //
-// select_slice_kernel covers all rows: grid (parts, rows), each block owns a 16384-entry slice
-// of one row. Per block: penalty on the slice's history ids (occurrence counts in LDS, each
-// applied one occurrence at a time like the reference loop), then either the greedy rank
-// maximum or {slice max, sum exp(l - slice max) in double, the slice's top-`want` ranks by a
-// radix select on 64-bit (value desc, index asc) ranks}. A row held by one slice finishes in
-// the same block; otherwise select_merge_kernel (one block per row, second launch) merges the
-// slices, sorts the global top-`want`, and runs top-p, top-k and the draw in reference order.
+// select_slice_kernel covers all rows: grid (parts, rows), each 512-thread block owns an
+// 8192-entry slice of one row, 16 values per thread held in registers. Per block: penalty on
+// the slice's history ids (occurrence counts in LDS, each applied one occurrence at a time like
+// the reference loop), then either the greedy rank maximum or {slice max, sum exp(l - slice max)
+// in double, the slice's top-`want` ranks}. A row held by one slice finishes in the same
+// block; otherwise select_merge_kernel (one block per row, second launch) merges the slices,
+// ranks the global top-`want`, and runs top-p, top-k and the draw in reference order.
+//
+// The top-`want` of a block (block_top) is found by distance from the block's maximum: a
+// 256-bin histogram of (max - v) locates the bin holding the want-th rank, every entry of a
+// nearer bin is taken, and the boundary bin's entries are ranked exactly among themselves by
+// the 64-bit (value desc, index asc) rank. Only the boundary bin needs exact work, and the
+// histogram's atomics spread over 8 replicas. Blocks whose values do not bin usefully (all
+// equal, non-finite extremes, an overfull boundary bin) fall back to a radix select on ranks.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -18,9 +25,19 @@
 
 namespace twd {
 
-constexpr uint32_t kMaxParts = 32;  // vocab <= 32 * 16384 = 524288
-constexpr uint32_t kMergePerThread = kMaxParts * kMaxWant / kSelThreads;  // 8
-constexpr int kSelWaves = kSelThreads / 64;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kSliceThreads = 512;     // two slice blocks share a CU
+constexpr int kSelPerThread = 16;
+constexpr uint32_t kSlice = kSliceThreads * kSelPerThread;  // vocabulary entries per slice block
+constexpr uint32_t kMaxParts = 64;    // vocab <= 64 * 8192 = 524288
+constexpr int kMergeThreads = 256;
+constexpr int kMergePerThread = kMaxParts * kMaxWant / kMergeThreads;  // 64
+constexpr int kMaxWaves = 16;
+constexpr uint32_t kBins = 256;         // distance-from-max bins of block_top
+constexpr uint32_t kReps = 8;           // histogram replicas: lane l counts into replica l % 8
+constexpr uint32_t kGatherMax = 512;    // boundary-bin entries ranked directly
+constexpr float kBinRange = 64.0f;      // widest span of values the bins resolve
 
 struct SelectArgs {
     uint32_t rows;
@@ -43,101 +60,149 @@ struct SelectBufs {
     uint64_t* cand;
 };
 
-struct SelectShared {
-    union {
-        uint32_t cnt[kSlice];                 // penalty occurrence counts of the slice
-        float val[kSlice];                    // then the slice's penalised values
-        uint64_t cand[kMaxParts * kMaxWant];  // then, in the merge kernel, every slice's ranks
-    } u;
-    uint32_t hist[256];         // radix digit histogram
+// Shared memory: what every block needs (reductions, the row's shortlist and its sums)...
+struct SelCommon {
     uint32_t misc[8];
-    uint64_t red64[kSelWaves];
-    double redd[kSelWaves];
-    float redf[kSelWaves];
-    uint32_t redu[kSelWaves];
-    uint64_t top[kMaxWant];     // selected ranks, sorted in place
+    uint64_t red64[kMaxWaves];
+    double redd[kMaxWaves];
+    float redf[kMaxWaves];
+    float redf2[kMaxWaves];
+    uint32_t redu[kMaxWaves];
+    uint64_t top[kMaxWant];     // selected ranks
+    uint64_t sorted[kMaxWant];  // the same, in descending order
     double e[kMaxWant];         // exp(l - max) / total
     double q[kMaxWant];         // exp((l - max) / T), then the running sum
+    double exp2_tbl[64];        // 2^(j/64), for the row sum's exponentials
     float gmax;
     double total;
     uint32_t flag;
 };
 
-__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, SelectShared& sh) {
+// ... block_top's work space ...
+struct TopScratch {
+    uint32_t hist[kReps * kBins];  // radix digit histogram / replicated bin histogram [bin][rep]
+    uint64_t gath[kGatherMax];     // the boundary bin's ranks
+};
+
+// ... and per kernel: the slice kernel's penalty counts, then a copy of its values for the
+// radix fallback, one entry per thread and slot so neither needs a barrier to hand over (two
+// slice blocks fit on a CU); the merge kernel keeps every slice's ranks.
+struct SliceShared {
+    union {
+        uint32_t cnt[kSlice];
+        float vals[kSlice];
+    } u;
+    TopScratch t;
+    SelCommon c;
+};
+
+struct MergeShared {
+    uint64_t cand[kMaxParts * kMaxWant];  // every slice's ranks, packed
+    uint32_t offs[kMaxParts + 1];         // where each slice's ranks start in cand
+    TopScratch t;
+    SelCommon c;
+};
+
+template <int NT>
+__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, SelCommon& c) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     v = wave_max_u64(v);
-    if (lane == 0) sh.red64[wave] = v;
+    if (lane == 0) c.red64[wave] = v;
     __syncthreads();
-    uint64_t r = sh.red64[0];
-    for (int w = 1; w < kSelWaves; ++w) r = sh.red64[w] > r ? sh.red64[w] : r;
-    __syncthreads();
-    return r;
-}
-
-__device__ __forceinline__ float block_max_f32(float v, SelectShared& sh) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float o = __shfl_xor(v, m);
-        v = (v < o) ? o : v;
-    }
-    if (lane == 0) sh.redf[wave] = v;
-    __syncthreads();
-    float r = sh.redf[0];
-    for (int w = 1; w < kSelWaves; ++w) r = (r < sh.redf[w]) ? sh.redf[w] : r;
+    uint64_t r = c.red64[0];
+    for (int w = 1; w < NT / 64; ++w) r = c.red64[w] > r ? c.red64[w] : r;
     __syncthreads();
     return r;
 }
 
-__device__ __forceinline__ double block_sum_f64(double v, SelectShared& sh) {
+template <int NT>
+__device__ __forceinline__ double block_sum_f64(double v, SelCommon& c) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-    if (lane == 0) sh.redd[wave] = v;
+    if (lane == 0) c.redd[wave] = v;
     __syncthreads();
     double r = 0.0;
-    for (int w = 0; w < kSelWaves; ++w) r += sh.redd[w];
+    for (int w = 0; w < NT / 64; ++w) r += c.redd[w];
     __syncthreads();
     return r;
 }
 
-__device__ __forceinline__ uint32_t block_or_u32(uint32_t v, SelectShared& sh) {
+// One exchange for three block reductions: OR of the NaN flags, max and min (NaN-ignoring).
+template <int NT>
+__device__ __forceinline__ void block_stats(uint32_t& flag, float& mx, float& mn, SelCommon& c) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v |= __shfl_xor(v, m);
-    if (lane == 0) sh.redu[wave] = v;
+    for (int m = 32; m >= 1; m >>= 1) {
+        flag |= __shfl_xor(flag, m);
+        mx = fmaxf(mx, __shfl_xor(mx, m));
+        mn = fminf(mn, __shfl_xor(mn, m));
+    }
+    if (lane == 0) {
+        c.redu[wave] = flag;
+        c.redf[wave] = mx;
+        c.redf2[wave] = mn;
+    }
     __syncthreads();
-    uint32_t r = 0;
-    for (int w = 0; w < kSelWaves; ++w) r |= sh.redu[w];
+    flag = 0;
+    mx = -INFINITY;
+    mn = INFINITY;
+    for (int w = 0; w < NT / 64; ++w) {
+        flag |= c.redu[w];
+        mx = fmaxf(mx, c.redf[w]);
+        mn = fminf(mn, c.redf2[w]);
+    }
     __syncthreads();
-    return r;
+}
+
+// exp(x) for the row sum, x = l - max <= 0 with l and max floats (so x is exact in double).
+// Tang's table method: x = k ln2/64 + r with |r| <= ln2/128 (Cody-Waite split of ln2/64),
+// exp(x) = 2^(k>>6) * 2^((k&63)/64) * e^r, e^r by its degree-5 Taylor polynomial (truncation
+// below 4e-17 relative). tbl holds 2^(j/64), j = 0..63. Within 2 ulp; only the sum over the
+// row uses it, whose summation order already differs from the reference's in the last bits.
+__device__ __forceinline__ double exp_for_sum(double x, const double* tbl) {
+    if (x < -745.5) return 0.0;  // also -inf
+    const double kInvL = 92.332482616893656;             // 64 / ln2
+    const double kLHi = 6.93147180369123816490e-01 / 64;  // ln2 / 64, high part (exact products)
+    const double kLLo = 1.90821492927058770002e-10 / 64;  // ln2 / 64, low part
+    const double kd = __builtin_rint(x * kInvL);
+    const int k = static_cast<int>(kd);
+    double r = fma(-kd, kLHi, x);
+    r = fma(-kd, kLLo, r);
+    double p = fma(r, 1.0 / 120.0, 1.0 / 24.0);
+    p = fma(r, p, 1.0 / 6.0);
+    p = fma(r, p, 0.5);
+    p = fma(r, p, 1.0);
+    p = fma(r, p, 1.0);
+    return ldexp(tbl[k & 63] * p, k >> 6);
 }
 
 // The smallest rank T with exactly `want` of the block's ranks >= T (ranks are distinct; rank
 // 0 marks an empty slot and is never selected while want <= number of real ranks). Radix
 // descent over 8-bit digits from the top, stopping once a digit bin is taken whole.
-template <typename KeyAt>
-__device__ uint64_t block_select(uint32_t per_thread, KeyAt key_at, uint32_t want,
-                                 SelectShared& sh) {
+template <int NT, int PER, typename KeyAt>
+__device__ __forceinline__ uint64_t block_select(KeyAt key_at, int per, uint32_t want, uint32_t* hist,
+                                                 SelCommon& c) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     uint64_t prefix = 0, mask = 0;
     uint32_t need = want;
     for (int shift = 56; shift >= 0; shift -= 8) {
-        for (int i = tid; i < 256; i += kSelThreads) sh.hist[i] = 0;
+        for (int i = tid; i < 256; i += NT) hist[i] = 0;
         __syncthreads();
-#pragma unroll 4
-        for (uint32_t e = 0; e < per_thread; ++e) {
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            if (e >= per) break;
             const uint64_t k = key_at(e);
-            if (k != 0 && (k & mask) == prefix) atomicAdd(&sh.hist[(k >> shift) & 255u], 1u);
+            if (k != 0 && (k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
         }
         __syncthreads();
         if (wave == 0) {
-            uint32_t c[4];
+            uint32_t cc[4];
             uint32_t t = 0;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                c[j] = sh.hist[4 * lane + j];
-                t += c[j];
+                cc[j] = hist[4 * lane + j];
+                t += cc[j];
             }
             uint32_t x = t;  // inclusive suffix sum over lanes >= lane
 #pragma unroll
@@ -148,16 +213,16 @@ __device__ uint64_t block_select(uint32_t per_thread, KeyAt key_at, uint32_t wan
             uint32_t above = x - t;
 #pragma unroll
             for (int j = 3; j >= 0; --j) {
-                if (above < need && need <= above + c[j]) {
-                    sh.misc[0] = 4 * lane + j;
-                    sh.misc[1] = above;
-                    sh.misc[2] = c[j];
+                if (above < need && need <= above + cc[j]) {
+                    c.misc[0] = 4 * lane + j;
+                    c.misc[1] = above;
+                    c.misc[2] = cc[j];
                 }
-                above += c[j];
+                above += cc[j];
             }
         }
         __syncthreads();
-        const uint32_t d = sh.misc[0], above = sh.misc[1], cnt = sh.misc[2];
+        const uint32_t d = c.misc[0], above = c.misc[1], cnt = c.misc[2];
         need -= above;
         prefix |= static_cast<uint64_t>(d) << shift;
         mask |= 255ull << shift;
@@ -166,97 +231,273 @@ __device__ uint64_t block_select(uint32_t per_thread, KeyAt key_at, uint32_t wan
     return prefix;
 }
 
-// Bitonic sort of sh.top[0..n2) into descending order, n2 a power of two <= 256.
-__device__ void block_sort_desc(SelectShared& sh, uint32_t n2) {
-    const int tid = threadIdx.x;
-    for (uint32_t k = 2; k <= n2; k <<= 1) {
-        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-            if (static_cast<uint32_t>(tid) < n2) {
-                const uint32_t i = tid, x = i ^ j;
-                if (x > i) {
-                    const uint64_t a = sh.top[i], b = sh.top[x];
-                    const bool desc = (i & k) == 0;
-                    if (desc ? (a < b) : (a > b)) {
-                        sh.top[i] = b;
-                        sh.top[x] = a;
-                    }
-                }
-            }
-            __syncthreads();
-        }
+// Appends k (where pred holds) to dst through the shared counter, one atomic per wave: the
+// wave's slots are reserved by its first active lane and handed out in lane order. Slots at
+// or beyond cap are dropped (a guard: callers reserve exactly what they need).
+__device__ __forceinline__ void wave_put(bool pred, uint64_t k, uint32_t* counter, uint64_t* dst,
+                                         uint32_t cap) {
+    const uint64_t mask = __ballot(pred);
+    if (mask == 0) return;
+    const int lane = threadIdx.x & 63;
+    const int leader = __ffsll(static_cast<long long>(mask)) - 1;
+    uint32_t base = 0;
+    if (lane == leader) base = atomicAdd(counter, static_cast<uint32_t>(__popcll(mask)));
+    base = __builtin_amdgcn_readlane(base, leader);
+    if (pred) {
+        const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                          __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+        if (base + below < cap) dst[base + below] = k;
     }
 }
 
-// Steps 5-7 of sample_token on the sorted shortlist sh.top[0..want) (sampling.cpp:168-197).
-__device__ uint32_t finish_sampled(SelectShared& sh, uint32_t want, const twd_row_params& p) {
-    const int tid = threadIdx.x;
-    const double mx = static_cast<double>(sh.gmax);
-    const double total = sh.total;
-    const double td = static_cast<double>(p.temperature);
-    if (static_cast<uint32_t>(tid) < want) {
-        const double l = static_cast<double>(rank_value(sh.top[tid]));
-        sh.e[tid] = exp(l - mx) / total;
-        sh.q[tid] = exp((l - mx) / td);
+// The block's top-`want` ranks (value desc, index asc), appended to out[0..want) in no
+// particular order; every thread returns once out is complete, with c.misc[4] holding how
+// many were found (want, unless fewer entries carry a rank). Entry e < per (per <= PER, the
+// same in every thread) of the calling thread has value val_at(e) and rank key_at(e) (0 = no
+// entry); slow_key(e) gives the same rank for the radix fallback, from memory the compiler
+// cannot keep in registers across its passes. mx / mn are the largest and smallest finite
+// values among the entries. ts.hist must be zero on entry (cleared behind an earlier barrier).
+//
+// bin(v) = floor((mx - v) * 255 / min(mx - mn, kBinRange)), capped at 254, is monotone in v,
+// so every entry of a bin nearer than the boundary bin bt outranks every entry of bt, which
+// outranks every farther one. The boundary bin's entries are ranked against each other.
+template <int NT, int PER, typename ValAt, typename KeyAt, typename SlowVal, typename SlowKey>
+__device__ __forceinline__ void block_top(ValAt val_at, KeyAt key_at, SlowVal slow_val, SlowKey slow_key,
+                                          int per, float mx, float mn, uint32_t want, uint64_t* out,
+                                          TopScratch& ts, SelCommon& c) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float span = mx - mn;
+    // 0: take every entry; 1: rank the gathered boundary bin; 2: radix inside the boundary bin;
+    // 3: radix over the whole block
+    int mode = 3;
+    uint32_t bt = kBins, above = 0, nbt = 0;
+    float scale = 0.0f;
+    auto bin_of_value = [&](float x) -> uint32_t {
+        const float dist = (mx - x) * scale;
+        return dist < static_cast<float>(kBins - 2) ? static_cast<uint32_t>(dist) : kBins - 2;
+    };
+    // each entry's bin, computed once: 8 bits per entry, 0xFF for entries without a rank
+    uint32_t bins[(PER + 3) / 4];
+#pragma unroll
+    for (int j = 0; j < (PER + 3) / 4; ++j) bins[j] = 0;
+    auto bin_at = [&](int e) -> uint32_t { return (bins[e / 4] >> (8 * (e % 4))) & 0xFFu; };
+    if (__builtin_isfinite(mx) && __builtin_isfinite(mn) && span > 0.0f) {
+        scale = static_cast<float>(kBins - 1) / (span < kBinRange ? span : kBinRange);
+        const uint32_t rep = lane & (kReps - 1);
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            if (e >= per) break;
+            if (key_at(e) != 0) {
+                const uint32_t b = bin_of_value(val_at(e));
+                atomicAdd(&ts.hist[b * kReps + rep], 1u);
+                bins[e / 4] |= b << (8 * (e % 4));
+            } else {
+                bins[e / 4] |= 0xFFu << (8 * (e % 4));  // no rank: never gathered or taken
+            }
+        }
+        __syncthreads();
+        if (wave == 0) {  // lane l owns bins 4l .. 4l+3: their replicas are 32 consecutive words
+            uint32_t cc[4], t = 0;
+            const u32x4* h4 = reinterpret_cast<const u32x4*>(ts.hist) + lane * (4 * kReps / 4);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const u32x4 a = h4[2 * j], b2 = h4[2 * j + 1];
+                cc[j] = a.x + a.y + a.z + a.w + b2.x + b2.y + b2.z + b2.w;
+                t += cc[j];
+            }
+            uint32_t x = t;  // inclusive prefix sum over lanes <= lane
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const uint32_t y = __shfl_up(x, off);
+                if (lane >= off) x += y;
+            }
+            uint32_t before = x - t;
+            if (lane == 63) {
+                c.misc[0] = kBins;  // no boundary: fewer ranked entries than want
+                c.misc[3] = 0;
+            }
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (before < want && want <= before + cc[j]) {
+                    c.misc[0] = 4 * lane + j;
+                    c.misc[1] = before;
+                    c.misc[2] = cc[j];
+                }
+                before += cc[j];
+            }
+        }
+        __syncthreads();
+        bt = c.misc[0];
+        above = c.misc[1];
+        nbt = c.misc[2];
+        mode = (bt == kBins) ? 0 : (nbt <= kGatherMax ? 1 : 2);
+    }
+
+    uint64_t thr = 0;
+    if (mode == 1) {
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            if (e >= per) break;
+            const bool in_bt = bin_at(e) == bt;
+            wave_put(in_bt, in_bt ? key_at(e) : 0ull, &c.misc[3], ts.gath, kGatherMax);
+        }
+    } else if (mode == 2) {
+        auto key_in_bin = [&](int e) -> uint64_t {
+            return bin_of_value(slow_val(e)) == bt ? slow_key(e) : 0ull;
+        };
+        thr = block_select<NT, PER>(key_in_bin, per, want - above, ts.hist, c);
+    } else if (mode == 3) {
+        thr = block_select<NT, PER>(slow_key, per, want, ts.hist, c);
+    }
+    if (tid == 0) c.misc[4] = 0;
+    __syncthreads();
+    // every entry that is taken whole, then (mode 1) the boundary bin's top `want - above`;
+    // exactly `want` ranks are written
+    if (mode == 0 || mode == 1) {
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            if (e >= per) break;
+            const bool take = bin_at(e) < (mode == 0 ? kBins - 1 : bt);  // 0xFF: no rank
+            wave_put(take, take ? key_at(e) : 0ull, &c.misc[4], out, want);
+        }
+    } else {
+        for (int e = 0; e < per; ++e) {
+            const uint64_t k = slow_key(e);
+            bool take = k != 0;
+            if (take && mode == 3) take = k >= thr;
+            if (take && mode == 2) {
+                const uint32_t b = bin_of_value(slow_val(e));
+                take = b < bt || (b == bt && k >= thr);
+            }
+            wave_put(take, k, &c.misc[4], out, want);
+        }
+    }
+    if (mode == 1) {
+        const uint32_t need = want - above;
+        for (uint32_t i0 = 0; i0 < nbt; i0 += NT) {  // the same trip count in every thread
+            const uint32_t i = i0 + tid;
+            uint64_t k = 0;
+            uint32_t higher = need;
+            if (i < nbt) {
+                k = ts.gath[i];
+                higher = 0;
+                for (uint32_t j = 0; j < nbt; ++j) higher += ts.gath[j] > k ? 1u : 0u;
+            }
+            wave_put(higher < need, k, &c.misc[4], out, want);
+        }
     }
     __syncthreads();
+}
+
+// c.sorted[0..n) = c.top[0..n) in descending order (ranks are distinct): each entry's
+// position is the number of entries above it.
+__device__ __forceinline__ void block_sort_desc(SelCommon& c, uint32_t n) {
+    const int tid = threadIdx.x;
+    if (static_cast<uint32_t>(tid) < n) {
+        const uint64_t k = c.top[tid];
+        uint32_t higher = 0;
+        for (uint32_t j = 0; j < n; ++j) higher += c.top[j] > k ? 1u : 0u;
+        c.sorted[higher] = k;
+    }
+    __syncthreads();
+}
+
+// Steps 5-7 of sample_token on the sorted shortlist c.sorted[0..want) (sampling.cpp:168-197).
+__device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, const twd_row_params& p) {
+    const int tid = threadIdx.x;
+    const double mx = static_cast<double>(c.gmax);
+    const double total = c.total;
+    const double td = static_cast<double>(p.temperature);
+    if (static_cast<uint32_t>(tid) < want) {
+        const double l = static_cast<double>(rank_value(c.sorted[tid]));
+        c.e[tid] = exp(l - mx) / total;
+        c.q[tid] = exp((l - mx) / td);
+    }
+    __syncthreads();
+    // One lane runs the reference's sequential loops in their order; entries are fetched eight
+    // at a time so the LDS latency is paid once per chunk rather than once per addition.
+    constexpr uint32_t kChunk = 8;
     if (tid == 0) {
         uint32_t cut = want;
         if (p.top_p < 1.0f) {
             const double pp = static_cast<double>(p.top_p);
             double run = 0.0;
-            for (uint32_t i = 0; i < want; ++i) {
-                run += sh.e[i];
-                if (run >= pp) {
-                    cut = i + 1;
-                    break;
+            bool found = false;
+            for (uint32_t i0 = 0; i0 < want && !found; i0 += kChunk) {
+                double ev[kChunk];
+#pragma unroll
+                for (uint32_t j = 0; j < kChunk; ++j) ev[j] = c.e[min(i0 + j, want - 1)];
+#pragma unroll
+                for (uint32_t j = 0; j < kChunk; ++j) {
+                    if (!found && i0 + j < want) {
+                        run += ev[j];
+                        if (run >= pp) {
+                            cut = i0 + j + 1;
+                            found = true;
+                        }
+                    }
                 }
             }
         }
         if (p.top_k > 0 && cut > static_cast<uint32_t>(p.top_k)) cut = static_cast<uint32_t>(p.top_k);
         if (cut < 1) cut = 1;
         double denom = 0.0;
-        for (uint32_t i = 0; i < cut; ++i) {
-            denom += sh.q[i];
-            sh.q[i] = denom;  // the running sums acc_i of the draw loop
-        }
-        const double r = static_cast<double>(p.uniform) * denom;
-        uint32_t tok = rank_index(sh.top[cut - 1]);
-        for (uint32_t i = 0; i < cut; ++i) {
-            if (sh.q[i] >= r) {
-                tok = rank_index(sh.top[i]);
-                break;
+        for (uint32_t i0 = 0; i0 < cut; i0 += kChunk) {
+            double qv[kChunk];
+#pragma unroll
+            for (uint32_t j = 0; j < kChunk; ++j) qv[j] = c.q[min(i0 + j, cut - 1)];
+#pragma unroll
+            for (uint32_t j = 0; j < kChunk; ++j) {
+                if (i0 + j < cut) {
+                    denom += qv[j];
+                    c.q[i0 + j] = denom;  // the running sums acc_i of the draw loop
+                }
             }
         }
-        sh.misc[4] = tok;
+        const double r = static_cast<double>(p.uniform) * denom;
+        uint32_t pick = cut - 1;
+        bool found = false;
+        for (uint32_t i0 = 0; i0 < cut && !found; i0 += kChunk) {
+            double qv[kChunk];
+#pragma unroll
+            for (uint32_t j = 0; j < kChunk; ++j) qv[j] = c.q[min(i0 + j, cut - 1)];
+#pragma unroll
+            for (uint32_t j = 0; j < kChunk; ++j) {
+                if (!found && i0 + j < cut && qv[j] >= r) {
+                    pick = i0 + j;
+                    found = true;
+                }
+            }
+        }
+        c.misc[5] = rank_index(c.sorted[pick]);
     }
     __syncthreads();
-    return sh.misc[4];
+    return c.misc[5];
 }
 
-// After sh.top[0..want) holds the row's shortlist and sh.gmax/total/flag its statistics:
+// After c.top[0..want) holds the row's shortlist and c.gmax/total/flag its statistics:
 // the degenerate check of sampling.cpp:145-147, the shortlist sort, and steps 5-7.
-__device__ void finish_row(SelectShared& sh, uint32_t want, const twd_row_params& p,
+__device__ __forceinline__ void finish_row(SelCommon& c, uint32_t want, const twd_row_params& p,
                            uint32_t* token_out) {
     const int tid = threadIdx.x;
-    if (sh.flag != 0 || !(sh.total > 0.0)) {
+    if (c.flag != 0 || !(c.total > 0.0)) {
         if (tid == 0) *token_out = TWD_TOKEN_DEGENERATE;
         return;
     }
-    uint32_t n2 = 1;
-    while (n2 < want) n2 <<= 1;
-    if (static_cast<uint32_t>(tid) >= want && static_cast<uint32_t>(tid) < n2) sh.top[tid] = 0;
-    __syncthreads();
-    block_sort_desc(sh, n2);
-    const uint32_t tok = finish_sampled(sh, want, p);
+    block_sort_desc(c, want);
+    const uint32_t tok = finish_sampled(c, want, p);
     if (tid == 0) *token_out = tok;
 }
 
 // SelectArgs is the first kernel argument, so it sits at offset 0 of the kernarg segment. The
 // row's parameters are read through that pointer: indexing the by-value argument with
 // blockIdx.y would make the compiler copy all of it into per-lane scratch memory.
-__global__ __launch_bounds__(kSelThreads) void select_slice_kernel(SelectArgs args_by_value, SelectBufs b) {
+__global__ __launch_bounds__(kSliceThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void select_slice_kernel(SelectArgs args_by_value, SelectBufs b) {
+    constexpr int NT = kSliceThreads;
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    SelectShared& sh = *reinterpret_cast<SelectShared*>(smem_raw);
+    SliceShared& sh = *reinterpret_cast<SliceShared*>(smem_raw);
 #if __HIP_DEVICE_COMPILE__
     const SelectArgs& args =
         *reinterpret_cast<const SelectArgs*>(__builtin_amdgcn_kernarg_segment_ptr());
@@ -274,17 +515,18 @@ __global__ __launch_bounds__(kSelThreads) void select_slice_kernel(SelectArgs ar
     float v[kSelPerThread];
 #pragma unroll
     for (int e = 0; e < kSelPerThread; ++e) {
-        const uint32_t i = lo + tid + kSelThreads * e;
+        const uint32_t i = lo + tid + NT * e;
         v[e] = i < hi ? lg[i] : 0.0f;
     }
+    for (uint32_t i = tid; i < kReps * kBins; i += NT) sh.t.hist[i] = 0;  // for block_top
 
     // ---- repetition penalty, sampling.cpp:103-119 ----
     if (p.repetition_penalty != 1.0f && p.history_len > 0) {
 #pragma unroll
-        for (int e = 0; e < kSelPerThread; ++e) sh.u.cnt[tid + kSelThreads * e] = 0;
+        for (int e = 0; e < kSelPerThread; ++e) sh.u.cnt[tid + NT * e] = 0;
         __syncthreads();
         const uint32_t* hist = b.history + p.history_offset;
-        for (uint32_t j = tid; j < p.history_len; j += kSelThreads) {
+        for (uint32_t j = tid; j < p.history_len; j += NT) {
             const uint32_t id = hist[j];
             if (id >= lo && id < hi) atomicAdd(&sh.u.cnt[id - lo], 1u);
         }
@@ -293,7 +535,7 @@ __global__ __launch_bounds__(kSelThreads) void select_slice_kernel(SelectArgs ar
         const float limit = (p.softcap > 0.0f) ? p.softcap * 0.9999f : 0.0f;
 #pragma unroll
         for (int e = 0; e < kSelPerThread; ++e) {
-            const uint32_t n = sh.u.cnt[tid + kSelThreads * e];
+            const uint32_t n = sh.u.cnt[tid + NT * e];
             if (n == 0) continue;
             float x = v[e];
             for (uint32_t t = 0; t < n; ++t) {
@@ -304,24 +546,25 @@ __global__ __launch_bounds__(kSelThreads) void select_slice_kernel(SelectArgs ar
                 }
             }
             v[e] = x;
-            lg[lo + tid + kSelThreads * e] = x;
+            lg[lo + tid + NT * e] = x;
         }
     }
     if (args.penalty_only) return;
 
+    auto key_at = [&](int e) -> uint64_t {
+        const uint32_t i = lo + tid + NT * e;
+        return i < hi ? rank_key(v[e], i) : 0ull;
+    };
     const bool greedy = !(p.temperature > 0.0f);
     if (greedy) {
         // ---- sampling.cpp:126-133 ----
         uint64_t k = 0;
 #pragma unroll
         for (int e = 0; e < kSelPerThread; ++e) {
-            const uint32_t i = lo + tid + kSelThreads * e;
-            if (i < hi) {
-                const uint64_t r = rank_key(v[e], i);
-                k = r > k ? r : k;
-            }
+            const uint64_t r = key_at(e);
+            k = r > k ? r : k;
         }
-        k = block_max_u64(k, sh);
+        k = block_max_u64<NT>(k, sh.c);
         if (parts == 1) {
             if (tid == 0) b.tokens[row] = rank_index(k);
             return;
@@ -331,53 +574,46 @@ __global__ __launch_bounds__(kSelThreads) void select_slice_kernel(SelectArgs ar
     }
 
     // ---- sampled: slice statistics, sampling.cpp:138-147 ----
+    // Any NaN makes the row degenerate, so the max only has to be right for NaN-free rows.
     uint32_t nan_seen = 0;
-    float mx = -INFINITY;
-    bool any = false;
+    float mx = -INFINITY, mn = INFINITY;
 #pragma unroll
     for (int e = 0; e < kSelPerThread; ++e) {
-        const uint32_t i = lo + tid + kSelThreads * e;
-        if (i < hi) {
+        sh.u.vals[tid + NT * e] = v[e];  // the slot's count was read by this same thread
+        if (lo + tid + NT * e < hi) {
             if (v[e] != v[e]) nan_seen = 1;
-            mx = any ? ((mx < v[e]) ? v[e] : mx) : v[e];
-            any = true;
+            mx = fmaxf(mx, v[e]);
+            if (__builtin_isfinite(v[e])) mn = fminf(mn, v[e]);
         }
     }
-    __syncthreads();  // the penalty's counts are dead from here on: the region now holds values
-#pragma unroll
-    for (int e = 0; e < kSelPerThread; ++e) sh.u.val[tid + kSelThreads * e] = v[e];
-    nan_seen = block_or_u32(nan_seen, sh);
-    mx = block_max_f32(any ? mx : -INFINITY, sh);
+    if (tid < 64) sh.c.exp2_tbl[tid] = exp2(static_cast<double>(tid) / 64.0);
+    block_stats<NT>(nan_seen, mx, mn, sh.c);  // its barriers also retire the penalty's counts
     const double dmx = static_cast<double>(mx);
     double s = 0.0;
-    const uint32_t n_here = hi - lo;
-#pragma unroll 2
-    for (uint32_t e = 0; e < kSelPerThread; ++e) {
-        const uint32_t i = tid + kSelThreads * e;
-        if (i < n_here) s += exp(static_cast<double>(sh.u.val[i]) - dmx);
-    }
-    s = block_sum_f64(s, sh);
+#pragma unroll
+    for (int e = 0; e < kSelPerThread; ++e)
+        if (lo + tid + NT * e < hi) s += exp_for_sum(static_cast<double>(v[e]) - dmx, sh.c.exp2_tbl);
+    s = block_sum_f64<NT>(s, sh.c);
+    // A slice of -inf entries only adds exp(-inf - row max) = 0 to the row's sum whenever the
+    // row has a finite maximum elsewhere (its own exp(-inf - -inf) would be NaN). If the whole
+    // row is -inf every slice reports 0, the row total is 0 and the row is degenerate, as the
+    // reference's NaN total makes it.
+    if (mx == -INFINITY) s = 0.0;
 
     // ---- shortlist of this slice, sampling.cpp:149-166 ----
     const uint32_t want_row = (p.top_k > 0) ? min(static_cast<uint32_t>(p.top_k), b.vocab)
                                             : min(kMaxWant, b.vocab);
+    const uint32_t n_here = hi - lo;
     const uint32_t want = min(want_row, n_here);
-    auto local_key = [&](uint32_t e) -> uint64_t {
-        const uint32_t i = tid + kSelThreads * e;
-        return i < n_here ? rank_key(sh.u.val[i], lo + i) : 0ull;
+    auto val_at = [&](int e) -> float { return v[e]; };
+    auto slow_val = [&](int e) -> float { return sh.u.vals[tid + NT * e]; };
+    auto slow_key = [&](int e) -> uint64_t {
+        const uint32_t i = lo + tid + NT * e;
+        return i < hi ? rank_key(sh.u.vals[tid + NT * e], i) : 0ull;
     };
-    const uint64_t thr = block_select(kSelPerThread, local_key, want, sh);
-    if (tid == 0) sh.misc[3] = 0;
-    __syncthreads();
-    uint64_t* out = (parts == 1) ? sh.top : b.cand + (static_cast<size_t>(row) * parts + part) * kMaxWant;
-#pragma unroll 4
-    for (uint32_t e = 0; e < kSelPerThread; ++e) {
-        const uint64_t k = local_key(e);
-        if (k != 0 && k >= thr) {
-            const uint32_t pos = atomicAdd(&sh.misc[3], 1u);
-            if (pos < want) out[pos] = k;  // exactly `want` ranks pass; the bound is a guard
-        }
-    }
+    uint64_t* out = (parts == 1) ? sh.c.top : b.cand + (static_cast<size_t>(row) * parts + part) * kMaxWant;
+    block_top<NT, kSelPerThread>(val_at, key_at, slow_val, slow_key, kSelPerThread, mx, mn, want, out,
+                                 sh.t, sh.c);
 
     if (parts > 1) {
         if (tid == 0) {
@@ -385,85 +621,105 @@ __global__ __launch_bounds__(kSelThreads) void select_slice_kernel(SelectArgs ar
             b.part_max[o] = mx;
             b.part_sum[o] = s;
             b.part_flag[o] = nan_seen;
-            b.part_count[o] = want;
+            b.part_count[o] = min(sh.c.misc[4], want);  // fewer only when NaNs hold no rank
         }
         return;  // select_merge_kernel finishes the row
     }
     if (tid == 0) {
-        sh.gmax = mx;
-        sh.total = s;
-        sh.flag = nan_seen;
+        sh.c.gmax = mx;
+        sh.c.total = s;
+        sh.c.flag = nan_seen;
     }
     __syncthreads();
-    finish_row(sh, want_row, p, b.tokens + row);
+    finish_row(sh.c, want_row, p, b.tokens + row);
 }
 
 // Second launch when a row spans several slices: global max, the rescaled sum of exponentials,
 // the global shortlist from every slice's candidates, then the draw. One block per row.
-__global__ __launch_bounds__(kSelThreads) void select_merge_kernel(SelectArgs args_by_value, SelectBufs b) {
+__global__ __launch_bounds__(kMergeThreads) void select_merge_kernel(SelectArgs args_by_value, SelectBufs b) {
+    constexpr int NT = kMergeThreads;
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    SelectShared& sh = *reinterpret_cast<SelectShared*>(smem_raw);
+    MergeShared& sh = *reinterpret_cast<MergeShared*>(smem_raw);
 #if __HIP_DEVICE_COMPILE__
     const SelectArgs& args =
         *reinterpret_cast<const SelectArgs*>(__builtin_amdgcn_kernarg_segment_ptr());
 #else
     const SelectArgs& args = args_by_value;
 #endif
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
     const uint32_t row = blockIdx.x;
-    const uint32_t parts = args.parts;
+    const uint32_t parts = args.parts;  // <= kMaxParts = 64: one lane of wave 0 per slice
     const twd_row_params p = args.p[row];
     const size_t o = static_cast<size_t>(row) * parts;
 
     if (!(p.temperature > 0.0f)) {  // greedy: the best rank over the slices
-        uint64_t m = 0;
-        for (uint32_t q = tid; q < parts; q += kSelThreads) {
-            const uint64_t x = b.part_key[o + q];
-            m = x > m ? x : m;
+        if (tid < 64) {
+            const uint64_t m = wave_max_u64(static_cast<uint32_t>(lane) < parts ? b.part_key[o + lane] : 0ull);
+            if (tid == 0) b.tokens[row] = rank_index(m);
         }
-        m = block_max_u64(m, sh);
-        if (tid == 0) b.tokens[row] = rank_index(m);
         return;
     }
     const uint32_t want_row = (p.top_k > 0) ? min(static_cast<uint32_t>(p.top_k), b.vocab)
                                             : min(kMaxWant, b.vocab);
-    if (tid == 0) {
-        float gm = b.part_max[o];
-        uint32_t fl = b.part_flag[o];
-        for (uint32_t q = 1; q < parts; ++q) {
-            const float x = b.part_max[o + q];
-            gm = (gm < x) ? x : gm;
-            fl |= b.part_flag[o + q];
+    for (uint32_t i = tid; i < kReps * kBins; i += NT) sh.t.hist[i] = 0;  // for block_top
+    // Wave 0: global max and NaN flag over the slices, the row sum
+    // sum_q part_sum[q] * exp(part_max[q] - max), and where each slice's ranks go.
+    if (tid < 64) {
+        const bool live = static_cast<uint32_t>(lane) < parts;
+        const float pm = live ? b.part_max[o + lane] : -INFINITY;
+        const double ps = live ? b.part_sum[o + lane] : 0.0;
+        uint32_t fl = live ? b.part_flag[o + lane] : 0u;
+        const uint32_t cnt = live ? b.part_count[o + lane] : 0u;
+        float gm = pm;
+        uint32_t x = cnt;  // inclusive prefix sum of the counts
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            gm = fmaxf(gm, __shfl_xor(gm, m));
+            fl |= __shfl_xor(fl, m);
         }
-        double tot = 0.0;
-        for (uint32_t q = 0; q < parts; ++q)
-            tot += b.part_sum[o + q] *
-                   exp(static_cast<double>(b.part_max[o + q]) - static_cast<double>(gm));
-        sh.gmax = gm;
-        sh.total = tot;
-        sh.flag = fl;
-    }
-    for (uint32_t f = tid; f < kMaxParts * kMaxWant; f += kSelThreads) {
-        const uint32_t q = f / kMaxWant, slot = f % kMaxWant;
-        uint64_t k = 0;
-        if (q < parts && slot < b.part_count[o + q]) k = b.cand[(o + q) * kMaxWant + slot];
-        sh.u.cand[f] = k;
-    }
-    __syncthreads();
-    auto merge_key = [&](uint32_t e) -> uint64_t { return sh.u.cand[tid + kSelThreads * e]; };
-    const uint64_t thr = block_select(kMergePerThread, merge_key, want_row, sh);
-    if (tid == 0) sh.misc[3] = 0;
-    __syncthreads();
-#pragma unroll 4
-    for (uint32_t e = 0; e < kMergePerThread; ++e) {
-        const uint64_t k = merge_key(e);
-        if (k != 0 && k >= thr) {
-            const uint32_t pos = atomicAdd(&sh.misc[3], 1u);
-            if (pos < want_row) sh.top[pos] = k;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint32_t y = __shfl_up(x, off);
+            if (lane >= off) x += y;
+        }
+        double contrib = live ? ps * exp(static_cast<double>(pm) - static_cast<double>(gm)) : 0.0;
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) contrib += __shfl_xor(contrib, m);
+        sh.offs[lane] = x - cnt;
+        if (lane == 63) sh.offs[kMaxParts] = x;
+        if (lane == 0) {
+            sh.c.gmax = gm;
+            sh.c.total = contrib;
+            sh.c.flag = fl;
         }
     }
     __syncthreads();
-    finish_row(sh, want_row, p, b.tokens + row);
+    const uint32_t n_cand = sh.offs[kMaxParts];
+    const float gm = sh.c.gmax;
+    // every slice's ranks, packed into cand[0 .. n_cand)
+    float cmn = INFINITY;
+    for (uint32_t f = tid; f < parts * want_row; f += NT) {
+        const uint32_t q = f / want_row, slot = f % want_row;
+        const uint32_t at = sh.offs[q] + slot;
+        if (at < sh.offs[q + 1]) {
+            const uint64_t k = b.cand[(o + q) * kMaxWant + slot];
+            sh.cand[at] = k;
+            const float x = rank_value(k);
+            if (k != 0 && __builtin_isfinite(x)) cmn = fminf(cmn, x);
+        }
+    }
+    uint32_t no_flag = 0;
+    float no_max = -INFINITY;
+    block_stats<NT>(no_flag, no_max, cmn, sh.c);  // its barriers also publish sh.cand
+    auto merge_key = [&](int e) -> uint64_t {
+        const uint32_t f = tid + NT * e;
+        return f < n_cand ? sh.cand[f] : 0ull;
+    };
+    auto merge_val = [&](int e) -> float { return rank_value(merge_key(e)); };
+    const int per = static_cast<int>((n_cand + NT - 1) / NT);
+    block_top<NT, kMergePerThread>(merge_val, merge_key, merge_val, merge_key, per, gm, cmn, want_row,
+                                   sh.c.top, sh.t, sh.c);
+    finish_row(sh.c, want_row, p, b.tokens + row);
 }
 
 __global__ void verify_compare_kernel(const uint32_t* row_tokens, uint32_t rows,
@@ -574,11 +830,10 @@ int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_
     b.part_count = s.part_count;
     b.part_key = s.part_key;
     b.cand = s.cand;
-    const size_t smem = sizeof(SelectShared);
-    select_slice_kernel<<<dim3(parts, rows), kSelThreads, smem, stream>>>(a, b);
+    select_slice_kernel<<<dim3(parts, rows), kSliceThreads, sizeof(SliceShared), stream>>>(a, b);
     TWD_HIP(hipGetLastError());
     if (parts > 1 && !penalty_only) {
-        select_merge_kernel<<<rows, kSelThreads, smem, stream>>>(a, b);
+        select_merge_kernel<<<rows, kMergeThreads, sizeof(MergeShared), stream>>>(a, b);
         TWD_HIP(hipGetLastError());
     }
     return TWD_OK;
@@ -603,15 +858,15 @@ TWD_API int twd_selector_create(uint32_t max_vocab, uint32_t max_rows, twd_selec
     *out = nullptr;
     if (max_vocab == 0 || max_rows == 0 || max_rows > TWD_MAX_ROWS + 1)
         return fail(TWD_E_INVALID, "max_vocab must be > 0 and max_rows in 1..65");
-    if (parts_for(max_vocab) > kMaxParts) return fail(TWD_E_UNSUPPORTED, "max_vocab above 1048576");
+    if (parts_for(max_vocab) > kMaxParts) return fail(TWD_E_UNSUPPORTED, "max_vocab above 524288");
     static bool attr_done = false;
     if (!attr_done) {
         TWD_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(select_slice_kernel),
                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    static_cast<int>(sizeof(SelectShared))));
+                                    static_cast<int>(sizeof(SliceShared))));
         TWD_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(select_merge_kernel),
                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    static_cast<int>(sizeof(SelectShared))));
+                                    static_cast<int>(sizeof(MergeShared))));
         attr_done = true;
     }
     twd_selector* s = new twd_selector();

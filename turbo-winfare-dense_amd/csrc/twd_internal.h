@@ -36,9 +36,6 @@ constexpr uint32_t kUnitNibbleBytes = 1024;
 constexpr uint32_t kUnitBytes = 1152;
 
 // ---- selection -----------------------------------------------------------------------------------
-constexpr uint32_t kSelThreads = 1024;
-constexpr uint32_t kSelPerThread = 16;
-constexpr uint32_t kSlice = kSelThreads * kSelPerThread;  // vocabulary entries per select block
 constexpr uint32_t kMaxWant = TWD_MAX_WANT;
 
 // Orderable 32-bit key of a float: larger float -> larger key, -0 folded into +0. NaN maps to 0
