@@ -79,6 +79,21 @@ def test_logits_parity(torch_dev, oracle, M):
     assert ratio <= 1.0
 
 
+@pytest.mark.parametrize("d,M", [(128, 1), (128, 20), (384, 5), (384, 17), (640, 64), (256, 64)])
+def test_logits_parity_odd_and_short_depth(torch_dev, oracle, d, M):
+    # d/128 odd (1, 3, 5 chunks): the kernels pad the last super-unit with a zero chunk, which
+    # must add exactly nothing; d = 256 is the shortest even depth (one stage)
+    V = 300
+    W, S, B = oracle.gen_lm_head(7 * d + M, V, d)
+    head = make_head(torch_dev, W, S, B, V, d, CAP)
+    hb = hidden_bf16(d + M, M, d)
+    got = head.logits(to_dev_bf16(torch_dev, hb)).cpu().numpy()
+    want = oracle_rows(oracle, W, S, B, hb, CAP)
+    ratio, err, _ = allclose_report(got, want, 1e-3, 1e-3)
+    print(f"d={d} M={M} max|err|={err:.3e} worst tolerance ratio {ratio:.3f}")
+    assert ratio <= 1.0
+
+
 def _reference_test_weights(rows, d, seed):
     # the value ranges of tests/test_gpu_kernels.cpp:272-275 and :532-535
     rng = np.random.default_rng(seed)

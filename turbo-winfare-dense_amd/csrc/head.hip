@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 #include <cstring>
 #include <string>
 
@@ -429,7 +430,10 @@ __global__ __launch_bounds__(kHeadThreads) void prep_hidden_kernel(const uint16_
                                                                    u32x4_t* __restrict__ hx) {
     const uint32_t per_chunk = NMT * 256;  // 16 B vectors per chunk (NMT*16 rows x 16)
     const uint32_t nunits = d / kChunkK;
-    const uint32_t task = blockIdx.x * kHeadThreads + threadIdx.x;  // grid covers nunits chunks
+    // an odd chunk count is padded with one zero chunk: the kernel always computes both
+    // chunks of a stage, and a zero h makes the padding add exactly nothing
+    const uint32_t padded = nunits + (nunits & 1);
+    const uint32_t task = blockIdx.x * kHeadThreads + threadIdx.x;  // grid covers padded chunks
     const uint32_t U = task / per_chunk, rem = task % per_chunk;
     const uint32_t m = rem >> 4, c = rem & 15;
     u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
@@ -439,7 +443,7 @@ __global__ __launch_bounds__(kHeadThreads) void prep_hidden_kernel(const uint16_
     s += __shfl_xor(s, 1);
     s += __shfl_xor(s, 2);
     s += __shfl_xor(s, 4);
-    if (U < nunits) {
+    if (U < padded) {
         hp[((static_cast<size_t>(U) * NMT + (m >> 4)) * 4 + (c >> 2)) * 64 + (c & 3) * 16 + (m & 15)] =
             prep_h(v);
         if ((c & 7) == 0) {
@@ -449,90 +453,111 @@ __global__ __launch_bounds__(kHeadThreads) void prep_hidden_kernel(const uint16_
                 return x + (((static_cast<size_t>(g >> 2) * NMT + (m >> 4)) * 4 + kg) * 16 + (m & 15)) * 4 +
                        (g & 3);
             };
-            bias_slices(s, at);
-            // an odd chunk count leaves groups 2, 3 of the last super-unit empty
-            if ((nunits & 1) && U == nunits - 1) bias_slices(0.0f, [&](int kg) { return at(kg) + 2; });
+            bias_slices(s, at);  // zero slices for the padding chunk's two groups
         }
     }
 }
 
 // Block = 4 waves; wave w owns RT consecutive 16-row tiles. NMT = number of 16-wide m tiles
 // (1 for M <= 16, 4 for M <= 64); NI = accumulator lanes per m tile that can hold a live row.
-// A stage is one super-unit (two chunks): one barrier per stage, the next stage's h loaded into
-// registers while this one computes, and a two-deep register ring of weight units per row tile.
-// Each group runs all RT x NMT MFMA chains before its FMAs, so results are consumed well after
-// the MFMA pipe produced them. hp holds one chunk past the end, so stage loads are unconditional.
+// A stage is one super-unit (two chunks). Each stage: one barrier; the next stage's h loaded
+// into registers and stored to the other LDS buffer at the stage's end; the weights of the
+// stage after next requested into a three-deep register ring (stage S reads buffer S % 3).
+// The loop body has no branch and every ring slot keeps its registers, so the compiler's
+// memory waits stay partial and the ring stays in flight across stages.
 template <int NMT, int NI, int RT, int MODE>
 __global__ __launch_bounds__(kHeadThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void head_wide_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_t* __restrict__ hx) {
-    constexpr int PF = 2;
-    __shared__ u32x4_t sA[2][PF][NMT][4][64];
-    __shared__ u32x4_t sXA[2][NMT][64];
+    constexpr int kVec = NMT * 4 * 64;  // 16 B A-fragment vectors per chunk
+    constexpr int kXA = NMT * 64;       // 16 B bias vectors per super-unit
+    constexpr int kPer = 2 * kVec / kHeadThreads;  // h vectors per thread and stage
+    __shared__ u32x4_t sA[2][2 * kVec];  // [stage parity][chunk of the stage][mt][t][lane]
+    __shared__ u32x4_t sXA[2][kXA];
     __shared__ EpiShared se;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const uint32_t tile0 = (blockIdx.x * kHeadWaves + wave_id()) * RT;
+    const uint32_t wave = wave_id();
+    const uint32_t tile0 = (blockIdx.x * kHeadWaves + wave) * RT;
     const uint32_t magic = vgpr_const(0x43004300u);
-    constexpr int kVec = NMT * 4 * 64;  // 16 B vectors per chunk
-    constexpr int kXA = NMT * 64;       // 16 B bias vectors per super-unit
-
-    u32x4_t hv[PF][kVec / kHeadThreads];
-    u32x4_t xv_st = u32x4_t{0u, 0u, 0u, 0u};
-    auto stage_load = [&](uint32_t S) {
-        const u32x4_t* src = hp + static_cast<size_t>(S) * PF * kVec;
-#pragma unroll
-        for (int u = 0; u < PF; ++u)
-#pragma unroll
-            for (int it = 0; it < kVec / kHeadThreads; ++it)
-                hv[u][it] = (src + u * kVec + kHeadThreads * it)[tid];
-        if (tid < kXA) xv_st = hx[static_cast<size_t>(S) * kXA + tid];
-    };
-    auto stage_store = [&](int buf) {
-#pragma unroll
-        for (int u = 0; u < PF; ++u) {
-            u32x4_t* dst = &sA[buf][u][0][0][0];
-#pragma unroll
-            for (int it = 0; it < kVec / kHeadThreads; ++it) dst[tid + kHeadThreads * it] = hv[u][it];
-        }
-        if (tid < kXA) (&sXA[buf][0][0])[tid] = xv_st;
-    };
-
-    f32x4_t tot[RT][NMT], bacc[RT][NMT];
-#pragma unroll
-    for (int j = 0; j < RT; ++j)
-#pragma unroll
-        for (int mt = 0; mt < NMT; ++mt) {
-            tot[j][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-            bacc[j][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        }
+    const uint32_t nstages = (a.nunits + 1) / 2;
 
     __amdgpu_buffer_rsrc_t rs[RT];
     tile_streams<RT>(a, tile0, rs);
     const uint32_t vo_w = lane * 16, vo_s = kUnitNibbleBytes + (lane & 15) * 8;
-    u32x4_t wq[PF][RT];
-    u32x2_t sq[PF][RT];
+
+    // Stage S's h: loaded into registers at the start of stage S-1, stored to LDS buffer P at
+    // its end; hp and hx hold one stage past the end, so the loads need no branch.
+    u32x4_t hv[kPer];
+    u32x4_t xv_st = u32x4_t{0u, 0u, 0u, 0u};
+    auto stage_load = [&](uint32_t S) {
+        const u32x4_t* src = hp + static_cast<size_t>(S) * 2 * kVec;
 #pragma unroll
-    for (int u = 0; u < PF; ++u)
-        if (static_cast<uint32_t>(u) < a.nunits) load_unit<RT>(rs, u, vo_w, vo_s, wq[u], sq[u]);
+        for (int it = 0; it < kPer; ++it) hv[it] = (src + kHeadThreads * it)[tid];
+        if (tid < kXA) xv_st = hx[static_cast<size_t>(S) * kXA + tid];
+    };
+    auto stage_store = [&](int P) {
+#pragma unroll
+        for (int it = 0; it < kPer; ++it) sA[P][kHeadThreads * it + tid] = hv[it];
+        if (tid < kXA) sXA[P][tid] = xv_st;
+    };
+    // Stage S's weights into register buffer P: both chunks' nibbles, and the four groups'
+    // {b, t} words side by side, which is also the bias MFMA's B fragment. Chunks past the
+    // end re-read the last one; their h is zero, so they add nothing.
+    constexpr int NB = 3;  // weight buffers: stage S reads buffer S % 3 and requests stage S + 2
+    u32x4_t wr[NB][2][RT];
+    u32x4_t br[NB][RT];
+    auto stage_w = [&](uint32_t S, int P) {
+        const uint32_t U0 = min(2 * S, a.nunits - 1), U1 = min(2 * S + 1, a.nunits - 1);
+#pragma unroll
+        for (int j = 0; j < RT; ++j) {
+            wr[P][0][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                          rs[j], vo_w, static_cast<int>(U0 * kUnitBytes), kNonTemporal));
+            wr[P][1][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                          rs[j], vo_w, static_cast<int>(U1 * kUnitBytes), kNonTemporal));
+            const u32x2_t lo = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
+                                                               rs[j], vo_s, static_cast<int>(U0 * kUnitBytes), kNonTemporal));
+            const u32x2_t hi = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
+                                                               rs[j], vo_s, static_cast<int>(U1 * kUnitBytes), kNonTemporal));
+            br[P][j] = u32x4_t{lo.x, lo.y, hi.x, hi.y};
+        }
+    };
+
+    f32x4_t tot[RT][NMT];
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt) tot[j][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    // Software pipeline over group steps (two per chunk, parity = the group g): while the MFMA
+    // chains of step s run into acc[g], the VALU applies step s-1's scales from acc[g ^ 1]
+    // (tot += t * acc) and converts step s+1's nibbles into bq[g ^ 1].
+    f32x4_t acc[2][RT][NMT];
+    float tp[2][RT];
+    bf16x8_t bq[2][RT][2];
+
     stage_load(0);
     stage_store(0);
+    stage_w(0, 0);
+    stage_w(1, 1);
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+        tp[1][j] = 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt) acc[1][j][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        bq[0][j][0] = nibbles_to_bf16(wr[0][0][j].x, magic);
+        bq[0][j][1] = nibbles_to_bf16(wr[0][0][j].y, magic);
+    }
 
-    const uint32_t nstages = (a.nunits + PF - 1) / PF;
-    for (uint32_t S = 0; S < nstages; ++S) {
-        __syncthreads();
-        const int buf = S & 1;
-        const bool more = (S + 1) < nstages;
-        if (more) stage_load(S + 1);
-        u32x4_t bp[RT];  // {b, t} words of the super-unit's four groups: the bias B fragment
+    auto stage = [&](uint32_t S, auto which) {
+        constexpr int B = decltype(which)::value;  // weight buffer of stage S
+        constexpr int B1 = (B + 1) % NB, B2 = (B + 2) % NB;
+        const int P = S & 1;                       // LDS buffer of stage S
+        __syncthreads();  // stage S's h is in sA[P]; sA[P ^ 1] is free
+        stage_load(S + 1);
+        stage_w(S + 2, B2);
 #pragma unroll
-        for (int u = 0; u < PF; ++u) {
-            const uint32_t U = S * PF + u;
-            if (U >= a.nunits) {  // odd chunk count: no second unit
-#pragma unroll
-                for (int j = 0; j < RT; ++j) bp[j].z = bp[j].w = 0u;
-                break;
-            }
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
             for (int g = 0; g < 2; ++g) {
                 bf16x8_t av[NMT][2];
@@ -540,57 +565,68 @@ void head_wide_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_t*
                 for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
                     for (int t = 0; t < 2; ++t)
-                        av[mt][t] = __builtin_bit_cast(bf16x8_t, sA[buf][u][mt][2 * g + t][lane]);
-                f32x4_t acc[RT][NMT];
+                        av[mt][t] = __builtin_bit_cast(bf16x8_t, sA[P][u * kVec + (mt * 4 + 2 * g + t) * 64 + lane]);
 #pragma unroll
-                for (int j = 0; j < RT; ++j) {
-                    const bf16x8_t b0 = nibbles_to_bf16(wq[u][j][2 * g], magic);
-                    const bf16x8_t b1 = nibbles_to_bf16(wq[u][j][2 * g + 1], magic);
+                for (int j = 0; j < RT; ++j)
 #pragma unroll
                     for (int mt = 0; mt < NMT; ++mt) {
-                        acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            av[mt][0], b0, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                        acc[j][mt] =
-                            __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt][1], b1, acc[j][mt], 0, 0, 0);
+                        acc[g][j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            av[mt][0], bq[g][j][0], f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        acc[g][j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt][1], bq[g][j][1],
+                                                                                acc[g][j][mt], 0, 0, 0);
                     }
-                }
 #pragma unroll
-                for (int j = 0; j < RT; ++j) {
-                    const float t = bf16_hi(g ? sq[u][j].y : sq[u][j].x);
+                for (int j = 0; j < RT; ++j)
 #pragma unroll
                     for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
-                        for (int i = 0; i < NI; ++i) tot[j][mt][i] = fmaf(t, acc[j][mt][i], tot[j][mt][i]);
-                }
-            }
+                        for (int i = 0; i < NI; ++i)
+                            tot[j][mt][i] = fmaf(tp[g ^ 1][j], acc[g ^ 1][j][mt][i], tot[j][mt][i]);
+                // the next step's nibbles: this chunk's second group, the next chunk, or the
+                // next stage's first chunk (buffer P ^ 1, requested at this stage's start)
 #pragma unroll
-            for (int j = 0; j < RT; ++j) {
-                if (u == 0) {
-                    bp[j].x = sq[u][j].x;
-                    bp[j].y = sq[u][j].y;
-                } else {
-                    bp[j].z = sq[u][j].x;
-                    bp[j].w = sq[u][j].y;
+                for (int j = 0; j < RT; ++j) {
+                    const u32x4_t& nx = (g == 0) ? wr[B][u][j] : (u == 0 ? wr[B][1][j] : wr[B1][0][j]);
+                    bq[g ^ 1][j][0] = nibbles_to_bf16(g == 0 ? nx.z : nx.x, magic);
+                    bq[g ^ 1][j][1] = nibbles_to_bf16(g == 0 ? nx.w : nx.y, magic);
+                    const uint32_t bt = (u == 0) ? (g == 0 ? br[B][j].x : br[B][j].y)
+                                                 : (g == 0 ? br[B][j].z : br[B][j].w);
+                    tp[g][j] = bf16_hi(bt);
+                }
+#pragma unroll
+                for (int k = 0; k < RT * NMT * 2; ++k) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // then up to four VALU
                 }
             }
-            if (U + PF < a.nunits) load_unit<RT>(rs, U + PF, vo_w, vo_s, wq[u], sq[u]);
-        }
-        // the super-unit's bias: one K=32 MFMA per row tile and m tile
+        // the super-unit's bias: one K=32 MFMA per row tile and m tile, into the totals
         bf16x8_t xa[NMT];
 #pragma unroll
-        for (int mt = 0; mt < NMT; ++mt) xa[mt] = __builtin_bit_cast(bf16x8_t, sXA[buf][mt][lane]);
+        for (int mt = 0; mt < NMT; ++mt) xa[mt] = __builtin_bit_cast(bf16x8_t, sXA[P][mt * 64 + lane]);
 #pragma unroll
         for (int j = 0; j < RT; ++j)
 #pragma unroll
             for (int mt = 0; mt < NMT; ++mt)
-                bacc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    xa[mt], __builtin_bit_cast(bf16x8_t, bp[j]), bacc[j][mt], 0, 0, 0);
-        if (more) stage_store(buf ^ 1);
+                tot[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    xa[mt], __builtin_bit_cast(bf16x8_t, br[B][j]), tot[j][mt], 0, 0, 0);
+        stage_store(P ^ 1);
+    };
+    uint32_t S = 0;
+    for (; S + 2 < nstages; S += 3) {
+        stage(S, std::integral_constant<int, 0>{});
+        stage(S + 1, std::integral_constant<int, 1>{});
+        stage(S + 2, std::integral_constant<int, 2>{});
     }
+    if (S < nstages) stage(S, std::integral_constant<int, 0>{});
+    if (S + 1 < nstages) stage(S + 1, std::integral_constant<int, 1>{});
+    // the last step (always a second group) still owes its scales
 #pragma unroll
     for (int j = 0; j < RT; ++j)
 #pragma unroll
-        for (int mt = 0; mt < NMT; ++mt) tot[j][mt] += bacc[j][mt];
+        for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+            for (int i = 0; i < NI; ++i) tot[j][mt][i] = fmaf(tp[1][j], acc[1][j][mt][i], tot[j][mt][i]);
+    __syncthreads();  // no wave is still reading sA when the epilogue reuses LDS
     head_epilogue<NMT, NI, RT, MODE>(a, tot, tile0, se);
 }
 
@@ -696,6 +732,7 @@ uint32_t blocks_for(uint32_t ntiles, int rt) {
 }
 
 uint32_t super_units(uint32_t nunits) { return (nunits + 1) / 2; }
+uint32_t padded_units(uint32_t nunits) { return nunits + (nunits & 1); }
 
 int check_geometry(uint32_t vocab, uint32_t d, uint32_t group) {
     if (group != kGroup) return fail(TWD_E_UNSUPPORTED, "group_size must be 64");
@@ -744,8 +781,9 @@ int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
     // gbest: per-row maxima, the arrival counter, and the repack's bad-scale flag
     if (e == hipSuccess) e = hipMalloc(&h->gbest, sizeof(uint64_t) * (TWD_MAX_ROWS + 2));
     if (e == hipSuccess) e = hipMemset(h->gbest, 0, sizeof(uint64_t) * (TWD_MAX_ROWS + 2));
-    if (e == hipSuccess) e = hipMalloc(&h->hp, sizeof(u32x4_t) * (h->nunits + 1) * 4 * 4 * 64);
-    if (e == hipSuccess) e = hipMalloc(&h->hx, sizeof(u32x4_t) * super_units(h->nunits) * 4 * 64);
+    // hp / hx: one stage past the end (the stage loop requests the next stage unconditionally)
+    if (e == hipSuccess) e = hipMalloc(&h->hp, sizeof(u32x4_t) * (h->nunits + 3) * 4 * 4 * 64);
+    if (e == hipSuccess) e = hipMalloc(&h->hx, sizeof(u32x4_t) * (super_units(h->nunits) + 1) * 4 * 64);
     if (e != hipSuccess) {
         twd_head_destroy(h);
         return hip_fail(e, "allocating the LM head");
@@ -804,11 +842,13 @@ int launch_head(twd_head* h, const uint16_t* hidden, uint32_t rows, float* logit
         head_small_kernel<4, kRTS4, kPFS4, MODE><<<blocks_for(h->ntiles, kRTS4), kHeadThreads,
                                                    small_smem_bytes(rows, h->d), stream>>>(a);
     } else if (rows <= 16) {
-        prep_hidden_kernel<1><<<h->nunits * 1, kHeadThreads, 0, stream>>>(hidden, rows, h->d, h->hp, h->hx);
+        prep_hidden_kernel<1><<<padded_units(h->nunits) * 1, kHeadThreads, 0, stream>>>(hidden, rows, h->d,
+                                                                                       h->hp, h->hx);
         head_wide_kernel<1, 4, kRT1, MODE>
             <<<blocks_for(h->ntiles, kRT1), kHeadThreads, 0, stream>>>(a, h->hp, h->hx);
     } else {
-        prep_hidden_kernel<4><<<h->nunits * 4, kHeadThreads, 0, stream>>>(hidden, rows, h->d, h->hp, h->hx);
+        prep_hidden_kernel<4><<<padded_units(h->nunits) * 4, kHeadThreads, 0, stream>>>(hidden, rows, h->d,
+                                                                                       h->hp, h->hx);
         head_wide_kernel<4, 4, kRT4, MODE>
             <<<blocks_for(h->ntiles, kRT4), kHeadThreads, 0, stream>>>(a, h->hp, h->hx);
     }
