@@ -66,8 +66,9 @@ def test_layout_single_unit(torch_dev, oracle):
     assert np.allclose(lg, want, rtol=1e-5, atol=1e-4)
 
 
-@pytest.mark.parametrize("M", [1, 2, 4, 5, 16, 17, 33, 64])
+@pytest.mark.parametrize("M", [1, 2, 4, 5, 6, 7, 8, 9, 16, 17, 33, 64])
 def test_logits_parity(torch_dev, oracle, M):
+    # M = 2..6 and M = 7, 8 run the resident-h kernel with 8 and 16 waves per block at d = 5376
     V = 1000  # not a multiple of 16: the last row tile is partial
     W, S, B = oracle.gen_lm_head(100 + M, V, D)
     head = make_head(torch_dev, W, S, B, V, D, CAP)
@@ -232,7 +233,7 @@ def _check_full_rows(oracle, head_logits, hb, sample_rows):
         assert ratio <= 1.0, (m, ratio, err)
 
 
-@pytest.mark.parametrize("M", [1, 5, 64])
+@pytest.mark.parametrize("M", [1, 5, 8, 64])
 def test_full_geometry_greedy(torch_dev, full_head, oracle, M):
     # configs 2 (M=1), 4 (M=5) and 5 (M=64): softcap 30, greedy argmax per row
     torch, dev = torch_dev
@@ -269,3 +270,32 @@ def test_full_geometry_verify_config4(torch_dev, full_head, oracle):
         got = twd().decode_verify(res)
         want = oracle.verify(drafts, list(logits.cpu().numpy()), base_seed=0)
         assert got["tokens"] == want["tokens"] and got["num_accepted"] == want["num_accepted"]
+
+
+@pytest.mark.parametrize("what", ["scale_above_2^100", "scale_inf", "bias_inf", "bias_-inf"])
+def test_create_rejects_unrepresentable_parameters(torch_dev, oracle, what):
+    # t = -128 s must be finite, and a bias must be finite: the kernels multiply both by bf16
+    # slices and by padding entries that can be exactly zero (inf * 0 would turn into NaN)
+    V, d = 40, 256
+    W, S, B = oracle.gen_lm_head(7, V, d)
+    S, B = S.copy(), B.copy()
+    bad = {"scale_above_2^100": 0x7200,  # 2^101 in bf16
+           "scale_inf": 0x7F80, "bias_inf": 0x7F80, "bias_-inf": 0xFF80}[what]
+    (S if what.startswith("scale") else B)[33, 2] = bad
+    with pytest.raises(twd().TwdError) as e:
+        make_head(torch_dev, W, S, B, V, d, CAP)
+    assert e.value.code == twd().TWD_E_UNSUPPORTED
+
+
+def test_create_accepts_scale_at_2_100(torch_dev, oracle):
+    V, d = 40, 256
+    W, S, B = oracle.gen_lm_head(8, V, d)
+    S = S.copy()
+    S[5, 1] = 0x7180  # 2^100, the largest accepted magnitude: t = -2^107 is finite
+    head = make_head(torch_dev, W, S, B, V, d, 0.0)
+    hb = hidden_bf16(9, 1, d)
+    got = head.logits(to_dev_bf16(torch_dev, hb)).cpu().numpy()
+    want = oracle_rows(oracle, W, S, B, hb, 0.0)
+    assert np.isfinite(got).all()
+    ratio, err, _ = allclose_report(got, want, 1e-3, 1e-3)
+    assert ratio <= 1.0, (ratio, err)

@@ -162,12 +162,14 @@ __device__ __forceinline__ void bias_slices(float x, At at) {
 }
 
 // Shared memory of the head epilogue (cross-wave greedy reduction).
-struct EpiShared {
-    uint64_t red[kHeadWaves][TWD_MAX_ROWS];
+template <int NW>
+struct EpiSharedT {
+    uint64_t red[NW][TWD_MAX_ROWS];
     uint64_t seen[TWD_MAX_ROWS];
     uint32_t tok[TWD_MAX_ROWS];
     int last;
 };
+using EpiShared = EpiSharedT<kHeadWaves>;
 
 // Softcap, logits store, and -- for the greedy modes -- the per-row rank maximum over the
 // whole grid, finished by the last block to arrive (tokens, then greedy verify bookkeeping).
@@ -180,9 +182,9 @@ struct EpiShared {
 // stores, so no device-scope fence is needed: on this part such a fence writes back the XCD's
 // L2 and, paid by each of ~1000 blocks, costs more than the streaming pass itself.
 // tot[j][mt][i] holds row r = (tile0 + j) * 16 + lane % 16 of m = 16 mt + 4 (lane / 16) + i.
-template <int NMT, int NI, int RT, int MODE>
+template <int NMT, int NI, int RT, int MODE, int NW>
 __device__ __forceinline__ void head_epilogue(const HeadArgs& a, f32x4_t (&tot)[RT][NMT],
-                                              uint32_t tile0, EpiShared& se) {
+                                              uint32_t tile0, EpiSharedT<NW>& se) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     uint64_t best[NMT][NI];
 #pragma unroll
@@ -229,7 +231,7 @@ __device__ __forceinline__ void head_epilogue(const HeadArgs& a, f32x4_t (&tot)[
     if (static_cast<uint32_t>(tid) < a.M) {
         uint64_t k = se.red[0][tid];
 #pragma unroll
-        for (int w = 1; w < kHeadWaves; ++w) k = se.red[w][tid] > k ? se.red[w][tid] : k;
+        for (int w = 1; w < NW; ++w) k = se.red[w][tid] > k ? se.red[w][tid] : k;
         // the returning form: the maximum is performed before this block counts itself in
         se.seen[tid] = __hip_atomic_fetch_max(reinterpret_cast<unsigned long long*>(a.gbest + tid),
                                               static_cast<unsigned long long>(k), __ATOMIC_RELAXED,
@@ -289,6 +291,43 @@ __device__ __forceinline__ void load_unit(const __amdgpu_buffer_rsrc_t (&rs)[RT]
     }
 }
 
+// The two halves of load_unit, each issued in a fixed order and fenced from the surrounding
+// code. A ring whose prologue and loop issue their loads in the same order lets the wait before
+// each slot's first use count only that slot's loads; any other order makes the wait at the
+// loop head cover the worst case of both.
+template <int RT>
+__device__ __forceinline__ void load_nibbles_ordered(const __amdgpu_buffer_rsrc_t (&rs)[RT], uint32_t U,
+                                                     uint32_t vo_w, u32x4_t (&w)[RT]) {
+    const int so = static_cast<int>(U * kUnitBytes);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+        w[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs[j], vo_w, so, kNonTemporal));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+template <int RT>
+__device__ __forceinline__ void load_scales_ordered(const __amdgpu_buffer_rsrc_t (&rs)[RT], uint32_t U,
+                                                    uint32_t vo_s, u32x2_t (&sb)[RT]) {
+    const int so = static_cast<int>(U * kUnitBytes);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+        sb[j] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rs[j], vo_s, so, kNonTemporal));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>), in order.
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<N, I + 1>(f);
+    }
+}
+
 // Wave index as a scalar: keeps tile and address arithmetic on the scalar unit.
 __device__ __forceinline__ uint32_t wave_id() {
     return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -297,51 +336,89 @@ __device__ __forceinline__ uint32_t wave_id() {
 // ---- M <= 8: the whole h resident in LDS, no barrier in the streaming loop ---------------------
 //
 // LDS holds the prepared h in A-fragment order, [m][chunk U][k-step t][kg] of 16 B, and the bias
-// A-fragment entries [super-unit P][slice kg][m] of 16 B. A-fragment rows m >= M only feed output
-// rows that are never stored, so their lanes simply read row 0. Each wave streams its RT row
-// tiles through a PF-deep register ring of weight units, with no synchronisation until the
-// epilogue.
-template <int NI, int RT, int PF, int MODE>
-__global__ __launch_bounds__(kHeadThreads) void head_small_kernel(HeadArgs a) {
+// A-fragment entries [super-unit P][slice kg][m] of 16 B, both over npad = nunits rounded up to
+// the ring depth PF; the chunks past nunits hold zeros, so the streaming loop runs whole ring
+// cycles with no branch: its weight loads are clamped to the last unit, whose contribution the
+// zero h and zero bias entries cancel exactly (the loader rejects infinite biases and scales
+// above 2^100, so every product with those zeros is zero). A-fragment rows m >= M only feed
+// output rows that are never stored, so their lanes simply read row 0. Each wave streams its
+// RT row tiles through the PF-deep register ring with no synchronisation until the epilogue.
+template <int PF>
+__host__ __device__ constexpr uint32_t small_pad_units(uint32_t nunits) {
+    return (nunits + PF - 1) / PF * PF;
+}
+
+template <int NI, int RT, int PF, int NW, int MODE>
+__global__ __launch_bounds__(NW * 64) void head_small_kernel(HeadArgs a) {
     static_assert(PF % 2 == 0, "the ring holds whole super-units");
+    constexpr int NT = NW * 64;
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    __shared__ EpiShared se;
+    __shared__ EpiSharedT<NW> se;
     u32x4_t* sH = reinterpret_cast<u32x4_t*>(smem_raw);
     const uint32_t row_vecs = a.d / 8;  // 16 B vectors per h row
-    u32x4_t* sXF = sH + a.M * row_vecs;  // [super-units][4][M]
+    const uint32_t npad = small_pad_units<PF>(a.nunits);
+    const uint32_t pad_vecs = npad * 16;  // 16 B vectors per padded LDS row
+    u32x4_t* sXF = sH + a.M * pad_vecs;   // [super-units][4][M]
     const int tid = threadIdx.x, lane = tid & 63;
-    const uint32_t tile0 = (blockIdx.x * kHeadWaves + wave_id()) * RT;
+    const uint32_t tile0 = (blockIdx.x * NW + wave_id()) * RT;
     const uint32_t magic = vgpr_const(0x43004300u);
 
-    // ---- stage h: 8 consecutive threads cover one 64-column group ----
-    const uint32_t tasks = a.M * row_vecs;
-    for (uint32_t base = 0; base < tasks; base += kHeadThreads) {
-        const uint32_t task = base + tid;
-        u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
-        if (task < tasks) v = *reinterpret_cast<const u32x4_t*>(a.h + static_cast<size_t>(task) * 8);
-        float s = sum8_bf16(v);
-        s += __shfl_xor(s, 1);
-        s += __shfl_xor(s, 2);
-        s += __shfl_xor(s, 4);
-        if (task < tasks) {
-            const uint32_t m = task / row_vecs, c8 = task % row_vecs;
-            const uint32_t U = c8 >> 4, c = c8 & 15;
-            sH[((m * a.nunits + U) * 4 + (c >> 2)) * 4 + (c & 3)] = prep_h(v);
-            if ((c8 & 7) == 0) {
-                const uint32_t g = c8 >> 3;
-                uint32_t* x = reinterpret_cast<uint32_t*>(sXF);
-                auto at = [&](int kg) { return x + (((g >> 2) * 4 + kg) * a.M + m) * 4 + (g & 3); };
-                bias_slices(s, at);
-                // an odd chunk count leaves groups 2, 3 of the last super-unit empty
-                if ((a.nunits & 1) && U == a.nunits - 1)
-                    bias_slices(0.0f, [&](int kg) { return at(kg) + 2; });
+    __amdgpu_buffer_rsrc_t rs[RT];
+    tile_streams<RT>(a, tile0, rs);
+    const uint32_t vo_w = lane * 16, vo_s = kUnitNibbleBytes + (lane & 15) * 8;
+    const uint32_t last = a.nunits - 1;
+    u32x4_t wq[PF][RT];
+    u32x2_t sq[PF][RT];
+    // The ring is filled before h is staged, so the two memory round trips overlap. Ring order,
+    // the same in the prologue and in every cycle: per super-unit, the even unit's nibbles, then
+    // its {b, t} words, then the odd unit's nibbles and words. The even unit's words are refilled
+    // only after the odd step's bias MFMA has read them, so the bias fragment needs no copy that
+    // outlives the refill.
+#pragma unroll
+    for (int s = 0; s < PF; ++s) {
+        const uint32_t U = min(static_cast<uint32_t>(s), last);
+        load_nibbles_ordered<RT>(rs, U, vo_w, wq[s]);
+        load_scales_ordered<RT>(rs, U, vo_s, sq[s]);
+    }
+
+    // ---- stage h: 8 consecutive threads cover one 64-column group; padding chunks get zeros.
+    // Each thread issues kBatch loads before it waits, so a block pays about one round trip per
+    // kBatch * NT vectors.
+    constexpr int kBatch = 4;
+    const uint32_t tasks = a.M * pad_vecs;
+    for (uint32_t base = 0; base < tasks; base += NT * kBatch) {
+        u32x4_t v[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const uint32_t task = base + b * NT + tid;
+            const uint32_t m = task / pad_vecs, c8 = task % pad_vecs;
+            v[b] = u32x4_t{0u, 0u, 0u, 0u};
+            if (task < tasks && c8 < row_vecs)
+                v[b] = *reinterpret_cast<const u32x4_t*>(a.h + (static_cast<size_t>(m) * row_vecs + c8) * 8);
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const uint32_t task = base + b * NT + tid;
+            const uint32_t m = task / pad_vecs, c8 = task % pad_vecs;
+            float s = sum8_bf16(v[b]);
+            s += __shfl_xor(s, 1);
+            s += __shfl_xor(s, 2);
+            s += __shfl_xor(s, 4);
+            if (task < tasks) {
+                const uint32_t U = c8 >> 4, c = c8 & 15;
+                sH[((m * npad + U) * 4 + (c >> 2)) * 4 + (c & 3)] = prep_h(v[b]);
+                if ((c8 & 7) == 0) {
+                    const uint32_t g = c8 >> 3;
+                    uint32_t* x = reinterpret_cast<uint32_t*>(sXF);
+                    bias_slices(s, [&](int kg) { return x + (((g >> 2) * 4 + kg) * a.M + m) * 4 + (g & 3); });
+                }
             }
         }
     }
     __syncthreads();
 
     const uint32_t m_lane = (lane & 15) < a.M ? (lane & 15) : 0u;
-    const u32x4_t* aRow = sH + m_lane * row_vecs + (lane >> 4);
+    const u32x4_t* aRow = sH + m_lane * pad_vecs + (lane >> 4);
     const u32x4_t* xRow = sXF + (lane >> 4) * a.M + m_lane;
 
     f32x4_t tot[RT][1], bacc[RT];
@@ -351,68 +428,62 @@ __global__ __launch_bounds__(kHeadThreads) void head_small_kernel(HeadArgs a) {
         bacc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
 
-    __amdgpu_buffer_rsrc_t rs[RT];
-    tile_streams<RT>(a, tile0, rs);
-    const uint32_t vo_w = lane * 16, vo_s = kUnitNibbleBytes + (lane & 15) * 8;
-    u32x4_t wq[PF][RT];
-    u32x2_t sq[PF][RT];
-#pragma unroll
-    for (int s = 0; s < PF; ++s)
-        if (static_cast<uint32_t>(s) < a.nunits) load_unit<RT>(rs, s, vo_w, vo_s, wq[s], sq[s]);
 
-    u32x4_t bp[RT];  // {b, t} words of the super-unit's four groups: the bias B fragment
-    for (uint32_t U0 = 0; U0 < a.nunits; U0 += PF) {
+    // One unit of the ring: slot s holds chunk U0 + s; RELOAD refills the slot PF chunks ahead.
+    auto step = [&](uint32_t U0, auto slot, auto reload) {
+        constexpr int s = decltype(slot)::value;
+        const uint32_t U = U0 + s;
+        bf16x8_t av[4];
 #pragma unroll
-        for (int s = 0; s < PF; ++s) {
-            const uint32_t U = U0 + s;
-            if (U >= a.nunits) break;
-            bf16x8_t av[4];
+        for (int t = 0; t < 4; ++t) av[t] = __builtin_bit_cast(bf16x8_t, aRow[(U * 4 + t) * 4]);
+        f32x4_t acc[RT][2];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) av[t] = __builtin_bit_cast(bf16x8_t, aRow[(U * 4 + t) * 4]);
-            f32x4_t acc[RT][2];
+        for (int j = 0; j < RT; ++j)
 #pragma unroll
-            for (int j = 0; j < RT; ++j)
+            for (int g = 0; g < 2; ++g) {
+                const bf16x8_t b0 = nibbles_to_bf16(wq[s][j][2 * g], magic);
+                const bf16x8_t b1 = nibbles_to_bf16(wq[s][j][2 * g + 1], magic);
+                acc[j][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[2 * g], b0,
+                                                                    f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                acc[j][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[2 * g + 1], b1, acc[j][g], 0, 0, 0);
+            }
 #pragma unroll
-                for (int g = 0; g < 2; ++g) {
-                    const bf16x8_t b0 = nibbles_to_bf16(wq[s][j][2 * g], magic);
-                    const bf16x8_t b1 = nibbles_to_bf16(wq[s][j][2 * g + 1], magic);
-                    acc[j][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[2 * g], b0,
-                                                                        f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    acc[j][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[2 * g + 1], b1, acc[j][g], 0, 0, 0);
-                }
+        for (int j = 0; j < RT; ++j)
 #pragma unroll
-            for (int j = 0; j < RT; ++j)
+            for (int g = 0; g < 2; ++g) {
+                const float t = bf16_hi(g ? sq[s][j].y : sq[s][j].x);
 #pragma unroll
-                for (int g = 0; g < 2; ++g) {
-                    const float t = bf16_hi(g ? sq[s][j].y : sq[s][j].x);
-#pragma unroll
-                    for (int i = 0; i < NI; ++i) tot[j][0][i] = fmaf(t, acc[j][g][i], tot[j][0][i]);
-                }
-            const bool odd = (s & 1) != 0;
+                for (int i = 0; i < NI; ++i) tot[j][0][i] = fmaf(t, acc[j][g][i], tot[j][0][i]);
+            }
+        // the fences in the loads keep each refill inside its step: the scheduler would otherwise
+        // sink every refill of the cycle below the last MFMA, leaving no loads in flight while
+        // the cycle computes
+        constexpr bool kReload = decltype(reload)::value;
+        const uint32_t Un = min(U + PF, last);
+        if constexpr ((s & 1) == 0) {
+            if constexpr (kReload) load_nibbles_ordered<RT>(rs, Un, vo_w, wq[s]);
+        } else {
+            // {b, t} words of the super-unit's four groups: the bias B fragment
+            const bf16x8_t xa = __builtin_bit_cast(bf16x8_t, xRow[(U >> 1) * 4 * a.M]);
 #pragma unroll
             for (int j = 0; j < RT; ++j) {
-                if (odd) {
-                    bp[j].z = sq[s][j].x;
-                    bp[j].w = sq[s][j].y;
-                } else {
-                    bp[j].x = sq[s][j].x;
-                    bp[j].y = sq[s][j].y;
-                }
+                const u32x4_t bp = u32x4_t{sq[s - 1][j].x, sq[s - 1][j].y, sq[s][j].x, sq[s][j].y};
+                bacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, __builtin_bit_cast(bf16x8_t, bp),
+                                                                  bacc[j], 0, 0, 0);
             }
-            if (odd || U + 1 == a.nunits) {
-                if (!odd) {
-#pragma unroll
-                    for (int j = 0; j < RT; ++j) bp[j].z = bp[j].w = 0u;  // no second unit
-                }
-                const bf16x8_t xa = __builtin_bit_cast(bf16x8_t, xRow[(U >> 1) * 4 * a.M]);
-#pragma unroll
-                for (int j = 0; j < RT; ++j)
-                    bacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        xa, __builtin_bit_cast(bf16x8_t, bp[j]), bacc[j], 0, 0, 0);
+            if constexpr (kReload) {
+                load_scales_ordered<RT>(rs, min(U - 1 + PF, last), vo_s, sq[s - 1]);
+                load_nibbles_ordered<RT>(rs, Un, vo_w, wq[s]);
+                load_scales_ordered<RT>(rs, Un, vo_s, sq[s]);
             }
-            if (U + PF < a.nunits) load_unit<RT>(rs, U + PF, vo_w, vo_s, wq[s], sq[s]);
         }
-    }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto cycle = [&](uint32_t U0, auto reload) {
+        static_for<PF>([&](auto slot) { step(U0, slot, reload); });
+    };
+    for (uint32_t U0 = 0; U0 + PF < npad; U0 += PF) cycle(U0, std::true_type{});
+    cycle(npad - PF, std::false_type{});
 #pragma unroll
     for (int j = 0; j < RT; ++j) tot[j][0] += bacc[j];
     head_epilogue<1, NI, RT, MODE>(a, tot, tile0, se);
@@ -631,7 +702,9 @@ void head_wide_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_t*
 }
 
 // ---- layout repack: reference [W|S|B] -> units ----------------------------------------------
-// Sets *bad when a scale's magnitude exceeds kMaxScale (t = -128 s would not be finite).
+// Sets *bad when a scale's magnitude exceeds kMaxScale (t = -128 s would not be finite) or a bias
+// is infinite: the kernels multiply every bias and t by bf16 slices and padding entries that can
+// be exactly zero, which would turn such a term into NaN where the reference's sum is infinite.
 __global__ void repack_kernel(const uint32_t* __restrict__ W, const uint16_t* __restrict__ S,
                               const uint16_t* __restrict__ B, uint32_t vocab, uint32_t d,
                               uint32_t ntiles, uint32_t nunits, uint8_t* __restrict__ out,
@@ -661,7 +734,9 @@ __global__ void repack_kernel(const uint32_t* __restrict__ W, const uint16_t* __
 #pragma unroll
                 for (int k = 0; k < 2; ++k) {
                     const float s = __uint_as_float(static_cast<uint32_t>(sr[k]) << 16);
-                    if (fabsf(s) > kMaxScale) __hip_atomic_fetch_or(bad, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    const float b = __uint_as_float(static_cast<uint32_t>(br[k]) << 16);
+                    if (fabsf(s) > kMaxScale || __builtin_isinf(b))
+                        __hip_atomic_fetch_or(bad, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     word[k] = static_cast<uint32_t>(br[k]) | (f32_to_bf16_rne(-128.0f * s) << 16);
                 }
                 sb = u32x2_t{word[0], word[1]};
@@ -720,14 +795,19 @@ namespace {
 // staged-h kernel: row tiles per wave (measured on MI355X: M = 16 -> 4, M = 64 -> 2)
 constexpr int kRT1 = 4;  // M <= 16
 constexpr int kRT4 = 2;  // M <= 64
-// resident-h kernel: row tiles per wave and weight units in flight (measured best on MI355X:
-// M = 1 -> 2 tiles x 4 units; M = 5 -> 4 tiles x 2 units)
-constexpr int kRTS1 = 2, kPFS1 = 4;  // M == 1
-constexpr int kRTS4 = 4, kPFS4 = 2;  // 2 <= M <= 8
+// resident-h kernel: row tiles per wave, weight units in flight and waves per block, measured
+// best on MI355X at V = 262144, d = 5376. Each choice leaves 16 waves resident per CU and the
+// grid an exact number of rounds of resident blocks on 256 CUs. M = 1: 512 blocks of 8 waves.
+// 2 <= M <= 8: 8 waves per block while two blocks' h fit in LDS, else 16 waves per block, one
+// block per CU; one LDS copy of h then serves 16 waves.
+constexpr int kRTS1 = 4, kPFS1 = 2, kNWS1 = 8;  // M == 1
+constexpr int kRTS4 = 2, kPFS4 = 4;            // 2 <= M <= 8
+constexpr int kNWS4 = 8, kNWS8 = 16;
+constexpr size_t kLdsBytes = 160 * 1024;
 constexpr uint32_t kSmallMaxRows = 8;
 
-uint32_t blocks_for(uint32_t ntiles, int rt) {
-    const uint32_t per = kHeadWaves * rt;
+uint32_t blocks_for(uint32_t ntiles, int rt, int nw = kHeadWaves) {
+    const uint32_t per = nw * rt;
     return (ntiles + per - 1) / per;
 }
 
@@ -743,10 +823,12 @@ int check_geometry(uint32_t vocab, uint32_t d, uint32_t group) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Dynamic LDS of the resident-h kernel: prepared h (M x d bf16) + bias entries [groups4][M].
+// Dynamic LDS of the resident-h kernel with ring depth PF: prepared h (M rows of npad chunks of
+// 256 B) + bias entries (npad / 2 super-units x 4 slices x M of 16 B).
+template <int PF>
 size_t small_smem_bytes(uint32_t rows, uint32_t d) {
-    const size_t groups4 = ((d / kGroup) + 3) & ~size_t{3};
-    return static_cast<size_t>(rows) * d * 2 + groups4 * rows * 16;
+    const size_t npad = small_pad_units<PF>(d / kChunkK);
+    return static_cast<size_t>(rows) * npad * (256 + 32);
 }
 
 template <typename K>
@@ -757,14 +839,17 @@ hipError_t allow_smem(K kernel, size_t bytes) {
 
 // Lets every resident-h instantiation use the LDS it needs for kSmallMaxRows rows of d.
 int enable_small_kernels(uint32_t d) {
-    const size_t bytes = small_smem_bytes(kSmallMaxRows, d);
-    if (bytes > 160 * 1024 - sizeof(EpiShared))
+    const size_t bytes1 = small_smem_bytes<kPFS1>(1, d);
+    const size_t bytes4 = small_smem_bytes<kPFS4>(kSmallMaxRows, d);
+    if (bytes1 + sizeof(EpiSharedT<kNWS1>) > kLdsBytes || bytes4 + sizeof(EpiSharedT<kNWS8>) > kLdsBytes)
         return fail(TWD_E_UNSUPPORTED, "d_model too large for the LDS-resident head");
     hipError_t e = hipSuccess;
-    if (e == hipSuccess) e = allow_smem(head_small_kernel<1, kRTS1, kPFS1, kModeLogits>, bytes);
-    if (e == hipSuccess) e = allow_smem(head_small_kernel<1, kRTS1, kPFS1, kModeGreedy>, bytes);
-    if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS4, kPFS4, kModeLogits>, bytes);
-    if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS4, kPFS4, kModeGreedy>, bytes);
+    if (e == hipSuccess) e = allow_smem(head_small_kernel<1, kRTS1, kPFS1, kNWS1, kModeLogits>, bytes1);
+    if (e == hipSuccess) e = allow_smem(head_small_kernel<1, kRTS1, kPFS1, kNWS1, kModeGreedy>, bytes1);
+    if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS4, kPFS4, kNWS4, kModeLogits>, bytes4);
+    if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS4, kPFS4, kNWS4, kModeGreedy>, bytes4);
+    if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS4, kPFS4, kNWS8, kModeLogits>, bytes4);
+    if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS4, kPFS4, kNWS8, kModeGreedy>, bytes4);
     if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
     return TWD_OK;
 }
@@ -836,11 +921,16 @@ int launch_head(twd_head* h, const uint16_t* hidden, uint32_t rows, float* logit
     a.n_drafts = n_drafts;
     a.vres = vres;
     if (rows == 1) {
-        head_small_kernel<1, kRTS1, kPFS1, MODE><<<blocks_for(h->ntiles, kRTS1), kHeadThreads,
-                                                   small_smem_bytes(rows, h->d), stream>>>(a);
+        head_small_kernel<1, kRTS1, kPFS1, kNWS1, MODE><<<blocks_for(h->ntiles, kRTS1, kNWS1), kNWS1 * 64,
+                                                   small_smem_bytes<kPFS1>(rows, h->d), stream>>>(a);
     } else if (rows <= kSmallMaxRows) {
-        head_small_kernel<4, kRTS4, kPFS4, MODE><<<blocks_for(h->ntiles, kRTS4), kHeadThreads,
-                                                   small_smem_bytes(rows, h->d), stream>>>(a);
+        const size_t bytes = small_smem_bytes<kPFS4>(rows, h->d);
+        if (2 * (bytes + sizeof(EpiSharedT<kNWS4>)) <= kLdsBytes)
+            head_small_kernel<4, kRTS4, kPFS4, kNWS4, MODE>
+                <<<blocks_for(h->ntiles, kRTS4, kNWS4), kNWS4 * 64, bytes, stream>>>(a);
+        else
+            head_small_kernel<4, kRTS4, kPFS4, kNWS8, MODE>
+                <<<blocks_for(h->ntiles, kRTS4, kNWS8), kNWS8 * 64, bytes, stream>>>(a);
     } else if (rows <= 16) {
         prep_hidden_kernel<1><<<padded_units(h->nunits) * 1, kHeadThreads, 0, stream>>>(hidden, rows, h->d,
                                                                                        h->hp, h->hx);
@@ -892,7 +982,7 @@ TWD_API int twd_head_create_device(const void* wsb_dev, uint64_t wsb_bytes, uint
     }
     if (bad) {
         twd_head_destroy(h);
-        return fail(TWD_E_UNSUPPORTED, "a group scale exceeds 2^100 in magnitude");
+        return fail(TWD_E_UNSUPPORTED, "a group scale exceeds 2^100 in magnitude or a group bias is infinite");
     }
     *out = h;
     return TWD_OK;
