@@ -50,17 +50,25 @@ def hidden_pool(torch, dev, n, rows, seed):
     return torch.from_numpy(h.view(np.int16)).to(dev)
 
 
-def time_loop(torch, steps, warmup, step_fn):
-    """Runs `warmup` untimed steps, then `steps` timed ones bracketed by synchronize + HIP events
-    on the current stream (the stream every launch below uses). Returns seconds on the GPU
-    clock between the two events."""
-    for i in range(warmup):
-        step_fn(i)
-    torch.cuda.synchronize()
+def time_loop(torch, steps, warmup, step_fn, min_warm_s=0.1):
+    """Runs `warmup` untimed steps (more, in chunks, until at least `min_warm_s` of warmup has
+    passed: after the host-side set-up between configs the first few milliseconds of launches
+    run measurably slower), then `steps` timed ones bracketed by synchronize + HIP events on the
+    current stream (the stream every launch below uses). Returns seconds on the GPU clock
+    between the two events."""
+    t0 = time.perf_counter()
+    i = 0
+    while True:
+        for _ in range(max(warmup, 1)):
+            step_fn(i)
+            i += 1
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= min_warm_s:
+            break
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for i in range(steps):
-        step_fn(warmup + i)
+    for k in range(steps):
+        step_fn(i + k)
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / 1e3
