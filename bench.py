@@ -77,7 +77,7 @@ def time_loop(torch, steps, warmup, step_fn, min_warm_s=0.1):
 def cpu_baseline(wsb_dev, hidden_rows, n_rows: int):
     """Scalar single-thread LM head + softcap + greedy argmax over `n_rows` full rows (every
     vocabulary row each), the oracle's restatement of cpu_reference.cpp:643-665 and
-    sampling.cpp:126-133, on the same weights and hidden states the GPU uses."""
+    sampling.cpp:97-104, on the same weights and hidden states the GPU uses."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     host = wsb_dev.cpu().numpy()

@@ -18,7 +18,7 @@
  *
  * A selected id of TWD_TOKEN_DEGENERATE (0xFFFFFFFF) in a token output marks a row whose
  * distribution the reference rejects: sample_token throws when sum(exp(l - max)) is not
- * > 0, e.g. NaN logits (src/sampling.cpp:141-147).
+ * > 0, e.g. NaN logits (src/sampling.cpp:112-118).
  */
 #ifndef TWD_HEAD_H
 #define TWD_HEAD_H
@@ -44,9 +44,9 @@ extern "C" {
 
 /* Per-row selection parameters. temperature/top_p/top_k/repetition_penalty have the meaning of
  * g4dense::SamplingParams (include/g4dense/sampling.hpp:9-18). `uniform` is the draw in [0,1):
- * sample_token derives it as next_uniform(seed) (src/sampling.cpp:54-57,190-191); the host
+ * sample_token derives it as next_uniform(seed) (src/sampling.cpp:25-28,161-162); the host
  * supplies it here (twd_uniform_from_seed computes the reference's value). `softcap` is the
- * clamp bound handed to apply_repetition_penalty (src/sampling.cpp:103-119). The history is
+ * clamp bound handed to apply_repetition_penalty (src/sampling.cpp:74-90). The history is
  * history_ids[history_offset .. history_offset + history_len). */
 typedef struct {
     float temperature;
@@ -106,7 +106,7 @@ TWD_API int twd_head_logits(twd_head* head, const uint16_t* hidden_bf16, uint32_
  * on ties, -0 == +0), fused into the head pass. `logits` may be NULL (not materialised).
  * Replaces LMHeadGreedy + ArgmaxReduce (shaders/LMHeadGreedy.hlsl:28-72,
  * ArgmaxReduce.hlsl:21-61) with the softcap the reference's sample_token sees
- * (src/sampling.cpp:126-133). */
+ * (src/sampling.cpp:97-104). */
 TWD_API int twd_head_greedy(twd_head* head, const uint16_t* hidden_bf16, uint32_t rows,
                             float* logits, uint32_t* tokens, void* stream);
 
@@ -120,8 +120,8 @@ TWD_API int twd_head_sample(twd_head* head, const uint16_t* hidden_bf16, uint32_
                             float* logits, uint32_t* tokens, void* stream);
 
 /* Greedy speculative verify over rows = n_drafts + 1 target rows [pending, d1..dK]:
- * SpeculativeCoordinator::evaluate_verification's greedy branch (src/speculator.cpp:95-114,
- * 183-195) fused into the head pass. `drafts` is device memory (n_drafts ids), `result` a
+ * SpeculativeCoordinator::evaluate_verification's greedy branch (src/speculator.cpp:50-69,
+ * 138-150) fused into the head pass. `drafts` is device memory (n_drafts ids), `result` a
  * device twd_verify_result. `logits` may be NULL. */
 TWD_API int twd_head_verify_greedy(twd_head* head, const uint16_t* hidden_bf16, uint32_t rows,
                                    const uint32_t* drafts, uint32_t n_drafts, float* logits,
@@ -133,13 +133,13 @@ TWD_API int twd_selector_create(uint32_t max_vocab, uint32_t max_rows, twd_selec
 TWD_API void twd_selector_destroy(twd_selector* sel);
 
 /* Per row m of `logits` (device, row stride `row_stride` floats): apply_repetition_penalty in
- * place (src/sampling.cpp:103-119), then sample_token (src/sampling.cpp:121-198) with
+ * place (src/sampling.cpp:74-90), then sample_token (src/sampling.cpp:92-169) with
  * params[m].uniform. tokens[m] receives the id (device). */
 TWD_API int twd_select(twd_selector* sel, float* logits, uint32_t vocab, uint32_t rows,
                        uint64_t row_stride, const twd_row_params* params,
                        const uint32_t* history_ids, uint32_t* tokens, void* stream);
 
-/* evaluate_verification without draft logits (src/speculator.cpp:79-198 minus :116-167): row i
+/* evaluate_verification without draft logits (src/speculator.cpp:34-153 minus :71-122): row i
  * is sampled with uniform next_uniform(splitmix64(base_seed + i)) and compared with draft i;
  * the first mismatch emits the target token, a full match adds the bonus row. Greedy params
  * (temperature <= 0) give the greedy branch. `params` applies to every row and its history
@@ -149,12 +149,12 @@ TWD_API int twd_verify(twd_selector* sel, const float* logits, uint32_t vocab, u
                        const uint32_t* drafts, uint32_t n_drafts, twd_verify_result* result,
                        void* stream);
 
-/* ---- the reference's seeding, for callers that keep seeds (src/sampling.cpp:47-101) -------- */
+/* ---- the reference's seeding, for callers that keep seeds (src/sampling.cpp:18-72) -------- */
 TWD_API uint64_t twd_splitmix64(uint64_t x);
 TWD_API uint64_t twd_seed_for(int has_seed, uint64_t seed, int position);
 TWD_API float twd_uniform_from_seed(uint64_t seed);
 /* 0 when validate_sampling accepts the parameters, TWD_E_INVALID (with a message) otherwise
- * (src/sampling.cpp:61-83). */
+ * (src/sampling.cpp:32-54). */
 TWD_API int twd_validate_sampling(float temperature, float top_p, int32_t top_k,
                                   float repetition_penalty);
 

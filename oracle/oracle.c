@@ -30,7 +30,7 @@
 #include <stdlib.h>
 #include <string.h>
 
-/* sampling.cpp:85-90 */
+/* sampling.cpp:56-61 */
 uint64_t or_splitmix64(uint64_t x) {
     x += 0x9E3779B97F4A7C15ULL;
     x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ULL;
@@ -38,7 +38,7 @@ uint64_t or_splitmix64(uint64_t x) {
     return x ^ (x >> 31);
 }
 
-/* sampling.cpp:92-101 */
+/* sampling.cpp:63-72 */
 uint64_t or_seed_for(int has_seed, uint64_t seed, int position) {
     const uint64_t pos = (uint64_t)(int64_t)position;
     const uint64_t base = has_seed ? seed + pos
@@ -47,7 +47,7 @@ uint64_t or_seed_for(int has_seed, uint64_t seed, int position) {
     return s ? s : 0x9E3779B97F4A7C15ULL;
 }
 
-/* xorshift64*, sampling.cpp:47-52 */
+/* xorshift64*, sampling.cpp:18-23 */
 uint64_t or_next_random(uint64_t* state) {
     uint64_t s = *state;
     s ^= s >> 12;
@@ -57,7 +57,7 @@ uint64_t or_next_random(uint64_t* state) {
     return s * 0x2545F4914F6CDD1DULL;
 }
 
-/* sampling.cpp:54-57: the top 24 bits of the draw as an exact fraction of 2^24 */
+/* sampling.cpp:25-28: the top 24 bits of the draw as an exact fraction of 2^24 */
 float or_next_uniform(uint64_t* state) {
     return (float)((or_next_random(state) >> 40) & 0xFFFFFFu) / 16777216.0f;
 }
@@ -67,7 +67,7 @@ float or_uniform_from_seed(uint64_t seed) {
     return or_next_uniform(&s);
 }
 
-/* sampling.cpp:61-83, kMaxTopK = 256 (:44) */
+/* sampling.cpp:32-54, kMaxTopK = 256 (:15) */
 int or_validate_sampling(float t, float p, int k, float rp) {
     if (!isfinite(t) || t < 0.0f) return OR_ERR_INVALID;
     if (!isfinite(p) || p <= 0.0f || p > 1.0f) return OR_ERR_INVALID;
@@ -77,7 +77,7 @@ int or_validate_sampling(float t, float p, int k, float rp) {
     return OR_OK;
 }
 
-/* sampling.cpp:103-119: every occurrence applies the op again, so duplicates compound */
+/* sampling.cpp:74-90: every occurrence applies the op again, so duplicates compound */
 void or_apply_repetition_penalty(float* logits, uint32_t vocab, const uint32_t* history,
                                  size_t n, float penalty, float softcap) {
     if (penalty == 1.0f || n == 0) return;
@@ -96,7 +96,7 @@ void or_apply_repetition_penalty(float* logits, uint32_t vocab, const uint32_t* 
     }
 }
 
-/* sampling.cpp:126-133 */
+/* sampling.cpp:97-104 */
 uint32_t or_argmax(const float* logits, uint32_t vocab) {
     uint32_t best = 0;
     float best_v = logits[0];
@@ -109,7 +109,7 @@ uint32_t or_argmax(const float* logits, uint32_t vocab) {
     return best;
 }
 
-/* The shortlist order of sampling.cpp:157-160: value descending, index ascending; '!=' makes
+/* The shortlist order of sampling.cpp:128-131: value descending, index ascending; '!=' makes
  * -0 and +0 equal so they fall through to the index. */
 static int ranks_before(const float* l, uint32_t a, uint32_t b) {
     if (l[a] != l[b]) return l[a] > l[b];
@@ -124,7 +124,7 @@ static int cmp_rank(const void* pa, const void* pb, void* ctx) {
 }
 
 /* Bounded heap whose root is the worst kept index. Any correct selection under a strict total
- * order yields the same set as std::nth_element (sampling.cpp:161-166). */
+ * order yields the same set as std::nth_element (sampling.cpp:132-137). */
 static void sift_down(const float* l, uint32_t* h, uint32_t n, uint32_t i) {
     for (;;) {
         uint32_t worst = i;
@@ -167,7 +167,7 @@ uint32_t or_shortlist(const float* logits, uint32_t vocab, uint32_t want, uint32
     return n;
 }
 
-/* sampling.cpp:121-198 with the uniform supplied by the caller */
+/* sampling.cpp:92-169 with the uniform supplied by the caller */
 int or_sample_token_u(const float* logits, uint32_t vocab, float temperature, float top_p,
                       int top_k, float u, uint32_t* out, or_sample_diag* diag) {
     if (vocab == 0) return OR_ERR_EMPTY_VOCAB;
@@ -256,8 +256,8 @@ int or_sample_token(const float* logits, uint32_t vocab, float temperature, floa
                              out, diag);
 }
 
-/* speculator.cpp:79-198; the greedy branch (:103-114) and the no-draft-logits branch
- * (:168-178) both call sample_token(row_i, splitmix64(base_seed + i)) and compare. */
+/* speculator.cpp:34-153; the greedy branch (:58-69) and the no-draft-logits branch
+ * (:123-134) both call sample_token(row_i, splitmix64(base_seed + i)) and compare. */
 int or_verify(const uint32_t* drafts, size_t n_drafts, const float* const* rows, size_t n_rows,
               uint32_t vocab, float temperature, float top_p, int top_k, uint64_t base_seed,
               or_verify_result* out) {

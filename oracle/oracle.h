@@ -7,9 +7,9 @@
  * is missing instead of falling back to this code.
  *
  * Reference files restated (paths relative to the reference checkout):
- *   src/sampling.cpp:15-198      seeding, validation, repetition penalty, sample_token
- *   src/speculator.cpp:79-198    evaluate_verification (every branch except the draft-logits
- *                                rejection branch, :116-167)
+ *   src/sampling.cpp:15-169      seeding, validation, repetition penalty, sample_token
+ *   src/speculator.cpp:34-153    evaluate_verification (every branch except the draft-logits
+ *                                rejection branch, :71-122)
  *   src/cpu_reference.cpp:635-665 scalar INT4 g64 LM head + tanh softcap
  *   shaders/Common.hlsli:163-222 weight layout (low nibble first, group = c / 64)
  *
@@ -27,9 +27,9 @@ extern "C" {
 
 enum {
     OR_OK = 0,
-    OR_ERR_EMPTY_VOCAB = 1,   /* sampling.cpp:123 */
-    OR_ERR_DEGENERATE = 2,    /* sampling.cpp:145-147 */
-    OR_ERR_INVALID = 3        /* validate_sampling rejections, sampling.cpp:61-83 */
+    OR_ERR_EMPTY_VOCAB = 1,   /* sampling.cpp:94 */
+    OR_ERR_DEGENERATE = 2,    /* sampling.cpp:116-118 */
+    OR_ERR_INVALID = 3        /* validate_sampling rejections, sampling.cpp:32-54 */
 };
 
 /* Diagnostics of one sampled draw: how far the decisions were from flipping. */
@@ -65,20 +65,20 @@ int or_validate_sampling(float temperature, float top_p, int top_k, float repeti
 void or_apply_repetition_penalty(float* logits, uint32_t vocab, const uint32_t* history,
                                  size_t history_len, float penalty, float softcap);
 
-/* sample_token with the seed path (sampling.cpp:121-198). */
+/* sample_token with the seed path (sampling.cpp:92-169). */
 int or_sample_token(const float* logits, uint32_t vocab, float temperature, float top_p,
                     int top_k, uint64_t seed, uint32_t* out, or_sample_diag* diag);
 /* Same algorithm with the uniform injected directly instead of drawn from the seed. */
 int or_sample_token_u(const float* logits, uint32_t vocab, float temperature, float top_p,
                       int top_k, float u, uint32_t* out, or_sample_diag* diag);
 
-/* Greedy argmax: strict '>' so ties keep the lower index (sampling.cpp:125-133). */
+/* Greedy argmax: strict '>' so ties keep the lower index (sampling.cpp:96-104). */
 uint32_t or_argmax(const float* logits, uint32_t vocab);
 
 /* Sorted shortlist of `want` indices under (value desc, index asc). Returns its length. */
 uint32_t or_shortlist(const float* logits, uint32_t vocab, uint32_t want, uint32_t* idx_out);
 
-/* evaluate_verification without draft logits (speculator.cpp:79-198, the greedy branch and
+/* evaluate_verification without draft logits (speculator.cpp:34-153, the greedy branch and
  * the sample-and-compare branch; both call sample_token identically). */
 int or_verify(const uint32_t* drafts, size_t n_drafts, const float* const* rows, size_t n_rows,
               uint32_t vocab, float temperature, float top_p, int top_k,

@@ -146,7 +146,7 @@ def apply_repetition_penalty(logits, history, penalty: float, softcap: float) ->
 
 def sample_token(logits, t: float, p: float, k: int, seed: int = 0, u: float | None = None,
                  diag: bool = False):
-    """sample_token of sampling.cpp:121-198. With `u` given, the draw uses it directly."""
+    """sample_token of sampling.cpp:92-169. With `u` given, the draw uses it directly."""
     lg = _f32(logits)
     out = C.c_uint32(0)
     dg = SampleDiag()

@@ -38,7 +38,7 @@ def main() -> None:
     R = O.Reference()
     out: dict = {"source": "reference src/sampling.cpp + src/speculator.cpp via oracle/_ref"}
 
-    # ---- seeding (sampling.cpp:85-101) --------------------------------------------------------
+    # ---- seeding (sampling.cpp:56-72) --------------------------------------------------------
     xs = [0, 1, 2, 3, 0x9E3779B97F4A7C15, 0xFFFFFFFFFFFFFFFF, 12345, 1 << 63]
     out["splitmix64"] = [[str(x), str(R.splitmix64(x))] for x in xs]
     seeds = []
@@ -47,7 +47,7 @@ def main() -> None:
             seeds.append([int(has_seed), str(seed), pos, str(R.seed_for(has_seed, seed, pos))])
     out["seed_for"] = seeds
 
-    # ---- validate_sampling (sampling.cpp:61-83) ------------------------------------------------
+    # ---- validate_sampling (sampling.cpp:32-54) ------------------------------------------------
     grid = []
     for t in [0.0, 0.2, -0.1, float("inf"), float("nan"), 1.5]:
         for p in [1.0, 0.95, 0.0, 1.5, float("nan")]:
@@ -56,7 +56,7 @@ def main() -> None:
                     grid.append([t, p, k, rp, R.validate_sampling(t, p, k, rp)])
     out["validate_sampling"] = [[repr(a), repr(b), c, repr(d), e] for a, b, c, d, e in grid]
 
-    # ---- repetition penalty (sampling.cpp:103-119) ----------------------------------------------
+    # ---- repetition penalty (sampling.cpp:74-90) ----------------------------------------------
     pen = []
     rng = np.random.default_rng(7)
     for case, (vocab, nhist, rp, cap, dup) in enumerate([
@@ -124,7 +124,7 @@ def main() -> None:
                    "draws": draws})
     out["penalised_sampling"] = c3
 
-    # ---- greedy speculative verify (speculator.cpp:79-198) ------------------------------------
+    # ---- greedy speculative verify (speculator.cpp:34-153) ------------------------------------
     ver = []
     vrng = np.random.default_rng(44)
     vocab = 4096

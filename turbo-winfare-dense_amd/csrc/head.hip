@@ -51,7 +51,7 @@ struct HeadArgs {
     twd_verify_result* vres;
 };
 
-// speculator.cpp:91-114 and :183-195, greedy branch, over per-row target tokens tok[0..rows).
+// speculator.cpp:46-69 and :138-150, greedy branch, over per-row target tokens tok[0..rows).
 __device__ void verify_bookkeeping(const uint32_t* tok, uint32_t rows, const uint32_t* drafts,
                                    uint32_t nd, twd_verify_result* v) {
     uint32_t n = 0, acc = 0, bonus = 0, sampled = 0;

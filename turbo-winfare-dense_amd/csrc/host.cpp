@@ -1,6 +1,6 @@
 // Host side of the C-ABI: thread-local errors (the convention of src/c_api.cpp:82-93) and the
 // reference's seeding and validation, which are parameter logic rather than per-token compute
-// (src/sampling.cpp:44-101).
+// (src/sampling.cpp:15-72).
 #include <hip/hip_runtime.h>
 
 #include <cmath>

@@ -1,5 +1,5 @@
 // Token selection over device logit rows on gfx950: repetition penalty, greedy argmax and the
-// sampled chain of sample_token (src/sampling.cpp:103-198), plus verify bookkeeping.
+// sampled chain of sample_token (src/sampling.cpp:74-169), plus verify bookkeeping.
 //
 // select_slice_kernel covers all rows: grid (parts, rows), each 512-thread block owns an
 // 8192-entry slice of one row, 16 values per thread held in registers. Per block: penalty on
@@ -403,7 +403,7 @@ __device__ __forceinline__ void block_sort_desc(SelCommon& c, uint32_t n) {
     __syncthreads();
 }
 
-// Steps 5-7 of sample_token on the sorted shortlist c.sorted[0..want) (sampling.cpp:168-197).
+// Steps 5-7 of sample_token on the sorted shortlist c.sorted[0..want) (sampling.cpp:139-168).
 __device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, const twd_row_params& p) {
     const int tid = threadIdx.x;
     const double mx = static_cast<double>(c.gmax);
@@ -477,7 +477,7 @@ __device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, 
 }
 
 // After c.top[0..want) holds the row's shortlist and c.gmax/total/flag its statistics:
-// the degenerate check of sampling.cpp:145-147, the shortlist sort, and steps 5-7.
+// the degenerate check of sampling.cpp:116-118, the shortlist sort, and steps 5-7.
 __device__ __forceinline__ void finish_row(SelCommon& c, uint32_t want, const twd_row_params& p,
                            uint32_t* token_out) {
     const int tid = threadIdx.x;
@@ -520,7 +520,7 @@ void select_slice_kernel(SelectArgs args_by_value, SelectBufs b) {
     }
     for (uint32_t i = tid; i < kReps * kBins; i += NT) sh.t.hist[i] = 0;  // for block_top
 
-    // ---- repetition penalty, sampling.cpp:103-119 ----
+    // ---- repetition penalty, sampling.cpp:74-90 ----
     if (p.repetition_penalty != 1.0f && p.history_len > 0) {
 #pragma unroll
         for (int e = 0; e < kSelPerThread; ++e) sh.u.cnt[tid + NT * e] = 0;
@@ -557,7 +557,7 @@ void select_slice_kernel(SelectArgs args_by_value, SelectBufs b) {
     };
     const bool greedy = !(p.temperature > 0.0f);
     if (greedy) {
-        // ---- sampling.cpp:126-133 ----
+        // ---- sampling.cpp:97-104 ----
         uint64_t k = 0;
 #pragma unroll
         for (int e = 0; e < kSelPerThread; ++e) {
@@ -573,7 +573,7 @@ void select_slice_kernel(SelectArgs args_by_value, SelectBufs b) {
         return;
     }
 
-    // ---- sampled: slice statistics, sampling.cpp:138-147 ----
+    // ---- sampled: slice statistics, sampling.cpp:109-118 ----
     // Any NaN makes the row degenerate, so the max only has to be right for NaN-free rows.
     uint32_t nan_seen = 0;
     float mx = -INFINITY, mn = INFINITY;
@@ -600,7 +600,7 @@ void select_slice_kernel(SelectArgs args_by_value, SelectBufs b) {
     // reference's NaN total makes it.
     if (mx == -INFINITY) s = 0.0;
 
-    // ---- shortlist of this slice, sampling.cpp:149-166 ----
+    // ---- shortlist of this slice, sampling.cpp:120-137 ----
     const uint32_t want_row = (p.top_k > 0) ? min(static_cast<uint32_t>(p.top_k), b.vocab)
                                             : min(kMaxWant, b.vocab);
     const uint32_t n_here = hi - lo;

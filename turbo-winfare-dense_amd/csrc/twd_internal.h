@@ -40,7 +40,7 @@ constexpr uint32_t kMaxWant = TWD_MAX_WANT;
 
 // Orderable 32-bit key of a float: larger float -> larger key, -0 folded into +0. NaN maps to 0
 // (below -inf) so it never wins a comparison, except at index 0 where the reference's argmax
-// returns 0 when logits[0] is NaN (every later '>' test against NaN fails, sampling.cpp:126-133).
+// returns 0 when logits[0] is NaN (every later '>' test against NaN fails, sampling.cpp:97-104).
 __device__ __forceinline__ uint32_t float_key(float v) {
     v = v + 0.0f;  // -0 + 0 == +0 under round-to-nearest; +0 and every other value unchanged
     const uint32_t b = __float_as_uint(v);
@@ -52,7 +52,7 @@ __device__ __forceinline__ float key_float(uint32_t k) {
 }
 
 // 64-bit rank: value descending, then index ascending -- the total order of sample_token's
-// shortlist comparator (sampling.cpp:157-160). Distinct indices make every rank distinct.
+// shortlist comparator (sampling.cpp:128-131). Distinct indices make every rank distinct.
 __device__ __forceinline__ uint64_t rank_key(float v, uint32_t idx) {
     uint32_t k = float_key(v);
     if (v != v) k = (idx == 0) ? 0xFFFFFFFFu : 0u;

@@ -233,7 +233,7 @@ def _selector(vocab: int) -> Selector:
 
 
 def apply_repetition_penalty(logits, vocab: int, history, penalty: float, softcap: float):
-    """In place on a float32 device tensor holding one row (sampling.cpp:103-119)."""
+    """In place on a float32 device tensor holding one row (sampling.cpp:74-90)."""
     import torch
     if float(penalty) == 1.0 or history is None or len(history) == 0:
         return logits
@@ -246,7 +246,7 @@ def apply_repetition_penalty(logits, vocab: int, history, penalty: float, softca
 
 
 def sample_token(logits, vocab: int, p: SamplingParams, seed: int) -> int:
-    """sample_token (sampling.cpp:121-198) on a float32 device tensor holding one row."""
+    """sample_token (sampling.cpp:92-169) on a float32 device tensor holding one row."""
     if vocab == 0:
         raise G4DenseFormatError("sample_token: empty vocabulary")
     sel = _selector(vocab)
