@@ -149,10 +149,30 @@ TWD_API int twd_verify(twd_selector* sel, const float* logits, uint32_t vocab, u
                        const uint32_t* drafts, uint32_t n_drafts, twd_verify_result* result,
                        void* stream);
 
+/* evaluate_verification with draft logits, every branch (src/speculator.cpp:34-153). As
+ * twd_verify, plus: `draft_rows` is a host array of n_draft_rows device pointers; a non-NULL
+ * entry i is position i's draft logit row (vocab floats) and selects the rejection-sampling
+ * branch (:71-122) there: fp32 softmaxes of both rows at params->temperature (compute_softmax,
+ * :14-30, its sequential fp32 sums reproduced exactly), the ratio test p/q against u1 and, on
+ * rejection, a draw from (p - q)+ with u2, where (u1, u2) are the first two
+ * uniform_real_distribution<float> draws of mt19937_64(splitmix64(base_seed + i))
+ * (twd_rejection_uniforms). NULL entries, positions >= n_draft_rows and greedy params
+ * (temperature <= 0 and repetition_penalty == 1) sample-and-compare as twd_verify does. The
+ * first call with draft rows allocates 8 * vocab bytes of scratch per such position on the
+ * selector (kept, and grown when a later call needs more). */
+TWD_API int twd_verify_draft(twd_selector* sel, const float* logits, uint32_t vocab, uint32_t rows,
+                             uint64_t row_stride, const float* const* draft_rows,
+                             uint32_t n_draft_rows, const twd_row_params* params,
+                             uint64_t base_seed, const uint32_t* drafts, uint32_t n_drafts,
+                             twd_verify_result* result, void* stream);
+
 /* ---- the reference's seeding, for callers that keep seeds (src/sampling.cpp:18-72) -------- */
 TWD_API uint64_t twd_splitmix64(uint64_t x);
 TWD_API uint64_t twd_seed_for(int has_seed, uint64_t seed, int position);
 TWD_API float twd_uniform_from_seed(uint64_t seed);
+/* The two draws of src/speculator.cpp:87-89,105 for a step seed: the host C++ standard
+ * library's std::uniform_real_distribution<float>(0, 1) over std::mt19937_64(step_seed). */
+TWD_API void twd_rejection_uniforms(uint64_t step_seed, float* u1, float* u2);
 /* 0 when validate_sampling accepts the parameters, TWD_E_INVALID (with a message) otherwise
  * (src/sampling.cpp:32-54). */
 TWD_API int twd_validate_sampling(float temperature, float top_p, int32_t top_k,

@@ -18,6 +18,14 @@
  *                         from the reference build; the u seam equals the seed path for
  *                         seed-derived u
  *   or_verify             the three cases of tests/test_speculative.cpp:48-76; reference build
+ *   or_mt64_*             the standard's known answer ([rand.predef]: the 10000th output of a
+ *                         default-seeded mt19937_64 is 9981545732273789042)
+ *   or_canonical_float,   against libstdc++'s std::uniform_real_distribution<float> over
+ *   or_rejection_uniforms std::mt19937_64 (gen_std.cpp) for 10^4 seeds; closed forms at the
+ *                         extremes (x = 0, x >= 2^64 - 2^39 -> nextafter(1, 0))
+ *   or_softmax,           reference build (oracle/_ref) on random rows, every branch incl.
+ *   or_verify_draft       rejections and forced fallbacks; golden file; identical draft and
+ *                         target rows always accept (r == 1)
  *   or_lm_head(_f64)      numpy float64 dequant + matmul (closed form w = q*s + b)
  *   or_gen_lm_head        numpy restatement of the documented counter formula
  * Parity is unpinned at the libm layer: exp(double) and tanhf are glibc's here, and no
@@ -285,6 +293,185 @@ int or_verify(const uint32_t* drafts, size_t n_drafts, const float* const* rows,
         uint32_t tok = 0;
         const int rc = or_sample_token(rows[k], vocab, temperature, top_p, top_k,
                                        or_splitmix64(base_seed + k), &tok, NULL);
+        if (rc != OR_OK) return rc;
+        out->bonus_token = tok;
+        out->bonus_token_sampled = 1;
+        out->tokens[out->n_tokens++] = tok;
+    }
+    out->num_accepted = (uint32_t)accepted;
+    out->acceptance_rate = out->total_drafted == 0 ? 0.0
+                                                   : (double)out->num_accepted / out->total_drafted;
+    return OR_OK;
+}
+
+/* ---- rejection-sampling verify (speculator.cpp:14-30, :71-122) ------------------------------ */
+
+/* MT19937-64 as the C++ standard defines std::mt19937_64: w=64, n=312, m=156, r=31,
+ * a=0xB5026F5AA96619E9, u=29, d=0x5555555555555555, s=17, b=0x71D67FFFEDA60000, t=37,
+ * c=0xFFF7EEE000000000, l=43, f=6364136223846793005. */
+void or_mt64_seed(or_mt64* g, uint64_t seed) {
+    g->mt[0] = seed;
+    for (int i = 1; i < 312; ++i)
+        g->mt[i] = 6364136223846793005ULL * (g->mt[i - 1] ^ (g->mt[i - 1] >> 62)) + (uint64_t)i;
+    g->idx = 312;
+}
+
+uint64_t or_mt64_next(or_mt64* g) {
+    if (g->idx >= 312) {
+        for (int i = 0; i < 312; ++i) {
+            const uint64_t x = (g->mt[i] & 0xFFFFFFFF80000000ULL) | (g->mt[(i + 1) % 312] & 0x7FFFFFFFULL);
+            uint64_t xa = x >> 1;
+            if (x & 1) xa ^= 0xB5026F5AA96619E9ULL;
+            g->mt[i] = g->mt[(i + 156) % 312] ^ xa;
+        }
+        g->idx = 0;
+    }
+    uint64_t y = g->mt[g->idx++];
+    y ^= (y >> 29) & 0x5555555555555555ULL;
+    y ^= (y << 17) & 0x71D67FFFEDA60000ULL;
+    y ^= (y << 37) & 0xFFF7EEE000000000ULL;
+    y ^= y >> 43;
+    return y;
+}
+
+float or_canonical_float(uint64_t x) {
+    const float sum = (float)x;                  /* _RealType(g() - g.min()) * 1 */
+    float r = sum / 18446744073709551616.0f;     /* / 2^64, exact in float */
+    if (r >= 1.0f) r = nextafterf(1.0f, 0.0f);
+    return 0.0f + r * (1.0f - 0.0f);             /* uniform_real_distribution: a + c (b - a) */
+}
+
+void or_rejection_uniforms(uint64_t step_seed, float* u1, float* u2) {
+    or_mt64 g;
+    or_mt64_seed(&g, step_seed);
+    *u1 = or_canonical_float(or_mt64_next(&g));
+    *u2 = or_canonical_float(or_mt64_next(&g));
+}
+
+/* speculator.cpp:14-30 */
+void or_softmax(float* l, uint32_t n, float temp) {
+    if (temp <= 0.0f) temp = 1.0f;
+    float max_l = -1e9f;
+    for (uint32_t i = 0; i < n; ++i) {
+        l[i] /= temp;
+        if (l[i] > max_l) max_l = l[i];
+    }
+    float sum = 0.0f;
+    for (uint32_t i = 0; i < n; ++i) {
+        l[i] = expf(l[i] - max_l);
+        sum += l[i];
+    }
+    const float inv = 1.0f / (sum > 1e-12f ? sum : 1.0f);
+    for (uint32_t i = 0; i < n; ++i) l[i] *= inv;
+}
+
+static float softmax_sum(const float* l, uint32_t n, float temp) {
+    /* the sum compute_softmax forms, for the diagnostics */
+    if (temp <= 0.0f) temp = 1.0f;
+    float max_l = -1e9f;
+    for (uint32_t i = 0; i < n; ++i) {
+        const float x = l[i] / temp;
+        if (x > max_l) max_l = x;
+    }
+    float sum = 0.0f;
+    for (uint32_t i = 0; i < n; ++i) sum += expf(l[i] / temp - max_l);
+    return sum;
+}
+
+/* speculator.cpp:34-153, all branches */
+int or_verify_draft(const uint32_t* drafts, size_t n_drafts, const float* const* rows,
+                    size_t n_rows, const float* const* draft_rows, size_t n_draft_rows,
+                    uint32_t vocab, float temperature, float top_p, int top_k,
+                    float repetition_penalty, uint64_t base_seed, or_verify_result* out,
+                    or_reject_diag* diag) {
+    memset(out, 0, sizeof(*out));
+    out->total_drafted = (uint32_t)n_drafts;
+    if (n_drafts == 0 || n_rows == 0) return OR_OK;
+    const int greedy = temperature <= 0.0f && repetition_penalty == 1.0f; /* sampling.hpp:17 */
+    const size_t k = n_drafts < n_rows ? n_drafts : n_rows;
+    size_t accepted = 0;
+    float* p = NULL;
+    float* q = NULL;
+    int rc = OR_OK;
+    for (size_t i = 0; i < k; ++i) {
+        const uint32_t draft = drafts[i];
+        const uint64_t step_seed = or_splitmix64(base_seed + i);
+        const int has_draft = !greedy && i < n_draft_rows && draft_rows[i] != NULL;
+        if (!has_draft) {
+            uint32_t tok = 0;
+            rc = or_sample_token(rows[i], vocab, temperature, top_p, top_k, step_seed, &tok, NULL);
+            if (rc != OR_OK) break;
+            if (draft == tok) {
+                out->tokens[out->n_tokens++] = tok;
+                ++accepted;
+                continue;
+            }
+            out->bonus_token = tok;
+            out->bonus_token_sampled = 1;
+            out->tokens[out->n_tokens++] = tok;
+            break;
+        }
+        if (!p) {
+            p = (float*)malloc(sizeof(float) * vocab);
+            q = (float*)malloc(sizeof(float) * vocab);
+        }
+        memcpy(p, rows[i], sizeof(float) * vocab);
+        or_softmax(p, vocab, temperature);
+        memcpy(q, draft_rows[i], sizeof(float) * vocab);
+        or_softmax(q, vocab, temperature);
+        const float p_val = draft < vocab ? p[draft] : 0.0f;
+        const float q_val = draft < vocab ? q[draft] : 0.0f;
+        const float r = (q_val > 1e-12f) ? (p_val / q_val) : 1.0f;
+        float u1, u2;
+        or_rejection_uniforms(step_seed, &u1, &u2);
+        or_reject_diag dg = {r, u1, u2, softmax_sum(rows[i], vocab, temperature),
+                             softmax_sum(draft_rows[i], vocab, temperature), -1.0f, -1.0f, 0, 0};
+        if (u1 <= r) {
+            dg.accepted = 1;
+            if (diag) diag[i] = dg;
+            out->tokens[out->n_tokens++] = draft;
+            ++accepted;
+            continue;
+        }
+        /* rejection: draw from (p - q)+ */
+        float sum_diff = 0.0f;
+        for (uint32_t v = 0; v < vocab; ++v) {
+            const float x = p[v] - q[v];
+            sum_diff += (0.0f < x) ? x : 0.0f;  /* std::max(0.0f, x) */
+        }
+        uint32_t corr = 0;
+        dg.sum_diff = sum_diff;
+        if (sum_diff > 1e-9f) {
+            const float r_val = u2 * sum_diff;
+            dg.r_val = r_val;
+            float acc = 0.0f;
+            for (uint32_t v = 0; v < vocab; ++v) {
+                const float x = p[v] - q[v];
+                acc += (0.0f < x) ? x : 0.0f;
+                if (acc >= r_val) {
+                    corr = v;
+                    break;
+                }
+            }
+            dg.corr = corr;
+        } else {
+            rc = or_sample_token(rows[i], vocab, temperature, top_p, top_k, step_seed, &corr, NULL);
+            dg.corr = 0xFFFFFFFFu;
+            if (rc != OR_OK) break;
+        }
+        if (diag) diag[i] = dg;
+        out->bonus_token = corr;
+        out->bonus_token_sampled = 1;
+        out->tokens[out->n_tokens++] = corr;
+        break;
+    }
+    free(p);
+    free(q);
+    if (rc != OR_OK) return rc;
+    if (accepted == k && n_rows > k) {
+        uint32_t tok = 0;
+        rc = or_sample_token(rows[k], vocab, temperature, top_p, top_k, or_splitmix64(base_seed + k),
+                             &tok, NULL);
         if (rc != OR_OK) return rc;
         out->bonus_token = tok;
         out->bonus_token_sampled = 1;

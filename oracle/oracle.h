@@ -8,8 +8,7 @@
  *
  * Reference files restated (paths relative to the reference checkout):
  *   src/sampling.cpp:15-169      seeding, validation, repetition penalty, sample_token
- *   src/speculator.cpp:34-153    evaluate_verification (every branch except the draft-logits
- *                                rejection branch, :71-122)
+ *   src/speculator.cpp:14-153    compute_softmax and evaluate_verification, every branch
  *   src/cpu_reference.cpp:635-665 scalar INT4 g64 LM head + tanh softcap
  *   shaders/Common.hlsli:163-222 weight layout (low nibble first, group = c / 64)
  *
@@ -84,6 +83,52 @@ int or_verify(const uint32_t* drafts, size_t n_drafts, const float* const* rows,
               uint32_t vocab, float temperature, float top_p, int top_k,
               uint64_t base_seed, or_verify_result* out);
 
+/* ---- the draft-logits (rejection sampling) branch of evaluate_verification ---------------- */
+
+/* std::mt19937_64 (the C++ standard's definition, [rand.predef]: Matsumoto-Nishimura MT19937-64
+ * parameters, default seed 5489). */
+typedef struct {
+    uint64_t mt[312];
+    int idx;
+} or_mt64;
+void or_mt64_seed(or_mt64* g, uint64_t seed);
+uint64_t or_mt64_next(or_mt64* g);
+
+/* libstdc++'s std::uniform_real_distribution<float>(0, 1) over a 64-bit engine: one engine call,
+ * generate_canonical<float, 24>: float(x) / 2^64 in float, values that round to 1 replaced by
+ * nextafter(1, 0); then 0 + 1 * c. */
+float or_canonical_float(uint64_t x);
+/* The two draws of speculator.cpp:87-89,105: rng = mt19937_64(step_seed); u1 = udist(rng) for the
+ * ratio test, u2 = udist(rng) for the residual draw. */
+void or_rejection_uniforms(uint64_t step_seed, float* u1, float* u2);
+
+/* compute_softmax of speculator.cpp:14-30, in place: divide by temp (1 when temp <= 0), max from
+ * -1e9f with '>', expf(l - max) summed in index order in float, times 1/sum (sum > 1e-12f, else
+ * 1). */
+void or_softmax(float* logits, uint32_t n, float temp);
+
+/* Per-position diagnostics of the rejection branch. */
+typedef struct {
+    float r;            /* p_val / q_val (1 when q_val <= 1e-12f) */
+    float u1;           /* ratio-test draw */
+    float u2;           /* residual draw */
+    float sum_p, sum_q; /* compute_softmax sums */
+    float sum_diff;     /* sum of (p - q)+, or -1 when accepted */
+    float r_val;        /* u2 * sum_diff, or -1 */
+    uint32_t corr;      /* residual token, or 0xFFFFFFFF when the fallback sample_token ran */
+    int accepted;
+} or_reject_diag;
+
+/* evaluate_verification, every branch (speculator.cpp:34-153). draft_rows[i] (i < n_draft_rows)
+ * holds position i's draft logits, or NULL for "no draft probabilities" (an empty vector in the
+ * reference); positions >= n_draft_rows have none. diag (optional) receives one entry per
+ * position that ran the rejection branch, indexed by position. */
+int or_verify_draft(const uint32_t* drafts, size_t n_drafts, const float* const* rows,
+                    size_t n_rows, const float* const* draft_rows, size_t n_draft_rows,
+                    uint32_t vocab, float temperature, float top_p, int top_k,
+                    float repetition_penalty, uint64_t base_seed, or_verify_result* out,
+                    or_reject_diag* diag);
+
 /* Scalar INT4 g64 LM head (cpu_reference.cpp:643-665): fp32 sequential dot over c, then
  * softcap*tanhf(sum/softcap) when softcap > 0. W is [V][d/8] u32, S/B are [V][d/G] bf16 bits,
  * hidden is fp32 [d]. Computes rows [row0, row0+nrows). */
@@ -109,6 +154,10 @@ void or_gen_lm_head(uint64_t seed, uint32_t d, uint32_t group, uint32_t row0, ui
  * std::normal_distribution<float>(mean, sd) (tests/test_sampling.cpp:177-180,238-242).
  * Implemented in gen_std.cpp against libstdc++. */
 void or_gen_mt19937_normal(uint32_t seed, float mean, float sd, size_t n, float* out);
+/* libstdc++'s std::uniform_real_distribution<float>(0, 1) over std::mt19937_64(seeds[i]), two
+ * draws per seed; and the 10000th output of a default-seeded std::mt19937_64. gen_std.cpp. */
+void or_std_rejection_uniforms(const uint64_t* seeds, size_t n, float* out);
+uint64_t or_std_mt64_10000th(void);
 
 #ifdef __cplusplus
 }

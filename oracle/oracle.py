@@ -48,6 +48,20 @@ class VerifyResult(C.Structure):
     ]
 
 
+class RejectDiag(C.Structure):
+    _fields_ = [
+        ("r", C.c_float),
+        ("u1", C.c_float),
+        ("u2", C.c_float),
+        ("sum_p", C.c_float),
+        ("sum_q", C.c_float),
+        ("sum_diff", C.c_float),
+        ("r_val", C.c_float),
+        ("corr", C.c_uint32),
+        ("accepted", C.c_int),
+    ]
+
+
 def build(ref: bool = True) -> None:
     """Compiles liboracle.so, and _ref/libref.so when the reference checkout is present."""
     subprocess.run(["make", "-s", "-C", HERE, "liboracle.so"], check=True)
@@ -97,6 +111,25 @@ def _load():
                                    _u32p, _u16p, _u16p]
     lib.or_gen_mt19937_normal.restype = None
     lib.or_gen_mt19937_normal.argtypes = [C.c_uint32, C.c_float, C.c_float, C.c_size_t, _f32p]
+    lib.or_mt64_seed.restype = None
+    lib.or_mt64_seed.argtypes = [C.c_void_p, C.c_uint64]
+    lib.or_mt64_next.restype = C.c_uint64
+    lib.or_mt64_next.argtypes = [C.c_void_p]
+    lib.or_canonical_float.restype = C.c_float
+    lib.or_canonical_float.argtypes = [C.c_uint64]
+    lib.or_rejection_uniforms.restype = None
+    lib.or_rejection_uniforms.argtypes = [C.c_uint64, C.POINTER(C.c_float), C.POINTER(C.c_float)]
+    lib.or_softmax.restype = None
+    lib.or_softmax.argtypes = [_f32p, C.c_uint32, C.c_float]
+    lib.or_verify_draft.restype = C.c_int
+    lib.or_verify_draft.argtypes = [_u32p, C.c_size_t, C.POINTER(C.c_void_p), C.c_size_t,
+                                    C.POINTER(C.c_void_p), C.c_size_t, C.c_uint32, C.c_float,
+                                    C.c_float, C.c_int, C.c_float, C.c_uint64,
+                                    C.POINTER(VerifyResult), C.POINTER(RejectDiag)]
+    lib.or_std_rejection_uniforms.restype = None
+    lib.or_std_rejection_uniforms.argtypes = [C.POINTER(C.c_uint64), C.c_size_t, _f32p]
+    lib.or_std_mt64_10000th.restype = C.c_uint64
+    lib.or_std_mt64_10000th.argtypes = []
     return lib
 
 
@@ -194,6 +227,74 @@ def verify(drafts, rows, t=0.0, p=1.0, k=0, base_seed=0) -> dict:
     }
 
 
+# ---- rejection-sampling verify (speculator.cpp:14-30, :71-122) -------------------------------
+
+class MT64(C.Structure):
+    _fields_ = [("mt", C.c_uint64 * 312), ("idx", C.c_int)]
+
+
+def mt64_outputs(seed: int, n: int) -> list:
+    g = MT64()
+    lib().or_mt64_seed(C.byref(g), seed & 0xFFFFFFFFFFFFFFFF)
+    return [int(lib().or_mt64_next(C.byref(g))) for _ in range(n)]
+
+
+def canonical_float(x: int) -> float:
+    return float(lib().or_canonical_float(x & 0xFFFFFFFFFFFFFFFF))
+
+
+def rejection_uniforms(step_seed: int):
+    u1, u2 = C.c_float(), C.c_float()
+    lib().or_rejection_uniforms(step_seed & 0xFFFFFFFFFFFFFFFF, C.byref(u1), C.byref(u2))
+    return float(u1.value), float(u2.value)
+
+
+def std_rejection_uniforms(seeds) -> np.ndarray:
+    """libstdc++'s own two draws per seed (gen_std.cpp): [n, 2] float32."""
+    sd = (C.c_uint64 * len(seeds))(*[int(x) & 0xFFFFFFFFFFFFFFFF for x in seeds])
+    out = np.zeros(2 * len(seeds), np.float32)
+    lib().or_std_rejection_uniforms(sd, len(seeds), out)
+    return out.reshape(-1, 2)
+
+
+def std_mt64_10000th() -> int:
+    return int(lib().or_std_mt64_10000th())
+
+
+def softmax(logits, temp: float) -> np.ndarray:
+    out = _f32(logits).copy()
+    lib().or_softmax(out, out.size, temp)
+    return out
+
+
+def verify_draft(drafts, rows, draft_rows, t=0.8, p=1.0, k=0, rp=1.0, base_seed=0) -> dict:
+    """evaluate_verification with draft logits; draft_rows entries may be None."""
+    d = _u32(drafts) if len(drafts) else np.zeros(1, np.uint32)
+    rows = [_f32(r) for r in rows]
+    drs = [None if r is None else _f32(r) for r in draft_rows]
+    vocab = rows[0].size if rows else 0
+    ptrs = (C.c_void_p * max(1, len(rows)))(*[r.ctypes.data for r in rows])
+    dptrs = (C.c_void_p * max(1, len(drs)))(*[None if r is None else r.ctypes.data for r in drs])
+    res = VerifyResult()
+    diag = (RejectDiag * max(1, len(drafts)))()
+    for i in range(len(diag)):
+        diag[i].r = -1.0
+    rc = lib().or_verify_draft(d, len(drafts), ptrs, len(rows), dptrs, len(drs), vocab, t, p, k,
+                               rp, base_seed & 0xFFFFFFFFFFFFFFFF, C.byref(res), diag)
+    if rc != OR_OK:
+        raise RuntimeError(f"oracle verify failed with code {rc}")
+    return {
+        "tokens": [int(res.tokens[i]) for i in range(res.n_tokens)],
+        "num_accepted": int(res.num_accepted),
+        "total_drafted": int(res.total_drafted),
+        "bonus_token_sampled": bool(res.bonus_token_sampled),
+        "bonus_token": int(res.bonus_token),
+        "acceptance_rate": float(res.acceptance_rate),
+        "diag": [None if diag[i].r == -1.0 else {f: getattr(diag[i], f) for f, _ in RejectDiag._fields_}
+                 for i in range(len(drafts))],
+    }
+
+
 # ---- LM head (cpu_reference.cpp:643-665) -----------------------------------------------------
 
 def lm_head(W, S, B, hidden, d: int, group: int = 64, row0: int = 0, nrows: int | None = None,
@@ -261,6 +362,13 @@ class Reference:
         L.ref_sample_token.argtypes = [_f32p, C.c_uint32, C.c_float, C.c_float, C.c_int,
                                        C.c_float, C.c_uint64, C.POINTER(C.c_uint32),
                                        C.c_char_p, C.c_size_t]
+        L.ref_evaluate_verification_draft.restype = C.c_int
+        L.ref_evaluate_verification_draft.argtypes = [_u32p, C.c_size_t, C.POINTER(C.c_void_p),
+                                                      C.c_size_t, C.POINTER(C.c_void_p),
+                                                      C.c_size_t, C.c_uint32, C.c_float,
+                                                      C.c_float, C.c_int, C.c_float, C.c_uint64,
+                                                      _u32p, _u32p, C.POINTER(C.c_double),
+                                                      C.c_char_p, C.c_size_t]
         L.ref_evaluate_verification.restype = C.c_int
         L.ref_evaluate_verification.argtypes = [_u32p, C.c_size_t, C.POINTER(C.c_void_p),
                                                 C.c_size_t, C.c_uint32, C.c_float, C.c_float,
@@ -310,6 +418,32 @@ class Reference:
         rc = self.lib.ref_evaluate_verification(d, len(drafts), ptrs, len(rows), vocab, t, p, k,
                                                 rp, base_seed & 0xFFFFFFFFFFFFFFFF, toks, info,
                                                 C.byref(rate), buf, 256)
+        if rc != 0:
+            raise RuntimeError(buf.value.decode())
+        return {
+            "tokens": [int(x) for x in toks[: info[0]]],
+            "num_accepted": int(info[1]),
+            "total_drafted": int(info[2]),
+            "bonus_token_sampled": bool(info[3]),
+            "bonus_token": int(info[4]),
+            "acceptance_rate": float(rate.value),
+        }
+
+    def verify_draft(self, drafts, rows, draft_rows, t=0.8, p=1.0, k=0, rp=1.0, base_seed=0):
+        d = _u32(drafts) if len(drafts) else np.zeros(1, np.uint32)
+        rows = [_f32(r) for r in rows]
+        drs = [None if r is None else _f32(r) for r in draft_rows]
+        vocab = rows[0].size if rows else 0
+        ptrs = (C.c_void_p * max(1, len(rows)))(*[r.ctypes.data for r in rows])
+        dptrs = (C.c_void_p * max(1, len(drs)))(*[None if r is None else r.ctypes.data for r in drs])
+        toks = np.zeros(len(drafts) + 2, np.uint32)
+        info = np.zeros(5, np.uint32)
+        rate = C.c_double(0.0)
+        buf = C.create_string_buffer(256)
+        rc = self.lib.ref_evaluate_verification_draft(d, len(drafts), ptrs, len(rows), dptrs,
+                                                      len(drs), vocab, t, p, k, rp,
+                                                      base_seed & 0xFFFFFFFFFFFFFFFF, toks, info,
+                                                      C.byref(rate), buf, 256)
         if rc != 0:
             raise RuntimeError(buf.value.decode())
         return {

@@ -95,4 +95,35 @@ int ref_evaluate_verification(const uint32_t* drafts, size_t n_drafts, const flo
     }
 }
 
+// evaluate_verification with draft logits: draft_rows[i] (i < n_draft_rows) is position i's
+// draft row, or NULL for an empty vector. Outputs as ref_evaluate_verification.
+int ref_evaluate_verification_draft(const uint32_t* drafts, size_t n_drafts,
+                                    const float* const* rows, size_t n_rows,
+                                    const float* const* draft_rows, size_t n_draft_rows,
+                                    uint32_t vocab, float t, float p, int k, float rp,
+                                    uint64_t base_seed, uint32_t* tokens_out, uint32_t* info_out,
+                                    double* rate_out, char* err, size_t err_len) {
+    try {
+        SpeculativeCoordinator sc;
+        std::vector<uint32_t> d(drafts, drafts + n_drafts);
+        std::vector<const float*> r(rows, rows + n_rows);
+        std::vector<std::vector<float>> dl(n_draft_rows);
+        for (size_t i = 0; i < n_draft_rows; ++i)
+            if (draft_rows[i]) dl[i].assign(draft_rows[i], draft_rows[i] + vocab);
+        SpeculativeEvaluation ev =
+            sc.evaluate_verification(d, r, vocab, make_params(t, p, k, rp, 0, 0), base_seed, dl);
+        for (size_t i = 0; i < ev.accepted_tokens.size(); ++i) tokens_out[i] = ev.accepted_tokens[i];
+        info_out[0] = static_cast<uint32_t>(ev.accepted_tokens.size());
+        info_out[1] = ev.num_accepted;
+        info_out[2] = ev.total_drafted;
+        info_out[3] = ev.bonus_token_sampled ? 1u : 0u;
+        info_out[4] = ev.bonus_token;
+        *rate_out = ev.acceptance_rate;
+        return 0;
+    } catch (const std::exception& e) {
+        copy_err(e, err, err_len);
+        return 2;
+    }
+}
+
 }  // extern "C"

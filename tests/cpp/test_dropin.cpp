@@ -132,6 +132,45 @@ int main() {
         CHECK(spec.total_draft_tokens() == 10 && spec.total_accepted_tokens() == 6);
     }
     std::puts("speculative verify ok");
+
+    {
+        // draft logits (speculator.cpp:71-122). Identical draft and target rows: p == q, so
+        // r == 1 and every position is accepted; the bonus is sample_token of the last row.
+        SpeculativeCoordinator spec;
+        const uint32_t V = 1024;
+        std::mt19937 rng(99);
+        std::normal_distribution<float> nd(0.0f, 3.0f);
+        std::vector<std::vector<float>> rows(4, std::vector<float>(V));
+        for (auto& r : rows)
+            for (auto& x : r) x = nd(rng);
+        std::vector<const float*> ptrs;
+        for (auto& r : rows) ptrs.push_back(r.data());
+        SamplingParams sp{0.9f, 1.0f, 0, 1.0f, false, 0};
+        std::vector<std::vector<float>> drafts_l(rows.begin(), rows.begin() + 3);
+        auto e = spec.evaluate_verification({5, 6, 7}, ptrs, V, sp, 321, drafts_l);
+        CHECK(e.num_accepted == 3 && e.bonus_token_sampled);
+        CHECK(e.bonus_token == sample_token(ptrs[3], V, sp, splitmix64(321 + 3)));
+
+        // Flat target logits (p = 1/1024 everywhere) against a draft row of zeros with one NaN:
+        // the draft's softmax sum is NaN, so q stays unnormalised (q = 1), r = 2^-10, and a
+        // rejection finds (p - q)+ summing to 0: the fallback sample_token of the target row.
+        std::vector<float> flat(V, 0.0f);
+        std::vector<std::vector<float>> nan_row(1, std::vector<float>(V, 0.0f));
+        nan_row[0][500] = std::nanf("");
+        std::vector<const float*> one{flat.data()};
+        const uint64_t base = 777;
+        std::mt19937_64 g(splitmix64(base));
+        std::uniform_real_distribution<float> ud(0.0f, 1.0f);
+        const float u1 = ud(g);
+        auto f = spec.evaluate_verification({9}, one, V, sp, base, nan_row);
+        if (u1 <= 1.0f / 1024.0f) {
+            CHECK(f.num_accepted == 1 && f.accepted_tokens[0] == 9);
+        } else {
+            CHECK(f.num_accepted == 0 && f.accepted_tokens.size() == 1);
+            CHECK(f.accepted_tokens[0] == sample_token(flat.data(), V, sp, splitmix64(base)));
+        }
+    }
+    std::puts("draft-logits verify ok");
     std::puts("ALL OK");
     return 0;
 }

@@ -34,6 +34,25 @@ def f32_hex(a) -> list[str]:
     return [f"{int(x):08x}" for x in np.asarray(a, np.float32).view(np.uint32)]
 
 
+def draft_case_rows(seed: int, vocab: int, nrows: int) -> list:
+    """Target rows of a verify_draft case: softcap(30) of N(0, 4^2) rows from std::mt19937."""
+    return [O.softcap(O.gen_mt19937_normal(seed + j, 0.0, 4.0, vocab), 30.0) for j in range(nrows)]
+
+
+def draft_case_drafts(seed: int, vocab: int, rows: list, alpha: float, sd: float, mask) -> list:
+    """Draft rows: alpha * target + N(0, sd^2) noise in float32 (None where mask is False); a
+    position past the target rows mixes with row 0."""
+    out = []
+    for i, m in enumerate(mask):
+        if not m:
+            out.append(None)
+            continue
+        base = rows[min(i, len(rows) - 1)]
+        noise = O.gen_mt19937_normal(seed + 1000 + i, 0.0, sd, vocab)
+        out.append((np.float32(alpha) * base + noise).astype(np.float32))
+    return out
+
+
 def main() -> None:
     R = O.Reference()
     out: dict = {"source": "reference src/sampling.cpp + src/speculator.cpp via oracle/_ref"}
@@ -148,6 +167,49 @@ def main() -> None:
                     "drafts": drafts, "t": t, "p": p, "k": k, "base_seed": str(base),
                     "result": res})
     out["verify"] = ver
+
+    # ---- verify with draft logits: the rejection branch (speculator.cpp:71-122) ---------------
+    vd = []
+    drng = np.random.default_rng(77)
+    for case in range(40):
+        vocab = V_FULL if case % 10 == 9 else 4096
+        nrows = int(drng.integers(1, 7))
+        ndraft = int(drng.integers(1, 7))
+        seed_t = 9000 + 32 * case
+        rws = draft_case_rows(seed_t, vocab, nrows)
+        alpha = float(drng.choice([0.0, 0.5, 0.9, 1.0]))
+        dsd = float(drng.choice([0.5, 2.0, 4.0]))
+        mask = [bool(drng.random() < 0.85) for _ in range(ndraft)]
+        drs = draft_case_drafts(seed_t, vocab, rws, alpha, dsd, mask)
+        arg = [int(np.argmax(r)) for r in rws]
+        drafts = [arg[i] if i < nrows and drng.random() < 0.5 else int(drng.integers(0, vocab))
+                  for i in range(ndraft)]
+        t, rp = [(0.8, 1.0), (1.0, 1.0), (0.5, 1.0), (1.3, 1.0), (0.0, 1.1)][case % 5]
+        p, k = [(1.0, 0), (0.9, 40)][(case // 5) % 2]
+        base = int(drng.integers(0, 2**63))
+        res = R.verify_draft(drafts, rws, drs, t, p, k, rp, base)
+        vd.append({"vocab": vocab, "rows_seed": seed_t, "nrows": nrows, "alpha": alpha,
+                   "draft_sd": dsd, "mask": mask, "drafts": drafts, "t": t, "p": p, "k": k,
+                   "rp": rp, "base_seed": str(base), "result": res})
+    # A draft row equal to its target row except for one NaN: compute_softmax's sum is then NaN,
+    # so q is left unnormalised (inv = 1), q >= p everywhere, p/q = 1/sum_p, and a rejection
+    # finds (p - q)+ summing to 0 -- the fallback to sample_token (:113-115).
+    for case in range(6):
+        vocab = 4096
+        seed_t = 12000 + 32 * case
+        rws = draft_case_rows(seed_t, vocab, 3)
+        drs = draft_case_drafts(seed_t, vocab, rws, 1.0, 0.0, [True, True])
+        nan_at = [int(drng.integers(0, vocab)) for _ in drs]
+        for r, j in zip(drs, nan_at):
+            r[j] = np.nan
+        drafts = [int(np.argsort(rws[i])[-2]) for i in range(2)]  # not the argmax, not NaN
+        t, p, k = [(0.8, 1.0, 0), (1.0, 0.9, 40), (0.6, 1.0, 0)][case % 3]
+        base = int(drng.integers(0, 2**63))
+        res = R.verify_draft(drafts, rws, drs, t, p, k, 1.0, base)
+        vd.append({"vocab": vocab, "rows_seed": seed_t, "nrows": 3, "alpha": 1.0,
+                   "draft_sd": 0.0, "mask": [True, True], "nan_at": nan_at, "drafts": drafts,
+                   "t": t, "p": p, "k": k, "rp": 1.0, "base_seed": str(base), "result": res})
+    out["verify_draft"] = vd
 
     path = os.path.join(HERE, "sampling_golden.json")
     with open(path, "w") as f:

@@ -22,7 +22,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(LIB)
     syms = declared_symbols()
-    assert len(syms) == 19, syms
+    assert len(syms) == 21, syms
     missing = [s for s in syms if not hasattr(lib, s)]
     assert not missing, missing
 
@@ -50,6 +50,24 @@ def test_host_seeding_matches_oracle(oracle):
                 s = t.seed_for(p, pos)
                 assert s == oracle.seed_for(has, seed, pos)
                 assert t.uniform_from_seed(s) == oracle.uniform_from_seed(s)
+
+
+def test_rejection_uniforms_match_oracle(oracle):
+    # host-side draws of the rejection branch: the library's std::mt19937_64 +
+    # uniform_real_distribution<float> against the oracle's restatement
+    t = twd()
+    for i in range(2000):
+        seed = oracle.splitmix64(i * 7919)
+        assert t.rejection_uniforms(seed) == oracle.rejection_uniforms(seed)
+
+
+def test_verify_draft_argument_checks():
+    t = twd()
+    res = ctypes.c_void_p(16)
+    rp = t.RowParams(0.8, 1.0, 0, 1.0, 0.0, 0.0, 0, 0)
+    assert t.lib.twd_verify_draft(None, None, 10, 1, 10, None, 0, ctypes.byref(rp), 0, None, 0,
+                                  res, None) == t.TWD_E_INVALID
+    assert b"null selector" in t.lib.twd_last_error()
 
 
 def test_host_validation_matches_golden(golden):

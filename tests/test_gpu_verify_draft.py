@@ -1,0 +1,151 @@
+"""GPU parity of speculative verify with draft logits (src/speculator.cpp:14-30, :34-153): the
+rejection-sampling branch (fp32 softmaxes of target and draft rows, ratio test, residual draw
+from (p - q)+) composed with sample-and-compare and the bonus row.
+
+The device reproduces the reference's sequential fp32 sums exactly, so results are compared
+bit-exactly: against the reference build's outputs in tests/golden/sampling_golden.json, and
+against the oracle (oracle.c, pinned by tests/test_oracle.py) on random cases. The oracle's
+ratio-test margin |u1 - r| is printed for every rejection-branch position: only an expf last-ulp
+difference within that margin could flip a decision."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from helpers import ROOT, twd
+
+pytestmark = pytest.mark.gpu
+
+V = 262144
+
+
+@pytest.fixture(scope="module")
+def env():
+    import torch
+    assert torch.cuda.is_available(), "GPU test run without a GPU"
+    t = twd()
+    return torch, torch.device("cuda:0"), t, t.Selector(V, 65)
+
+
+def run_device(env, rows, draft_rows, drafts, T, p, k, rp, base):
+    torch, dev, t, sel = env
+    lg = torch.from_numpy(np.ascontiguousarray(np.stack(rows), np.float32)).to(dev)
+    drs = [None if d is None else torch.from_numpy(np.ascontiguousarray(d, np.float32)).to(dev)
+           for d in draft_rows]
+    d = torch.from_numpy(np.asarray(drafts, np.uint32).view(np.int32)).to(dev)
+    params = t.RowParams(T, p, k, rp, 0.0, 0.0, 0, 0)
+    res = sel.verify_draft(lg, drs, params, base, d)
+    torch.cuda.synchronize()
+    return t.decode_verify(res)
+
+
+def same(got, want):
+    keys = ("tokens", "num_accepted", "total_drafted", "bonus_token_sampled")
+    return all(got[k] == want[k] for k in keys) and (
+        not want["bonus_token_sampled"] or got["bonus_token"] == want["bonus_token"])
+
+
+def golden_case(c):
+    sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+    from make_golden import draft_case_drafts, draft_case_rows
+    rows = draft_case_rows(c["rows_seed"], c["vocab"], c["nrows"])
+    drs = draft_case_drafts(c["rows_seed"], c["vocab"], rows, c["alpha"], c["draft_sd"], c["mask"])
+    for r, j in zip(drs, c.get("nan_at", [])):
+        r[j] = np.nan
+    return rows, drs
+
+
+def test_verify_draft_golden(env, golden):
+    # 46 cases (6 at V=262144) with the reference build's own outputs: accepted positions,
+    # residual draws and the NaN-driven fallback to sample_token
+    for i, c in enumerate(golden["verify_draft"]):
+        rows, drs = golden_case(c)
+        got = run_device(env, rows, drs, c["drafts"], c["t"], c["p"], c["k"], c["rp"],
+                         int(c["base_seed"]))
+        print(f"case {i} V={c['vocab']} -> {got['tokens']} accepted {got['num_accepted']}")
+        assert same(got, c["result"]), (i, got, c["result"])
+
+
+def _random_case(rng, vocab):
+    K = int(rng.integers(1, 6))
+    rows = [(rng.standard_normal(vocab) * rng.uniform(1.0, 5.0)).astype(np.float32)
+            for _ in range(K + int(rng.integers(0, 2)))]
+    drs = []
+    for i in range(K):
+        if rng.random() < 0.15:
+            drs.append(None)
+            continue
+        mix = float(rng.choice([0.3, 0.8, 0.95]))
+        base = rows[min(i, len(rows) - 1)]
+        drs.append((mix * base + (1 - mix) * rng.standard_normal(vocab) * 3).astype(np.float32))
+    drafts = [int(np.argmax(rows[i])) if i < len(rows) and rng.random() < 0.5
+              else int(rng.integers(0, vocab)) for i in range(K)]
+    T = float(rng.choice([0.5, 0.8, 1.0, 1.3]))
+    k = int(rng.choice([0, 40]))
+    return rows, drs, drafts, T, (1.0 if k == 0 else 0.9), k, int(rng.integers(0, 2**63))
+
+
+@pytest.mark.parametrize("vocab", [3000, 50000, V])
+def test_verify_draft_random_vs_oracle(env, oracle, vocab):
+    rng = np.random.default_rng(vocab)
+    n_rej = 0
+    for case in range(12 if vocab == V else 30):
+        rows, drs, drafts, T, p, k, base = _random_case(rng, vocab)
+        want = oracle.verify_draft(drafts, rows, drs, T, p, k, 1.0, base)
+        for i, d in enumerate(want.pop("diag")):
+            if d is not None:
+                print(f"case {case} pos {i}: r={d['r']:.7g} u1={d['u1']:.7g} "
+                      f"margin={abs(d['u1'] - d['r']):.3g} accepted={d['accepted']}")
+                n_rej += 0 if d["accepted"] else 1
+        got = run_device(env, rows, drs, drafts, T, p, k, 1.0, base)
+        assert same(got, want), (case, got, want)
+    assert n_rej > 0
+
+
+def test_verify_draft_edges(env, oracle):
+    rng = np.random.default_rng(3)
+    vocab = 5000
+    t_rows = [(rng.standard_normal(vocab) * 3).astype(np.float32) for _ in range(4)]
+    d_rows = [(rng.standard_normal(vocab) * 3).astype(np.float32) for _ in range(3)]
+    cases = []
+    # a draft id past the vocabulary: q_val = 0, so r = 1 and the position is accepted
+    cases.append((t_rows, d_rows, [vocab + 7, 1, 2], 0.8, 1.0))
+    # NaN in a target row: its softmax sum is NaN, p stays unnormalised
+    tr = [r.copy() for r in t_rows]
+    tr[0][17] = np.nan
+    cases.append((tr, d_rows, [int(np.argmax(t_rows[0])), 3, 4], 0.8, 1.0))
+    # a draft row of -inf except one entry: q is one-hot
+    dr = [r.copy() for r in d_rows]
+    dr[1][:] = -np.inf
+    dr[1][123] = 0.0
+    cases.append((t_rows, dr, [int(np.argmax(t_rows[0])), 123, 9], 1.0, 1.0))
+    # temperature 0 with a penalty: not greedy, compute_softmax runs at T = 1
+    cases.append((t_rows, d_rows, [5, 6, 7], 0.0, 1.1))
+    # greedy params: the draft rows are ignored
+    cases.append((t_rows, d_rows, [int(np.argmax(t_rows[0])), 6, 7], 0.0, 1.0))
+    # fewer target rows than drafts: k = rows, no bonus row
+    cases.append((t_rows[:2], d_rows, [11, 12, 13], 0.9, 1.0))
+    for i, (tr, dr, drafts, T, rp) in enumerate(cases):
+        base = 1000 + i
+        want = oracle.verify_draft(drafts, tr, dr, T, 1.0, 0, rp, base)
+        want.pop("diag")
+        got = run_device(env, tr, dr, drafts, T, 1.0, 0, rp, base)
+        assert same(got, want), (i, got, want)
+
+
+def test_python_coordinator_with_draft_logits(env, oracle):
+    torch, dev, t, sel = env
+    rng = np.random.default_rng(8)
+    vocab = 2048
+    rows = [(rng.standard_normal(vocab) * 2).astype(np.float32) for _ in range(4)]
+    drs = [(0.5 * rows[i] + rng.standard_normal(vocab)).astype(np.float32) for i in range(3)]
+    drafts = [int(np.argmax(rows[i])) for i in range(3)]
+    sc = t.SpeculativeCoordinator()
+    sp = t.SamplingParams(0.9, 1.0, 0, 1.0)
+    lg = torch.from_numpy(np.stack(rows)).to(dev)
+    got = sc.evaluate_verification(drafts, lg, vocab, sp, 77,
+                                   [torch.from_numpy(d).to(dev) for d in drs])
+    want = oracle.verify_draft(drafts, rows, drs, 0.9, 1.0, 0, 1.0, 77)
+    want.pop("diag")
+    assert same(got, want), (got, want)

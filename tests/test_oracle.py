@@ -5,11 +5,14 @@ GPU; the reference-build comparisons are skipped when oracle/_ref was not built.
 """
 import hashlib
 import math
+import os
+import sys
 
 import numpy as np
 import pytest
 
 V = 262144
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def sha(a):
@@ -324,6 +327,119 @@ def test_reference_build_verify(oracle, reference):
         got = oracle.verify(drafts, rows, t, 0.9 if t else 1.0, 20 if t else 0, base)
         want = reference.verify(drafts, rows, t, 0.9 if t else 1.0, 20 if t else 0, 1.0, base)
         assert got == want
+
+
+# ---- verify with draft logits: the rejection branch (speculator.cpp:14-30, :71-122) --------
+
+def test_mt19937_64_known_answer(oracle):
+    # [rand.predef]: the 10000th consecutive invocation of a default-constructed mt19937_64
+    # produces 9981545732273789042
+    assert oracle.mt64_outputs(5489, 10000)[-1] == 9981545732273789042
+    assert oracle.std_mt64_10000th() == 9981545732273789042
+
+
+def test_rejection_uniforms_match_libstdcxx(oracle):
+    seeds = [oracle.splitmix64(i) for i in range(10000)] + [0, 1, 5489, 2**63, 2**64 - 1]
+    std = oracle.std_rejection_uniforms(seeds)
+    mine = np.array([oracle.rejection_uniforms(s) for s in seeds], np.float32)
+    assert np.array_equal(std.view(np.uint32), mine.view(np.uint32))
+    assert float(std.min()) >= 0.0 and float(std.max()) < 1.0
+
+
+def test_canonical_float_closed_forms(oracle):
+    assert oracle.canonical_float(0) == 0.0
+    assert oracle.canonical_float(1 << 40) == 2.0 ** -24
+    assert oracle.canonical_float(3 << 62) == 0.75
+    below_one = float(np.nextafter(np.float32(1), np.float32(0)))
+    # every x whose float rounds to 2^64 is clamped below 1
+    for x in (2**64 - 1, 2**64 - 2**39, 2**64 - 2**40 + 1):
+        assert oracle.canonical_float(x) == below_one
+    assert oracle.canonical_float(2**64 - 2**40 - 2**39) < below_one
+
+
+def test_softmax_closed_forms(oracle):
+    # equal logits: every p is 1/n; T scales the logits first; T <= 0 means T = 1
+    p = oracle.softmax(np.zeros(8, np.float32), 0.7)
+    assert np.all(p == np.float32(1.0 / 8.0))
+    two = np.array([0.0, np.log(3.0)], np.float32)
+    q = oracle.softmax(two, 0.0)
+    assert abs(float(q[1]) / float(q[0]) - 3.0) < 1e-6
+    # all logits below -1e9: every exp underflows, the sum is 0 and the division uses 1
+    z = oracle.softmax(np.full(4, -3e9, np.float32), 1.0)
+    assert np.all(z == 0.0)
+
+
+def _draft_case(golden_case):
+    sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+    from make_golden import draft_case_drafts, draft_case_rows
+    c = golden_case
+    rows = draft_case_rows(c["rows_seed"], c["vocab"], c["nrows"])
+    drs = draft_case_drafts(c["rows_seed"], c["vocab"], rows, c["alpha"], c["draft_sd"], c["mask"])
+    for r, j in zip(drs, c.get("nan_at", [])):
+        r[j] = np.nan
+    return rows, drs
+
+
+def test_verify_draft_golden(oracle, golden):
+    kinds = {"accepted": 0, "residual": 0, "fallback": 0}
+    for c in golden["verify_draft"]:
+        rows, drs = _draft_case(c)
+        got = oracle.verify_draft(c["drafts"], rows, drs, c["t"], c["p"], c["k"], c["rp"],
+                                  int(c["base_seed"]))
+        for d in got.pop("diag"):
+            if d is not None:
+                kinds["accepted" if d["accepted"] else
+                      ("fallback" if d["corr"] == 0xFFFFFFFF else "residual")] += 1
+        assert got == c["result"], c
+    assert min(kinds.values()) >= 5, kinds
+
+
+def test_verify_draft_identical_rows_always_accept(oracle):
+    # p == q elementwise gives r = p/q = 1 exactly, and every draw is < 1
+    rng = np.random.default_rng(5)
+    for trial in range(20):
+        vocab = int(rng.integers(2, 3000))
+        rows = [rng.standard_normal(vocab).astype(np.float32) * 3 for _ in range(4)]
+        drafts = [int(rng.integers(0, vocab)) for _ in range(3)]
+        got = oracle.verify_draft(drafts, rows, [r.copy() for r in rows[:3]], 0.9, 1.0, 0, 1.0,
+                                  int(rng.integers(0, 2**63)))
+        assert got["num_accepted"] == 3 and got["tokens"][:3] == drafts
+        assert all(d["r"] == 1.0 for d in got["diag"])
+
+
+def test_reference_build_verify_draft(oracle, reference):
+    rng = np.random.default_rng(31)
+    kinds = set()
+    for case in range(150):
+        vocab = int(rng.integers(2, 5000))
+        K = int(rng.integers(1, 6))
+        rows = [(rng.standard_normal(vocab) * rng.uniform(0.5, 4)).astype(np.float32)
+                for _ in range(K + int(rng.integers(0, 2)))]
+        drs = []
+        for i in range(K):
+            if rng.random() < 0.15:
+                drs.append(None)
+                continue
+            mix = float(rng.uniform(0, 1))
+            d = (mix * rows[min(i, len(rows) - 1)] +
+                 (1 - mix) * rng.standard_normal(vocab) * 2).astype(np.float32)
+            if rng.random() < 0.1:
+                d = rows[min(i, len(rows) - 1)].copy()
+                d[int(rng.integers(0, vocab))] = np.nan  # unnormalised q: the fallback
+            drs.append(d)
+        drafts = [int(np.argmax(rows[i])) if i < len(rows) and rng.random() < 0.5
+                  else int(rng.integers(0, vocab)) for i in range(K)]
+        t = float(rng.choice([0.0, 0.5, 0.8, 1.0, 1.3]))
+        rp = float(rng.choice([1.0, 1.1]))
+        k = int(rng.choice([0, 40]))
+        p = 1.0 if k == 0 else 0.9
+        base = int(rng.integers(0, 2**63))
+        got = oracle.verify_draft(drafts, rows, drs, t, p, k, rp, base)
+        for d in got.pop("diag"):
+            if d is not None:
+                kinds.add("a" if d["accepted"] else ("f" if d["corr"] == 0xFFFFFFFF else "r"))
+        assert got == reference.verify_draft(drafts, rows, drs, t, p, k, rp, base), case
+    assert kinds == {"a", "r", "f"}
 
 
 # ---- LM head ---------------------------------------------------------------------------------------------

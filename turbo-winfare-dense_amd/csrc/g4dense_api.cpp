@@ -28,6 +28,8 @@ struct Staging {
     uint32_t sel_vocab = 0, sel_rows = 0;
     float* logits = nullptr;
     size_t logits_cap = 0;
+    float* dlogits = nullptr;  // draft rows of evaluate_verification
+    size_t dlogits_cap = 0;
     uint32_t* history = nullptr;
     size_t history_cap = 0;
     uint32_t* drafts = nullptr;
@@ -156,16 +158,19 @@ G4_API SpeculativeEvaluation SpeculativeCoordinator::evaluate_verification(
     eval.total_drafted = static_cast<uint32_t>(draft_tokens.size());
     total_draft_tokens_ += eval.total_drafted;
     if (draft_tokens.empty() || target_logits_per_pos.empty()) return eval;
-    if (!sampling.is_greedy()) {
-        for (const auto& d : draft_logits)
-            if (!d.empty())
-                throw G4DenseFormatError(
-                    "evaluate_verification: rejection sampling with draft logits is not "
-                    "implemented on the device path");
-    }
     const size_t k = std::min(draft_tokens.size(), target_logits_per_pos.size());
     if (k > TWD_MAX_ROWS) throw G4DenseFormatError("evaluate_verification: more than 64 drafts");
     const uint32_t rows = static_cast<uint32_t>(std::min(target_logits_per_pos.size(), k + 1));
+    // positions whose draft probabilities select the rejection branch (speculator.cpp:72)
+    uint32_t n_draft_rows = 0;
+    if (!sampling.is_greedy()) {
+        for (size_t i = 0; i < k && i < draft_logits.size(); ++i) {
+            if (draft_logits[i].empty()) continue;
+            if (draft_logits[i].size() < vocab_size)
+                throw G4DenseFormatError("evaluate_verification: a draft logit row is shorter than vocab_size");
+            n_draft_rows = static_cast<uint32_t>(i + 1);
+        }
+    }
 
     Staging& s = staging();
     std::lock_guard<std::mutex> lock(s.mu);
@@ -175,10 +180,32 @@ G4_API SpeculativeEvaluation SpeculativeCoordinator::evaluate_verification(
                             vocab_size * sizeof(float), hipMemcpyHostToDevice), "upload rows");
     check_hip(hipMemcpy(s.drafts, draft_tokens.data(), k * sizeof(uint32_t), hipMemcpyHostToDevice),
               "upload drafts");
-    const twd_row_params r = row_params(sampling, 0.0f);
-    if (twd_verify(s.sel, s.logits, vocab_size, rows, vocab_size, &r, base_seed, s.drafts,
-                   static_cast<uint32_t>(k), s.vres, nullptr) != TWD_OK)
-        throw_last("evaluate_verification");
+    twd_row_params r = row_params(sampling, 0.0f);
+    if (n_draft_rows == 0) {
+        if (twd_verify(s.sel, s.logits, vocab_size, rows, vocab_size, &r, base_seed, s.drafts,
+                       static_cast<uint32_t>(k), s.vres, nullptr) != TWD_OK)
+            throw_last("evaluate_verification");
+    } else {
+        const size_t need = static_cast<size_t>(n_draft_rows) * vocab_size;
+        if (s.dlogits_cap < need) {
+            if (s.dlogits) check_hip(hipFree(s.dlogits), "hipFree");
+            s.dlogits = nullptr;
+            check_hip(hipMalloc(&s.dlogits, need * sizeof(float)), "hipMalloc draft rows");
+            s.dlogits_cap = need;
+        }
+        const float* dptr[TWD_MAX_ROWS] = {};
+        for (uint32_t i = 0; i < n_draft_rows; ++i) {
+            if (draft_logits[i].empty()) continue;
+            float* dst = s.dlogits + static_cast<size_t>(i) * vocab_size;
+            check_hip(hipMemcpy(dst, draft_logits[i].data(), vocab_size * sizeof(float),
+                                hipMemcpyHostToDevice), "upload draft rows");
+            dptr[i] = dst;
+        }
+        r.repetition_penalty = sampling.repetition_penalty;  // is_greedy() needs it
+        if (twd_verify_draft(s.sel, s.logits, vocab_size, rows, vocab_size, dptr, n_draft_rows, &r,
+                             base_seed, s.drafts, static_cast<uint32_t>(k), s.vres, nullptr) != TWD_OK)
+            throw_last("evaluate_verification");
+    }
     twd_verify_result v{};
     check_hip(hipMemcpy(&v, s.vres, sizeof(v), hipMemcpyDeviceToHost), "download result");
     if (v.n_tokens == TWD_TOKEN_DEGENERATE)

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <random>
 #include <string>
 
 #include "twd_internal.h"
@@ -57,6 +58,15 @@ TWD_API float twd_uniform_from_seed(uint64_t seed) {
     s ^= s >> 27;
     const uint64_t r = s * 0x2545F4914F6CDD1DULL;
     return static_cast<float>((r >> 40) & 0xFFFFFFu) / 16777216.0f;
+}
+
+TWD_API void twd_rejection_uniforms(uint64_t step_seed, float* u1, float* u2) {
+    std::mt19937_64 rng(step_seed);
+    std::uniform_real_distribution<float> udist(0.0f, 1.0f);
+    const float a = udist(rng);  // ratio test
+    const float b = udist(rng);  // residual draw
+    if (u1) *u1 = a;
+    if (u2) *u2 = b;
 }
 
 TWD_API int twd_validate_sampling(float t, float p, int32_t k, float rp) {

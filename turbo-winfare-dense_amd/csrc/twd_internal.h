@@ -114,6 +114,19 @@ struct SelectScratch {
 int scratch_alloc(SelectScratch* s, uint32_t max_vocab, uint32_t max_rows);
 void scratch_free(SelectScratch* s);
 
+// Scratch of the draft-logits verify, allocated on its first use by a selector.
+struct DraftScratch {
+    float* e = nullptr;        // [2 positions][vocab] expf(l / T - max)
+    float* part = nullptr;     // [2 positions][parts] partial maxima
+    uint32_t* flags = nullptr; // [2 * TWD_MAX_ROWS] NaN flags
+    uint32_t* rej = nullptr;   // [TWD_MAX_ROWS][4] per-position outcome
+    size_t e_capacity = 0;
+    size_t part_capacity = 0;
+};
+
+int draft_scratch_reserve(DraftScratch* d, uint32_t vocab, uint32_t npos);
+void draft_scratch_free(DraftScratch* d);
+
 // Enqueues penalty + selection over `rows` rows. `params` is a host array.
 int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_t rows,
                   uint64_t stride, const twd_row_params* params, const uint32_t* history,
@@ -127,5 +140,6 @@ int launch_verify_compare(const uint32_t* row_tokens, uint32_t rows, const uint3
 
 struct twd_selector {
     twd::SelectScratch scratch;
+    twd::DraftScratch draft;
     uint32_t max_vocab = 0;
 };

@@ -78,6 +78,9 @@ _SIGS = {
     "twd_select": (C.c_int, [_vp, _vp, _u32, _u32, _u64, C.POINTER(RowParams), _vp, _vp, _vp]),
     "twd_verify": (C.c_int, [_vp, _vp, _u32, _u32, _u64, C.POINTER(RowParams), _u64, _vp, _u32,
                              _vp, _vp]),
+    "twd_verify_draft": (C.c_int, [_vp, _vp, _u32, _u32, _u64, C.POINTER(_vp), _u32,
+                                   C.POINTER(RowParams), _u64, _vp, _u32, _vp, _vp]),
+    "twd_rejection_uniforms": (None, [_u64, C.POINTER(_f32), C.POINTER(_f32)]),
     "twd_splitmix64": (_u64, [_u64]),
     "twd_seed_for": (_u64, [C.c_int, _u64, C.c_int]),
     "twd_uniform_from_seed": (_f32, [_u64]),
@@ -221,6 +224,36 @@ class Selector:
                               _stream(stream)))
         return result
 
+    def verify_draft(self, logits, draft_rows, params: RowParams, base_seed: int, drafts,
+                     result=None, stream=None):
+        """evaluate_verification with draft logits (speculator.cpp:34-153): draft_rows[i] is a
+        float32 device row of position i's draft logits, or None."""
+        import torch
+        rows, vocab = logits.shape
+        if result is None:
+            result = torch.zeros(VERIFY_WORDS, dtype=torch.int32, device=logits.device)
+        if logits.stride(1) != 1:
+            raise ValueError("logit rows must be contiguous")
+        for r in draft_rows:
+            if r is not None and (r.numel() != vocab or not r.is_contiguous()):
+                raise ValueError("each draft row must be a contiguous row of vocab floats")
+        stride = logits.stride(0) if rows > 1 else vocab
+        ptrs = (_vp * max(1, len(draft_rows)))(*[None if r is None else r.data_ptr()
+                                                  for r in draft_rows])
+        _check(lib.twd_verify_draft(self.handle, _ptr(logits), vocab, rows, stride, ptrs,
+                                    len(draft_rows), C.byref(params),
+                                    base_seed & 0xFFFFFFFFFFFFFFFF, _ptr(drafts),
+                                    0 if drafts is None else drafts.numel(), _ptr(result),
+                                    _stream(stream)))
+        return result
+
+
+def rejection_uniforms(step_seed: int):
+    """The two draws of speculator.cpp:87-89,105 for one step seed."""
+    u1, u2 = _f32(), _f32()
+    lib.twd_rejection_uniforms(step_seed & 0xFFFFFFFFFFFFFFFF, C.byref(u1), C.byref(u2))
+    return float(u1.value), float(u2.value)
+
 
 _default_selector: Selector | None = None
 
@@ -287,20 +320,24 @@ class SpeculativeCoordinator:
 
     def evaluate_verification(self, draft_tokens, target_logits, vocab_size: int,
                               sampling: SamplingParams, base_seed: int, draft_logits=()):
-        """target_logits: float32 device tensor [rows, vocab]."""
+        """target_logits: float32 device tensor [rows, vocab]. draft_logits: per position a
+        float32 device row of vocab entries, or an empty sequence / None for none."""
         import torch
         n = len(draft_tokens)
         self.total_draft_tokens += n
         if n == 0 or target_logits.shape[0] == 0:
             return {"tokens": [], "num_accepted": 0, "total_drafted": n,
                     "bonus_token_sampled": False, "bonus_token": 0, "acceptance_rate": 0.0}
-        if not sampling.is_greedy() and any(len(d) for d in draft_logits):
-            raise G4DenseFormatError("evaluate_verification: rejection sampling with draft "
-                                     "logits is not implemented on the device path")
         drafts = torch.tensor(list(draft_tokens), dtype=torch.int64).to(torch.int32).to(
             target_logits.device)
         sel = _selector(vocab_size)
-        res = sel.verify(target_logits[:, :vocab_size], row_params(sampling), base_seed, drafts)
+        rows = [None if d is None or len(d) == 0 else d for d in draft_logits]
+        if not sampling.is_greedy() and any(r is not None for r in rows):
+            res = sel.verify_draft(target_logits[:, :vocab_size], rows, row_params(sampling),
+                                   base_seed, drafts)
+        else:
+            res = sel.verify(target_logits[:, :vocab_size], row_params(sampling), base_seed,
+                             drafts)
         out = decode_verify(res)
         self.total_accepted_tokens += out["num_accepted"]
         return out
