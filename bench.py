@@ -230,6 +230,25 @@ def main():
         results[4] = {"rows_per_s": 5 * n4 / r_s, "ms_per_step": k4 * 1e3,
                       "kernel_us_mean": k4 * 1e6, "hbm_frac": algorithmic_bytes(5) / k4 / PEAK_HBM}
 
+        # the same 5 rows verified with draft logits (rejection sampling, speculator.cpp:71-122):
+        # the head's logits plus 4 synthetic draft rows, T=0.8, k=40, p=0.9
+        lg4 = torch.empty(5, V, dtype=torch.float32, device=dev)
+        head.logits(hp4[0], out=lg4, stream=stream)
+        drng = np.random.default_rng(44)
+        drows = [(0.8 * lg4[i] + torch.from_numpy(
+            (drng.standard_normal(V) * 1.5).astype(np.float32)).to(dev)).contiguous()
+            for i in range(4)]
+        sel4 = twd.Selector(V, 5)
+        p4 = twd.RowParams(0.8, 0.9, 40, 1.0, 0.0, CAP, 0, 0)
+
+        def step4d(i):
+            sel4.verify_draft(lg4, drows, p4, 1000 + i, drafts[i % 64], result=res4,
+                              stream=stream)
+
+        nd = max(20, args.steps // 20)
+        r_d = time_loop(torch, nd, 5, step4d)
+        results[4]["draft_logits_verify_us"] = r_d / nd * 1e6
+
     # ---- config 5: M=64 rows, each with own T/k/p, rp 1.1 over its own 2048-id history ---------
     if 5 in cfgs:
         log("config 5: M=64 sampled, MFMA path")

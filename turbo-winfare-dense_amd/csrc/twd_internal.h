@@ -120,6 +120,7 @@ struct DraftScratch {
     float* part = nullptr;     // [2 positions][parts] partial maxima
     uint32_t* flags = nullptr; // [2 * TWD_MAX_ROWS] NaN flags
     uint32_t* rej = nullptr;   // [TWD_MAX_ROWS][4] per-position outcome
+    float* sums = nullptr;     // [2 * TWD_MAX_ROWS] softmax sums
     size_t e_capacity = 0;
     size_t part_capacity = 0;
 };

@@ -11,7 +11,8 @@
 // Kernels, all on the caller's stream:
 //   draft_max_kernel     grid (parts, 2P): per row, partial maxima of l / T (T = 1 when <= 0)
 //   draft_exp_kernel     grid (parts, 2P): e = expf(l / T - max) to scratch, NaN flags
-//   draft_reject_kernel  grid P, 1024 threads: the two sums, the ratio test, the residual draw
+//   draft_sum_kernel     grid 2P, 1024 threads: each softmax's sequential sum
+//   draft_reject_kernel  grid P, 1024 threads: the ratio test, the residual sum and draw
 //   draft_finish_kernel  one thread: the accept chain over all positions, bonus, result
 // where P is the number of positions with a draft row; the target tokens of the other
 // positions, of the fallback and of the bonus row come from the selector (launch_select).
@@ -35,7 +36,7 @@ constexpr uint32_t kDraftChunk = kDraftThreads * kDraftPer;  // entries per bloc
 constexpr uint32_t kDraftMaxParts = 128;                     // vocab <= 524288
 constexpr int kRejThreads = 1024;    // one block per position
 constexpr int kRejWaves = kRejThreads / 64;
-constexpr int kRejPer = 8;           // terms per thread per window
+constexpr int kRejPer = 16;          // terms per thread per window
 constexpr uint32_t kRejWin = kRejThreads * kRejPer;
 constexpr uint32_t kNoEvent = 0xFFFFFFFFu;
 
@@ -48,6 +49,7 @@ struct DraftPos {
 
 struct DraftArgs {
     uint32_t vocab;
+    uint32_t estride;             // row stride of e: vocab rounded up to 16 floats
     uint32_t parts;
     uint32_t npos;
     float temp;                   // compute_softmax's temperature (1 when <= 0)
@@ -55,6 +57,7 @@ struct DraftArgs {
     float* part;                  // [2P][parts] partial maxima
     float* e;                     // [2P][vocab] expf(l / T - max)
     uint32_t* flags;              // [2P] bit 0: a NaN term
+    float* sums;                  // [2P] compute_softmax sums
     uint32_t* rej;                // [64][4] {accepted, token, fallback, valid}
     DraftPos pos[TWD_MAX_ROWS];
 };
@@ -109,7 +112,7 @@ __global__ __launch_bounds__(kDraftThreads) void draft_exp_kernel(DraftArgs a) {
     }
     const uint32_t base = blockIdx.x * kDraftChunk + threadIdx.x;
     bool nan = false;
-    float* e = a.e + static_cast<size_t>(r) * a.vocab;
+    float* e = a.e + static_cast<size_t>(r) * a.estride;
 #pragma unroll
     for (int it = 0; it < kDraftPer; ++it) {
         const uint32_t j = base + it * kDraftThreads;
@@ -136,76 +139,67 @@ __global__ __launch_bounds__(kDraftThreads) void draft_exp_kernel(DraftArgs a) {
 // a binade the sums are integer prefix sums whose only data dependence is the parity of S / u
 // at each tie, which a scan over 2-state transfer functions resolves in parallel. The first
 // term whose sum leaves the binade (S / u reaching 2^24) is added with one real fp32 add, and
-// the scan restarts from there with the new binade's unit.
+// the scan restarts after it with the new binade's unit. Increments saturate at 2^30: any
+// prefix that large has left the binade, and saturating addition stays associative.
+
+constexpr uint32_t kSat = 1u << 30;
+constexpr uint32_t kL = 1u << 24;  // S / u at the top of a binade
+constexpr int kMarks = 128;         // recorded (k0, S) window starts, for a later search
+constexpr uint32_t kSerialUntil = 2048;  // terms summed one by one, in order, at the start
 
 struct Xfer {  // input parity p -> (total increment, output parity)
-    uint64_t inc0, inc1;
-    uint32_t out0, out1;
+    uint32_t inc0, inc1;
+    uint32_t out;  // bit p: output parity for input parity p
 };
 
-__device__ __forceinline__ Xfer xfer_id() { return Xfer{0, 0, 0u, 1u}; }
+__device__ __forceinline__ uint32_t sat_add(uint32_t a, uint32_t b) { return min(a + b, kSat); }
+
+__device__ __forceinline__ Xfer xfer_id() { return Xfer{0u, 0u, 2u}; }
 
 // f, then g
 __device__ __forceinline__ Xfer xfer_then(const Xfer& f, const Xfer& g) {
+    const uint32_t f0 = f.out & 1u, f1 = (f.out >> 1) & 1u;
     Xfer h;
-    h.inc0 = f.inc0 + (f.out0 ? g.inc1 : g.inc0);
-    h.out0 = f.out0 ? g.out1 : g.out0;
-    h.inc1 = f.inc1 + (f.out1 ? g.inc1 : g.inc0);
-    h.out1 = f.out1 ? g.out1 : g.out0;
+    h.inc0 = sat_add(f.inc0, f0 ? g.inc1 : g.inc0);
+    h.inc1 = sat_add(f.inc1, f1 ? g.inc1 : g.inc0);
+    h.out = ((g.out >> f0) & 1u) | (((g.out >> f1) & 1u) << 1);
     return h;
 }
 
 __device__ __forceinline__ Xfer xfer_shfl_up(const Xfer& x, int d) {
-    Xfer y;
-    y.inc0 = (static_cast<uint64_t>(__shfl_up(static_cast<uint32_t>(x.inc0 >> 32), d)) << 32) |
-             __shfl_up(static_cast<uint32_t>(x.inc0), d);
-    y.inc1 = (static_cast<uint64_t>(__shfl_up(static_cast<uint32_t>(x.inc1 >> 32), d)) << 32) |
-             __shfl_up(static_cast<uint32_t>(x.inc1), d);
-    const uint32_t o = __shfl_up(x.out0 | (x.out1 << 1), d);
-    y.out0 = o & 1u;
-    y.out1 = o >> 1;
-    return y;
+    return Xfer{static_cast<uint32_t>(__shfl_up(x.inc0, d)), static_cast<uint32_t>(__shfl_up(x.inc1, d)),
+                static_cast<uint32_t>(__shfl_up(x.out, d))};
 }
 
-// Term a >= 0 in units of u = 2^(E - 23): floor k, and kind 0 exact/rounds down, 1 rounds up,
-// 2 exactly half-way.
-__device__ __forceinline__ void split_term(float a, int E, uint64_t& k, uint32_t& kind) {
+__device__ __forceinline__ Xfer xfer_shfl(const Xfer& x, int src) {
+    return Xfer{static_cast<uint32_t>(__shfl(x.inc0, src)), static_cast<uint32_t>(__shfl(x.inc1, src)),
+                static_cast<uint32_t>(__shfl(x.out, src))};
+}
+
+// Term a >= 0 in units of u = 2^(E - 23): floor k (saturated), and kind 0 exact or rounds
+// down, 1 rounds up, 2 exactly half-way. Branch-free: a zero term, or one below u / 2 (shift
+// >= 25), comes out as k = 0, kind 0; one at least u * 2^24 saturates.
+__device__ __forceinline__ void split_term(float a, int E, uint32_t& k, uint32_t& kind) {
     const uint32_t b = __float_as_uint(a);
     const uint32_t f = b >> 23;
-    uint32_t m = b & 0x7FFFFFu;
-    int ea = -126;
-    if (f) {
-        m |= 0x800000u;
-        ea = static_cast<int>(f) - 127;
-    }
-    const int sh = E - ea;
-    kind = 0;
-    if (m == 0) {
-        k = 0;
-    } else if (sh <= 0) {
-        k = static_cast<uint64_t>(m) << min(-sh, 39);  // >= 2^24 from -sh >= 1: leaves the binade
-    } else if (sh >= 25) {
-        k = 0;  // a < u / 2
-    } else {
-        k = m >> sh;
-        const uint32_t rem = m & ((1u << sh) - 1u), half = 1u << (sh - 1);
-        kind = rem > half ? 1u : (rem == half ? 2u : 0u);
-    }
+    const uint32_t m = (b & 0x7FFFFFu) | (f ? 0x800000u : 0u);
+    const int sh = E - (max(static_cast<int>(f), 1) - 127);
+    const int shc = min(max(sh, 1), 31);
+    const uint32_t rem = m & ((1u << shc) - 1u), half = 1u << (shc - 1);
+    const uint32_t kr = rem > half ? 1u : (rem == half ? 2u : 0u);
+    k = sh > 0 ? (m >> shc) : (sh == 0 ? m : kSat);
+    kind = sh > 0 ? kr : 0u;
 }
 
-__device__ __forceinline__ Xfer term_xfer(uint64_t k, uint32_t kind) {
-    if (kind == 2) {
-        const uint32_t kp = static_cast<uint32_t>(k & 1);
-        return Xfer{k + kp, k + (kp ^ 1u), 0u, 0u};  // ties go to the even neighbour
-    }
-    const uint64_t c = k + kind;
-    const uint32_t cp = static_cast<uint32_t>(c & 1);
-    return Xfer{c, c, cp, cp ^ 1u};
+__device__ __forceinline__ Xfer term_xfer(uint32_t k, uint32_t kind) {
+    const uint32_t c = k + (kind & 1u), cp = c & 1u;
+    const uint32_t kp = k & 1u;
+    const bool tie = kind == 2u;  // ties go to the even neighbour
+    return Xfer{tie ? k + kp : c, tie ? k + (kp ^ 1u) : c, tie ? 0u : (cp | ((cp ^ 1u) << 1))};
 }
 
-__device__ __forceinline__ uint64_t term_inc(uint64_t k, uint32_t kind, uint32_t par) {
-    if (kind == 2) return k + ((par + static_cast<uint32_t>(k)) & 1u);
-    return k + kind;
+__device__ __forceinline__ uint32_t term_inc(uint32_t k, uint32_t kind, uint32_t par) {
+    return k + (kind == 2u ? ((par + k) & 1u) : kind);
 }
 
 struct SeqShared {
@@ -214,107 +208,230 @@ struct SeqShared {
     float S;
     uint32_t k0;
     uint32_t stop;
+    uint32_t n_marks;
+    uint32_t mark_k0[kMarks];
+    float mark_S[kMarks];
+    float head[kSerialUntil];  // the first terms, for the serial start
 };
 
-// Returns the sequential sum of term(0..n); *stop_at (when non-null) receives the first index
-// whose prefix is >= thr, or n when none is.
-template <typename Term>
-__device__ float block_seq_sum(Term term, uint32_t n, float thr, uint32_t* stop_at, SeqShared& sh) {
+// One window of block_seq_sum: PER terms per thread from the 16-aligned start a0 <= k0; terms
+// before k0 or at n and beyond count as zero. load(j0, a) fills a[0..PER) with terms j0.. (j0
+// a multiple of PER, in range or not), term(j) gives one term.
+template <int PER, typename Load, typename Term>
+__device__ __forceinline__ void seq_window(Load load, Term term, uint32_t n, float& S, uint32_t& k0,
+                                           float thr, bool want_stop, uint32_t& stop, SeqShared& sh) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const bool want_stop = stop_at != nullptr;
-    float S = 0.0f;
-    uint32_t k0 = 0;
-    uint32_t stop = n;
-    while (k0 < n) {
-        // the binade of S: S = B * 2^(E - 23) with B < 2^24
-        const uint32_t sb = __float_as_uint(S);
-        const uint32_t sf = sb >> 23;
-        const int E = sf ? static_cast<int>(sf) - 127 : -126;
-        const uint64_t B = sf ? ((sb & 0x7FFFFFu) | 0x800000u) : sb;
-        const uint32_t p0 = static_cast<uint32_t>(B & 1);
-        const double Tu = want_stop ? ldexp(static_cast<double>(thr), 23 - E) : 0.0;
-        constexpr uint64_t L = 1ull << 24;
+    constexpr uint32_t kWin = kRejThreads * PER;
+    // the binade of S: S = B * 2^(E - 23) with B < 2^24
+    const uint32_t sb = __float_as_uint(S);
+    const uint32_t sf = sb >> 23;
+    const int E = sf ? static_cast<int>(sf) - 127 : -126;
+    const uint32_t B = sf ? ((sb & 0x7FFFFFu) | 0x800000u) : sb;
+    const uint32_t p0 = B & 1u;
+    // the prefix threshold in units of u: R >= thr / u <=> R >= ceil(thr / u) for integer R
+    uint32_t Tu = 0xFFFFFFFFu;
+    if (want_stop) {
+        const double t = ceil(ldexp(static_cast<double>(thr), 23 - E));
+        Tu = t <= 0.0 ? 0u : (t >= 4294967295.0 ? 0xFFFFFFFFu : static_cast<uint32_t>(t));
+    }
 
-        // this thread's terms of the window
-        const uint32_t j0 = k0 + static_cast<uint32_t>(tid) * kRejPer;
-        uint64_t kk[kRejPer];
-        uint32_t kd[kRejPer];
-        Xfer t = xfer_id();
+    const uint32_t a0 = k0 & ~(kRejPer - 1u);
+    const uint32_t j0 = a0 + static_cast<uint32_t>(tid) * PER;
+    uint32_t kk[PER], kd[PER];
+    Xfer t = xfer_id();
+    {
+        // rows are padded to a multiple of 16 floats: a load starting below that end stays in
+        // the row, one starting at or past it is skipped (its terms are all past n)
+        float a[PER];
+        if (j0 < ((n + 15u) & ~15u)) {
+            load(j0, a);
+        } else {
 #pragma unroll
-        for (int q = 0; q < kRejPer; ++q) {
+            for (int q = 0; q < PER; ++q) a[q] = 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
             const uint32_t j = j0 + q;
-            const float a = j < n ? term(j) : 0.0f;
-            split_term(a, E, kk[q], kd[q]);
+            split_term((j >= k0 && j < n) ? a[q] : 0.0f, E, kk[q], kd[q]);
             t = xfer_then(t, term_xfer(kk[q], kd[q]));
         }
-        // wave inclusive scan, then exclusive
-        Xfer inc = t;
+    }
+    // wave inclusive scan
+    Xfer inc = t;
 #pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const Xfer o = xfer_shfl_up(inc, d);
-            if (lane >= d) inc = xfer_then(o, inc);
-        }
-        Xfer ex = xfer_shfl_up(inc, 1);
-        if (lane == 0) ex = xfer_id();
-        if (lane == 63) sh.wave_total[wave] = inc;
-        if (tid == 0) sh.event = kNoEvent;
-        __syncthreads();
-        Xfer wp = xfer_id();
-        for (int w = 0; w < wave; ++w) wp = xfer_then(wp, sh.wave_total[w]);
-        const Xfer in = xfer_then(wp, ex);
+    for (int d = 1; d < 64; d <<= 1) {
+        const Xfer o = xfer_shfl_up(inc, d);
+        if (lane >= d) inc = xfer_then(o, inc);
+    }
+    Xfer ex = xfer_shfl_up(inc, 1);
+    if (lane == 0) ex = xfer_id();
+    if (lane == 63) sh.wave_total[wave] = inc;
+    if (tid == 0) sh.event = kNoEvent;
+    __syncthreads();
+    // prefix over the waves before this one: a 16-lane scan of the wave totals
+    Xfer wt = lane < kRejWaves ? sh.wave_total[lane] : xfer_id();
+#pragma unroll
+    for (int d = 1; d < kRejWaves; d <<= 1) {
+        const Xfer o = xfer_shfl_up(wt, d);
+        if (lane >= d) wt = xfer_then(o, wt);
+    }
+    Xfer wp = xfer_shfl(wt, wave > 0 ? wave - 1 : 0);
+    if (wave == 0) wp = xfer_id();
+    const Xfer in = xfer_then(wp, ex);
 
-        // replay: the first term that leaves the binade, or reaches thr
-        uint64_t R = B + (p0 ? in.inc1 : in.inc0);
-        uint32_t par = p0 ? in.out1 : in.out0;
-        uint32_t my_event = kNoEvent;
-        uint64_t R_before = R;
+    // replay: the first term that leaves the binade (an exact add follows), or whose prefix
+    // reaches thr. A thread entering at R >= 2^24 follows an earlier thread's event.
+    uint32_t R = sat_add(B, p0 ? in.inc1 : in.inc0);
+    uint32_t par = (in.out >> p0) & 1u;
+    uint32_t my_event = kNoEvent;
+    uint32_t R_before = R;
+    bool live = R < kL;
 #pragma unroll
-        for (int q = 0; q < kRejPer; ++q) {
-            if (my_event != kNoEvent) break;
-            const uint32_t j = j0 + q;
-            if (j >= n) break;
-            const uint64_t d = term_inc(kk[q], kd[q], par);
-            if (R + d >= L) {
-                my_event = 2 * j;  // crossing: exact add
-                R_before = R;
-                break;
-            }
-            R += d;
-            par = (par + static_cast<uint32_t>(d)) & 1u;
-            if (want_stop && static_cast<double>(R) >= Tu) my_event = 2 * j + 1;
+    for (int q = 0; q < PER; ++q) {
+        const uint32_t j = j0 + q;
+        const uint32_t d = term_inc(kk[q], kd[q], par);
+        const bool go = live && j >= k0 && j < n;
+        const bool cross = go && (R + d >= kL);
+        const bool adv = go && !cross;
+        if (cross) {
+            my_event = 2 * j;
+            R_before = R;
         }
-        if (my_event != kNoEvent) atomicMin(&sh.event, my_event);
-        __syncthreads();
-        const uint32_t ev = sh.event;
-        if (ev == kNoEvent) {
-            if (tid == kRejThreads - 1) {
-                sh.S = ldexpf(static_cast<float>(R), E - 23);
-                sh.k0 = min(n, k0 + kRejWin);
-                sh.stop = n;
-            }
-        } else if (my_event == ev) {
-            const uint32_t j = ev >> 1;
-            if (ev & 1) {  // stop, no crossing before it
-                sh.S = ldexpf(static_cast<float>(R), E - 23);
-                sh.k0 = n;
-                sh.stop = j;
+        R = adv ? R + d : R;
+        par = adv ? ((par + d) & 1u) : par;
+        const bool hit = adv && R >= Tu;
+        if (hit) my_event = 2 * j + 1;
+        live = live && !cross && !hit;
+    }
+    if (my_event != kNoEvent) atomicMin(&sh.event, my_event);
+    __syncthreads();
+    const uint32_t ev = sh.event;
+    if (ev == kNoEvent) {
+        if (tid == kRejThreads - 1) {
+            sh.S = ldexpf(static_cast<float>(R), E - 23);
+            sh.k0 = min(n, a0 + kWin);
+            sh.stop = n;
+        }
+    } else if (my_event == ev) {
+        const uint32_t j = ev >> 1;
+        if (ev & 1) {  // reaches thr, no binade change before it
+            sh.S = ldexpf(static_cast<float>(R), E - 23);
+            sh.k0 = n;
+            sh.stop = j;
+        } else {
+            const float s_new = ldexpf(static_cast<float>(R_before), E - 23) + term(j);
+            const bool hit = want_stop && s_new >= thr;
+            sh.S = s_new;
+            sh.k0 = hit ? n : j + 1;
+            sh.stop = hit ? j : n;
+        }
+    }
+    __syncthreads();
+    S = sh.S;
+    k0 = sh.k0;
+    stop = sh.stop;
+    __syncthreads();  // sh is rewritten by the next window
+}
+
+// Continues the sequential sum from prefix S (the sum of terms [0, k0)) over terms [k0, n).
+// Returns the sum; *stop_at (when non-null) receives the first index whose prefix is >= thr, or
+// n when none is. With `record`, the start (k0, S) of every window is kept in sh's marks.
+// Windows are short (4 terms per thread) while k0 < kShortUntil, where the sum still changes
+// binade often and each change discards the rest of its window, and long (16) after.
+constexpr uint32_t kShortUntil = 65536;
+
+template <typename Load, typename Term>
+__device__ float block_seq_sum(Load load, Term term, uint32_t n, float S, uint32_t k0, float thr,
+                               uint32_t* stop_at, bool record, SeqShared& sh) {
+    const bool want_stop = stop_at != nullptr;
+    uint32_t stop = n;
+    if (record && threadIdx.x == 0) sh.n_marks = 0;
+    if (k0 < kSerialUntil) {
+        // The head of the sequence, where the sum changes binade at almost every doubling of
+        // its length: staged in LDS by the whole block, then added one term at a time, in
+        // order, by wave 0 -- the sequential loop itself, with no window restarts.
+        if (record && threadIdx.x == 0) {
+            sh.mark_k0[0] = k0;
+            sh.mark_S[0] = S;
+            sh.n_marks = 1;
+        }
+        const uint32_t end = min(n, kSerialUntil);
+        for (uint32_t base = 0; base < kSerialUntil; base += kRejThreads * 4) {
+            const uint32_t j0 = base + threadIdx.x * 4;
+            float a[4];
+            if (j0 < ((n + 15u) & ~15u)) {
+                load(j0, a);
             } else {
-                const float prev = ldexpf(static_cast<float>(R_before), E - 23);
-                const float s_new = prev + term(j);
-                sh.S = s_new;
-                sh.k0 = j + 1;
-                sh.stop = (want_stop && s_new >= thr) ? j : n;
-                if (sh.stop != n) sh.k0 = n;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) a[q] = 0.0f;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) sh.head[j0 + q] = a[q];
+        }
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            float s = S;
+            uint32_t hit = n;
+            for (uint32_t j = k0; j < end; ++j) {
+                s += sh.head[j];
+                if (want_stop && s >= thr) {
+                    hit = j;
+                    break;
+                }
+            }
+            if (threadIdx.x == 0) {
+                sh.S = s;
+                sh.k0 = hit < n ? n : end;
+                sh.stop = hit;
             }
         }
         __syncthreads();
         S = sh.S;
         k0 = sh.k0;
         stop = sh.stop;
-        __syncthreads();  // sh is rewritten by the next window
+        __syncthreads();
+    }
+    while (k0 < n) {
+        if (record && threadIdx.x == 0 && sh.n_marks < kMarks) {
+            sh.mark_k0[sh.n_marks] = k0;
+            sh.mark_S[sh.n_marks] = S;
+            ++sh.n_marks;
+        }
+        if (k0 < kShortUntil)
+            seq_window<4>(load, term, n, S, k0, thr, want_stop, stop, sh);
+        else
+            seq_window<kRejPer>(load, term, n, S, k0, thr, want_stop, stop, sh);
     }
     if (want_stop) *stop_at = stop;
     return S;
+}
+
+// PER consecutive floats from a 16 B aligned row position (row stride padded to 16 floats, so
+// reads past n stay inside the row's allocation)
+template <int PER>
+__device__ __forceinline__ void load_row(const float* row, uint32_t j0, float (&a)[PER]) {
+    const float4* p = reinterpret_cast<const float4*>(row + j0);
+#pragma unroll
+    for (int v = 0; v < PER / 4; ++v) {
+        const float4 x = p[v];
+        a[4 * v] = x.x;
+        a[4 * v + 1] = x.y;
+        a[4 * v + 2] = x.z;
+        a[4 * v + 3] = x.w;
+    }
+}
+
+// One block per softmax row (2 per position with draft probabilities): the sum of
+// compute_softmax (speculator.cpp:22-26), NaN as soon as one term is NaN.
+__global__ __launch_bounds__(kRejThreads) void draft_sum_kernel(DraftArgs a) {
+    __shared__ SeqShared sh;
+    const uint32_t r = blockIdx.x;
+    const float* e = a.e + static_cast<size_t>(r) * a.estride;
+    float s = __uint_as_float(0x7FC00000u);
+    if (!(a.flags[r] & 1u))
+        s = block_seq_sum([&](uint32_t j0, auto& v) { load_row(e, j0, v); },
+                          [&](uint32_t j) { return e[j]; }, a.vocab, 0.0f, 0u, 0.0f, nullptr, false, sh);
+    if (threadIdx.x == 0) a.sums[r] = s;
 }
 
 // One block per position with draft probabilities (speculator.cpp:74-121).
@@ -323,15 +440,9 @@ __global__ __launch_bounds__(kRejThreads) void draft_reject_kernel(DraftArgs a) 
     const uint32_t pi = blockIdx.x;
     const DraftPos& P = a.pos[pi];
     const uint32_t V = a.vocab;
-    const float* et = a.e + static_cast<size_t>(2 * pi) * V;
-    const float* ed = a.e + static_cast<size_t>(2 * pi + 1) * V;
-    const float nanf_ = __uint_as_float(0x7FC00000u);
-
-    // compute_softmax sums (:22-26): NaN as soon as one term is NaN
-    float sp = (a.flags[2 * pi] & 1u) ? nanf_
-                                      : block_seq_sum([&](uint32_t j) { return et[j]; }, V, 0.0f, nullptr, sh);
-    float sq = (a.flags[2 * pi + 1] & 1u) ? nanf_
-                                          : block_seq_sum([&](uint32_t j) { return ed[j]; }, V, 0.0f, nullptr, sh);
+    const float* et = a.e + static_cast<size_t>(2 * pi) * a.estride;
+    const float* ed = a.e + static_cast<size_t>(2 * pi + 1) * a.estride;
+    const float sp = a.sums[2 * pi], sq = a.sums[2 * pi + 1];
     const float inv_p = 1.0f / (sp > 1e-12f ? sp : 1.0f);
     const float inv_q = 1.0f / (sq > 1e-12f ? sq : 1.0f);
 
@@ -350,19 +461,36 @@ __global__ __launch_bounds__(kRejThreads) void draft_reject_kernel(DraftArgs a) 
         }
         return;
     }
-    // residual (p - q)+ (:94-112): std::max(0.0f, x) keeps 0 for x <= 0 and for NaN
-    // p[v] - q[v], each product rounded on its own as in the reference's separate loops
-    auto diff = [&](uint32_t j) {
-        const float x = et[j] * inv_p - ed[j] * inv_q;
+    // residual (p - q)+ (:94-112): std::max(0.0f, x) keeps 0 for x <= 0 and for NaN;
+    // p[v] - q[v] with each product rounded on its own, as in the reference's separate loops
+    auto diff1 = [&](float pt, float qd) {
+        const float x = pt * inv_p - qd * inv_q;
         return (0.0f < x) ? x : 0.0f;
     };
-    const float sum_diff = block_seq_sum(diff, V, 0.0f, nullptr, sh);
+    auto diff = [&](uint32_t j) { return diff1(et[j], ed[j]); };
+    auto load_diff = [&](uint32_t j0, auto& v) {
+        constexpr int PER = sizeof(v) / sizeof(float);
+        float w[PER];
+        load_row(et, j0, v);
+        load_row(ed, j0, w);
+#pragma unroll
+        for (int q = 0; q < PER; ++q) v[q] = diff1(v[q], w[q]);
+    };
+    const float sum_diff = block_seq_sum(load_diff, diff, V, 0.0f, 0u, 0.0f, nullptr, true, sh);
     uint32_t corr = 0;
     uint32_t fallback = 0;
     if (sum_diff > 1e-9f) {
         const float r_val = P.u2 * sum_diff;
+        // restart from the last recorded window start whose prefix is still below r_val: the
+        // prefixes never decrease, so the first index reaching r_val lies at or after it
+        uint32_t m = 0;
+        for (uint32_t i = 1; i < sh.n_marks; ++i)
+            if (sh.mark_S[i] < r_val) m = i;
+        const float S0 = sh.mark_S[m];
+        const uint32_t k0 = sh.mark_k0[m];
+        __syncthreads();  // every thread has read the marks
         uint32_t at = V;
-        block_seq_sum(diff, V, r_val, &at, sh);
+        block_seq_sum(load_diff, diff, V, S0, k0, r_val, &at, false, sh);
         corr = at < V ? at : 0u;  // corr_tok starts at 0 (:101)
     } else {
         fallback = 1;  // sample_token on the target row (:114): the selector's token
@@ -431,7 +559,7 @@ __global__ void draft_finish_kernel(const uint32_t* row_tokens, uint32_t rows, c
 
 int draft_scratch_reserve(DraftScratch* d, uint32_t vocab, uint32_t npos) {
     const uint32_t parts = (vocab + kDraftChunk - 1) / kDraftChunk;
-    const size_t need_e = static_cast<size_t>(2) * npos * vocab;
+    const size_t need_e = static_cast<size_t>(2) * npos * ((vocab + 15u) & ~15u);
     if (d->e && d->e_capacity >= need_e && d->part_capacity >= static_cast<size_t>(2) * npos * parts)
         return TWD_OK;
     draft_scratch_free(d);  // grows: later calls with as many positions reuse it
@@ -441,6 +569,7 @@ int draft_scratch_reserve(DraftScratch* d, uint32_t vocab, uint32_t npos) {
     d->part_capacity = static_cast<size_t>(2) * npos * parts;
     TWD_HIP(hipMalloc(&d->flags, 2 * TWD_MAX_ROWS * sizeof(uint32_t)));
     TWD_HIP(hipMalloc(&d->rej, 4 * TWD_MAX_ROWS * sizeof(uint32_t)));
+    TWD_HIP(hipMalloc(&d->sums, 2 * TWD_MAX_ROWS * sizeof(float)));
     return TWD_OK;
 }
 
@@ -449,6 +578,7 @@ void draft_scratch_free(DraftScratch* d) {
     if (d->part) (void)hipFree(d->part);
     if (d->flags) (void)hipFree(d->flags);
     if (d->rej) (void)hipFree(d->rej);
+    if (d->sums) (void)hipFree(d->sums);
     *d = DraftScratch{};
 }
 
@@ -506,6 +636,7 @@ TWD_API int twd_verify_draft(twd_selector* sel, const float* logits, uint32_t vo
 
     if ((rc = draft_scratch_reserve(&sel->draft, vocab, a.npos))) return rc;
     a.vocab = vocab;
+    a.estride = (vocab + 15u) & ~15u;
     a.parts = (vocab + kDraftChunk - 1) / kDraftChunk;
     a.temp = params->temperature <= 0.0f ? 1.0f : params->temperature;
     a.drafts = drafts;
@@ -513,9 +644,11 @@ TWD_API int twd_verify_draft(twd_selector* sel, const float* logits, uint32_t vo
     a.e = sel->draft.e;
     a.flags = sel->draft.flags;
     a.rej = sel->draft.rej;
+    a.sums = sel->draft.sums;
     const dim3 grid(a.parts, 2 * a.npos);
     draft_max_kernel<<<grid, kDraftThreads, 0, s>>>(a);
     draft_exp_kernel<<<grid, kDraftThreads, 0, s>>>(a);
+    draft_sum_kernel<<<2 * a.npos, kRejThreads, 0, s>>>(a);
     draft_reject_kernel<<<a.npos, kRejThreads, 0, s>>>(a);
     draft_finish_kernel<<<1, 64, 0, s>>>(sel->scratch.verify_tokens, used, drafts, n_drafts, has,
                                          a.rej, result);
