@@ -172,6 +172,19 @@ def main():
     log(f"config 2: {rows_s:.1f} rows/s, {step_s * 1e6:.1f} us per launch, "
         f"{bytes2 / step_s / 1e12:.2f} TB/s")
 
+    # the same row entering as the model's fp32 hidden state, with the final RMSNorm (eps 1e-6,
+    # bf16 weight) computed as the head's prologue
+    xr = torch.from_numpy(np.random.default_rng(22).uniform(-2, 2, (64, 1, D)).astype(np.float32)).to(dev)
+    nw = torch.from_numpy(bf16_rne(np.random.default_rng(23).uniform(0.5, 1.5, D).astype(np.float32))
+                          .view(np.int16)).to(dev)
+
+    def step2n(i):
+        head.greedy_rmsnorm(xr[i % 64], nw, tokens=tok, stream=stream)
+
+    nn = max(100, args.steps // 4)
+    r_n = time_loop(torch, nn, args.warmup, step2n)
+    results[2]["rmsnorm_prologue_us_per_row"] = r_n / nn * 1e6
+
     # ---- config 1: selection only over one fp32 row (1 MB): greedy, then T=.8 k=64 p=.95 u=.37 ----
     if 1 in cfgs:
         log("config 1: select on one 1 MB row")

@@ -127,6 +127,27 @@ TWD_API int twd_head_verify_greedy(twd_head* head, const uint16_t* hidden_bf16, 
                                    const uint32_t* drafts, uint32_t n_drafts, float* logits,
                                    twd_verify_result* result, void* stream);
 
+/* ---- the same passes with the final RMSNorm as their prologue --------------------------------
+ * h[m] = x[m] * (1 / sqrt(mean(x[m]^2) + eps)) * norm_weight, the model's last step before the
+ * head (src/runner.cpp:1889-1918, shaders/RMSNormK.hlsl with has_weight = 1, eps = 1e-6 there;
+ * CPU form src/cpu_reference.cpp:141-150), computed inside the head pass: x is fp32 [rows][d]
+ * (16-byte aligned, rows <= 8, the reference's verify batch limit), norm_weight bf16 [d], and h
+ * is carried at fp32 precision (as two bf16 halves) into the head, as the reference's fp32 GEMV
+ * consumes it. Outputs and their meaning as the bf16-h entry points above. */
+TWD_API int twd_head_logits_rmsnorm(twd_head* head, const float* x, const uint16_t* norm_weight,
+                                    float eps, uint32_t rows, float* logits, void* stream);
+TWD_API int twd_head_greedy_rmsnorm(twd_head* head, const float* x, const uint16_t* norm_weight,
+                                    float eps, uint32_t rows, float* logits, uint32_t* tokens,
+                                    void* stream);
+TWD_API int twd_head_verify_greedy_rmsnorm(twd_head* head, const float* x,
+                                           const uint16_t* norm_weight, float eps, uint32_t rows,
+                                           const uint32_t* drafts, uint32_t n_drafts,
+                                           float* logits, twd_verify_result* result, void* stream);
+TWD_API int twd_head_sample_rmsnorm(twd_head* head, const float* x, const uint16_t* norm_weight,
+                                    float eps, uint32_t rows, const twd_row_params* params,
+                                    const uint32_t* history_ids, float* logits, uint32_t* tokens,
+                                    void* stream);
+
 /* ---- selection over caller-owned logits ----------------------------------------------------
  * A selector owns the scratch for up to max_rows rows of up to max_vocab entries. */
 TWD_API int twd_selector_create(uint32_t max_vocab, uint32_t max_rows, twd_selector** out);

@@ -27,6 +27,8 @@
  *   or_verify_draft       rejections and forced fallbacks; golden file; identical draft and
  *                         target rows always accept (r == 1)
  *   or_lm_head(_f64)      numpy float64 dequant + matmul (closed form w = q*s + b)
+ *   or_rmsnorm            closed forms (constant rows, zero rows, unit weight) and numpy
+ *                         float64 within the reference test's 1e-4/1e-3 (test_gpu_kernels.cpp:197)
  *   or_gen_lm_head        numpy restatement of the documented counter formula
  * Parity is unpinned at the libm layer: exp(double) and tanhf are glibc's here, and no
  * reference test fixes their last-ulp behaviour (the reference toolchain is unpinned).
@@ -481,6 +483,16 @@ int or_verify_draft(const uint32_t* drafts, size_t n_drafts, const float* const*
     out->acceptance_rate = out->total_drafted == 0 ? 0.0
                                                    : (double)out->num_accepted / out->total_drafted;
     return OR_OK;
+}
+
+static float bf16_to_f32(uint16_t v);
+
+/* cpu_reference.cpp:141-150 */
+void or_rmsnorm(const float* x, const uint16_t* weight_bf16, uint32_t dim, float eps, float* out) {
+    float sum_sq = 0.0f;
+    for (uint32_t i = 0; i < dim; ++i) sum_sq += x[i] * x[i];
+    const float rms = 1.0f / sqrtf((sum_sq / (float)dim) + eps);
+    for (uint32_t i = 0; i < dim; ++i) out[i] = x[i] * rms * bf16_to_f32(weight_bf16[i]);
 }
 
 static float bf16_to_f32(uint16_t v) {

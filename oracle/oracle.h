@@ -139,6 +139,10 @@ void or_lm_head(const uint32_t* W, const uint16_t* S, const uint16_t* B, const f
  * fp32 loop and the device kernels. */
 void or_lm_head_f64(const uint32_t* W, const uint16_t* S, const uint16_t* B, const float* hidden,
                     uint32_t d, uint32_t group, uint32_t row0, uint32_t nrows, double* out);
+/* The final RMSNorm, cpu_reference.cpp:141-150: sum of squares in index order (fp32),
+ * rms = 1 / sqrt(sum / dim + eps), out = x * rms * weight; the bf16 weight widened to fp32 as
+ * cpu_reference.cpp:614-618 does. */
+void or_rmsnorm(const float* x, const uint16_t* weight_bf16, uint32_t dim, float eps, float* out);
 /* softcap*tanhf(z/softcap) elementwise, identity for softcap <= 0 (Softcap.hlsl:16-30). */
 void or_softcap(float* z, size_t n, float softcap);
 

@@ -104,6 +104,8 @@ def _load():
     lib.or_lm_head_f64.restype = None
     lib.or_lm_head_f64.argtypes = [_u32p, _u16p, _u16p, _f32p, C.c_uint32, C.c_uint32,
                                    C.c_uint32, C.c_uint32, _f64p]
+    lib.or_rmsnorm.restype = None
+    lib.or_rmsnorm.argtypes = [_f32p, _u16p, C.c_uint32, C.c_float, _f32p]
     lib.or_softcap.restype = None
     lib.or_softcap.argtypes = [_f32p, C.c_size_t, C.c_float]
     lib.or_gen_lm_head.restype = None
@@ -296,6 +298,15 @@ def verify_draft(drafts, rows, draft_rows, t=0.8, p=1.0, k=0, rp=1.0, base_seed=
 
 
 # ---- LM head (cpu_reference.cpp:643-665) -----------------------------------------------------
+
+def rmsnorm(x, weight_bf16, eps: float = 1e-6) -> np.ndarray:
+    """The final RMSNorm of cpu_reference.cpp:141-150 on one fp32 row."""
+    xs = _f32(x)
+    w = np.ascontiguousarray(weight_bf16, dtype=np.uint16)
+    out = np.zeros_like(xs)
+    lib().or_rmsnorm(xs, w, xs.size, eps, out)
+    return out
+
 
 def lm_head(W, S, B, hidden, d: int, group: int = 64, row0: int = 0, nrows: int | None = None,
             softcap: float = 0.0) -> np.ndarray:

@@ -5,7 +5,7 @@ token ids are compared bit-exactly with the oracle run on the GPU's own logits."
 import numpy as np
 import pytest
 
-from helpers import allclose_report, bf16_to_f32, hidden_bf16, twd, wsb_bytes
+from helpers import allclose_report, bf16_rne, bf16_to_f32, hidden_bf16, twd, wsb_bytes
 
 pytestmark = pytest.mark.gpu
 
@@ -299,3 +299,91 @@ def test_create_accepts_scale_at_2_100(torch_dev, oracle):
     assert np.isfinite(got).all()
     ratio, err, _ = allclose_report(got, want, 1e-3, 1e-3)
     assert ratio <= 1.0, (ratio, err)
+
+
+# ---- the final RMSNorm as the head's prologue (runner.cpp:1889-1918, RMSNormK.hlsl) ----------
+
+def _norm_inputs(seed, M, d):
+    # the reference kernel test's ranges (test_gpu_kernels.cpp:145-160): x ~ U(-2, 2), the
+    # weight U(-2, 2) * 0.5 + 1 rounded to bf16
+    rng = np.random.default_rng(seed)
+    x = rng.uniform(-2, 2, (M, d)).astype(np.float32)
+    w = bf16_rne(rng.uniform(-2, 2, d).astype(np.float32) * 0.5 + 1.0)
+    return x, w
+
+
+def _norm_oracle(oracle, W, S, B, x, w, cap, rows=None):
+    out = []
+    for m in range(x.shape[0]):
+        h = oracle.rmsnorm(x[m], w, 1e-6)
+        if rows is None:
+            out.append(oracle.lm_head(W, S, B, h, x.shape[1], softcap=cap))
+        else:
+            out.append(np.array([oracle.lm_head(W, S, B, h, x.shape[1], row0=int(r), nrows=1,
+                                                softcap=cap)[0] for r in rows], np.float32))
+    return np.stack(out)
+
+
+@pytest.mark.parametrize("d,M", [(D, 1), (D, 3), (D, 5), (D, 8), (128, 1), (384, 8), (640, 2)])
+def test_rmsnorm_logits_parity(torch_dev, oracle, d, M):
+    torch, dev = torch_dev
+    V = 1000
+    W, S, B = oracle.gen_lm_head(500 + M + d, V, d)
+    head = make_head(torch_dev, W, S, B, V, d, CAP)
+    x, w = _norm_inputs(d + M, M, d)
+    xd = torch.from_numpy(x).to(dev)
+    wd = torch.from_numpy(w.view(np.int16)).to(dev)
+    got = head.logits_rmsnorm(xd, wd).cpu().numpy()
+    want = _norm_oracle(oracle, W, S, B, x, w, CAP)
+    ratio, err, i = allclose_report(got, want, 1e-3, 1e-3)
+    print(f"d={d} M={M} max|err|={err:.3e} worst tolerance ratio {ratio:.3f}")
+    assert ratio <= 1.0
+    # the reference feeds its GEMV the fp32 h; the two-bf16 split keeps that precision: the
+    # device error is far below what rounding h to one bf16 would cost
+    hb = np.stack([bf16_to_f32(bf16_rne(oracle.rmsnorm(x[m], w, 1e-6))) for m in range(M)])
+    one_bf16 = np.stack([oracle.lm_head(W, S, B, hb[m], d, softcap=CAP) for m in range(M)])
+    err_bf16 = float(np.max(np.abs(one_bf16 - want)))
+    print(f"  one-bf16 h would give max|err|={err_bf16:.3e}")
+    assert err < 0.25 * err_bf16
+    tok = head.greedy_rmsnorm(xd, wd).cpu().numpy().astype(np.int64)
+    assert [int(t) for t in tok] == [int(oracle.argmax(got[m])) for m in range(M)]
+
+
+def test_rmsnorm_verify_and_sample(torch_dev, oracle):
+    torch, dev = torch_dev
+    t = twd()
+    V, d, M = 3000, D, 5
+    W, S, B = oracle.gen_lm_head(808, V, d)
+    head = make_head(torch_dev, W, S, B, V, d, CAP)
+    x, w = _norm_inputs(9, M, d)
+    xd = torch.from_numpy(x).to(dev)
+    wd = torch.from_numpy(w.view(np.int16)).to(dev)
+    lg = head.logits_rmsnorm(xd, wd).cpu().numpy()
+    arg = [int(oracle.argmax(lg[m])) for m in range(M)]
+    drafts = torch.tensor([arg[0], arg[1], (arg[2] + 1) % V, arg[3]], dtype=torch.int32, device=dev)
+    res = t.decode_verify(head.verify_greedy_rmsnorm(xd, wd, drafts))
+    assert res["tokens"] == [arg[0], arg[1], arg[2]] and res["num_accepted"] == 2
+    params = [t.RowParams(0.8, 0.9, 40, 1.0, 0.25 + 0.1 * m, CAP, 0, 0) for m in range(M)]
+    tok, lg2 = head.sample_rmsnorm(xd, wd, params)
+    lg2 = lg2.cpu().numpy()
+    assert np.array_equal(lg2, lg)
+    want = [oracle.sample_token(lg2[m], 0.8, 0.9, 40, u=0.25 + 0.1 * m) for m in range(M)]
+    assert [int(v) for v in tok.cpu().numpy()] == want
+
+
+def test_rmsnorm_full_geometry(torch_dev, full_head, oracle):
+    torch, dev = torch_dev
+    head, _ = full_head
+    x, w = _norm_inputs(77, 1, D)
+    xd = torch.from_numpy(x).to(dev)
+    wd = torch.from_numpy(w.view(np.int16)).to(dev)
+    logits = torch.empty(1, V_FULL, dtype=torch.float32, device=dev)
+    tok = int(head.greedy_rmsnorm(xd, wd, logits=logits).cpu().numpy()[0])
+    lg = logits.cpu().numpy()
+    rng = np.random.default_rng(5)
+    sample_rows = np.unique(np.concatenate([rng.integers(0, V_FULL, 64), [tok, 0, V_FULL - 1]]))
+    W, S, B = zip(*[oracle.gen_lm_head(SEED_FULL, 1, D, row0=int(r)) for r in sample_rows])
+    want = _norm_oracle(oracle, np.concatenate(W), np.concatenate(S), np.concatenate(B), x, w, CAP)
+    ratio, err, _ = allclose_report(lg[0, sample_rows], want[0], 1e-3, 1e-3)
+    assert ratio <= 1.0, (ratio, err)
+    assert tok == oracle.argmax(lg[0])

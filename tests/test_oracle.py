@@ -442,6 +442,42 @@ def test_reference_build_verify_draft(oracle, reference):
     assert kinds == {"a", "r", "f"}
 
 
+# ---- final RMSNorm (cpu_reference.cpp:141-150) ----------------------------------------------
+
+def _bf16(x):
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def test_rmsnorm_closed_forms(oracle):
+    d = 5376
+    one = _bf16(np.ones(d, np.float32))
+    # a constant row c: mean square c^2, so every output is c / sqrt(c^2 + eps)
+    for c in (2.0, -0.5, 0.125):  # c * c sums exactly in fp32
+        out = oracle.rmsnorm(np.full(d, c, np.float32), one, 1e-6)
+        want = c / math.sqrt(c * c + 1e-6)
+        assert np.allclose(out, want, rtol=2e-6, atol=0)
+    # a zero row stays zero; the weight scales elementwise
+    assert np.all(oracle.rmsnorm(np.zeros(d, np.float32), one, 1e-6) == 0.0)
+    w = _bf16(np.linspace(-2, 2, d).astype(np.float32))
+    out = oracle.rmsnorm(np.full(d, 3.0, np.float32), w, 0.0)
+    assert np.allclose(out, (w.astype(np.uint32) << 16).view(np.float32), rtol=1e-6, atol=0)
+
+
+def test_rmsnorm_against_float64(oracle):
+    # the reference kernel test's data (test_gpu_kernels.cpp:145-160) and its tolerance
+    rng = np.random.default_rng(6)
+    d = 5376
+    x = rng.uniform(-2, 2, d).astype(np.float32)
+    w = _bf16(rng.uniform(-2, 2, d).astype(np.float32) * 0.5 + 1.0)
+    wf = (w.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    xd = x.astype(np.float64)
+    want = xd / np.sqrt(np.mean(xd * xd) + 1e-6) * wf
+    got = oracle.rmsnorm(x, w, 1e-6)
+    assert np.all(np.abs(got - want) <= 1e-4 + 1e-3 * np.abs(want))
+    assert np.max(np.abs(got - want) / np.abs(want)) < 1e-5
+
+
 # ---- LM head ---------------------------------------------------------------------------------------------
 
 def _dequant_f64(W, S, B, d, group=64):

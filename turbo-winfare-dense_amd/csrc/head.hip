@@ -49,6 +49,9 @@ struct HeadArgs {
     const uint32_t* drafts;
     uint32_t n_drafts;
     twd_verify_result* vres;
+    // 1: MFMA rows 8..15 hold the low halves of rows 0..7 (the fp32 h of the RMSNorm prologue
+    // split into two bf16 parts); the epilogue adds them to their rows first
+    uint32_t fold;
 };
 
 // speculator.cpp:46-69 and :138-150, greedy branch, over per-row target tokens tok[0..rows).
@@ -185,6 +188,12 @@ using EpiShared = EpiSharedT<kHeadWaves>;
 template <int NMT, int NI, int RT, int MODE, int NW>
 __device__ __forceinline__ void head_epilogue(const HeadArgs& a, f32x4_t (&tot)[RT][NMT],
                                               uint32_t tile0, EpiSharedT<NW>& se) {
+    if (NMT == 1 && a.fold) {  // rows r and r + 8 sit in lanes l and l + 32
+#pragma unroll
+        for (int j = 0; j < RT; ++j)
+#pragma unroll
+            for (int i = 0; i < NI; ++i) tot[j][0][i] += __shfl_xor(tot[j][0][i], 32);
+    }
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     uint64_t best[NMT][NI];
 #pragma unroll
@@ -525,6 +534,91 @@ __global__ __launch_bounds__(kHeadThreads) void prep_hidden_kernel(const uint16_
                        (g & 3);
             };
             bias_slices(s, at);  // zero slices for the padding chunk's two groups
+        }
+    }
+}
+
+// The final RMSNorm as the head's prologue (src/runner.cpp:1889-1918, shaders/RMSNormK.hlsl;
+// CPU: src/cpu_reference.cpp:141-150): h[m] = x[m] * (1 / sqrt(mean(x[m]^2) + eps)) * w, fp32
+// x rows, bf16 weight, for rows <= 8. h is fp32, which the bf16 MFMA operands cannot hold, so
+// it is split into h_hi = bf16(h) and h_lo = bf16(h - h_hi) (|h - h_hi - h_lo| <= 2^-18 |h|),
+// placed as MFMA rows m and m + 8 of one 16-row tile; the kernel's epilogue adds row m + 8 to
+// row m (HeadArgs::fold). The bias term uses the group sums of the fp32 h, on rows < 8 only.
+// Every block recomputes the rows' mean squares itself (M x d fp32 from L2), so the prologue
+// needs no launch of its own. Output: the hp / hx layout of prep_hidden_kernel<1>.
+__global__ __launch_bounds__(kHeadThreads) void prep_rmsnorm_kernel(const float* __restrict__ x,
+                                                                    const uint16_t* __restrict__ w,
+                                                                    float eps, uint32_t M, uint32_t d,
+                                                                    u32x4_t* __restrict__ hp,
+                                                                    u32x4_t* __restrict__ hx) {
+    __shared__ float red[kHeadWaves][8];
+    __shared__ float rms[8];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // mean squares: thread t sums the float4 chunks t, t + 256, ... of every row
+    float ss[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        ss[r] = 0.0f;
+        if (static_cast<uint32_t>(r) < M) {
+            const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(r) * d);
+            for (uint32_t q = tid; q < d / 4; q += kHeadThreads) {
+                const float4 v = xr[q];
+                ss[r] += v.x * v.x;
+                ss[r] += v.y * v.y;
+                ss[r] += v.z * v.z;
+                ss[r] += v.w * v.w;
+            }
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss[r] += __shfl_xor(ss[r], o);
+        if (lane == 0) red[wave][r] = ss[r];
+    }
+    __syncthreads();
+    if (tid < 8) {
+        float t = 0.0f;
+        for (int w2 = 0; w2 < kHeadWaves; ++w2) t += red[w2][tid];
+        rms[tid] = 1.0f / sqrtf(t / static_cast<float>(d) + eps);
+    }
+    __syncthreads();
+
+    const uint32_t nunits = d / kChunkK;
+    const uint32_t padded = nunits + (nunits & 1);
+    const uint32_t task = blockIdx.x * kHeadThreads + tid;  // grid covers padded chunks
+    const uint32_t U = task / 256, rem = task % 256;
+    const uint32_t m = rem >> 4, c = rem & 15;
+    const uint32_t row = m & 7, lo_plane = m >> 3;
+    u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
+    float s = 0.0f;
+    if (U < nunits && row < M) {
+        const size_t col = static_cast<size_t>(U) * kChunkK + c * 8;
+        const float4 x0 = *reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * d + col);
+        const float4 x1 = *reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * d + col + 4);
+        const u32x4_t wv = *reinterpret_cast<const u32x4_t*>(w + col);
+        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        const uint32_t ws[4] = {wv.x, wv.y, wv.z, wv.w};
+        const float r = rms[row];
+        uint32_t half[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t wb = (ws[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+            const float he = (xs[e] * r) * __uint_as_float(wb << 16);  // x * rms * weight
+            const uint32_t hi = f32_to_bf16_rne(he);
+            half[e] = lo_plane ? f32_to_bf16_rne(he - __uint_as_float(hi << 16)) : hi;
+            s += he;
+        }
+        v = u32x4_t{half[0] | (half[1] << 16), half[2] | (half[3] << 16), half[4] | (half[5] << 16),
+                    half[6] | (half[7] << 16)};
+        if (lo_plane) s = 0.0f;  // the bias is added once, on the high rows
+    }
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    if (U < padded) {
+        hp[((static_cast<size_t>(U) * 1 + 0) * 4 + (c >> 2)) * 64 + (c & 3) * 16 + m] = prep_h(v);
+        if ((c & 7) == 0) {
+            const uint32_t g = 2 * U + (c >> 3);
+            uint32_t* xo = reinterpret_cast<uint32_t*>(hx);
+            bias_slices(s, [&](int kg) { return xo + ((static_cast<size_t>(g >> 2) * 4 + kg) * 16 + m) * 4 + (g & 3); });
         }
     }
 }
@@ -946,6 +1040,42 @@ int launch_head(twd_head* h, const uint16_t* hidden, uint32_t rows, float* logit
     return TWD_OK;
 }
 
+// The head pass with the final RMSNorm as its prologue: fp32 x rows (rows <= 8) and the bf16
+// norm weight in, the same outputs as launch_head.
+template <int MODE>
+int launch_head_rmsnorm(twd_head* h, const float* x, const uint16_t* norm_w, float eps,
+                        uint32_t rows, float* logits, uint32_t* tokens, const uint32_t* drafts,
+                        uint32_t n_drafts, twd_verify_result* vres, hipStream_t stream) {
+    if (!h) return fail(TWD_E_INVALID, "null head");
+    if (!x || !aligned16(x)) return fail(TWD_E_INVALID, "x must be a 16-byte aligned device pointer");
+    if (!norm_w || !aligned16(norm_w))
+        return fail(TWD_E_INVALID, "norm_weight must be a 16-byte aligned device pointer");
+    if (rows == 0 || rows > 8) return fail(TWD_E_INVALID, "rows must be in 1..8 with the RMSNorm prologue");
+    if (!(eps >= 0.0f) || !std::isfinite(eps)) return fail(TWD_E_INVALID, "eps must be finite and >= 0");
+    HeadArgs a{};
+    a.tiled = h->tiled;
+    a.ntiles = h->ntiles;
+    a.nunits = h->nunits;
+    a.h = nullptr;
+    a.M = rows;
+    a.d = h->d;
+    a.softcap = h->softcap;
+    a.logits = logits;
+    a.vocab = h->vocab;
+    a.gbest = h->gbest;
+    a.gcount = reinterpret_cast<uint32_t*>(h->gbest + TWD_MAX_ROWS);
+    a.tokens = tokens;
+    a.drafts = drafts;
+    a.n_drafts = n_drafts;
+    a.vres = vres;
+    a.fold = 1;
+    prep_rmsnorm_kernel<<<padded_units(h->nunits), kHeadThreads, 0, stream>>>(x, norm_w, eps, rows, h->d,
+                                                                              h->hp, h->hx);
+    head_wide_kernel<1, 4, kRT1, MODE><<<blocks_for(h->ntiles, kRT1), kHeadThreads, 0, stream>>>(a, h->hp, h->hx);
+    TWD_HIP(hipGetLastError());
+    return TWD_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1067,6 +1197,49 @@ TWD_API int twd_head_sample(twd_head* h, const uint16_t* hidden, uint32_t rows,
     if (!logits || !tokens || !params) return fail(TWD_E_INVALID, "null logits, tokens or params");
     const hipStream_t s = static_cast<hipStream_t>(stream);
     int rc = launch_head<kModeLogits>(h, hidden, rows, logits, nullptr, nullptr, 0, nullptr, s);
+    if (rc) return rc;
+    return launch_select(h->sel->scratch, logits, h->vocab, rows, h->vocab, params, history,
+                         tokens, s);
+}
+
+TWD_API int twd_head_logits_rmsnorm(twd_head* h, const float* x, const uint16_t* norm_w, float eps,
+                                    uint32_t rows, float* logits, void* stream) {
+    clear_error();
+    if (!logits) return fail(TWD_E_INVALID, "null logits");
+    return launch_head_rmsnorm<kModeLogits>(h, x, norm_w, eps, rows, logits, nullptr, nullptr, 0,
+                                            nullptr, static_cast<hipStream_t>(stream));
+}
+
+TWD_API int twd_head_greedy_rmsnorm(twd_head* h, const float* x, const uint16_t* norm_w, float eps,
+                                    uint32_t rows, float* logits, uint32_t* tokens, void* stream) {
+    clear_error();
+    if (!tokens) return fail(TWD_E_INVALID, "null tokens");
+    return launch_head_rmsnorm<kModeGreedy>(h, x, norm_w, eps, rows, logits, tokens, nullptr, 0,
+                                            nullptr, static_cast<hipStream_t>(stream));
+}
+
+TWD_API int twd_head_verify_greedy_rmsnorm(twd_head* h, const float* x, const uint16_t* norm_w,
+                                           float eps, uint32_t rows, const uint32_t* drafts,
+                                           uint32_t n_drafts, float* logits,
+                                           twd_verify_result* result, void* stream) {
+    clear_error();
+    if (!result) return fail(TWD_E_INVALID, "null result");
+    if (n_drafts > 0 && !drafts) return fail(TWD_E_INVALID, "null drafts");
+    if (n_drafts > TWD_MAX_ROWS) return fail(TWD_E_INVALID, "n_drafts must be <= 64");
+    return launch_head_rmsnorm<kModeGreedy>(h, x, norm_w, eps, rows, logits, nullptr, drafts, n_drafts,
+                                            result, static_cast<hipStream_t>(stream));
+}
+
+TWD_API int twd_head_sample_rmsnorm(twd_head* h, const float* x, const uint16_t* norm_w, float eps,
+                                    uint32_t rows, const twd_row_params* params,
+                                    const uint32_t* history, float* logits, uint32_t* tokens,
+                                    void* stream) {
+    clear_error();
+    if (!h) return fail(TWD_E_INVALID, "null head");
+    if (!logits || !tokens || !params) return fail(TWD_E_INVALID, "null logits, tokens or params");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    int rc = launch_head_rmsnorm<kModeLogits>(h, x, norm_w, eps, rows, logits, nullptr, nullptr, 0,
+                                              nullptr, s);
     if (rc) return rc;
     return launch_select(h->sel->scratch, logits, h->vocab, rows, h->vocab, params, history,
                          tokens, s);

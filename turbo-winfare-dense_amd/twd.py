@@ -73,6 +73,12 @@ _SIGS = {
     "twd_head_greedy": (C.c_int, [_vp, _vp, _u32, _vp, _vp, _vp]),
     "twd_head_sample": (C.c_int, [_vp, _vp, _u32, C.POINTER(RowParams), _vp, _vp, _vp, _vp]),
     "twd_head_verify_greedy": (C.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _vp]),
+    "twd_head_logits_rmsnorm": (C.c_int, [_vp, _vp, _vp, _f32, _u32, _vp, _vp]),
+    "twd_head_greedy_rmsnorm": (C.c_int, [_vp, _vp, _vp, _f32, _u32, _vp, _vp, _vp]),
+    "twd_head_verify_greedy_rmsnorm": (C.c_int, [_vp, _vp, _vp, _f32, _u32, _vp, _u32, _vp, _vp,
+                                                 _vp]),
+    "twd_head_sample_rmsnorm": (C.c_int, [_vp, _vp, _vp, _f32, _u32, C.POINTER(RowParams), _vp,
+                                          _vp, _vp, _vp]),
     "twd_selector_create": (C.c_int, [_u32, _u32, C.POINTER(_vp)]),
     "twd_selector_destroy": (None, [_vp]),
     "twd_select": (C.c_int, [_vp, _vp, _u32, _u32, _u64, C.POINTER(RowParams), _vp, _vp, _vp]),
@@ -427,3 +433,49 @@ class LMHead:
         _check(lib.twd_head_verify_greedy(self.handle, _ptr(hidden), rows, _ptr(drafts), nd,
                                           _ptr(logits), _ptr(result), _stream(stream)))
         return result
+
+    # ---- with the final RMSNorm as the prologue: x fp32 [rows, d], norm_weight bf16 bits [d] ----
+
+    def logits_rmsnorm(self, x, norm_weight, eps=1e-6, out=None, stream=None):
+        import torch
+        rows = x.shape[0]
+        if out is None:
+            out = torch.empty(rows, self.vocab, dtype=torch.float32, device=x.device)
+        _check(lib.twd_head_logits_rmsnorm(self.handle, _ptr(x), _ptr(norm_weight), eps, rows,
+                                           _ptr(out), _stream(stream)))
+        return out
+
+    def greedy_rmsnorm(self, x, norm_weight, eps=1e-6, logits=None, tokens=None, stream=None):
+        import torch
+        rows = x.shape[0]
+        if tokens is None:
+            tokens = torch.empty(rows, dtype=torch.int32, device=x.device)
+        _check(lib.twd_head_greedy_rmsnorm(self.handle, _ptr(x), _ptr(norm_weight), eps, rows,
+                                           _ptr(logits), _ptr(tokens), _stream(stream)))
+        return tokens
+
+    def verify_greedy_rmsnorm(self, x, norm_weight, drafts, eps=1e-6, logits=None, result=None,
+                              stream=None):
+        import torch
+        rows = x.shape[0]
+        if result is None:
+            result = torch.zeros(VERIFY_WORDS, dtype=torch.int32, device=x.device)
+        nd = 0 if drafts is None else drafts.numel()
+        _check(lib.twd_head_verify_greedy_rmsnorm(self.handle, _ptr(x), _ptr(norm_weight), eps,
+                                                  rows, _ptr(drafts), nd, _ptr(logits),
+                                                  _ptr(result), _stream(stream)))
+        return result
+
+    def sample_rmsnorm(self, x, norm_weight, params: Sequence[RowParams], eps=1e-6, history=None,
+                       logits=None, tokens=None, stream=None):
+        import torch
+        rows = x.shape[0]
+        if logits is None:
+            logits = torch.empty(rows, self.vocab, dtype=torch.float32, device=x.device)
+        if tokens is None:
+            tokens = torch.empty(rows, dtype=torch.int32, device=x.device)
+        arr = _params_array(params)
+        _check(lib.twd_head_sample_rmsnorm(self.handle, _ptr(x), _ptr(norm_weight), eps, rows, arr,
+                                           _ptr(history), _ptr(logits), _ptr(tokens),
+                                           _stream(stream)))
+        return tokens, logits
