@@ -148,6 +148,41 @@ TWD_API int twd_head_sample_rmsnorm(twd_head* head, const float* x, const uint16
                                     const uint32_t* history_ids, float* logits, uint32_t* tokens,
                                     void* stream);
 
+/* ---- the .g4dense container ----------------------------------------------------------------
+ * The fields of the container header (include/g4dense/format.hpp:26-110) this path uses. */
+typedef struct {
+    uint32_t version;
+    uint32_t quant_type;
+    uint32_t num_layers;
+    uint32_t d_model;
+    uint32_t d_ff;
+    uint32_t vocab_size;
+    uint32_t quant_group_size;
+    uint32_t scale_dtype;
+    uint32_t tied_embeddings;
+    float final_logit_softcapping;
+    uint64_t embed_offset;
+    uint64_t embed_size;
+    uint64_t lm_head_offset;
+    uint64_t lm_head_size;
+    uint64_t file_size;
+} twd_container_info;
+
+/* Reads and validates a container's 4096-byte header as validate_header(header, file_size)
+ * does (src/format.cpp:6-65): the same checks, in the same order, with the same messages
+ * (TWD_E_INVALID). Host only. */
+TWD_API int twd_container_inspect(const char* path, twd_container_info* info);
+/* Validates the header, then loads the LM head as the runner does at start-up: the tied head's
+ * [W|S|B] slice at lm_head_offset (src/runner.cpp:423-443, rejected when it exceeds
+ * lm_head_size) with the header's final_logit_softcapping as the softcap, and the final
+ * RMSNorm weight stored after the embedding table (src/runner.cpp:488-497), kept on the head
+ * for the *_rmsnorm entry points (twd_head_norm_weight). The head must be affine INT4 with
+ * 64-wide groups and bf16 scales (TWD_E_UNSUPPORTED otherwise). Synchronous. */
+TWD_API int twd_head_load(const char* path, void* stream, twd_head** out);
+/* Device copy of the final RMSNorm weight (bf16 [d_model]) of a head loaded by twd_head_load,
+ * NULL for heads created from a bare [W|S|B] slice. */
+TWD_API const uint16_t* twd_head_norm_weight(const twd_head* head);
+
 /* ---- selection over caller-owned logits ----------------------------------------------------
  * A selector owns the scratch for up to max_rows rows of up to max_vocab entries. */
 TWD_API int twd_selector_create(uint32_t max_vocab, uint32_t max_rows, twd_selector** out);

@@ -380,6 +380,8 @@ class Reference:
                                                       C.c_float, C.c_int, C.c_float, C.c_uint64,
                                                       _u32p, _u32p, C.POINTER(C.c_double),
                                                       C.c_char_p, C.c_size_t]
+        L.ref_validate_header.restype = C.c_int
+        L.ref_validate_header.argtypes = [C.c_char_p, C.c_uint64, C.c_char_p, C.c_size_t]
         L.ref_evaluate_verification.restype = C.c_int
         L.ref_evaluate_verification.argtypes = [_u32p, C.c_size_t, C.POINTER(C.c_void_p),
                                                 C.c_size_t, C.c_uint32, C.c_float, C.c_float,
@@ -465,3 +467,9 @@ class Reference:
             "bonus_token": int(info[4]),
             "acceptance_rate": float(rate.value),
         }
+
+    def validate_header(self, header: bytes, file_size: int = 0):
+        """None when the reference's validate_header accepts the header, else its message."""
+        buf = C.create_string_buffer(512)
+        rc = self.lib.ref_validate_header(bytes(header), file_size, buf, 512)
+        return None if rc == 0 else buf.value.decode()

@@ -5,6 +5,7 @@
 //
 // TEST INFRASTRUCTURE ONLY. Every function returns 0 on success and a nonzero code when the
 // reference threw (the message is copied into `err` when it is given).
+#include "g4dense/format.hpp"
 #include "g4dense/sampling.hpp"
 #include "g4dense/speculator.hpp"
 
@@ -92,6 +93,19 @@ int ref_evaluate_verification(const uint32_t* drafts, size_t n_drafts, const flo
     } catch (const std::exception& e) {
         copy_err(e, err, err_len);
         return 2;
+    }
+}
+
+// validate_header (src/format.cpp:6-65) on a 4096-byte header image; 0 when accepted.
+int ref_validate_header(const void* header, uint64_t file_size, char* err, size_t err_len) {
+    try {
+        G4DenseHeader h;
+        std::memcpy(&h, header, sizeof(h));
+        validate_header(h, file_size);
+        return 0;
+    } catch (const std::exception& e) {
+        copy_err(e, err, err_len);
+        return 4;
     }
 }
 

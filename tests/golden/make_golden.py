@@ -53,6 +53,40 @@ def draft_case_drafts(seed: int, vocab: int, rows: list, alpha: float, sd: float
     return out
 
 
+# A valid header in the shape of tests/test_format.cpp:33-66 (4 layers of 131072 bytes after a
+# 65536-byte embedding at 4096), and the mutations its tests and validate_header's branches reject.
+HEADER_BASE = dict(magic=0x4734444E, version=3, quant_type=1, num_layers=4, d_model=256, d_ff=512,
+                   num_q_heads=4, num_kv_heads=2, head_dim=64, vocab_size=1024,
+                   sliding_window=512, quant_group_size=64, scale_dtype=1, tied_embeddings=1,
+                   global_layer_mask=(1 << 1) | (1 << 3), final_logit_softcapping=30.0,
+                   embed_offset=4096, embed_size=65536, lm_head_offset=4096, lm_head_size=65536,
+                   layer_offsets=[4096 + 65536 + 131072 * i for i in range(4)],
+                   layer_sizes=[131072] * 4)
+HEADER_END = 4096 + 65536 + 4 * 131072
+
+
+def header_cases():
+    lo = HEADER_BASE["layer_offsets"]
+    ls = HEADER_BASE["layer_sizes"]
+    return [
+        ("valid", {}, HEADER_END),
+        ("valid_no_file_size", {}, 0),
+        ("bad_magic", {"magic": 0xDEADBEEF}, HEADER_END),
+        ("version_2", {"version": 2}, HEADER_END),
+        ("no_layers", {"num_layers": 0}, HEADER_END),
+        ("61_layers", {"num_layers": 61}, HEADER_END),
+        ("zero_d_model", {"d_model": 0}, HEADER_END),
+        ("zero_vocab", {"vocab_size": 0}, HEADER_END),
+        ("embed_unaligned", {"embed_offset": 4097}, HEADER_END),
+        ("lm_head_unaligned", {"lm_head_offset": 8192 + 16}, HEADER_END),
+        ("layer0_unaligned", {"layer_offsets": [4097] + lo[1:]}, HEADER_END),
+        ("layer2_size_0", {"layer_sizes": ls[:2] + [0] + ls[3:]}, HEADER_END),
+        ("past_file_end", {}, HEADER_END - 100),
+        ("overflow", {"layer_offsets": lo[:3] + [2**64 - 4096], "layer_sizes": ls[:3] + [8192]},
+         0),
+    ]
+
+
 def main() -> None:
     R = O.Reference()
     out: dict = {"source": "reference src/sampling.cpp + src/speculator.cpp via oracle/_ref"}
@@ -210,6 +244,16 @@ def main() -> None:
                    "draft_sd": 0.0, "mask": [True, True], "nan_at": nan_at, "drafts": drafts,
                    "t": t, "p": p, "k": k, "rp": 1.0, "base_seed": str(base), "result": res})
     out["verify_draft"] = vd
+
+    # ---- container header validation (src/format.cpp:6-65) -------------------------------------
+    sys.path.insert(0, os.path.join(HERE, ".."))
+    from helpers import container_header
+    hv = []
+    for name, over, fsize in header_cases():
+        hdr = container_header(**{**HEADER_BASE, **over})
+        hv.append({"case": name, "fields": over, "file_size": fsize,
+                   "error": R.validate_header(hdr, fsize)})
+    out["container_headers"] = hv
 
     path = os.path.join(HERE, "sampling_golden.json")
     with open(path, "w") as f:

@@ -882,6 +882,7 @@ struct twd_head {
     u32x4_t* hp = nullptr;        // prepared h in A-fragment order for M > 8 (prep_hidden_kernel)
     u32x4_t* hx = nullptr;        // its bias A-fragment entries
     twd_selector* sel = nullptr;
+    uint16_t* norm_w = nullptr;   // final RMSNorm weight, when loaded from a container
 };
 
 namespace {
@@ -1078,6 +1079,15 @@ int launch_head_rmsnorm(twd_head* h, const float* x, const uint16_t* norm_w, flo
 
 }  // namespace
 
+namespace twd {
+int head_set_norm_weight(twd_head* h, const uint16_t* host_w, uint32_t d) {
+    if (!h || !host_w || d != h->d) return fail(TWD_E_INVALID, "norm weight of the wrong length");
+    if (!h->norm_w) TWD_HIP(hipMalloc(&h->norm_w, static_cast<size_t>(d) * sizeof(uint16_t)));
+    TWD_HIP(hipMemcpy(h->norm_w, host_w, static_cast<size_t>(d) * sizeof(uint16_t), hipMemcpyHostToDevice));
+    return TWD_OK;
+}
+}  // namespace twd
+
 extern "C" {
 
 TWD_API uint64_t twd_head_bytes(uint32_t vocab, uint32_t d_model, uint32_t group_size) {
@@ -1148,8 +1158,11 @@ TWD_API void twd_head_destroy(twd_head* h) {
     if (h->hp) (void)hipFree(h->hp);
     if (h->hx) (void)hipFree(h->hx);
     if (h->sel) twd_selector_destroy(h->sel);
+    if (h->norm_w) (void)hipFree(h->norm_w);
     delete h;
 }
+
+TWD_API const uint16_t* twd_head_norm_weight(const twd_head* h) { return h ? h->norm_w : nullptr; }
 
 TWD_API int twd_head_info(const twd_head* h, uint32_t* vocab, uint32_t* d_model, float* softcap,
                           uint64_t* device_bytes) {

@@ -126,6 +126,8 @@ struct DraftScratch {
 };
 
 int draft_scratch_reserve(DraftScratch* d, uint32_t vocab, uint32_t npos);
+// Gives the head a device copy of the final RMSNorm weight (bf16 [d]), freed with the head.
+int head_set_norm_weight(twd_head* h, const uint16_t* host_w, uint32_t d);
 void draft_scratch_free(DraftScratch* d);
 
 // Enqueues penalty + selection over `rows` rows. `params` is a host array.

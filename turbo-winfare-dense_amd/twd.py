@@ -60,6 +60,16 @@ class VerifyResult(C.Structure):
 
 VERIFY_WORDS = C.sizeof(VerifyResult) // 4
 
+
+class ContainerInfo(C.Structure):
+    """twd_container_info: the .g4dense header fields of this path (format.hpp:26-110)."""
+    _fields_ = [(n, C.c_uint32) for n in ("version", "quant_type", "num_layers", "d_model", "d_ff",
+                                           "vocab_size", "quant_group_size", "scale_dtype",
+                                           "tied_embeddings")] + [
+        ("final_logit_softcapping", C.c_float)] + [
+        (n, C.c_uint64) for n in ("embed_offset", "embed_size", "lm_head_offset", "lm_head_size",
+                                  "file_size")]
+
 _vp, _u32, _u64, _f32, _i32 = C.c_void_p, C.c_uint32, C.c_uint64, C.c_float, C.c_int32
 
 _SIGS = {
@@ -79,6 +89,9 @@ _SIGS = {
                                                  _vp]),
     "twd_head_sample_rmsnorm": (C.c_int, [_vp, _vp, _vp, _f32, _u32, C.POINTER(RowParams), _vp,
                                           _vp, _vp, _vp]),
+    "twd_container_inspect": (C.c_int, [C.c_char_p, C.POINTER(ContainerInfo)]),
+    "twd_head_load": (C.c_int, [C.c_char_p, _vp, C.POINTER(_vp)]),
+    "twd_head_norm_weight": (_vp, [_vp]),
     "twd_selector_create": (C.c_int, [_u32, _u32, C.POINTER(_vp)]),
     "twd_selector_destroy": (None, [_vp]),
     "twd_select": (C.c_int, [_vp, _vp, _u32, _u32, _u64, C.POINTER(RowParams), _vp, _vp, _vp]),
@@ -121,8 +134,8 @@ def _check(rc: int) -> None:
 
 
 def _ptr(t) -> int | None:
-    if t is None:
-        return None
+    if t is None or isinstance(t, int):
+        return t
     return t.data_ptr()
 
 
@@ -362,8 +375,32 @@ def generate_head(buf, vocab: int, d_model: int, seed: int, group: int = 64, str
     return buf
 
 
+def container_info(path: str) -> dict:
+    """The validated header of a .g4dense container (validate_header, format.cpp:6-65)."""
+    info = ContainerInfo()
+    _check(lib.twd_container_inspect(os.fsencode(path), C.byref(info)))
+    return {n: getattr(info, n) for n, _ in ContainerInfo._fields_}
+
+
 class LMHead:
     """The tied INT4 g64 LM head resident in HBM (twd_head)."""
+
+    @classmethod
+    def load(cls, path: str, stream=None) -> "LMHead":
+        """The head of a .g4dense container (runner.cpp:423-443), with its final norm weight."""
+        h = C.c_void_p()
+        _check(lib.twd_head_load(os.fsencode(path), _stream(stream), C.byref(h)))
+        self = cls.__new__(cls)
+        self.handle = h
+        vocab, d, cap, nbytes = _u32(), _u32(), _f32(), _u64()
+        _check(lib.twd_head_info(h, C.byref(vocab), C.byref(d), C.byref(cap), C.byref(nbytes)))
+        self.vocab, self.d_model, self.softcap = vocab.value, d.value, cap.value
+        self.nbytes = head_bytes(self.vocab, self.d_model)
+        return self
+
+    def norm_weight(self) -> int | None:
+        """Device address of the container's final RMSNorm weight (bf16 [d]), or None."""
+        return lib.twd_head_norm_weight(self.handle)
 
     def __init__(self, wsb, vocab: int, d_model: int, softcap: float, group: int = 64,
                  stream=None):
