@@ -183,6 +183,49 @@ TWD_API int twd_head_load(const char* path, void* stream, twd_head** out);
  * NULL for heads created from a bare [W|S|B] slice. */
 TWD_API const uint16_t* twd_head_norm_weight(const twd_head* head);
 
+/* ---- the decode loop around the head -------------------------------------------------------
+ * ForwardRunner::generate's per-step glue (src/runner.cpp:2312-2344) with the history in device
+ * memory: per step, the head pass over the step's hidden state, then apply_repetition_penalty
+ * over the whole history (when repetition_penalty != 1, clamped at the head's softcap), then
+ * sample_token with the draw of seed_for(position = history length - 1), then the token is
+ * appended; the generation finishes after max_tokens or on a stop id. The caller runs the
+ * model between steps. The sampling fields mean what G4DenseGenerationOptions' do
+ * (include/g4dense/c_api.h:24-36). */
+typedef struct {
+    float temperature;
+    float top_p;
+    int32_t top_k;
+    float repetition_penalty;
+    int32_t has_seed;
+    uint64_t seed;
+    uint32_t max_tokens;
+} twd_generation_params;
+
+typedef struct twd_generator twd_generator;
+
+/* `prompt` (host, prompt_len >= 1 ids) starts the history; stop_ids (host) end the generation
+ * when sampled. Allocates the history (prompt_len + max_tokens ids) and one logit row. */
+TWD_API int twd_generator_create(twd_head* head, const twd_generation_params* params,
+                                 const uint32_t* prompt, uint32_t prompt_len,
+                                 const uint32_t* stop_ids, uint32_t n_stop, twd_generator** out);
+TWD_API void twd_generator_destroy(twd_generator* gen);
+/* One step on a bf16 hidden state [d_model]. With token_out or finished given, the token is
+ * brought to the host (4 bytes, the call then waits for the stream) and the stop rules are
+ * applied; a degenerate distribution returns TWD_E_DEGENERATE. Without them the call only
+ * enqueues, and the stop rules see max_tokens alone. */
+TWD_API int twd_generator_step(twd_generator* gen, const uint16_t* hidden_bf16, void* stream,
+                               uint32_t* token_out, int* finished);
+/* The same step with the final RMSNorm as the head's prologue (fp32 x [d_model]). */
+TWD_API int twd_generator_step_rmsnorm(twd_generator* gen, const float* x,
+                                       const uint16_t* norm_weight, float eps, void* stream,
+                                       uint32_t* token_out, int* finished);
+/* The device history (prompt then sampled ids) and its current length. */
+TWD_API int twd_generator_history(const twd_generator* gen, const uint32_t** history_dev,
+                                  uint32_t* len);
+/* The history copied to host memory (at most `capacity` ids); waits for the device. */
+TWD_API int twd_generator_tokens(const twd_generator* gen, uint32_t* host_out, uint32_t capacity,
+                                 uint32_t* len);
+
 /* ---- selection over caller-owned logits ----------------------------------------------------
  * A selector owns the scratch for up to max_rows rows of up to max_vocab entries. */
 TWD_API int twd_selector_create(uint32_t max_vocab, uint32_t max_rows, twd_selector** out);

@@ -387,3 +387,39 @@ def test_rmsnorm_full_geometry(torch_dev, full_head, oracle):
     ratio, err, _ = allclose_report(lg[0, sample_rows], want[0], 1e-3, 1e-3)
     assert ratio <= 1.0, (ratio, err)
     assert tok == oracle.argmax(lg[0])
+
+
+# ---- the decode loop around the head (runner.cpp:2312-2344) --------------------------------
+
+@pytest.mark.parametrize("T,p,k,rp", [(0.0, 1.0, 0, 1.0), (0.0, 1.0, 0, 1.3), (0.8, 0.9, 40, 1.1),
+                                      (1.2, 1.0, 0, 1.0)])
+def test_generator_matches_oracle_loop(torch_dev, oracle, T, p, k, rp):
+    torch, dev = torch_dev
+    t = twd()
+    V, d, steps = 3000, 512, 24
+    W, S, B = oracle.gen_lm_head(900, V, d)
+    head = make_head(torch_dev, W, S, B, V, d, CAP)
+    rng = np.random.default_rng(3)
+    prompt = [int(x) for x in rng.integers(0, V, 40)]
+    sp = t.SamplingParams(T, p, k, rp, True, 4242)
+    stop = [int(x) for x in rng.integers(0, V, 2)]
+    gen = t.Generator(head, sp, prompt, steps, stop_ids=stop)
+    history = list(prompt)
+    hs = hidden_bf16(11, steps, d)
+    for i in range(steps):
+        h = to_dev_bf16(torch_dev, hs[i:i + 1])
+        raw = head.logits(h).cpu().numpy()[0]  # the same kernel: identical raw logits
+        tok, fin = gen.step(h)
+        # the reference's step on those logits
+        pos = len(history) - 1
+        lg = oracle.apply_repetition_penalty(raw, history, rp, CAP) if rp != 1.0 else raw
+        want = oracle.sample_token(lg, T, p, k, seed=oracle.seed_for(True, 4242, pos))
+        assert tok == want, (i, tok, want)
+        history.append(want)
+        if fin:
+            assert want in stop or i == steps - 1
+            break
+    _, n = gen.history()
+    assert n == len(history)
+    assert gen.tokens() == history
+    gen.close()

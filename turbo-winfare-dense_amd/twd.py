@@ -61,6 +61,13 @@ class VerifyResult(C.Structure):
 VERIFY_WORDS = C.sizeof(VerifyResult) // 4
 
 
+class GenerationParams(C.Structure):
+    """twd_generation_params: G4DenseGenerationOptions' sampling fields (c_api.h:24-36)."""
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_int32),
+                ("repetition_penalty", C.c_float), ("has_seed", C.c_int32),
+                ("seed", C.c_uint64), ("max_tokens", C.c_uint32)]
+
+
 class ContainerInfo(C.Structure):
     """twd_container_info: the .g4dense header fields of this path (format.hpp:26-110)."""
     _fields_ = [(n, C.c_uint32) for n in ("version", "quant_type", "num_layers", "d_model", "d_ff",
@@ -92,6 +99,14 @@ _SIGS = {
     "twd_container_inspect": (C.c_int, [C.c_char_p, C.POINTER(ContainerInfo)]),
     "twd_head_load": (C.c_int, [C.c_char_p, _vp, C.POINTER(_vp)]),
     "twd_head_norm_weight": (_vp, [_vp]),
+    "twd_generator_create": (C.c_int, [_vp, C.POINTER(GenerationParams), C.POINTER(_u32), _u32,
+                                       C.POINTER(_u32), _u32, C.POINTER(_vp)]),
+    "twd_generator_destroy": (None, [_vp]),
+    "twd_generator_step": (C.c_int, [_vp, _vp, _vp, C.POINTER(_u32), C.POINTER(C.c_int)]),
+    "twd_generator_step_rmsnorm": (C.c_int, [_vp, _vp, _vp, _f32, _vp, C.POINTER(_u32),
+                                             C.POINTER(C.c_int)]),
+    "twd_generator_history": (C.c_int, [_vp, C.POINTER(_vp), C.POINTER(_u32)]),
+    "twd_generator_tokens": (C.c_int, [_vp, C.POINTER(_u32), _u32, C.POINTER(_u32)]),
     "twd_selector_create": (C.c_int, [_u32, _u32, C.POINTER(_vp)]),
     "twd_selector_destroy": (None, [_vp]),
     "twd_select": (C.c_int, [_vp, _vp, _u32, _u32, _u64, C.POINTER(RowParams), _vp, _vp, _vp]),
@@ -373,6 +388,61 @@ def generate_head(buf, vocab: int, d_model: int, seed: int, group: int = 64, str
     _check(lib.twd_generate_head(_ptr(buf), vocab, d_model, group,
                                  seed & 0xFFFFFFFFFFFFFFFF, _stream(stream)))
     return buf
+
+
+class Generator:
+    """The decode loop around the head (runner.cpp:2312-2344) with a device-resident history."""
+
+    def __init__(self, head: "LMHead", sampling: SamplingParams, prompt, max_tokens: int,
+                 stop_ids=()):
+        p = GenerationParams(sampling.temperature, sampling.top_p, sampling.top_k,
+                             sampling.repetition_penalty, 1 if sampling.has_seed else 0,
+                             sampling.seed & 0xFFFFFFFFFFFFFFFF, max_tokens)
+        pr = (_u32 * max(1, len(prompt)))(*[int(t) for t in prompt])
+        st = (_u32 * max(1, len(stop_ids)))(*[int(t) for t in stop_ids])
+        h = C.c_void_p()
+        _check(lib.twd_generator_create(head.handle, C.byref(p), pr, len(prompt), st,
+                                        len(stop_ids), C.byref(h)))
+        self.handle = h
+        self.head = head
+
+    def close(self):
+        if self.handle:
+            lib.twd_generator_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def step(self, hidden_bf16, stream=None):
+        """One step; returns (token, finished)."""
+        tok, fin = _u32(), C.c_int()
+        _check(lib.twd_generator_step(self.handle, _ptr(hidden_bf16), _stream(stream),
+                                      C.byref(tok), C.byref(fin)))
+        return int(tok.value), bool(fin.value)
+
+    def step_rmsnorm(self, x, norm_weight, eps=1e-6, stream=None):
+        tok, fin = _u32(), C.c_int()
+        _check(lib.twd_generator_step_rmsnorm(self.handle, _ptr(x), _ptr(norm_weight), eps,
+                                              _stream(stream), C.byref(tok), C.byref(fin)))
+        return int(tok.value), bool(fin.value)
+
+    def history(self):
+        """(device address, length) of the history."""
+        ptr, n = _vp(), _u32()
+        _check(lib.twd_generator_history(self.handle, C.byref(ptr), C.byref(n)))
+        return ptr.value, n.value
+
+    def tokens(self) -> list:
+        """The history (prompt, then the sampled ids), copied to the host."""
+        _, n = self.history()
+        buf = (_u32 * max(1, n))()
+        got = _u32()
+        _check(lib.twd_generator_tokens(self.handle, buf, n, C.byref(got)))
+        return [int(buf[i]) for i in range(got.value)]
 
 
 def container_info(path: str) -> dict:
