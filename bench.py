@@ -227,6 +227,24 @@ def main():
         results[3] = {"rows_per_s": n3 / r_s, "ms_per_step": r_s * 1e3 / n3,
                       "hbm_frac": b3 / (r_s / n3) / PEAK_HBM}
 
+        # the same chain through the decode-loop generator: a 4096-id prompt, each sampled id
+        # appended to the device history as runner.cpp:2328 does, no host round trip per step
+        prompt3 = [int(x) for x in rng.integers(0, V, 4096)]
+
+        def gen_run(readback):
+            g = twd.Generator(head, sp, prompt3, n3 + 200)
+            step = (lambda i: g.step(hp3[i % n3], stream=stream)) if readback else (
+                lambda i: twd.twd.lib.twd_generator_step(g.handle, hp3[i % n3].data_ptr(), stream,
+                                                     None, None))
+            r = time_loop(torch, n3, 20, step, min_warm_s=0.0)
+            g.close()
+            return r
+
+        r_g = gen_run(False)
+        r_gr = gen_run(True)
+        results[3]["generator_rows_per_s"] = n3 / r_g
+        results[3]["generator_with_token_readback_rows_per_s"] = n3 / r_gr
+
     # ---- config 4: M=5 greedy verify of 4 drafts ------------------------------------------------
     if 4 in cfgs:
         log("config 4: M=5 verify")
