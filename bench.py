@@ -310,6 +310,19 @@ def main():
                       "head_hbm_frac": (HEAD_BYTES + 64 * D * 2 + 64 * V * 4) / kh / PEAK_HBM,
                       "head_mfma_frac": 2.0 * 64 * V * D / kh / PEAK_BF16}
 
+    # the practical ceiling: a pure-read probe over the same 792 MB buffer (no arithmetic)
+    best = None
+    for waves in (8192, 32768):
+        gbps, us, nb = twd.probe_read_bandwidth(wsb, waves=waves, launches=50, stream=stream)
+        if best is None or gbps > best[0]:
+            best = (gbps, us, nb, waves)
+    ceiling = {"gbps": best[0], "frac_of_peak": best[0] * 1e9 / PEAK_HBM,
+               "kernel_frac_of_ceiling": (bytes2 / step_s) / (best[0] * 1e9),
+               "probe": f"{best[3]} waves streaming {best[2] / best[3] / 1024:.0f} KB stripes, "
+                        f"16 B nt buffer loads, 8 KB in flight per wave"}
+    log(f"read ceiling {best[0]:.0f} GB/s ({ceiling['frac_of_peak'] * 100:.1f}% of peak); "
+        f"the head pass reaches {ceiling['kernel_frac_of_ceiling'] * 100:.1f}% of it")
+
     cpu = None
     if not args.no_cpu_baseline:
         log(f"cpu baseline: scalar LM head, {args.cpu_rows} full rows")
@@ -340,7 +353,8 @@ def main():
                      "unit": "GB/s", "frac": achieved / PEAK_HBM, "traffic": traffic,
                      "traffic_source": traffic_src,
                      "kernel": "head_small_kernel<1,4,2,8,1> (M=1 greedy, single launch)",
-                     "bytes_per_launch": bytes2},
+                     "bytes_per_launch": bytes2,
+                     "read_ceiling": ceiling},
         "cpu_baseline": cpu,
         "configs": {str(k): results[k] for k in sorted(results)},
     }

@@ -283,6 +283,13 @@ TWD_API int twd_validate_sampling(float temperature, float top_p, int32_t top_k,
  * >> 40) / 2^24, S[j] = bf16_rne(fmaf(9e-3, u_j, 1e-3)), B[j] = -8 * S[j]. */
 TWD_API int twd_generate_head(void* wsb_dev, uint32_t vocab, uint32_t d_model,
                               uint32_t group_size, uint64_t seed, void* stream);
+/* A pure-read probe with no counterpart in the reference, for measurement: `waves` (a multiple
+ * of 8) each stream a contiguous stripe of `bytes / waves` bytes (rounded down to 1 KB) of `buf`
+ * with 16-byte non-temporal loads, 8 KB in flight per wave -- the head kernels' access pattern
+ * with no arithmetic. Times `launches` launches after 5 warm-up ones on `stream`. */
+TWD_API int twd_probe_read_bandwidth(const void* buf, uint64_t bytes, uint32_t waves,
+                                     uint32_t launches, void* stream, float* us_per_launch,
+                                     uint64_t* bytes_read);
 /* Bytes of the reference layout for a V x d head with 64-wide groups. */
 TWD_API uint64_t twd_head_bytes(uint32_t vocab, uint32_t d_model, uint32_t group_size);
 

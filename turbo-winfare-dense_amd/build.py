@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libtwd_head.so")
 SOURCES = ["csrc/head.hip", "csrc/select.hip", "csrc/verify.hip", "csrc/host.cpp", "csrc/g4dense_api.cpp",
-           "csrc/container.cpp", "csrc/generator.cpp"]
+           "csrc/container.cpp", "csrc/generator.cpp", "csrc/probe.hip"]
 ARCH = os.environ.get("TWD_OFFLOAD_ARCH", "gfx950")
 
 # Packed-fp32 VALU forms are kept out of the code object: hipcc would otherwise pair fp32 adds

@@ -121,6 +121,8 @@ _SIGS = {
     "twd_validate_sampling": (C.c_int, [_f32, _f32, _i32, _f32]),
     "twd_generate_head": (C.c_int, [_vp, _u32, _u32, _u32, _u64, _vp]),
     "twd_head_bytes": (_u64, [_u32, _u32, _u32]),
+    "twd_probe_read_bandwidth": (C.c_int, [_vp, _u64, _u32, _u32, _vp, C.POINTER(_f32),
+                                           C.POINTER(_u64)]),
 }
 
 
@@ -586,3 +588,11 @@ class LMHead:
                                            _ptr(history), _ptr(logits), _ptr(tokens),
                                            _stream(stream)))
         return tokens, logits
+
+
+def probe_read_bandwidth(buf, waves: int = 32768, launches: int = 50, stream=None):
+    """Pure-read ceiling over a uint8 device tensor: (GB/s, us per launch, bytes per launch)."""
+    us, nbytes = _f32(), _u64()
+    _check(lib.twd_probe_read_bandwidth(_ptr(buf), buf.numel(), waves, launches, _stream(stream),
+                                        C.byref(us), C.byref(nbytes)))
+    return nbytes.value / us.value / 1e3, us.value, nbytes.value
