@@ -352,7 +352,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9,
                      "unit": "GB/s", "frac": achieved / PEAK_HBM, "traffic": traffic,
                      "traffic_source": traffic_src,
-                     "kernel": "head_small_kernel<1,4,2,8,1> (M=1 greedy, single launch)",
+                     "kernel": "head_small_kernel<4,4,2,8,1> (M=1 greedy, single launch)",
                      "bytes_per_launch": bytes2,
                      "read_ceiling": ceiling},
         "cpu_baseline": cpu,

@@ -184,10 +184,13 @@ using EpiShared = EpiSharedT<kHeadWaves>;
 // precede its arrival, and the last block observes all of them. No data travels through plain
 // stores, so no device-scope fence is needed: on this part such a fence writes back the XCD's
 // L2 and, paid by each of ~1000 blocks, costs more than the streaming pass itself.
-// tot[j][mt][i] holds row r = (tile0 + j) * 16 + lane % 16 of m = 16 mt + 4 (lane / 16) + i.
-template <int NMT, int NI, int RT, int MODE, int NW>
+// tot[j][mt][i] holds row r = (tile0 + j) * 16 + lane % 16 of MFMA row 16 mt + 4 (lane / 16) + i,
+// which carries h row m = (16 mt + 4 (lane / 16) + i) / MS when i is a multiple of MS (MS > 1:
+// the rows are spread over the MFMA rows, see head_small_kernel); other entries are not outputs.
+template <int NMT, int NI, int RT, int MODE, int NW, int MS = 1>
 __device__ __forceinline__ void head_epilogue(const HeadArgs& a, f32x4_t (&tot)[RT][NMT],
                                               uint32_t tile0, EpiSharedT<NW>& se) {
+    static_assert(MS == 1 || (NMT == 1 && NI == 4), "spread rows live in one m tile");
     if (NMT == 1 && a.fold) {  // rows r and r + 8 sit in lanes l and l + 32
 #pragma unroll
         for (int j = 0; j < RT; ++j)
@@ -207,8 +210,8 @@ __device__ __forceinline__ void head_epilogue(const HeadArgs& a, f32x4_t (&tot)[
 #pragma unroll
         for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
-            for (int i = 0; i < NI; ++i) {
-                const uint32_t m = mt * 16 + 4 * (lane >> 4) + i;
+            for (int i = 0; i < NI; i += MS) {
+                const uint32_t m = (mt * 16 + 4 * (lane >> 4) + i) / MS;
                 float v = tot[j][mt][i];
                 if (a.softcap > 0.0f) v = a.softcap * tanhf(v / a.softcap);
                 const bool live = (m < a.M) && (r < a.vocab);
@@ -225,14 +228,14 @@ __device__ __forceinline__ void head_epilogue(const HeadArgs& a, f32x4_t (&tot)[
 #pragma unroll
     for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
+        for (int i = 0; i < NI; i += MS) {
             uint64_t k = best[mt][i];
 #pragma unroll
             for (int msk = 1; msk < 16; msk <<= 1) {
                 const uint64_t o = shfl_xor_u64(k, msk);
                 k = o > k ? o : k;
             }
-            const uint32_t m = mt * 16 + 4 * (lane >> 4) + i;
+            const uint32_t m = (mt * 16 + 4 * (lane >> 4) + i) / MS;
             if ((lane & 15) == 0 && m < TWD_MAX_ROWS) se.red[wave][m] = k;
         }
     __syncthreads();
@@ -357,9 +360,16 @@ __host__ __device__ constexpr uint32_t small_pad_units(uint32_t nunits) {
     return (nunits + PF - 1) / PF * PF;
 }
 
-template <int NI, int RT, int PF, int NW, int MODE>
+//
+// MS spreads the rows over the MFMA's 16 A rows: h row m sits in A row MS * m, so its outputs
+// land in accumulator entry i = (MS * m) % 4 of the lanes with lane / 16 = MS * m / 4. With
+// MS = 4 (M <= 4) every output is entry 0 and each group costs one scale FMA per accumulator
+// instead of four; MS = 2 (M <= 8) uses entries 0 and 2. A rows that carry no h row read row 0;
+// their outputs are never stored.
+template <int MS, int RT, int PF, int NW, int MODE>
 __global__ __launch_bounds__(NW * 64) void head_small_kernel(HeadArgs a) {
     static_assert(PF % 2 == 0, "the ring holds whole super-units");
+    static_assert(MS == 2 || MS == 4, "rows spread over 16 MFMA rows with stride 2 or 4");
     constexpr int NT = NW * 64;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     __shared__ EpiSharedT<NW> se;
@@ -426,7 +436,8 @@ __global__ __launch_bounds__(NW * 64) void head_small_kernel(HeadArgs a) {
     }
     __syncthreads();
 
-    const uint32_t m_lane = (lane & 15) < a.M ? (lane & 15) : 0u;
+    const uint32_t rho = lane & 15;  // this lane's A row
+    const uint32_t m_lane = (rho % MS == 0 && rho / MS < a.M) ? rho / MS : 0u;
     const u32x4_t* aRow = sH + m_lane * pad_vecs + (lane >> 4);
     const u32x4_t* xRow = sXF + (lane >> 4) * a.M + m_lane;
 
@@ -462,7 +473,7 @@ __global__ __launch_bounds__(NW * 64) void head_small_kernel(HeadArgs a) {
             for (int g = 0; g < 2; ++g) {
                 const float t = bf16_hi(g ? sq[s][j].y : sq[s][j].x);
 #pragma unroll
-                for (int i = 0; i < NI; ++i) tot[j][0][i] = fmaf(t, acc[j][g][i], tot[j][0][i]);
+                for (int i = 0; i < 4; i += MS) tot[j][0][i] = fmaf(t, acc[j][g][i], tot[j][0][i]);
             }
         // the fences in the loads keep each refill inside its step: the scheduler would otherwise
         // sink every refill of the cycle below the last MFMA, leaving no loads in flight while
@@ -495,7 +506,7 @@ __global__ __launch_bounds__(NW * 64) void head_small_kernel(HeadArgs a) {
     cycle(npad - PF, std::false_type{});
 #pragma unroll
     for (int j = 0; j < RT; ++j) tot[j][0] += bacc[j];
-    head_epilogue<1, NI, RT, MODE>(a, tot, tile0, se);
+    head_epilogue<1, 4, RT, MODE, NW, MS>(a, tot, tile0, se);
 }
 
 // ---- 9 <= M <= 64: h prepared once per call, staged through LDS by plain copies -------------------
@@ -890,13 +901,11 @@ namespace {
 // staged-h kernel: row tiles per wave (measured on MI355X: M = 16 -> 4, M = 64 -> 2)
 constexpr int kRT1 = 4;  // M <= 16
 constexpr int kRT4 = 2;  // M <= 64
-// resident-h kernel: row tiles per wave, weight units in flight and waves per block, measured
-// best on MI355X at V = 262144, d = 5376. Each choice leaves 16 waves resident per CU and the
-// grid an exact number of rounds of resident blocks on 256 CUs. M = 1: 512 blocks of 8 waves.
-// 2 <= M <= 8: 8 waves per block while two blocks' h fit in LDS, else 16 waves per block, one
-// block per CU; one LDS copy of h then serves 16 waves.
-constexpr int kRTS1 = 4, kPFS1 = 2, kNWS1 = 8;  // M == 1
-constexpr int kRTS4 = 2, kPFS4 = 4;            // 2 <= M <= 8
+// resident-h kernel: row tiles per wave and weight units in flight, measured best on MI355X at
+// V = 262144, d = 5376: 4096 waves, 16 resident per CU, one round on 256 CUs. M <= 4: 512 blocks
+// of 8 waves, two per CU. 5 <= M <= 8: 256 blocks of 16 waves, one per CU (one LDS copy of h
+// serves 16 waves; M = 8 leaves no room for a second block's h anyway).
+constexpr int kRTS = 4, kPFS = 2;
 constexpr int kNWS4 = 8, kNWS8 = 16;
 constexpr size_t kLdsBytes = 160 * 1024;
 constexpr uint32_t kSmallMaxRows = 8;
@@ -934,17 +943,15 @@ hipError_t allow_smem(K kernel, size_t bytes) {
 
 // Lets every resident-h instantiation use the LDS it needs for kSmallMaxRows rows of d.
 int enable_small_kernels(uint32_t d) {
-    const size_t bytes1 = small_smem_bytes<kPFS1>(1, d);
-    const size_t bytes4 = small_smem_bytes<kPFS4>(kSmallMaxRows, d);
-    if (bytes1 + sizeof(EpiSharedT<kNWS1>) > kLdsBytes || bytes4 + sizeof(EpiSharedT<kNWS8>) > kLdsBytes)
+    const size_t bytes4 = small_smem_bytes<kPFS>(4, d);
+    const size_t bytes8 = small_smem_bytes<kPFS>(kSmallMaxRows, d);
+    if (bytes4 + sizeof(EpiSharedT<kNWS4>) > kLdsBytes || bytes8 + sizeof(EpiSharedT<kNWS8>) > kLdsBytes)
         return fail(TWD_E_UNSUPPORTED, "d_model too large for the LDS-resident head");
     hipError_t e = hipSuccess;
-    if (e == hipSuccess) e = allow_smem(head_small_kernel<1, kRTS1, kPFS1, kNWS1, kModeLogits>, bytes1);
-    if (e == hipSuccess) e = allow_smem(head_small_kernel<1, kRTS1, kPFS1, kNWS1, kModeGreedy>, bytes1);
-    if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS4, kPFS4, kNWS4, kModeLogits>, bytes4);
-    if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS4, kPFS4, kNWS4, kModeGreedy>, bytes4);
-    if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS4, kPFS4, kNWS8, kModeLogits>, bytes4);
-    if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS4, kPFS4, kNWS8, kModeGreedy>, bytes4);
+    if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS, kPFS, kNWS4, kModeLogits>, bytes4);
+    if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS, kPFS, kNWS4, kModeGreedy>, bytes4);
+    if (e == hipSuccess) e = allow_smem(head_small_kernel<2, kRTS, kPFS, kNWS8, kModeLogits>, bytes8);
+    if (e == hipSuccess) e = allow_smem(head_small_kernel<2, kRTS, kPFS, kNWS8, kModeGreedy>, bytes8);
     if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
     return TWD_OK;
 }
@@ -1015,17 +1022,12 @@ int launch_head(twd_head* h, const uint16_t* hidden, uint32_t rows, float* logit
     a.drafts = drafts;
     a.n_drafts = n_drafts;
     a.vres = vres;
-    if (rows == 1) {
-        head_small_kernel<1, kRTS1, kPFS1, kNWS1, MODE><<<blocks_for(h->ntiles, kRTS1, kNWS1), kNWS1 * 64,
-                                                   small_smem_bytes<kPFS1>(rows, h->d), stream>>>(a);
+    if (rows <= 4) {
+        head_small_kernel<4, kRTS, kPFS, kNWS4, MODE><<<blocks_for(h->ntiles, kRTS, kNWS4), kNWS4 * 64,
+                                                      small_smem_bytes<kPFS>(rows, h->d), stream>>>(a);
     } else if (rows <= kSmallMaxRows) {
-        const size_t bytes = small_smem_bytes<kPFS4>(rows, h->d);
-        if (2 * (bytes + sizeof(EpiSharedT<kNWS4>)) <= kLdsBytes)
-            head_small_kernel<4, kRTS4, kPFS4, kNWS4, MODE>
-                <<<blocks_for(h->ntiles, kRTS4, kNWS4), kNWS4 * 64, bytes, stream>>>(a);
-        else
-            head_small_kernel<4, kRTS4, kPFS4, kNWS8, MODE>
-                <<<blocks_for(h->ntiles, kRTS4, kNWS8), kNWS8 * 64, bytes, stream>>>(a);
+        head_small_kernel<2, kRTS, kPFS, kNWS8, MODE><<<blocks_for(h->ntiles, kRTS, kNWS8), kNWS8 * 64,
+                                                      small_smem_bytes<kPFS>(rows, h->d), stream>>>(a);
     } else if (rows <= 16) {
         prep_hidden_kernel<1><<<padded_units(h->nunits) * 1, kHeadThreads, 0, stream>>>(hidden, rows, h->d,
                                                                                        h->hp, h->hx);
