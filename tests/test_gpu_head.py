@@ -339,12 +339,14 @@ def test_rmsnorm_logits_parity(torch_dev, oracle, d, M):
     print(f"d={d} M={M} max|err|={err:.3e} worst tolerance ratio {ratio:.3f}")
     assert ratio <= 1.0
     # the reference feeds its GEMV the fp32 h; the two-bf16 split keeps that precision: the
-    # device error is far below what rounding h to one bf16 would cost
+    # device error is far below what rounding h to one bf16 would cost. Measured 0.008 of it at
+    # most; a bias term built from the group sums of h rather than of hi + lo leaves the 2^-18
+    # split gap multiplied by 128 s and read 0.014-0.035 here (5 of these 7 cases fail).
     hb = np.stack([bf16_to_f32(bf16_rne(oracle.rmsnorm(x[m], w, 1e-6))) for m in range(M)])
     one_bf16 = np.stack([oracle.lm_head(W, S, B, hb[m], d, softcap=CAP) for m in range(M)])
     err_bf16 = float(np.max(np.abs(one_bf16 - want)))
     print(f"  one-bf16 h would give max|err|={err_bf16:.3e}")
-    assert err < 0.25 * err_bf16
+    assert err < 0.015 * err_bf16
     tok = head.greedy_rmsnorm(xd, wd).cpu().numpy().astype(np.int64)
     assert [int(t) for t in tok] == [int(oracle.argmax(got[m])) for m in range(M)]
 

@@ -52,6 +52,10 @@ struct HeadArgs {
     // 1: MFMA rows 8..15 hold the low halves of rows 0..7 (the fp32 h of the RMSNorm prologue
     // split into two bf16 parts); the epilogue adds them to their rows first
     uint32_t fold;
+    // the RMSNorm prologue of the resident-h kernel: fp32 rows x [M][d], bf16 weight [d]
+    const float* x;
+    const uint16_t* norm_w;
+    float eps;
 };
 
 // speculator.cpp:46-69 and :138-150, greedy branch, over per-row target tokens tok[0..rows).
@@ -366,10 +370,17 @@ __host__ __device__ constexpr uint32_t small_pad_units(uint32_t nunits) {
 // MS = 4 (M <= 4) every output is entry 0 and each group costs one scale FMA per accumulator
 // instead of four; MS = 2 (M <= 8) uses entries 0 and 2. A rows that carry no h row read row 0;
 // their outputs are never stored.
-template <int MS, int RT, int PF, int NW, int MODE>
+//
+// NORM: the final RMSNorm as the prologue (M <= 4). Each block computes the rows' mean squares
+// itself and stages h = (x * rms) * w, which is fp32, as two bf16 halves hi = bf16(h) and
+// lo = bf16(h - hi) (|h - hi - lo| <= 2^-18 |h|) in LDS rows 2m and 2m + 1, fed as A rows 4m
+// and 4m + 1; their outputs, entries 0 and 1 of one lane, are added before the softcap. The
+// bias term uses the group sums of hi + lo (what the MFMA rows carry), on the hi rows only.
+template <int MS, int RT, int PF, int NW, int MODE, bool NORM = false>
 __global__ __launch_bounds__(NW * 64) void head_small_kernel(HeadArgs a) {
     static_assert(PF % 2 == 0, "the ring holds whole super-units");
     static_assert(MS == 2 || MS == 4, "rows spread over 16 MFMA rows with stride 2 or 4");
+    static_assert(!NORM || MS == 4, "the RMSNorm prologue takes two MFMA rows per h row");
     constexpr int NT = NW * 64;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     __shared__ EpiSharedT<NW> se;
@@ -377,7 +388,8 @@ __global__ __launch_bounds__(NW * 64) void head_small_kernel(HeadArgs a) {
     const uint32_t row_vecs = a.d / 8;  // 16 B vectors per h row
     const uint32_t npad = small_pad_units<PF>(a.nunits);
     const uint32_t pad_vecs = npad * 16;  // 16 B vectors per padded LDS row
-    u32x4_t* sXF = sH + a.M * pad_vecs;   // [super-units][4][M]
+    const uint32_t lrows = NORM ? 2 * a.M : a.M;  // LDS rows of prepared h
+    u32x4_t* sXF = sH + lrows * pad_vecs;          // [super-units][4][lrows]
     const int tid = threadIdx.x, lane = tid & 63;
     const uint32_t tile0 = (blockIdx.x * NW + wave_id()) * RT;
     const uint32_t magic = vgpr_const(0x43004300u);
@@ -405,6 +417,79 @@ __global__ __launch_bounds__(NW * 64) void head_small_kernel(HeadArgs a) {
     // kBatch * NT vectors.
     constexpr int kBatch = 4;
     const uint32_t tasks = a.M * pad_vecs;
+    // NORM: the per-row scale 1 / sqrt(mean(x^2) + eps) is common to every term of a row's
+    // logit, so h' = x * w is staged and the sum is scaled once in the epilogue; the mean
+    // squares are gathered from the same loads (partial sums per wave in ss_red).
+    __shared__ float ss_red[NORM ? NW : 1][4];
+    if constexpr (NORM) {
+        // row by row, so each thread's square sum belongs to one row; one vector per thread in
+        // flight (its temporaries share the registers with the filled weight ring: two would
+        // cost a wave per SIMD)
+        constexpr int kBatchN = 1;
+        uint32_t* xo = reinterpret_cast<uint32_t*>(sXF);
+        for (uint32_t m = 0; m < a.M; ++m) {
+            const float* xrow = a.x + static_cast<size_t>(m) * a.d;
+            float ssm = 0.0f;
+            for (uint32_t base = 0; base < pad_vecs; base += NT * kBatchN) {
+                float4 x0[kBatchN], x1[kBatchN];
+                u32x4_t wv[kBatchN];
+#pragma unroll
+                for (int b = 0; b < kBatchN; ++b) {
+                    const uint32_t c8 = base + b * NT + tid;
+                    x0[b] = x1[b] = float4{0.f, 0.f, 0.f, 0.f};
+                    wv[b] = u32x4_t{0u, 0u, 0u, 0u};
+                    if (c8 < row_vecs) {
+                        x0[b] = *reinterpret_cast<const float4*>(xrow + c8 * 8);
+                        x1[b] = *reinterpret_cast<const float4*>(xrow + c8 * 8 + 4);
+                        wv[b] = *reinterpret_cast<const u32x4_t*>(a.norm_w + c8 * 8);
+                    }
+                }
+#pragma unroll
+                for (int b = 0; b < kBatchN; ++b) {
+                    const uint32_t c8 = base + b * NT + tid;
+                    const float xs[8] = {x0[b].x, x0[b].y, x0[b].z, x0[b].w, x1[b].x, x1[b].y, x1[b].z, x1[b].w};
+                    const uint32_t ws[4] = {wv[b].x, wv[b].y, wv[b].z, wv[b].w};
+                    uint32_t hi[8], lo[8];
+                    float sum = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const uint32_t wb = (ws[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+                        const float he = xs[e] * __uint_as_float(wb << 16);  // x * weight
+                        hi[e] = f32_to_bf16_rne(he);
+                        lo[e] = f32_to_bf16_rne(he - __uint_as_float(hi[e] << 16));
+                        // the sum of what the MFMA rows carry (hi + lo, exact in fp32), so that
+                        // the bias term cancels their 128 X exactly
+                        sum += __uint_as_float(hi[e] << 16) + __uint_as_float(lo[e] << 16);
+                        ssm += xs[e] * xs[e];
+                    }
+                    sum += __shfl_xor(sum, 1);
+                    sum += __shfl_xor(sum, 2);
+                    sum += __shfl_xor(sum, 4);
+                    if (c8 < pad_vecs) {
+                        const uint32_t U = c8 >> 4, c = c8 & 15;
+                        const u32x4_t vh = u32x4_t{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16),
+                                                   hi[4] | (hi[5] << 16), hi[6] | (hi[7] << 16)};
+                        const u32x4_t vl = u32x4_t{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16),
+                                                   lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16)};
+                        sH[(((2 * m) * npad + U) * 4 + (c >> 2)) * 4 + (c & 3)] = prep_h(vh);
+                        sH[(((2 * m + 1) * npad + U) * 4 + (c >> 2)) * 4 + (c & 3)] = prep_h(vl);
+                        if ((c8 & 7) == 0) {
+                            const uint32_t g = c8 >> 3;
+                            bias_slices(sum, [&](int kg) {
+                                return xo + (((g >> 2) * 4 + kg) * lrows + 2 * m) * 4 + (g & 3);
+                            });
+                            bias_slices(0.0f, [&](int kg) {
+                                return xo + (((g >> 2) * 4 + kg) * lrows + 2 * m + 1) * 4 + (g & 3);
+                            });
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) ssm += __shfl_xor(ssm, o);
+            if (lane == 0) ss_red[tid >> 6][m] = ssm;
+        }
+    } else
     for (uint32_t base = 0; base < tasks; base += NT * kBatch) {
         u32x4_t v[kBatch];
 #pragma unroll
@@ -436,10 +521,13 @@ __global__ __launch_bounds__(NW * 64) void head_small_kernel(HeadArgs a) {
     }
     __syncthreads();
 
-    const uint32_t rho = lane & 15;  // this lane's A row
-    const uint32_t m_lane = (rho % MS == 0 && rho / MS < a.M) ? rho / MS : 0u;
-    const u32x4_t* aRow = sH + m_lane * pad_vecs + (lane >> 4);
-    const u32x4_t* xRow = sXF + (lane >> 4) * a.M + m_lane;
+    // this lane's A row rho: h row rho / MS when rho % MS is 0 (NORM: its hi half, and its lo
+    // half when rho % MS is 1); any other A row reads LDS row 0
+    const uint32_t rho = lane & 15, part = rho % MS, m_of = rho / MS;
+    const uint32_t lrow = NORM ? ((part < 2 && m_of < a.M) ? 2 * m_of + part : 0u)
+                               : ((part == 0 && m_of < a.M) ? m_of : 0u);
+    const u32x4_t* aRow = sH + lrow * pad_vecs + (lane >> 4);
+    const u32x4_t* xRow = sXF + (lane >> 4) * lrows + lrow;
 
     f32x4_t tot[RT][1], bacc[RT];
 #pragma unroll
@@ -473,7 +561,8 @@ __global__ __launch_bounds__(NW * 64) void head_small_kernel(HeadArgs a) {
             for (int g = 0; g < 2; ++g) {
                 const float t = bf16_hi(g ? sq[s][j].y : sq[s][j].x);
 #pragma unroll
-                for (int i = 0; i < 4; i += MS) tot[j][0][i] = fmaf(t, acc[j][g][i], tot[j][0][i]);
+                for (int i = 0; i < 4; ++i)
+                    if (i % MS == 0 || (NORM && i % MS == 1)) tot[j][0][i] = fmaf(t, acc[j][g][i], tot[j][0][i]);
             }
         // the fences in the loads keep each refill inside its step: the scheduler would otherwise
         // sink every refill of the cycle below the last MFMA, leaving no loads in flight while
@@ -484,7 +573,7 @@ __global__ __launch_bounds__(NW * 64) void head_small_kernel(HeadArgs a) {
             if constexpr (kReload) load_nibbles_ordered<RT>(rs, Un, vo_w, wq[s]);
         } else {
             // {b, t} words of the super-unit's four groups: the bias B fragment
-            const bf16x8_t xa = __builtin_bit_cast(bf16x8_t, xRow[(U >> 1) * 4 * a.M]);
+            const bf16x8_t xa = __builtin_bit_cast(bf16x8_t, xRow[(U >> 1) * 4 * lrows]);
 #pragma unroll
             for (int j = 0; j < RT; ++j) {
                 const u32x4_t bp = u32x4_t{sq[s - 1][j].x, sq[s - 1][j].y, sq[s][j].x, sq[s][j].y};
@@ -506,6 +595,15 @@ __global__ __launch_bounds__(NW * 64) void head_small_kernel(HeadArgs a) {
     cycle(npad - PF, std::false_type{});
 #pragma unroll
     for (int j = 0; j < RT; ++j) tot[j][0] += bacc[j];
+    if constexpr (NORM) {
+        // row lane / 16: the two halves' sums, times the row's 1 / sqrt(mean(x^2) + eps)
+        const uint32_t m = (lane >> 4) < a.M ? (lane >> 4) : 0u;
+        float t = 0.0f;
+        for (int w2 = 0; w2 < NW; ++w2) t += ss_red[w2][m];
+        const float rms = 1.0f / sqrtf(t / static_cast<float>(a.d) + a.eps);
+#pragma unroll
+        for (int j = 0; j < RT; ++j) tot[j][0][0] = (tot[j][0][0] + tot[j][0][1]) * rms;
+    }
     head_epilogue<1, 4, RT, MODE, NW, MS>(a, tot, tile0, se);
 }
 
@@ -554,7 +652,7 @@ __global__ __launch_bounds__(kHeadThreads) void prep_hidden_kernel(const uint16_
 // x rows, bf16 weight, for rows <= 8. h is fp32, which the bf16 MFMA operands cannot hold, so
 // it is split into h_hi = bf16(h) and h_lo = bf16(h - h_hi) (|h - h_hi - h_lo| <= 2^-18 |h|),
 // placed as MFMA rows m and m + 8 of one 16-row tile; the kernel's epilogue adds row m + 8 to
-// row m (HeadArgs::fold). The bias term uses the group sums of the fp32 h, on rows < 8 only.
+// row m (HeadArgs::fold). The bias term uses the group sums of hi + lo, on rows < 8 only.
 // Every block recomputes the rows' mean squares itself (M x d fp32 from L2), so the prologue
 // needs no launch of its own. Output: the hp / hx layout of prep_hidden_kernel<1>.
 __global__ __launch_bounds__(kHeadThreads) void prep_rmsnorm_kernel(const float* __restrict__ x,
@@ -614,8 +712,12 @@ __global__ __launch_bounds__(kHeadThreads) void prep_rmsnorm_kernel(const float*
             const uint32_t wb = (ws[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
             const float he = (xs[e] * r) * __uint_as_float(wb << 16);  // x * rms * weight
             const uint32_t hi = f32_to_bf16_rne(he);
-            half[e] = lo_plane ? f32_to_bf16_rne(he - __uint_as_float(hi << 16)) : hi;
-            s += he;
+            const uint32_t lo = f32_to_bf16_rne(he - __uint_as_float(hi << 16));
+            half[e] = lo_plane ? lo : hi;
+            // the group sum of what the MFMA rows carry, hi + lo (exact in fp32): the bias
+            // term's X must cancel the MFMA's 128 X to the last bit, or the 2^-18 gap between
+            // h and hi + lo comes back multiplied by 128 s
+            s += __uint_as_float(hi << 16) + __uint_as_float(lo << 16);
         }
         v = u32x4_t{half[0] | (half[1] << 16), half[2] | (half[3] << 16), half[4] | (half[5] << 16),
                     half[6] | (half[7] << 16)};
@@ -952,6 +1054,11 @@ int enable_small_kernels(uint32_t d) {
     if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS, kPFS, kNWS4, kModeGreedy>, bytes4);
     if (e == hipSuccess) e = allow_smem(head_small_kernel<2, kRTS, kPFS, kNWS8, kModeLogits>, bytes8);
     if (e == hipSuccess) e = allow_smem(head_small_kernel<2, kRTS, kPFS, kNWS8, kModeGreedy>, bytes8);
+    // the RMSNorm prologue variant: two LDS rows per h row, M <= 4
+    if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS, kPFS, kNWS4, kModeLogits, true>, bytes8);
+    if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS, kPFS, kNWS4, kModeGreedy, true>, bytes8);
+    if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS, kPFS, kNWS8, kModeLogits, true>, bytes8);
+    if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS, kPFS, kNWS8, kModeGreedy, true>, bytes8);
     if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
     return TWD_OK;
 }
@@ -1071,6 +1178,21 @@ int launch_head_rmsnorm(twd_head* h, const float* x, const uint16_t* norm_w, flo
     a.drafts = drafts;
     a.n_drafts = n_drafts;
     a.vres = vres;
+    if (rows <= 4) {
+        // the resident-h kernel stages the normalised rows itself, two LDS rows each
+        a.x = x;
+        a.norm_w = norm_w;
+        a.eps = eps;
+        const size_t bytes = small_smem_bytes<kPFS>(2 * rows, h->d);
+        if (2 * (bytes + sizeof(EpiSharedT<kNWS4>)) <= kLdsBytes)
+            head_small_kernel<4, kRTS, kPFS, kNWS4, MODE, true>
+                <<<blocks_for(h->ntiles, kRTS, kNWS4), kNWS4 * 64, bytes, stream>>>(a);
+        else
+            head_small_kernel<4, kRTS, kPFS, kNWS8, MODE, true>
+                <<<blocks_for(h->ntiles, kRTS, kNWS8), kNWS8 * 64, bytes, stream>>>(a);
+        TWD_HIP(hipGetLastError());
+        return TWD_OK;
+    }
     a.fold = 1;
     prep_rmsnorm_kernel<<<padded_units(h->nunits), kHeadThreads, 0, stream>>>(x, norm_w, eps, rows, h->d,
                                                                               h->hp, h->hx);
