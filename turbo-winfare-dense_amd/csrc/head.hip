@@ -280,6 +280,7 @@ __device__ __forceinline__ void head_epilogue(const HeadArgs& a, f32x4_t (&tot)[
 // wave-uniform) re-read the last tile: their rows are >= vocab and never stored.
 constexpr int kBufferWord3 = 0x00020000;  // descriptor word 3: 32-bit data format
 constexpr int kNonTemporal = 2;           // cache-policy bit of a streaming load
+constexpr int kWaitVm0 = 0x0F70;          // s_waitcnt vmcnt(0), other counters not waited on
 
 template <int RT>
 __device__ __forceinline__ void tile_streams(const HeadArgs& a, uint32_t tile0,
@@ -737,67 +738,78 @@ __global__ __launch_bounds__(kHeadThreads) void prep_rmsnorm_kernel(const float*
 }
 
 // Block = 4 waves; wave w owns RT consecutive 16-row tiles. NMT = number of 16-wide m tiles
-// (1 for M <= 16, 4 for M <= 64); NI = accumulator lanes per m tile that can hold a live row.
-// A stage is one super-unit (two chunks). Each stage: one barrier; the next stage's h loaded
-// into registers and stored to the other LDS buffer at the stage's end; the weights of the
-// stage after next requested into a three-deep register ring (stage S reads buffer S % 3).
-// The loop body has no branch and every ring slot keeps its registers, so the compiler's
-// memory waits stay partial and the ring stays in flight across stages.
-template <int NMT, int NI, int RT, int MODE>
-__global__ __launch_bounds__(kHeadThreads) __attribute__((amdgpu_waves_per_eu(2)))
+// (1 for M <= 16, 4 for M <= 64). A stage is one chunk (two groups). Each stage: one barrier;
+// the next chunk's prepared h copied straight from global memory into the other LDS buffer
+// (for an even chunk also the next super-unit's bias fragment); the weights of the next chunk
+// requested into the other half of a two-deep register ring. One chunk per stage keeps the LDS
+// at 41 KB per block (three blocks per CU at M = 64, VGPR-limited to 154), where two-chunk
+// stages needed 77 KB and two blocks. Measured on MI355X at V = 262144, d = 5376 against the
+// two-chunk register-staged form: M = 64 277.5 -> 249.1 us, M = 16 143.8 -> 136.2 us.
+//
+// Per group step the MFMA chains of all RT x NMT accumulators run first; the scales are
+// applied (tot += t * acc) right after, while the next step's nibbles are converted.
+template <int NMT, int RT, int MODE>
+__global__ __launch_bounds__(kHeadThreads) __attribute__((amdgpu_waves_per_eu(3)))
 void head_wide_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_t* __restrict__ hx) {
     constexpr int kVec = NMT * 4 * 64;  // 16 B A-fragment vectors per chunk
     constexpr int kXA = NMT * 64;       // 16 B bias vectors per super-unit
-    constexpr int kPer = 2 * kVec / kHeadThreads;  // h vectors per thread and stage
-    __shared__ u32x4_t sA[2][2 * kVec];  // [stage parity][chunk of the stage][mt][t][lane]
-    __shared__ u32x4_t sXA[2][kXA];
+    constexpr int kCopies = kVec / 64 / kHeadWaves;  // 1 KB pieces each wave copies per chunk
+    static_assert(kCopies >= 1 && kXA / 64 <= kHeadWaves, "copy split");
+    // two buffers as separate arrays: each LDS read names the buffer it reads
+    __shared__ u32x4_t sA0[kVec], sA1[kVec];  // [mt][t][lane] of one chunk
+    __shared__ u32x4_t sXA0[kXA], sXA1[kXA];  // [mt][lane] of one super-unit
     __shared__ EpiShared se;
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
+    const int lane = threadIdx.x & 63;
     const uint32_t wave = wave_id();
     const uint32_t tile0 = (blockIdx.x * kHeadWaves + wave) * RT;
     const uint32_t magic = vgpr_const(0x43004300u);
-    const uint32_t nstages = (a.nunits + 1) / 2;
+    // an odd chunk count ends with hp's zero chunk; its weight loads re-read the last unit
+    const uint32_t nchunks = a.nunits + (a.nunits & 1);
 
     __amdgpu_buffer_rsrc_t rs[RT];
     tile_streams<RT>(a, tile0, rs);
     const uint32_t vo_w = lane * 16, vo_s = kUnitNibbleBytes + (lane & 15) * 8;
 
-    // Stage S's h: loaded into registers at the start of stage S-1, stored to LDS buffer P at
-    // its end; hp and hx hold one stage past the end, so the loads need no branch.
-    u32x4_t hv[kPer];
-    u32x4_t xv_st = u32x4_t{0u, 0u, 0u, 0u};
-    auto stage_load = [&](uint32_t S) {
-        const u32x4_t* src = hp + static_cast<size_t>(S) * 2 * kVec;
-#pragma unroll
-        for (int it = 0; it < kPer; ++it) hv[it] = (src + kHeadThreads * it)[tid];
-        if (tid < kXA) xv_st = hx[static_cast<size_t>(S) * kXA + tid];
+    // 16 B per lane from global memory into LDS at l + 16 * lane (global_load_lds_dwordx4 with
+    // the wave's LDS base in M0). Issued by inline asm, so the compiler neither holds its LDS
+    // reads of the other buffer behind these copies nor counts them: the wait and barrier at
+    // each stage's start cover them. hp and hx hold one chunk and one super-unit past the end,
+    // so the copies need no branch.
+    auto copy16 = [&](const u32x4_t* g, u32x4_t* l) {
+        // the LDS offset of l: an address-space cast, not the low bits of the flat address
+        const uint32_t la = static_cast<uint32_t>(
+            reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) u32x4_t*)l));
+        // M0 is reserved to the compiler, which sets it next to each instruction of its own that
+        // reads it; this kernel has no such instruction, so the value left here is never read
+        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(la), "v"(g) : "memory");
     };
-    auto stage_store = [&](int P) {
+    auto chunk_copy = [&](uint32_t C, auto parity) {
+        constexpr int P = decltype(parity)::value;
+        u32x4_t* dst = P ? sA1 : sA0;
+        const u32x4_t* src = hp + static_cast<size_t>(C) * kVec;
 #pragma unroll
-        for (int it = 0; it < kPer; ++it) sA[P][kHeadThreads * it + tid] = hv[it];
-        if (tid < kXA) sXA[P][tid] = xv_st;
+        for (int it = 0; it < kCopies; ++it) {
+            const uint32_t piece = wave * kCopies + it;
+            copy16(src + piece * 64 + lane, dst + piece * 64);
+        }
+        // chunk C opens super-unit C / 2 when even; its bias buffer is (C / 2) & 1
+        if constexpr (P == 0) {
+            if (wave < static_cast<uint32_t>(kXA / 64))
+                copy16(hx + static_cast<size_t>(C >> 1) * kXA + wave * 64 + lane,
+                       (((C >> 1) & 1) ? sXA1 : sXA0) + wave * 64);
+        }
     };
-    // Stage S's weights into register buffer P: both chunks' nibbles, and the four groups'
-    // {b, t} words side by side, which is also the bias MFMA's B fragment. Chunks past the
-    // end re-read the last one; their h is zero, so they add nothing.
-    constexpr int NB = 3;  // weight buffers: stage S reads buffer S % 3 and requests stage S + 2
-    u32x4_t wr[NB][2][RT];
-    u32x4_t br[NB][RT];
-    auto stage_w = [&](uint32_t S, int P) {
-        const uint32_t U0 = min(2 * S, a.nunits - 1), U1 = min(2 * S + 1, a.nunits - 1);
+    // chunk C's weights into ring slot B: the lane's 16 B of nibbles and its row's two {b, t} words
+    u32x4_t wr[2][RT];
+    u32x2_t sc[2][RT];
+    auto chunk_w = [&](uint32_t C, auto slot) {
+        constexpr int B = decltype(slot)::value;
+        const int so = static_cast<int>(min(C, a.nunits - 1) * kUnitBytes);
 #pragma unroll
         for (int j = 0; j < RT; ++j) {
-            wr[P][0][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                          rs[j], vo_w, static_cast<int>(U0 * kUnitBytes), kNonTemporal));
-            wr[P][1][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                          rs[j], vo_w, static_cast<int>(U1 * kUnitBytes), kNonTemporal));
-            const u32x2_t lo = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
-                                                               rs[j], vo_s, static_cast<int>(U0 * kUnitBytes), kNonTemporal));
-            const u32x2_t hi = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
-                                                               rs[j], vo_s, static_cast<int>(U1 * kUnitBytes), kNonTemporal));
-            br[P][j] = u32x4_t{lo.x, lo.y, hi.x, hi.y};
+            wr[B][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs[j], vo_w, so, kNonTemporal));
+            sc[B][j] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rs[j], vo_s, so, kNonTemporal));
         }
     };
 
@@ -806,106 +818,87 @@ void head_wide_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_t*
     for (int j = 0; j < RT; ++j)
 #pragma unroll
         for (int mt = 0; mt < NMT; ++mt) tot[j][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    bf16x8_t bq[2][RT][2];  // converted nibbles of the current and the next group step
+    u32x2_t sc_even[RT];    // the even chunk's {b, t} words, for the super-unit's bias MFMA
 
-    // Software pipeline over group steps (two per chunk, parity = the group g): while the MFMA
-    // chains of step s run into acc[g], the VALU applies step s-1's scales from acc[g ^ 1]
-    // (tot += t * acc) and converts step s+1's nibbles into bq[g ^ 1].
-    f32x4_t acc[2][RT][NMT];
-    float tp[2][RT];
-    bf16x8_t bq[2][RT][2];
-
-    stage_load(0);
-    stage_store(0);
-    stage_w(0, 0);
-    stage_w(1, 1);
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    chunk_copy(0, I0{});
+    chunk_w(0, I0{});
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
 #pragma unroll
     for (int j = 0; j < RT; ++j) {
-        tp[1][j] = 0.0f;
-#pragma unroll
-        for (int mt = 0; mt < NMT; ++mt) acc[1][j][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        bq[0][j][0] = nibbles_to_bf16(wr[0][0][j].x, magic);
-        bq[0][j][1] = nibbles_to_bf16(wr[0][0][j].y, magic);
+        bq[0][j][0] = nibbles_to_bf16(wr[0][j].x, magic);
+        bq[0][j][1] = nibbles_to_bf16(wr[0][j].y, magic);
     }
 
-    auto stage = [&](uint32_t S, auto which) {
-        constexpr int B = decltype(which)::value;  // weight buffer of stage S
-        constexpr int B1 = (B + 1) % NB, B2 = (B + 2) % NB;
-        const int P = S & 1;                       // LDS buffer of stage S
-        __syncthreads();  // stage S's h is in sA[P]; sA[P ^ 1] is free
-        stage_load(S + 1);
-        stage_w(S + 2, B2);
+    // chunk C in LDS buffer and ring slot P = C & 1
+    auto stage = [&](uint32_t C, auto parity) {
+        constexpr int P = decltype(parity)::value;
+        const u32x4_t* sA = P ? sA1 : sA0;
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this wave's copies of chunk C, its weights
+        __syncthreads();                        // every wave's copies; buffer P ^ 1 is free
+        chunk_copy(C + 1, std::integral_constant<int, P ^ 1>{});
+        chunk_w(C + 1, std::integral_constant<int, P ^ 1>{});
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int g = 0; g < 2; ++g) {
+            bf16x8_t av[NMT][2];
 #pragma unroll
-            for (int g = 0; g < 2; ++g) {
-                bf16x8_t av[NMT][2];
+            for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    av[mt][t] = __builtin_bit_cast(bf16x8_t, sA[(mt * 4 + 2 * g + t) * 64 + lane]);
+            f32x4_t acc[RT][NMT];
+#pragma unroll
+            for (int j = 0; j < RT; ++j)
+#pragma unroll
+                for (int mt = 0; mt < NMT; ++mt) {
+                    acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt][0], bq[g][j][0],
+                                                                         f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt][1], bq[g][j][1], acc[j][mt], 0, 0, 0);
+                }
+            // the next step's nibbles: this chunk's second group, or the next chunk's first
+#pragma unroll
+            for (int j = 0; j < RT; ++j) {
+                const u32x4_t& nx = (g == 0) ? wr[P][j] : wr[P ^ 1][j];
+                bq[g ^ 1][j][0] = nibbles_to_bf16(g == 0 ? nx.z : nx.x, magic);
+                bq[g ^ 1][j][1] = nibbles_to_bf16(g == 0 ? nx.w : nx.y, magic);
+            }
+#pragma unroll
+            for (int j = 0; j < RT; ++j) {
+                const float t = bf16_hi(g == 0 ? sc[P][j].x : sc[P][j].y);
 #pragma unroll
                 for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
-                    for (int t = 0; t < 2; ++t)
-                        av[mt][t] = __builtin_bit_cast(bf16x8_t, sA[P][u * kVec + (mt * 4 + 2 * g + t) * 64 + lane]);
-#pragma unroll
-                for (int j = 0; j < RT; ++j)
-#pragma unroll
-                    for (int mt = 0; mt < NMT; ++mt) {
-                        acc[g][j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            av[mt][0], bq[g][j][0], f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                        acc[g][j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt][1], bq[g][j][1],
-                                                                                acc[g][j][mt], 0, 0, 0);
-                    }
-#pragma unroll
-                for (int j = 0; j < RT; ++j)
-#pragma unroll
-                    for (int mt = 0; mt < NMT; ++mt)
-#pragma unroll
-                        for (int i = 0; i < NI; ++i)
-                            tot[j][mt][i] = fmaf(tp[g ^ 1][j], acc[g ^ 1][j][mt][i], tot[j][mt][i]);
-                // the next step's nibbles: this chunk's second group, the next chunk, or the
-                // next stage's first chunk (buffer P ^ 1, requested at this stage's start)
-#pragma unroll
-                for (int j = 0; j < RT; ++j) {
-                    const u32x4_t& nx = (g == 0) ? wr[B][u][j] : (u == 0 ? wr[B][1][j] : wr[B1][0][j]);
-                    bq[g ^ 1][j][0] = nibbles_to_bf16(g == 0 ? nx.z : nx.x, magic);
-                    bq[g ^ 1][j][1] = nibbles_to_bf16(g == 0 ? nx.w : nx.y, magic);
-                    const uint32_t bt = (u == 0) ? (g == 0 ? br[B][j].x : br[B][j].y)
-                                                 : (g == 0 ? br[B][j].z : br[B][j].w);
-                    tp[g][j] = bf16_hi(bt);
-                }
-#pragma unroll
-                for (int k = 0; k < RT * NMT * 2; ++k) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // then up to four VALU
-                }
+                    for (int i = 0; i < 4; ++i) tot[j][mt][i] = fmaf(t, acc[j][mt][i], tot[j][mt][i]);
             }
-        // the super-unit's bias: one K=32 MFMA per row tile and m tile, into the totals
-        bf16x8_t xa[NMT];
+        }
+        if constexpr (P == 0) {
 #pragma unroll
-        for (int mt = 0; mt < NMT; ++mt) xa[mt] = __builtin_bit_cast(bf16x8_t, sXA[P][mt * 64 + lane]);
+            for (int j = 0; j < RT; ++j) sc_even[j] = sc[0][j];
+        } else {
+            // the super-unit's bias after its odd chunk: one K=32 MFMA per row tile and m tile
+            const u32x4_t* sXA = ((C >> 1) & 1) ? sXA1 : sXA0;
+            bf16x8_t xa[NMT];
 #pragma unroll
-        for (int j = 0; j < RT; ++j)
+            for (int mt = 0; mt < NMT; ++mt) xa[mt] = __builtin_bit_cast(bf16x8_t, sXA[mt * 64 + lane]);
 #pragma unroll
-            for (int mt = 0; mt < NMT; ++mt)
-                tot[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    xa[mt], __builtin_bit_cast(bf16x8_t, br[B][j]), tot[j][mt], 0, 0, 0);
-        stage_store(P ^ 1);
+            for (int j = 0; j < RT; ++j) {
+                const u32x4_t bw = u32x4_t{sc_even[j].x, sc_even[j].y, sc[1][j].x, sc[1][j].y};
+#pragma unroll
+                for (int mt = 0; mt < NMT; ++mt)
+                    tot[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[mt], __builtin_bit_cast(bf16x8_t, bw),
+                                                                         tot[j][mt], 0, 0, 0);
+            }
+        }
     };
-    uint32_t S = 0;
-    for (; S + 2 < nstages; S += 3) {
-        stage(S, std::integral_constant<int, 0>{});
-        stage(S + 1, std::integral_constant<int, 1>{});
-        stage(S + 2, std::integral_constant<int, 2>{});
+    for (uint32_t C = 0; C < nchunks; C += 2) {
+        stage(C, I0{});
+        stage(C + 1, I1{});
     }
-    if (S < nstages) stage(S, std::integral_constant<int, 0>{});
-    if (S + 1 < nstages) stage(S + 1, std::integral_constant<int, 1>{});
-    // the last step (always a second group) still owes its scales
-#pragma unroll
-    for (int j = 0; j < RT; ++j)
-#pragma unroll
-        for (int mt = 0; mt < NMT; ++mt)
-#pragma unroll
-            for (int i = 0; i < NI; ++i) tot[j][mt][i] = fmaf(tp[1][j], acc[1][j][mt][i], tot[j][mt][i]);
-    __syncthreads();  // no wave is still reading sA when the epilogue reuses LDS
-    head_epilogue<NMT, NI, RT, MODE>(a, tot, tile0, se);
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);  // the last (unused) copies land before LDS is reused
+    __syncthreads();
+    head_epilogue<NMT, 4, RT, MODE>(a, tot, tile0, se);
 }
 
 // ---- layout repack: reference [W|S|B] -> units ----------------------------------------------
@@ -1138,12 +1131,12 @@ int launch_head(twd_head* h, const uint16_t* hidden, uint32_t rows, float* logit
     } else if (rows <= 16) {
         prep_hidden_kernel<1><<<padded_units(h->nunits) * 1, kHeadThreads, 0, stream>>>(hidden, rows, h->d,
                                                                                        h->hp, h->hx);
-        head_wide_kernel<1, 4, kRT1, MODE>
+        head_wide_kernel<1, kRT1, MODE>
             <<<blocks_for(h->ntiles, kRT1), kHeadThreads, 0, stream>>>(a, h->hp, h->hx);
     } else {
         prep_hidden_kernel<4><<<padded_units(h->nunits) * 4, kHeadThreads, 0, stream>>>(hidden, rows, h->d,
                                                                                        h->hp, h->hx);
-        head_wide_kernel<4, 4, kRT4, MODE>
+        head_wide_kernel<4, kRT4, MODE>
             <<<blocks_for(h->ntiles, kRT4), kHeadThreads, 0, stream>>>(a, h->hp, h->hx);
     }
     TWD_HIP(hipGetLastError());
@@ -1196,7 +1189,7 @@ int launch_head_rmsnorm(twd_head* h, const float* x, const uint16_t* norm_w, flo
     a.fold = 1;
     prep_rmsnorm_kernel<<<padded_units(h->nunits), kHeadThreads, 0, stream>>>(x, norm_w, eps, rows, h->d,
                                                                               h->hp, h->hx);
-    head_wide_kernel<1, 4, kRT1, MODE><<<blocks_for(h->ntiles, kRT1), kHeadThreads, 0, stream>>>(a, h->hp, h->hx);
+    head_wide_kernel<1, kRT1, MODE><<<blocks_for(h->ntiles, kRT1), kHeadThreads, 0, stream>>>(a, h->hp, h->hx);
     TWD_HIP(hipGetLastError());
     return TWD_OK;
 }
