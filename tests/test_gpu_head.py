@@ -324,7 +324,7 @@ def _norm_oracle(oracle, W, S, B, x, w, cap, rows=None):
     return np.stack(out)
 
 
-@pytest.mark.parametrize("d,M", [(D, 1), (D, 3), (D, 5), (D, 8), (128, 1), (384, 8), (640, 2)])
+@pytest.mark.parametrize("d,M", [(D, 1), (D, 3), (D, 4), (D, 5), (D, 8), (128, 1), (384, 8), (640, 2), (640, 4)])
 def test_rmsnorm_logits_parity(torch_dev, oracle, d, M):
     torch, dev = torch_dev
     V = 1000
@@ -351,10 +351,11 @@ def test_rmsnorm_logits_parity(torch_dev, oracle, d, M):
     assert [int(t) for t in tok] == [int(oracle.argmax(got[m])) for m in range(M)]
 
 
-def test_rmsnorm_verify_and_sample(torch_dev, oracle):
+@pytest.mark.parametrize("M", [3, 5])  # the resident-h prologue (M <= 4) and the staged one
+def test_rmsnorm_verify_and_sample(torch_dev, oracle, M):
     torch, dev = torch_dev
     t = twd()
-    V, d, M = 3000, D, 5
+    V, d = 3000, D
     W, S, B = oracle.gen_lm_head(808, V, d)
     head = make_head(torch_dev, W, S, B, V, d, CAP)
     x, w = _norm_inputs(9, M, d)
@@ -362,9 +363,11 @@ def test_rmsnorm_verify_and_sample(torch_dev, oracle):
     wd = torch.from_numpy(w.view(np.int16)).to(dev)
     lg = head.logits_rmsnorm(xd, wd).cpu().numpy()
     arg = [int(oracle.argmax(lg[m])) for m in range(M)]
-    drafts = torch.tensor([arg[0], arg[1], (arg[2] + 1) % V, arg[3]], dtype=torch.int32, device=dev)
-    res = t.decode_verify(head.verify_greedy_rmsnorm(xd, wd, drafts))
-    assert res["tokens"] == [arg[0], arg[1], arg[2]] and res["num_accepted"] == 2
+    # drafts match rows 0 .. M - 3, then miss: M - 2 accepted, the target token of row M - 2
+    drafts = arg[:M - 2] + [(arg[M - 2] + 1) % V]
+    res = t.decode_verify(head.verify_greedy_rmsnorm(xd, wd, torch.tensor(drafts, dtype=torch.int32,
+                                                                           device=dev)))
+    assert res["tokens"] == arg[:M - 1] and res["num_accepted"] == M - 2
     params = [t.RowParams(0.8, 0.9, 40, 1.0, 0.25 + 0.1 * m, CAP, 0, 0) for m in range(M)]
     tok, lg2 = head.sample_rmsnorm(xd, wd, params)
     lg2 = lg2.cpu().numpy()
