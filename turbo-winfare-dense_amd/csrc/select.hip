@@ -522,13 +522,32 @@ void select_slice_kernel(SelectArgs args_by_value, SelectBufs b) {
 
     // ---- repetition penalty, sampling.cpp:74-90 ----
     if (p.repetition_penalty != 1.0f && p.history_len > 0) {
+        // history ids in batches of kHistBatch per thread, each batch requested at once (one
+        // round trip, not one per id); the first batch before the counts are cleared
+        constexpr int kHistBatch = 8;
+        const uint32_t* hist = b.history + p.history_offset;
+        const uint32_t hlen = p.history_len;
+        uint32_t ids[kHistBatch];
+        auto fetch = [&](uint32_t j0) {
+#pragma unroll
+            for (int q = 0; q < kHistBatch; ++q) {
+                const uint32_t j = j0 + tid + NT * q;
+                ids[q] = j < hlen ? hist[j] : 0xFFFFFFFFu;  // never inside a slice
+            }
+        };
+        auto count = [&]() {
+#pragma unroll
+            for (int q = 0; q < kHistBatch; ++q)
+                if (ids[q] >= lo && ids[q] < hi) atomicAdd(&sh.u.cnt[ids[q] - lo], 1u);
+        };
+        fetch(0);
 #pragma unroll
         for (int e = 0; e < kSelPerThread; ++e) sh.u.cnt[tid + NT * e] = 0;
         __syncthreads();
-        const uint32_t* hist = b.history + p.history_offset;
-        for (uint32_t j = tid; j < p.history_len; j += NT) {
-            const uint32_t id = hist[j];
-            if (id >= lo && id < hi) atomicAdd(&sh.u.cnt[id - lo], 1u);
+        count();
+        for (uint32_t j0 = NT * kHistBatch; j0 < hlen; j0 += NT * kHistBatch) {
+            fetch(j0);
+            count();
         }
         __syncthreads();
         const float rp = p.repetition_penalty;
@@ -698,14 +717,31 @@ __global__ __launch_bounds__(kMergeThreads) void select_merge_kernel(SelectArgs 
     const float gm = sh.c.gmax;
     // every slice's ranks, packed into cand[0 .. n_cand)
     float cmn = INFINITY;
-    for (uint32_t f = tid; f < parts * want_row; f += NT) {
-        const uint32_t q = f / want_row, slot = f % want_row;
-        const uint32_t at = sh.offs[q] + slot;
-        if (at < sh.offs[q + 1]) {
-            const uint64_t k = b.cand[(o + q) * kMaxWant + slot];
-            sh.cand[at] = k;
-            const float x = rank_value(k);
-            if (k != 0 && __builtin_isfinite(x)) cmn = fminf(cmn, x);
+    const uint32_t nf = parts * want_row;
+    constexpr int kGatherBatch = 4;  // loads requested together, then stored
+    for (uint32_t f0 = 0; f0 < nf; f0 += NT * kGatherBatch) {
+        uint64_t kk[kGatherBatch];
+        uint32_t at[kGatherBatch];
+#pragma unroll
+        for (int u = 0; u < kGatherBatch; ++u) {
+            const uint32_t f = f0 + tid + NT * u;
+            at[u] = 0xFFFFFFFFu;
+            kk[u] = 0;
+            if (f < nf) {
+                const uint32_t q = f / want_row, slot = f % want_row;
+                const uint32_t a = sh.offs[q] + slot;
+                if (a < sh.offs[q + 1]) {
+                    at[u] = a;
+                    kk[u] = b.cand[(o + q) * kMaxWant + slot];
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kGatherBatch; ++u) {
+            if (at[u] == 0xFFFFFFFFu) continue;
+            sh.cand[at[u]] = kk[u];
+            const float x = rank_value(kk[u]);
+            if (kk[u] != 0 && __builtin_isfinite(x)) cmn = fminf(cmn, x);
         }
     }
     uint32_t no_flag = 0;
