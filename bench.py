@@ -74,6 +74,30 @@ def time_loop(torch, steps, warmup, step_fn, min_warm_s=0.1):
     return e0.elapsed_time(e1) / 1e3
 
 
+def launch_percentiles(torch, n, step_fn):
+    """Each of n launches between its own pair of HIP events (after the timed region, so the
+    GPU is warm): the p10 / p50 / p90 of single-launch durations in microseconds."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for i, (a, b) in enumerate(evs):
+        a.record()
+        step_fn(i)
+        b.record()
+    torch.cuda.synchronize()
+    us = np.array([a.elapsed_time(b) * 1e3 for a, b in evs])
+    return {f"launch_us_p{q}": float(np.percentile(us, q)) for q in (10, 50, 90)}
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def cpu_baseline(wsb_dev, hidden_rows, n_rows: int):
     """Scalar single-thread LM head + softcap + greedy argmax over `n_rows` full rows (every
     vocabulary row each), the oracle's restatement of cpu_reference.cpp:643-665 and
@@ -94,8 +118,7 @@ def cpu_baseline(wsb_dev, hidden_rows, n_rows: int):
     return {"value": n_rows / dt, "unit": "rows/s", "cores": 1, "kind": "port",
             "sample": f"{n_rows} full rows of BASELINE config 2 (all {V} vocabulary rows, fp32 "
                       f"scalar dot as cpu_reference.cpp:643-665, softcap, argmax) in {dt:.1f} s, "
-                      f"one thread of {platform.processor() or platform.machine()}, "
-                      f"nproc={os.cpu_count()}"}
+                      f"one thread of {cpu_model()}, nproc={os.cpu_count()}"}
 
 
 def measured_traffic():
@@ -169,6 +192,7 @@ def main():
     bytes2 = algorithmic_bytes(1)
     results[2] = {"rows_per_s": rows_s, "ms_per_step": step_s * 1e3,
                   "kernel_us_mean": step_s * 1e6, "hbm_frac": bytes2 / step_s / PEAK_HBM}
+    results[2].update(launch_percentiles(torch, 200, step2))
     log(f"config 2: {rows_s:.1f} rows/s, {step_s * 1e6:.1f} us per launch, "
         f"{bytes2 / step_s / 1e12:.2f} TB/s")
 
