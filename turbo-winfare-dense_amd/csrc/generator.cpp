@@ -16,10 +16,9 @@ struct twd_generator {
     uint32_t vocab = 0;
     float softcap = 0.0f;
     twd_generation_params p{};
-    uint32_t* history = nullptr;  // device, capacity `cap`
+    uint32_t* history = nullptr;  // device, capacity `cap`; each step writes its token at [len]
     uint32_t len = 0, cap = 0;
     uint32_t emitted = 0;
-    uint32_t* token_dev = nullptr;
     uint32_t* token_host = nullptr;  // pinned
     float* logits = nullptr;         // device [vocab]
     std::vector<uint32_t> stop_ids;
@@ -45,16 +44,16 @@ twd_row_params step_params(const twd_generator* g) {
     return r;
 }
 
-// After the head pass has put the step's token in g->token_dev: append it to the history and,
-// when asked, bring it to the host and apply the stop rules (src/runner.cpp:2327-2336).
+// After the head pass has written the step's token at history[len] (the selection of this step
+// read history[0, len) only): count it in and, when asked, bring it to the host and apply the
+// stop rules (src/runner.cpp:2327-2336).
 int finish_step(twd_generator* g, hipStream_t s, uint32_t* token_out, int* finished) {
-    TWD_HIP(hipMemcpyAsync(g->history + g->len, g->token_dev, sizeof(uint32_t),
-                           hipMemcpyDeviceToDevice, s));
+    const uint32_t* token_dev = g->history + g->len;
     ++g->len;
     ++g->emitted;
     bool done = g->emitted >= g->p.max_tokens;
     if (token_out || finished) {
-        TWD_HIP(hipMemcpyAsync(g->token_host, g->token_dev, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+        TWD_HIP(hipMemcpyAsync(g->token_host, token_dev, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
         TWD_HIP(hipStreamSynchronize(s));
         const uint32_t t = *g->token_host;
         if (t == TWD_TOKEN_DEGENERATE) {  // sample_token throws here; the generation ends
@@ -110,7 +109,6 @@ TWD_API int twd_generator_create(twd_head* head, const twd_generation_params* pa
     g->len = prompt_len;
     g->stop_ids.assign(stop_ids, stop_ids + n_stop);
     hipError_t e = hipMalloc(&g->history, std::max<size_t>(g->cap, 1) * sizeof(uint32_t));
-    if (e == hipSuccess) e = hipMalloc(&g->token_dev, sizeof(uint32_t));
     if (e == hipSuccess) e = hipMalloc(&g->logits, static_cast<size_t>(vocab) * sizeof(float));
     if (e == hipSuccess) e = hipHostMalloc(&g->token_host, sizeof(uint32_t), hipHostMallocDefault);
     if (e == hipSuccess) e = hipMemcpy(g->history, prompt, prompt_len * sizeof(uint32_t), hipMemcpyHostToDevice);
@@ -126,7 +124,6 @@ TWD_API int twd_generator_create(twd_head* head, const twd_generation_params* pa
 TWD_API void twd_generator_destroy(twd_generator* g) {
     if (!g) return;
     if (g->history) (void)hipFree(g->history);
-    if (g->token_dev) (void)hipFree(g->token_dev);
     if (g->logits) (void)hipFree(g->logits);
     if (g->token_host) (void)hipHostFree(g->token_host);
     delete g;
@@ -138,11 +135,12 @@ TWD_API int twd_generator_step(twd_generator* g, const uint16_t* hidden_bf16, vo
     int rc = check_step(g);
     if (rc) return rc;
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    uint32_t* slot = g->history + g->len;  // the token lands in the history directly
     if (fused_greedy(g)) {
-        rc = twd_head_greedy(g->head, hidden_bf16, 1, nullptr, g->token_dev, stream);
+        rc = twd_head_greedy(g->head, hidden_bf16, 1, nullptr, slot, stream);
     } else {
         const twd_row_params r = step_params(g);
-        rc = twd_head_sample(g->head, hidden_bf16, 1, &r, g->history, g->logits, g->token_dev, stream);
+        rc = twd_head_sample(g->head, hidden_bf16, 1, &r, g->history, g->logits, slot, stream);
     }
     if (rc) return rc;
     return finish_step(g, s, token_out, finished);
@@ -154,12 +152,13 @@ TWD_API int twd_generator_step_rmsnorm(twd_generator* g, const float* x, const u
     int rc = check_step(g);
     if (rc) return rc;
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    uint32_t* slot = g->history + g->len;
     if (fused_greedy(g)) {
-        rc = twd_head_greedy_rmsnorm(g->head, x, norm_weight, eps, 1, nullptr, g->token_dev, stream);
+        rc = twd_head_greedy_rmsnorm(g->head, x, norm_weight, eps, 1, nullptr, slot, stream);
     } else {
         const twd_row_params r = step_params(g);
         rc = twd_head_sample_rmsnorm(g->head, x, norm_weight, eps, 1, &r, g->history, g->logits,
-                                     g->token_dev, stream);
+                                     slot, stream);
     }
     if (rc) return rc;
     return finish_step(g, s, token_out, finished);
