@@ -294,24 +294,12 @@ __device__ __forceinline__ void tile_streams(const HeadArgs& a, uint32_t tile0,
     }
 }
 
-// Unit U of the RT row tiles: 16 B of nibbles (lane offset lane * 16) and the 8 B {b, t} pair
-// of the lane's row (lane offset 1024 + (lane % 16) * 8).
-template <int RT>
-__device__ __forceinline__ void load_unit(const __amdgpu_buffer_rsrc_t (&rs)[RT], uint32_t U,
-                                          uint32_t vo_w, uint32_t vo_s, u32x4_t (&w)[RT],
-                                          u32x2_t (&sb)[RT]) {
-    const int so = static_cast<int>(U * kUnitBytes);
-#pragma unroll
-    for (int j = 0; j < RT; ++j) {
-        w[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs[j], vo_w, so, kNonTemporal));
-        sb[j] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rs[j], vo_s, so, kNonTemporal));
-    }
-}
-
-// The two halves of load_unit, each issued in a fixed order and fenced from the surrounding
-// code. A ring whose prologue and loop issue their loads in the same order lets the wait before
-// each slot's first use count only that slot's loads; any other order makes the wait at the
-// loop head cover the worst case of both.
+// Unit U of the RT row tiles, in two halves: 16 B of nibbles per lane (lane offset lane * 16),
+// and the 8 B {b, t} pair of the lane's row (lane offset 1024 + (lane % 16) * 8). Each half is
+// issued in a fixed order and fenced from the surrounding code. A ring whose prologue and loop
+// issue their loads in the same order lets the wait before each slot's first use count only
+// that slot's loads; any other order makes the wait at the loop head cover the worst case of
+// both.
 template <int RT>
 __device__ __forceinline__ void load_nibbles_ordered(const __amdgpu_buffer_rsrc_t (&rs)[RT], uint32_t U,
                                                      uint32_t vo_w, u32x4_t (&w)[RT]) {
@@ -1069,7 +1057,8 @@ int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
     // gbest: per-row maxima, the arrival counter, and the repack's bad-scale flag
     if (e == hipSuccess) e = hipMalloc(&h->gbest, sizeof(uint64_t) * (TWD_MAX_ROWS + 2));
     if (e == hipSuccess) e = hipMemset(h->gbest, 0, sizeof(uint64_t) * (TWD_MAX_ROWS + 2));
-    // hp / hx: one stage past the end (the stage loop requests the next stage unconditionally)
+    // hp / hx: room past the last chunk and super-unit (each stage copies the next one
+    // unconditionally)
     if (e == hipSuccess) e = hipMalloc(&h->hp, sizeof(u32x4_t) * (h->nunits + 3) * 4 * 4 * 64);
     if (e == hipSuccess) e = hipMalloc(&h->hx, sizeof(u32x4_t) * (super_units(h->nunits) + 1) * 4 * 64);
     if (e != hipSuccess) {
