@@ -14,6 +14,7 @@ Prints ONE JSON line on stdout; progress goes to stderr.
 from __future__ import annotations
 
 import argparse
+import hashlib
 import importlib
 import json
 import os
@@ -98,13 +99,12 @@ def cpu_model():
     return platform.processor() or platform.machine()
 
 
-def cpu_baseline(wsb_dev, hidden_rows, n_rows: int):
+def cpu_baseline(host, hidden_rows, n_rows: int):
     """Scalar single-thread LM head + softcap + greedy argmax over `n_rows` full rows (every
     vocabulary row each), the oracle's restatement of cpu_reference.cpp:643-665 and
     sampling.cpp:97-104, on the same weights and hidden states the GPU uses."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
-    host = wsb_dev.cpu().numpy()
     wpr, gpr = D // 8, D // G
     W = host[: V * wpr * 4].view(np.uint32).reshape(V, wpr)
     S = host[V * wpr * 4: V * wpr * 4 + V * gpr * 2].view(np.uint16).reshape(V, gpr)
@@ -141,7 +141,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--configs", default="1,2,3,4,5")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=3, help="full rows in the CPU baseline")
+    ap.add_argument("--cpu-rows", type=int, default=8, help="full rows in the CPU baseline (about 14 s)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (FETCH_SIZE/WRITE_SIZE calibration)")
     args = ap.parse_args()
@@ -347,10 +347,14 @@ def main():
     log(f"read ceiling {best[0]:.0f} GB/s ({ceiling['frac_of_peak'] * 100:.1f}% of peak); "
         f"the head pass reaches {ceiling['kernel_frac_of_ceiling'] * 100:.1f}% of it")
 
+    # the synthetic inputs, pinned by digest (outside every timed region)
+    host = wsb.cpu().numpy()
+    digests = {"weights_sha256": hashlib.sha256(memoryview(host)).hexdigest(),
+               "hidden_sha256": hashlib.sha256(hp.cpu().numpy().tobytes()).hexdigest()}
     cpu = None
     if not args.no_cpu_baseline:
         log(f"cpu baseline: scalar LM head, {args.cpu_rows} full rows")
-        cpu = cpu_baseline(wsb, hp[: args.cpu_rows].cpu().numpy().view(np.uint16).reshape(-1, D),
+        cpu = cpu_baseline(host, hp[: args.cpu_rows].cpu().numpy().view(np.uint16).reshape(-1, D),
                            args.cpu_rows)
 
     achieved = bytes2 / step_s
@@ -372,7 +376,9 @@ def main():
                                "~N(0,1), fused softcap 30 + greedy argmax",
                    "vocab": V, "d_model": D, "group": G, "rows_per_step": 1,
                    "weights": "q~U{0..15}, s~U(1e-3,1e-2) bf16, b=-8s (twd_generate_head seed "
-                              f"{SEED})"},
+                              f"{SEED})",
+                   "hidden": "64 bf16 rows ~N(0,1), numpy default_rng(2), cycled over the steps",
+                   **digests},
         "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9,
                      "unit": "GB/s", "frac": achieved / PEAK_HBM, "traffic": traffic,
                      "traffic_source": traffic_src,
