@@ -211,8 +211,11 @@ struct SeqShared {
     uint32_t n_marks;
     uint32_t mark_k0[kMarks];
     float mark_S[kMarks];
-    float head[kSerialUntil];  // the first terms, for the serial start
+    // the first terms, for the serial start: every thread stages four, so the array spans
+    // 4 * kRejThreads entries although only [0, kSerialUntil) is read
+    float head[4 * kRejThreads];
 };
+static_assert(kSerialUntil <= 4 * kRejThreads, "the serial start is staged in one pass");
 
 // One window of block_seq_sum: PER terms per thread from the 16-aligned start a0 <= k0; terms
 // before k0 or at n and beyond count as zero. load(j0, a) fills a[0..PER) with terms j0.. (j0
