@@ -104,3 +104,28 @@ def test_head_bytes_matches_reference_size():
     # docs/FORWARD_PASS.md:55 of the reference: 792,723,456 B for V=262144, d=5376
     t = twd()
     assert t.head_bytes(262144, 5376) == 262144 * (2688 + 168 + 168)
+
+
+def test_generator_and_probe_argument_errors_without_gpu():
+    t = twd()
+    lib = t.twd.lib
+    out = ctypes.c_void_p()
+    gp = t.twd.GenerationParams(0.7, 0.9, 40, 1.1, 1, 5, 16)
+    prompt = (ctypes.c_uint32 * 2)(1, 2)
+    assert lib.twd_generator_create(None, ctypes.byref(gp), prompt, 2, None, 0,
+                                    ctypes.byref(out)) == t.twd.TWD_E_INVALID
+    assert "null head" in t.twd.last_error()
+    tok, fin = ctypes.c_uint32(), ctypes.c_int()
+    assert lib.twd_generator_step(None, None, None, ctypes.byref(tok),
+                                  ctypes.byref(fin)) == t.twd.TWD_E_INVALID
+    assert "null generator" in t.twd.last_error()
+    us, nb = ctypes.c_float(), ctypes.c_uint64()
+    assert lib.twd_probe_read_bandwidth(None, 1 << 20, 64, 1, None, ctypes.byref(us),
+                                        ctypes.byref(nb)) == t.twd.TWD_E_INVALID
+    buf = np.zeros(16, np.uint8)
+    # waves must be a multiple of 8, and each stripe at least 1 KB
+    assert lib.twd_probe_read_bandwidth(buf.ctypes.data, 1 << 20, 12, 1, None, ctypes.byref(us),
+                                        ctypes.byref(nb)) == t.twd.TWD_E_INVALID
+    assert lib.twd_probe_read_bandwidth(buf.ctypes.data, 4096, 8, 1, None, ctypes.byref(us),
+                                        ctypes.byref(nb)) == t.twd.TWD_E_INVALID
+    assert "stripes" in t.twd.last_error()
