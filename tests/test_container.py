@@ -127,3 +127,18 @@ def test_head_load_rejections(oracle, tmp_path):
     with pytest.raises(t.TwdError) as e:
         t.LMHead.load(path)
     assert e.value.code == t.TWD_E_INVALID and "exceeds header lm_head_size 4096" in str(e.value)
+
+
+def test_head_load_rejects_offsets_past_the_file(oracle, tmp_path):
+    # an LM-head offset near 2^64 must not wrap around the bounds check; the load fails on the
+    # host before any device allocation
+    t = twd()
+    V, d = 64, 128
+    W, S, B = oracle.gen_lm_head(2, V, d)
+    norm = bf16_rne(np.ones(d, np.float32))
+    path = str(tmp_path / "far.g4dense")
+    write_container(path, W, S, B, norm, V, d, lm_head_offset=(1 << 64) - 4096, lm_head_size=1 << 40)
+    out = ctypes.c_void_p()
+    rc = t.lib.twd_head_load(os.fsencode(path), None, ctypes.byref(out))
+    assert rc == t.TWD_E_INVALID and not out.value
+    assert "extends beyond the file" in t.lib.twd_last_error().decode()

@@ -428,3 +428,18 @@ def test_generator_matches_oracle_loop(torch_dev, oracle, T, p, k, rp):
     assert n == len(history)
     assert gen.tokens() == history
     gen.close()
+
+
+def test_generator_rejects_a_capacity_past_32_bits(torch_dev, oracle):
+    # prompt_len + max_tokens sizes the device history; a sum that wraps must be refused before
+    # the prompt is copied into a buffer sized by the wrapped value
+    t = twd()
+    V, d = 1000, 128
+    W, S, B = oracle.gen_lm_head(901, V, d)
+    head = make_head(torch_dev, W, S, B, V, d, CAP)
+    sp = t.SamplingParams(0.0, 1.0, 0, 1.0, False, 0)
+    with pytest.raises(t.TwdError) as e:
+        t.Generator(head, sp, [1, 2, 3], 0xFFFFFFFF)
+    assert e.value.code == t.TWD_E_INVALID and "32 bits" in str(e.value)
+    gen = t.Generator(head, sp, [1, 2, 3], 5)
+    gen.close()

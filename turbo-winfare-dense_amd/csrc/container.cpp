@@ -168,7 +168,8 @@ TWD_API int twd_head_load(const char* path, void* stream, twd_head** out) {
         return fail(TWD_E_INVALID, "ForwardRunner: computed LM head size " + std::to_string(total) +
                                        " exceeds header lm_head_size " + std::to_string(h.lm_head_size));
     }
-    if (h.lm_head_offset + total > size) return fail(TWD_E_INVALID, "the LM head extends beyond the file");
+    if (h.lm_head_offset > size || total > size - h.lm_head_offset)
+        return fail(TWD_E_INVALID, "the LM head extends beyond the file");
 
     // the slice, staged through a pinned chunk into a device copy of the reference layout
     const hipStream_t s = static_cast<hipStream_t>(stream);
@@ -201,9 +202,9 @@ TWD_API int twd_head_load(const char* path, void* stream, twd_head** out) {
     if (rc) return rc;
 
     // the final RMSNorm weight follows the embedding table's [W|S|B] (runner.cpp:488-497)
-    if (h.embed_offset > 0) {
+    if (h.embed_offset > 0 && h.embed_offset <= size && total <= size - h.embed_offset) {
         const uint64_t at = h.embed_offset + total;
-        if (at + 2ull * d <= size) {
+        if (2ull * d <= size - at) {
             std::vector<uint16_t> w(d);
             if (!read_at(file.f, at, w.data(), 2ull * d)) {
                 twd_head_destroy(head);

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdint>
 #include <cstring>
 #include <vector>
 
@@ -95,6 +96,8 @@ TWD_API int twd_generator_create(twd_head* head, const twd_generation_params* pa
     *out = nullptr;
     if (prompt_len == 0 || !prompt) return fail(TWD_E_INVALID, "the prompt must hold at least one token");
     if (n_stop > 0 && !stop_ids) return fail(TWD_E_INVALID, "null stop_ids");
+    if (params->max_tokens > UINT32_MAX - prompt_len)
+        return fail(TWD_E_INVALID, "prompt_len + max_tokens must fit 32 bits");
     uint32_t vocab = 0, d = 0;
     float cap = 0.0f;
     uint64_t bytes = 0;
