@@ -81,8 +81,8 @@ TWD_API const char* twd_last_error(void);
  * is the container's contiguous LM-head slice [W u32 V x d/8 | S bf16 V x d/64 | B bf16 V x d/64]
  * (include/g4dense/format.hpp:60-61), element c of row r being nibble c%8 (low first) of word
  * r*d/8 + c/8 and w = q*s + b (shaders/Common.hlsli:163-222). The head is repacked once into
- * the HBM layout the kernels stream. group_size must be 64, d_model a multiple of 128, and the
- * call is synchronous. A head with a group scale above 2^100 in magnitude or an infinite group
+ * the HBM layout the kernels stream. group_size must be 64, d_model a multiple of 128, vocab at
+ * most 2^30, and the call is synchronous. A head with a group scale above 2^100 in magnitude or an infinite group
  * bias is rejected with TWD_E_UNSUPPORTED. */
 TWD_API int twd_head_create(const void* wsb_host, uint64_t wsb_bytes, uint32_t vocab,
                             uint32_t d_model, uint32_t group_size, float softcap,

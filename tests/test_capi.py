@@ -97,6 +97,9 @@ def test_argument_errors_without_gpu():
                                ctypes.byref(out)) == t.twd.TWD_E_UNSUPPORTED
     assert lib.twd_head_create(buf.ctypes.data, 16, 16, 128, 64, 30.0,
                                ctypes.byref(out)) == t.twd.TWD_E_INVALID  # too few bytes
+    assert lib.twd_head_create(buf.ctypes.data, 16, (1 << 30) + 1, 128, 64, 30.0,
+                               ctypes.byref(out)) == t.twd.TWD_E_UNSUPPORTED
+    assert "2^30" in t.twd.last_error()
     assert t.head_bytes(262144, 5376) == 792723456
 
 

@@ -1019,6 +1019,8 @@ uint32_t padded_units(uint32_t nunits) { return nunits + (nunits & 1); }
 int check_geometry(uint32_t vocab, uint32_t d, uint32_t group) {
     if (group != kGroup) return fail(TWD_E_UNSUPPORTED, "group_size must be 64");
     if (vocab == 0) return fail(TWD_E_INVALID, "vocab must be > 0");
+    // tile counts and row indices stay far from 32-bit wrap-around
+    if (vocab > (1u << 30)) return fail(TWD_E_UNSUPPORTED, "vocab must be at most 2^30");
     if (d == 0 || d % kChunkK != 0) return fail(TWD_E_UNSUPPORTED, "d_model must be a positive multiple of 128");
     return TWD_OK;
 }
