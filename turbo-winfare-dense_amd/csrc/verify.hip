@@ -171,6 +171,34 @@ __device__ __forceinline__ Xfer xfer_shfl_up(const Xfer& x, int d) {
                 static_cast<uint32_t>(__shfl_up(x.out, d))};
 }
 
+// The value of a lane CTRL selects (a DPP row shift or row broadcast), or the identity where the
+// source lies outside the row or the destination row is masked off: a scan step in a few VALU
+// cycles, without the LDS round trip of a permute.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ Xfer xfer_dpp(const Xfer& x) {
+    const Xfer id = xfer_id();
+    return Xfer{static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(id.inc0), static_cast<int>(x.inc0),
+                                                                  CTRL, ROW_MASK, 0xF, false)),
+                static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(id.inc1), static_cast<int>(x.inc1),
+                                                                  CTRL, ROW_MASK, 0xF, false)),
+                static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(id.out), static_cast<int>(x.out),
+                                                                  CTRL, ROW_MASK, 0xF, false))};
+}
+constexpr int kDppRowShr = 0x110;     // + n: row_shr:n
+constexpr int kDppRowBcast15 = 0x142;  // lane 15 of each row to the next row
+constexpr int kDppRowBcast31 = 0x143;  // lane 31 to rows 2 and 3
+
+// Inclusive scan of the 64 lanes' transfer functions, lane order (earlier lanes applied first).
+__device__ __forceinline__ Xfer xfer_wave_scan(Xfer v) {
+    v = xfer_then(xfer_dpp<kDppRowShr + 1, 0xF>(v), v);
+    v = xfer_then(xfer_dpp<kDppRowShr + 2, 0xF>(v), v);
+    v = xfer_then(xfer_dpp<kDppRowShr + 4, 0xF>(v), v);
+    v = xfer_then(xfer_dpp<kDppRowShr + 8, 0xF>(v), v);
+    v = xfer_then(xfer_dpp<kDppRowBcast15, 0xA>(v), v);
+    v = xfer_then(xfer_dpp<kDppRowBcast31, 0xC>(v), v);
+    return v;
+}
+
 __device__ __forceinline__ Xfer xfer_shfl(const Xfer& x, int src) {
     return Xfer{static_cast<uint32_t>(__shfl(x.inc0, src)), static_cast<uint32_t>(__shfl(x.inc1, src)),
                 static_cast<uint32_t>(__shfl(x.out, src))};
@@ -260,24 +288,19 @@ __device__ __forceinline__ void seq_window(Load load, Term term, uint32_t n, flo
         }
     }
     // wave inclusive scan
-    Xfer inc = t;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const Xfer o = xfer_shfl_up(inc, d);
-        if (lane >= d) inc = xfer_then(o, inc);
-    }
+    const Xfer inc = xfer_wave_scan(t);
     Xfer ex = xfer_shfl_up(inc, 1);
     if (lane == 0) ex = xfer_id();
     if (lane == 63) sh.wave_total[wave] = inc;
     if (tid == 0) sh.event = kNoEvent;
     __syncthreads();
     // prefix over the waves before this one: a 16-lane scan of the wave totals
+    static_assert(kRejWaves == 16, "the wave totals fill one DPP row");
     Xfer wt = lane < kRejWaves ? sh.wave_total[lane] : xfer_id();
-#pragma unroll
-    for (int d = 1; d < kRejWaves; d <<= 1) {
-        const Xfer o = xfer_shfl_up(wt, d);
-        if (lane >= d) wt = xfer_then(o, wt);
-    }
+    wt = xfer_then(xfer_dpp<kDppRowShr + 1, 0xF>(wt), wt);
+    wt = xfer_then(xfer_dpp<kDppRowShr + 2, 0xF>(wt), wt);
+    wt = xfer_then(xfer_dpp<kDppRowShr + 4, 0xF>(wt), wt);
+    wt = xfer_then(xfer_dpp<kDppRowShr + 8, 0xF>(wt), wt);
     Xfer wp = xfer_shfl(wt, wave > 0 ? wave - 1 : 0);
     if (wave == 0) wp = xfer_id();
     const Xfer in = xfer_then(wp, ex);
