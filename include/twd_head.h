@@ -265,6 +265,16 @@ TWD_API int twd_verify_draft(twd_selector* sel, const float* logits, uint32_t vo
                              uint64_t base_seed, const uint32_t* drafts, uint32_t n_drafts,
                              twd_verify_result* result, void* stream);
 
+/* The exact sequential-sum engine of twd_verify_draft on its own. No counterpart in the
+ * reference's API; it is for callers and tests that check the engine against an in-order fp32
+ * loop (the sums of compute_softmax, src/speculator.cpp:22-26, and of the residual draw,
+ * :104-116, are formed that way). terms: n finite values >= 0 in device memory, 16-byte
+ * aligned and readable up to n rounded up to a multiple of 16 floats. *sum_out (device)
+ * receives ((t0 + t1) + t2) + ... in fp32; when stop_out (device) is non-NULL it receives the
+ * first index whose prefix sum is >= thr, or n when none is. Asynchronous on `stream`. */
+TWD_API int twd_sequential_sum(const float* terms, uint32_t n, float thr, float* sum_out,
+                               uint32_t* stop_out, void* stream);
+
 /* ---- the reference's seeding, for callers that keep seeds (src/sampling.cpp:18-72) -------- */
 TWD_API uint64_t twd_splitmix64(uint64_t x);
 TWD_API uint64_t twd_seed_for(int has_seed, uint64_t seed, int position);

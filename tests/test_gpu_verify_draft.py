@@ -149,3 +149,64 @@ def test_python_coordinator_with_draft_logits(env, oracle):
     want = oracle.verify_draft(drafts, rows, drs, 0.9, 1.0, 0, 1.0, 77)
     want.pop("diag")
     assert same(got, want), (got, want)
+
+
+# ---- the exact sequential-sum engine on its own --------------------------------------------
+
+def _seq_sum(env, x, thr=None):
+    import ctypes
+    torch, dev, t, sel = env
+    n = len(x)
+    buf = torch.zeros((n + 15) // 16 * 16, dtype=torch.float32, device=dev)
+    buf[:n] = torch.from_numpy(np.ascontiguousarray(x, np.float32))
+    out = torch.zeros(1, dtype=torch.float32, device=dev)
+    stop = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    rc = t.lib.twd_sequential_sum(ctypes.c_void_p(buf.data_ptr()), ctypes.c_uint32(n),
+                                  ctypes.c_float(0.0 if thr is None else thr),
+                                  ctypes.c_void_p(out.data_ptr()),
+                                  None if thr is None else ctypes.c_void_p(stop.data_ptr()), None)
+    assert rc == 0, t.last_error()
+    torch.cuda.synchronize()
+    return out.cpu().numpy()[0], int(stop.cpu().numpy()[0])
+
+
+def _seq_cases():
+    rng = np.random.default_rng(41)
+    cases = []
+    for n in (1, 5, 2048, 2049, 4097, 70001, V):  # around the serial start and the window sizes
+        for sd in (1.0, 4.0):
+            z = (rng.standard_normal(n) * sd).astype(np.float32)
+            cases.append((f"softmax n={n} sd={sd}", np.exp(z - z.max()).astype(np.float32)))
+    cases.append(("uniform", rng.random(100000).astype(np.float32)))
+    # S in [0.5, 1) after the first term, terms k * 2^-25: every odd k is an exact half-way case
+    ties = (rng.integers(0, 8, 50000) * 2.0 ** -25).astype(np.float32)
+    ties[0] = 0.75
+    cases.append(("ties", ties))
+    # crossing into [1, 2) and beyond, with ties on both sides
+    cross = (rng.integers(0, 64, 60000) * 2.0 ** -24).astype(np.float32)
+    cross[0] = 0.999
+    cases.append(("ties across binades", cross))
+    # half the terms zero, and terms below half an ulp that never move the sum
+    z = rng.random(30000).astype(np.float32)
+    z[rng.random(30000) < 0.5] = 0.0
+    cases.append(("zeros", z))
+    tiny = np.full(20000, 1e-9, np.float32)
+    tiny[0] = 1.0
+    cases.append(("below half an ulp", tiny))
+    return cases
+
+
+def test_sequential_sum_is_the_in_order_fp32_sum(env):
+    # np.add.accumulate over float32 adds in index order, rounding each step to fp32: the loop
+    # of speculator.cpp:22-26 and :104-116
+    for name, x in _seq_cases():
+        acc = np.add.accumulate(x, dtype=np.float32)
+        got, _ = _seq_sum(env, x)
+        assert np.float32(got).view(np.uint32) == acc[-1].view(np.uint32), (name, got, acc[-1])
+        for frac in (0.0, 0.37, 0.999, 1.0):
+            thr = np.float32(acc[-1] * np.float32(frac))
+            want = int(np.argmax(acc >= thr)) if (acc >= thr).any() else len(x)
+            s, stop = _seq_sum(env, x, float(thr))
+            assert stop == want, (name, frac, stop, want)
+            # the sum returned with a stop is the prefix through the stop index
+            assert np.float32(s).view(np.uint32) == acc[min(want, len(x) - 1)].view(np.uint32), (name, frac)
