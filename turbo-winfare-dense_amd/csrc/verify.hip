@@ -461,18 +461,19 @@ __global__ __launch_bounds__(kRejThreads) void draft_sum_kernel(DraftArgs a) {
 }
 
 // The sequential-sum engine alone, over one array: its sum, and the first index whose prefix
-// reaches thr when stop is wanted.
+// reaches thr when STOP. STOP is a template argument so that the sum-only form compiles the
+// serial start without the stop test (whose early exit keeps its loads from being batched).
+template <bool STOP>
 __global__ __launch_bounds__(kRejThreads) void seq_sum_kernel(const float* x, uint32_t n, float thr,
-                                                              uint32_t want_stop, float* sum_out,
-                                                              uint32_t* stop_out) {
+                                                              float* sum_out, uint32_t* stop_out) {
     __shared__ SeqShared sh;
     uint32_t stop = n;
     const float s = block_seq_sum([&](uint32_t j0, auto& v) { load_row(x, j0, v); },
                                   [&](uint32_t j) { return x[j]; }, n, 0.0f, 0u, thr,
-                                  want_stop ? &stop : nullptr, false, sh);
+                                  STOP ? &stop : nullptr, false, sh);
     if (threadIdx.x == 0) {
         *sum_out = s;
-        if (want_stop) *stop_out = stop;
+        if (STOP) *stop_out = stop;
     }
 }
 
@@ -636,8 +637,11 @@ TWD_API int twd_sequential_sum(const float* terms, uint32_t n, float thr, float*
     if (!terms || !sum_out) return fail(TWD_E_INVALID, "null terms or sum_out");
     if (n == 0) return fail(TWD_E_INVALID, "n must be > 0");
     if ((reinterpret_cast<uintptr_t>(terms) & 15u) != 0) return fail(TWD_E_INVALID, "terms must be 16-byte aligned");
-    seq_sum_kernel<<<1, kRejThreads, 0, static_cast<hipStream_t>(stream)>>>(terms, n, thr, stop_out ? 1u : 0u,
-                                                                           sum_out, stop_out);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (stop_out)
+        seq_sum_kernel<true><<<1, kRejThreads, 0, s>>>(terms, n, thr, sum_out, stop_out);
+    else
+        seq_sum_kernel<false><<<1, kRejThreads, 0, s>>>(terms, n, thr, sum_out, stop_out);
     TWD_HIP(hipGetLastError());
     return TWD_OK;
 }
