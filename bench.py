@@ -7,8 +7,9 @@ with the softcap and greedy argmax fused, rows/s with every input already reside
 One step = one launch over one hidden row. The other BASELINE configs are timed the same way and
 reported under "configs". `roofline` is the dominant kernel (the head pass of config 2): its
 algorithmic bytes per launch divided by its mean launch duration, measured with HIP events on
-the stream the kernel runs on. `cpu_baseline` times the scalar CPU LM head of
-src/cpu_reference.cpp:643-665 (restated in oracle/) on a bounded sample of vocabulary rows.
+the stream the kernel runs on. `cpu_baseline` times the reference's CPU path (restated in oracle/:
+the scalar LM head of src/cpu_reference.cpp:643-665, then the config's selection or verify) on a
+bounded sample of each config, one thread; its `value` is config 2's.
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
 from __future__ import annotations
@@ -99,26 +100,109 @@ def cpu_model():
     return platform.processor() or platform.machine()
 
 
-def cpu_baseline(host, hidden_rows, n_rows: int):
-    """Scalar single-thread LM head + softcap + greedy argmax over `n_rows` full rows (every
-    vocabulary row each), the oracle's restatement of cpu_reference.cpp:643-665 and
-    sampling.cpp:97-104, on the same weights and hidden states the GPU uses."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle as O
+def _head_arrays(host):
     wpr, gpr = D // 8, D // G
     W = host[: V * wpr * 4].view(np.uint32).reshape(V, wpr)
     S = host[V * wpr * 4: V * wpr * 4 + V * gpr * 2].view(np.uint16).reshape(V, gpr)
     B = host[V * wpr * 4 + V * gpr * 2:].view(np.uint16).reshape(V, gpr)
+    return W, S, B
+
+
+def _rows_f32(rows_bf16):
+    return (np.asarray(rows_bf16, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def cpu_baseline(host, work: dict, rows2: int):
+    """The reference's CPU path, restated in oracle/ (built -O3, one thread), on the same
+    weights, hidden rows, histories and parameters the GPU legs use: the scalar LM head
+    (cpu_reference.cpp:643-665) with softcap for every row, then per config what the engine
+    does with the row -- greedy argmax (config 2), apply_repetition_penalty + sample_token
+    (sampling.cpp:74-169; configs 3 and 5), evaluate_verification's greedy branch
+    (speculator.cpp:34-69; config 4) -- and config 1's selection alone on its 1 MB row. Each
+    config runs on a bounded sample; its rows/s is rows / (the sample's wall time)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    W, S, B = _head_arrays(host)
+    where = f"one thread of {cpu_model()}, nproc={os.cpu_count()}"
+    per = {}
+
+    def head_row(hb):
+        return O.lm_head(W, S, B, _rows_f32(hb), D, softcap=CAP)
+
+    # config 2: head + softcap + greedy over `rows2` rows
     t0 = time.perf_counter()
-    for m in range(n_rows):
-        hf = (hidden_rows[m].astype(np.uint32) << 16).view(np.float32)
-        lg = O.lm_head(W, S, B, hf, D, softcap=CAP)
-        _ = O.argmax(lg)
+    for m in range(rows2):
+        O.argmax(head_row(work[2][m]))
     dt = time.perf_counter() - t0
-    return {"value": n_rows / dt, "unit": "rows/s", "cores": 1, "kind": "port",
-            "sample": f"{n_rows} full rows of BASELINE config 2 (all {V} vocabulary rows, fp32 "
-                      f"scalar dot as cpu_reference.cpp:643-665, softcap, argmax) in {dt:.1f} s, "
-                      f"one thread of {cpu_model()}, nproc={os.cpu_count()}"}
+    per["2"] = {"rows_per_s": rows2 / dt, "sample": f"{rows2} rows in {dt:.1f} s"}
+    value = rows2 / dt
+
+    # config 1: selection alone on the 1 MB row (softcapped N(0, 4^2)), greedy and T=.8 k=64
+    # p=.95 u=.37
+    z = work.get(1)
+    reps = 20
+    if z is None:
+        reps = 0
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        O.argmax(z)
+    tg = (time.perf_counter() - t0) / max(reps, 1)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        O.sample_token(z, 0.8, 0.95, 64, u=0.37)
+    ts = (time.perf_counter() - t0) / max(reps, 1)
+    if reps:
+        per["1"] = {"greedy_us_per_row": tg * 1e6, "sampled_us_per_row": ts * 1e6,
+                    "sample": f"{reps} passes each over the {V}-entry row"}
+    if 3 not in work or 4 not in work or 5 not in work:
+        return {"value": value, "unit": "rows/s", "cores": 1, "kind": "port",
+                "sample": f"config 2: {rows2} full rows; oracle built -O3; {where}", "configs": per}
+
+    # config 3: head + penalty over a 4096-id history + sample_token (T .7, k 40, p .9) per step
+    hs3, hist3, us3 = work[3]
+    n3 = 2
+    t0 = time.perf_counter()
+    sel_s = 0.0
+    for i in range(n3):
+        lg = head_row(hs3[i])
+        t1 = time.perf_counter()
+        pen = O.apply_repetition_penalty(lg, hist3[i: i + 4096], 1.1, CAP)
+        O.sample_token(pen, 0.7, 0.9, 40, u=us3[i])
+        sel_s += time.perf_counter() - t1
+    dt = time.perf_counter() - t0
+    per["3"] = {"rows_per_s": n3 / dt, "selection_us_per_row": sel_s / n3 * 1e6,
+                "sample": f"{n3} steps in {dt:.1f} s (head + penalty + sample_token each)"}
+
+    # config 4: five rows through the head, then the greedy verify of four drafts
+    hs4, drafts4 = work[4]
+    t0 = time.perf_counter()
+    rows = [head_row(hs4[m]) for m in range(5)]
+    t1 = time.perf_counter()
+    O.verify([int(x) for x in drafts4], rows, base_seed=0)
+    tv = time.perf_counter() - t1
+    dt = time.perf_counter() - t0
+    per["4"] = {"rows_per_s": 5 / dt, "verify_us": tv * 1e6,
+                "sample": f"one 5-row verify in {dt:.1f} s"}
+
+    # config 5: per row, head + its own penalty and parameters + sample_token
+    hs5, hist5, prm5 = work[5]
+    n5 = 2
+    t0 = time.perf_counter()
+    sel_s = 0.0
+    for m in range(n5):
+        lg = head_row(hs5[m])
+        T, p, k, u = prm5[m]
+        t1 = time.perf_counter()
+        pen = O.apply_repetition_penalty(lg, hist5[2048 * m: 2048 * (m + 1)], 1.1, CAP)
+        O.sample_token(pen, T, p, k, u=u)
+        sel_s += time.perf_counter() - t1
+    dt = time.perf_counter() - t0
+    per["5"] = {"rows_per_s": n5 / dt, "selection_us_per_row": sel_s / n5 * 1e6,
+                "sample": f"rows 0..{n5 - 1} of the 64 in {dt:.1f} s"}
+    return {"value": value, "unit": "rows/s", "cores": 1, "kind": "port",
+            "sample": f"config 2: {rows2} full rows (all {V} vocabulary rows, fp32 scalar dot as "
+                      f"cpu_reference.cpp:643-665, softcap, argmax); oracle built -O3; {where}",
+            "configs": per}
 
 
 def measured_traffic():
@@ -141,7 +225,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--configs", default="1,2,3,4,5")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=8, help="full rows in the CPU baseline (about 14 s)")
+    ap.add_argument("--cpu-rows", type=int, default=3,
+                    help="full rows of config 2 in the CPU baseline (each about 1.7 s; the other "
+                         "configs add about 15 s)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (FETCH_SIZE/WRITE_SIZE calibration)")
     args = ap.parse_args()
@@ -169,6 +255,7 @@ def main():
     twd = importlib.import_module("turbo-winfare-dense_amd")
     cfgs = {int(c) for c in args.configs.split(",") if c}
     cfgs.add(2)
+    work = {}  # each config's inputs, for the CPU baseline
 
     log(f"generating the synthetic head V={V} d={D} ({HEAD_BYTES / 1e6:.1f} MB) on {dev}")
     wsb = torch.empty(HEAD_BYTES, dtype=torch.uint8, device=dev)
@@ -216,6 +303,7 @@ def main():
         z = np.random.default_rng(1).standard_normal(V).astype(np.float32) * 4.0
         z = (30.0 * np.tanh(z / 30.0)).astype(np.float32)
         zr = torch.from_numpy(z).to(dev).view(1, V)
+        work[1] = z
         t1 = torch.empty(1, dtype=torch.int32, device=dev)
         p_g = [twd.RowParams(0.0, 1.0, 0, 1.0, 0.0, CAP, 0, 0)]
         p_s = [twd.RowParams(0.8, 0.95, 64, 1.0, 0.37, CAP, 0, 0)]
@@ -241,6 +329,8 @@ def main():
         # the history is a sliding 4096-id window; uniforms follow seed_for(sp, position)
         prm = [[twd.RowParams(0.7, 0.9, 40, 1.1, twd.uniform_from_seed(twd.seed_for(sp, 4096 + i)),
                               CAP, i, 4096)] for i in range(n3 + 20)]
+        work[3] = (hp3[:4].cpu().numpy().view(np.uint16).reshape(-1, D), hist.cpu().numpy().view(np.uint32),
+                   [prm[i][0].uniform for i in range(4)])
 
         def step3(i):
             head.sample(hp3[i % n3], prm[i % len(prm)], history=hist, logits=lg3, tokens=t3,
@@ -275,6 +365,7 @@ def main():
         hp4 = hidden_pool(torch, dev, 64, 5, 4)
         drafts = torch.from_numpy(np.random.default_rng(4).integers(0, V, (64, 4)).astype(np.int32)).to(dev)
         res4 = torch.zeros(twd.twd.VERIFY_WORDS, dtype=torch.int32, device=dev)
+        work[4] = (hp4[0].cpu().numpy().view(np.uint16), drafts[0].cpu().numpy().view(np.uint32))
 
         def step4(i):
             head.verify_greedy(hp4[i % 64], drafts[i % 64], result=res4, stream=stream)
@@ -316,6 +407,8 @@ def main():
                 for m in range(64)]
         lg5 = torch.empty(64, V, dtype=torch.float32, device=dev)
         t5 = torch.empty(64, dtype=torch.int32, device=dev)
+        work[5] = (hp5[0].cpu().numpy().view(np.uint16), hist5.cpu().numpy().view(np.uint32),
+                   [(p.temperature, p.top_p, p.top_k, p.uniform) for p in prm5])
 
         def step5(i):
             head.sample(hp5[i % 8], prm5, history=hist5, logits=lg5, tokens=t5, stream=stream)
@@ -355,9 +448,9 @@ def main():
                "hidden_sha256": hashlib.sha256(hp.cpu().numpy().tobytes()).hexdigest()}
     cpu = None
     if not args.no_cpu_baseline:
-        log(f"cpu baseline: scalar LM head, {args.cpu_rows} full rows")
-        cpu = cpu_baseline(host, hp[: args.cpu_rows].cpu().numpy().view(np.uint16).reshape(-1, D),
-                           args.cpu_rows)
+        log(f"cpu baseline: every config's CPU path, config 2 on {args.cpu_rows} full rows")
+        work[2] = hp[: args.cpu_rows].cpu().numpy().view(np.uint16).reshape(-1, D)
+        cpu = cpu_baseline(host, work, args.cpu_rows)
 
     achieved = bytes2 / step_s
     traffic, traffic_src = measured_traffic()

@@ -127,6 +127,20 @@ TWD_API int twd_head_verify_greedy(twd_head* head, const uint16_t* hidden_bf16, 
                                    const uint32_t* drafts, uint32_t n_drafts, float* logits,
                                    twd_verify_result* result, void* stream);
 
+/* ---- calls on several streams, and the grid-finish state -------------------------------------
+ * The greedy and verify passes finish on the device: every block folds its per-row maxima into
+ * the head's finish state with atomics and the last block to arrive writes the result. That
+ * state, the M > 8 staging of h and the head's selection scratch are shared by the head's calls,
+ * so calls that arrive on another stream than the previous call are ordered after it (the
+ * first change of stream waits for the device once; after that each call records an event
+ * and a call on another stream waits for it). A head is driven by one host thread at a time.
+ * The arrival count carries each launch's own epoch, so a count left behind by anything else
+ * never decides which block finishes.
+ *
+ * No counterpart in the reference: the device address of that state (64 per-row uint64 maxima,
+ * then the uint64 arrival counter {epoch << 32 | arrivals}), for diagnostics and tests. */
+TWD_API void* twd_head_finish_state(const twd_head* head);
+
 /* ---- the same passes with the final RMSNorm as their prologue --------------------------------
  * h[m] = x[m] * (1 / sqrt(mean(x[m]^2) + eps)) * norm_weight, the model's last step before the
  * head (src/runner.cpp:1889-1918, shaders/RMSNormK.hlsl with has_weight = 1, eps = 1e-6 there;
@@ -208,13 +222,71 @@ typedef struct twd_generator twd_generator;
 TWD_API int twd_generator_create(twd_head* head, const twd_generation_params* params,
                                  const uint32_t* prompt, uint32_t prompt_len,
                                  const uint32_t* stop_ids, uint32_t n_stop, twd_generator** out);
+
+/* The reference's own generation options and token callback, layout-identical to
+ * include/g4dense/c_api.h:24-40 of the reference. They are declared here only when that header
+ * has not been included first, so a caller that already holds the reference's struct passes it
+ * unchanged (include c_api.h before this header). */
+#ifndef G4DENSE_C_API_H
+typedef struct {
+    int max_tokens;
+    float temperature;
+    float top_p;
+    int top_k;
+    float repetition_penalty;
+    int has_seed;
+    unsigned long long seed;
+    const char* system_prompt;
+    const char* const* stop_strings;
+    int stop_count;
+    int tier_id;
+} G4DenseGenerationOptions;
+typedef int (*G4DenseTokenCallback)(void* user, int index, unsigned int token_id, const char* delta);
+#endif
+
+/* Why a generation finished (twd_generator_stop_reason). */
+#define TWD_STOP_NONE 0        /* still running */
+#define TWD_STOP_MAX_TOKENS 1  /* max_tokens ids emitted */
+#define TWD_STOP_TOKEN 2       /* a stop id was sampled (it is the history's last id) */
+#define TWD_STOP_CALLBACK 3    /* the token callback returned 0 (its id is the last one) */
+#define TWD_STOP_CANCELLED 4   /* twd_generator_cancel; the step sampled nothing */
+#define TWD_STOP_DEGENERATE 5  /* sample_token's degenerate-distribution error */
+
+/* twd_generator_create with the options g4dense_engine_generate_ex receives
+ * (src/c_api.cpp:121-162): max_tokens and the sampling fields are taken as c_api.cpp:132-140
+ * maps them (a NULL opts means GenerationOptions' defaults: 512 tokens, greedy). system_prompt,
+ * stop_strings, stop_count and tier_id are ignored, as generate_ex ignores the first three and
+ * the memory tiers are not on this path. max_tokens <= 0 emits nothing. on_token (may be NULL)
+ * is called once per emitted id, on the thread that runs the step, with (user, index, id, "")
+ * where index counts emitted ids from 0 and the text piece is empty (detokenising is not on
+ * this path); a return of 0 ends the generation after that id (runner.cpp:2330-2333,
+ * c_api.cpp:148-155). With a callback every step reads its id back. Stop ids are checked after
+ * the callback, as runner.cpp:2336 does. */
+TWD_API int twd_generator_create_ex(twd_head* head, const G4DenseGenerationOptions* opts,
+                                    const uint32_t* prompt, uint32_t prompt_len,
+                                    const uint32_t* stop_ids, uint32_t n_stop,
+                                    G4DenseTokenCallback on_token, void* user,
+                                    twd_generator** out);
+/* The cancel flag of ForwardRunner::generate (src/runner.cpp:2064, tested at the start of each
+ * step, :2315). Safe to call from any thread while another runs steps: the next step samples
+ * nothing and finishes the generation with TWD_STOP_CANCELLED (it returns TWD_OK, sets
+ * *finished and leaves *token_out untouched). */
+TWD_API void twd_generator_cancel(twd_generator* gen);
+/* TWD_STOP_* of the generation (TWD_STOP_NONE while it runs). */
+TWD_API int twd_generator_stop_reason(const twd_generator* gen);
 TWD_API void twd_generator_destroy(twd_generator* gen);
-/* One step on a bf16 hidden state [d_model]. With token_out or finished given, the token is
- * brought to the host (4 bytes, the call then waits for the stream) and the stop rules are
- * applied; a degenerate distribution returns TWD_E_DEGENERATE. Without them the call only
- * enqueues, and the stop rules see max_tokens alone. */
+/* One step on a bf16 hidden state [d_model]. With token_out or finished given (or a token
+ * callback registered), the token is brought to the host (4 bytes, the call then waits for the
+ * stream) and the stop rules are applied; a degenerate distribution returns TWD_E_DEGENERATE.
+ * Without them the call only enqueues: the stop rules see max_tokens alone until
+ * twd_generator_sync applies them to the ids emitted so far. */
 TWD_API int twd_generator_step(twd_generator* gen, const uint16_t* hidden_bf16, void* stream,
                                uint32_t* token_out, int* finished);
+/* Waits for the device and applies the stop rules to the ids emitted since the last readback,
+ * in order: the history is cut after the first stop id, or before the first degenerate draw
+ * (returning TWD_E_DEGENERATE), and *finished (may be NULL) tells whether the generation is
+ * over. Steps enqueued without readback past such an id are discarded this way. */
+TWD_API int twd_generator_sync(twd_generator* gen, int* finished);
 /* The same step with the final RMSNorm as the head's prologue (fp32 x [d_model]). */
 TWD_API int twd_generator_step_rmsnorm(twd_generator* gen, const float* x,
                                        const uint16_t* norm_weight, float eps, void* stream,
@@ -222,7 +294,9 @@ TWD_API int twd_generator_step_rmsnorm(twd_generator* gen, const float* x,
 /* The device history (prompt then sampled ids) and its current length. */
 TWD_API int twd_generator_history(const twd_generator* gen, const uint32_t** history_dev,
                                   uint32_t* len);
-/* The history copied to host memory (at most `capacity` ids); waits for the device. */
+/* The history copied to host memory (at most `capacity` ids); waits for the device. Ids of
+ * steps that were enqueued without readback are copied as they are: call twd_generator_sync
+ * first to apply the stop rules to them. */
 TWD_API int twd_generator_tokens(const twd_generator* gen, uint32_t* host_out, uint32_t capacity,
                                  uint32_t* len);
 
@@ -269,9 +343,11 @@ TWD_API int twd_verify_draft(twd_selector* sel, const float* logits, uint32_t vo
  * reference's API; it is for callers and tests that check the engine against an in-order fp32
  * loop (the sums of compute_softmax, src/speculator.cpp:22-26, and of the residual draw,
  * :104-116, are formed that way). terms: n finite values >= 0 in device memory, 16-byte
- * aligned and readable up to n rounded up to a multiple of 16 floats. *sum_out (device)
- * receives ((t0 + t1) + t2) + ... in fp32; when stop_out (device) is non-NULL it receives the
- * first index whose prefix sum is >= thr, or n when none is. Asynchronous on `stream`. */
+ * aligned and readable up to n rounded up to a multiple of 16 floats. With stop_out NULL,
+ * *sum_out (device) receives the full in-order fp32 sum ((t0 + t1) + t2) + ... . With stop_out
+ * (device) given, the sum stops at the first index i whose prefix sum t0 + ... + ti is >= thr:
+ * *stop_out receives i and *sum_out that prefix sum; when no prefix reaches thr, *stop_out
+ * receives n and *sum_out the full sum. Asynchronous on `stream`. */
 TWD_API int twd_sequential_sum(const float* terms, uint32_t n, float thr, float* sum_out,
                                uint32_t* stop_out, void* stream);
 

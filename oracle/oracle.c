@@ -272,6 +272,7 @@ int or_verify(const uint32_t* drafts, size_t n_drafts, const float* const* rows,
               uint32_t vocab, float temperature, float top_p, int top_k, uint64_t base_seed,
               or_verify_result* out) {
     memset(out, 0, sizeof(*out));
+    if (n_drafts > OR_MAX_DRAFTS) return OR_ERR_INVALID;
     out->total_drafted = (uint32_t)n_drafts;
     if (n_drafts == 0 || n_rows == 0) return OR_OK;
     const size_t k = n_drafts < n_rows ? n_drafts : n_rows;
@@ -387,6 +388,7 @@ int or_verify_draft(const uint32_t* drafts, size_t n_drafts, const float* const*
                     float repetition_penalty, uint64_t base_seed, or_verify_result* out,
                     or_reject_diag* diag) {
     memset(out, 0, sizeof(*out));
+    if (n_drafts > OR_MAX_DRAFTS) return OR_ERR_INVALID;
     out->total_drafted = (uint32_t)n_drafts;
     if (n_drafts == 0 || n_rows == 0) return OR_OK;
     const int greedy = temperature <= 0.0f && repetition_penalty == 1.0f; /* sampling.hpp:17 */

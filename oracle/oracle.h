@@ -43,8 +43,11 @@ typedef struct {
     float u;             /* the uniform actually used */
 } or_sample_diag;
 
+/* The verify entry points take at most OR_MAX_DRAFTS drafts (OR_ERR_INVALID beyond). */
+#define OR_MAX_DRAFTS 1024
+
 typedef struct {
-    uint32_t tokens[65];      /* accepted drafts + the correction or bonus token */
+    uint32_t tokens[OR_MAX_DRAFTS + 1]; /* accepted drafts + the correction or bonus token */
     uint32_t n_tokens;
     uint32_t num_accepted;
     uint32_t total_drafted;

@@ -36,9 +36,12 @@ class SampleDiag(C.Structure):
     ]
 
 
+OR_MAX_DRAFTS = 1024
+
+
 class VerifyResult(C.Structure):
     _fields_ = [
-        ("tokens", C.c_uint32 * 65),
+        ("tokens", C.c_uint32 * (OR_MAX_DRAFTS + 1)),
         ("n_tokens", C.c_uint32),
         ("num_accepted", C.c_uint32),
         ("total_drafted", C.c_uint32),

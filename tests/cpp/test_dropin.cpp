@@ -171,6 +171,41 @@ int main() {
         }
     }
     std::puts("draft-logits verify ok");
+
+    // evaluate_verification has no bound on the number of drafts (speculator.cpp:50): 100
+    // drafts against 101 rows, greedy and sampled, each row's expected id from sample_token
+    // with the step seed splitmix64(base + i) (:56)
+    {
+        const uint32_t V = 1536, K = 100;
+        std::mt19937 gen(4242);
+        std::normal_distribution<float> nd(0.0f, 2.0f);
+        std::vector<std::vector<float>> rows(K + 1, std::vector<float>(V));
+        for (auto& r : rows)
+            for (auto& x : r) x = nd(gen);
+        std::vector<const float*> ptrs;
+        for (auto& r : rows) ptrs.push_back(r.data());
+        const uint64_t base = 31337;
+        for (int sampled = 0; sampled < 2; ++sampled) {
+            SamplingParams sp = sampled ? SamplingParams{0.8f, 0.9f, 40, 1.0f, false, 0}
+                                        : SamplingParams{};
+            std::vector<uint32_t> want;
+            for (uint32_t i = 0; i <= K; ++i) want.push_back(sample_token(ptrs[i], V, sp, splitmix64(base + i)));
+            // all accepted: 100 drafts, then the bonus row's id
+            std::vector<uint32_t> drafts(want.begin(), want.begin() + K);
+            SpeculativeCoordinator spec;
+            auto all = spec.evaluate_verification(drafts, ptrs, V, sp, base);
+            CHECK(all.num_accepted == K && all.bonus_token_sampled && all.bonus_token == want[K]);
+            CHECK(all.accepted_tokens.size() == K + 1 && all.accepted_tokens == want);
+            CHECK(all.total_drafted == K);
+            // a mismatch at position 77, in the second batch of 64: 77 accepted + the correction
+            drafts[77] = (drafts[77] + 1) % V;
+            auto miss = spec.evaluate_verification(drafts, ptrs, V, sp, base);
+            CHECK(miss.num_accepted == 77 && miss.bonus_token_sampled && miss.bonus_token == want[77]);
+            CHECK(miss.accepted_tokens.size() == 78 && miss.accepted_tokens[77] == want[77]);
+            CHECK(spec.total_draft_tokens() == 2 * K && spec.total_accepted_tokens() == K + 77);
+        }
+    }
+    std::puts("100-draft verify ok");
     std::puts("ALL OK");
     return 0;
 }

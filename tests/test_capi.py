@@ -22,7 +22,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(LIB)
     syms = declared_symbols()
-    assert len(syms) == 36, syms
+    assert len(syms) == 41, syms
     missing = [s for s in syms if not hasattr(lib, s)]
     assert not missing, missing
 
@@ -132,3 +132,64 @@ def test_generator_and_probe_argument_errors_without_gpu():
     assert lib.twd_probe_read_bandwidth(buf.ctypes.data, 4096, 8, 1, None, ctypes.byref(us),
                                         ctypes.byref(nb)) == t.twd.TWD_E_INVALID
     assert "stripes" in t.twd.last_error()
+
+
+OPTION_FIELDS = ["max_tokens", "temperature", "top_p", "top_k", "repetition_penalty", "has_seed",
+                 "seed", "system_prompt", "stop_strings", "stop_count", "tier_id"]
+
+
+def _layout_of(tmp_path, include_lines, name):
+    """sizeof and every field offset of G4DenseGenerationOptions as a C compiler sees it."""
+    src = tmp_path / f"{name}.c"
+    body = "\n".join(f'    printf("%zu\\n", offsetof(G4DenseGenerationOptions, {f}));'
+                     for f in OPTION_FIELDS)
+    src.write_text("#include <stddef.h>\n#include <stdio.h>\n" + include_lines +
+                   "\nint main(void) {\n    printf(\"%zu\\n\", sizeof(G4DenseGenerationOptions));\n"
+                   + body + "\n    return 0;\n}\n")
+    exe = tmp_path / name
+    subprocess.run(["gcc", "-std=c11", "-I" + os.path.join(ROOT, "include"), str(src), "-o",
+                    str(exe)], check=True, capture_output=True)
+    return [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True,
+                                           check=True).stdout.split()]
+
+
+def test_generation_options_layout(tmp_path):
+    # twd_head.h declares the reference's G4DenseGenerationOptions (c_api.h:24-36) when the
+    # reference header is absent; both must give the same layout, and the ctypes mirror too
+    t = twd()
+    ours = _layout_of(tmp_path, '#include "twd_head.h"', "ours")
+    ct = t.twd.GenerationOptions
+    assert ours == [ctypes.sizeof(ct)] + [getattr(ct, f).offset for f in OPTION_FIELDS]
+    ref_h = "/root/reference/include/g4dense/c_api.h"
+    if os.path.exists(ref_h):
+        theirs = _layout_of(tmp_path, f'#include "{ref_h}"', "theirs")
+        assert ours == theirs
+        # the reference header first, then ours: one declaration, no conflict
+        both = _layout_of(tmp_path, f'#include "{ref_h}"\n#include "twd_head.h"', "both")
+        assert both == theirs
+
+
+def test_options_default_mirror():
+    # g4dense_options_default's values (c_api.cpp:40-53 of the reference)
+    t = twd()
+    o = t.twd.options_default()
+    assert (o.max_tokens, o.top_k, o.has_seed, o.seed, o.stop_count, o.tier_id) == (512, 64, 0, 0, 0, 1)
+    assert np.float32(o.temperature) == np.float32(0.2) and np.float32(o.top_p) == np.float32(0.95)
+    assert o.repetition_penalty == 1.0 and not o.system_prompt and not o.stop_strings
+
+
+def test_generator_ex_argument_errors_without_gpu():
+    t = twd()
+    lib = t.twd.lib
+    out = ctypes.c_void_p()
+    o = t.twd.options_default()
+    prompt = (ctypes.c_uint32 * 2)(1, 2)
+    assert lib.twd_generator_create_ex(None, ctypes.byref(o), prompt, 2, None, 0,
+                                       t.twd.TokenCallback(), None,
+                                       ctypes.byref(out)) == t.twd.TWD_E_INVALID
+    assert "null head" in t.twd.last_error()
+    fin = ctypes.c_int()
+    assert lib.twd_generator_sync(None, ctypes.byref(fin)) == t.twd.TWD_E_INVALID
+    assert lib.twd_generator_stop_reason(None) == t.twd.STOP_NONE
+    lib.twd_generator_cancel(None)  # a no-op on a null generator
+    assert lib.twd_head_finish_state(None) is None

@@ -275,3 +275,39 @@ def test_cpp_dropin_program():
     res = subprocess.run([exe], capture_output=True, text=True, timeout=120)
     print(res.stdout, res.stderr)
     assert res.returncode == 0 and "ALL OK" in res.stdout
+
+
+@pytest.mark.parametrize("n", [1000, V])
+def test_plus_inf_rows(env, oracle, n):
+    # A row holding +inf has exp(+inf - max) = exp(NaN) in sample_token's total
+    # (sampling.cpp:112-115), so the total is NaN and the reference throws (:116-118): the device
+    # reports the degenerate id. Greedy takes the first +inf (strict '>', :97-104). A +inf that
+    # the penalty clamps to 0.9999 * cap (:79-87) is finite again and samples normally.
+    torch, dev, t, sel = env
+    rng = np.random.default_rng(77 + n)
+    base = (rng.standard_normal(n) * 3).astype(np.float32)
+    one = base.copy()
+    one[n // 3] = np.inf
+    two = base.copy()
+    two[[n // 5, n - 2]] = np.inf
+    both = base.copy()
+    both[[3, n // 2]] = [np.inf, -np.inf]
+    rows = [one, two, both, two, one]
+    params = [rp(t, 0.8, 0.95, 64, 0.37), rp(t, 1.0, 1.0, 0, 0.5), rp(t, 0.7, 0.9, 40, 0.1),
+              rp(t, 0.0, 1.0, 0, 0.0), rp(t, 0.0, 1.0, 0, 0.0)]
+    tok, _ = select_rows(env, np.stack(rows), params)
+    for i in range(3):
+        with pytest.raises(RuntimeError):
+            oracle.sample_token(rows[i], params[i].temperature, params[i].top_p, params[i].top_k,
+                                u=params[i].uniform)
+        assert int(tok[i]) == t.TOKEN_DEGENERATE, i
+    assert int(tok[3]) == n // 5 == oracle.argmax(two)
+    assert int(tok[4]) == n // 3 == oracle.argmax(one)
+    # the penalty clamps the +inf of an id in the history, after which the row is finite
+    hist = np.array([n // 3, 5, n // 3], np.uint32)
+    p = [rp(t, 0.8, 0.95, 64, 0.37, rep=1.1, cap=30.0, off=0, n=3)]
+    tok, pen = select_rows(env, one[None, :], p, history=hist)
+    want_pen = oracle.apply_repetition_penalty(one, hist, 1.1, 30.0)
+    assert np.isfinite(want_pen).all()
+    assert np.array_equal(pen[0].view(np.uint32), want_pen.view(np.uint32))
+    assert int(tok[0]) == oracle.sample_token(want_pen, 0.8, 0.95, 64, u=0.37)

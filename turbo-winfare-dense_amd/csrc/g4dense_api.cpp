@@ -150,6 +150,11 @@ G4_API uint32_t sample_token(const float* logits, uint32_t vocab, const Sampling
     return tok;
 }
 
+// evaluate_verification (speculator.cpp:34-153) has no bound on the number of drafts; the
+// device entry points take at most TWD_MAX_ROWS per call. Longer drafts are verified in batches
+// of TWD_MAX_ROWS positions in order: a batch whose drafts are all accepted hands over to the
+// next, whose positions keep their global index in the seeds (base_seed + i, speculator.cpp:56,
+// 88) by passing base_seed + batch start. Only the last batch may add the bonus row.
 G4_API SpeculativeEvaluation SpeculativeCoordinator::evaluate_verification(
     const std::vector<uint32_t>& draft_tokens, const std::vector<const float*>& target_logits_per_pos,
     uint32_t vocab_size, const SamplingParams& sampling, uint64_t base_seed,
@@ -159,61 +164,70 @@ G4_API SpeculativeEvaluation SpeculativeCoordinator::evaluate_verification(
     total_draft_tokens_ += eval.total_drafted;
     if (draft_tokens.empty() || target_logits_per_pos.empty()) return eval;
     const size_t k = std::min(draft_tokens.size(), target_logits_per_pos.size());
-    if (k > TWD_MAX_ROWS) throw G4DenseFormatError("evaluate_verification: more than 64 drafts");
-    const uint32_t rows = static_cast<uint32_t>(std::min(target_logits_per_pos.size(), k + 1));
-    // positions whose draft probabilities select the rejection branch (speculator.cpp:72)
-    uint32_t n_draft_rows = 0;
+    const size_t rows_all = std::min(target_logits_per_pos.size(), k + 1);
     if (!sampling.is_greedy()) {
-        for (size_t i = 0; i < k && i < draft_logits.size(); ++i) {
-            if (draft_logits[i].empty()) continue;
-            if (draft_logits[i].size() < vocab_size)
+        for (size_t i = 0; i < k && i < draft_logits.size(); ++i)
+            if (!draft_logits[i].empty() && draft_logits[i].size() < vocab_size)
                 throw G4DenseFormatError("evaluate_verification: a draft logit row is shorter than vocab_size");
-            n_draft_rows = static_cast<uint32_t>(i + 1);
-        }
     }
 
     Staging& s = staging();
     std::lock_guard<std::mutex> lock(s.mu);
-    ensure(s, vocab_size, rows, 0);
-    for (uint32_t i = 0; i < rows; ++i)
-        check_hip(hipMemcpy(s.logits + static_cast<size_t>(i) * vocab_size, target_logits_per_pos[i],
-                            vocab_size * sizeof(float), hipMemcpyHostToDevice), "upload rows");
-    check_hip(hipMemcpy(s.drafts, draft_tokens.data(), k * sizeof(uint32_t), hipMemcpyHostToDevice),
-              "upload drafts");
-    twd_row_params r = row_params(sampling, 0.0f);
-    if (n_draft_rows == 0) {
-        if (twd_verify(s.sel, s.logits, vocab_size, rows, vocab_size, &r, base_seed, s.drafts,
-                       static_cast<uint32_t>(k), s.vres, nullptr) != TWD_OK)
-            throw_last("evaluate_verification");
-    } else {
-        const size_t need = static_cast<size_t>(n_draft_rows) * vocab_size;
-        if (s.dlogits_cap < need) {
-            if (s.dlogits) check_hip(hipFree(s.dlogits), "hipFree");
-            s.dlogits = nullptr;
-            check_hip(hipMalloc(&s.dlogits, need * sizeof(float)), "hipMalloc draft rows");
-            s.dlogits_cap = need;
+    for (size_t b0 = 0; b0 < k; b0 += TWD_MAX_ROWS) {
+        const uint32_t kb = static_cast<uint32_t>(std::min<size_t>(TWD_MAX_ROWS, k - b0));
+        const bool last = b0 + kb == k;
+        // rows of this batch: its kb positions, plus the bonus row after the final draft
+        const uint32_t rows = last ? static_cast<uint32_t>(rows_all - b0) : kb;
+        // positions of this batch whose draft probabilities select the rejection branch
+        // (speculator.cpp:72)
+        uint32_t n_draft_rows = 0;
+        if (!sampling.is_greedy()) {
+            for (uint32_t i = 0; i < kb && b0 + i < draft_logits.size(); ++i)
+                if (!draft_logits[b0 + i].empty()) n_draft_rows = i + 1;
         }
-        const float* dptr[TWD_MAX_ROWS] = {};
-        for (uint32_t i = 0; i < n_draft_rows; ++i) {
-            if (draft_logits[i].empty()) continue;
-            float* dst = s.dlogits + static_cast<size_t>(i) * vocab_size;
-            check_hip(hipMemcpy(dst, draft_logits[i].data(), vocab_size * sizeof(float),
-                                hipMemcpyHostToDevice), "upload draft rows");
-            dptr[i] = dst;
+        ensure(s, vocab_size, rows, 0);
+        for (uint32_t i = 0; i < rows; ++i)
+            check_hip(hipMemcpy(s.logits + static_cast<size_t>(i) * vocab_size, target_logits_per_pos[b0 + i],
+                                vocab_size * sizeof(float), hipMemcpyHostToDevice), "upload rows");
+        check_hip(hipMemcpy(s.drafts, draft_tokens.data() + b0, kb * sizeof(uint32_t), hipMemcpyHostToDevice),
+                  "upload drafts");
+        twd_row_params r = row_params(sampling, 0.0f);
+        const uint64_t seed = base_seed + b0;
+        if (n_draft_rows == 0) {
+            if (twd_verify(s.sel, s.logits, vocab_size, rows, vocab_size, &r, seed, s.drafts, kb, s.vres,
+                           nullptr) != TWD_OK)
+                throw_last("evaluate_verification");
+        } else {
+            const size_t need = static_cast<size_t>(n_draft_rows) * vocab_size;
+            if (s.dlogits_cap < need) {
+                if (s.dlogits) check_hip(hipFree(s.dlogits), "hipFree");
+                s.dlogits = nullptr;
+                check_hip(hipMalloc(&s.dlogits, need * sizeof(float)), "hipMalloc draft rows");
+                s.dlogits_cap = need;
+            }
+            const float* dptr[TWD_MAX_ROWS] = {};
+            for (uint32_t i = 0; i < n_draft_rows; ++i) {
+                if (draft_logits[b0 + i].empty()) continue;
+                float* dst = s.dlogits + static_cast<size_t>(i) * vocab_size;
+                check_hip(hipMemcpy(dst, draft_logits[b0 + i].data(), vocab_size * sizeof(float),
+                                    hipMemcpyHostToDevice), "upload draft rows");
+                dptr[i] = dst;
+            }
+            r.repetition_penalty = sampling.repetition_penalty;  // is_greedy() needs it
+            if (twd_verify_draft(s.sel, s.logits, vocab_size, rows, vocab_size, dptr, n_draft_rows, &r, seed,
+                                 s.drafts, kb, s.vres, nullptr) != TWD_OK)
+                throw_last("evaluate_verification");
         }
-        r.repetition_penalty = sampling.repetition_penalty;  // is_greedy() needs it
-        if (twd_verify_draft(s.sel, s.logits, vocab_size, rows, vocab_size, dptr, n_draft_rows, &r,
-                             base_seed, s.drafts, static_cast<uint32_t>(k), s.vres, nullptr) != TWD_OK)
-            throw_last("evaluate_verification");
+        twd_verify_result v{};
+        check_hip(hipMemcpy(&v, s.vres, sizeof(v), hipMemcpyDeviceToHost), "download result");
+        if (v.n_tokens == TWD_TOKEN_DEGENERATE)
+            throw G4DenseFormatError("sample_token: logit distribution is degenerate");
+        eval.accepted_tokens.insert(eval.accepted_tokens.end(), v.tokens, v.tokens + v.n_tokens);
+        eval.num_accepted += v.num_accepted;
+        eval.bonus_token_sampled = v.bonus_token_sampled != 0;
+        eval.bonus_token = v.bonus_token;
+        if (v.num_accepted < kb) break;  // a correction ended the verification
     }
-    twd_verify_result v{};
-    check_hip(hipMemcpy(&v, s.vres, sizeof(v), hipMemcpyDeviceToHost), "download result");
-    if (v.n_tokens == TWD_TOKEN_DEGENERATE)
-        throw G4DenseFormatError("sample_token: logit distribution is degenerate");
-    eval.accepted_tokens.assign(v.tokens, v.tokens + v.n_tokens);
-    eval.num_accepted = v.num_accepted;
-    eval.bonus_token_sampled = v.bonus_token_sampled != 0;
-    eval.bonus_token = v.bonus_token;
     total_accepted_tokens_ += eval.num_accepted;
     eval.acceptance_rate =
         eval.total_drafted == 0 ? 0.0 : static_cast<double>(eval.num_accepted) / eval.total_drafted;

@@ -41,10 +41,11 @@ struct HeadArgs {
     float softcap;
     float* logits;
     uint32_t vocab;
-    // greedy finish: running per-row maxima and the arrival count, both zero between
-    // launches, and where the last block puts its results
+    // greedy finish: running per-row maxima (zero between launches), the arrival counter
+    // {epoch, count} and this launch's epoch, and where the last block puts its results
     uint64_t* gbest;    // [TWD_MAX_ROWS]
-    uint32_t* gcount;
+    uint64_t* gctr;
+    uint32_t epoch;
     uint32_t* tokens;
     const uint32_t* drafts;
     uint32_t n_drafts;
@@ -182,12 +183,17 @@ using EpiShared = EpiSharedT<kHeadWaves>;
 // whole grid, finished by the last block to arrive (tokens, then greedy verify bookkeeping).
 //
 // Cross-block publication uses device-scope atomics only: each block folds its ranks into
-// gbest[m] with a returning atomic max, then counts itself in with an atomic add; the block that
-// sees the final count reads and clears gbest with atomic exchanges. Returning atomics are
+// gbest[m] with a returning atomic max, then counts itself in on the arrival counter; the block
+// that completes the count reads and clears gbest with atomic exchanges. Returning atomics are
 // performed at the memory-side coherence point before they return, so every block's maxima
 // precede its arrival, and the last block observes all of them. No data travels through plain
 // stores, so no device-scope fence is needed: on this part such a fence writes back the XCD's
 // L2 and, paid by each of ~1000 blocks, costs more than the streaming pass itself.
+//
+// The counter holds {launch epoch (high 32 bits), arrivals (low 32 bits)}. Each launch carries
+// a fresh epoch; a block that finds another epoch there starts the count at 1 (compare-and-swap),
+// so a count left behind by anything but this launch -- a write from outside, a launch that did
+// not finish -- can never make the wrong block the last one, and nothing has to clear it.
 // tot[j][mt][i] holds row r = (tile0 + j) * 16 + lane % 16 of MFMA row 16 mt + 4 (lane / 16) + i,
 // which carries h row m = (16 mt + 4 (lane / 16) + i) / MS when i is a multiple of MS (MS > 1:
 // the rows are spread over the MFMA rows, see head_small_kernel); other entries are not outputs.
@@ -202,6 +208,12 @@ __device__ __forceinline__ void head_epilogue(const HeadArgs& a, f32x4_t (&tot)[
             for (int i = 0; i < NI; ++i) tot[j][0][i] += __shfl_xor(tot[j][0][i], 32);
     }
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // the counter's current value, a hint for the compare-and-swap below, fetched now so that
+    // its round trip overlaps the epilogue's arithmetic
+    unsigned long long ctr_hint = 0;
+    if (MODE != kModeLogits && tid == 0)
+        ctr_hint = __hip_atomic_load(reinterpret_cast<unsigned long long*>(a.gctr), __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
     uint64_t best[NMT][NI];
 #pragma unroll
     for (int mt = 0; mt < NMT; ++mt)
@@ -254,9 +266,18 @@ __device__ __forceinline__ void head_epilogue(const HeadArgs& a, f32x4_t (&tot)[
                                               __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    if (tid == 0)
-        se.last = __hip_atomic_fetch_add(a.gcount, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                  nb - 1;
+    if (tid == 0) {
+        // every failed exchange means another block counted itself in, so this loop ends after
+        // at most gridDim.x attempts; usually the hint is current and the first one succeeds
+        unsigned long long cur = ctr_hint, want;
+        const unsigned long long ep = static_cast<unsigned long long>(a.epoch) << 32;
+        do {
+            want = ((cur & 0xFFFFFFFF00000000ull) == ep) ? cur + 1 : (ep | 1ull);
+        } while (!__hip_atomic_compare_exchange_strong(reinterpret_cast<unsigned long long*>(a.gctr), &cur,
+                                                       want, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT));
+        se.last = static_cast<uint32_t>(want) == nb;
+    }
     __syncthreads();
     if (!se.last) return;
     // every other block's maximum was performed before its arrival was counted
@@ -268,10 +289,7 @@ __device__ __forceinline__ void head_epilogue(const HeadArgs& a, f32x4_t (&tot)[
         if (a.tokens) a.tokens[tid] = t;
     }
     __syncthreads();
-    if (tid == 0) {
-        __hip_atomic_exchange(a.gcount, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (a.vres) verify_bookkeeping(se.tok, a.M, a.drafts, a.n_drafts, a.vres);
-    }
+    if (tid == 0 && a.vres) verify_bookkeeping(se.tok, a.M, a.drafts, a.n_drafts, a.vres);
 }
 
 // Weight streams: one buffer descriptor per row tile covering its stripe of units, so a unit
@@ -985,7 +1003,11 @@ struct twd_head {
     float softcap = 0.f;
     uint8_t* tiled = nullptr;
     uint64_t tiled_bytes = 0;
-    uint64_t* gbest = nullptr;    // [TWD_MAX_ROWS] + arrival counter, zero between launches
+    // [TWD_MAX_ROWS] per-row maxima (zero between launches), the arrival counter, and the
+    // repack's flag
+    uint64_t* gbest = nullptr;
+    uint32_t epoch = 0;           // of the last launch; 0 is never used
+    StreamOrder order;            // calls on several streams share gbest, hp/hx and sel
     u32x4_t* hp = nullptr;        // prepared h in A-fragment order for M > 8 (prep_hidden_kernel)
     u32x4_t* hx = nullptr;        // its bias A-fragment entries
     twd_selector* sel = nullptr;
@@ -1089,6 +1111,11 @@ int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
     return TWD_OK;
 }
 
+uint32_t next_epoch(twd_head* h) {
+    if (++h->epoch == 0) h->epoch = 1;
+    return h->epoch;
+}
+
 uint32_t* repack_flag(twd_head* h) { return reinterpret_cast<uint32_t*>(h->gbest + TWD_MAX_ROWS + 1); }
 
 int head_repack(twd_head* h, const uint8_t* wsb_dev, hipStream_t stream) {
@@ -1123,7 +1150,8 @@ int launch_head(twd_head* h, const uint16_t* hidden, uint32_t rows, float* logit
     a.logits = logits;
     a.vocab = h->vocab;
     a.gbest = h->gbest;
-    a.gcount = reinterpret_cast<uint32_t*>(h->gbest + TWD_MAX_ROWS);
+    a.gctr = h->gbest + TWD_MAX_ROWS;
+    a.epoch = next_epoch(h);
     a.tokens = tokens;
     a.drafts = drafts;
     a.n_drafts = n_drafts;
@@ -1177,7 +1205,8 @@ int launch_head_rmsnorm(twd_head* h, const float* x, const uint16_t* norm_w, flo
     a.logits = logits;
     a.vocab = h->vocab;
     a.gbest = h->gbest;
-    a.gcount = reinterpret_cast<uint32_t*>(h->gbest + TWD_MAX_ROWS);
+    a.gctr = h->gbest + TWD_MAX_ROWS;
+    a.epoch = next_epoch(h);
     a.tokens = tokens;
     a.drafts = drafts;
     a.n_drafts = n_drafts;
@@ -1203,6 +1232,18 @@ int launch_head_rmsnorm(twd_head* h, const float* x, const uint16_t* norm_w, flo
     head_wide_kernel<1, kRT1, MODE, kHeadWaves><<<blocks_for(h->ntiles, kRT1), kHeadThreads, 0, stream>>>(a, h->hp, h->hx);
     TWD_HIP(hipGetLastError());
     return TWD_OK;
+}
+
+// Runs one call's launches with the head's cross-stream ordering around them.
+template <typename F>
+int ordered(twd_head* h, void* stream, F&& launches) {
+    if (!h) return fail(TWD_E_INVALID, "null head");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    int rc = order_before(h->order, s);
+    if (rc) return rc;
+    rc = launches(s);
+    const int rc2 = order_after(h->order, s);
+    return rc ? rc : rc2;
 }
 
 }  // namespace
@@ -1287,6 +1328,7 @@ TWD_API void twd_head_destroy(twd_head* h) {
     if (h->hx) (void)hipFree(h->hx);
     if (h->sel) twd_selector_destroy(h->sel);
     if (h->norm_w) (void)hipFree(h->norm_w);
+    order_release(h->order);
     delete h;
 }
 
@@ -1307,16 +1349,18 @@ TWD_API int twd_head_logits(twd_head* h, const uint16_t* hidden, uint32_t rows, 
                             void* stream) {
     clear_error();
     if (!logits) return fail(TWD_E_INVALID, "null logits");
-    return launch_head<kModeLogits>(h, hidden, rows, logits, nullptr, nullptr, 0, nullptr,
-                                    static_cast<hipStream_t>(stream));
+    return ordered(h, stream, [&](hipStream_t s) {
+        return launch_head<kModeLogits>(h, hidden, rows, logits, nullptr, nullptr, 0, nullptr, s);
+    });
 }
 
 TWD_API int twd_head_greedy(twd_head* h, const uint16_t* hidden, uint32_t rows, float* logits,
                             uint32_t* tokens, void* stream) {
     clear_error();
     if (!tokens) return fail(TWD_E_INVALID, "null tokens");
-    return launch_head<kModeGreedy>(h, hidden, rows, logits, tokens, nullptr, 0, nullptr,
-                                    static_cast<hipStream_t>(stream));
+    return ordered(h, stream, [&](hipStream_t s) {
+        return launch_head<kModeGreedy>(h, hidden, rows, logits, tokens, nullptr, 0, nullptr, s);
+    });
 }
 
 TWD_API int twd_head_verify_greedy(twd_head* h, const uint16_t* hidden, uint32_t rows,
@@ -1326,37 +1370,42 @@ TWD_API int twd_head_verify_greedy(twd_head* h, const uint16_t* hidden, uint32_t
     if (!result) return fail(TWD_E_INVALID, "null result");
     if (n_drafts > 0 && !drafts) return fail(TWD_E_INVALID, "null drafts");
     if (n_drafts > TWD_MAX_ROWS) return fail(TWD_E_INVALID, "n_drafts must be <= 64");
-    return launch_head<kModeGreedy>(h, hidden, rows, logits, nullptr, drafts, n_drafts, result,
-                                    static_cast<hipStream_t>(stream));
+    return ordered(h, stream, [&](hipStream_t s) {
+        return launch_head<kModeGreedy>(h, hidden, rows, logits, nullptr, drafts, n_drafts, result, s);
+    });
 }
 
 TWD_API int twd_head_sample(twd_head* h, const uint16_t* hidden, uint32_t rows,
                             const twd_row_params* params, const uint32_t* history, float* logits,
                             uint32_t* tokens, void* stream) {
     clear_error();
-    if (!h) return fail(TWD_E_INVALID, "null head");
     if (!logits || !tokens || !params) return fail(TWD_E_INVALID, "null logits, tokens or params");
-    const hipStream_t s = static_cast<hipStream_t>(stream);
-    int rc = launch_head<kModeLogits>(h, hidden, rows, logits, nullptr, nullptr, 0, nullptr, s);
-    if (rc) return rc;
-    return launch_select(h->sel->scratch, logits, h->vocab, rows, h->vocab, params, history,
-                         tokens, s);
+    return ordered(h, stream, [&](hipStream_t s) {
+        int rc = launch_head<kModeLogits>(h, hidden, rows, logits, nullptr, nullptr, 0, nullptr, s);
+        if (rc) return rc;
+        return launch_select(h->sel->scratch, logits, h->vocab, rows, h->vocab, params, history,
+                             tokens, s);
+    });
 }
 
 TWD_API int twd_head_logits_rmsnorm(twd_head* h, const float* x, const uint16_t* norm_w, float eps,
                                     uint32_t rows, float* logits, void* stream) {
     clear_error();
     if (!logits) return fail(TWD_E_INVALID, "null logits");
-    return launch_head_rmsnorm<kModeLogits>(h, x, norm_w, eps, rows, logits, nullptr, nullptr, 0,
-                                            nullptr, static_cast<hipStream_t>(stream));
+    return ordered(h, stream, [&](hipStream_t s) {
+        return launch_head_rmsnorm<kModeLogits>(h, x, norm_w, eps, rows, logits, nullptr, nullptr, 0,
+                                                nullptr, s);
+    });
 }
 
 TWD_API int twd_head_greedy_rmsnorm(twd_head* h, const float* x, const uint16_t* norm_w, float eps,
                                     uint32_t rows, float* logits, uint32_t* tokens, void* stream) {
     clear_error();
     if (!tokens) return fail(TWD_E_INVALID, "null tokens");
-    return launch_head_rmsnorm<kModeGreedy>(h, x, norm_w, eps, rows, logits, tokens, nullptr, 0,
-                                            nullptr, static_cast<hipStream_t>(stream));
+    return ordered(h, stream, [&](hipStream_t s) {
+        return launch_head_rmsnorm<kModeGreedy>(h, x, norm_w, eps, rows, logits, tokens, nullptr, 0,
+                                                nullptr, s);
+    });
 }
 
 TWD_API int twd_head_verify_greedy_rmsnorm(twd_head* h, const float* x, const uint16_t* norm_w,
@@ -1367,8 +1416,10 @@ TWD_API int twd_head_verify_greedy_rmsnorm(twd_head* h, const float* x, const ui
     if (!result) return fail(TWD_E_INVALID, "null result");
     if (n_drafts > 0 && !drafts) return fail(TWD_E_INVALID, "null drafts");
     if (n_drafts > TWD_MAX_ROWS) return fail(TWD_E_INVALID, "n_drafts must be <= 64");
-    return launch_head_rmsnorm<kModeGreedy>(h, x, norm_w, eps, rows, logits, nullptr, drafts, n_drafts,
-                                            result, static_cast<hipStream_t>(stream));
+    return ordered(h, stream, [&](hipStream_t s) {
+        return launch_head_rmsnorm<kModeGreedy>(h, x, norm_w, eps, rows, logits, nullptr, drafts,
+                                                n_drafts, result, s);
+    });
 }
 
 TWD_API int twd_head_sample_rmsnorm(twd_head* h, const float* x, const uint16_t* norm_w, float eps,
@@ -1376,14 +1427,18 @@ TWD_API int twd_head_sample_rmsnorm(twd_head* h, const float* x, const uint16_t*
                                     const uint32_t* history, float* logits, uint32_t* tokens,
                                     void* stream) {
     clear_error();
-    if (!h) return fail(TWD_E_INVALID, "null head");
     if (!logits || !tokens || !params) return fail(TWD_E_INVALID, "null logits, tokens or params");
-    const hipStream_t s = static_cast<hipStream_t>(stream);
-    int rc = launch_head_rmsnorm<kModeLogits>(h, x, norm_w, eps, rows, logits, nullptr, nullptr, 0,
-                                              nullptr, s);
-    if (rc) return rc;
-    return launch_select(h->sel->scratch, logits, h->vocab, rows, h->vocab, params, history,
-                         tokens, s);
+    return ordered(h, stream, [&](hipStream_t s) {
+        int rc = launch_head_rmsnorm<kModeLogits>(h, x, norm_w, eps, rows, logits, nullptr, nullptr, 0,
+                                                  nullptr, s);
+        if (rc) return rc;
+        return launch_select(h->sel->scratch, logits, h->vocab, rows, h->vocab, params, history,
+                             tokens, s);
+    });
+}
+
+TWD_API void* twd_head_finish_state(const twd_head* h) {
+    return h ? static_cast<void*>(h->gbest) : nullptr;
 }
 
 TWD_API int twd_generate_head(void* wsb_dev, uint32_t vocab, uint32_t d_model,

@@ -28,6 +28,36 @@ int hip_fail(hipError_t e, const char* what) {
     return TWD_E_HIP;
 }
 
+int order_before(StreamOrder& o, hipStream_t s) {
+    if (!o.used) {
+        o.used = true;
+        o.last = s;
+        return TWD_OK;
+    }
+    if (s == o.last) return TWD_OK;
+    if (!o.multi) {
+        // the first change of stream: nothing recorded the old stream's last call, so wait for
+        // the device once, then track every call with the event
+        TWD_HIP(hipDeviceSynchronize());
+        TWD_HIP(hipEventCreateWithFlags(&o.ev, hipEventDisableTiming));
+        o.multi = true;
+    } else {
+        TWD_HIP(hipStreamWaitEvent(s, o.ev, 0));
+    }
+    o.last = s;
+    return TWD_OK;
+}
+
+int order_after(StreamOrder& o, hipStream_t s) {
+    if (o.multi) TWD_HIP(hipEventRecord(o.ev, s));
+    return TWD_OK;
+}
+
+void order_release(StreamOrder& o) {
+    if (o.ev) (void)hipEventDestroy(o.ev);
+    o = StreamOrder{};
+}
+
 }  // namespace twd
 
 using namespace twd;

@@ -161,6 +161,7 @@ __device__ __forceinline__ void block_stats(uint32_t& flag, float& mx, float& mn
 // below 4e-17 relative). tbl holds 2^(j/64), j = 0..63. Within 2 ulp; only the sum over the
 // row uses it, whose summation order already differs from the reference's in the last bits.
 __device__ __forceinline__ double exp_for_sum(double x, const double* tbl) {
+    if (x != x) return x;        // NaN stays NaN (+inf - +inf): the row total becomes NaN
     if (x < -745.5) return 0.0;  // also -inf
     const double kInvL = 92.332482616893656;             // 64 / ln2
     const double kLHi = 6.93147180369123816490e-01 / 64;  // ln2 / 64, high part (exact products)
@@ -918,6 +919,7 @@ TWD_API int twd_selector_create(uint32_t max_vocab, uint32_t max_rows, twd_selec
 
 TWD_API void twd_selector_destroy(twd_selector* s) {
     if (!s) return;
+    order_release(s->order);
     scratch_free(&s->scratch);
     draft_scratch_free(&s->draft);
     delete s;
@@ -929,8 +931,12 @@ TWD_API int twd_select(twd_selector* sel, float* logits, uint32_t vocab, uint32_
     clear_error();
     if (!sel) return fail(TWD_E_INVALID, "null selector");
     if (vocab > sel->max_vocab) return fail(TWD_E_INVALID, "vocab larger than this selector's max_vocab");
-    return launch_select(sel->scratch, logits, vocab, rows, row_stride, params, history, tokens,
-                         static_cast<hipStream_t>(stream));
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    int rc = order_before(sel->order, s);
+    if (rc) return rc;
+    rc = launch_select(sel->scratch, logits, vocab, rows, row_stride, params, history, tokens, s);
+    const int rc2 = order_after(sel->order, s);
+    return rc ? rc : rc2;
 }
 
 TWD_API int twd_verify(twd_selector* sel, const float* logits, uint32_t vocab, uint32_t rows,
@@ -943,6 +949,22 @@ TWD_API int twd_verify(twd_selector* sel, const float* logits, uint32_t vocab, u
     if (n_drafts > TWD_MAX_ROWS) return fail(TWD_E_INVALID, "n_drafts must be <= 64");
     if (rows > sel->scratch.max_rows) return fail(TWD_E_INVALID, "rows out of range for this selector");
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    int rc = order_before(sel->order, s);
+    if (rc) return rc;
+    rc = verify_launches(sel, logits, vocab, rows, row_stride, params, base_seed, drafts, n_drafts,
+                         result, s);
+    const int rc2 = order_after(sel->order, s);
+    return rc ? rc : rc2;
+}
+
+}  // extern "C"
+
+namespace twd {
+
+int verify_launches(twd_selector* sel, const float* logits, uint32_t vocab, uint32_t rows,
+                    uint64_t row_stride, const twd_row_params* params, uint64_t base_seed,
+                    const uint32_t* drafts, uint32_t n_drafts, twd_verify_result* result,
+                    hipStream_t s) {
     if (n_drafts == 0 || rows == 0)
         return launch_verify_compare(sel->scratch.verify_tokens, 0, drafts, n_drafts, result, s);
     // Only rows 0..min(n_drafts, rows) can be consulted; sample them all, as the reference
@@ -963,4 +985,4 @@ TWD_API int twd_verify(twd_selector* sel, const float* logits, uint32_t vocab, u
     return launch_verify_compare(sel->scratch.verify_tokens, used, drafts, n_drafts, result, s);
 }
 
-}  // extern "C"
+}  // namespace twd

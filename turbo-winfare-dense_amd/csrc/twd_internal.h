@@ -98,6 +98,22 @@ int hip_fail(hipError_t e, const char* what);
         if (e_ != hipSuccess) return hip_fail(e_, #call); \
     } while (0)
 
+// ---- calls on several streams ------------------------------------------------------------------------
+// An object whose calls share device state (a head's grid-finish state and staging buffers, a
+// selector's scratch) orders them when they arrive on different streams: the first change of
+// stream waits for the device once; from then on every call records an event on its stream and
+// a call on another stream waits for that event first. Calls on one stream cost nothing extra.
+// Not thread-safe: one host thread drives an object at a time, as the reference's runner does.
+struct StreamOrder {
+    hipStream_t last = nullptr;
+    bool used = false;
+    bool multi = false;
+    hipEvent_t ev = nullptr;
+};
+int order_before(StreamOrder& o, hipStream_t s);  // before enqueueing work that uses the state
+int order_after(StreamOrder& o, hipStream_t s);   // after enqueueing it
+void order_release(StreamOrder& o);
+
 // ---- device scratch shared by the launch helpers ------------------------------------------------------
 struct SelectScratch {
     uint32_t max_rows = 0;
@@ -141,7 +157,22 @@ int launch_verify_compare(const uint32_t* row_tokens, uint32_t rows, const uint3
 
 }  // namespace twd
 
+struct twd_selector;
+namespace twd {
+// twd_verify's launches, without the selector's stream ordering (callers that hold it already).
+int verify_launches(twd_selector* sel, const float* logits, uint32_t vocab, uint32_t rows,
+                    uint64_t row_stride, const twd_row_params* params, uint64_t base_seed,
+                    const uint32_t* drafts, uint32_t n_drafts, twd_verify_result* result,
+                    hipStream_t s);
+// twd_verify_draft's launches, likewise.
+int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab, uint32_t rows,
+                          uint64_t row_stride, const float* const* draft_rows, uint32_t n_draft_rows,
+                          const twd_row_params* params, uint64_t base_seed, const uint32_t* drafts,
+                          uint32_t n_drafts, twd_verify_result* result, hipStream_t s);
+}  // namespace twd
+
 struct twd_selector {
+    twd::StreamOrder order;
     twd::SelectScratch scratch;
     twd::DraftScratch draft;
     uint32_t max_vocab = 0;

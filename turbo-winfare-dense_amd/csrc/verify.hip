@@ -659,6 +659,22 @@ TWD_API int twd_verify_draft(twd_selector* sel, const float* logits, uint32_t vo
     if (n_draft_rows > 0 && !draft_rows) return fail(TWD_E_INVALID, "null draft_rows");
     if (vocab > sel->max_vocab) return fail(TWD_E_INVALID, "vocab above the selector's max_vocab");
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    int rc = order_before(sel->order, s);
+    if (rc) return rc;
+    rc = verify_draft_launches(sel, logits, vocab, rows, row_stride, draft_rows, n_draft_rows, params,
+                               base_seed, drafts, n_drafts, result, s);
+    const int rc2 = order_after(sel->order, s);
+    return rc ? rc : rc2;
+}
+
+}  // extern "C"
+
+namespace twd {
+
+int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab, uint32_t rows,
+                          uint64_t row_stride, const float* const* draft_rows, uint32_t n_draft_rows,
+                          const twd_row_params* params, uint64_t base_seed, const uint32_t* drafts,
+                          uint32_t n_drafts, twd_verify_result* result, hipStream_t s) {
     const bool greedy = params->temperature <= 0.0f && params->repetition_penalty == 1.0f;
     const uint32_t k = std::min(n_drafts, rows);
     uint64_t has = 0;
@@ -675,8 +691,8 @@ TWD_API int twd_verify_draft(twd_selector* sel, const float* logits, uint32_t vo
         }
     }
     if (a.npos == 0)  // greedy, or no draft probabilities anywhere: sample-and-compare
-        return twd_verify(sel, logits, vocab, rows, row_stride, params, base_seed, drafts, n_drafts,
-                          result, stream);
+        return verify_launches(sel, logits, vocab, rows, row_stride, params, base_seed, drafts,
+                               n_drafts, result, s);
     if (vocab == 0) return fail(TWD_E_INVALID, "vocab must be > 0");
 
     // target tokens for the positions without draft rows, the fallback and the bonus row
@@ -714,4 +730,4 @@ TWD_API int twd_verify_draft(twd_selector* sel, const float* logits, uint32_t vo
     return TWD_OK;
 }
 
-}  // extern "C"
+}  // namespace twd

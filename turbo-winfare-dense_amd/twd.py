@@ -68,6 +68,26 @@ class GenerationParams(C.Structure):
                 ("seed", C.c_uint64), ("max_tokens", C.c_uint32)]
 
 
+class GenerationOptions(C.Structure):
+    """G4DenseGenerationOptions, layout-identical to the reference's c_api.h:24-36."""
+    _fields_ = [("max_tokens", C.c_int), ("temperature", C.c_float), ("top_p", C.c_float),
+                ("top_k", C.c_int), ("repetition_penalty", C.c_float), ("has_seed", C.c_int),
+                ("seed", C.c_ulonglong), ("system_prompt", C.c_char_p),
+                ("stop_strings", C.POINTER(C.c_char_p)), ("stop_count", C.c_int),
+                ("tier_id", C.c_int)]
+
+
+# G4DenseTokenCallback (c_api.h:40): nonzero continues
+TokenCallback = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int, C.c_uint, C.c_char_p)
+
+STOP_NONE, STOP_MAX_TOKENS, STOP_TOKEN, STOP_CALLBACK, STOP_CANCELLED, STOP_DEGENERATE = range(6)
+
+
+def options_default() -> GenerationOptions:
+    """The values g4dense_options_default writes (the reference's c_api.cpp:40-53)."""
+    return GenerationOptions(512, 0.2, 0.95, 64, 1.0, 0, 0, None, None, 0, 1)
+
+
 class ContainerInfo(C.Structure):
     """twd_container_info: the .g4dense header fields of this path (format.hpp:26-110)."""
     _fields_ = [(n, C.c_uint32) for n in ("version", "quant_type", "num_layers", "d_model", "d_ff",
@@ -101,6 +121,13 @@ _SIGS = {
     "twd_head_norm_weight": (_vp, [_vp]),
     "twd_generator_create": (C.c_int, [_vp, C.POINTER(GenerationParams), C.POINTER(_u32), _u32,
                                        C.POINTER(_u32), _u32, C.POINTER(_vp)]),
+    "twd_generator_create_ex": (C.c_int, [_vp, C.POINTER(GenerationOptions), C.POINTER(_u32), _u32,
+                                          C.POINTER(_u32), _u32, TokenCallback, _vp,
+                                          C.POINTER(_vp)]),
+    "twd_generator_cancel": (None, [_vp]),
+    "twd_generator_stop_reason": (C.c_int, [_vp]),
+    "twd_generator_sync": (C.c_int, [_vp, C.POINTER(C.c_int)]),
+    "twd_head_finish_state": (_vp, [_vp]),
     "twd_generator_destroy": (None, [_vp]),
     "twd_generator_step": (C.c_int, [_vp, _vp, _vp, C.POINTER(_u32), C.POINTER(C.c_int)]),
     "twd_generator_step_rmsnorm": (C.c_int, [_vp, _vp, _vp, _f32, _vp, C.POINTER(_u32),
@@ -357,24 +384,46 @@ class SpeculativeCoordinator:
     def evaluate_verification(self, draft_tokens, target_logits, vocab_size: int,
                               sampling: SamplingParams, base_seed: int, draft_logits=()):
         """target_logits: float32 device tensor [rows, vocab]. draft_logits: per position a
-        float32 device row of vocab entries, or an empty sequence / None for none."""
+        float32 device row of vocab entries, or an empty sequence / None for none.
+
+        Any number of drafts, as speculator.cpp:34-153: the device verifies at most MAX_ROWS
+        positions per call, so longer drafts go in batches of MAX_ROWS positions, each with
+        base_seed + its first position (the seeds stay base_seed + i), until a correction or
+        the end; only the last batch adds the bonus row."""
         import torch
         n = len(draft_tokens)
         self.total_draft_tokens += n
-        if n == 0 or target_logits.shape[0] == 0:
-            return {"tokens": [], "num_accepted": 0, "total_drafted": n,
-                    "bonus_token_sampled": False, "bonus_token": 0, "acceptance_rate": 0.0}
-        drafts = torch.tensor(list(draft_tokens), dtype=torch.int64).to(torch.int32).to(
-            target_logits.device)
+        out = {"tokens": [], "num_accepted": 0, "total_drafted": n,
+               "bonus_token_sampled": False, "bonus_token": 0, "acceptance_rate": 0.0}
+        rows_all = target_logits.shape[0]
+        if n == 0 or rows_all == 0:
+            return out
+        k = min(n, rows_all)
+        drafts_all = [int(x) for x in draft_tokens]
         sel = _selector(vocab_size)
         rows = [None if d is None or len(d) == 0 else d for d in draft_logits]
-        if not sampling.is_greedy() and any(r is not None for r in rows):
-            res = sel.verify_draft(target_logits[:, :vocab_size], rows, row_params(sampling),
-                                   base_seed, drafts)
-        else:
-            res = sel.verify(target_logits[:, :vocab_size], row_params(sampling), base_seed,
-                             drafts)
-        out = decode_verify(res)
+        use_draft = not sampling.is_greedy() and any(r is not None for r in rows)
+        for b0 in range(0, k, MAX_ROWS):
+            kb = min(MAX_ROWS, k - b0)
+            last = b0 + kb == k
+            nrows = min(rows_all, k + 1) - b0 if last else kb
+            drafts = torch.tensor(drafts_all[b0:b0 + kb], dtype=torch.int64).to(torch.int32).to(
+                target_logits.device)
+            tl = target_logits[b0:b0 + nrows, :vocab_size]
+            seed = base_seed + b0
+            batch_rows = rows[b0:b0 + kb]
+            if use_draft and any(r is not None for r in batch_rows):
+                res = sel.verify_draft(tl, batch_rows, row_params(sampling), seed, drafts)
+            else:
+                res = sel.verify(tl, row_params(sampling), seed, drafts)
+            got = decode_verify(res)
+            out["tokens"] += got["tokens"]
+            out["num_accepted"] += got["num_accepted"]
+            out["bonus_token_sampled"] = got["bonus_token_sampled"]
+            out["bonus_token"] = got["bonus_token"]
+            if got["num_accepted"] < kb:
+                break
+        out["acceptance_rate"] = out["num_accepted"] / n
         self.total_accepted_tokens += out["num_accepted"]
         return out
 
@@ -407,6 +456,44 @@ class Generator:
                                         len(stop_ids), C.byref(h)))
         self.handle = h
         self.head = head
+        self._cb = None
+
+    @classmethod
+    def from_options(cls, head: "LMHead", options: GenerationOptions | None, prompt,
+                     stop_ids=(), on_token=None) -> "Generator":
+        """twd_generator_create_ex: the reference's G4DenseGenerationOptions (None = its
+        GenerationOptions defaults) and an optional on_token(index, token_id, delta) -> bool
+        that ends the generation when it returns False (c_api.cpp:148-155)."""
+        self = cls.__new__(cls)
+        pr = (_u32 * max(1, len(prompt)))(*[int(t) for t in prompt])
+        st = (_u32 * max(1, len(stop_ids)))(*[int(t) for t in stop_ids])
+        self._cb = None
+        if on_token is not None:
+            self._cb = TokenCallback(lambda user, i, tok, delta: 1 if on_token(i, tok, delta) else 0)
+        h = C.c_void_p()
+        _check(lib.twd_generator_create_ex(head.handle, None if options is None else C.byref(options),
+                                           pr, len(prompt), st, len(stop_ids),
+                                           self._cb if self._cb is not None else TokenCallback(),
+                                           None, C.byref(h)))
+        self.handle = h
+        self.head = head
+        return self
+
+    def cancel(self):
+        lib.twd_generator_cancel(self.handle)
+
+    def stop_reason(self) -> int:
+        return int(lib.twd_generator_stop_reason(self.handle))
+
+    def sync(self) -> bool:
+        """Applies the stop rules to ids of steps taken without readback; returns finished."""
+        fin = C.c_int()
+        _check(lib.twd_generator_sync(self.handle, C.byref(fin)))
+        return bool(fin.value)
+
+    def step_async(self, hidden_bf16, stream=None):
+        """A step that only enqueues (no readback, no stop rules until sync())."""
+        _check(lib.twd_generator_step(self.handle, _ptr(hidden_bf16), _stream(stream), None, None))
 
     def close(self):
         if self.handle:
