@@ -134,11 +134,14 @@ TWD_API int twd_head_verify_greedy(twd_head* head, const uint16_t* hidden_bf16, 
  * so calls that arrive on another stream than the previous call are ordered after it (the
  * first change of stream waits for the device once; after that each call records an event
  * and a call on another stream waits for it). A head is driven by one host thread at a time.
- * The arrival count carries each launch's own epoch, so a count left behind by anything else
+ * Each launch counts its blocks in under its own epoch, and its last block arms the counter for
+ * the next launch; a launch that finds the counter not armed for it (a launch that did not
+ * finish, a write from outside) counts in on a fallback word instead, so a count left behind
  * never decides which block finishes.
  *
- * No counterpart in the reference: the device address of that state (64 per-row uint64 maxima,
- * then the uint64 arrival counter {epoch << 32 | arrivals}), for diagnostics and tests. */
+ * No counterpart in the reference: the device address of that state, for diagnostics and
+ * tests: 64 per-row uint64 maxima, then the uint64 counter {arrivals << 32 | epoch}, then the
+ * uint64 fallback counter. */
 TWD_API void* twd_head_finish_state(const twd_head* head);
 
 /* ---- the same passes with the final RMSNorm as their prologue --------------------------------

@@ -239,9 +239,11 @@ def test_greedy_after_counter_left_nonzero(small, oracle, M):
     torch.cuda.synchronize()
     cur = ctypes.c_uint64()
     assert hip.hipMemcpy(ctypes.byref(cur), ctr_addr, 8, 2) == 0
-    last_epoch = cur.value >> 32
-    assert cur.value & 0xFFFFFFFF > 0  # the last greedy launch counted its blocks there
-    for garbage in (5, (last_epoch << 32) | 7, 0xFFFFFFFFFFFFFFFF, ((last_epoch + 1000) << 32) | 3):
+    nxt = cur.value & 0xFFFFFFFF
+    assert cur.value >> 32 == 0 and nxt > 0  # armed for the next launch's epoch
+    # a launch of the previous epoch that stopped after 7 blocks, another epoch's count,
+    # all ones, and zero
+    for garbage in ((7 << 32) | (nxt - 1), (3 << 32) | (nxt + 1000), 0xFFFFFFFFFFFFFFFF, 0):
         torch.cuda.synchronize()
         g = ctypes.c_uint64(garbage)
         assert hip.hipMemcpy(ctr_addr, ctypes.byref(g), 8, 1) == 0
@@ -249,6 +251,9 @@ def test_greedy_after_counter_left_nonzero(small, oracle, M):
         assert tok == want, hex(garbage)
         tok = head.greedy(h).cpu().numpy().astype(np.int64).tolist()  # and the launch after it
         assert tok == want, hex(garbage)
+    torch.cuda.synchronize()
+    assert hip.hipMemcpy(ctypes.byref(cur), ctr_addr, 8, 2) == 0
+    assert cur.value >> 32 == 0 and cur.value & 0xFFFFFFFF != 0  # armed again
 
 
 def test_calls_alternating_between_streams(small, oracle):

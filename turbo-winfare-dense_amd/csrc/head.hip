@@ -44,8 +44,8 @@ struct HeadArgs {
     // greedy finish: running per-row maxima (zero between launches), the arrival counter
     // {epoch, count} and this launch's epoch, and where the last block puts its results
     uint64_t* gbest;    // [TWD_MAX_ROWS]
-    uint64_t* gctr;
-    uint32_t epoch;
+    uint64_t* gctr;     // [2]: the armed counter, then the fallback counter
+    uint32_t epoch, next_epoch;
     uint32_t* tokens;
     const uint32_t* drafts;
     uint32_t n_drafts;
@@ -190,10 +190,13 @@ using EpiShared = EpiSharedT<kHeadWaves>;
 // stores, so no device-scope fence is needed: on this part such a fence writes back the XCD's
 // L2 and, paid by each of ~1000 blocks, costs more than the streaming pass itself.
 //
-// The counter holds {launch epoch (high 32 bits), arrivals (low 32 bits)}. Each launch carries
-// a fresh epoch; a block that finds another epoch there starts the count at 1 (compare-and-swap),
-// so a count left behind by anything but this launch -- a write from outside, a launch that did
-// not finish -- can never make the wrong block the last one, and nothing has to clear it.
+// Arrivals are counted in gctr[0] = {arrivals (high 32 bits), epoch (low 32 bits)}: every
+// launch carries its own epoch, and the last block of each launch leaves the counter armed for
+// the next one, {0, next epoch}. A block adds 1 to the high half, which never carries into the
+// epoch, so every block of a launch sees the same epoch there. When it is not this launch's
+// (the first launch on a fresh state, a launch that did not finish, a write from outside), the
+// blocks count themselves in on gctr[1] instead, by compare-and-swap with the epoch attached,
+// and the last one re-arms gctr[0]; only that case pays for contended retries.
 // tot[j][mt][i] holds row r = (tile0 + j) * 16 + lane % 16 of MFMA row 16 mt + 4 (lane / 16) + i,
 // which carries h row m = (16 mt + 4 (lane / 16) + i) / MS when i is a multiple of MS (MS > 1:
 // the rows are spread over the MFMA rows, see head_small_kernel); other entries are not outputs.
@@ -208,12 +211,6 @@ __device__ __forceinline__ void head_epilogue(const HeadArgs& a, f32x4_t (&tot)[
             for (int i = 0; i < NI; ++i) tot[j][0][i] += __shfl_xor(tot[j][0][i], 32);
     }
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    // the counter's current value, a hint for the compare-and-swap below, fetched now so that
-    // its round trip overlaps the epilogue's arithmetic
-    unsigned long long ctr_hint = 0;
-    if (MODE != kModeLogits && tid == 0)
-        ctr_hint = __hip_atomic_load(reinterpret_cast<unsigned long long*>(a.gctr), __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
     uint64_t best[NMT][NI];
 #pragma unroll
     for (int mt = 0; mt < NMT; ++mt)
@@ -267,16 +264,29 @@ __device__ __forceinline__ void head_epilogue(const HeadArgs& a, f32x4_t (&tot)[
     }
     __syncthreads();
     if (tid == 0) {
-        // every failed exchange means another block counted itself in, so this loop ends after
-        // at most gridDim.x attempts; usually the hint is current and the first one succeeds
-        unsigned long long cur = ctr_hint, want;
-        const unsigned long long ep = static_cast<unsigned long long>(a.epoch) << 32;
-        do {
-            want = ((cur & 0xFFFFFFFF00000000ull) == ep) ? cur + 1 : (ep | 1ull);
-        } while (!__hip_atomic_compare_exchange_strong(reinterpret_cast<unsigned long long*>(a.gctr), &cur,
-                                                       want, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                       __HIP_MEMORY_SCOPE_AGENT));
-        se.last = static_cast<uint32_t>(want) == nb;
+        unsigned long long* ctr = reinterpret_cast<unsigned long long*>(a.gctr);
+        const unsigned long long ep = a.epoch;
+        const unsigned long long old = __hip_atomic_fetch_add(ctr, 1ull << 32, __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT);
+        bool last;
+        if ((old & 0xFFFFFFFFull) == ep && (old >> 32) < nb) {
+            last = (old >> 32) == nb - 1;
+        } else {
+            // not armed for this launch: count in on the fallback word; every failed exchange
+            // means another block counted itself in, so the loop ends after at most nb tries
+            unsigned long long* c2 = ctr + 1;
+            unsigned long long cur = __hip_atomic_load(c2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), want;
+            do {
+                want = ((cur & 0xFFFFFFFFull) == ep) ? cur + (1ull << 32) : (ep | (1ull << 32));
+            } while (!__hip_atomic_compare_exchange_strong(c2, &cur, want, __ATOMIC_RELAXED,
+                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+            last = (want >> 32) == nb;
+        }
+        // every block of this launch has added to gctr[0] by now: arm it for the next launch
+        if (last)
+            __hip_atomic_exchange(ctr, static_cast<unsigned long long>(a.next_epoch), __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+        se.last = last;
     }
     __syncthreads();
     if (!se.last) return;
@@ -1083,6 +1093,9 @@ int enable_small_kernels(uint32_t d) {
     return TWD_OK;
 }
 
+// Epochs run through 1 .. 2^31 - 1 and repeat; 0 never arms the counter.
+uint32_t epoch_after(uint32_t e) { return e % 0x7FFFFFFFu + 1u; }
+
 int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
     twd_head* h = new twd_head();
     h->vocab = vocab;
@@ -1092,9 +1105,12 @@ int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
     h->nunits = d / kChunkK;
     h->tiled_bytes = static_cast<uint64_t>(h->ntiles) * h->nunits * kUnitBytes;
     hipError_t e = hipMalloc(&h->tiled, h->tiled_bytes);
-    // gbest: per-row maxima, the arrival counter, and the repack's bad-scale flag
-    if (e == hipSuccess) e = hipMalloc(&h->gbest, sizeof(uint64_t) * (TWD_MAX_ROWS + 2));
-    if (e == hipSuccess) e = hipMemset(h->gbest, 0, sizeof(uint64_t) * (TWD_MAX_ROWS + 2));
+    // gbest: per-row maxima, the two arrival counters, and the repack's bad-scale flag; the
+    // counter starts armed for the first launch's epoch
+    const uint64_t armed = epoch_after(0);
+    if (e == hipSuccess) e = hipMalloc(&h->gbest, sizeof(uint64_t) * (TWD_MAX_ROWS + 3));
+    if (e == hipSuccess) e = hipMemset(h->gbest, 0, sizeof(uint64_t) * (TWD_MAX_ROWS + 3));
+    if (e == hipSuccess) e = hipMemcpy(h->gbest + TWD_MAX_ROWS, &armed, sizeof(armed), hipMemcpyHostToDevice);
     // hp / hx: room past the last chunk and super-unit (each stage copies the next one
     // unconditionally)
     if (e == hipSuccess) e = hipMalloc(&h->hp, sizeof(u32x4_t) * (h->nunits + 3) * 4 * 4 * 64);
@@ -1111,12 +1127,7 @@ int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
     return TWD_OK;
 }
 
-uint32_t next_epoch(twd_head* h) {
-    if (++h->epoch == 0) h->epoch = 1;
-    return h->epoch;
-}
-
-uint32_t* repack_flag(twd_head* h) { return reinterpret_cast<uint32_t*>(h->gbest + TWD_MAX_ROWS + 1); }
+uint32_t* repack_flag(twd_head* h) { return reinterpret_cast<uint32_t*>(h->gbest + TWD_MAX_ROWS + 2); }
 
 int head_repack(twd_head* h, const uint8_t* wsb_dev, hipStream_t stream) {
     const uint64_t w_bytes = static_cast<uint64_t>(h->vocab) * (h->d / 8) * 4;
@@ -1151,7 +1162,9 @@ int launch_head(twd_head* h, const uint16_t* hidden, uint32_t rows, float* logit
     a.vocab = h->vocab;
     a.gbest = h->gbest;
     a.gctr = h->gbest + TWD_MAX_ROWS;
-    a.epoch = next_epoch(h);
+    if (MODE != kModeLogits) h->epoch = epoch_after(h->epoch);  // only greedy launches count in
+    a.epoch = h->epoch;
+    a.next_epoch = epoch_after(h->epoch);
     a.tokens = tokens;
     a.drafts = drafts;
     a.n_drafts = n_drafts;
@@ -1206,7 +1219,9 @@ int launch_head_rmsnorm(twd_head* h, const float* x, const uint16_t* norm_w, flo
     a.vocab = h->vocab;
     a.gbest = h->gbest;
     a.gctr = h->gbest + TWD_MAX_ROWS;
-    a.epoch = next_epoch(h);
+    if (MODE != kModeLogits) h->epoch = epoch_after(h->epoch);  // only greedy launches count in
+    a.epoch = h->epoch;
+    a.next_epoch = epoch_after(h->epoch);
     a.tokens = tokens;
     a.drafts = drafts;
     a.n_drafts = n_drafts;
