@@ -20,6 +20,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 
 #include "twd_internal.h"
 
@@ -803,6 +804,66 @@ __global__ void verify_compare_kernel(const uint32_t* row_tokens, uint32_t rows,
 
 static uint32_t parts_for(uint32_t vocab) { return (vocab + kSlice - 1) / kSlice; }
 
+// ---- the no-allocation selection: scratch in a device array of fixed size ------------------------
+// The selection scratch of at most kStaticRows rows of at most kStaticVocab entries, carved the
+// way scratch_alloc lays it out. Each GPU holds its own copy for the life of the process; every
+// twd_select_noalloc call on a GPU shares it.
+constexpr uint32_t kStaticRows = TWD_MAX_ROWS;
+constexpr uint32_t kStaticVocab = 262144;
+constexpr uint32_t kStaticParts = kStaticVocab / kSlice;  // 32
+constexpr size_t kStaticSlots = static_cast<size_t>(kStaticRows) * kStaticParts;
+constexpr size_t kStaticOffSum = 0;                                   // double [slots]
+constexpr size_t kStaticOffKey = kStaticOffSum + 8 * kStaticSlots;    // uint64 [slots]
+constexpr size_t kStaticOffMax = kStaticOffKey + 8 * kStaticSlots;    // float [slots]
+constexpr size_t kStaticOffFlag = kStaticOffMax + 4 * kStaticSlots;   // uint32 [slots]
+constexpr size_t kStaticOffCount = kStaticOffFlag + 4 * kStaticSlots; // uint32 [slots]
+constexpr size_t kStaticOffCand = kStaticOffCount + 4 * kStaticSlots; // uint64 [slots][kMaxWant]
+constexpr size_t kStaticBytes = kStaticOffCand + 8 * kStaticSlots * kMaxWant;  // 4,259,840 B
+static_assert(kStaticOffCand % 256 == 0, "candidate array alignment");
+
+static __device__ __align__(256) unsigned char scratch[kStaticBytes];
+
+namespace {
+
+// The device address of `scratch` on each GPU (its own copy there), found once per device with
+// that device current. Host code uses these addresses, never the array's name: on the host the
+// name is a stand-in that no kernel may dereference.
+constexpr int kMaxDevices = 64;
+std::mutex g_static_mu;
+void* g_static_ptr[kMaxDevices] = {};
+
+int static_scratch(SelectScratch* out) {
+    int dev = 0;
+    TWD_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(TWD_E_UNSUPPORTED, "device index above 63");
+    void* base = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_static_mu);
+        if (!g_static_ptr[dev]) {
+            void* p = nullptr;
+            TWD_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+            if (!p) return fail(TWD_E_HIP, "hipGetSymbolAddress returned no address for the scratch array");
+            g_static_ptr[dev] = p;
+        }
+        base = g_static_ptr[dev];
+    }
+    unsigned char* b = static_cast<unsigned char*>(base);
+    SelectScratch s{};
+    s.max_rows = kStaticRows;
+    s.max_parts = kStaticParts;
+    s.part_sum = reinterpret_cast<double*>(b + kStaticOffSum);
+    s.part_key = reinterpret_cast<uint64_t*>(b + kStaticOffKey);
+    s.part_max = reinterpret_cast<float*>(b + kStaticOffMax);
+    s.part_flag = reinterpret_cast<uint32_t*>(b + kStaticOffFlag);
+    s.part_count = reinterpret_cast<uint32_t*>(b + kStaticOffCount);
+    s.cand = reinterpret_cast<uint64_t*>(b + kStaticOffCand);
+    s.verify_tokens = nullptr;  // twd_select does not use it
+    *out = s;
+    return TWD_OK;
+}
+
+}  // namespace
+
 int scratch_alloc(SelectScratch* s, uint32_t max_vocab, uint32_t max_rows) {
     s->max_rows = max_rows;
     s->max_parts = parts_for(max_vocab);
@@ -831,6 +892,23 @@ void scratch_free(SelectScratch* s) {
     (void)hipFree(s->cand);
     (void)hipFree(s->verify_tokens);
     *s = SelectScratch{};
+}
+
+// Lets the selection kernels use the LDS they need (no memory is allocated).
+int enable_select_kernels() {
+    static std::once_flag once;
+    static hipError_t err = hipSuccess;
+    std::call_once(once, [] {
+        err = hipFuncSetAttribute(reinterpret_cast<const void*>(select_slice_kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  static_cast<int>(sizeof(SliceShared)));
+        if (err == hipSuccess)
+            err = hipFuncSetAttribute(reinterpret_cast<const void*>(select_merge_kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      static_cast<int>(sizeof(MergeShared)));
+    });
+    if (err != hipSuccess) return hip_fail(err, "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
+    return TWD_OK;
 }
 
 int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_t rows,
@@ -896,16 +974,8 @@ TWD_API int twd_selector_create(uint32_t max_vocab, uint32_t max_rows, twd_selec
     if (max_vocab == 0 || max_rows == 0 || max_rows > TWD_MAX_ROWS + 1)
         return fail(TWD_E_INVALID, "max_vocab must be > 0 and max_rows in 1..65");
     if (parts_for(max_vocab) > kMaxParts) return fail(TWD_E_UNSUPPORTED, "max_vocab above 524288");
-    static bool attr_done = false;
-    if (!attr_done) {
-        TWD_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(select_slice_kernel),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    static_cast<int>(sizeof(SliceShared))));
-        TWD_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(select_merge_kernel),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    static_cast<int>(sizeof(MergeShared))));
-        attr_done = true;
-    }
+    int rc0 = enable_select_kernels();
+    if (rc0) return rc0;
     twd_selector* s = new twd_selector();
     s->max_vocab = max_vocab;
     const int rc = scratch_alloc(&s->scratch, max_vocab, max_rows);
@@ -937,6 +1007,21 @@ TWD_API int twd_select(twd_selector* sel, float* logits, uint32_t vocab, uint32_
     rc = launch_select(sel->scratch, logits, vocab, rows, row_stride, params, history, tokens, s);
     const int rc2 = order_after(sel->order, s);
     return rc ? rc : rc2;
+}
+
+TWD_API int twd_select_noalloc(float* logits, uint32_t vocab, uint32_t rows, uint64_t row_stride,
+                               const twd_row_params* params, const uint32_t* history,
+                               uint32_t* tokens, void* stream) {
+    clear_error();
+    if (vocab > kStaticVocab)
+        return fail(TWD_E_INVALID, "twd_select_noalloc: vocab above its fixed scratch's 262144 entries");
+    if (rows > kStaticRows) return fail(TWD_E_INVALID, "twd_select_noalloc: rows above 64");
+    int rc = enable_select_kernels();
+    if (rc) return rc;
+    SelectScratch s{};
+    if ((rc = static_scratch(&s))) return rc;
+    return launch_select(s, logits, vocab, rows, row_stride, params, history, tokens,
+                         static_cast<hipStream_t>(stream));
 }
 
 TWD_API int twd_verify(twd_selector* sel, const float* logits, uint32_t vocab, uint32_t rows,

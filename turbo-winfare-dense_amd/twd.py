@@ -137,6 +137,7 @@ _SIGS = {
     "twd_selector_create": (C.c_int, [_u32, _u32, C.POINTER(_vp)]),
     "twd_selector_destroy": (None, [_vp]),
     "twd_select": (C.c_int, [_vp, _vp, _u32, _u32, _u64, C.POINTER(RowParams), _vp, _vp, _vp]),
+    "twd_select_noalloc": (C.c_int, [_vp, _u32, _u32, _u64, C.POINTER(RowParams), _vp, _vp, _vp]),
     "twd_verify": (C.c_int, [_vp, _vp, _u32, _u32, _u64, C.POINTER(RowParams), _u64, _vp, _u32,
                              _vp, _vp]),
     "twd_verify_draft": (C.c_int, [_vp, _vp, _u32, _u32, _u64, C.POINTER(_vp), _u32,
