@@ -28,7 +28,11 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
-enum HeadMode { kModeLogits = 0, kModeGreedy = 1 };  // greedy: also write block ranks
+// greedy: also the grid-wide rank maximum; sample (M <= 4, resident-h kernel only): the
+// repetition penalty in place and each block's selection statistics
+enum HeadMode { kModeLogits = 0, kModeGreedy = 1, kModeSample = 2 };
+
+constexpr uint32_t kSampleRows = 4;  // rows of the sample mode
 
 constexpr int kHeadThreads = 256;
 constexpr int kHeadWaves = 4;
@@ -57,6 +61,13 @@ struct HeadArgs {
     const float* x;
     const uint16_t* norm_w;
     float eps;
+    // sample mode: per row m, the penalty over history[hist_off[m], + hist_len[m]) (rp != 1)
+    // clamped to +-clamp[m] (0.9999 softcap; 0: no clamp), and where each block's statistics go
+    // (index m * gridDim.x + block)
+    const uint32_t* history;
+    uint32_t hist_off[kSampleRows], hist_len[kSampleRows];
+    float rp[kSampleRows], clamp[kSampleRows];
+    SampleStats stats;
 };
 
 // speculator.cpp:46-69 and :138-150, greedy branch, over per-row target tokens tok[0..rows).
@@ -302,6 +313,75 @@ __device__ __forceinline__ void head_epilogue(const HeadArgs& a, f32x4_t (&tot)[
     if (tid == 0 && a.vres) verify_bookkeeping(se.tok, a.M, a.drafts, a.n_drafts, a.vres);
 }
 
+// Sample mode of the resident-h kernel with rows spread four apart (MS = 4: row m's outputs are
+// accumulator entry 0 of lanes 16m .. 16m + 15). Per live entry: the softcap, then
+// apply_repetition_penalty (sampling.cpp:74-90) with the entry's occurrence count from the
+// block's LDS counts, one occurrence at a time (divide or multiply, then clamp), then the store.
+// Each wave then publishes, per row, the statistics of its 64 vocabulary rows that
+// select_sample_merge_kernel needs -- its best rank (value desc, index asc) and the sum of
+// exp(v - that value) in double, NaN when the wave saw a NaN (the row is then degenerate, as a
+// NaN makes the reference's total NaN) -- with no barrier and no cross-wave step. tbl holds
+// 2^(j/64), j < 64, for exp_for_sum.
+template <int RT, int NW>
+__device__ __forceinline__ void head_epilogue_sample(const HeadArgs& a, f32x4_t (&tot)[RT][1],
+                                                     uint32_t tile0, uint32_t block_row0,
+                                                     const uint32_t* cnt, const double* tbl) {
+    constexpr uint32_t kRowsPerBlock = NW * RT * kTileRows;
+    const int lane = threadIdx.x & 63;
+    const uint32_t m = lane >> 4;
+    const bool mlive = m < a.M;
+    const uint32_t mm = mlive ? m : 0u;
+    const float rp = a.rp[mm], lim = a.clamp[mm];
+    float v[RT];
+    uint64_t best = 0;
+    uint32_t nan = 0;
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+        const uint32_t r = (tile0 + j) * kTileRows + (lane & 15);
+        const bool live = mlive && r < a.vocab;
+        float x = tot[j][0][0];
+        if (a.softcap > 0.0f) x = a.softcap * tanhf(x / a.softcap);
+        if (live && rp != 1.0f) {
+            const uint32_t n = cnt[mm * kRowsPerBlock + (r - block_row0)];
+            for (uint32_t t = 0; t < n; ++t) {
+                x = (x > 0.0f) ? (x / rp) : (x * rp);
+                if (lim > 0.0f) x = (x < -lim) ? -lim : ((lim < x) ? lim : x);
+            }
+        }
+        if (live) {
+            a.logits[static_cast<size_t>(m) * a.vocab + r] = x;
+            const uint64_t k = rank_key(x, r);
+            best = k > best ? k : best;
+            if (x != x) nan = 1;
+        }
+        v[j] = live ? x : -INFINITY;
+    }
+    // the 16 lanes of a row
+#pragma unroll
+    for (int msk = 1; msk < 16; msk <<= 1) {
+        const uint64_t o = shfl_xor_u64(best, msk);
+        best = o > best ? o : best;
+        nan |= __shfl_xor(nan, msk);
+    }
+    // the wave's largest value (exact: the best rank's value, -0 read as +0); a wave of -inf
+    // entries adds nothing to the row's sum
+    const float wm = best != 0 ? rank_value(best) : -INFINITY;
+    double sum = 0.0;
+    if (wm != -INFINITY) {
+        const double dwm = static_cast<double>(wm);
+#pragma unroll
+        for (int j = 0; j < RT; ++j) sum += exp_for_sum(static_cast<double>(v[j]) - dwm, tbl);
+    }
+#pragma unroll
+    for (int msk = 1; msk < 16; msk <<= 1) sum += __shfl_xor(sum, msk);
+    if (nan) sum = __builtin_nan("");
+    if ((lane & 15) == 0 && mlive) {
+        const size_t o = static_cast<size_t>(m) * (gridDim.x * NW) + blockIdx.x * NW + (threadIdx.x >> 6);
+        a.stats.key[o] = best;
+        a.stats.sum[o] = sum;
+    }
+}
+
 // Weight streams: one buffer descriptor per row tile covering its stripe of units, so a unit
 // load is one buffer_load with the unit offset in a scalar register and a fixed per-lane offset
 // -- no per-lane address arithmetic in the streaming loop. Tiles past the end (tile0 is
@@ -417,6 +497,37 @@ __global__ __launch_bounds__(NW * 64) void head_small_kernel(HeadArgs a) {
     const uint32_t last = a.nunits - 1;
     u32x4_t wq[PF][RT];
     u32x2_t sq[PF][RT];
+    // sample mode: occurrence counts of the block's rows in each row's history
+    constexpr uint32_t kRowsPerBlock = NW * RT * kTileRows;
+    __shared__ uint32_t cnt[MODE == kModeSample ? kSampleRows * kRowsPerBlock : 1];
+    __shared__ double exp2_tbl[MODE == kModeSample ? 64 : 1];
+    const uint32_t block_row0 = blockIdx.x * kRowsPerBlock;
+    if constexpr (MODE == kModeSample) {
+        for (uint32_t i = tid; i < kSampleRows * kRowsPerBlock; i += NT) cnt[i] = 0;
+        if (tid < 64) exp2_tbl[tid] = kExp2Table[tid];
+    }
+    // sample mode: the history's first batch (kHistBatch ids per thread of the first row with a
+    // penalty) is requested first, so that its round trip overlaps the ring fill and the staging
+    // of h
+    constexpr int kHistBatch = 8;
+    uint32_t hids[MODE == kModeSample ? kHistBatch : 1];
+    uint32_t m_first = kSampleRows;
+    if constexpr (MODE == kModeSample) {
+        for (uint32_t m = 0; m < a.M; ++m)
+            if (a.rp[m] != 1.0f && a.hist_len[m] != 0) {
+                m_first = m;
+                break;
+            }
+        if (m_first < a.M) {
+            const uint32_t* hs = a.history + a.hist_off[m_first];
+#pragma unroll
+            for (int q = 0; q < kHistBatch; ++q) {
+                const uint32_t j = tid + NT * q;
+                hids[q] = j < a.hist_len[m_first] ? hs[j] : 0xFFFFFFFFu;
+            }
+        }
+    }
+
     // The ring is filled before h is staged, so the two memory round trips overlap. Ring order,
     // the same in the prologue and in every cycle: per super-unit, the even unit's nibbles, then
     // its {b, t} words, then the odd unit's nibbles and words. The even unit's words are refilled
@@ -536,6 +647,33 @@ __global__ __launch_bounds__(NW * 64) void head_small_kernel(HeadArgs a) {
             }
         }
     }
+    if constexpr (MODE == kModeSample) {
+        // every wave's zeros are in place; then the occurrence counts of the block's rows, each
+        // history id of this block counted once (ids >= vocab never match a live row)
+        __syncthreads();
+        auto count = [&](uint32_t m, const uint32_t (&ids)[kHistBatch]) {
+#pragma unroll
+            for (int q = 0; q < kHistBatch; ++q) {
+                const uint32_t lr = ids[q] - block_row0;
+                if (lr < kRowsPerBlock) atomicAdd(&cnt[m * kRowsPerBlock + lr], 1u);
+            }
+        };
+        if (m_first < a.M) count(m_first, hids);
+        for (uint32_t m = m_first; m < a.M; ++m) {
+            if (a.rp[m] == 1.0f || a.hist_len[m] == 0) continue;
+            const uint32_t* hs = a.history + a.hist_off[m];
+            const uint32_t len = a.hist_len[m];
+            for (uint32_t j0 = (m == m_first) ? NT * kHistBatch : 0; j0 < len; j0 += NT * kHistBatch) {
+                uint32_t ids[kHistBatch];
+#pragma unroll
+                for (int q = 0; q < kHistBatch; ++q) {
+                    const uint32_t j = j0 + tid + NT * q;
+                    ids[q] = j < len ? hs[j] : 0xFFFFFFFFu;
+                }
+                count(m, ids);
+            }
+        }
+    }
     __syncthreads();
 
     // this lane's A row rho: h row rho / MS when rho % MS is 0 (NORM: its hi half, and its lo
@@ -621,7 +759,12 @@ __global__ __launch_bounds__(NW * 64) void head_small_kernel(HeadArgs a) {
 #pragma unroll
         for (int j = 0; j < RT; ++j) tot[j][0][0] = (tot[j][0][0] + tot[j][0][1]) * rms;
     }
-    head_epilogue<1, 4, RT, MODE, NW, MS>(a, tot, tile0, se);
+    if constexpr (MODE == kModeSample) {
+        static_assert(MS == 4, "the sample mode takes rows spread four apart (M <= 4)");
+        head_epilogue_sample<RT, NW>(a, tot, tile0, block_row0, cnt, exp2_tbl);
+    } else {
+        head_epilogue<1, 4, RT, MODE, NW, MS>(a, tot, tile0, se);
+    }
 }
 
 // ---- 9 <= M <= 64: h prepared once per call, staged through LDS by plain copies -------------------
@@ -1022,6 +1165,8 @@ struct twd_head {
     u32x4_t* hx = nullptr;        // its bias A-fragment entries
     twd_selector* sel = nullptr;
     uint16_t* norm_w = nullptr;   // final RMSNorm weight, when loaded from a container
+    SampleStats stats{};          // per-wave statistics of the fused sample pass (M <= 4)
+    uint32_t sample_blocks = 0;   // its head blocks (0: no fused sample pass for this head)
 };
 
 namespace {
@@ -1089,6 +1234,9 @@ int enable_small_kernels(uint32_t d) {
     if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS, kPFS, kNWS4, kModeGreedy, true>, bytes8);
     if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS, kPFS, kNWS8, kModeLogits, true>, bytes8);
     if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS, kPFS, kNWS8, kModeGreedy, true>, bytes8);
+    // the fused sample pass (M <= 4), with and without the RMSNorm prologue
+    if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS, kPFS, kNWS4, kModeSample>, bytes4);
+    if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS, kPFS, kNWS4, kModeSample, true>, bytes8);
     if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
     return TWD_OK;
 }
@@ -1115,6 +1263,13 @@ int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
     // unconditionally)
     if (e == hipSuccess) e = hipMalloc(&h->hp, sizeof(u32x4_t) * (h->nunits + 3) * 4 * 4 * 64);
     if (e == hipSuccess) e = hipMalloc(&h->hx, sizeof(u32x4_t) * (super_units(h->nunits) + 1) * 4 * 64);
+    const uint32_t sb = blocks_for(h->ntiles, kRTS, kNWS4);
+    if (sb * kNWS4 <= kSampleMaxWaves) {
+        h->sample_blocks = sb;
+        const size_t n = static_cast<size_t>(kSampleRows) * sb * kNWS4;
+        if (e == hipSuccess) e = hipMalloc(&h->stats.key, n * sizeof(uint64_t));
+        if (e == hipSuccess) e = hipMalloc(&h->stats.sum, n * sizeof(double));
+    }
     if (e != hipSuccess) {
         twd_head_destroy(h);
         return hip_fail(e, "allocating the LM head");
@@ -1249,6 +1404,65 @@ int launch_head_rmsnorm(twd_head* h, const float* x, const uint16_t* norm_w, flo
     return TWD_OK;
 }
 
+// The fused sample pass: the resident-h kernel in sample mode (softcap, penalty from LDS
+// occurrence counts, logits store, per-block statistics), then select_sample_merge_kernel. Used
+// for rows <= 4 when the head's block count allows it and the rows' histories (where the
+// penalty applies) hold at most kSampleMaxHistory ids together: every head block scans them.
+constexpr uint32_t kSampleMaxHistory = 16384;
+
+bool sample_fusable(const twd_head* h, uint32_t rows, const twd_row_params* params) {
+    if (rows == 0 || rows > kSampleRows || h->sample_blocks == 0) return false;
+    uint64_t ids = 0;
+    for (uint32_t m = 0; m < rows; ++m)
+        if (params[m].repetition_penalty != 1.0f) ids += params[m].history_len;
+    return ids <= kSampleMaxHistory;
+}
+
+// x/norm_w/eps select the RMSNorm prologue (x != nullptr) instead of bf16 hidden rows.
+int launch_head_sample(twd_head* h, const uint16_t* hidden, const float* x, const uint16_t* norm_w,
+                       float eps, uint32_t rows, const twd_row_params* params,
+                       const uint32_t* history, float* logits, uint32_t* tokens, hipStream_t stream) {
+    HeadArgs a{};
+    a.tiled = h->tiled;
+    a.ntiles = h->ntiles;
+    a.nunits = h->nunits;
+    a.h = hidden;
+    a.M = rows;
+    a.d = h->d;
+    a.softcap = h->softcap;
+    a.logits = logits;
+    a.vocab = h->vocab;
+    a.x = x;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.history = history;
+    for (uint32_t m = 0; m < kSampleRows; ++m) {
+        const bool live = m < rows;
+        a.rp[m] = live ? params[m].repetition_penalty : 1.0f;
+        // the bound apply_repetition_penalty clamps to (sampling.cpp:79), in the same fp32
+        a.clamp[m] = (live && params[m].softcap > 0.0f) ? params[m].softcap * 0.9999f : 0.0f;
+        a.hist_off[m] = live ? params[m].history_offset : 0u;
+        a.hist_len[m] = live ? params[m].history_len : 0u;
+        if (!live) continue;
+        if (params[m].temperature > 0.0f && params[m].top_k > static_cast<int32_t>(TWD_MAX_WANT))
+            return fail(TWD_E_UNSUPPORTED, "top_k > 256 is not supported on the device path (validate_sampling rejects it)");
+        if (params[m].repetition_penalty != 1.0f && params[m].history_len > 0 && !history)
+            return fail(TWD_E_INVALID, "null history with a non-empty history_len");
+    }
+    a.stats = h->stats;
+    const uint32_t grid = h->sample_blocks;
+    if (x) {
+        const size_t bytes = small_smem_bytes<kPFS>(2 * rows, h->d);
+        head_small_kernel<4, kRTS, kPFS, kNWS4, kModeSample, true><<<grid, kNWS4 * 64, bytes, stream>>>(a);
+    } else {
+        head_small_kernel<4, kRTS, kPFS, kNWS4, kModeSample><<<grid, kNWS4 * 64, small_smem_bytes<kPFS>(rows, h->d),
+                                                             stream>>>(a);
+    }
+    TWD_HIP(hipGetLastError());
+    static_assert(kRTS * kTileRows == kSampleWaveRows, "a wave of the sample pass owns 64 rows");
+    return launch_sample_merge(h->stats, grid * kNWS4, logits, h->vocab, rows, params, tokens, stream);
+}
+
 // Runs one call's launches with the head's cross-stream ordering around them.
 template <typename F>
 int ordered(twd_head* h, void* stream, F&& launches) {
@@ -1343,6 +1557,8 @@ TWD_API void twd_head_destroy(twd_head* h) {
     if (h->hx) (void)hipFree(h->hx);
     if (h->sel) twd_selector_destroy(h->sel);
     if (h->norm_w) (void)hipFree(h->norm_w);
+    if (h->stats.key) (void)hipFree(h->stats.key);
+    if (h->stats.sum) (void)hipFree(h->stats.sum);
     order_release(h->order);
     delete h;
 }
@@ -1396,6 +1612,12 @@ TWD_API int twd_head_sample(twd_head* h, const uint16_t* hidden, uint32_t rows,
     clear_error();
     if (!logits || !tokens || !params) return fail(TWD_E_INVALID, "null logits, tokens or params");
     return ordered(h, stream, [&](hipStream_t s) {
+        if (sample_fusable(h, rows, params)) {
+            if (!hidden || !aligned16(hidden))
+                return fail(TWD_E_INVALID, "hidden must be a 16-byte aligned device pointer");
+            return launch_head_sample(h, hidden, nullptr, nullptr, 0.0f, rows, params, history, logits,
+                                      tokens, s);
+        }
         int rc = launch_head<kModeLogits>(h, hidden, rows, logits, nullptr, nullptr, 0, nullptr, s);
         if (rc) return rc;
         return launch_select(h->sel->scratch, logits, h->vocab, rows, h->vocab, params, history,
@@ -1444,6 +1666,13 @@ TWD_API int twd_head_sample_rmsnorm(twd_head* h, const float* x, const uint16_t*
     clear_error();
     if (!logits || !tokens || !params) return fail(TWD_E_INVALID, "null logits, tokens or params");
     return ordered(h, stream, [&](hipStream_t s) {
+        if (sample_fusable(h, rows, params)) {
+            if (!x || !aligned16(x)) return fail(TWD_E_INVALID, "x must be a 16-byte aligned device pointer");
+            if (!norm_w || !aligned16(norm_w))
+                return fail(TWD_E_INVALID, "norm_weight must be a 16-byte aligned device pointer");
+            if (!(eps >= 0.0f) || !std::isfinite(eps)) return fail(TWD_E_INVALID, "eps must be finite and >= 0");
+            return launch_head_sample(h, nullptr, x, norm_w, eps, rows, params, history, logits, tokens, s);
+        }
         int rc = launch_head_rmsnorm<kModeLogits>(h, x, norm_w, eps, rows, logits, nullptr, nullptr, 0,
                                                   nullptr, s);
         if (rc) return rc;

@@ -156,32 +156,10 @@ __device__ __forceinline__ void block_stats(uint32_t& flag, float& mx, float& mn
     __syncthreads();
 }
 
-// exp(x) for the row sum, x = l - max <= 0 with l and max floats (so x is exact in double).
-// Tang's table method: x = k ln2/64 + r with |r| <= ln2/128 (Cody-Waite split of ln2/64),
-// exp(x) = 2^(k>>6) * 2^((k&63)/64) * e^r, e^r by its degree-5 Taylor polynomial (truncation
-// below 4e-17 relative). tbl holds 2^(j/64), j = 0..63. Within 2 ulp; only the sum over the
-// row uses it, whose summation order already differs from the reference's in the last bits.
-__device__ __forceinline__ double exp_for_sum(double x, const double* tbl) {
-    if (x != x) return x;        // NaN stays NaN (+inf - +inf): the row total becomes NaN
-    if (x < -745.5) return 0.0;  // also -inf
-    const double kInvL = 92.332482616893656;             // 64 / ln2
-    const double kLHi = 6.93147180369123816490e-01 / 64;  // ln2 / 64, high part (exact products)
-    const double kLLo = 1.90821492927058770002e-10 / 64;  // ln2 / 64, low part
-    const double kd = __builtin_rint(x * kInvL);
-    const int k = static_cast<int>(kd);
-    double r = fma(-kd, kLHi, x);
-    r = fma(-kd, kLLo, r);
-    double p = fma(r, 1.0 / 120.0, 1.0 / 24.0);
-    p = fma(r, p, 1.0 / 6.0);
-    p = fma(r, p, 0.5);
-    p = fma(r, p, 1.0);
-    p = fma(r, p, 1.0);
-    return ldexp(tbl[k & 63] * p, k >> 6);
-}
-
 // The smallest rank T with exactly `want` of the block's ranks >= T (ranks are distinct; rank
 // 0 marks an empty slot and is never selected while want <= number of real ranks). Radix
 // descent over 8-bit digits from the top, stopping once a digit bin is taken whole.
+// PER = 0: `per` entries per thread with a loop that is not unrolled (entries read from memory).
 template <int NT, int PER, typename KeyAt>
 __device__ __forceinline__ uint64_t block_select(KeyAt key_at, int per, uint32_t want, uint32_t* hist,
                                                  SelCommon& c) {
@@ -191,11 +169,18 @@ __device__ __forceinline__ uint64_t block_select(KeyAt key_at, int per, uint32_t
     for (int shift = 56; shift >= 0; shift -= 8) {
         for (int i = tid; i < 256; i += NT) hist[i] = 0;
         __syncthreads();
-#pragma unroll
-        for (int e = 0; e < PER; ++e) {
-            if (e >= per) break;
+        auto count = [&](int e) {
             const uint64_t k = key_at(e);
             if (k != 0 && (k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+        };
+        if constexpr (PER > 0) {
+#pragma unroll
+            for (int e = 0; e < PER; ++e) {
+                if (e >= per) break;
+                count(e);
+            }
+        } else {
+            for (int e = 0; e < per; ++e) count(e);
         }
         __syncthreads();
         if (wave == 0) {
@@ -406,8 +391,16 @@ __device__ __forceinline__ void block_sort_desc(SelCommon& c, uint32_t n) {
 }
 
 // Steps 5-7 of sample_token on the sorted shortlist c.sorted[0..want) (sampling.cpp:139-168).
+// Every thread i < want computes its two terms as the reference does: e_i = exp(l_i - max) /
+// total (top-p, at T = 1) and q_i = exp((l_i - max) / T). The two sequential double sums then run
+// in reference order on two lanes of wave 0, one v_add per term for both: lane 0 forms the
+// running sums acc_i of q (stored back), lane 1 the top-p running sum, kChunk terms at a time,
+// until lane 1's sum reaches p (the cut). denom is acc at the cut (the additions of the
+// reference's denom loop), and the draw -- the first i < cut with acc_i >= u * denom, else
+// cut - 1 -- is a ballot over the stored sums in wave 0. Needs want <= blockDim.x. The id is
+// returned to the threads of wave 0 (callers store it from thread 0).
 __device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, const twd_row_params& p) {
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
     const double mx = static_cast<double>(c.gmax);
     const double total = c.total;
     const double td = static_cast<double>(p.temperature);
@@ -417,65 +410,54 @@ __device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, 
         c.q[tid] = exp((l - mx) / td);
     }
     __syncthreads();
-    // One lane runs the reference's sequential loops in their order; entries are fetched eight
-    // at a time so the LDS latency is paid once per chunk rather than once per addition.
-    constexpr uint32_t kChunk = 8;
-    if (tid == 0) {
-        uint32_t cut = want;
-        if (p.top_p < 1.0f) {
-            const double pp = static_cast<double>(p.top_p);
-            double run = 0.0;
-            bool found = false;
-            for (uint32_t i0 = 0; i0 < want && !found; i0 += kChunk) {
-                double ev[kChunk];
+    if (tid >= 64) return 0;
+    constexpr uint32_t kChunk = 16;
+    const bool topp = p.top_p < 1.0f;
+    const double pp = static_cast<double>(p.top_p);
+    uint32_t cut = want;
+    if (lane < 2) {
+        // lane 0 reads q and stores its running sums over q; lane 1 reads e and stores its own
+        // (unused) over e, so that no store needs a branch
+        double* src = lane == 0 ? c.q : c.e;
+        double run = 0.0;
+        for (uint32_t i0 = 0; i0 < want; i0 += kChunk) {
+            double x[kChunk], pre[kChunk];
 #pragma unroll
-                for (uint32_t j = 0; j < kChunk; ++j) ev[j] = c.e[min(i0 + j, want - 1)];
-#pragma unroll
-                for (uint32_t j = 0; j < kChunk; ++j) {
-                    if (!found && i0 + j < want) {
-                        run += ev[j];
-                        if (run >= pp) {
-                            cut = i0 + j + 1;
-                            found = true;
-                        }
-                    }
-                }
-            }
-        }
-        if (p.top_k > 0 && cut > static_cast<uint32_t>(p.top_k)) cut = static_cast<uint32_t>(p.top_k);
-        if (cut < 1) cut = 1;
-        double denom = 0.0;
-        for (uint32_t i0 = 0; i0 < cut; i0 += kChunk) {
-            double qv[kChunk];
-#pragma unroll
-            for (uint32_t j = 0; j < kChunk; ++j) qv[j] = c.q[min(i0 + j, cut - 1)];
+            for (uint32_t j = 0; j < kChunk; ++j) x[j] = src[min(i0 + j, want - 1)];
 #pragma unroll
             for (uint32_t j = 0; j < kChunk; ++j) {
-                if (i0 + j < cut) {
-                    denom += qv[j];
-                    c.q[i0 + j] = denom;  // the running sums acc_i of the draw loop
-                }
+                run += x[j];
+                pre[j] = run;
             }
-        }
-        const double r = static_cast<double>(p.uniform) * denom;
-        uint32_t pick = cut - 1;
-        bool found = false;
-        for (uint32_t i0 = 0; i0 < cut && !found; i0 += kChunk) {
-            double qv[kChunk];
-#pragma unroll
-            for (uint32_t j = 0; j < kChunk; ++j) qv[j] = c.q[min(i0 + j, cut - 1)];
+            uint32_t hit = 0;
 #pragma unroll
             for (uint32_t j = 0; j < kChunk; ++j) {
-                if (!found && i0 + j < cut && qv[j] >= r) {
-                    pick = i0 + j;
-                    found = true;
-                }
+                src[i0 + j] = pre[j];  // i0 + j < want rounded up to kChunk <= kMaxWant
+                hit |= (pre[j] >= pp ? 1u : 0u) << j;
+            }
+            // lane 1's sums decide; entries past want repeat the last term and never count
+            uint32_t h1 = __builtin_amdgcn_readlane(hit, 1);
+            h1 &= want - i0 >= kChunk ? 0xFFFFu : ((1u << (want - i0)) - 1u);
+            if (topp && h1 != 0) {  // lane 0's sums cover the cut
+                cut = i0 + static_cast<uint32_t>(__builtin_ctz(h1)) + 1;
+                break;
             }
         }
-        c.misc[5] = rank_index(c.sorted[pick]);
     }
-    __syncthreads();
-    return c.misc[5];
+    cut = __builtin_amdgcn_readfirstlane(cut);
+    if (p.top_k > 0 && cut > static_cast<uint32_t>(p.top_k)) cut = static_cast<uint32_t>(p.top_k);
+    if (cut < 1) cut = 1;
+    const double r = static_cast<double>(p.uniform) * c.q[cut - 1];  // r = u * denom
+    uint32_t pick = cut - 1;  // the reference's fallback: the last survivor
+    for (uint32_t i0 = 0; i0 < cut; i0 += 64) {
+        const uint32_t i = i0 + static_cast<uint32_t>(lane);
+        const uint64_t m = __ballot(i < cut && c.q[min(i, cut - 1)] >= r);
+        if (m != 0) {
+            pick = i0 + static_cast<uint32_t>(__ffsll(static_cast<long long>(m)) - 1);
+            break;
+        }
+    }
+    return rank_index(c.sorted[pick]);
 }
 
 // After c.top[0..want) holds the row's shortlist and c.gmax/total/flag its statistics:
@@ -607,7 +589,7 @@ void select_slice_kernel(SelectArgs args_by_value, SelectBufs b) {
             if (__builtin_isfinite(v[e])) mn = fminf(mn, v[e]);
         }
     }
-    if (tid < 64) sh.c.exp2_tbl[tid] = exp2(static_cast<double>(tid) / 64.0);
+    if (tid < 64) sh.c.exp2_tbl[tid] = kExp2Table[tid];
     block_stats<NT>(nan_seen, mx, mn, sh.c);  // its barriers also retire the penalty's counts
     const double dmx = static_cast<double>(mx);
     double s = 0.0;
@@ -760,6 +742,262 @@ __global__ __launch_bounds__(kMergeThreads) void select_merge_kernel(SelectArgs 
     finish_row(sh.c, want_row, p, b.tokens + row);
 }
 
+// ---- after the head's sample mode: one block per row ---------------------------------------------
+//
+// The head's waves have applied the penalty (the logits hold the penalised rows) and published
+// per wave {best rank, sum exp(v - best value) in double, NaN when a NaN was seen}, one record
+// per 64 vocabulary rows. This kernel finishes sample_token (sampling.cpp:92-169) per row:
+//   * greedy rows take the best rank over the waves;
+//   * the row max and the rescaled sum of exponentials come from the records (a NaN sum makes
+//     the row degenerate, as the reference's NaN total does);
+//   * the shortlist only needs the waves that can hold a top-`want` entry. The wave maxima are
+//     binned by distance from the row max (256 bins, monotone in the value) and b* is the first
+//     bin at which `want` maxima have been counted: `want` entries lie in bins <= b*, so the
+//     want-th largest entry X does too, every top-`want` entry is in a bin <= b*, and it lives in
+//     a wave whose maximum is in a bin <= b*. Only those waves' rows are read, and only entries
+//     in bins <= b* are kept;
+//   * the survivors are ranked exactly (by counting when they fit one per thread, else by
+//     block_top; by a radix select over the candidate waves' rows in memory if they overflow
+//     the LDS list), then steps 5-7 run on one wave from registers.
+constexpr int kSmThreads = 1024;
+constexpr uint32_t kSmPer = kSampleMaxWaves / kSmThreads;  // wave records per thread
+constexpr uint32_t kSmCap = 2048;     // survivors kept in LDS
+constexpr uint32_t kSmMaxCand = 2048; // candidate waves listed in LDS
+
+struct SampleMergeBufs {
+    const float* logits;  // [rows][vocab], penalised
+    uint32_t vocab;
+    uint32_t waves;       // head waves (records per row)
+    SampleStats st;
+    uint32_t* tokens;
+};
+
+struct SampleMergeShared {
+    uint32_t cwave[kSmMaxCand];  // the candidate waves
+    uint64_t cand[kSmCap];       // surviving ranks
+    TopScratch t;
+    SelCommon c;
+};
+
+__global__ __launch_bounds__(kSmThreads) void select_sample_merge_kernel(SelectArgs args_by_value,
+                                                                         SampleMergeBufs b) {
+    constexpr int NT = kSmThreads;
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    SampleMergeShared& sh = *reinterpret_cast<SampleMergeShared*>(smem_raw);
+#if __HIP_DEVICE_COMPILE__
+    const SelectArgs& args =
+        *reinterpret_cast<const SelectArgs*>(__builtin_amdgcn_kernarg_segment_ptr());
+#else
+    const SelectArgs& args = args_by_value;
+#endif
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t row = blockIdx.x;
+    const twd_row_params p = args.p[row];
+    const uint32_t W = b.waves;
+    const size_t o = static_cast<size_t>(row) * W;
+    const float* lg = b.logits + static_cast<size_t>(row) * b.vocab;
+
+    // ---- the wave records, one round trip: thread tid holds waves tid + NT * q
+    uint64_t key[kSmPer];
+    double wsum[kSmPer];
+#pragma unroll
+    for (uint32_t q = 0; q < kSmPer; ++q) {
+        const uint32_t i = tid + NT * q;
+        key[q] = i < W ? b.st.key[o + i] : 0ull;
+        wsum[q] = i < W ? b.st.sum[o + i] : 0.0;
+    }
+    for (uint32_t i = tid; i < kReps * kBins; i += NT) sh.t.hist[i] = 0;
+    if (!(p.temperature > 0.0f)) {  // greedy: the best rank over the waves
+        uint64_t k = 0;
+#pragma unroll
+        for (uint32_t q = 0; q < kSmPer; ++q) k = key[q] > k ? key[q] : k;
+        k = block_max_u64<NT>(k, sh.c);
+        if (tid == 0) b.tokens[row] = rank_index(k);
+        return;
+    }
+    float wm[kSmPer];
+    uint32_t flag = 0;
+    float gm = -INFINITY, mn = INFINITY;
+#pragma unroll
+    for (uint32_t q = 0; q < kSmPer; ++q) {
+        wm[q] = key[q] != 0 ? rank_value(key[q]) : -INFINITY;
+        if (wsum[q] != wsum[q]) flag = 1;
+        gm = fmaxf(gm, wm[q]);
+        if (key[q] != 0 && __builtin_isfinite(wm[q])) mn = fminf(mn, wm[q]);
+    }
+    if (tid < 64) sh.c.exp2_tbl[tid] = kExp2Table[tid];
+    block_stats<NT>(flag, gm, mn, sh.c);  // NaN seen, row max, smallest finite wave max
+    double part = 0.0;
+#pragma unroll
+    for (uint32_t q = 0; q < kSmPer; ++q)
+        if (key[q] != 0 && wsum[q] != 0.0)
+            part += wsum[q] * exp_for_sum(static_cast<double>(wm[q]) - static_cast<double>(gm), sh.c.exp2_tbl);
+    const double total = block_sum_f64<NT>(part, sh.c);
+    if (flag != 0 || !(total > 0.0)) {  // sampling.cpp:116-118
+        if (tid == 0) b.tokens[row] = TWD_TOKEN_DEGENERATE;
+        return;
+    }
+    const uint32_t want = (p.top_k > 0) ? min(static_cast<uint32_t>(p.top_k), b.vocab)
+                                        : min(kMaxWant, b.vocab);
+
+    // ---- b*: bins of distance from the row max (block_top's binning), 8 replicas
+    const float span = gm - mn;
+    const bool binned = __builtin_isfinite(gm) && __builtin_isfinite(mn) && span > 0.0f;
+    const float scale = binned ? static_cast<float>(kBins - 1) / (span < kBinRange ? span : kBinRange) : 0.0f;
+    auto bin_of = [&](float x) -> uint32_t {
+        if (!binned) return 0u;
+        const float dist = (gm - x) * scale;
+        return dist < static_cast<float>(kBins - 2) ? static_cast<uint32_t>(dist) : kBins - 2;
+    };
+#pragma unroll
+    for (uint32_t q = 0; q < kSmPer; ++q)
+        if (key[q] != 0) atomicAdd(&sh.t.hist[bin_of(wm[q]) * kReps + (lane & (kReps - 1))], 1u);
+    __syncthreads();
+    if (wave == 0) {  // lane l owns bins 4l .. 4l + 3
+        uint32_t cc[4], tsum = 0;
+        const u32x4* h4 = reinterpret_cast<const u32x4*>(sh.t.hist) + lane * (4 * kReps / 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const u32x4 x = h4[2 * j], y = h4[2 * j + 1];
+            cc[j] = x.x + x.y + x.z + x.w + y.x + y.y + y.z + y.w;
+            tsum += cc[j];
+        }
+        uint32_t incl = tsum;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint32_t y = __shfl_up(incl, off);
+            if (lane >= off) incl += y;
+        }
+        uint32_t before = incl - tsum;
+        if (lane == 63) sh.c.misc[0] = kBins - 1;  // fewer maxima than want: every bin
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (before < want && want <= before + cc[j]) sh.c.misc[0] = 4 * lane + j;
+            before += cc[j];
+        }
+        if (lane == 0) {
+            sh.c.misc[3] = 0;  // candidate waves
+            sh.c.misc[4] = 0;  // survivors
+        }
+    }
+    __syncthreads();
+    const uint32_t bstar = sh.c.misc[0];
+    // the candidate waves, in any order
+#pragma unroll
+    for (uint32_t q = 0; q < kSmPer; ++q) {
+        const uint32_t i = tid + NT * q;
+        const bool is_cand = key[q] != 0 && bin_of(wm[q]) <= bstar;
+        const uint64_t mask = __ballot(is_cand);
+        if (mask != 0) {
+            const int leader = __ffsll(static_cast<long long>(mask)) - 1;
+            uint32_t base = 0;
+            if (lane == leader) base = atomicAdd(&sh.c.misc[3], static_cast<uint32_t>(__popcll(mask)));
+            base = __builtin_amdgcn_readlane(base, leader);
+            if (is_cand) {
+                const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+                if (base + below < kSmMaxCand) sh.cwave[base + below] = i;
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t ncw = sh.c.misc[3];
+    if (ncw > kSmMaxCand) {
+        // a candidate list this long only comes from values that barely bin (huge ties): the
+        // two-launch path's kernels are not reachable from here, so rank over every wave
+        if (tid == 0) sh.c.misc[3] = 0;
+        __syncthreads();
+    }
+    const bool all_waves = ncw > kSmMaxCand;
+    const uint32_t nent = all_waves ? W * kSampleWaveRows : ncw * kSampleWaveRows;  // entries to scan
+    auto entry_row = [&](uint32_t f) -> uint32_t {  // row of entry f of the candidate waves
+        const uint32_t w = all_waves ? f / kSampleWaveRows : sh.cwave[f / kSampleWaveRows];
+        return w * kSampleWaveRows + f % kSampleWaveRows;
+    };
+
+    // ---- survivors: entries in bins <= b* of the candidate waves, kGatherBatch loads at a time
+    float smn = INFINITY;
+    constexpr uint32_t kGatherBatch = 8;
+    const uint32_t per = (nent + NT - 1) / NT;
+    for (uint32_t i0 = 0; i0 < per; i0 += kGatherBatch) {
+        float v[kGatherBatch];
+        uint32_t r[kGatherBatch];
+#pragma unroll
+        for (uint32_t q = 0; q < kGatherBatch; ++q) {
+            const uint32_t f = (i0 + q) * NT + static_cast<uint32_t>(tid);
+            r[q] = 0xFFFFFFFFu;
+            v[q] = 0.0f;
+            if (i0 + q < per && f < nent) {
+                const uint32_t rr = entry_row(f);
+                if (rr < b.vocab) {
+                    r[q] = rr;
+                    v[q] = lg[rr];
+                }
+            }
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < kGatherBatch; ++q) {
+            const bool keep = r[q] != 0xFFFFFFFFu && bin_of(v[q]) <= bstar;
+            if (keep && __builtin_isfinite(v[q])) smn = fminf(smn, v[q]);
+            wave_put(keep, keep ? rank_key(v[q], r[q]) : 0ull, &sh.c.misc[4], sh.cand, kSmCap);
+        }
+    }
+    uint32_t no_flag = 0;
+    float no_max = -INFINITY;
+    block_stats<NT>(no_flag, no_max, smn, sh.c);  // the survivors' smallest finite value
+    const uint32_t n = sh.c.misc[4];              // may exceed kSmCap: then only counted
+
+    // ---- the shortlist, sorted (value desc, index asc)
+    if (n <= static_cast<uint32_t>(NT)) {
+        if (static_cast<uint32_t>(tid) < n) {
+            const uint64_t k = sh.cand[tid];
+            uint32_t higher = 0;
+#pragma unroll 8
+            for (uint32_t j = 0; j < n; ++j) higher += sh.cand[j] > k ? 1u : 0u;
+            if (higher < want) sh.c.sorted[higher] = k;
+        }
+        __syncthreads();
+    } else if (n <= kSmCap) {
+        auto merge_key = [&](int e) -> uint64_t {
+            const uint32_t f = tid + NT * e;
+            return f < n ? sh.cand[f] : 0ull;
+        };
+        auto merge_val = [&](int e) -> float { return rank_value(merge_key(e)); };
+        for (uint32_t i = tid; i < kReps * kBins; i += NT) sh.t.hist[i] = 0;
+        __syncthreads();
+        block_top<NT, kSmCap / NT>(merge_val, merge_key, merge_val, merge_key, static_cast<int>((n + NT - 1) / NT),
+                                   gm, smn, want, sh.c.top, sh.t, sh.c);
+        block_sort_desc(sh.c, want);
+    } else {
+        // overflow (heavy ties): a radix select over the candidate waves' rows in memory
+        auto cand_key = [&](int e) -> uint64_t {
+            const uint32_t f = static_cast<uint32_t>(e) * NT + static_cast<uint32_t>(tid);
+            if (f >= nent) return 0ull;
+            const uint32_t rr = entry_row(f);
+            if (rr >= b.vocab) return 0ull;
+            const float x = lg[rr];
+            return bin_of(x) <= bstar ? rank_key(x, rr) : 0ull;
+        };
+        const uint64_t thr = block_select<NT, 0>(cand_key, static_cast<int>(per), want, sh.t.hist, sh.c);
+        if (tid == 0) sh.c.misc[4] = 0;
+        __syncthreads();
+        for (uint32_t e = 0; e < per; ++e) {
+            const uint64_t k = cand_key(static_cast<int>(e));
+            wave_put(k != 0 && k >= thr, k, &sh.c.misc[4], sh.c.top, want);
+        }
+        __syncthreads();
+        block_sort_desc(sh.c, want);
+    }
+    if (tid == 0) {
+        sh.c.gmax = gm;
+        sh.c.total = total;
+    }
+    __syncthreads();
+    const uint32_t tok = finish_sampled(sh.c, want, p);
+    if (tid == 0) b.tokens[row] = tok;
+}
+
 __global__ void verify_compare_kernel(const uint32_t* row_tokens, uint32_t rows,
                                       const uint32_t* drafts, uint32_t nd,
                                       twd_verify_result* v) {
@@ -906,6 +1144,10 @@ int enable_select_kernels() {
             err = hipFuncSetAttribute(reinterpret_cast<const void*>(select_merge_kernel),
                                       hipFuncAttributeMaxDynamicSharedMemorySize,
                                       static_cast<int>(sizeof(MergeShared)));
+        if (err == hipSuccess)
+            err = hipFuncSetAttribute(reinterpret_cast<const void*>(select_sample_merge_kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      static_cast<int>(sizeof(SampleMergeShared)));
     });
     if (err != hipSuccess) return hip_fail(err, "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
     return TWD_OK;
@@ -951,6 +1193,28 @@ int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_
         select_merge_kernel<<<rows, kMergeThreads, sizeof(MergeShared), stream>>>(a, b);
         TWD_HIP(hipGetLastError());
     }
+    return TWD_OK;
+}
+
+int launch_sample_merge(const SampleStats& st, uint32_t waves, const float* logits, uint32_t vocab,
+                        uint32_t rows, const twd_row_params* params, uint32_t* tokens,
+                        hipStream_t stream) {
+    if (waves == 0 || waves > kSampleMaxWaves) return fail(TWD_E_INVALID, "sample merge: head waves out of range");
+    if (rows == 0 || rows > TWD_MAX_ROWS) return fail(TWD_E_INVALID, "sample merge: rows out of range");
+    int rc = enable_select_kernels();
+    if (rc) return rc;
+    SelectArgs a{};
+    a.rows = rows;
+    a.parts = waves;
+    for (uint32_t r = 0; r < rows; ++r) a.p[r] = params[r];
+    SampleMergeBufs b{};
+    b.logits = logits;
+    b.vocab = vocab;
+    b.waves = waves;
+    b.st = st;
+    b.tokens = tokens;
+    select_sample_merge_kernel<<<rows, kSmThreads, sizeof(SampleMergeShared), stream>>>(a, b);
+    TWD_HIP(hipGetLastError());
     return TWD_OK;
 }
 

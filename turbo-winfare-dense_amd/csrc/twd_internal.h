@@ -82,6 +82,52 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return v;
 }
 
+// 2^(j/64), j = 0..63, each the double nearest the exact value: the table of exp_for_sum.
+static __constant__ double kExp2Table[64] = {
+    0x1.0000000000000p+0, 0x1.02c9a3e778061p+0, 0x1.059b0d3158574p+0, 0x1.0874518759bc8p+0,
+    0x1.0b5586cf9890fp+0, 0x1.0e3ec32d3d1a2p+0, 0x1.11301d0125b51p+0, 0x1.1429aaea92de0p+0,
+    0x1.172b83c7d517bp+0, 0x1.1a35beb6fcb75p+0, 0x1.1d4873168b9aap+0, 0x1.2063b88628cd6p+0,
+    0x1.2387a6e756238p+0, 0x1.26b4565e27cddp+0, 0x1.29e9df51fdee1p+0, 0x1.2d285a6e4030bp+0,
+    0x1.306fe0a31b715p+0, 0x1.33c08b26416ffp+0, 0x1.371a7373aa9cbp+0, 0x1.3a7db34e59ff7p+0,
+    0x1.3dea64c123422p+0, 0x1.4160a21f72e2ap+0, 0x1.44e086061892dp+0, 0x1.486a2b5c13cd0p+0,
+    0x1.4bfdad5362a27p+0, 0x1.4f9b2769d2ca7p+0, 0x1.5342b569d4f82p+0, 0x1.56f4736b527dap+0,
+    0x1.5ab07dd485429p+0, 0x1.5e76f15ad2148p+0, 0x1.6247eb03a5585p+0, 0x1.6623882552225p+0,
+    0x1.6a09e667f3bcdp+0, 0x1.6dfb23c651a2fp+0, 0x1.71f75e8ec5f74p+0, 0x1.75feb564267c9p+0,
+    0x1.7a11473eb0187p+0, 0x1.7e2f336cf4e62p+0, 0x1.82589994cce13p+0, 0x1.868d99b4492edp+0,
+    0x1.8ace5422aa0dbp+0, 0x1.8f1ae99157736p+0, 0x1.93737b0cdc5e5p+0, 0x1.97d829fde4e50p+0,
+    0x1.9c49182a3f090p+0, 0x1.a0c667b5de565p+0, 0x1.a5503b23e255dp+0, 0x1.a9e6b5579fdbfp+0,
+    0x1.ae89f995ad3adp+0, 0x1.b33a2b84f15fbp+0, 0x1.b7f76f2fb5e47p+0, 0x1.bcc1e904bc1d2p+0,
+    0x1.c199bdd85529cp+0, 0x1.c67f12e57d14bp+0, 0x1.cb720dcef9069p+0, 0x1.d072d4a07897cp+0,
+    0x1.d5818dcfba487p+0, 0x1.da9e603db3285p+0, 0x1.dfc97337b9b5fp+0, 0x1.e502ee78b3ff6p+0,
+    0x1.ea4afa2a490dap+0, 0x1.efa1bee615a27p+0, 0x1.f50765b6e4540p+0, 0x1.fa7c1819e90d8p+0,
+};
+
+// exp(x) for the row sum, x = l - max <= 0 with l and max floats (so x is exact in double).
+// Tang's table method: x = k ln2/64 + r with |r| <= ln2/128 (Cody-Waite split of ln2/64),
+// exp(x) = 2^(k>>6) * 2^((k&63)/64) * e^r, e^r by its degree-5 Taylor polynomial (truncation
+// below 4e-17 relative). tbl holds 2^(j/64), j = 0..63. Within 2 ulp; only the sum over the
+// row uses it, whose summation order already differs from the reference's in the last bits.
+__device__ __forceinline__ double exp_for_sum(double x, const double* tbl) {
+    // branch-free: the polynomial runs on a safe argument, then NaN (+inf - +inf) stays NaN
+    // and anything below -745.5 (also -inf) gives 0
+    const bool nan = x != x, tiny = x < -745.5;
+    const double xs = (nan || tiny) ? 0.0 : x;
+    const double kInvL = 92.332482616893656;             // 64 / ln2
+    const double kLHi = 6.93147180369123816490e-01 / 64;  // ln2 / 64, high part (exact products)
+    const double kLLo = 1.90821492927058770002e-10 / 64;  // ln2 / 64, low part
+    const double kd = __builtin_rint(xs * kInvL);
+    const int k = static_cast<int>(kd);
+    double r = fma(-kd, kLHi, xs);
+    r = fma(-kd, kLLo, r);
+    double p = fma(r, 1.0 / 120.0, 1.0 / 24.0);
+    p = fma(r, p, 1.0 / 6.0);
+    p = fma(r, p, 0.5);
+    p = fma(r, p, 1.0);
+    p = fma(r, p, 1.0);
+    const double v = ldexp(tbl[k & 63] * p, k >> 6);
+    return nan ? x : (tiny ? 0.0 : v);
+}
+
 // bf16 bit patterns <-> float
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
@@ -113,6 +159,22 @@ struct StreamOrder {
 int order_before(StreamOrder& o, hipStream_t s);  // before enqueueing work that uses the state
 int order_after(StreamOrder& o, hipStream_t s);   // after enqueueing it
 void order_release(StreamOrder& o);
+
+// ---- the fused sample pass ------------------------------------------------------------------------
+// The resident-h head kernel's sample mode publishes, per row m and wave w of the grid (index
+// m * waves + w), the selection statistics of the wave's 64 vocabulary rows [64 w, 64 w + 64);
+// select_sample_merge_kernel finishes the rows from them and the penalised logits.
+struct SampleStats {
+    uint64_t* key;  // best rank (value desc, index asc) of the wave's rows (0: none live)
+    double* sum;    // sum of exp(v - best value) over them in double; NaN when a NaN was seen
+};
+constexpr uint32_t kSampleMaxWaves = 8192;  // waves a fused sample pass may have
+constexpr uint32_t kSampleWaveRows = 64;    // vocabulary rows per wave
+
+// Enqueues the merge after a sample-mode head pass over `rows` rows (params: host array).
+int launch_sample_merge(const SampleStats& st, uint32_t waves, const float* logits, uint32_t vocab,
+                        uint32_t rows, const twd_row_params* params, uint32_t* tokens,
+                        hipStream_t stream);
 
 // ---- device scratch shared by the launch helpers ------------------------------------------------------
 struct SelectScratch {
