@@ -365,6 +365,14 @@ TWD_API int twd_verify_draft(twd_selector* sel, const float* logits, uint32_t vo
 TWD_API int twd_sequential_sum(const float* terms, uint32_t n, float thr, float* sum_out,
                                uint32_t* stop_out, void* stream);
 
+/* No counterpart in the reference: the fp32 softmax sums (compute_softmax, speculator.cpp:22-26)
+ * of the last twd_verify_draft call on this selector that ran the rejection branch, for
+ * diagnostics and tests. *n receives the number of positions that had draft rows; for each,
+ * positions[i] is the position and sums[2i], sums[2i + 1] the target and draft rows' sums (at
+ * most `capacity` positions). Waits for the device. */
+TWD_API int twd_verify_draft_sums(const twd_selector* sel, float* sums, uint32_t* positions,
+                                  uint32_t capacity, uint32_t* n);
+
 /* ---- the reference's seeding, for callers that keep seeds (src/sampling.cpp:18-72) -------- */
 TWD_API uint64_t twd_splitmix64(uint64_t x);
 TWD_API uint64_t twd_seed_for(int has_seed, uint64_t seed, int position);
@@ -390,6 +398,10 @@ TWD_API int twd_generate_head(void* wsb_dev, uint32_t vocab, uint32_t d_model,
 TWD_API int twd_probe_read_bandwidth(const void* buf, uint64_t bytes, uint32_t waves,
                                      uint32_t launches, void* stream, float* us_per_launch,
                                      uint64_t* bytes_read);
+/* No counterpart in the reference: out[i] = the device expf the draft-logits verify uses
+ * (glibc's expf method, bit-exact with the x86-64 host library) of x[i], for tests. Device
+ * buffers of n floats; asynchronous on `stream`. */
+TWD_API int twd_probe_expf(const float* x, float* out, uint64_t n, void* stream);
 /* Bytes of the reference layout for a V x d head with 64-wide groups. */
 TWD_API uint64_t twd_head_bytes(uint32_t vocab, uint32_t d_model, uint32_t group_size);
 

@@ -351,6 +351,11 @@ void or_rejection_uniforms(uint64_t step_seed, float* u1, float* u2) {
     *u2 = or_canonical_float(or_mt64_next(&g));
 }
 
+/* speculator.cpp:23: std::exp(float) is the C library's expf */
+void or_expf(const float* x, float* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = expf(x[i]);
+}
+
 /* speculator.cpp:14-30 */
 void or_softmax(float* l, uint32_t n, float temp) {
     if (temp <= 0.0f) temp = 1.0f;

@@ -132,6 +132,10 @@ int or_verify_draft(const uint32_t* drafts, size_t n_drafts, const float* const*
                     float repetition_penalty, uint64_t base_seed, or_verify_result* out,
                     or_reject_diag* diag);
 
+/* out[i] = expf(x[i]) of the host C library: std::exp(float) as compute_softmax calls it
+ * (speculator.cpp:23). */
+void or_expf(const float* x, float* out, size_t n);
+
 /* Scalar INT4 g64 LM head (cpu_reference.cpp:643-665): fp32 sequential dot over c, then
  * softcap*tanhf(sum/softcap) when softcap > 0. W is [V][d/8] u32, S/B are [V][d/G] bf16 bits,
  * hidden is fp32 [d]. Computes rows [row0, row0+nrows). */

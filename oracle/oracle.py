@@ -78,6 +78,8 @@ def _load():
         build(ref=False)
     lib = C.CDLL(LIB_PATH)
     lib.or_splitmix64.restype = C.c_uint64
+    lib.or_expf.argtypes = [_f32p, _f32p, C.c_size_t]
+    lib.or_expf.restype = None
     lib.or_splitmix64.argtypes = [C.c_uint64]
     lib.or_seed_for.restype = C.c_uint64
     lib.or_seed_for.argtypes = [C.c_int, C.c_uint64, C.c_int]
@@ -264,6 +266,14 @@ def std_rejection_uniforms(seeds) -> np.ndarray:
 
 def std_mt64_10000th() -> int:
     return int(lib().or_std_mt64_10000th())
+
+
+def expf(x) -> np.ndarray:
+    """The host C library's expf, as compute_softmax's std::exp(float) (speculator.cpp:23)."""
+    xs = _f32(x).copy()
+    out = np.empty_like(xs)
+    lib().or_expf(xs, out, xs.size)
+    return out
 
 
 def softmax(logits, temp: float) -> np.ndarray:

@@ -89,18 +89,27 @@ def _random_case(rng, vocab):
 @pytest.mark.parametrize("vocab", [3000, 50000, V])
 def test_verify_draft_random_vs_oracle(env, oracle, vocab):
     rng = np.random.default_rng(vocab)
-    n_rej = 0
+    n_rej = n_sums = 0
     for case in range(12 if vocab == V else 30):
         rows, drs, drafts, T, p, k, base = _random_case(rng, vocab)
         want = oracle.verify_draft(drafts, rows, drs, T, p, k, 1.0, base)
-        for i, d in enumerate(want.pop("diag")):
+        want_diag = want.pop("diag")
+        for i, d in enumerate(want_diag):
             if d is not None:
                 print(f"case {case} pos {i}: r={d['r']:.7g} u1={d['u1']:.7g} "
                       f"margin={abs(d['u1'] - d['r']):.3g} accepted={d['accepted']}")
                 n_rej += 0 if d["accepted"] else 1
         got = run_device(env, rows, drs, drafts, T, p, k, 1.0, base)
         assert same(got, want), (case, got, want)
-    assert n_rej > 0
+        # the compute_softmax sums, bit for bit, at every position that ran the ratio test
+        sums = env[3].draft_sums()
+        for i, d in enumerate(want_diag):
+            if d is not None:
+                sp, sq = sums[i]
+                assert np.float32(sp) == np.float32(d["sum_p"]) and np.float32(sq) == np.float32(d["sum_q"]), \
+                    (case, i, sp, d["sum_p"], sq, d["sum_q"])
+                n_sums += 1
+    assert n_rej > 0 and n_sums > 0
 
 
 def test_verify_draft_edges(env, oracle):
@@ -210,3 +219,20 @@ def test_sequential_sum_is_the_in_order_fp32_sum(env):
             assert stop == want, (name, frac, stop, want)
             # the sum returned with a stop is the prefix through the stop index
             assert np.float32(s).view(np.uint32) == acc[min(want, len(x) - 1)].view(np.uint32), (name, frac)
+
+
+def test_device_expf_matches_host(env, oracle):
+    # the device build of the verify's expf against the host C library's expf (the
+    # reference's std::exp(float)): every 16th float of [-104, 0], then random arguments
+    torch, dev, t, _ = env
+    top = int(np.float32(104.0).view(np.uint32))
+    neg = (np.arange(0, top + 1, 16, dtype=np.uint64).astype(np.uint32) | np.uint32(0x80000000)).view(np.float32)
+    rng = np.random.default_rng(5)
+    more = rng.uniform(-120, 95, 1 << 20).astype(np.float32)
+    special = np.array([np.inf, -np.inf, np.nan, 88.72, -103.97, 0.0, -0.0], np.float32)
+    for x in (neg, more, special):
+        got = t.probe_expf(torch.from_numpy(x).to(dev)).cpu().numpy()
+        want = oracle.expf(x)
+        both_nan = np.isnan(got) & np.isnan(want)
+        bad = (got.view(np.uint32) != want.view(np.uint32)) & ~both_nan
+        assert not bad.any(), (int(bad.sum()), x[bad][:5], got[bad][:5], want[bad][:5])

@@ -4,6 +4,9 @@
 // access pattern of the head kernels.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
+#include "expf_libm.h"
 #include "twd_internal.h"
 
 namespace twd {
@@ -38,6 +41,13 @@ __global__ __launch_bounds__(kProbeWaves * 64) void read_probe_kernel(const uint
 #pragma unroll
     for (int q = 0; q < kProbePF; ++q) acc ^= r[q].y;
     if (acc == 0x9E3779B9u) sink[0] = acc;  // keeps the loads; almost never taken
+}
+
+// The draft verify's device expf (expf_libm<true>) over n floats, for tests.
+__global__ void expf_probe_kernel(const float* __restrict__ x, float* __restrict__ out, uint64_t n) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = expf_libm<true>(x[i]);
 }
 
 }  // namespace
@@ -83,6 +93,16 @@ TWD_API int twd_probe_read_bandwidth(const void* buf, uint64_t bytes, uint32_t w
     if (e != hipSuccess) return hip_fail(e, "read probe");
     *us_per_launch = ms * 1000.0f / static_cast<float>(launches);
     if (bytes_read) *bytes_read = stripe * waves;
+    return TWD_OK;
+}
+
+TWD_API int twd_probe_expf(const float* x, float* out, uint64_t n, void* stream) {
+    clear_error();
+    if (n == 0) return TWD_OK;
+    if (!x || !out) return fail(TWD_E_INVALID, "null x or out");
+    const uint64_t blocks = std::min<uint64_t>((n + 255) / 256, 1u << 16);
+    expf_probe_kernel<<<static_cast<uint32_t>(blocks), 256, 0, static_cast<hipStream_t>(stream)>>>(x, out, n);
+    TWD_HIP(hipGetLastError());
     return TWD_OK;
 }
 

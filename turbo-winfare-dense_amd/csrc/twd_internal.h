@@ -201,6 +201,8 @@ struct DraftScratch {
     float* sums = nullptr;     // [2 * TWD_MAX_ROWS] softmax sums
     size_t e_capacity = 0;
     size_t part_capacity = 0;
+    uint32_t last_npos = 0;               // positions of the last call with draft rows
+    uint32_t last_pos[TWD_MAX_ROWS] = {};
 };
 
 int draft_scratch_reserve(DraftScratch* d, uint32_t vocab, uint32_t npos);

@@ -22,6 +22,7 @@
 #include <cmath>
 #include <cstring>
 
+#include "expf_libm.h"
 #include "twd_internal.h"
 
 // Every float expression in this file rounds each operation on its own: hipcc would otherwise
@@ -62,11 +63,6 @@ struct DraftArgs {
     DraftPos pos[TWD_MAX_ROWS];
 };
 
-// (float)exp((double)x): correctly rounded except where exp's double result lies within an ulp
-// of a float rounding boundary. The reference calls the host libm's expf.
-__device__ __forceinline__ float expf_cr(float x) {
-    return static_cast<float>(exp(static_cast<double>(x)));
-}
 
 __device__ __forceinline__ const float* draft_row(const DraftArgs& a, uint32_t r) {
     return (r & 1) ? a.pos[r >> 1].draft : a.pos[r >> 1].target;
@@ -118,7 +114,7 @@ __global__ __launch_bounds__(kDraftThreads) void draft_exp_kernel(DraftArgs a) {
         const uint32_t j = base + it * kDraftThreads;
         if (j < a.vocab) {
             const float x = l[j] / a.temp;
-            const float v = expf_cr(x - mx);
+            const float v = expf_libm<true>(x - mx);  // std::exp(float) of speculator.cpp:23
             nan |= (v != v);
             e[j] = v;
         }
@@ -631,6 +627,20 @@ using namespace twd;
 
 extern "C" {
 
+TWD_API int twd_verify_draft_sums(const twd_selector* sel, float* sums, uint32_t* positions,
+                                  uint32_t capacity, uint32_t* n) {
+    clear_error();
+    if (!sel || !n) return fail(TWD_E_INVALID, "null selector or n");
+    const uint32_t np = sel->draft.last_npos;
+    *n = np;
+    if (np == 0) return TWD_OK;
+    if (capacity < np || !sums || !positions) return fail(TWD_E_INVALID, "capacity below the positions of the last call");
+    TWD_HIP(hipDeviceSynchronize());
+    TWD_HIP(hipMemcpy(sums, sel->draft.sums, 2 * np * sizeof(float), hipMemcpyDeviceToHost));
+    for (uint32_t i = 0; i < np; ++i) positions[i] = sel->draft.last_pos[i];
+    return TWD_OK;
+}
+
 TWD_API int twd_sequential_sum(const float* terms, uint32_t n, float thr, float* sum_out,
                                uint32_t* stop_out, void* stream) {
     clear_error();
@@ -719,6 +729,8 @@ int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab
     a.flags = sel->draft.flags;
     a.rej = sel->draft.rej;
     a.sums = sel->draft.sums;
+    sel->draft.last_npos = a.npos;
+    for (uint32_t i = 0; i < a.npos; ++i) sel->draft.last_pos[i] = a.pos[i].position;
     const dim3 grid(a.parts, 2 * a.npos);
     draft_max_kernel<<<grid, kDraftThreads, 0, s>>>(a);
     draft_exp_kernel<<<grid, kDraftThreads, 0, s>>>(a);

@@ -143,6 +143,8 @@ _SIGS = {
     "twd_verify_draft": (C.c_int, [_vp, _vp, _u32, _u32, _u64, C.POINTER(_vp), _u32,
                                    C.POINTER(RowParams), _u64, _vp, _u32, _vp, _vp]),
     "twd_rejection_uniforms": (None, [_u64, C.POINTER(_f32), C.POINTER(_f32)]),
+    "twd_verify_draft_sums": (C.c_int, [_vp, C.POINTER(_f32), C.POINTER(_u32), _u32, C.POINTER(_u32)]),
+    "twd_probe_expf": (C.c_int, [_vp, _vp, _u64, _vp]),
     "twd_splitmix64": (_u64, [_u64]),
     "twd_seed_for": (_u64, [C.c_int, _u64, C.c_int]),
     "twd_uniform_from_seed": (_f32, [_u64]),
@@ -288,6 +290,14 @@ class Selector:
                               _stream(stream)))
         return result
 
+    def draft_sums(self) -> dict:
+        """{position: (target sum, draft sum)} of the last verify_draft that had draft rows."""
+        sums = (_f32 * (2 * MAX_ROWS))()
+        pos = (_u32 * MAX_ROWS)()
+        n = _u32()
+        _check(lib.twd_verify_draft_sums(self.handle, sums, pos, MAX_ROWS, C.byref(n)))
+        return {int(pos[i]): (float(sums[2 * i]), float(sums[2 * i + 1])) for i in range(n.value)}
+
     def verify_draft(self, logits, draft_rows, params: RowParams, base_seed: int, drafts,
                      result=None, stream=None):
         """evaluate_verification with draft logits (speculator.cpp:34-153): draft_rows[i] is a
@@ -310,6 +320,15 @@ class Selector:
                                     0 if drafts is None else drafts.numel(), _ptr(result),
                                     _stream(stream)))
         return result
+
+
+def probe_expf(x, out=None, stream=None):
+    """The draft verify's device expf over a float32 device tensor (twd_probe_expf)."""
+    import torch
+    if out is None:
+        out = torch.empty_like(x)
+    _check(lib.twd_probe_expf(_ptr(x), _ptr(out), x.numel(), _stream(stream)))
+    return out
 
 
 def rejection_uniforms(step_seed: int):
