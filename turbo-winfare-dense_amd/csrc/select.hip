@@ -765,7 +765,8 @@ constexpr uint32_t kSmCap = 2048;     // survivors kept in LDS
 constexpr uint32_t kSmMaxCand = 2048; // candidate waves listed in LDS
 
 struct SampleMergeBufs {
-    const float* logits;  // [rows][vocab], penalised
+    const float* logits;  // [rows][stride], penalised
+    uint64_t stride;
     uint32_t vocab;
     uint32_t waves;       // head waves (records per row)
     SampleStats st;
@@ -795,7 +796,7 @@ __global__ __launch_bounds__(kSmThreads) void select_sample_merge_kernel(SelectA
     const twd_row_params p = args.p[row];
     const uint32_t W = b.waves;
     const size_t o = static_cast<size_t>(row) * W;
-    const float* lg = b.logits + static_cast<size_t>(row) * b.vocab;
+    const float* lg = b.logits + static_cast<size_t>(row) * b.stride;
 
     // ---- the wave records, one round trip: thread tid holds waves tid + NT * q
     uint64_t key[kSmPer];
@@ -998,6 +999,221 @@ __global__ __launch_bounds__(kSmThreads) void select_sample_merge_kernel(SelectA
     if (tid == 0) b.tokens[row] = tok;
 }
 
+// ---- the wave-record path for logits that are already in memory ---------------------------------
+//
+// Rows whose logits the caller holds (twd_select, the head for rows > 4) reach
+// select_sample_merge_kernel through two short passes instead of the slice kernels:
+//   * penalty_hash_kernel, one block per row: the row's history ids into an LDS hash table of
+//     (id, occurrences), then each distinct id's logit gets the penalty once per occurrence, one
+//     after another as the reference loop applies them (sampling.cpp:74-90); only those entries
+//     are read and written;
+//   * wave_stats_kernel: per 64 entries of a row, the record the head's sample mode publishes
+//     -- the best rank (value desc, index asc) and the sum of exp(v - that value) in double,
+//     NaN when a NaN was seen. Eight lanes hold one record's 64 entries, eight each.
+constexpr int kPhThreads = 1024;
+constexpr uint32_t kHashSlots = 8192;    // LDS hash table of one row's history
+constexpr uint32_t kHashMaxIds = 4096;   // history ids per row the table takes (load <= 1/2)
+constexpr uint32_t kHashEmpty = 0xFFFFFFFFu;  // never an id below vocab <= 2^30
+
+struct PenaltyBufs {
+    float* logits;
+    uint64_t stride;
+    uint32_t vocab;
+    const uint32_t* history;
+};
+
+__global__ __launch_bounds__(kPhThreads) void penalty_hash_kernel(SelectArgs args_by_value, PenaltyBufs b) {
+    constexpr int NT = kPhThreads;
+    constexpr uint32_t kIdsPer = kHashMaxIds / NT;     // history ids per thread
+    constexpr uint32_t kSlotsPer = kHashSlots / NT;    // table slots per thread
+    __shared__ uint32_t keys[kHashSlots];
+    __shared__ uint32_t cnt[kHashSlots];
+#if __HIP_DEVICE_COMPILE__
+    const SelectArgs& args =
+        *reinterpret_cast<const SelectArgs*>(__builtin_amdgcn_kernarg_segment_ptr());
+#else
+    const SelectArgs& args = args_by_value;
+#endif
+    const int tid = threadIdx.x;
+    const uint32_t row = blockIdx.x;
+    const twd_row_params p = args.p[row];
+    if (p.repetition_penalty == 1.0f || p.history_len == 0) return;  // the whole block
+    // every id requested at once (history_len <= kHashMaxIds, checked by the launch)
+    const uint32_t* hist = b.history + p.history_offset;
+    uint32_t ids[kIdsPer];
+#pragma unroll
+    for (uint32_t q = 0; q < kIdsPer; ++q) {
+        const uint32_t j = tid + NT * q;
+        const uint32_t id = hist[min(j, p.history_len - 1)];  // unconditional: no branch per load
+        ids[q] = j < p.history_len ? id : kHashEmpty;
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < kSlotsPer; ++q) {
+        keys[tid + NT * q] = kHashEmpty;
+        cnt[tid + NT * q] = 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t q = 0; q < kIdsPer; ++q) {
+        const uint32_t id = ids[q];
+        if (id >= b.vocab) continue;  // out-of-range ids are ignored (sampling.cpp:82)
+        // linear probing from a multiplicative hash; the table is at most half full, so a free
+        // or matching slot is always found
+        uint32_t h = (id * 0x9E3779B1u) >> (32 - 13);
+        for (;;) {
+            const uint32_t prev = atomicCAS(&keys[h], kHashEmpty, id);
+            if (prev == kHashEmpty || prev == id) {
+                atomicAdd(&cnt[h], 1u);
+                break;
+            }
+            h = (h + 1) & (kHashSlots - 1);
+        }
+    }
+    __syncthreads();
+    float* lg = b.logits + static_cast<size_t>(row) * b.stride;
+    const float rp = p.repetition_penalty;
+    const float limit = (p.softcap > 0.0f) ? p.softcap * 0.9999f : 0.0f;
+    // each distinct id: its logit (all of this thread's requested at once), the penalty once
+    // per occurrence, the store
+    uint32_t id[kSlotsPer], n[kSlotsPer];
+    float x[kSlotsPer];
+#pragma unroll
+    for (uint32_t q = 0; q < kSlotsPer; ++q) {
+        id[q] = keys[tid + NT * q];
+        n[q] = cnt[tid + NT * q];
+        x[q] = lg[id[q] != kHashEmpty ? id[q] : 0u];  // unconditional: no branch per load
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < kSlotsPer; ++q) {
+        if (id[q] == kHashEmpty) continue;
+        float v = x[q];
+        for (uint32_t t = 0; t < n[q]; ++t) {
+            v = (v > 0.0f) ? (v / rp) : (v * rp);
+            if (limit > 0.0f) v = (v < -limit) ? -limit : ((limit < v) ? limit : v);
+        }
+        lg[id[q]] = v;
+    }
+}
+
+constexpr int kWsThreads = 256;
+constexpr uint32_t kWsEntries = kWsThreads * 8;         // entries of one batch of a block
+
+struct WaveStatsBufs {
+    const float* logits;
+    uint64_t stride;
+    uint32_t vocab;
+    uint32_t waves;  // records per row, ceil(vocab / 64)
+    uint32_t vec;    // rows 16-byte aligned: 16 B loads
+    SampleStats st;
+};
+
+// NB 8-entry batches per lane. One: many short blocks, so that later blocks' loads overlap
+// earlier blocks' arithmetic (with four, every wave requested all its loads first, and the pass
+// ran as a load phase, then an arithmetic phase).
+template <uint32_t NB>
+__global__ __launch_bounds__(kWsThreads) __attribute__((amdgpu_waves_per_eu(8)))
+void wave_stats_kernel(WaveStatsBufs b) {
+    constexpr uint32_t kWsBatches = NB;
+    constexpr uint32_t kWsBlockEntries = kWsEntries * NB;
+    __shared__ double tbl[64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    if (tid < 64) tbl[tid] = kExp2Table[tid];
+    const uint32_t row = blockIdx.y;
+    const float* lg = b.logits + static_cast<size_t>(row) * b.stride;
+    // batch k of this lane: entries e0 + 8 * 256 * k .. + 7; all loads requested at once
+    const uint32_t e0 = blockIdx.x * kWsBlockEntries + static_cast<uint32_t>(tid) * 8;
+    float v[kWsBatches][8];
+#pragma unroll
+    for (uint32_t k = 0; k < kWsBatches; ++k) {
+        const uint32_t e = e0 + kWsEntries * k;
+        if (b.vec && e + 8 <= b.vocab) {
+            const float4 x0 = *reinterpret_cast<const float4*>(lg + e);
+            const float4 x1 = *reinterpret_cast<const float4*>(lg + e + 4);
+            v[k][0] = x0.x; v[k][1] = x0.y; v[k][2] = x0.z; v[k][3] = x0.w;
+            v[k][4] = x1.x; v[k][5] = x1.y; v[k][6] = x1.z; v[k][7] = x1.w;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) v[k][q] = e + q < b.vocab ? lg[e + q] : -INFINITY;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t k = 0; k < kWsBatches; ++k) {
+        const uint32_t e = e0 + kWsEntries * k;
+        // common case, decided per wave: every entry of the wave finite and live, and every
+        // exp argument v - (record best) in [-700, 0]. The lane's best rank is its largest value
+        // at its lowest index (equal values, -0 and +0 included, rank by index), and exp_core
+        // needs no special cases.
+        float hi = v[k][0], lo = v[k][0];
+        bool ok = e + 8 <= b.vocab;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            ok &= __builtin_isfinite(v[k][q]);
+            hi = fmaxf(hi, v[k][q]);
+            lo = fminf(lo, v[k][q]);
+        }
+        if (__ballot(!ok) == 0) {
+            uint32_t qi = 7;
+#pragma unroll
+            for (int q = 6; q >= 0; --q) qi = v[k][q] == hi ? static_cast<uint32_t>(q) : qi;
+            uint64_t best = rank_key(hi, e + qi);
+#pragma unroll
+            for (int m = 1; m < 8; m <<= 1) {
+                const uint64_t o = shfl_xor_u64(best, m);
+                best = o > best ? o : best;
+            }
+            const float wm = rank_value(best);
+            if (__ballot(lo < wm - 700.0f) == 0) {
+                const double dwm = static_cast<double>(wm);
+                double sum = 0.0;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) sum += exp_core(static_cast<double>(v[k][q]) - dwm, tbl);
+#pragma unroll
+                for (int m = 1; m < 8; m <<= 1) sum += __shfl_xor(sum, m);
+                const uint32_t w = e / kSampleWaveRows;
+                if ((lane & 7) == 0) {
+                    const size_t o = static_cast<size_t>(row) * b.waves + w;
+                    b.st.key[o] = best;
+                    b.st.sum[o] = sum;
+                }
+                continue;
+            }
+        }
+        // entries past the vocabulary hold -inf and no rank: they add nothing
+        uint64_t best = 0;
+        uint32_t nan = 0;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const uint64_t key = e + q < b.vocab ? rank_key(v[k][q], e + q) : 0ull;
+            best = key > best ? key : best;
+            nan |= v[k][q] != v[k][q] ? 1u : 0u;
+        }
+        // the record's 64 entries are the 8 lanes with the same lane >> 3
+#pragma unroll
+        for (int m = 1; m < 8; m <<= 1) {
+            const uint64_t o = shfl_xor_u64(best, m);
+            best = o > best ? o : best;
+            nan |= __shfl_xor(nan, m);
+        }
+        // a record of -inf entries only (best value -inf, or no entry) adds nothing
+        const float wm = best != 0 ? rank_value(best) : -INFINITY;
+        const double dwm = wm != -INFINITY ? static_cast<double>(wm) : 0.0;
+        double sum = 0.0;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) sum += exp_for_sum(static_cast<double>(v[k][q]) - dwm, tbl);
+        if (wm == -INFINITY) sum = 0.0;
+#pragma unroll
+        for (int m = 1; m < 8; m <<= 1) sum += __shfl_xor(sum, m);
+        if (nan) sum = __builtin_nan("");
+        const uint32_t w = e / kSampleWaveRows;
+        if ((lane & 7) == 0 && w < b.waves) {
+            const size_t o = static_cast<size_t>(row) * b.waves + w;
+            b.st.key[o] = best;
+            b.st.sum[o] = sum;
+        }
+    }
+}
+
 __global__ void verify_compare_kernel(const uint32_t* row_tokens, uint32_t rows,
                                       const uint32_t* drafts, uint32_t nd,
                                       twd_verify_result* v) {
@@ -1114,6 +1330,11 @@ int scratch_alloc(SelectScratch* s, uint32_t max_vocab, uint32_t max_rows) {
     if (e == hipSuccess) e = hipMalloc(&s->part_key, n * sizeof(uint64_t));
     if (e == hipSuccess) e = hipMalloc(&s->cand, n * kMaxWant * sizeof(uint64_t));
     if (e == hipSuccess) e = hipMalloc(&s->verify_tokens, (max_rows + 1) * sizeof(uint32_t));
+    // the wave records of the wave-record path, ceil(max_vocab / 64) per row
+    s->wave_cap = (max_vocab + kSampleWaveRows - 1) / kSampleWaveRows;
+    const size_t nw = static_cast<size_t>(max_rows) * s->wave_cap;
+    if (e == hipSuccess) e = hipMalloc(&s->wkey, nw * sizeof(uint64_t));
+    if (e == hipSuccess) e = hipMalloc(&s->wsum, nw * sizeof(double));
     if (e != hipSuccess) {
         scratch_free(s);
         return hip_fail(e, "allocating selection scratch");
@@ -1129,6 +1350,8 @@ void scratch_free(SelectScratch* s) {
     (void)hipFree(s->part_key);
     (void)hipFree(s->cand);
     (void)hipFree(s->verify_tokens);
+    (void)hipFree(s->wkey);
+    (void)hipFree(s->wsum);
     *s = SelectScratch{};
 }
 
@@ -1175,6 +1398,43 @@ int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_
             return fail(TWD_E_INVALID, "null history with a non-empty history_len");
         a.p[r] = p;
     }
+    // sampled rows with short histories: the wave-record path (penalty pass, per-64-entry
+    // statistics, then the one-block-per-row merge that reads only the candidate waves)
+    const uint32_t waves = (vocab + kSampleWaveRows - 1) / kSampleWaveRows;
+    bool records = !penalty_only && s.wkey != nullptr && waves <= s.wave_cap && waves <= kSampleMaxWaves;
+    bool any_sampled = false, any_penalty = false;
+    for (uint32_t r = 0; r < rows; ++r) {
+        const twd_row_params& p = params[r];
+        any_sampled |= p.temperature > 0.0f;
+        if (p.repetition_penalty != 1.0f && p.history_len > 0) {
+            any_penalty = true;
+            records &= p.history_len <= kHashMaxIds;
+        }
+    }
+    if (records && any_sampled) {
+        int rc = enable_select_kernels();
+        if (rc) return rc;
+        if (any_penalty) {
+            PenaltyBufs pb{logits, stride, vocab, history};
+            penalty_hash_kernel<<<rows, kPhThreads, 0, stream>>>(a, pb);
+            TWD_HIP(hipGetLastError());
+        }
+        const SampleStats st{s.wkey, s.wsum};
+        WaveStatsBufs wb{logits, stride, vocab, waves,
+                         (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && (stride & 3) == 0 ? 1u : 0u, st};
+        wave_stats_kernel<1><<<dim3((vocab + kWsEntries - 1) / kWsEntries, rows), kWsThreads, 0, stream>>>(wb);
+        TWD_HIP(hipGetLastError());
+        SampleMergeBufs mb{};
+        mb.logits = logits;
+        mb.stride = stride;
+        mb.vocab = vocab;
+        mb.waves = waves;
+        mb.st = st;
+        mb.tokens = tokens;
+        select_sample_merge_kernel<<<rows, kSmThreads, sizeof(SampleMergeShared), stream>>>(a, mb);
+        TWD_HIP(hipGetLastError());
+        return TWD_OK;
+    }
     SelectBufs b{};
     b.logits = logits;
     b.vocab = vocab;
@@ -1209,6 +1469,7 @@ int launch_sample_merge(const SampleStats& st, uint32_t waves, const float* logi
     for (uint32_t r = 0; r < rows; ++r) a.p[r] = params[r];
     SampleMergeBufs b{};
     b.logits = logits;
+    b.stride = vocab;
     b.vocab = vocab;
     b.waves = waves;
     b.st = st;

@@ -128,6 +128,32 @@ __device__ __forceinline__ double exp_for_sum(double x, const double* tbl) {
     return nan ? x : (tiny ? 0.0 : v);
 }
 
+// exp_for_sum without its special cases, for finite x in [-700, 0]: the same reduction,
+// polynomial and table, so the same value there. k is read from the bits of fl(x * 64/ln2) +
+// 1.5 * 2^52 (that addition rounds to the nearest integer, ties to even, as rint does) and
+// 2^(k >> 6) is added to the table entry's exponent, which is exact because the result stays
+// normal: no rint, conversion or ldexp instruction.
+__device__ __forceinline__ double exp_core(double x, const double* tbl) {
+#pragma clang fp contract(off)
+    const double kInvL = 92.332482616893656;             // 64 / ln2
+    const double kLHi = 6.93147180369123816490e-01 / 64;  // ln2 / 64, high part
+    const double kLLo = 1.90821492927058770002e-10 / 64;  // ln2 / 64, low part
+    const double kShift = 0x1.8p52;
+    const double t = x * kInvL + kShift;  // two roundings, as rint(x * kInvL)
+    const int k = static_cast<int>(static_cast<uint32_t>(__builtin_bit_cast(uint64_t, t)));
+    const double kd = t - kShift;
+    double r = fma(-kd, kLHi, x);
+    r = fma(-kd, kLLo, r);
+    double p = fma(r, 1.0 / 120.0, 1.0 / 24.0);
+    p = fma(r, p, 1.0 / 6.0);
+    p = fma(r, p, 0.5);
+    p = fma(r, p, 1.0);
+    p = fma(r, p, 1.0);
+    const uint64_t tb = __builtin_bit_cast(uint64_t, tbl[k & 63]) +
+                        (static_cast<uint64_t>(static_cast<int64_t>(k >> 6)) << 52);
+    return __builtin_bit_cast(double, tb) * p;
+}
+
 // bf16 bit patterns <-> float
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
@@ -187,6 +213,9 @@ struct SelectScratch {
     uint64_t* part_key = nullptr;   // [rows][parts] greedy best rank
     uint64_t* cand = nullptr;       // [rows][parts][kMaxWant]
     uint32_t* verify_tokens = nullptr;  // [max_rows] scratch for twd_verify
+    uint32_t wave_cap = 0;              // wave records per row (0: no wave-record path)
+    uint64_t* wkey = nullptr;           // [rows][wave_cap] best rank per 64 entries
+    double* wsum = nullptr;             // [rows][wave_cap] sum of exp(v - best value)
 };
 
 int scratch_alloc(SelectScratch* s, uint32_t max_vocab, uint32_t max_rows);
