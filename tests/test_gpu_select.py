@@ -121,6 +121,40 @@ def test_penalty_bit_exact_random(env, oracle):
         assert int(tok[0]) == oracle.argmax(want)
 
 
+def test_penalty_sampled_rows(env, oracle):
+    # sampled rows take the penalty pass over a per-row hash of the history (<= 4096 ids) and
+    # fall back to the slice kernels past that: duplicates (one id 4096 times), ids past the
+    # vocabulary, lengths at and past the limit, penalties below and above 1, with and without
+    # the softcap clamp; penalised rows bit-exact, tokens against the oracle
+    torch, dev, t, sel = env
+    rng = np.random.default_rng(77)
+    hashed = [(1, 1.1, 30.0), (4096, 1.3, 30.0), (3000, 0.7, 0.0), (4096, 2.0, 30.0),
+              (2048, 1.1, 30.0), (0, 1.5, 30.0), (4096, 1.05, 0.0)]
+    fallback = [(10, 1.1, 30.0), (4096, 1.3, 30.0), (4097, 1.3, 30.0)]  # one row past the limit
+    for n, cases in ((1000, hashed), (40000, hashed), (V, hashed), (V, fallback)):
+        rows, params, hists, off = [], [], [], 0
+        for c, (hlen, rep, cap) in enumerate(cases):
+            row = (rng.standard_normal(n) * 4.0).astype(np.float32)
+            row = oracle.softcap(row, 30.0) if c % 2 else row
+            h = rng.integers(0, n + 5, size=hlen, dtype=np.uint32)  # out-of-range ids included
+            if c == 1:
+                h[:] = h[0] % n  # one id, 4096 occurrences
+            elif hlen and c % 3 == 0:
+                h[: hlen // 2] = h[0]
+            rows.append(row)
+            params.append(rp(t, 0.8, 0.95, 50, float(rng.uniform()), rep, cap, off, hlen))
+            hists.append(h)
+            off += hlen
+        hist = np.concatenate([h for h in hists if len(h)])
+        tok, pen = select_rows(env, np.stack(rows), params, hist)
+        for m, (row, h, p) in enumerate(zip(rows, hists, params)):
+            want_pen = oracle.apply_repetition_penalty(row, h, p.repetition_penalty, p.softcap)
+            assert np.array_equal(pen[m].view(np.uint32), want_pen.view(np.uint32)), (n, m)
+            want, dg = oracle.sample_token(want_pen, p.temperature, p.top_p, p.top_k, u=p.uniform,
+                                           diag=True)
+            assert int(tok[m]) == want, (n, m, dg["cut_margin"], dg["draw_margin"])
+
+
 @pytest.mark.parametrize("n", [1, 5, 100, 16384, 16385, 50000, V])
 def test_select_random_vs_oracle(env, oracle, n):
     torch, dev, t, sel = env
