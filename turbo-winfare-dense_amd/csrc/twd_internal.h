@@ -228,6 +228,9 @@ struct DraftScratch {
     uint32_t* flags = nullptr; // [2 * TWD_MAX_ROWS] NaN flags
     uint32_t* rej = nullptr;   // [TWD_MAX_ROWS][4] per-position outcome
     float* sums = nullptr;     // [2 * TWD_MAX_ROWS] softmax sums
+    double* seg_d = nullptr;   // [2 * TWD_MAX_ROWS][513] segment double sums of the exact-sum pipeline
+    void* seg_rec = nullptr;   // [2 * TWD_MAX_ROWS][512] segment records
+    uint32_t* live = nullptr;  // [TWD_MAX_ROWS] 1: the position's draft was rejected
     size_t e_capacity = 0;
     size_t part_capacity = 0;
     uint32_t last_npos = 0;               // positions of the last call with draft rows

@@ -6,13 +6,15 @@
 // run sequentially in index order, a ratio test p/q against a uniform, and on rejection a draw
 // from (p - q)+ by a sequential fp32 prefix sum. Token ids only match the reference if those
 // sequential float sums are reproduced bit for bit, so the device recomputes them exactly
-// (block_seq_sum below) instead of summing in a tree.
+// (block_seq_sum and the segmented form below) instead of summing in a tree.
 //
 // Kernels, all on the caller's stream:
 //   draft_max_kernel     grid (parts, 2P): per row, partial maxima of l / T (T = 1 when <= 0)
 //   draft_exp_kernel     grid (parts, 2P): e = expf(l / T - max) to scratch, NaN flags
-//   draft_sum_kernel     grid 2P, 1024 threads: each softmax's sequential sum
-//   draft_reject_kernel  grid P, 1024 threads: the ratio test, the residual sum and draw
+//   seg_dsum_kernel, seg_xfer_kernel, seg_sum_kernel: each softmax's sequential sum
+//   draft_ratio_kernel   the ratio tests
+//   seg_dsum_kernel, seg_xfer_kernel, seg_residual_kernel: each rejected position's residual
+//                        sum and draw
 //   draft_finish_kernel  one thread: the accept chain over all positions, bonus, result
 // where P is the number of positions with a draft row; the target tokens of the other
 // positions, of the fallback and of the bonus row come from the selector (launch_select).
@@ -21,6 +23,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 
 #include "expf_libm.h"
 #include "twd_internal.h"
@@ -394,12 +397,25 @@ __device__ float block_seq_sum(Load load, Term term, uint32_t n, float S, uint32
         if (threadIdx.x < 64) {
             float s = S;
             uint32_t hit = n;
-            for (uint32_t j = k0; j < end; ++j) {
-                s += sh.head[j];
-                if (want_stop && s >= thr) {
-                    hit = j;
-                    break;
+            if (want_stop) {
+                for (uint32_t j = k0; j < end; ++j) {
+                    s += sh.head[j];
+                    if (s >= thr) {
+                        hit = j;
+                        break;
+                    }
                 }
+            } else {
+                // no exit: sixteen terms read at a time, then added in order
+                uint32_t j = k0;
+                for (; j + 16 <= end; j += 16) {
+                    float t[16];
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) t[q] = sh.head[j + q];
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) s += t[q];
+                }
+                for (; j < end; ++j) s += sh.head[j];
             }
             if (threadIdx.x == 0) {
                 sh.S = s;
@@ -443,40 +459,357 @@ __device__ __forceinline__ void load_row(const float* row, uint32_t j0, float (&
     }
 }
 
-// One block per softmax row (2 per position with draft probabilities): the sum of
-// compute_softmax (speculator.cpp:22-26), NaN as soon as one term is NaN.
-__global__ __launch_bounds__(kRejThreads) void draft_sum_kernel(DraftArgs a) {
+// ---- the segmented form: the same exact sums, spread over the GPU ---------------------------------
+//
+// block_seq_sum runs one row on one CU. Here a row's terms after the serial head are cut into
+// segments of kSegLen, and three launches sum them exactly:
+//   seg_dsum_kernel  (segment x row blocks): each segment's sum in double, and the head's;
+//   seg_xfer_kernel  (segment x row blocks): the double prefix D before the segment predicts the
+//                    binade of the fp32 running sum there. For that binade and its nearer
+//                    neighbour the segment's terms become transfer functions (as in a window of
+//                    block_seq_sum) and their ordered composition is the segment's record;
+//   a chain kernel   (one block per row): the serial head with block_seq_sum, then a walk by one
+//                    thread over the records: when the exact sum S at a segment start lies in one
+//                    of the record's two binades, and the composed increment keeps it there (and
+//                    below a stop threshold), S jumps to the segment's end in a few instructions;
+//                    otherwise (a binade change, a wrong prediction, the stop) the whole block
+//                    sums that one segment exactly with block_seq_sum, and the walk resumes.
+// A prediction only decides which transfer functions are ready; the walk checks every record
+// against the exact S, so a wrong prediction costs one exact segment, never a wrong sum. No
+// block waits on another: the launches are ordered on the stream.
+constexpr uint32_t kSegHead = kSerialUntil;  // terms summed serially at the start
+constexpr uint32_t kSegLen = 1024;           // terms per segment after the head
+constexpr int kSegThreads = 256;             // 4 terms per thread
+constexpr uint32_t kSegMax = 512;            // segments per row (vocab <= 2048 + 512 * 1024)
+
+__host__ __device__ inline uint32_t seg_count(uint32_t n) {
+    return n > kSegHead ? (n - kSegHead + kSegLen - 1) / kSegLen : 0u;
+}
+
+struct SegRec {
+    int E[2];   // the two candidate binades (exponents of S's leading bit; -126: below 2^-125)
+    Xfer f[2];  // the segment's composed transfer functions in units of 2^(E - 23)
+};
+
+// Term sources: active(row) and term(row, j) for j < n (the kernels give zero past n).
+struct SegSrcArray {  // one plain array (twd_sequential_sum)
+    const float* x;
+    __device__ bool active(uint32_t) const { return true; }
+    __device__ float term(uint32_t, uint32_t j) const { return x[j]; }
+};
+struct SegSrcSoftmax {  // the e rows of compute_softmax, NaN rows skipped
+    const float* e;
+    uint32_t estride;
+    const uint32_t* flags;
+    __device__ bool active(uint32_t r) const { return !(flags[r] & 1u); }
+    __device__ float term(uint32_t r, uint32_t j) const { return e[static_cast<size_t>(r) * estride + j]; }
+};
+struct SegSrcResidual {  // (p - q)+ of a rejected position (draft_reject_kernel's diff)
+    const float* e;
+    uint32_t estride;
+    const float* sums;
+    const uint32_t* live;  // [P] 1: the position was rejected
+    __device__ bool active(uint32_t pi) const { return live[pi] != 0u; }
+    __device__ float term(uint32_t pi, uint32_t j) const {
+        const float sp = sums[2 * pi], sq = sums[2 * pi + 1];
+        const float inv_p = 1.0f / (sp > 1e-12f ? sp : 1.0f);
+        const float inv_q = 1.0f / (sq > 1e-12f ? sq : 1.0f);
+        const float pt = e[static_cast<size_t>(2 * pi) * estride + j];
+        const float qd = e[static_cast<size_t>(2 * pi + 1) * estride + j];
+        const float x = pt * inv_p - qd * inv_q;
+        return (0.0f < x) ? x : 0.0f;
+    }
+};
+
+// sum of one double per thread over a 256-thread block (any order: the value only predicts)
+__device__ __forceinline__ double seg_block_sum(double v, double* red) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const double t = red[0] + red[1] + red[2] + red[3];
+    __syncthreads();
+    return t;
+}
+
+// grid (1 + segments, rows): block 0 the head [0, kSegHead), block s the segment s - 1
+template <class Src>
+__global__ __launch_bounds__(kSegThreads) void seg_dsum_kernel(Src src, uint32_t n, double* d) {
+    __shared__ double red[kSegThreads / 64];
+    const uint32_t row = blockIdx.y, b = blockIdx.x;
+    if (!src.active(row)) return;  // the whole block
+    const uint32_t nseg = seg_count(n);
+    const uint32_t lo = b == 0 ? 0u : kSegHead + (b - 1) * kSegLen;
+    const uint32_t hi = b == 0 ? min(n, kSegHead) : min(n, lo + kSegLen);
+    double t = 0.0;
+    for (uint32_t j = lo + threadIdx.x; j < hi; j += kSegThreads) t += static_cast<double>(src.term(row, j));
+    t = seg_block_sum(t, red);
+    if (threadIdx.x == 0) d[static_cast<size_t>(row) * (nseg + 1) + b] = t;
+}
+
+// grid (segments, rows): the record of segment blockIdx.x
+template <class Src>
+__global__ __launch_bounds__(kSegThreads) void seg_xfer_kernel(Src src, uint32_t n, const double* d, SegRec* rec) {
+    __shared__ double red[kSegThreads / 64];
+    __shared__ Xfer wt[2][kSegThreads / 64];
+    const uint32_t row = blockIdx.y, s = blockIdx.x;
+    if (!src.active(row)) return;  // the whole block
+    const uint32_t nseg = seg_count(n);
+    const double* dr = d + static_cast<size_t>(row) * (nseg + 1);
+    // D: the head's and the earlier segments' double sums
+    double t = 0.0;
+    for (uint32_t i = threadIdx.x; i <= s; i += kSegThreads) t += dr[i];
+    const double D = seg_block_sum(t, red);
+    int ex = 0;
+    const double m = frexp(D, &ex);  // D = m * 2^ex, m in [0.5, 1)
+    const bool low = D < 0x1p-125;
+    const int E0 = low ? -126 : ex - 1;
+    const int E1 = low ? -125 : max(-126, m < 0.75 ? ex - 2 : ex);
+    // this thread's four terms, in order, for both candidates
+    const uint32_t k0 = kSegHead + s * kSegLen;
+    Xfer f0 = xfer_id(), f1 = xfer_id();
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t j = k0 + threadIdx.x * 4 + q;
+        const float a = (j < n && j < k0 + kSegLen) ? src.term(row, j) : 0.0f;
+        uint32_t kk, kd;
+        split_term(a, E0, kk, kd);
+        f0 = xfer_then(f0, term_xfer(kk, kd));
+        split_term(a, E1, kk, kd);
+        f1 = xfer_then(f1, term_xfer(kk, kd));
+    }
+    // ordered composition: wave scans, then the four wave totals in order
+    f0 = xfer_wave_scan(f0);
+    f1 = xfer_wave_scan(f1);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 63) {
+        wt[0][wave] = f0;
+        wt[1][wave] = f1;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        SegRec r;
+        r.E[0] = E0;
+        r.E[1] = E1;
+        r.f[0] = xfer_then(xfer_then(wt[0][0], wt[0][1]), xfer_then(wt[0][2], wt[0][3]));
+        r.f[1] = xfer_then(xfer_then(wt[1][0], wt[1][1]), xfer_then(wt[1][2], wt[1][3]));
+        rec[static_cast<size_t>(row) * kSegMax + s] = r;
+    }
+}
+
+// One segment summed exactly by one wave, with no block barrier and one load per term: terms
+// [k0, k1) of a row of n (k1 - k0 <= kSegLen, k0 a multiple of 16) from prefix S; lane l holds
+// terms k0 + 16 l .. + 15 in registers. Each pass does what a window of block_seq_sum does --
+// the terms in units of the binade of S, their transfer functions scanned across the wave, a
+// replay to the first term that leaves the binade or reaches thr -- and an exact add of that
+// term; the next pass continues after it from the same registers. Returns the sum; *stop_at
+// receives the first index whose prefix reaches thr (want_stop), else k1. Every lane returns
+// the same values.
+template <typename Load>
+__device__ float wave_seg_sum(Load load, uint32_t n, uint32_t k0, uint32_t k1, float S, float thr,
+                              bool want_stop, uint32_t* stop_at) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t j0 = k0 + static_cast<uint32_t>(lane) * 16u;
+    float a[16];
+    if (j0 < ((n + 15u) & ~15u)) {
+        load(j0, a);
+    } else {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) a[q] = 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q)
+        if (j0 + q >= k1) a[q] = 0.0f;
+    uint32_t kc = k0;  // the first term not yet added
+    uint32_t stop = k1;
+    for (uint32_t pass = 0; pass <= kSegLen; ++pass) {  // each pass adds at least one term
+        const uint32_t sb = __float_as_uint(S), sf = sb >> 23;
+        const int E = sf ? static_cast<int>(sf) - 127 : -126;
+        const uint32_t B = sf ? ((sb & 0x7FFFFFu) | 0x800000u) : sb;
+        const uint32_t p0 = B & 1u;
+        uint32_t Tu = 0xFFFFFFFFu;
+        if (want_stop) {
+            const double t = ceil(ldexp(static_cast<double>(thr), 23 - E));
+            Tu = t <= 0.0 ? 0u : (t >= 4294967295.0 ? 0xFFFFFFFFu : static_cast<uint32_t>(t));
+        }
+        uint32_t kk[16], kd[16];
+        Xfer t = xfer_id();
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            split_term(j0 + q >= kc ? a[q] : 0.0f, E, kk[q], kd[q]);
+            t = xfer_then(t, term_xfer(kk[q], kd[q]));
+        }
+        const Xfer incl = xfer_wave_scan(t);
+        Xfer ex = xfer_shfl_up(incl, 1);
+        if (lane == 0) ex = xfer_id();
+        uint32_t R = sat_add(B, p0 ? ex.inc1 : ex.inc0);
+        uint32_t par = (ex.out >> p0) & 1u;
+        uint32_t ev = kNoEvent, R_before = R;
+        bool live = R < kL;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const uint32_t j = j0 + q;
+            const uint32_t d = term_inc(kk[q], kd[q], par);
+            const bool go = live && j >= kc && j < k1;
+            const bool cross = go && (R + d >= kL);
+            const bool adv = go && !cross;
+            if (cross) {
+                ev = 2 * j;
+                R_before = R;
+            }
+            R = adv ? R + d : R;
+            par = adv ? ((par + d) & 1u) : par;
+            const bool hit = adv && R >= Tu;
+            if (hit) ev = 2 * j + 1;
+            live = live && !cross && !hit;
+        }
+        // the earliest event is the lowest lane's (lanes hold increasing indices)
+        const uint64_t m = __ballot(ev != kNoEvent);
+        if (m == 0) {  // no event: lane 63's inclusive transfer gives the segment's end
+            const uint32_t Rend = sat_add(B, p0 ? incl.inc1 : incl.inc0);
+            S = ldexpf(static_cast<float>(__shfl(Rend, 63)), E - 23);
+            break;
+        }
+        const int owner = __ffsll(static_cast<long long>(m)) - 1;
+        const uint32_t e = __shfl(ev, owner);
+        const uint32_t j = e >> 1;
+        if (e & 1u) {  // reaches thr, no binade change before it
+            S = ldexpf(static_cast<float>(__shfl(R, owner)), E - 23);
+            stop = j;
+            break;
+        }
+        // the term that leaves the binade, added exactly
+        float aj = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) aj = (j0 + q == j) ? a[q] : aj;
+        aj = __shfl(aj, owner);
+        const float s_new = ldexpf(static_cast<float>(__shfl(R_before, owner)), E - 23) + aj;
+        S = s_new;
+        if (want_stop && s_new >= thr) {
+            stop = j;
+            break;
+        }
+        kc = j + 1;
+        if (kc >= k1) break;
+    }
+    if (want_stop) *stop_at = stop;
+    return S;
+}
+
+struct ChainShared {
+    SegRec rec[kSegMax];
+    float start[kSegMax + 1];  // the exact sum at each segment start, then the row's sum
+    float S;
+    uint32_t s;
+};
+
+// The walk and the exact segments after the head: S is the sum of terms [0, kSegHead) on entry.
+// Returns the row's sum (or, with stop_at, the prefix at the first index reaching thr, whose
+// index goes to *stop_at; n when none does). ch.start[t] receives the sum before segment t for
+// every t the chain passes.
+template <typename Load, typename Term>
+__device__ float seg_chain(Load load, Term term, uint32_t n, float S, float thr, uint32_t* stop_at,
+                           SeqShared& sh, ChainShared& ch) {
+    (void)term;
+    (void)sh;
+    const uint32_t nseg = seg_count(n);
+    const bool want_stop = stop_at != nullptr;
+    if (threadIdx.x < 64) {
+        // wave 0: walks 64 records at a time (the composed increments of the lanes' records, an
+        // ordered scan of transfer functions, give every lane its segment's start and end at
+        // once), advancing to the first lane whose record does not apply; that segment it sums
+        // exactly with wave_seg_sum, then walks on
+        const int lane = threadIdx.x;
+        uint32_t stop = n;
+        uint32_t t = 0;
+        while (t < nseg) {
+            for (;;) {
+                const uint32_t sb = __float_as_uint(S), sf = sb >> 23;
+                const int E = sf ? static_cast<int>(sf) - 127 : -126;
+                const uint32_t B = sf ? ((sb & 0x7FFFFFu) | 0x800000u) : sb;
+                const uint32_t p0 = B & 1u;
+                const uint32_t idx = t + static_cast<uint32_t>(lane);
+                int c = -1;
+                Xfer f = xfer_id();
+                if (idx < nseg) {
+                    const SegRec& R = ch.rec[idx];
+                    c = R.E[0] == E ? 0 : (R.E[1] == E ? 1 : -1);
+                    if (c >= 0) f = R.f[c];
+                }
+                const Xfer incl = xfer_wave_scan(f);
+                Xfer excl = xfer_shfl_up(incl, 1);
+                if (lane == 0) excl = xfer_id();
+                const uint32_t b0 = B + (p0 ? excl.inc1 : excl.inc0);  // < 2^24 up to the first bad lane
+                const uint32_t b1 = B + (p0 ? incl.inc1 : incl.inc0);
+                const float Se = ldexpf(static_cast<float>(b1), E - 23);
+                const bool good = c >= 0 && b1 < kL && !(want_stop && Se >= thr);
+                const uint64_t bad = __ballot(!good);
+                const uint32_t first = bad ? static_cast<uint32_t>(__ffsll(static_cast<long long>(bad)) - 1) : 64u;
+                // every lane up to the first bad one starts where the records before it end
+                if (static_cast<uint32_t>(lane) <= first && idx < nseg) ch.start[idx] = ldexpf(static_cast<float>(b0), E - 23);
+                if (first > 0) S = __shfl(Se, static_cast<int>(first) - 1);
+                t += first;
+                if (first < 64 || t >= nseg) break;
+            }
+            if (t >= nseg) break;
+            // segment t exactly, from S
+            const uint32_t k0 = kSegHead + t * kSegLen, k1 = min(n, k0 + kSegLen);
+            uint32_t at = k1;
+            S = wave_seg_sum(load, n, k0, k1, S, thr, want_stop, &at);
+            if (want_stop && at < k1) {
+                stop = at;
+                break;
+            }
+            ++t;
+        }
+        if (lane == 0) {
+            ch.S = S;
+            ch.s = stop;
+            ch.start[nseg] = S;
+        }
+    }
+    __syncthreads();
+    S = ch.S;
+    if (want_stop) *stop_at = ch.s;
+    __syncthreads();  // ch is read before any later write
+    return S;
+}
+
+// The chain of one row: its records into LDS, the serial head, the walk.
+template <typename Load, typename Term>
+__device__ float seg_row_sum(Load load, Term term, uint32_t n, const SegRec* rec, float thr, uint32_t* stop_at,
+                             SeqShared& sh, ChainShared& ch) {
+    const uint32_t nseg = seg_count(n);
+    for (uint32_t i = threadIdx.x; i < nseg; i += blockDim.x) ch.rec[i] = rec[i];
+    __syncthreads();
+    uint32_t at = n;
+    const uint32_t nh = min(n, kSegHead);
+    float S = block_seq_sum(load, term, nh, 0.0f, 0u, thr, stop_at ? &at : nullptr, false, sh);
+    if (stop_at && at < nh) {
+        *stop_at = at;
+        return S;
+    }
+    return seg_chain(load, term, n, S, thr, stop_at, sh, ch);
+}
+
+// The softmax sums of the e rows: one block per row.
+__global__ __launch_bounds__(kRejThreads) void seg_sum_kernel(DraftArgs a, const SegRec* rec) {
     __shared__ SeqShared sh;
+    __shared__ ChainShared ch;
     const uint32_t r = blockIdx.x;
     const float* e = a.e + static_cast<size_t>(r) * a.estride;
     float s = __uint_as_float(0x7FC00000u);
     if (!(a.flags[r] & 1u))
-        s = block_seq_sum([&](uint32_t j0, auto& v) { load_row(e, j0, v); },
-                          [&](uint32_t j) { return e[j]; }, a.vocab, 0.0f, 0u, 0.0f, nullptr, false, sh);
+        s = seg_row_sum([&](uint32_t j0, auto& v) { load_row(e, j0, v); }, [&](uint32_t j) { return e[j]; },
+                        a.vocab, rec + static_cast<size_t>(r) * kSegMax, 0.0f, nullptr, sh, ch);
     if (threadIdx.x == 0) a.sums[r] = s;
 }
 
-// The sequential-sum engine alone, over one array: its sum, and the first index whose prefix
-// reaches thr when STOP. STOP is a template argument so that the sum-only form compiles the
-// serial start without the stop test (whose early exit keeps its loads from being batched).
-template <bool STOP>
-__global__ __launch_bounds__(kRejThreads) void seq_sum_kernel(const float* x, uint32_t n, float thr,
-                                                              float* sum_out, uint32_t* stop_out) {
-    __shared__ SeqShared sh;
-    uint32_t stop = n;
-    const float s = block_seq_sum([&](uint32_t j0, auto& v) { load_row(x, j0, v); },
-                                  [&](uint32_t j) { return x[j]; }, n, 0.0f, 0u, thr,
-                                  STOP ? &stop : nullptr, false, sh);
-    if (threadIdx.x == 0) {
-        *sum_out = s;
-        if (STOP) *stop_out = stop;
-    }
-}
-
-// One block per position with draft probabilities (speculator.cpp:74-121).
-__global__ __launch_bounds__(kRejThreads) void draft_reject_kernel(DraftArgs a) {
-    __shared__ SeqShared sh;
-    const uint32_t pi = blockIdx.x;
+// The ratio test of each position with draft probabilities (speculator.cpp:83-92): an accepted
+// draft is final; a rejected one is marked for the residual draw.
+__global__ void draft_ratio_kernel(DraftArgs a, uint32_t* live) {
+    const uint32_t pi = blockIdx.x * blockDim.x + threadIdx.x;
+    if (pi >= a.npos) return;
     const DraftPos& P = a.pos[pi];
     const uint32_t V = a.vocab;
     const float* et = a.e + static_cast<size_t>(2 * pi) * a.estride;
@@ -484,24 +817,39 @@ __global__ __launch_bounds__(kRejThreads) void draft_reject_kernel(DraftArgs a) 
     const float sp = a.sums[2 * pi], sq = a.sums[2 * pi + 1];
     const float inv_p = 1.0f / (sp > 1e-12f ? sp : 1.0f);
     const float inv_q = 1.0f / (sq > 1e-12f ? sq : 1.0f);
-
-    // ratio test (:83-92)
     const uint32_t dt = a.drafts[P.position];
     const float p_val = dt < V ? et[dt] * inv_p : 0.0f;
     const float q_val = dt < V ? ed[dt] * inv_q : 0.0f;
     const float r = (q_val > 1e-12f) ? (p_val / q_val) : 1.0f;
     uint32_t* out = a.rej + P.position * 4;
     if (P.u1 <= r) {
-        if (threadIdx.x == 0) {
-            out[0] = 1u;
-            out[1] = dt;
-            out[2] = 0u;
-            out[3] = 1u;
-        }
-        return;
+        out[0] = 1u;
+        out[1] = dt;
+        out[2] = 0u;
+        out[3] = 1u;
+        live[pi] = 0u;
+    } else {
+        live[pi] = 1u;
     }
-    // residual (p - q)+ (:94-112): std::max(0.0f, x) keeps 0 for x <= 0 and for NaN;
-    // p[v] - q[v] with each product rounded on its own, as in the reference's separate loops
+}
+
+// The residual (p - q)+ of a rejected position (speculator.cpp:94-116): its sum, then the first
+// index whose prefix reaches u2 * sum, found in the segment where the recorded starts straddle
+// it. One block per position; accepted positions return at once.
+__global__ __launch_bounds__(kRejThreads) void seg_residual_kernel(DraftArgs a, const uint32_t* live,
+                                                                   const SegRec* rec) {
+    __shared__ SeqShared sh;
+    __shared__ ChainShared ch;
+    const uint32_t pi = blockIdx.x;
+    if (!live[pi]) return;  // the whole block
+    const DraftPos& P = a.pos[pi];
+    const uint32_t V = a.vocab;
+    const float* et = a.e + static_cast<size_t>(2 * pi) * a.estride;
+    const float* ed = a.e + static_cast<size_t>(2 * pi + 1) * a.estride;
+    const float sp = a.sums[2 * pi], sq = a.sums[2 * pi + 1];
+    const float inv_p = 1.0f / (sp > 1e-12f ? sp : 1.0f);
+    const float inv_q = 1.0f / (sq > 1e-12f ? sq : 1.0f);
+    // std::max(0.0f, x) keeps 0 for x <= 0 and for NaN; each product rounded on its own
     auto diff1 = [&](float pt, float qd) {
         const float x = pt * inv_p - qd * inv_q;
         return (0.0f < x) ? x : 0.0f;
@@ -515,30 +863,59 @@ __global__ __launch_bounds__(kRejThreads) void draft_reject_kernel(DraftArgs a) 
 #pragma unroll
         for (int q = 0; q < PER; ++q) v[q] = diff1(v[q], w[q]);
     };
-    const float sum_diff = block_seq_sum(load_diff, diff, V, 0.0f, 0u, 0.0f, nullptr, true, sh);
-    uint32_t corr = 0;
-    uint32_t fallback = 0;
+    const SegRec* rr = rec + static_cast<size_t>(pi) * kSegMax;
+    const float sum_diff = seg_row_sum(load_diff, diff, V, rr, 0.0f, nullptr, sh, ch);
+    uint32_t corr = 0, fallback = 0;
     if (sum_diff > 1e-9f) {
         const float r_val = P.u2 * sum_diff;
-        // restart from the last recorded window start whose prefix is still below r_val: the
-        // prefixes never decrease, so the first index reaching r_val lies at or after it
-        uint32_t m = 0;
-        for (uint32_t i = 1; i < sh.n_marks; ++i)
-            if (sh.mark_S[i] < r_val) m = i;
-        const float S0 = sh.mark_S[m];
-        const uint32_t k0 = sh.mark_k0[m];
-        __syncthreads();  // every thread has read the marks
         uint32_t at = V;
-        block_seq_sum(load_diff, diff, V, S0, k0, r_val, &at, false, sh);
+        const uint32_t nh = min(V, kSegHead);
+        const uint32_t nseg = seg_count(V);
+        // the head holds the stop when its sum reaches r_val; otherwise the last segment whose
+        // recorded start lies below r_val does (prefixes never decrease)
+        const bool in_head = nseg == 0 || ch.start[0] >= r_val;
+        if (in_head) {
+            block_seq_sum(load_diff, diff, nh, 0.0f, 0u, r_val, &at, false, sh);
+        } else {
+            uint32_t t = 0;
+            for (uint32_t i = 1; i < nseg; ++i)
+                if (ch.start[i] < r_val) t = i;
+            const float S0 = ch.start[t];
+            const uint32_t k0 = kSegHead + t * kSegLen, k1 = min(V, k0 + kSegLen);
+            if (threadIdx.x < 64) {
+                wave_seg_sum(load_diff, V, k0, k1, S0, r_val, true, &at);
+                if (threadIdx.x == 0) ch.s = at;
+            }
+            __syncthreads();
+            at = ch.s;
+            if (at >= k1) at = V;
+        }
         corr = at < V ? at : 0u;  // corr_tok starts at 0 (:101)
     } else {
         fallback = 1;  // sample_token on the target row (:114): the selector's token
     }
     if (threadIdx.x == 0) {
+        uint32_t* out = a.rej + P.position * 4;
         out[0] = 0u;
         out[1] = corr;
         out[2] = fallback;
         out[3] = 1u;
+    }
+}
+
+// twd_sequential_sum through the segmented form: one row of n terms.
+template <bool STOP>
+__global__ __launch_bounds__(kRejThreads) void seg_array_kernel(const float* x, uint32_t n, float thr,
+                                                                const SegRec* rec, float* sum_out,
+                                                                uint32_t* stop_out) {
+    __shared__ SeqShared sh;
+    __shared__ ChainShared ch;
+    uint32_t stop = n;
+    const float s = seg_row_sum([&](uint32_t j0, auto& v) { load_row(x, j0, v); }, [&](uint32_t j) { return x[j]; },
+                                n, rec, thr, STOP ? &stop : nullptr, sh, ch);
+    if (threadIdx.x == 0) {
+        *sum_out = s;
+        if (STOP) *stop_out = stop;
     }
 }
 
@@ -609,6 +986,9 @@ int draft_scratch_reserve(DraftScratch* d, uint32_t vocab, uint32_t npos) {
     TWD_HIP(hipMalloc(&d->flags, 2 * TWD_MAX_ROWS * sizeof(uint32_t)));
     TWD_HIP(hipMalloc(&d->rej, 4 * TWD_MAX_ROWS * sizeof(uint32_t)));
     TWD_HIP(hipMalloc(&d->sums, 2 * TWD_MAX_ROWS * sizeof(float)));
+    TWD_HIP(hipMalloc(&d->seg_d, static_cast<size_t>(2) * TWD_MAX_ROWS * (kSegMax + 1) * sizeof(double)));
+    TWD_HIP(hipMalloc(&d->seg_rec, static_cast<size_t>(2) * TWD_MAX_ROWS * kSegMax * sizeof(SegRec)));
+    TWD_HIP(hipMalloc(&d->live, TWD_MAX_ROWS * sizeof(uint32_t)));
     return TWD_OK;
 }
 
@@ -618,6 +998,9 @@ void draft_scratch_free(DraftScratch* d) {
     if (d->flags) (void)hipFree(d->flags);
     if (d->rej) (void)hipFree(d->rej);
     if (d->sums) (void)hipFree(d->sums);
+    if (d->seg_d) (void)hipFree(d->seg_d);
+    if (d->seg_rec) (void)hipFree(d->seg_rec);
+    if (d->live) (void)hipFree(d->live);
     *d = DraftScratch{};
 }
 
@@ -647,11 +1030,27 @@ TWD_API int twd_sequential_sum(const float* terms, uint32_t n, float thr, float*
     if (!terms || !sum_out) return fail(TWD_E_INVALID, "null terms or sum_out");
     if (n == 0) return fail(TWD_E_INVALID, "n must be > 0");
     if ((reinterpret_cast<uintptr_t>(terms) & 15u) != 0) return fail(TWD_E_INVALID, "terms must be 16-byte aligned");
+    if (seg_count(n) > kSegMax) return fail(TWD_E_INVALID, "n above 2048 + 512 * 1024");
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    // one row's segment scratch, allocated on the first call and kept for the process
+    static std::mutex mu;
+    static double* seg_d = nullptr;
+    static SegRec* seg_rec = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        if (!seg_d) {
+            TWD_HIP(hipMalloc(&seg_d, (kSegMax + 1) * sizeof(double)));
+            TWD_HIP(hipMalloc(&seg_rec, kSegMax * sizeof(SegRec)));
+        }
+    }
+    const uint32_t nseg = seg_count(n);
+    const SegSrcArray src{terms};
+    seg_dsum_kernel<<<dim3(nseg + 1, 1), kSegThreads, 0, s>>>(src, n, seg_d);
+    if (nseg) seg_xfer_kernel<<<dim3(nseg, 1), kSegThreads, 0, s>>>(src, n, seg_d, seg_rec);
     if (stop_out)
-        seq_sum_kernel<true><<<1, kRejThreads, 0, s>>>(terms, n, thr, sum_out, stop_out);
+        seg_array_kernel<true><<<1, kRejThreads, 0, s>>>(terms, n, thr, seg_rec, sum_out, stop_out);
     else
-        seq_sum_kernel<false><<<1, kRejThreads, 0, s>>>(terms, n, thr, sum_out, stop_out);
+        seg_array_kernel<false><<<1, kRejThreads, 0, s>>>(terms, n, thr, seg_rec, sum_out, stop_out);
     TWD_HIP(hipGetLastError());
     return TWD_OK;
 }
@@ -734,8 +1133,20 @@ int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab
     const dim3 grid(a.parts, 2 * a.npos);
     draft_max_kernel<<<grid, kDraftThreads, 0, s>>>(a);
     draft_exp_kernel<<<grid, kDraftThreads, 0, s>>>(a);
-    draft_sum_kernel<<<2 * a.npos, kRejThreads, 0, s>>>(a);
-    draft_reject_kernel<<<a.npos, kRejThreads, 0, s>>>(a);
+    // the softmax sums, then the ratio tests, then the residual draws of rejected positions,
+    // each exact sum through the segmented pipeline
+    const uint32_t nseg = seg_count(vocab);
+    double* seg_d = sel->draft.seg_d;
+    SegRec* seg_rec = static_cast<SegRec*>(sel->draft.seg_rec);
+    const SegSrcSoftmax src_e{a.e, a.estride, a.flags};
+    seg_dsum_kernel<<<dim3(nseg + 1, 2 * a.npos), kSegThreads, 0, s>>>(src_e, vocab, seg_d);
+    if (nseg) seg_xfer_kernel<<<dim3(nseg, 2 * a.npos), kSegThreads, 0, s>>>(src_e, vocab, seg_d, seg_rec);
+    seg_sum_kernel<<<2 * a.npos, kRejThreads, 0, s>>>(a, seg_rec);
+    draft_ratio_kernel<<<1, 64, 0, s>>>(a, sel->draft.live);
+    const SegSrcResidual src_r{a.e, a.estride, a.sums, sel->draft.live};
+    seg_dsum_kernel<<<dim3(nseg + 1, a.npos), kSegThreads, 0, s>>>(src_r, vocab, seg_d);
+    if (nseg) seg_xfer_kernel<<<dim3(nseg, a.npos), kSegThreads, 0, s>>>(src_r, vocab, seg_d, seg_rec);
+    seg_residual_kernel<<<a.npos, kRejThreads, 0, s>>>(a, sel->draft.live, seg_rec);
     draft_finish_kernel<<<1, 64, 0, s>>>(sel->scratch.verify_tokens, used, drafts, n_drafts, has,
                                          a.rej, result);
     TWD_HIP(hipGetLastError());
