@@ -202,6 +202,21 @@ def _seq_cases():
     tiny = np.full(20000, 1e-9, np.float32)
     tiny[0] = 1.0
     cases.append(("below half an ulp", tiny))
+    # past the serial head the sum runs in 1024-term segments: lengths at segment edges, a sum
+    # that doubles inside many segments, one whose binade changes exactly at segment starts
+    # (each segment adds 2^k after a sum of 2^k), and long zero stretches between big terms
+    for n in (3071, 3072, 3073, 2048 + 1024 * 7, 2048 + 1024 * 7 + 1):
+        cases.append((f"segment edge n={n}", rng.random(n).astype(np.float32)))
+    cases.append(("growing terms", (np.arange(200000) * 1e-3).astype(np.float32)))
+    edge = np.zeros(2048 + 1024 * 12, np.float32)
+    edge[0] = 1.0
+    edge[1:2048] = 0.0
+    for k in range(12):  # segment k adds the running sum again: the sum doubles per segment
+        edge[2048 + 1024 * k] = np.float32(2.0 ** k)
+    cases.append(("binade change at segment starts", edge))
+    sparse = np.zeros(150000, np.float32)
+    sparse[rng.integers(0, 150000, 40)] = rng.random(40).astype(np.float32) * 100
+    cases.append(("sparse big terms", sparse))
     return cases
 
 
