@@ -7,6 +7,7 @@
 #include <cstdlib>
 #include <random>
 #include <set>
+#include <thread>
 #include <vector>
 
 #include "g4dense/sampling.hpp"
@@ -206,6 +207,32 @@ int main() {
         }
     }
     std::puts("100-draft verify ok");
+
+    // calls from several threads at once (each leases its own staging area and stream) give
+    // the ids of the same calls made one after another
+    {
+        const uint32_t V = 50000;
+        std::mt19937 gen(777);
+        std::normal_distribution<float> nd(0.0f, 3.0f);
+        constexpr int kThreads = 6, kCalls = 20;
+        std::vector<std::vector<float>> rows(kThreads * kCalls, std::vector<float>(V));
+        for (auto& r : rows)
+            for (auto& x : r) x = nd(gen);
+        const SamplingParams sp{0.8f, 0.95f, 64, 1.0f, false, 0};
+        std::vector<uint32_t> want(rows.size()), got(rows.size());
+        for (size_t i = 0; i < rows.size(); ++i) want[i] = sample_token(rows[i].data(), V, sp, splitmix64(i));
+        std::vector<std::thread> th;
+        for (int t = 0; t < kThreads; ++t)
+            th.emplace_back([&, t] {
+                for (int c = 0; c < kCalls; ++c) {
+                    const size_t i = static_cast<size_t>(t) * kCalls + c;
+                    got[i] = sample_token(rows[i].data(), V, sp, splitmix64(i));
+                }
+            });
+        for (auto& x : th) x.join();
+        CHECK(got == want);
+    }
+    std::puts("concurrent callers ok");
     std::puts("ALL OK");
     return 0;
 }

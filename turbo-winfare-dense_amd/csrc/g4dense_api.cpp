@@ -12,6 +12,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "g4dense/sampling.hpp"
 #include "g4dense/speculator.hpp"
@@ -21,9 +22,11 @@
 
 namespace {
 
-// Device staging shared by the host-pointer entry points; grown on demand, serialised.
+// Device staging of the host-pointer entry points: a pool of areas, one per concurrent caller.
+// A call leases an area (its selector, buffers and its own non-blocking stream), so calls from
+// different threads run concurrently; an area is grown on demand and returned to the pool.
 struct Staging {
-    std::mutex mu;
+    hipStream_t stream = nullptr;
     twd_selector* sel = nullptr;
     uint32_t sel_vocab = 0, sel_rows = 0;
     float* logits = nullptr;
@@ -39,10 +42,41 @@ struct Staging {
     ~Staging() = default;  // released with the process, like the reference's device context
 };
 
-Staging& staging() {
-    static Staging* s = new Staging();
-    return *s;
+struct StagingPool {
+    std::mutex mu;
+    std::vector<Staging*> idle;  // areas are kept for the process, like the reference's device context
+};
+
+StagingPool& pool() {
+    static StagingPool* p = new StagingPool();
+    return *p;
 }
+
+// One staging area for the duration of a call.
+class Lease {
+  public:
+    Lease() {
+        StagingPool& p = pool();
+        std::lock_guard<std::mutex> lock(p.mu);
+        if (p.idle.empty()) {
+            s_ = new Staging();
+        } else {
+            s_ = p.idle.back();
+            p.idle.pop_back();
+        }
+    }
+    ~Lease() {
+        StagingPool& p = pool();
+        std::lock_guard<std::mutex> lock(p.mu);
+        p.idle.push_back(s_);
+    }
+    Lease(const Lease&) = delete;
+    Lease& operator=(const Lease&) = delete;
+    Staging& operator*() const { return *s_; }
+
+  private:
+    Staging* s_;
+};
 
 [[noreturn]] void throw_last(const char* what) {
     throw g4dense::G4DenseFormatError(std::string(what) + ": " + twd_last_error());
@@ -54,6 +88,7 @@ void check_hip(hipError_t e, const char* what) {
 }
 
 void ensure(Staging& s, uint32_t vocab, uint32_t rows, size_t history_len) {
+    if (!s.stream) check_hip(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking), "hipStreamCreate");
     if (!s.sel || s.sel_vocab < vocab || s.sel_rows < rows) {
         if (s.sel) twd_selector_destroy(s.sel);
         s.sel = nullptr;
@@ -81,6 +116,16 @@ void ensure(Staging& s, uint32_t vocab, uint32_t rows, size_t history_len) {
         check_hip(hipMalloc(&s.drafts, (TWD_MAX_ROWS + 1) * sizeof(uint32_t)), "hipMalloc drafts");
         check_hip(hipMalloc(&s.vres, sizeof(twd_verify_result)), "hipMalloc verify result");
     }
+}
+
+void upload(Staging& s, void* dst, const void* src, size_t bytes, const char* what) {
+    check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s.stream), what);
+}
+
+// waits for everything enqueued on the area's stream, then copies back
+void download(Staging& s, void* dst, const void* src, size_t bytes, const char* what) {
+    check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s.stream), what);
+    check_hip(hipStreamSynchronize(s.stream), what);
 }
 
 twd_row_params row_params(const g4dense::SamplingParams& p, float uniform) {
@@ -115,12 +160,11 @@ G4_API void apply_repetition_penalty(float* logits, uint32_t vocab,
                                      const std::vector<uint32_t>& history, float penalty,
                                      float softcap) {
     if (penalty == 1.0f || history.empty() || vocab == 0) return;
-    Staging& s = staging();
-    std::lock_guard<std::mutex> lock(s.mu);
+    Lease lease;
+    Staging& s = *lease;
     ensure(s, vocab, 1, history.size());
-    check_hip(hipMemcpy(s.logits, logits, vocab * sizeof(float), hipMemcpyHostToDevice), "upload");
-    check_hip(hipMemcpy(s.history, history.data(), history.size() * sizeof(uint32_t),
-                        hipMemcpyHostToDevice), "upload history");
+    upload(s, s.logits, logits, vocab * sizeof(float), "upload");
+    upload(s, s.history, history.data(), history.size() * sizeof(uint32_t), "upload history");
     twd_row_params r{};
     r.temperature = 0.0f;
     r.top_p = 1.0f;
@@ -128,23 +172,23 @@ G4_API void apply_repetition_penalty(float* logits, uint32_t vocab,
     r.softcap = softcap;
     r.history_len = static_cast<uint32_t>(history.size());
     if (twd::launch_select(s.sel->scratch, s.logits, vocab, 1, vocab, &r, s.history, nullptr,
-                           nullptr, /*penalty_only=*/true) != TWD_OK)
+                           s.stream, /*penalty_only=*/true) != TWD_OK)
         throw_last("apply_repetition_penalty");
-    check_hip(hipMemcpy(logits, s.logits, vocab * sizeof(float), hipMemcpyDeviceToHost), "download");
+    download(s, logits, s.logits, vocab * sizeof(float), "download");
 }
 
 G4_API uint32_t sample_token(const float* logits, uint32_t vocab, const SamplingParams& p,
                              uint64_t seed) {
     if (vocab == 0) throw G4DenseFormatError("sample_token: empty vocabulary");
-    Staging& s = staging();
-    std::lock_guard<std::mutex> lock(s.mu);
+    Lease lease;
+    Staging& s = *lease;
     ensure(s, vocab, 1, 0);
-    check_hip(hipMemcpy(s.logits, logits, vocab * sizeof(float), hipMemcpyHostToDevice), "upload");
+    upload(s, s.logits, logits, vocab * sizeof(float), "upload");
     const twd_row_params r = row_params(p, twd_uniform_from_seed(seed));
-    if (twd_select(s.sel, s.logits, vocab, 1, vocab, &r, nullptr, s.tokens, nullptr) != TWD_OK)
+    if (twd_select(s.sel, s.logits, vocab, 1, vocab, &r, nullptr, s.tokens, s.stream) != TWD_OK)
         throw_last("sample_token");
     uint32_t tok = 0;
-    check_hip(hipMemcpy(&tok, s.tokens, sizeof(uint32_t), hipMemcpyDeviceToHost), "download");
+    download(s, &tok, s.tokens, sizeof(uint32_t), "download");
     if (tok == TWD_TOKEN_DEGENERATE)
         throw G4DenseFormatError("sample_token: logit distribution is degenerate");
     return tok;
@@ -171,8 +215,8 @@ G4_API SpeculativeEvaluation SpeculativeCoordinator::evaluate_verification(
                 throw G4DenseFormatError("evaluate_verification: a draft logit row is shorter than vocab_size");
     }
 
-    Staging& s = staging();
-    std::lock_guard<std::mutex> lock(s.mu);
+    Lease lease;
+    Staging& s = *lease;
     for (size_t b0 = 0; b0 < k; b0 += TWD_MAX_ROWS) {
         const uint32_t kb = static_cast<uint32_t>(std::min<size_t>(TWD_MAX_ROWS, k - b0));
         const bool last = b0 + kb == k;
@@ -187,19 +231,19 @@ G4_API SpeculativeEvaluation SpeculativeCoordinator::evaluate_verification(
         }
         ensure(s, vocab_size, rows, 0);
         for (uint32_t i = 0; i < rows; ++i)
-            check_hip(hipMemcpy(s.logits + static_cast<size_t>(i) * vocab_size, target_logits_per_pos[b0 + i],
-                                vocab_size * sizeof(float), hipMemcpyHostToDevice), "upload rows");
-        check_hip(hipMemcpy(s.drafts, draft_tokens.data() + b0, kb * sizeof(uint32_t), hipMemcpyHostToDevice),
-                  "upload drafts");
+            upload(s, s.logits + static_cast<size_t>(i) * vocab_size, target_logits_per_pos[b0 + i],
+                   vocab_size * sizeof(float), "upload rows");
+        upload(s, s.drafts, draft_tokens.data() + b0, kb * sizeof(uint32_t), "upload drafts");
         twd_row_params r = row_params(sampling, 0.0f);
         const uint64_t seed = base_seed + b0;
         if (n_draft_rows == 0) {
             if (twd_verify(s.sel, s.logits, vocab_size, rows, vocab_size, &r, seed, s.drafts, kb, s.vres,
-                           nullptr) != TWD_OK)
+                           s.stream) != TWD_OK)
                 throw_last("evaluate_verification");
         } else {
             const size_t need = static_cast<size_t>(n_draft_rows) * vocab_size;
             if (s.dlogits_cap < need) {
+                check_hip(hipStreamSynchronize(s.stream), "hipStreamSynchronize");  // earlier batches' copies
                 if (s.dlogits) check_hip(hipFree(s.dlogits), "hipFree");
                 s.dlogits = nullptr;
                 check_hip(hipMalloc(&s.dlogits, need * sizeof(float)), "hipMalloc draft rows");
@@ -209,17 +253,16 @@ G4_API SpeculativeEvaluation SpeculativeCoordinator::evaluate_verification(
             for (uint32_t i = 0; i < n_draft_rows; ++i) {
                 if (draft_logits[b0 + i].empty()) continue;
                 float* dst = s.dlogits + static_cast<size_t>(i) * vocab_size;
-                check_hip(hipMemcpy(dst, draft_logits[b0 + i].data(), vocab_size * sizeof(float),
-                                    hipMemcpyHostToDevice), "upload draft rows");
+                upload(s, dst, draft_logits[b0 + i].data(), vocab_size * sizeof(float), "upload draft rows");
                 dptr[i] = dst;
             }
             r.repetition_penalty = sampling.repetition_penalty;  // is_greedy() needs it
             if (twd_verify_draft(s.sel, s.logits, vocab_size, rows, vocab_size, dptr, n_draft_rows, &r, seed,
-                                 s.drafts, kb, s.vres, nullptr) != TWD_OK)
+                                 s.drafts, kb, s.vres, s.stream) != TWD_OK)
                 throw_last("evaluate_verification");
         }
         twd_verify_result v{};
-        check_hip(hipMemcpy(&v, s.vres, sizeof(v), hipMemcpyDeviceToHost), "download result");
+        download(s, &v, s.vres, sizeof(v), "download result");
         if (v.n_tokens == TWD_TOKEN_DEGENERATE)
             throw G4DenseFormatError("sample_token: logit distribution is degenerate");
         eval.accepted_tokens.insert(eval.accepted_tokens.end(), v.tokens, v.tokens + v.n_tokens);
