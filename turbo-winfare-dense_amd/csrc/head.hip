@@ -211,6 +211,9 @@ using EpiShared = EpiSharedT<kHeadWaves>;
 // tot[j][mt][i] holds row r = (tile0 + j) * 16 + lane % 16 of MFMA row 16 mt + 4 (lane / 16) + i,
 // which carries h row m = (16 mt + 4 (lane / 16) + i) / MS when i is a multiple of MS (MS > 1:
 // the rows are spread over the MFMA rows, see head_small_kernel); other entries are not outputs.
+template <int NW>
+__device__ __forceinline__ void grid_finish(const HeadArgs& a, EpiSharedT<NW>& se);
+
 template <int NMT, int NI, int RT, int MODE, int NW, int MS = 1>
 __device__ __forceinline__ void head_epilogue(const HeadArgs& a, f32x4_t (&tot)[RT][NMT],
                                               uint32_t tile0, EpiSharedT<NW>& se) {
@@ -262,6 +265,15 @@ __device__ __forceinline__ void head_epilogue(const HeadArgs& a, f32x4_t (&tot)[
             const uint32_t m = (mt * 16 + 4 * (lane >> 4) + i) / MS;
             if ((lane & 15) == 0 && m < TWD_MAX_ROWS) se.red[wave][m] = k;
         }
+    grid_finish<NW>(a, se);
+}
+
+// The greedy finish shared by the head kernels, once every wave has written its per-row maxima
+// to se.red[wave][m]: the block's maxima go to gbest, the block counts itself in, and the last
+// block of the launch writes the tokens (and the greedy verify bookkeeping).
+template <int NW>
+__device__ __forceinline__ void grid_finish(const HeadArgs& a, EpiSharedT<NW>& se) {
+    const int tid = threadIdx.x;
     __syncthreads();
     const uint32_t nb = gridDim.x;
     if (static_cast<uint32_t>(tid) < a.M) {
@@ -767,7 +779,8 @@ __global__ __launch_bounds__(NW * 64) void head_small_kernel(HeadArgs a) {
     }
 }
 
-// ---- 9 <= M <= 64: h prepared once per call, staged through LDS by plain copies -------------------
+// ---- 9 <= M <= 16 (and the RMSNorm prologue's 5 <= M <= 8): h prepared once per call, ------
+// staged through LDS by plain copies; M > 16 runs head_wide32_kernel below
 //
 // prep_hidden_kernel writes, once per call, the prepared h in A-fragment order,
 // hp[U][mt][t][lane] (16 B each, rows m >= M zero), and the bias A-fragment entries
@@ -897,22 +910,17 @@ __global__ __launch_bounds__(kHeadThreads) void prep_rmsnorm_kernel(const float*
 }
 
 // Block = NW waves; wave w owns RT consecutive 16-row tiles. NMT = number of 16-wide m tiles
-// (1 for M <= 16, 2 for M <= 32, 4 for M <= 64). A stage is one chunk (two groups). Each stage: one barrier;
+// (1: this kernel serves M <= 16). A stage is one chunk (two groups). Each stage: one barrier;
 // the next chunk's prepared h copied straight from global memory into the other LDS buffer
 // (for an even chunk also the next super-unit's bias fragment); the weights of the next chunk
 // requested into the other half of a two-deep register ring. One chunk per stage keeps the LDS
-// at 40 KB per block, where two-chunk stages needed 77 KB. Measured on MI355X at V = 262144,
-// d = 5376 against the two-chunk register-staged form: M = 64 277.5 -> 249.1 us, M = 16
-// 143.8 -> 136.2 us.
+// small; measured on MI355X at V = 262144, d = 5376 against a two-chunk register-staged form:
+// M = 16 143.8 -> 136.2 us.
 //
 // Per group step the MFMA chains of all RT x NMT accumulators run first; the scales are
 // applied (tot += t * acc) right after, while the next step's nibbles are converted.
-//
-// NW waves share one block's h stream: NW = 4 for one and two m tiles, 8 for four. Every block
-// re-reads all of h from L2, so eight waves halve those copies per weight byte (M = 64: 238 us
-// against 248 us with four waves); at 128 VGPRs two such blocks fill a CU.
 template <int NMT, int RT, int MODE, int NW>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW == 8 ? 4 : 3)))
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(3)))
 void head_wide_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_t* __restrict__ hx) {
     constexpr int kVec = NMT * 4 * 64;  // 16 B A-fragment vectors per chunk
     constexpr int kXA = NMT * 64;       // 16 B bias vectors per super-unit
@@ -956,17 +964,9 @@ void head_wide_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_t*
             const uint32_t piece = wave * kCopies + it;
             copy16(src + piece * 64 + lane, dst + piece * 64);
         }
-        // chunk C opens super-unit C / 2 when even; its bias buffer is (C / 2) & 1. With four
-        // m tiles every wave copies a piece (waves past the fourth copy the same four pieces
-        // again: identical bytes to the same LDS words, in a buffer no wave reads this stage),
-        // so no branch splits the stage, which the scheduler then interleaves as one basic
-        // block (5-6% faster at M = 64)
+        // chunk C opens super-unit C / 2 when even; its bias buffer is (C / 2) & 1
         if constexpr (P == 0) {
-            if constexpr (NMT == 4) {
-                const uint32_t xp = wave & 3;
-                copy16(hx + static_cast<size_t>(C >> 1) * kXA + xp * 64 + lane,
-                       (((C >> 1) & 1) ? sXA1 : sXA0) + xp * 64);
-            } else if (wave < static_cast<uint32_t>(kXA / 64)) {
+            if (wave < static_cast<uint32_t>(kXA / 64)) {
                 copy16(hx + static_cast<size_t>(C >> 1) * kXA + wave * 64 + lane,
                        (((C >> 1) & 1) ? sXA1 : sXA0) + wave * 64);
             }
@@ -1073,6 +1073,323 @@ void head_wide_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_t*
     head_epilogue<NMT, 4, RT, MODE>(a, tot, tile0, se);
 }
 
+// ---- 33 <= M <= 64: 32x32x16 MFMAs, weights and h streamed into LDS two chunks ahead ----------
+//
+// Lane l = 32 kh + n of a 32 x 32 x 16 MFMA carries B column n (a vocabulary row of the wave's
+// tile pair: tile n / 16, row n % 16) and k half kh. For k-step s of group g (64 columns) it
+// takes one nibble word of row n: the unit's lane 16 kg + n % 16, kg = kh for s = 0, 1 and
+// kh + 2 for s = 2, 3, word 2 g + (s & 1), i.e. columns 64 g + {0, 32, 16, 48}[s] + 8 kh + 0..7.
+// prep_hidden32_kernel lays the A entries (h rows) out in the same column order:
+// hp[U][mt][g][s][lane] is prep_h of h[32 mt + l % 32][128 U + 64 g + koff[s] + 8 (l / 32) ..+8]
+// (rows >= M zero), and hx[P][mt][f][lane] holds, in dword c, slice 2 f + l / 32 (hi, mid, lo,
+// zero) of X[32 mt + l % 32][4 P + c] duplicated into a bf16 pair. The group sums X are taken in
+// the order of prep_hidden_kernel: eight-column pieces summed in column order, then a
+// three-level pairwise tree over the pieces.
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+template <int NM>
+__global__ __launch_bounds__(kHeadThreads) void prep_hidden32_kernel(const uint16_t* __restrict__ h,
+                                                                     uint32_t M, uint32_t d,
+                                                                     u32x4_t* __restrict__ hp,
+                                                                     u32x4_t* __restrict__ hx) {
+    constexpr uint32_t per_chunk = NM * 512;  // tasks per chunk: [mt][g][row i][piece p]
+    const uint32_t nunits = d / kChunkK;
+    const uint32_t padded = nunits + (nunits & 1);
+    const uint32_t task = blockIdx.x * kHeadThreads + threadIdx.x;  // grid covers padded chunks
+    const uint32_t U = task / per_chunk, rem = task % per_chunk;
+    const uint32_t p = rem & 7, i = (rem >> 3) & 31, g = (rem >> 8) & 1, mt = rem >> 9;
+    const uint32_t m = 32 * mt + i;
+    u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
+    if (U < nunits && m < M)
+        v = *reinterpret_cast<const u32x4_t*>(h + static_cast<size_t>(m) * d + U * kChunkK + g * kGroup + p * 8);
+    float s = sum8_bf16(v);
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    if (U < padded) {
+        // piece p holds columns 8 p of the group: k-step {0, 2, 1, 3}[p / 2], k half p % 2
+        const uint32_t ks = ((p >> 1) == 1) ? 2u : ((p >> 1) == 2) ? 1u : (p >> 1);
+        hp[(((static_cast<size_t>(U) * NM + mt) * 2 + g) * 4 + ks) * 64 + (p & 1) * 32 + i] = prep_h(v);
+        if (p == 0) {
+            const uint32_t G = 2 * U + g;
+            uint32_t* x = reinterpret_cast<uint32_t*>(hx);
+            auto at = [&](int sl) {
+                return x + ((((static_cast<size_t>(G >> 2) * NM + mt) * 2 + (sl >> 1)) * 64 + (sl & 1) * 32 + i) * 4 +
+                            (G & 3));
+            };
+            bias_slices(s, at);  // zero slices for the padding chunk's two groups
+        }
+    }
+}
+
+// Softcap, logits store and, for the greedy modes, the per-row maxima of the 32 x 32 layout:
+// tot[mt][v] of lane l is vocabulary row 16 T0 + l % 32 and h row 32 mt + 8 (v / 4) + 4 (l / 32)
+// + v % 4.
+template <int NP, int NM, int MODE, int NW>
+__device__ __forceinline__ void head_epilogue32(const HeadArgs& a, f32x16_t (&tot)[NP][NM], uint32_t T0,
+                                                EpiSharedT<NW>& se) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t mb = 4 * (lane >> 5);
+    uint64_t best[NM][16];
+#pragma unroll
+    for (int mt = 0; mt < NM; ++mt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) best[mt][v] = 0;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        const uint32_t r = (T0 + 2 * p) * kTileRows + (lane & 31);
+#pragma unroll
+        for (int mt = 0; mt < NM; ++mt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const uint32_t m = 32 * mt + 8 * (v >> 2) + mb + (v & 3);
+                float x = tot[p][mt][v];
+                if (a.softcap > 0.0f) x = a.softcap * tanhf(x / a.softcap);
+                const bool live = (m < a.M) && (r < a.vocab);
+                if (live && a.logits) a.logits[static_cast<size_t>(m) * a.vocab + r] = x;
+                if (MODE != kModeLogits) {
+                    const uint64_t k = live ? rank_key(x, r) : 0ull;
+                    best[mt][v] = k > best[mt][v] ? k : best[mt][v];
+                }
+            }
+    }
+    if (MODE == kModeLogits) return;
+    // rows sharing m are the 32 lanes with the same lane / 32
+#pragma unroll
+    for (int mt = 0; mt < NM; ++mt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            uint64_t k = best[mt][v];
+#pragma unroll
+            for (int msk = 1; msk < 32; msk <<= 1) {
+                const uint64_t o = shfl_xor_u64(k, msk);
+                k = o > k ? o : k;
+            }
+            const uint32_t m = 32 * mt + 8 * (v >> 2) + mb + (v & 3);
+            if ((lane & 31) == 0 && m < TWD_MAX_ROWS) se.red[wave][m] = k;
+        }
+    grid_finish<NW>(a, se);
+}
+
+// Block = NW waves; wave w owns NP tile pairs (32 vocabulary rows each, tiles T0 + 2 p and
+// T0 + 2 p + 1, T0 = 2 NP (blockIdx.x * NW + w)) and all rows as NM m tiles of 32. Every
+// vector-memory access of the streaming loop is a DMA into LDS: the wave's own weights (per pair
+// and chunk, two 16 B nibble vectors and one scale dword per lane) two chunks ahead into a
+// private two-slot ring, and the block's share of the prepared h (with each even chunk also the
+// super-unit's bias entries) one chunk ahead into a two-slot ring -- h comes from L2, the weights
+// from HBM. At 79 KB two blocks share a CU, so one block's epilogue and pipeline fill overlap the
+// other's stream. A stage (one chunk, two groups):
+//   1. wait until only the weight DMAs of chunk C + 1 are outstanding; barrier (chunk C's h is in
+//      LDS for every wave, and every wave is done with chunk C - 1); the DMAs of chunk C + 1's h
+//      into the slot chunk C - 1 used;
+//   2. read the wave's weights of chunk C out of its ring slot into registers;
+//   3. per group: the A entries of the group once, then per pair 4 k-steps x NM m tiles of
+//      MFMAs into acc and tot += t * acc; before the second group, once the weight reads have
+//      landed, the DMAs of chunk C + 2's weights into the slot just read;
+//   4. after an odd chunk, the super-unit's bias MFMAs (two per pair and m tile: slices
+//      hi + mid, lo).
+// The loop issues no vector-memory instruction the compiler can see, so the one explicit wait
+// per stage is exact: it counts the youngest DMAs, chunk C + 1's weights.
+constexpr int kW32Waves = 8;
+constexpr int kW32Pairs = 1;
+
+template <int NP, int NM, int NW, int MODE>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 4 : 2)))
+void head_wide32_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_t* __restrict__ hx) {
+    constexpr int kVec = NM * 512;              // 16 B A vectors per chunk
+    constexpr int kXA = NM * 128;               // 16 B bias vectors per super-unit
+    constexpr int kHCopies = kVec / (64 * NW);  // 1 KB pieces of h each wave copies per chunk
+    constexpr int kXPieces = kXA / 64;
+    static_assert(kHCopies >= 1 && kVec % (64 * NW) == 0 && kXPieces <= NW, "copy split");
+    constexpr int kOpsW = 3 * NP;  // weight DMAs a wave issues per chunk
+    __shared__ u32x4_t sH[2][kVec];
+    __shared__ u32x4_t sX[2][kXA];
+    __shared__ u32x4_t sWn[NW][2][NP][2][64];
+    __shared__ uint32_t sWs[NW][2][NP][64];
+    __shared__ EpiSharedT<NW> se;
+
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = wave_id();
+    const uint32_t T0 = (blockIdx.x * NW + wave) * 2 * NP;
+    const uint32_t magic = vgpr_const(0x43004300u);
+    const uint32_t nchunks = a.nunits + (a.nunits & 1);
+    const uint32_t stripe = a.nunits * kUnitBytes;
+
+    // weights: SGPR base at the wave's first tile (clamped; tiles past the end re-read the last
+    // tile and their rows are never stored), per-lane offsets to the lane's tile of each pair
+    const uint32_t Tb = min(T0, a.ntiles - 1);
+    const uint32_t kh = lane >> 5, n = lane & 31;
+    uint32_t vo_n[NP], vo_s[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        vo_n[p] = (min(T0 + 2 * p + (n >> 4), a.ntiles - 1) - Tb) * stripe + (16 * kh + (n & 15)) * 16;
+        vo_s[p] = (min(T0 + 2 * p + kh, a.ntiles - 1) - Tb) * stripe + kUnitNibbleBytes + n * 4;
+    }
+    const uint8_t* wbase = a.tiled + static_cast<size_t>(Tb) * stripe;
+    const uint32_t vo_h = lane * 16;
+
+    auto lds_off = [](const void* q) {
+        return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)q));
+    };
+    // One DMA: 16 B (or 4 B) per lane from base + voff into LDS at dst + 16 * lane (4 * lane).
+    // No instruction offset: it would move the LDS address as well. Issued by inline asm,
+    // invisible to the compiler's wait insertion; M0 is reserved to the compiler, which sets it
+    // next to each instruction of its own that reads it, and this kernel has none, so the value
+    // left here is never read.
+    auto dma16 = [&](const void* base, uint32_t voff, uint32_t dst) {
+        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(dst), "v"(voff), "s"(base)
+                     : "memory");
+    };
+    // the weights stream once: non-temporal, so they do not push h out of L2
+    auto dma16_nt = [&](const void* base, uint32_t voff, uint32_t dst) {
+        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2 nt" ::"s"(dst), "v"(voff), "s"(base)
+                     : "memory");
+    };
+    auto dma4_nt = [&](const void* base, uint32_t voff, uint32_t dst) {
+        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2 nt" ::"s"(dst), "v"(voff), "s"(base)
+                     : "memory");
+    };
+    // chunk C's h pieces into slot C & 1, with an even C also super-unit C / 2's bias pieces
+    auto issue_h = [&](uint32_t C) {
+        const u32x4_t* src = hp + static_cast<size_t>(C) * kVec;
+#pragma unroll
+        for (int it = 0; it < kHCopies; ++it) {
+            const uint32_t piece = wave * kHCopies + it;
+            dma16(src + piece * 64, vo_h, lds_off(&sH[C & 1][piece * 64]));
+        }
+        if ((C & 1) == 0) {
+            const uint32_t xp = wave % kXPieces, P = C >> 1;
+            dma16(hx + static_cast<size_t>(P) * kXA + xp * 64, vo_h, lds_off(&sX[P & 1][xp * 64]));
+        }
+    };
+    // chunk C's weights into the wave's slot C & 1
+    auto issue_w = [&](uint32_t C) {
+        const uint32_t ws = C & 1;
+        const uint8_t* wb = wbase + static_cast<size_t>(min(C, a.nunits - 1)) * kUnitBytes;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            dma16_nt(wb, vo_n[p], lds_off(&sWn[wave][ws][p][0][0]));
+            dma16_nt(wb + 512, vo_n[p], lds_off(&sWn[wave][ws][p][1][0]));  // unit lanes 16 (kh + 2) + r
+            dma4_nt(wb, vo_s[p], lds_off(&sWs[wave][ws][p][0]));
+        }
+    };
+
+    f32x16_t tot[NP][NM];
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int mt = 0; mt < NM; ++mt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) tot[p][mt][v] = 0.0f;
+    u32x2_t sc_even[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) sc_even[p] = u32x2_t{0u, 0u};
+
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    issue_h(0);
+    issue_w(0);
+    issue_w(1);
+
+    auto stage = [&](uint32_t C, auto parity) {
+        constexpr int P = decltype(parity)::value;
+        __builtin_amdgcn_s_waitcnt(0x0F70 | kOpsW);  // outstanding now: chunk C + 1's weights
+        __syncthreads();
+        issue_h(C + 1);  // slot (C + 1) & 1: every wave is done with chunk C - 1
+        u32x4_t w0[NP], w1[NP];
+        u32x2_t sc[NP];
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            w0[p] = sWn[wave][P][p][0][lane];
+            w1[p] = sWn[wave][P][p][1][lane];
+            sc[p] = u32x2_t{sWs[wave][P][p][2 * n], sWs[wave][P][p][2 * n + 1]};
+        }
+        const u32x4_t* sA = sH[P];
+        // unit u = NP g + p: the MFMA chains of pair p over group g into acc[u & 1]; its scale
+        // FMAs are placed after the next unit's chains, so each wave has MFMA and VALU work
+        // that do not depend on each other
+        f32x16_t acc[2][NM];
+        bf16x8_t av[NM][4];
+        auto load_a = [&](int g) {
+#pragma unroll
+            for (int mt = 0; mt < NM; ++mt)
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    av[mt][s] = __builtin_bit_cast(bf16x8_t, sA[((mt * 2 + g) * 4 + s) * 64 + lane]);
+        };
+        auto chain = [&](int g, int p) {
+            const int u = (NP * g + p) & 1;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const uint32_t word = (s < 2) ? w0[p][2 * g + (s & 1)] : w1[p][2 * g + (s & 1)];
+                const bf16x8_t b = nibbles_to_bf16(word, magic);
+#pragma unroll
+                for (int mt = 0; mt < NM; ++mt) {
+                    if (s == 0)
+                        acc[u][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[mt][s], b, f32x16_t{}, 0, 0, 0);
+                    else
+                        acc[u][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[mt][s], b, acc[u][mt], 0, 0, 0);
+                }
+            }
+        };
+        auto scale = [&](int g, int p) {
+            const int u = (NP * g + p) & 1;
+            const float t = bf16_hi(g == 0 ? sc[p].x : sc[p].y);
+#pragma unroll
+            for (int mt = 0; mt < NM; ++mt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) tot[p][mt][v] = fmaf(t, acc[u][mt][v], tot[p][mt][v]);
+        };
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            load_a(g);
+            if (g == 1) {
+                // every LDS read of this wave's weight slot (and the group's A entries) has
+                // landed: the slot can take chunk C + 2
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                issue_w(C + 2);
+            }
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                chain(g, p);
+                if (p > 0) scale(g, p - 1);
+                else if (g > 0) scale(g - 1, NP - 1);
+            }
+        }
+        scale(1, NP - 1);
+        if constexpr (P == 0) {
+#pragma unroll
+            for (int p = 0; p < NP; ++p) sc_even[p] = sc[p];
+        } else {
+            // the super-unit's bias: B = the four groups' {b, t} words of row n (both k halves),
+            // A = X slices hi + mid, then lo + zero
+            const u32x4_t* sXA = sX[(C >> 1) & 1];
+            bf16x8_t xa[NM][2];
+#pragma unroll
+            for (int mt = 0; mt < NM; ++mt)
+#pragma unroll
+                for (int f = 0; f < 2; ++f) xa[mt][f] = __builtin_bit_cast(bf16x8_t, sXA[(mt * 2 + f) * 64 + lane]);
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                const bf16x8_t bb =
+                    __builtin_bit_cast(bf16x8_t, u32x4_t{sc_even[p].x, sc_even[p].y, sc[p].x, sc[p].y});
+#pragma unroll
+                for (int mt = 0; mt < NM; ++mt)
+#pragma unroll
+                    for (int f = 0; f < 2; ++f)
+                        tot[p][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[mt][f], bb, tot[p][mt], 0, 0, 0);
+            }
+        }
+    };
+    for (uint32_t C = 0; C < nchunks; C += 2) {
+        stage(C, I0{});
+        stage(C + 1, I1{});
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);  // the last (unused) DMAs land before LDS is reused
+    __syncthreads();
+    head_epilogue32<NP, NM, MODE, NW>(a, tot, T0, se);
+}
+
 // ---- layout repack: reference [W|S|B] -> units ----------------------------------------------
 // Sets *bad when a scale's magnitude exceeds kMaxScale (t = -128 s would not be finite) or a bias
 // is infinite: the kernels multiply every bias and t by bf16 slices and padding entries that can
@@ -1171,17 +1488,14 @@ struct twd_head {
 
 namespace {
 
-// staged-h kernel: row tiles per wave (measured on MI355X: M = 16 -> 4, M = 64 -> 2)
-constexpr int kRT1 = 4;  // M <= 16
-constexpr int kRT2 = 4;  // M <= 32 (M = 32: 174 us, against 236 us with four m tiles)
-constexpr int kRT4 = 2;  // M <= 64
+// staged-h kernel (M <= 16): row tiles per wave, measured best on MI355X
+constexpr int kRT1 = 4;
 // resident-h kernel: row tiles per wave and weight units in flight, measured best on MI355X at
 // V = 262144, d = 5376: 4096 waves, 16 resident per CU, one round on 256 CUs. M <= 4: 512 blocks
 // of 8 waves, two per CU. 5 <= M <= 8: 256 blocks of 16 waves, one per CU (one LDS copy of h
 // serves 16 waves; M = 8 leaves no room for a second block's h anyway).
 constexpr int kRTS = 4, kPFS = 2;
 constexpr int kNWS4 = 8, kNWS8 = 16;
-constexpr int kNWW4 = 8;  // waves per block of the wide kernel with four m tiles
 constexpr size_t kLdsBytes = 160 * 1024;
 constexpr uint32_t kSmallMaxRows = 8;
 
@@ -1336,15 +1650,15 @@ int launch_head(twd_head* h, const uint16_t* hidden, uint32_t rows, float* logit
         head_wide_kernel<1, kRT1, MODE, kHeadWaves>
             <<<blocks_for(h->ntiles, kRT1), kHeadThreads, 0, stream>>>(a, h->hp, h->hx);
     } else if (rows <= 32) {
-        prep_hidden_kernel<2><<<padded_units(h->nunits) * 2, kHeadThreads, 0, stream>>>(hidden, rows, h->d,
-                                                                                       h->hp, h->hx);
-        head_wide_kernel<2, kRT2, MODE, kHeadWaves>
-            <<<blocks_for(h->ntiles, kRT2), kHeadThreads, 0, stream>>>(a, h->hp, h->hx);
+        prep_hidden32_kernel<1><<<padded_units(h->nunits) * 2, kHeadThreads, 0, stream>>>(hidden, rows, h->d,
+                                                                                         h->hp, h->hx);
+        head_wide32_kernel<kW32Pairs, 1, kW32Waves, MODE>
+            <<<blocks_for(h->ntiles, 2 * kW32Pairs, kW32Waves), kW32Waves * 64, 0, stream>>>(a, h->hp, h->hx);
     } else {
-        prep_hidden_kernel<4><<<padded_units(h->nunits) * 4, kHeadThreads, 0, stream>>>(hidden, rows, h->d,
-                                                                                       h->hp, h->hx);
-        head_wide_kernel<4, kRT4, MODE, kNWW4>
-            <<<blocks_for(h->ntiles, kRT4, kNWW4), kNWW4 * 64, 0, stream>>>(a, h->hp, h->hx);
+        prep_hidden32_kernel<2><<<padded_units(h->nunits) * 4, kHeadThreads, 0, stream>>>(hidden, rows, h->d,
+                                                                                         h->hp, h->hx);
+        head_wide32_kernel<kW32Pairs, 2, kW32Waves, MODE>
+            <<<blocks_for(h->ntiles, 2 * kW32Pairs, kW32Waves), kW32Waves * 64, 0, stream>>>(a, h->hp, h->hx);
     }
     TWD_HIP(hipGetLastError());
     return TWD_OK;
