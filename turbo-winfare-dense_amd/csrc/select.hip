@@ -119,8 +119,7 @@ __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, SelCommon& c) {
 template <int NT>
 __device__ __forceinline__ double block_sum_f64(double v, SelCommon& c) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    v = wave_reduce(v, 0.0, [](double a, double b) { return a + b; });
     if (lane == 0) c.redd[wave] = v;
     __syncthreads();
     double r = 0.0;
@@ -133,12 +132,9 @@ __device__ __forceinline__ double block_sum_f64(double v, SelCommon& c) {
 template <int NT>
 __device__ __forceinline__ void block_stats(uint32_t& flag, float& mx, float& mn, SelCommon& c) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        flag |= __shfl_xor(flag, m);
-        mx = fmaxf(mx, __shfl_xor(mx, m));
-        mn = fminf(mn, __shfl_xor(mn, m));
-    }
+    flag = wave_reduce(flag, 0u, [](uint32_t a, uint32_t b) { return a | b; });
+    mx = wave_reduce(mx, -INFINITY, [](float a, float b) { return fmaxf(a, b); });
+    mn = wave_reduce(mn, INFINITY, [](float a, float b) { return fminf(a, b); });
     if (lane == 0) {
         c.redu[wave] = flag;
         c.redf[wave] = mx;
@@ -831,8 +827,11 @@ __global__ __launch_bounds__(kSmThreads) void select_sample_merge_kernel(SelectA
     double part = 0.0;
 #pragma unroll
     for (uint32_t q = 0; q < kSmPer; ++q)
-        if (key[q] != 0 && wsum[q] != 0.0)
-            part += wsum[q] * exp_for_sum(static_cast<double>(wm[q]) - static_cast<double>(gm), sh.c.exp2_tbl);
+        if (key[q] != 0 && wsum[q] != 0.0) {
+            // exp_core is exp_for_sum's value on [-700, 0] without its special cases
+            const double x = static_cast<double>(wm[q]) - static_cast<double>(gm);
+            part += wsum[q] * (x >= -700.0 ? exp_core(x, sh.c.exp2_tbl) : exp_for_sum(x, sh.c.exp2_tbl));
+        }
     const double total = block_sum_f64<NT>(part, sh.c);
     if (flag != 0 || !(total > 0.0)) {  // sampling.cpp:116-118
         if (tid == 0) b.tokens[row] = TWD_TOKEN_DEGENERATE;

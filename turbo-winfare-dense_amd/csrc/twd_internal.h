@@ -73,13 +73,57 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int mask) {
     return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const uint64_t o = shfl_xor_u64(v, m);
-        v = o > v ? o : v;
+// One DPP move of a 32- or 64-bit value (a 64-bit one as two 32-bit moves): lanes of rows
+// outside ROWS keep `old`.
+template <int CTRL, int ROWS = 0xF, typename T>
+__device__ __forceinline__ T dpp_move(T old, T v) {
+    static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit values");
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                                 __builtin_bit_cast(int, v), CTRL, ROWS, 0xF, false));
+    } else {
+        const uint64_t o = __builtin_bit_cast(uint64_t, old), x = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+            static_cast<int>(static_cast<uint32_t>(o)), static_cast<int>(static_cast<uint32_t>(x)), CTRL, ROWS, 0xF,
+            false));
+        const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+            static_cast<int>(static_cast<uint32_t>(o >> 32)), static_cast<int>(static_cast<uint32_t>(x >> 32)), CTRL,
+            ROWS, 0xF, false));
+        return __builtin_bit_cast(T, (static_cast<uint64_t>(hi) << 32) | lo);
     }
-    return v;
+}
+
+template <typename T>
+__device__ __forceinline__ T readlane63(T v) {
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+    } else {
+        const uint64_t x = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(x)), 63));
+        const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(x >> 32)), 63));
+        return __builtin_bit_cast(T, (static_cast<uint64_t>(hi) << 32) | lo);
+    }
+}
+
+// Reduction of a full wave (every lane active) under an associative, commutative op, returned
+// wave-uniform. Inside each row of 16 lanes: quad_perm [1,0,3,2] and [2,3,0,1], then
+// row_half_mirror and row_mirror, after which every lane holds its row's value; row_bcast:15
+// into rows 1 and 3 and row_bcast:31 into rows 2 and 3 leave the wave's value in lane 63. Each
+// step is a register move, where a shuffle is an LDS round trip. For max, min and OR the
+// result is the same as any other order; a floating-point sum is rounded in this tree's order.
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_reduce(T v, T ident, Op op) {
+    v = op(v, dpp_move<0xB1>(ident, v));
+    v = op(v, dpp_move<0x4E>(ident, v));
+    v = op(v, dpp_move<0x141>(ident, v));
+    v = op(v, dpp_move<0x140>(ident, v));
+    v = op(v, dpp_move<0x142, 0xA>(ident, v));
+    v = op(v, dpp_move<0x143, 0xC>(ident, v));
+    return readlane63(v);
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    return wave_reduce(v, uint64_t{0}, [](uint64_t a, uint64_t b) { return a > b ? a : b; });
 }
 
 // 2^(j/64), j = 0..63, each the double nearest the exact value: the table of exp_for_sum.
