@@ -165,14 +165,16 @@ def test_greedy_tie_goes_to_lower_index(torch_dev, oracle):
     assert int(head.greedy(to_dev_bf16(torch_dev, hb)).item()) == 5
 
 
-@pytest.mark.parametrize("case", range(8))
+@pytest.mark.parametrize("case", range(11))
 def test_verify_greedy_fused(torch_dev, oracle, case):
+    # K + 1 rows: up to 8 on the resident-h kernel, 21, 41 and 64 on the 32x32 kernel with one
+    # and two m tiles
     torch, dev = torch_dev
     V = 4096
     W, S, B = oracle.gen_lm_head(500, V, D)
     head = make_head(torch_dev, W, S, B, V, D, CAP)
     rng = np.random.default_rng(case)
-    K = [4, 4, 4, 1, 7, 0, 2, 4][case]
+    K = [4, 4, 4, 1, 7, 0, 2, 4, 20, 40, 63][case]
     rows = K + 1 if case != 6 else K  # case 6: no bonus row
     hb = hidden_bf16(600 + case, rows, D)
     h = to_dev_bf16(torch_dev, hb)
