@@ -89,6 +89,51 @@ def launch_percentiles(torch, n, step_fn):
     return {f"launch_us_p{q}": float(np.percentile(us, q)) for q in (10, 50, 90)}
 
 
+def power_during(torch, seconds, step_fn):
+    """Runs step_fn back to back for `seconds` (after the timed regions, outside every one of
+    them) while `amd-smi metric -p -c`, started as a child process, samples the socket power
+    and the eight XCDs' graphics clocks. Returns the medians over the samples taken once the
+    loop has run for half a second, or None where amd-smi is not available."""
+    import shutil
+    import subprocess
+    import threading
+    exe = shutil.which("amd-smi")
+    if not exe:
+        return None
+    samples, stop = [], threading.Event()
+
+    def sampler():
+        time.sleep(0.5)
+        while not stop.is_set():
+            try:
+                out = subprocess.run([exe, "metric", "-p", "-c", "--csv"], capture_output=True,
+                                     text=True, timeout=10).stdout
+                lines = [ln for ln in out.splitlines() if ln.strip()]
+                rec = dict(zip(lines[0].split(","), lines[1].split(",")))
+                clks = [float(rec[f"gfx_{x}_clk"]) for x in range(8) if f"gfx_{x}_clk" in rec]
+                samples.append((float(rec["socket_power"]), sum(clks) / len(clks)))
+            except (OSError, ValueError, KeyError, IndexError, ZeroDivisionError,
+                    subprocess.SubprocessError):
+                pass
+            time.sleep(0.2)
+
+    th = threading.Thread(target=sampler)
+    th.start()
+    t0, i = time.perf_counter(), 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(50):
+            step_fn(i)
+            i += 1
+        torch.cuda.synchronize()
+    stop.set()
+    th.join()
+    if not samples:
+        return None
+    w, mhz = np.median(np.array(samples), axis=0)
+    return {"socket_w": float(w), "gfx_mhz": float(mhz), "samples": len(samples),
+            "loop_s": seconds, "source": "amd-smi metric -p -c (socket power, mean of the XCD clocks)"}
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -427,6 +472,13 @@ def main():
                       "head_hbm_frac": (HEAD_BYTES + 64 * D * 2 + 64 * V * 4) / kh / PEAK_HBM,
                       "head_mfma_frac": 2.0 * 64 * V * D / kh / PEAK_BF16}
 
+    # socket power and clocks while config 2 (and the config-5 step) run back to back: both
+    # reach the part's socket power limit, and the clocks they run at are reported beside them
+    power = {"config2": power_during(torch, 3.0, step2)}
+    if 5 in cfgs:
+        power["config5"] = power_during(torch, 3.0, step5)
+    log(f"power: {power}")
+
     # the practical ceiling: a pure-read probe over the same 792 MB buffer (no arithmetic), the
     # best of several wave counts (more, shorter stripes read faster: 7.16 TB/s at 65536 waves
     # against 7.10 at 32768 in one sweep)
@@ -481,6 +533,7 @@ def main():
                      "bytes_per_launch": bytes2,
                      "read_ceiling": ceiling},
         "cpu_baseline": cpu,
+        "power": power,
         "configs": {str(k): results[k] for k in sorted(results)},
     }
     print(json.dumps(line), flush=True)
