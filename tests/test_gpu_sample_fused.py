@@ -1,6 +1,7 @@
 """The fused sample pass of the LM head (rows <= 4): softcap and repetition penalty in the head's
 epilogue, per-block selection statistics, then one merge launch that reads only the blocks able
-to hold a top-`want` entry. Every token is compared bit-exactly with the oracle's
+to hold a top-`want` entry; and head.sample past 4 rows (logits pass, then the selection over the
+logits in memory). Every token is compared bit-exactly with the oracle's
 apply_repetition_penalty + sample_token (sampling.cpp:74-169) on the GPU's own raw logits, and
 the penalised rows bit for bit. The cases reach every branch of the merge: survivors ranked by
 counting (few), by the binned top-`want` (up to 2048), by a radix select over the candidate blocks
@@ -155,3 +156,26 @@ def test_fused_degenerate_row(env, oracle, full_head):
     params = [t.RowParams(0.7, 0.9, 40, 1.0, 0.5, CAP, 0, 0), t.RowParams(0.7, 0.9, 40, 1.0, 0.5, CAP, 0, 0)]
     tok = run_and_check(env, oracle, full_head, hb, params, np.zeros(0, np.uint32), "nan row")
     assert tok[1] == t.TOKEN_DEGENERATE and tok[0] != t.TOKEN_DEGENERATE
+
+
+@pytest.mark.parametrize("M", [9, 20, 40, 64])
+def test_sample_rows_past_the_fused_pass(env, oracle, M):
+    # head.sample with more than 4 rows: the logits pass (the staged 16x16 kernel at 9 rows, the
+    # 32x32 kernel with one m tile at 20 and two at 40 and 64), then the penalty and the
+    # wave-record selection over the logits in memory; per-row parameters and histories
+    torch, dev, t = env
+    V, d = 3000, 640
+    W, S, B = oracle.gen_lm_head(750 + M, V, d)
+    head = t.LMHead(torch.from_numpy(wsb_bytes(W, S, B)).to(dev), V, d, CAP)
+    rng = np.random.default_rng(M)
+    hists, params, off = [], [], 0
+    for m in range(M):
+        n = int(rng.integers(0, 400))
+        hists.append(rng.integers(0, V + 10, n).astype(np.uint32))
+        T = 0.0 if m % 7 == 3 else float(rng.uniform(0.5, 1.2))
+        params.append(t.RowParams(T, float(rng.uniform(0.8, 0.98)), int(rng.integers(20, 101)),
+                                  1.0 if m % 5 == 1 else 1.1, float(rng.uniform()), CAP, off, n))
+        off += n
+    hist = np.concatenate(hists)
+    run_and_check(env, oracle, head, hidden_bf16(760 + M, M, d), params, hist, f"M={M}")
+    head.close()
