@@ -103,12 +103,21 @@ __global__ __launch_bounds__(kDraftThreads) void draft_exp_kernel(DraftArgs a) {
     const uint32_t r = blockIdx.y;
     const float* l = draft_row(a, r);
     // the row maximum; max over the partial maxima equals the reference's running '>' maximum
-    // (both ignore NaN, start from -1e9f, and equal values are interchangeable)
+    // (both ignore NaN, start from -1e9f, and equal values are interchangeable). The partial
+    // maxima are requested at once, one per thread, then reduced over the block: none is NaN,
+    // so the order of the comparisons does not matter.
+    __shared__ float red[kDraftThreads / 64];
     float mx = -1e9f;
-    for (uint32_t p = 0; p < a.parts; ++p) {
+    for (uint32_t p = threadIdx.x; p < a.parts; p += kDraftThreads) {
         const float y = a.part[r * a.parts + p];
         mx = y > mx ? y : mx;
     }
+    mx = wave_reduce(mx, -1e9f, [](float u, float v) { return v > u ? v : u; });
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = red[0];
+#pragma unroll
+    for (int w = 1; w < kDraftThreads / 64; ++w) mx = red[w] > mx ? red[w] : mx;
     const uint32_t base = blockIdx.x * kDraftChunk + threadIdx.x;
     bool nan = false;
     float* e = a.e + static_cast<size_t>(r) * a.estride;
