@@ -393,12 +393,13 @@ __device__ __forceinline__ void block_sort_desc(SelCommon& c, uint32_t n) {
 // running sums acc_i of q (stored back), lane 1 the top-p running sum, kChunk terms at a time,
 // until lane 1's sum reaches p (the cut). denom is acc at the cut (the additions of the
 // reference's denom loop), and the draw -- the first i < cut with acc_i >= u * denom, else
-// cut - 1 -- is a ballot over the stored sums in wave 0. Needs want <= blockDim.x. The id is
-// returned to the threads of wave 0 (callers store it from thread 0).
-__device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, const twd_row_params& p) {
+// cut - 1 -- is a ballot over the stored sums in wave 0. Needs want <= blockDim.x. gmax and total
+// are the row's maximum and sum of exponentials, the same in every thread. The id is returned to
+// the threads of wave 0 (callers store it from thread 0).
+__device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, const twd_row_params& p,
+                                                   float gmax, double total) {
     const int tid = threadIdx.x, lane = tid & 63;
-    const double mx = static_cast<double>(c.gmax);
-    const double total = c.total;
+    const double mx = static_cast<double>(gmax);
     const double td = static_cast<double>(p.temperature);
     if (static_cast<uint32_t>(tid) < want) {
         const double l = static_cast<double>(rank_value(c.sorted[tid]));
@@ -416,10 +417,17 @@ __device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, 
         // (unused) over e, so that no store needs a branch
         double* src = lane == 0 ? c.q : c.e;
         double run = 0.0;
-        for (uint32_t i0 = 0; i0 < want; i0 += kChunk) {
-            double x[kChunk], pre[kChunk];
+        double x[kChunk];
 #pragma unroll
-            for (uint32_t j = 0; j < kChunk; ++j) x[j] = src[min(i0 + j, want - 1)];
+        for (uint32_t j = 0; j < kChunk; ++j) x[j] = src[min(j, want - 1)];
+        for (uint32_t i0 = 0; i0 < want; i0 += kChunk) {
+            // the next chunk's terms are read before this chunk's sums are stored: they lie at
+            // i0 + kChunk or later (want - 1 >= i0 + kChunk when there is a next chunk)
+            double xn[kChunk], pre[kChunk];
+            if (i0 + kChunk < want) {
+#pragma unroll
+                for (uint32_t j = 0; j < kChunk; ++j) xn[j] = src[min(i0 + kChunk + j, want - 1)];
+            }
 #pragma unroll
             for (uint32_t j = 0; j < kChunk; ++j) {
                 run += x[j];
@@ -438,6 +446,8 @@ __device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, 
                 cut = i0 + static_cast<uint32_t>(__builtin_ctz(h1)) + 1;
                 break;
             }
+#pragma unroll
+            for (uint32_t j = 0; j < kChunk; ++j) x[j] = xn[j];
         }
     }
     cut = __builtin_amdgcn_readfirstlane(cut);
@@ -466,7 +476,7 @@ __device__ __forceinline__ void finish_row(SelCommon& c, uint32_t want, const tw
         return;
     }
     block_sort_desc(c, want);
-    const uint32_t tok = finish_sampled(c, want, p);
+    const uint32_t tok = finish_sampled(c, want, p, c.gmax, c.total);
     if (tid == 0) *token_out = tok;
 }
 
@@ -794,6 +804,8 @@ __global__ __launch_bounds__(kSmThreads) void select_sample_merge_kernel(SelectA
     const size_t o = static_cast<size_t>(row) * W;
     const float* lg = b.logits + static_cast<size_t>(row) * b.stride;
 
+    // the exp2 table first, so that its load overlaps the records' (the first barrier publishes it)
+    if (tid < 64) sh.c.exp2_tbl[tid] = kExp2Table[tid];
     // ---- the wave records, one round trip: thread tid holds waves tid + NT * q
     uint64_t key[kSmPer];
     double wsum[kSmPer];
@@ -822,8 +834,11 @@ __global__ __launch_bounds__(kSmThreads) void select_sample_merge_kernel(SelectA
         gm = fmaxf(gm, wm[q]);
         if (key[q] != 0 && __builtin_isfinite(wm[q])) mn = fminf(mn, wm[q]);
     }
-    if (tid < 64) sh.c.exp2_tbl[tid] = kExp2Table[tid];
     block_stats<NT>(flag, gm, mn, sh.c);  // NaN seen, row max, smallest finite wave max
+    if (flag != 0) {  // sampling.cpp:116-118: a NaN term makes the total NaN
+        if (tid == 0) b.tokens[row] = TWD_TOKEN_DEGENERATE;
+        return;
+    }
     double part = 0.0;
 #pragma unroll
     for (uint32_t q = 0; q < kSmPer; ++q)
@@ -832,11 +847,9 @@ __global__ __launch_bounds__(kSmThreads) void select_sample_merge_kernel(SelectA
             const double x = static_cast<double>(wm[q]) - static_cast<double>(gm);
             part += wsum[q] * (x >= -700.0 ? exp_core(x, sh.c.exp2_tbl) : exp_for_sum(x, sh.c.exp2_tbl));
         }
-    const double total = block_sum_f64<NT>(part, sh.c);
-    if (flag != 0 || !(total > 0.0)) {  // sampling.cpp:116-118
-        if (tid == 0) b.tokens[row] = TWD_TOKEN_DEGENERATE;
-        return;
-    }
+    // the waves' partial sums cross the histogram's barrier below (block_sum_f64's order)
+    part = wave_reduce(part, 0.0, [](double u, double v) { return u + v; });
+    if (lane == 0) sh.c.redd[wave] = part;
     const uint32_t want = (p.top_k > 0) ? min(static_cast<uint32_t>(p.top_k), b.vocab)
                                         : min(kMaxWant, b.vocab);
 
@@ -853,6 +866,13 @@ __global__ __launch_bounds__(kSmThreads) void select_sample_merge_kernel(SelectA
     for (uint32_t q = 0; q < kSmPer; ++q)
         if (key[q] != 0) atomicAdd(&sh.t.hist[bin_of(wm[q]) * kReps + (lane & (kReps - 1))], 1u);
     __syncthreads();
+    double total = 0.0;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) total += sh.c.redd[w];
+    if (!(total > 0.0)) {  // sampling.cpp:116-118 (uniform: every thread sums the same values)
+        if (tid == 0) b.tokens[row] = TWD_TOKEN_DEGENERATE;
+        return;
+    }
     if (wave == 0) {  // lane l owns bins 4l .. 4l + 3
         uint32_t cc[4], tsum = 0;
         const u32x4* h4 = reinterpret_cast<const u32x4*>(sh.t.hist) + lane * (4 * kReps / 4);
@@ -943,10 +963,13 @@ __global__ __launch_bounds__(kSmThreads) void select_sample_merge_kernel(SelectA
             wave_put(keep, keep ? rank_key(v[q], r[q]) : 0ull, &sh.c.misc[4], sh.cand, kSmCap);
         }
     }
-    uint32_t no_flag = 0;
-    float no_max = -INFINITY;
-    block_stats<NT>(no_flag, no_max, smn, sh.c);  // the survivors' smallest finite value
-    const uint32_t n = sh.c.misc[4];              // may exceed kSmCap: then only counted
+    __syncthreads();                  // the survivors are listed
+    const uint32_t n = sh.c.misc[4];  // may exceed kSmCap: then only counted
+    if (n > static_cast<uint32_t>(NT)) {  // block_top needs the survivors' smallest finite value
+        uint32_t no_flag = 0;
+        float no_max = -INFINITY;
+        block_stats<NT>(no_flag, no_max, smn, sh.c);
+    }
 
     // ---- the shortlist, sorted (value desc, index asc)
     if (n <= static_cast<uint32_t>(NT)) {
@@ -989,12 +1012,7 @@ __global__ __launch_bounds__(kSmThreads) void select_sample_merge_kernel(SelectA
         __syncthreads();
         block_sort_desc(sh.c, want);
     }
-    if (tid == 0) {
-        sh.c.gmax = gm;
-        sh.c.total = total;
-    }
-    __syncthreads();
-    const uint32_t tok = finish_sampled(sh.c, want, p);
+    const uint32_t tok = finish_sampled(sh.c, want, p, gm, total);
     if (tid == 0) b.tokens[row] = tok;
 }
 
