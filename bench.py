@@ -1,6 +1,7 @@
 """LM-head + token-selection throughput on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--configs 1,2,3,4,5]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-power]
+                    [--configs 1,2,3,4,5]
 
 Headline (`value`): BASELINE config 2 -- the INT4 g64 LM head at M=1 (V=262144, d=5376, bf16 h)
 with the softcap and greedy argmax fused, rows/s with every input already resident in HBM.
@@ -270,6 +271,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--configs", default="1,2,3,4,5")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-power", action="store_true",
+                    help="skip the amd-smi power sampling (needed under a profiler whose preloaded "
+                         "library initialises the GPU in child processes as well)")
     ap.add_argument("--cpu-rows", type=int, default=3,
                     help="full rows of config 2 in the CPU baseline (each about 1.7 s; the other "
                          "configs add about 15 s)")
@@ -474,9 +478,11 @@ def main():
 
     # socket power and clocks while config 2 (and the config-5 step) run back to back: both
     # reach the part's socket power limit, and the clocks they run at are reported beside them
-    power = {"config2": power_during(torch, 3.0, step2)}
-    if 5 in cfgs:
-        power["config5"] = power_during(torch, 3.0, step5)
+    power = {}
+    if not args.no_power:
+        power["config2"] = power_during(torch, 3.0, step2)
+        if 5 in cfgs:
+            power["config5"] = power_during(torch, 3.0, step5)
     log(f"power: {power}")
 
     # the practical ceiling: a pure-read probe over the same 792 MB buffer (no arithmetic), the
