@@ -1021,9 +1021,10 @@ __global__ __launch_bounds__(kSmThreads) void select_sample_merge_kernel(SelectA
 // Rows whose logits the caller holds (twd_select, the head for rows > 4) reach
 // select_sample_merge_kernel through two short passes instead of the slice kernels:
 //   * penalty_hash_kernel, one block per row: the row's history ids into an LDS hash table of
-//     (id, occurrences), then each distinct id's logit gets the penalty once per occurrence, one
-//     after another as the reference loop applies them (sampling.cpp:74-90); only those entries
-//     are read and written;
+//     (id, occurrences) while each id's logit is requested, then each distinct id's logit gets
+//     the penalty once per occurrence, one after another as the reference loop applies them
+//     (sampling.cpp:74-90), from the thread that entered the id; only those entries are read
+//     and written;
 //   * wave_stats_kernel: per 64 entries of a row, the record the head's sample mode publishes
 //     -- the best rank (value desc, index asc) and the sum of exp(v - that value) in double,
 //     NaN when a NaN was seen. Eight lanes hold one record's 64 entries, eight each.
@@ -1069,10 +1070,18 @@ __global__ __launch_bounds__(kPhThreads) void penalty_hash_kernel(SelectArgs arg
         keys[tid + NT * q] = kHashEmpty;
         cnt[tid + NT * q] = 0;
     }
+    // each id's logit, requested now so that its round trip overlaps the table's construction
+    // (only the thread that enters an id into the table uses it)
+    float* lg = b.logits + static_cast<size_t>(row) * b.stride;
+    float x[kIdsPer];
+#pragma unroll
+    for (uint32_t q = 0; q < kIdsPer; ++q) x[q] = lg[ids[q] < b.vocab ? ids[q] : 0u];  // no branch per load
     __syncthreads();
+    uint32_t slot[kIdsPer];  // the slot this thread entered id q into, or kHashEmpty
 #pragma unroll
     for (uint32_t q = 0; q < kIdsPer; ++q) {
         const uint32_t id = ids[q];
+        slot[q] = kHashEmpty;
         if (id >= b.vocab) continue;  // out-of-range ids are ignored (sampling.cpp:82)
         // linear probing from a multiplicative hash; the table is at most half full, so a free
         // or matching slot is always found
@@ -1081,34 +1090,26 @@ __global__ __launch_bounds__(kPhThreads) void penalty_hash_kernel(SelectArgs arg
             const uint32_t prev = atomicCAS(&keys[h], kHashEmpty, id);
             if (prev == kHashEmpty || prev == id) {
                 atomicAdd(&cnt[h], 1u);
+                if (prev == kHashEmpty) slot[q] = h;
                 break;
             }
             h = (h + 1) & (kHashSlots - 1);
         }
     }
     __syncthreads();
-    float* lg = b.logits + static_cast<size_t>(row) * b.stride;
     const float rp = p.repetition_penalty;
     const float limit = (p.softcap > 0.0f) ? p.softcap * 0.9999f : 0.0f;
-    // each distinct id: its logit (all of this thread's requested at once), the penalty once
-    // per occurrence, the store
-    uint32_t id[kSlotsPer], n[kSlotsPer];
-    float x[kSlotsPer];
+    // each distinct id, by the thread that entered it: the penalty once per occurrence, the store
 #pragma unroll
-    for (uint32_t q = 0; q < kSlotsPer; ++q) {
-        id[q] = keys[tid + NT * q];
-        n[q] = cnt[tid + NT * q];
-        x[q] = lg[id[q] != kHashEmpty ? id[q] : 0u];  // unconditional: no branch per load
-    }
-#pragma unroll
-    for (uint32_t q = 0; q < kSlotsPer; ++q) {
-        if (id[q] == kHashEmpty) continue;
+    for (uint32_t q = 0; q < kIdsPer; ++q) {
+        if (slot[q] == kHashEmpty) continue;
+        const uint32_t n = cnt[slot[q]];
         float v = x[q];
-        for (uint32_t t = 0; t < n[q]; ++t) {
+        for (uint32_t t = 0; t < n; ++t) {
             v = (v > 0.0f) ? (v / rp) : (v * rp);
             if (limit > 0.0f) v = (v < -limit) ? -limit : ((limit < v) ? limit : v);
         }
-        lg[id[q]] = v;
+        lg[ids[q]] = v;
     }
 }
 
