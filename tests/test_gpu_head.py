@@ -95,6 +95,66 @@ def test_logits_parity_odd_and_short_depth(torch_dev, oracle, d, M):
     assert ratio <= 1.0
 
 
+@pytest.mark.parametrize("M", [1, 5, 12, 20, 64])
+def test_power_of_two_scaling_is_exact(torch_dev, oracle, M):
+    # with no softcap the logits are linear in h, and every kernel's arithmetic (the -h/128
+    # entries, the MFMA products and fp32 sums, the exact bf16 slices of the group sums) commutes
+    # with a power-of-two scaling of h: h * 2^k must give the logits * 2^k bit for bit
+    V, d = 500, 640
+    W, S, B = oracle.gen_lm_head(900 + M, V, d)
+    head = make_head(torch_dev, W, S, B, V, d, 0.0)
+    hb = hidden_bf16(901 + M, M, d)
+    base = head.logits(to_dev_bf16(torch_dev, hb)).cpu().numpy()
+    for k in (90, -90, 7):
+        hk = bf16_rne(np.ldexp(bf16_to_f32(hb), k))  # exact: no bf16 overflow or underflow here
+        assert np.array_equal(np.ldexp(bf16_to_f32(hk), -k), bf16_to_f32(hb))
+        got = head.logits(to_dev_bf16(torch_dev, hk)).cpu().numpy()
+        assert np.array_equal(got, np.ldexp(base, k).astype(np.float32)), (M, k)
+
+
+@pytest.mark.parametrize("M,rows", [(20, "hard"), (40, "hard"), (33, "moderate"), (64, "moderate")])
+def test_wide_kernel_hard_rows(torch_dev, oracle, M, rows):
+    # the 17..64-row kernel on rows far from N(0,1). "hard": magnitudes spanning many binades
+    # (outliers up to 5e3, lognormal sigma 3); "moderate": heavy tails (student-t(3), lognormal
+    # sigma 1, uniform, one x30 entry per 128 columns). Both with rows of tiny values near the
+    # bf16 normal range, a zero row, a zero chunk and a tiny chunk.
+    V, d = 700, 1280
+    W, S, B = oracle.gen_lm_head(950 + M, V, d)
+    head = make_head(torch_dev, W, S, B, V, d, CAP)
+    rng = np.random.default_rng(951 + M)
+    x = rng.standard_normal((M, d)).astype(np.float32)
+    if rows == "hard":
+        x[0, rng.integers(0, d, 6)] = [300.0, -250.0, 1e3, -1e3, 5e3, 64.0]       # outliers
+        x[1] *= np.exp(3.0 * rng.standard_normal(d)).astype(np.float32)           # lognormal
+    else:
+        x[0] = rng.standard_t(3, d)
+        x[1] *= np.exp(rng.standard_normal(d)).astype(np.float32)
+        x[6] = rng.uniform(-1, 1, d)
+        x[7, ::128] *= 30.0
+    x[2] = np.ldexp(x[2], -115)                                                    # tiny
+    x[3] = 0.0                                                                     # zero row
+    x[4, :128] = 0.0                                                               # a zero chunk
+    x[5, 128:256] = np.ldexp(x[5, 128:256], -60)                                  # a tiny chunk
+    hb = bf16_rne(x)
+    got = head.logits(to_dev_bf16(torch_dev, hb)).cpu().numpy()
+    want = oracle_rows(oracle, W, S, B, hb, CAP)
+    # fp32 sums in any two orders differ by up to a small multiple of 2^-24 sum |w h|; rows whose
+    # terms reach 1e4 (lognormal sigma 3) make that more than the 1e-3 tolerance, so the allowance
+    # per logit adds 2^-16 sum_c |w_rc h_c| (negligible for the other rows)
+    c = np.arange(d)
+    q = ((W[:, c // 8] >> (4 * (c % 8)).astype(np.uint32)) & 15).astype(np.float64)
+    w = q * bf16_to_f32(S[:, c // 64]).astype(np.float64) + bf16_to_f32(B[:, c // 64]).astype(np.float64)
+    absdot = np.abs(bf16_to_f32(hb).astype(np.float64)) @ np.abs(w).T  # [M, V]
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    allow = 1e-3 + 1e-3 * np.abs(want.astype(np.float64)) + 2.0**-16 * absdot
+    ratio = err / allow
+    i = int(np.argmax(ratio))
+    print(f"M={M} {rows} max|err|={err.max():.3e} worst allowance ratio {ratio.max():.3f} at row {i // V}")
+    assert ratio.max() <= 1.0
+    # a zero row gives zero logits: every term, biases included, has a zero factor
+    assert np.array_equal(got[3], np.zeros(V, np.float32))
+
+
 def _reference_test_weights(rows, d, seed):
     # the value ranges of tests/test_gpu_kernels.cpp:272-275 and :532-535
     rng = np.random.default_rng(seed)

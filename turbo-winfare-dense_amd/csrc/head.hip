@@ -166,19 +166,17 @@ __device__ __forceinline__ float sum8_bf16(u32x4_t v) {
 //   A fragment, lane (row m, k-group kg): dword c = slice kg of X[m][4P + c], duplicated into
 //     a bf16 pair, with X = hi + mid + lo (slices kg = 0, 1, 2; slice 3 is zero).
 // Summed over k that is sum_c X_c * (b_c + t_c) = sum_c X_c * (b_c - 128 s_c).
-// bias_slices writes the four slice dwords of one (m, group) entry; at(kg) addresses them. Each
-// slice pairs with b (low half) and, with_t, also with t (high half).
+// bias_slices writes the four slice dwords of one (m, group) entry; at(kg) addresses them.
 template <typename At>
-__device__ __forceinline__ void bias_slices(float x, At at, bool with_t = true) {
+__device__ __forceinline__ void bias_slices(float x, At at) {
     const uint32_t hi = f32_to_bf16_rne(x);
     const float r1 = x - __uint_as_float(hi << 16);  // exact
     const uint32_t mid = f32_to_bf16_rne(r1);
     const float r2 = r1 - __uint_as_float(mid << 16);  // exact
     const uint32_t lo = f32_to_bf16_rne(r2);
-    const uint32_t pair = with_t ? 0x10001u : 1u;
-    *at(0) = hi * pair;
-    *at(1) = mid * pair;
-    *at(2) = lo * pair;
+    *at(0) = hi * 0x10001u;
+    *at(1) = mid * 0x10001u;
+    *at(2) = lo * 0x10001u;
     *at(3) = 0u;
 }
 
@@ -1075,161 +1073,51 @@ void head_wide_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_t*
     head_epilogue<NMT, 4, RT, MODE>(a, tot, tile0, se);
 }
 
-// ---- 17 <= M <= 64: scaled 32x32x64 fp8 MFMAs, weights and h streamed into LDS ---------------
+// ---- 33 <= M <= 64: 32x32x16 MFMAs, weights and h streamed into LDS two chunks ahead ----------
 //
-// The weights enter the MFMA as e4m3 bytes without any arithmetic: the byte 0x0q of a nibble q
-// (0..15) is the e4m3 encoding (exponent bias 7) of q * 2^-9 -- codes 0..7 are the subnormals
-// m * 2^-9, codes 8..15 the normals (8 + m) * 2^-9. A word's nibbles become two dwords of bytes,
-// w & 0x0F0F0F0F (nibbles 0, 2, 4, 6) and (w >> 4) & 0x0F0F0F0F (1, 3, 5, 7), three VALU
-// operations per eight weights. The scaled MFMA's B scale 2^2 makes them q / 128.
-//
-// h is exact in two e4m3 pieces: per row and 128-column chunk, piece 1 is -h rounded to four
-// significant bits under a power-of-two scale that puts the chunk's largest |h| in [128, 256),
-// and piece 2 the remainder (a bf16 value minus its four-bit rounding has at most four
-// significant bits) under its own such scale. The two scales are the MFMA's per-lane A scales
-// (E8M0, byte 0 of a dword). Only entries below 2^-9 of a piece's scaled range lose bits, and
-// such entries are 2^-14 or less of the chunk's largest. So per group and m tile the MFMAs
-// give acc = -sum q h / 128, the same quantity as the 16 x 16 kernels' (128 + q)(-h / 128) chain
-// minus its -sum h term; tot += t acc with t = -128 s adds s sum q h, and the bias MFMA adds
-// b X alone (its A entries pair X with b and zero with t).
-//
-// Lane l = 32 kh + n of the MFMA carries B column n (a vocabulary row of the wave's tile pair:
-// tile n / 16, row n % 16) and k half kh. For group g (64 columns) it takes four nibble words
-// of row n, word s = 0..3 being the unit's lane 16 kg + n % 16, kg = kh for s = 0, 1 and kh + 2
-// for s = 2, 3, word 2 g + (s & 1): columns 64 g + {0, 32, 16, 48}[s] + 8 kh + 0..7. B dword 2 s
-// + e holds, in byte b, column 64 g + {0, 32, 16, 48}[s] + 8 kh + 2 b + e; A dword 2 s + e of
-// lane 32 kh + i holds the same column of h row i. (The MFMA pairs A and B entries by lane half
-// and register position, so this is all the layout has to agree on.)
-// prep_hidden32_kernel writes hp[U][mt][g][piece][half][lane] (16 B each: dwords 4 half ..
-// 4 half + 3 of the lane; rows >= M zero), hs[U][lane] (dword 2 mt + piece: the E8M0 scale of row
-// 32 mt + l % 32 in chunk U) and hx[P][mt][f][lane], whose dword c holds, in its low half, slice
-// 2 f + l / 32 (hi, mid, lo, zero) of X[32 mt + l % 32][4 P + c] and zero in its high half. The
-// group sums X are taken in the order of prep_hidden_kernel: eight-column pieces summed in
-// column order, then a three-level pairwise tree over the pieces.
+// Lane l = 32 kh + n of a 32 x 32 x 16 MFMA carries B column n (a vocabulary row of the wave's
+// tile pair: tile n / 16, row n % 16) and k half kh. For k-step s of group g (64 columns) it
+// takes one nibble word of row n: the unit's lane 16 kg + n % 16, kg = kh for s = 0, 1 and
+// kh + 2 for s = 2, 3, word 2 g + (s & 1), i.e. columns 64 g + {0, 32, 16, 48}[s] + 8 kh + 0..7.
+// prep_hidden32_kernel lays the A entries (h rows) out in the same column order:
+// hp[U][mt][g][s][lane] is prep_h of h[32 mt + l % 32][128 U + 64 g + koff[s] + 8 (l / 32) ..+8]
+// (rows >= M zero), and hx[P][mt][f][lane] holds, in dword c, slice 2 f + l / 32 (hi, mid, lo,
+// zero) of X[32 mt + l % 32][4 P + c] duplicated into a bf16 pair. The group sums X are taken in
+// the order of prep_hidden_kernel: eight-column pieces summed in column order, then a
+// three-level pairwise tree over the pieces.
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef int i32x8_t __attribute__((ext_vector_type(8)));
-
-// y (finite, |y| < 256) rounded to nearest-even e4m3: the code, and the value it stands for.
-__device__ __forceinline__ uint32_t e4m3_rn(float y, float& val) {
-    const uint32_t sign = (__float_as_uint(y) >> 24) & 0x80u;
-    const float a = fabsf(y);
-    uint32_t code;
-    float v;
-    if (a < 0x1p-6f) {  // the subnormal grid, 2^-9 (zero included); 8 * 2^-9 is the first normal
-        const float q = rintf(a * 512.0f);
-        code = static_cast<uint32_t>(q);
-        v = q * 0x1p-9f;
-    } else {
-        const int E = static_cast<int>((__float_as_uint(a) >> 23) & 0xFFu) - 127;  // -6 .. 7
-        const float q = rintf(ldexpf(a, 3 - E));                                     // 8 .. 16
-        code = static_cast<uint32_t>((E + 7) << 3) + static_cast<uint32_t>(q) - 8u;  // 16 carries
-        v = ldexpf(q, E - 3);
-    }
-    val = sign ? -v : v;
-    return sign | code;
-}
-
-// The power-of-two scale exponent sigma with mx * 2^sigma in [128, 256), clamped so that the
-// MFMA's E8M0 scale 127 - sigma stays in 0..254; 0 for mx == 0.
-__device__ __forceinline__ int piece_sigma(float mx) {
-    if (!(mx > 0.0f)) return 0;
-    const int e = static_cast<int>((__float_as_uint(mx) >> 23) & 0xFFu) - 127;  // mx is a normal
-    const int sg = 7 - (e < -126 ? -126 : e);  // fp32 subnormal maxima take the smallest exponent
-    return sg > 127 ? 127 : sg;
-}
 
 template <int NM>
 __global__ __launch_bounds__(kHeadThreads) void prep_hidden32_kernel(const uint16_t* __restrict__ h,
                                                                      uint32_t M, uint32_t d,
                                                                      u32x4_t* __restrict__ hp,
-                                                                     uint32_t* __restrict__ hs,
                                                                      u32x4_t* __restrict__ hx) {
-    // task [U][mt][row i][piece p]: the 8 columns 128 U + 8 p of row 32 mt + i; the 16 pieces of
-    // a (row, chunk) are consecutive lanes
-    constexpr uint32_t per_chunk = NM * 512;
+    constexpr uint32_t per_chunk = NM * 512;  // tasks per chunk: [mt][g][row i][piece p]
     const uint32_t nunits = d / kChunkK;
     const uint32_t padded = nunits + (nunits & 1);
     const uint32_t task = blockIdx.x * kHeadThreads + threadIdx.x;  // grid covers padded chunks
     const uint32_t U = task / per_chunk, rem = task % per_chunk;
-    const uint32_t p = rem & 15, i = (rem >> 4) & 31, mt = rem >> 9;
+    const uint32_t p = rem & 7, i = (rem >> 3) & 31, g = (rem >> 8) & 1, mt = rem >> 9;
     const uint32_t m = 32 * mt + i;
     u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
     if (U < nunits && m < M)
-        v = *reinterpret_cast<const u32x4_t*>(h + static_cast<size_t>(m) * d + U * kChunkK + p * 8);
-    // the group sum for the bias: pieces in column order, then the pairwise tree over the group
+        v = *reinterpret_cast<const u32x4_t*>(h + static_cast<size_t>(m) * d + U * kChunkK + g * kGroup + p * 8);
     float s = sum8_bf16(v);
     s += __shfl_xor(s, 1);
     s += __shfl_xor(s, 2);
     s += __shfl_xor(s, 4);
-    const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
-    float y[8];
-    float mx = 0.0f;
-    bool bad = false;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const uint32_t b16 = (j & 1) ? (wv[j >> 1] >> 16) : (wv[j >> 1] & 0xFFFFu);
-        y[j] = -__uint_as_float(b16 << 16);
-        bad |= !__builtin_isfinite(y[j]);
-        mx = fmaxf(mx, fabsf(y[j]));
-    }
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-        mx = fmaxf(mx, __shfl_xor(mx, o));
-        bad |= __shfl_xor(static_cast<int>(bad), o) != 0;
-    }
-    // piece 1, the remainders, piece 2
-    const int sg1 = piece_sigma(mx);
-    uint32_t c1[8], c2[8];
-    float r[8];
-    float mx2 = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        float val;
-        c1[j] = e4m3_rn(ldexpf(y[j], sg1), val);
-        r[j] = y[j] - ldexpf(val, -sg1);  // exact
-        mx2 = fmaxf(mx2, fabsf(r[j]));
-    }
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) mx2 = fmaxf(mx2, __shfl_xor(mx2, o));
-    const int sg2 = piece_sigma(mx2);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        float val;
-        c2[j] = e4m3_rn(ldexpf(r[j], sg2), val);
-    }
     if (U < padded) {
-        // piece p: group g = p / 8; within the group columns 8 (p % 8) + t sit in word s =
-        // {0, 0, 2, 2, 1, 1, 3, 3}[p % 8] of k half kh = p % 2, t = 2 b + e
-        const uint32_t g = p >> 3, q8 = p & 7;
-        const uint32_t sw = (q8 >> 1) == 1 ? 2u : (q8 >> 1) == 2 ? 1u : (q8 >> 1);
-        const uint32_t kh = q8 & 1, half = sw >> 1, dw = (sw & 1) * 2;
-        const uint32_t lane = 32 * kh + i;
-#pragma unroll
-        for (int pc = 0; pc < 2; ++pc) {
-            const uint32_t* c = pc == 0 ? c1 : c2;
-            uint32_t lo = c[0] | (c[2] << 8) | (c[4] << 16) | (c[6] << 24);
-            uint32_t hi = c[1] | (c[3] << 8) | (c[5] << 16) | (c[7] << 24);
-            if (bad) lo = hi = 0x7F7F7F7Fu;  // a non-finite entry: the chunk's products are NaN
-            uint32_t* o = reinterpret_cast<uint32_t*>(
-                hp + (((((static_cast<size_t>(U) * NM + mt) * 2 + g) * 2 + pc) * 2 + half) * 64 + lane));
-            *reinterpret_cast<u32x2_t*>(o + dw) = u32x2_t{lo, hi};
-        }
+        // piece p holds columns 8 p of the group: k-step {0, 2, 1, 3}[p / 2], k half p % 2
+        const uint32_t ks = ((p >> 1) == 1) ? 2u : ((p >> 1) == 2) ? 1u : (p >> 1);
+        hp[(((static_cast<size_t>(U) * NM + mt) * 2 + g) * 4 + ks) * 64 + (p & 1) * 32 + i] = prep_h(v);
         if (p == 0) {
-            const uint32_t S1 = static_cast<uint32_t>(127 - sg1), S2 = static_cast<uint32_t>(127 - sg2);
-            uint32_t* sc = hs + static_cast<size_t>(U) * 256;
-            sc[i * 4 + 2 * mt] = S1;
-            sc[i * 4 + 2 * mt + 1] = S2;
-            sc[(32 + i) * 4 + 2 * mt] = S1;
-            sc[(32 + i) * 4 + 2 * mt + 1] = S2;
-        }
-        if (q8 == 0) {
             const uint32_t G = 2 * U + g;
             uint32_t* x = reinterpret_cast<uint32_t*>(hx);
             auto at = [&](int sl) {
                 return x + ((((static_cast<size_t>(G >> 2) * NM + mt) * 2 + (sl >> 1)) * 64 + (sl & 1) * 32 + i) * 4 +
                             (G & 3));
             };
-            bias_slices(s, at, false);  // zero slices for the padding chunk's two groups
+            bias_slices(s, at);  // zero slices for the padding chunk's two groups
         }
     }
 }
@@ -1287,19 +1175,17 @@ __device__ __forceinline__ void head_epilogue32(const HeadArgs& a, f32x16_t (&to
 // T0 + 2 p + 1, T0 = 2 NP (blockIdx.x * NW + w)) and all rows as NM m tiles of 32. Every
 // vector-memory access of the streaming loop is a DMA into LDS: the wave's own weights (per pair
 // and chunk, two 16 B nibble vectors and one scale dword per lane) two chunks ahead into a
-// private two-slot ring, and the block's share of the prepared h pieces and their scales (with
-// each even chunk also the super-unit's bias entries) one chunk ahead into a two-slot ring -- h
-// comes from L2, the weights from HBM. At 78 KB two blocks share a CU, so one block's epilogue
-// and pipeline fill overlap the other's stream. A stage (one chunk, two groups):
+// private two-slot ring, and the block's share of the prepared h (with each even chunk also the
+// super-unit's bias entries) one chunk ahead into a two-slot ring -- h comes from L2, the weights
+// from HBM. At 79 KB two blocks share a CU, so one block's epilogue and pipeline fill overlap the
+// other's stream. A stage (one chunk, two groups):
 //   1. wait until only the weight DMAs of chunk C + 1 are outstanding; barrier (chunk C's h is in
 //      LDS for every wave, and every wave is done with chunk C - 1); the DMAs of chunk C + 1's h
 //      into the slot chunk C - 1 used;
-//   2. read the wave's weights of chunk C out of its ring slot into registers, and the chunk's
-//      A scales;
-//   3. per group: the A entries of the group once, then per pair the group's nibbles as e4m3
-//      bytes, two scaled MFMAs (the pieces) per m tile into acc, and tot += t * acc; before the
-//      second group, once the weight reads have landed, the DMAs of chunk C + 2's weights into
-//      the slot just read;
+//   2. read the wave's weights of chunk C out of its ring slot into registers;
+//   3. per group: the A entries of the group once, then per pair 4 k-steps x NM m tiles of
+//      MFMAs into acc and tot += t * acc; before the second group, once the weight reads have
+//      landed, the DMAs of chunk C + 2's weights into the slot just read;
 //   4. after an odd chunk, the super-unit's bias MFMAs (two per pair and m tile: slices
 //      hi + mid, lo).
 // The loop issues no vector-memory instruction the compiler can see, so the one explicit wait
@@ -1309,8 +1195,7 @@ constexpr int kW32Pairs = 1;
 
 template <int NP, int NM, int NW, int MODE>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 4 : 2)))
-void head_wide32_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_t* __restrict__ hs,
-                        const u32x4_t* __restrict__ hx) {
+void head_wide32_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_t* __restrict__ hx) {
     constexpr int kVec = NM * 512;              // 16 B A vectors per chunk
     constexpr int kXA = NM * 128;               // 16 B bias vectors per super-unit
     constexpr int kHCopies = kVec / (64 * NW);  // 1 KB pieces of h each wave copies per chunk
@@ -1318,7 +1203,6 @@ void head_wide32_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_
     static_assert(kHCopies >= 1 && kVec % (64 * NW) == 0 && kXPieces <= NW, "copy split");
     constexpr int kOpsW = 3 * NP;  // weight DMAs a wave issues per chunk
     __shared__ u32x4_t sH[2][kVec];
-    __shared__ u32x4_t sS[2][64];  // the chunk's A scales, dword 2 mt + piece of each lane
     __shared__ u32x4_t sX[2][kXA];
     __shared__ u32x4_t sWn[NW][2][NP][2][64];
     __shared__ uint32_t sWs[NW][2][NP][64];
@@ -1327,9 +1211,7 @@ void head_wide32_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_
     const int lane = threadIdx.x & 63;
     const uint32_t wave = wave_id();
     const uint32_t T0 = (blockIdx.x * NW + wave) * 2 * NP;
-    // the B scale 2^2 (E8M0 129): the nibble bytes q * 2^-9 enter as q / 128. In a register: a
-    // constant scale operand would be encoded as a float.
-    const uint32_t scale_b = vgpr_const(129u);
+    const uint32_t magic = vgpr_const(0x43004300u);
     const uint32_t nchunks = a.nunits + (a.nunits & 1);
     const uint32_t stripe = a.nunits * kUnitBytes;
 
@@ -1367,8 +1249,7 @@ void head_wide32_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_
         asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2 nt" ::"s"(dst), "v"(voff), "s"(base)
                      : "memory");
     };
-    // chunk C's h pieces and scales into slot C & 1, with an even C also super-unit C / 2's
-    // bias pieces
+    // chunk C's h pieces into slot C & 1, with an even C also super-unit C / 2's bias pieces
     auto issue_h = [&](uint32_t C) {
         const u32x4_t* src = hp + static_cast<size_t>(C) * kVec;
 #pragma unroll
@@ -1376,7 +1257,6 @@ void head_wide32_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_
             const uint32_t piece = wave * kHCopies + it;
             dma16(src + piece * 64, vo_h, lds_off(&sH[C & 1][piece * 64]));
         }
-        if (wave == NW - 1) dma16(hs + static_cast<size_t>(C) * 64, vo_h, lds_off(&sS[C & 1][0]));
         if ((C & 1) == 0) {
             const uint32_t xp = wave % kXPieces, P = C >> 1;
             dma16(hx + static_cast<size_t>(P) * kXA + xp * 64, vo_h, lds_off(&sX[P & 1][xp * 64]));
@@ -1425,59 +1305,43 @@ void head_wide32_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_
             sc[p] = u32x2_t{sWs[wave][P][p][2 * n], sWs[wave][P][p][2 * n + 1]};
         }
         const u32x4_t* sA = sH[P];
-        const u32x4_t scv = sS[P][lane];
-        const uint32_t sv[4] = {scv.x, scv.y, scv.z, scv.w};
-        // per pair and group: the two pieces of each m tile into acc, then tot += t * acc
-        f32x16_t acc[NM];
-        u32x4_t av[NM][2][2];
+        // unit u = NP g + p: the MFMA chains of pair p over group g into acc[u & 1]; its scale
+        // FMAs are placed after the next unit's chains, so each wave has MFMA and VALU work
+        // that do not depend on each other
+        f32x16_t acc[2][NM];
+        bf16x8_t av[NM][4];
         auto load_a = [&](int g) {
 #pragma unroll
             for (int mt = 0; mt < NM; ++mt)
 #pragma unroll
-                for (int pc = 0; pc < 2; ++pc)
-#pragma unroll
-                    for (int hf = 0; hf < 2; ++hf) av[mt][pc][hf] = sA[(((mt * 2 + g) * 2 + pc) * 2 + hf) * 64 + lane];
+                for (int s = 0; s < 4; ++s)
+                    av[mt][s] = __builtin_bit_cast(bf16x8_t, sA[((mt * 2 + g) * 4 + s) * 64 + lane]);
         };
         auto chain = [&](int g, int p) {
-            const uint32_t ww[4] = {w0[p][2 * g], w0[p][2 * g + 1], w1[p][2 * g], w1[p][2 * g + 1]};
-            i32x8_t b;
+            const int u = (NP * g + p) & 1;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                b[2 * j] = static_cast<int>(ww[j] & 0x0F0F0F0Fu);
-                b[2 * j + 1] = static_cast<int>((ww[j] >> 4) & 0x0F0F0F0Fu);
-            }
+            for (int s = 0; s < 4; ++s) {
+                const uint32_t word = (s < 2) ? w0[p][2 * g + (s & 1)] : w1[p][2 * g + (s & 1)];
+                const bf16x8_t b = nibbles_to_bf16(word, magic);
 #pragma unroll
-            for (int mt = 0; mt < NM; ++mt)
-#pragma unroll
-                for (int pc = 0; pc < 2; ++pc) {
-                    const u32x4_t x0 = av[mt][pc][0], x1 = av[mt][pc][1];
-                    const i32x8_t A = i32x8_t{static_cast<int>(x0.x), static_cast<int>(x0.y), static_cast<int>(x0.z),
-                                              static_cast<int>(x0.w), static_cast<int>(x1.x), static_cast<int>(x1.y),
-                                              static_cast<int>(x1.z), static_cast<int>(x1.w)};
-                    // e4m3 A and B (format 0), scale byte 0 of each operand's register
-                    acc[mt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        A, b, pc == 0 ? f32x16_t{} : acc[mt], 0, 0, 0, static_cast<int>(sv[2 * mt + pc]), 0,
-                        static_cast<int>(scale_b));
+                for (int mt = 0; mt < NM; ++mt) {
+                    if (s == 0)
+                        acc[u][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[mt][s], b, f32x16_t{}, 0, 0, 0);
+                    else
+                        acc[u][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[mt][s], b, acc[u][mt], 0, 0, 0);
                 }
+            }
         };
         auto scale = [&](int g, int p) {
+            const int u = (NP * g + p) & 1;
             const float t = bf16_hi(g == 0 ? sc[p].x : sc[p].y);
 #pragma unroll
             for (int mt = 0; mt < NM; ++mt)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) tot[p][mt][v] = fmaf(t, acc[mt][v], tot[p][mt][v]);
+                for (int v = 0; v < 16; ++v) tot[p][mt][v] = fmaf(t, acc[u][mt][v], tot[p][mt][v]);
         };
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
-            // one group's A entries live at a time: reading the next group's early would spill.
-            // The empty asm takes the first group's totals (so its MFMAs and FMAs stay above) and
-            // clobbers memory (so the second group's reads stay below).
-            if (g == 1) {
-#pragma unroll
-                for (int p = 0; p < NP; ++p)
-#pragma unroll
-                    for (int mt = 0; mt < NM; ++mt) asm volatile("" : "+v"(tot[p][mt])::"memory");
-            }
             load_a(g);
             if (g == 1) {
                 // every LDS read of this wave's weight slot (and the group's A entries) has
@@ -1488,9 +1352,11 @@ void head_wide32_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
                 chain(g, p);
-                scale(g, p);
+                if (p > 0) scale(g, p - 1);
+                else if (g > 0) scale(g - 1, NP - 1);
             }
         }
+        scale(1, NP - 1);
         if constexpr (P == 0) {
 #pragma unroll
             for (int p = 0; p < NP; ++p) sc_even[p] = sc[p];
@@ -1614,7 +1480,6 @@ struct twd_head {
     StreamOrder order;            // calls on several streams share gbest, hp/hx and sel
     u32x4_t* hp = nullptr;        // prepared h in A-fragment order for M > 8 (prep_hidden_kernel)
     u32x4_t* hx = nullptr;        // its bias A-fragment entries
-    uint32_t* hs = nullptr;       // the A scales of the e4m3 pieces of h (prep_hidden32_kernel)
     twd_selector* sel = nullptr;
     uint16_t* norm_w = nullptr;   // final RMSNorm weight, when loaded from a container
     SampleStats stats{};          // per-wave statistics of the fused sample pass (M <= 4)
@@ -1712,7 +1577,6 @@ int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
     // unconditionally)
     if (e == hipSuccess) e = hipMalloc(&h->hp, sizeof(u32x4_t) * (h->nunits + 3) * 4 * 4 * 64);
     if (e == hipSuccess) e = hipMalloc(&h->hx, sizeof(u32x4_t) * (super_units(h->nunits) + 1) * 4 * 64);
-    if (e == hipSuccess) e = hipMalloc(&h->hs, sizeof(u32x4_t) * (h->nunits + 3) * 64);
     const uint32_t sb = blocks_for(h->ntiles, kRTS, kNWS4);
     if (sb * kNWS4 <= kSampleMaxWaves) {
         h->sample_blocks = sb;
@@ -1787,16 +1651,14 @@ int launch_head(twd_head* h, const uint16_t* hidden, uint32_t rows, float* logit
             <<<blocks_for(h->ntiles, kRT1), kHeadThreads, 0, stream>>>(a, h->hp, h->hx);
     } else if (rows <= 32) {
         prep_hidden32_kernel<1><<<padded_units(h->nunits) * 2, kHeadThreads, 0, stream>>>(hidden, rows, h->d,
-                                                                                         h->hp, h->hs, h->hx);
+                                                                                         h->hp, h->hx);
         head_wide32_kernel<kW32Pairs, 1, kW32Waves, MODE>
-            <<<blocks_for(h->ntiles, 2 * kW32Pairs, kW32Waves), kW32Waves * 64, 0, stream>>>(
-                a, h->hp, reinterpret_cast<const u32x4_t*>(h->hs), h->hx);
+            <<<blocks_for(h->ntiles, 2 * kW32Pairs, kW32Waves), kW32Waves * 64, 0, stream>>>(a, h->hp, h->hx);
     } else {
         prep_hidden32_kernel<2><<<padded_units(h->nunits) * 4, kHeadThreads, 0, stream>>>(hidden, rows, h->d,
-                                                                                         h->hp, h->hs, h->hx);
+                                                                                         h->hp, h->hx);
         head_wide32_kernel<kW32Pairs, 2, kW32Waves, MODE>
-            <<<blocks_for(h->ntiles, 2 * kW32Pairs, kW32Waves), kW32Waves * 64, 0, stream>>>(
-                a, h->hp, reinterpret_cast<const u32x4_t*>(h->hs), h->hx);
+            <<<blocks_for(h->ntiles, 2 * kW32Pairs, kW32Waves), kW32Waves * 64, 0, stream>>>(a, h->hp, h->hx);
     }
     TWD_HIP(hipGetLastError());
     return TWD_OK;
@@ -2007,7 +1869,6 @@ TWD_API void twd_head_destroy(twd_head* h) {
     if (h->gbest) (void)hipFree(h->gbest);
     if (h->hp) (void)hipFree(h->hp);
     if (h->hx) (void)hipFree(h->hx);
-    if (h->hs) (void)hipFree(h->hs);
     if (h->sel) twd_selector_destroy(h->sel);
     if (h->norm_w) (void)hipFree(h->norm_w);
     if (h->stats.key) (void)hipFree(h->stats.key);
