@@ -318,7 +318,7 @@ TWD_API int twd_select(twd_selector* sel, float* logits, uint32_t vocab, uint32_
 /* twd_select without a selector, allocating nothing: no counterpart in the reference. It is for
  * callers that cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). The selection scratch is a fixed device array of
- * 4,259,840 bytes per GPU, kept for the life of the process: at most 64 rows of at most 262144
+ * 4,252,176 bytes per GPU, kept for the life of the process: at most 64 rows of at most 262144
  * entries per call (TWD_E_INVALID beyond). Every call on one GPU uses that GPU's one array, so
  * calls that overlap on a GPU (other streams, other threads) race: order them. The first call on
  * each device looks the array's address up there. Results are those of twd_select. */

@@ -248,6 +248,51 @@ def test_rows_with_own_params_and_histories(env, oracle):
                                                   u=p.uniform)
 
 
+@pytest.mark.parametrize("n", [8193, 16384, 50000, V])
+def test_greedy_one_pass_vs_oracle(env, oracle, n):
+    # every row greedy and more than one slice: the slice blocks finish the rows (returning
+    # atomic max per row, an epoch-armed arrival count); called three times in a row so the
+    # counter is met both unarmed and armed. The reference's strict '>' scan: ties go to the
+    # lowest index across slices, -0 and +0 tie, NaN is skipped except at index 0, all -inf
+    # gives 0; penalised greedy rows take the penalty first (sampling.cpp:74-104)
+    torch, dev, t, sel = env
+    rng = np.random.default_rng(4000 + n)
+    rows, params, hist_parts = [], [], []
+    base = (rng.standard_normal((8, n)) * 3).astype(np.float32)
+    r0 = base[0]
+    r1 = base[1].copy()
+    top = r1.max() + 1.0
+    r1[[n - 1, 8200 % n, 5]] = top                        # ties in several slices
+    r2 = base[2].copy()
+    r2[:] = -np.abs(r2)
+    r2[n - 3] = 0.0
+    r2[9000 % n] = -0.0                                   # -0 and +0 tie at the top
+    r3 = base[3].copy()
+    r3[0] = np.nan                                        # NaN at index 0 -> 0
+    r4 = base[4].copy()
+    r4[rng.integers(0, n, 20)] = np.nan                   # NaN elsewhere is skipped
+    r5 = np.full(n, -np.inf, np.float32)                  # all -inf -> 0
+    r6 = base[6]
+    r7 = base[7]
+    hist = rng.integers(0, n + 5, 700).astype(np.uint32)
+    hist[:40] = np.argsort(-r6)[:40]                      # penalise the current leaders
+    for i, row in enumerate([r0, r1, r2, r3, r4, r5, r6, r7]):
+        rows.append(row)
+        if i in (6, 7):
+            params.append(rp(t, 0.0, 1.0, 0, 0.0, rep=1.3 if i == 6 else 0.7, cap=30.0, off=0, n=700))
+        else:
+            params.append(rp(t, 0.0, 1.0, 0, 0.0))
+    want = []
+    for i, row in enumerate(rows):
+        x = row
+        if i in (6, 7):
+            x = oracle.apply_repetition_penalty(row, hist, 1.3 if i == 6 else 0.7, 30.0)
+        want.append(oracle.argmax(x))
+    for rep_ in range(3):
+        tok, _ = select_rows(env, np.stack(rows), params, history=hist)
+        assert [int(x) for x in tok] == want, (n, rep_)
+
+
 def test_degenerate_rows(env):
     torch, dev, t, sel = env
     nan_row = np.zeros(5000, np.float32)

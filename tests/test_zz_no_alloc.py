@@ -71,6 +71,31 @@ def test_noalloc_matches_selector(shape):
     sel.close()
 
 
+def test_noalloc_greedy_one_pass():
+    # every row greedy: the one-pass finish on the fixed scratch's row slots and counter, two
+    # calls in a row (the second smaller), against the selector
+    import torch
+    assert torch.cuda.is_available(), "GPU test run without a GPU"
+    t = twd()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream().cuda_stream
+    sel = t.Selector(262144, 64)
+    rng = np.random.default_rng(8)
+    for rows, n in [(64, 262144), (3, 20000)]:
+        base = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
+        base[1 % rows, [n - 1, 4]] = base.max() + 1.0  # a tie across slices
+        params = [t.RowParams(0.0, 1.0, 0, 1.0, 0.0, 30.0, 0, 0) for _ in range(rows)]
+        a = torch.from_numpy(base).to(dev)
+        ta = torch.full((rows,), -7, dtype=torch.int32, device=dev)
+        tb = torch.full((rows,), -7, dtype=torch.int32, device=dev)
+        sel.select(a, params, None, ta, stream=stream)
+        _noalloc(t, a, params, None, tb, stream)
+        torch.cuda.synchronize()
+        want = [int(np.argmax(base[m])) for m in range(rows)]
+        assert ta.cpu().tolist() == want and tb.cpu().tolist() == want, (rows, n)
+    sel.close()
+
+
 def test_noalloc_rejects_sizes_beyond_its_scratch():
     import torch
     t = twd()

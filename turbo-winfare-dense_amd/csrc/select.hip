@@ -44,6 +44,8 @@ struct SelectArgs {
     uint32_t rows;
     uint32_t parts;
     uint32_t penalty_only;  // stop after the repetition penalty
+    uint32_t one_pass;      // every row greedy: the slice blocks finish the rows themselves
+    uint32_t epoch, next_epoch;
     twd_row_params p[TWD_MAX_ROWS + 1];  // verify samples up to K+1 rows
 };
 
@@ -59,6 +61,8 @@ struct SelectBufs {
     uint32_t* part_count;
     uint64_t* part_key;
     uint64_t* cand;
+    uint64_t* gbest;  // one-pass greedy: per-row best ranks, zero between launches
+    uint64_t* gctr;   // its arrival counter {arrivals (high 32 bits), epoch} and fallback word
 };
 
 // Shared memory: what every block needs (reductions, the row's shortlist and its sums)...
@@ -480,6 +484,56 @@ __device__ __forceinline__ void finish_row(SelCommon& c, uint32_t want, const tw
     if (tid == 0) *token_out = tok;
 }
 
+// One-pass greedy finish (every row of the launch greedy, more than one slice): each slice block
+// folds its best rank into its row's gbest slot with a returning atomic max and then counts
+// itself in; the block that completes the count reads and clears every row's slot and writes
+// the tokens. The protocol is the head's grid finish (device-scope atomics only, no fence):
+// a returning atomic is performed at the memory-side coherence point before it returns, and
+// the block waits for that return before it counts in, so every maximum precedes its
+// block's arrival. The counter holds {arrivals, epoch}; its last block arms it for the next
+// launch, and a launch that finds it armed for another epoch counts in on the fallback word
+// by compare-and-swap.
+__device__ __forceinline__ void select_greedy_finish(const SelectArgs& args, const SelectBufs& b, uint32_t row,
+                                                     uint64_t k, SelCommon& c) {
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        const unsigned long long seen = __hip_atomic_fetch_max(reinterpret_cast<unsigned long long*>(b.gbest + row),
+                                                               static_cast<unsigned long long>(k), __ATOMIC_RELAXED,
+                                                               __HIP_MEMORY_SCOPE_AGENT);
+        c.red64[0] = seen;  // waits for the return: the maximum is performed before the count
+        const uint32_t nb = gridDim.x * gridDim.y;
+        unsigned long long* ctr = reinterpret_cast<unsigned long long*>(b.gctr);
+        const unsigned long long ep = args.epoch;
+        const unsigned long long old = __hip_atomic_fetch_add(ctr, 1ull << 32, __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT);
+        bool last;
+        if ((old & 0xFFFFFFFFull) == ep && (old >> 32) < nb) {
+            last = (old >> 32) == nb - 1;
+        } else {
+            // not armed for this launch: every failed exchange means another block counted
+            // itself in, so the loop ends after at most nb tries
+            unsigned long long* c2 = ctr + 1;
+            unsigned long long cur = __hip_atomic_load(c2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), want;
+            do {
+                want = ((cur & 0xFFFFFFFFull) == ep) ? cur + (1ull << 32) : (ep | (1ull << 32));
+            } while (!__hip_atomic_compare_exchange_strong(c2, &cur, want, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT));
+            last = (want >> 32) == nb;
+        }
+        if (last)  // every block of this launch has added to ctr[0] by now
+            __hip_atomic_exchange(ctr, static_cast<unsigned long long>(args.next_epoch), __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+        c.misc[7] = last ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!c.misc[7]) return;
+    for (uint32_t r = tid; r < args.rows; r += blockDim.x) {
+        const uint64_t kk = __hip_atomic_exchange(reinterpret_cast<unsigned long long*>(b.gbest + r), 0ull,
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        b.tokens[r] = rank_index(kk);
+    }
+}
+
 // SelectArgs is the first kernel argument, so it sits at offset 0 of the kernarg segment. The
 // row's parameters are read through that pointer: indexing the by-value argument with
 // blockIdx.y would make the compiler copy all of it into per-lane scratch memory.
@@ -576,6 +630,10 @@ void select_slice_kernel(SelectArgs args_by_value, SelectBufs b) {
         k = block_max_u64<NT>(k, sh.c);
         if (parts == 1) {
             if (tid == 0) b.tokens[row] = rank_index(k);
+            return;
+        }
+        if (args.one_pass) {
+            select_greedy_finish(args, b, row, k, sh.c);
             return;
         }
         if (tid == 0) b.part_key[static_cast<size_t>(row) * parts + part] = k;
@@ -1290,7 +1348,8 @@ constexpr size_t kStaticOffMax = kStaticOffKey + 8 * kStaticSlots;    // float [
 constexpr size_t kStaticOffFlag = kStaticOffMax + 4 * kStaticSlots;   // uint32 [slots]
 constexpr size_t kStaticOffCount = kStaticOffFlag + 4 * kStaticSlots; // uint32 [slots]
 constexpr size_t kStaticOffCand = kStaticOffCount + 4 * kStaticSlots; // uint64 [slots][kMaxWant]
-constexpr size_t kStaticBytes = kStaticOffCand + 8 * kStaticSlots * kMaxWant;  // 4,259,840 B
+constexpr size_t kStaticOffGbest = kStaticOffCand + 8 * kStaticSlots * kMaxWant;  // uint64 [rows + 2]
+constexpr size_t kStaticBytes = kStaticOffGbest + 8 * (kStaticRows + 2);  // 4,252,176 B
 static_assert(kStaticOffCand % 256 == 0, "candidate array alignment");
 
 static __device__ __align__(256) unsigned char scratch[kStaticBytes];
@@ -1303,6 +1362,7 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_static_mu;
 void* g_static_ptr[kMaxDevices] = {};
+uint32_t g_static_epoch[kMaxDevices] = {};  // of each GPU's last one-pass greedy launch
 
 int static_scratch(SelectScratch* out) {
     int dev = 0;
@@ -1329,6 +1389,11 @@ int static_scratch(SelectScratch* out) {
     s.part_flag = reinterpret_cast<uint32_t*>(b + kStaticOffFlag);
     s.part_count = reinterpret_cast<uint32_t*>(b + kStaticOffCount);
     s.cand = reinterpret_cast<uint64_t*>(b + kStaticOffCand);
+    // zero at load: the first one-pass greedy launch finds its counter unarmed and counts in on
+    // the fallback word, then arms it for the next
+    s.gbest = reinterpret_cast<uint64_t*>(b + kStaticOffGbest);
+    s.gctr = s.gbest + kStaticRows;
+    s.epoch = &g_static_epoch[dev];
     s.verify_tokens = nullptr;  // twd_select does not use it
     *out = s;
     return TWD_OK;
@@ -1353,6 +1418,12 @@ int scratch_alloc(SelectScratch* s, uint32_t max_vocab, uint32_t max_rows) {
     const size_t nw = static_cast<size_t>(max_rows) * s->wave_cap;
     if (e == hipSuccess) e = hipMalloc(&s->wkey, nw * sizeof(uint64_t));
     if (e == hipSuccess) e = hipMalloc(&s->wsum, nw * sizeof(double));
+    if (e == hipSuccess) e = hipMalloc(&s->gbest, (max_rows + 2) * sizeof(uint64_t));
+    if (e == hipSuccess) e = hipMemset(s->gbest, 0, (max_rows + 2) * sizeof(uint64_t));
+    if (e == hipSuccess) {
+        s->gctr = s->gbest + max_rows;
+        s->epoch = new uint32_t(0);
+    }
     if (e != hipSuccess) {
         scratch_free(s);
         return hip_fail(e, "allocating selection scratch");
@@ -1370,6 +1441,8 @@ void scratch_free(SelectScratch* s) {
     (void)hipFree(s->verify_tokens);
     (void)hipFree(s->wkey);
     (void)hipFree(s->wsum);
+    (void)hipFree(s->gbest);
+    delete s->epoch;
     *s = SelectScratch{};
 }
 
@@ -1465,9 +1538,18 @@ int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_
     b.part_count = s.part_count;
     b.part_key = s.part_key;
     b.cand = s.cand;
+    // every row greedy: the slice blocks finish the rows (one launch instead of two)
+    if (!penalty_only && !any_sampled && parts > 1 && s.gbest && s.gctr && s.epoch) {
+        *s.epoch = *s.epoch % 0x7FFFFFFFu + 1u;  // 1 .. 2^31 - 1, never 0
+        a.one_pass = 1;
+        a.epoch = *s.epoch;
+        a.next_epoch = *s.epoch % 0x7FFFFFFFu + 1u;
+        b.gbest = s.gbest;
+        b.gctr = s.gctr;
+    }
     select_slice_kernel<<<dim3(parts, rows), kSliceThreads, sizeof(SliceShared), stream>>>(a, b);
     TWD_HIP(hipGetLastError());
-    if (parts > 1 && !penalty_only) {
+    if (parts > 1 && !penalty_only && !a.one_pass) {
         select_merge_kernel<<<rows, kMergeThreads, sizeof(MergeShared), stream>>>(a, b);
         TWD_HIP(hipGetLastError());
     }

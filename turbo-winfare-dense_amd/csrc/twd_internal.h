@@ -260,6 +260,11 @@ struct SelectScratch {
     uint32_t wave_cap = 0;              // wave records per row (0: no wave-record path)
     uint64_t* wkey = nullptr;           // [rows][wave_cap] best rank per 64 entries
     double* wsum = nullptr;             // [rows][wave_cap] sum of exp(v - best value)
+    // one-pass greedy launches: per-row best ranks (zero between launches), the arrival counter
+    // {arrivals, epoch} and its fallback word, and the host's epoch of the last such launch
+    uint64_t* gbest = nullptr;          // [max_rows]
+    uint64_t* gctr = nullptr;           // [2]
+    uint32_t* epoch = nullptr;          // host memory
 };
 
 int scratch_alloc(SelectScratch* s, uint32_t max_vocab, uint32_t max_rows);
