@@ -35,7 +35,7 @@
 namespace twd {
 
 constexpr int kDraftThreads = 256;   // max / exp kernels
-constexpr int kDraftPer = 16;
+constexpr int kDraftPer = 8;
 constexpr uint32_t kDraftChunk = kDraftThreads * kDraftPer;  // entries per block and row
 constexpr uint32_t kDraftMaxParts = 128;                     // vocab <= 524288
 constexpr int kRejThreads = 1024;    // one block per position
