@@ -487,9 +487,12 @@ __device__ __forceinline__ void load_row(const float* row, uint32_t j0, float (&
 // against the exact S, so a wrong prediction costs one exact segment, never a wrong sum. No
 // block waits on another: the launches are ordered on the stream.
 constexpr uint32_t kSegHead = kSerialUntil;  // terms summed serially at the start
-constexpr uint32_t kSegLen = 1024;           // terms per segment after the head
-constexpr int kSegThreads = 256;             // 4 terms per thread
-constexpr uint32_t kSegMax = 512;            // segments per row (vocab <= 2048 + 512 * 1024)
+constexpr uint32_t kSegLen = 512;                    // terms per segment after the head
+constexpr int kSegPer = kSegLen / 64;                // terms per lane when one wave sums a segment
+constexpr int kSegThreads = kSegLen / 4;             // 4 terms per thread in seg_xfer_kernel
+constexpr int kSegWaves = kSegThreads / 64;
+constexpr uint32_t kSegMax = (1u << 19) / kSegLen;  // segments per row (vocab <= 2048 + 2^19)
+static_assert(kSegLen % 256 == 0 && kSegPer % 4 == 0, "whole waves, 16-byte lane loads");
 
 __host__ __device__ inline uint32_t seg_count(uint32_t n) {
     return n > kSegHead ? (n - kSegHead + kSegLen - 1) / kSegLen : 0u;
@@ -530,13 +533,15 @@ struct SegSrcResidual {  // (p - q)+ of a rejected position (draft_reject_kernel
     }
 };
 
-// sum of one double per thread over a 256-thread block (any order: the value only predicts)
+// sum of one double per thread over a kSegThreads block (any order: the value only predicts)
 __device__ __forceinline__ double seg_block_sum(double v, double* red) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    const double t = red[0] + red[1] + red[2] + red[3];
+    double t = red[0];
+#pragma unroll
+    for (int w = 1; w < kSegWaves; ++w) t += red[w];
     __syncthreads();
     return t;
 }
@@ -544,7 +549,7 @@ __device__ __forceinline__ double seg_block_sum(double v, double* red) {
 // grid (1 + segments, rows): block 0 the head [0, kSegHead), block s the segment s - 1
 template <class Src>
 __global__ __launch_bounds__(kSegThreads) void seg_dsum_kernel(Src src, uint32_t n, double* d) {
-    __shared__ double red[kSegThreads / 64];
+    __shared__ double red[kSegWaves];
     const uint32_t row = blockIdx.y, b = blockIdx.x;
     if (!src.active(row)) return;  // the whole block
     const uint32_t nseg = seg_count(n);
@@ -559,8 +564,8 @@ __global__ __launch_bounds__(kSegThreads) void seg_dsum_kernel(Src src, uint32_t
 // grid (segments, rows): the record of segment blockIdx.x
 template <class Src>
 __global__ __launch_bounds__(kSegThreads) void seg_xfer_kernel(Src src, uint32_t n, const double* d, SegRec* rec) {
-    __shared__ double red[kSegThreads / 64];
-    __shared__ Xfer wt[2][kSegThreads / 64];
+    __shared__ double red[kSegWaves];
+    __shared__ Xfer wt[2][kSegWaves];
     const uint32_t row = blockIdx.y, s = blockIdx.x;
     if (!src.active(row)) return;  // the whole block
     const uint32_t nseg = seg_count(n);
@@ -600,15 +605,19 @@ __global__ __launch_bounds__(kSegThreads) void seg_xfer_kernel(Src src, uint32_t
         SegRec r;
         r.E[0] = E0;
         r.E[1] = E1;
-        r.f[0] = xfer_then(xfer_then(wt[0][0], wt[0][1]), xfer_then(wt[0][2], wt[0][3]));
-        r.f[1] = xfer_then(xfer_then(wt[1][0], wt[1][1]), xfer_then(wt[1][2], wt[1][3]));
+        r.f[0] = wt[0][0];
+        r.f[1] = wt[1][0];
+        for (int w = 1; w < kSegWaves; ++w) {
+            r.f[0] = xfer_then(r.f[0], wt[0][w]);
+            r.f[1] = xfer_then(r.f[1], wt[1][w]);
+        }
         rec[static_cast<size_t>(row) * kSegMax + s] = r;
     }
 }
 
 // One segment summed exactly by one wave, with no block barrier and one load per term: terms
-// [k0, k1) of a row of n (k1 - k0 <= kSegLen, k0 a multiple of 16) from prefix S; lane l holds
-// terms k0 + 16 l .. + 15 in registers. Each pass does what a window of block_seq_sum does --
+// [k0, k1) of a row of n (k1 - k0 <= kSegLen, k0 a multiple of kSegPer) from prefix S; lane l
+// holds terms k0 + kSegPer l .. + kSegPer - 1 in registers. Each pass does what a window of block_seq_sum does --
 // the terms in units of the binade of S, their transfer functions scanned across the wave, a
 // replay to the first term that leaves the binade or reaches thr -- and an exact add of that
 // term; the next pass continues after it from the same registers. Returns the sum; *stop_at
@@ -618,16 +627,16 @@ template <typename Load>
 __device__ float wave_seg_sum(Load load, uint32_t n, uint32_t k0, uint32_t k1, float S, float thr,
                               bool want_stop, uint32_t* stop_at) {
     const int lane = threadIdx.x & 63;
-    const uint32_t j0 = k0 + static_cast<uint32_t>(lane) * 16u;
-    float a[16];
-    if (j0 < ((n + 15u) & ~15u)) {
+    const uint32_t j0 = k0 + static_cast<uint32_t>(lane) * kSegPer;
+    float a[kSegPer];
+    if (j0 < ((n + 15u) & ~15u)) {  // rows are padded to 16 floats: the whole load is inside
         load(j0, a);
     } else {
 #pragma unroll
-        for (int q = 0; q < 16; ++q) a[q] = 0.0f;
+        for (int q = 0; q < kSegPer; ++q) a[q] = 0.0f;
     }
 #pragma unroll
-    for (int q = 0; q < 16; ++q)
+    for (int q = 0; q < kSegPer; ++q)
         if (j0 + q >= k1) a[q] = 0.0f;
     uint32_t kc = k0;  // the first term not yet added
     uint32_t stop = k1;
@@ -641,10 +650,10 @@ __device__ float wave_seg_sum(Load load, uint32_t n, uint32_t k0, uint32_t k1, f
             const double t = ceil(ldexp(static_cast<double>(thr), 23 - E));
             Tu = t <= 0.0 ? 0u : (t >= 4294967295.0 ? 0xFFFFFFFFu : static_cast<uint32_t>(t));
         }
-        uint32_t kk[16], kd[16];
+        uint32_t kk[kSegPer], kd[kSegPer];
         Xfer t = xfer_id();
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
+        for (int q = 0; q < kSegPer; ++q) {
             split_term(j0 + q >= kc ? a[q] : 0.0f, E, kk[q], kd[q]);
             t = xfer_then(t, term_xfer(kk[q], kd[q]));
         }
@@ -656,7 +665,7 @@ __device__ float wave_seg_sum(Load load, uint32_t n, uint32_t k0, uint32_t k1, f
         uint32_t ev = kNoEvent, R_before = R;
         bool live = R < kL;
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
+        for (int q = 0; q < kSegPer; ++q) {
             const uint32_t j = j0 + q;
             const uint32_t d = term_inc(kk[q], kd[q], par);
             const bool go = live && j >= kc && j < k1;
@@ -690,7 +699,7 @@ __device__ float wave_seg_sum(Load load, uint32_t n, uint32_t k0, uint32_t k1, f
         // the term that leaves the binade, added exactly
         float aj = 0.0f;
 #pragma unroll
-        for (int q = 0; q < 16; ++q) aj = (j0 + q == j) ? a[q] : aj;
+        for (int q = 0; q < kSegPer; ++q) aj = (j0 + q == j) ? a[q] : aj;
         aj = __shfl(aj, owner);
         const float s_new = ldexpf(static_cast<float>(__shfl(R_before, owner)), E - 23) + aj;
         S = s_new;
@@ -886,9 +895,11 @@ __global__ __launch_bounds__(kRejThreads) void seg_residual_kernel(DraftArgs a, 
         if (in_head) {
             block_seq_sum(load_diff, diff, nh, 0.0f, 0u, r_val, &at, false, sh);
         } else {
-            uint32_t t = 0;
-            for (uint32_t i = 1; i < nseg; ++i)
-                if (ch.start[i] < r_val) t = i;
+            // the starts never decrease, so the last one below r_val is at the count of those
+            // below it among starts 1 .. nseg - 1
+            int below = 0;
+            for (uint32_t i = 1 + threadIdx.x; i < nseg; i += kRejThreads) below += ch.start[i] < r_val;
+            const uint32_t t = static_cast<uint32_t>(__syncthreads_count(below));
             const float S0 = ch.start[t];
             const uint32_t k0 = kSegHead + t * kSegLen, k1 = min(V, k0 + kSegLen);
             if (threadIdx.x < 64) {
@@ -1039,7 +1050,7 @@ TWD_API int twd_sequential_sum(const float* terms, uint32_t n, float thr, float*
     if (!terms || !sum_out) return fail(TWD_E_INVALID, "null terms or sum_out");
     if (n == 0) return fail(TWD_E_INVALID, "n must be > 0");
     if ((reinterpret_cast<uintptr_t>(terms) & 15u) != 0) return fail(TWD_E_INVALID, "terms must be 16-byte aligned");
-    if (seg_count(n) > kSegMax) return fail(TWD_E_INVALID, "n above 2048 + 512 * 1024");
+    if (seg_count(n) > kSegMax) return fail(TWD_E_INVALID, "n above 2048 + 524288");
     const hipStream_t s = static_cast<hipStream_t>(stream);
     // one row's segment scratch, allocated on the first call and kept for the process
     static std::mutex mu;
