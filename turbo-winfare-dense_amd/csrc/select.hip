@@ -1615,6 +1615,7 @@ TWD_API int twd_selector_create(uint32_t max_vocab, uint32_t max_rows, twd_selec
 TWD_API void twd_selector_destroy(twd_selector* s) {
     if (!s) return;
     order_release(s->order);
+    draft_side_free(&s->draft);  // waits for the side stream's work
     scratch_free(&s->scratch);
     draft_scratch_free(&s->draft);
     delete s;

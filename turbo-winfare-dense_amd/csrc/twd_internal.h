@@ -277,9 +277,12 @@ struct DraftScratch {
     uint32_t* flags = nullptr; // [2 * TWD_MAX_ROWS] NaN flags
     uint32_t* rej = nullptr;   // [TWD_MAX_ROWS][4] per-position outcome
     float* sums = nullptr;     // [2 * TWD_MAX_ROWS] softmax sums
-    double* seg_d = nullptr;   // [2 * TWD_MAX_ROWS][513] segment double sums of the exact-sum pipeline
-    void* seg_rec = nullptr;   // [2 * TWD_MAX_ROWS][512] segment records
+    double* seg_d = nullptr;   // [2 * TWD_MAX_ROWS][segments + 1] double sums of the exact-sum pipeline
+    void* seg_rec = nullptr;   // [2 * TWD_MAX_ROWS][segments] segment records
+    void* seg_head = nullptr;  // [2 * TWD_MAX_ROWS] the serial heads' sums
     uint32_t* live = nullptr;  // [TWD_MAX_ROWS] 1: the position's draft was rejected
+    hipStream_t side = nullptr;  // twd_verify_draft's selection runs here, beside the draft chain
+    hipEvent_t fork = nullptr, join = nullptr;
     size_t e_capacity = 0;
     size_t part_capacity = 0;
     uint32_t last_npos = 0;               // positions of the last call with draft rows
@@ -289,7 +292,8 @@ struct DraftScratch {
 int draft_scratch_reserve(DraftScratch* d, uint32_t vocab, uint32_t npos);
 // Gives the head a device copy of the final RMSNorm weight (bf16 [d]), freed with the head.
 int head_set_norm_weight(twd_head* h, const uint16_t* host_w, uint32_t d);
-void draft_scratch_free(DraftScratch* d);
+void draft_scratch_free(DraftScratch* d);  // the buffers; the side stream stays
+void draft_side_free(DraftScratch* d);     // the side stream and its events
 
 // Enqueues penalty + selection over `rows` rows. `params` is a host array.
 int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_t rows,

@@ -253,6 +253,27 @@ struct SeqShared {
 };
 static_assert(kSerialUntil <= 4 * kRejThreads, "the serial start is staged in one pass");
 
+// s + t[0] + t[1] + ... + t[n - 1], added in order (n a multiple of 16, t in LDS): the next
+// sixteen terms are read while the current sixteen are added, so the reads' latency hides
+// behind the chain of adds.
+__device__ __forceinline__ float serial_sum16(const float* t, uint32_t n, float s) {
+    float c[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) c[q] = t[q];
+    for (uint32_t j = 16; j < n; j += 16) {
+        float nx[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) nx[q] = t[j + q];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) s += c[q];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) c[q] = nx[q];
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) s += c[q];
+    return s;
+}
+
 // One window of block_seq_sum: PER terms per thread from the 16-aligned start a0 <= k0; terms
 // before k0 or at n and beyond count as zero. load(j0, a) fills a[0..PER) with terms j0.. (j0
 // a multiple of PER, in range or not), term(j) gives one term.
@@ -503,6 +524,11 @@ struct SegRec {
     Xfer f[2];  // the segment's composed transfer functions in units of 2^(E - 23)
 };
 
+struct SegHead {  // the serial head's sum; with a stop, the first index whose prefix reaches thr
+    float S;
+    uint32_t stop;   // n when none in the head does
+};
+
 // Term sources: active(row) and term(row, j) for j < n (the kernels give zero past n).
 struct SegSrcArray {  // one plain array (twd_sequential_sum)
     const float* x;
@@ -561,13 +587,40 @@ __global__ __launch_bounds__(kSegThreads) void seg_dsum_kernel(Src src, uint32_t
     if (threadIdx.x == 0) d[static_cast<size_t>(row) * (nseg + 1) + b] = t;
 }
 
-// grid (segments, rows): the record of segment blockIdx.x
+// grid (1 + segments, rows): block 0 the serial head's sum (and its stop, with want_stop) into
+// head[row]; block 1 + s the record of segment s. The head runs here, beside the records, so
+// that the chain kernel starts at the walk.
 template <class Src>
-__global__ __launch_bounds__(kSegThreads) void seg_xfer_kernel(Src src, uint32_t n, const double* d, SegRec* rec) {
+__global__ __launch_bounds__(kSegThreads) void seg_xfer_kernel(Src src, uint32_t n, const double* d, SegRec* rec,
+                                                               float thr, uint32_t want_stop, SegHead* head) {
     __shared__ double red[kSegWaves];
     __shared__ Xfer wt[2][kSegWaves];
-    const uint32_t row = blockIdx.y, s = blockIdx.x;
+    __shared__ float hterm[kSegHead];
+    const uint32_t row = blockIdx.y;
     if (!src.active(row)) return;  // the whole block
+    if (blockIdx.x == 0) {
+        const uint32_t nh = min(n, kSegHead);
+        for (uint32_t j = threadIdx.x; j < kSegHead; j += kSegThreads) hterm[j] = j < nh ? src.term(row, j) : 0.0f;
+        __syncthreads();
+        if (threadIdx.x < 64) {  // wave 0, every lane the same: the in-order loop itself
+            float S = 0.0f;
+            uint32_t stop = n;
+            if (want_stop) {
+                for (uint32_t j = 0; j < nh; ++j) {
+                    S += hterm[j];
+                    if (S >= thr) {
+                        stop = j;
+                        break;
+                    }
+                }
+            } else {
+                S = serial_sum16(hterm, kSegHead, S);  // the zeros past nh leave S as it is
+            }
+            if (threadIdx.x == 0) head[row] = SegHead{S, stop};
+        }
+        return;
+    }
+    const uint32_t s = blockIdx.x - 1;
     const uint32_t nseg = seg_count(n);
     const double* dr = d + static_cast<size_t>(row) * (nseg + 1);
     // D: the head's and the earlier segments' double sums
@@ -793,25 +846,23 @@ __device__ float seg_chain(Load load, Term term, uint32_t n, float S, float thr,
     return S;
 }
 
-// The chain of one row: its records into LDS, the serial head, the walk.
+// The chain of one row: its records into LDS, the head's sum from seg_xfer_kernel, the walk.
 template <typename Load, typename Term>
-__device__ float seg_row_sum(Load load, Term term, uint32_t n, const SegRec* rec, float thr, uint32_t* stop_at,
-                             SeqShared& sh, ChainShared& ch) {
+__device__ float seg_row_sum(Load load, Term term, uint32_t n, const SegRec* rec, const SegHead* hd, float thr,
+                             uint32_t* stop_at, SeqShared& sh, ChainShared& ch) {
     const uint32_t nseg = seg_count(n);
     for (uint32_t i = threadIdx.x; i < nseg; i += blockDim.x) ch.rec[i] = rec[i];
     __syncthreads();
-    uint32_t at = n;
-    const uint32_t nh = min(n, kSegHead);
-    float S = block_seq_sum(load, term, nh, 0.0f, 0u, thr, stop_at ? &at : nullptr, false, sh);
-    if (stop_at && at < nh) {
-        *stop_at = at;
-        return S;
+    const SegHead h = *hd;  // the same value in every thread
+    if (stop_at && h.stop < min(n, kSegHead)) {
+        *stop_at = h.stop;
+        return h.S;
     }
-    return seg_chain(load, term, n, S, thr, stop_at, sh, ch);
+    return seg_chain(load, term, n, h.S, thr, stop_at, sh, ch);
 }
 
 // The softmax sums of the e rows: one block per row.
-__global__ __launch_bounds__(kRejThreads) void seg_sum_kernel(DraftArgs a, const SegRec* rec) {
+__global__ __launch_bounds__(kRejThreads) void seg_sum_kernel(DraftArgs a, const SegRec* rec, const SegHead* heads) {
     __shared__ SeqShared sh;
     __shared__ ChainShared ch;
     const uint32_t r = blockIdx.x;
@@ -819,7 +870,7 @@ __global__ __launch_bounds__(kRejThreads) void seg_sum_kernel(DraftArgs a, const
     float s = __uint_as_float(0x7FC00000u);
     if (!(a.flags[r] & 1u))
         s = seg_row_sum([&](uint32_t j0, auto& v) { load_row(e, j0, v); }, [&](uint32_t j) { return e[j]; },
-                        a.vocab, rec + static_cast<size_t>(r) * kSegMax, 0.0f, nullptr, sh, ch);
+                        a.vocab, rec + static_cast<size_t>(r) * kSegMax, heads + r, 0.0f, nullptr, sh, ch);
     if (threadIdx.x == 0) a.sums[r] = s;
 }
 
@@ -855,7 +906,7 @@ __global__ void draft_ratio_kernel(DraftArgs a, uint32_t* live) {
 // index whose prefix reaches u2 * sum, found in the segment where the recorded starts straddle
 // it. One block per position; accepted positions return at once.
 __global__ __launch_bounds__(kRejThreads) void seg_residual_kernel(DraftArgs a, const uint32_t* live,
-                                                                   const SegRec* rec) {
+                                                                   const SegRec* rec, const SegHead* heads) {
     __shared__ SeqShared sh;
     __shared__ ChainShared ch;
     const uint32_t pi = blockIdx.x;
@@ -882,7 +933,7 @@ __global__ __launch_bounds__(kRejThreads) void seg_residual_kernel(DraftArgs a, 
         for (int q = 0; q < PER; ++q) v[q] = diff1(v[q], w[q]);
     };
     const SegRec* rr = rec + static_cast<size_t>(pi) * kSegMax;
-    const float sum_diff = seg_row_sum(load_diff, diff, V, rr, 0.0f, nullptr, sh, ch);
+    const float sum_diff = seg_row_sum(load_diff, diff, V, rr, heads + pi, 0.0f, nullptr, sh, ch);
     uint32_t corr = 0, fallback = 0;
     if (sum_diff > 1e-9f) {
         const float r_val = P.u2 * sum_diff;
@@ -926,13 +977,13 @@ __global__ __launch_bounds__(kRejThreads) void seg_residual_kernel(DraftArgs a, 
 // twd_sequential_sum through the segmented form: one row of n terms.
 template <bool STOP>
 __global__ __launch_bounds__(kRejThreads) void seg_array_kernel(const float* x, uint32_t n, float thr,
-                                                                const SegRec* rec, float* sum_out,
-                                                                uint32_t* stop_out) {
+                                                                const SegRec* rec, const SegHead* hd,
+                                                                float* sum_out, uint32_t* stop_out) {
     __shared__ SeqShared sh;
     __shared__ ChainShared ch;
     uint32_t stop = n;
     const float s = seg_row_sum([&](uint32_t j0, auto& v) { load_row(x, j0, v); }, [&](uint32_t j) { return x[j]; },
-                                n, rec, thr, STOP ? &stop : nullptr, sh, ch);
+                                n, rec, hd, thr, STOP ? &stop : nullptr, sh, ch);
     if (threadIdx.x == 0) {
         *sum_out = s;
         if (STOP) *stop_out = stop;
@@ -996,7 +1047,7 @@ __global__ void draft_finish_kernel(const uint32_t* row_tokens, uint32_t rows, c
 int draft_scratch_reserve(DraftScratch* d, uint32_t vocab, uint32_t npos) {
     const uint32_t parts = (vocab + kDraftChunk - 1) / kDraftChunk;
     const size_t need_e = static_cast<size_t>(2) * npos * ((vocab + 15u) & ~15u);
-    if (d->e && d->e_capacity >= need_e && d->part_capacity >= static_cast<size_t>(2) * npos * parts)
+    if (d->e && d->side && d->e_capacity >= need_e && d->part_capacity >= static_cast<size_t>(2) * npos * parts)
         return TWD_OK;
     draft_scratch_free(d);  // grows: later calls with as many positions reuse it
     TWD_HIP(hipMalloc(&d->e, need_e * sizeof(float)));
@@ -1008,7 +1059,13 @@ int draft_scratch_reserve(DraftScratch* d, uint32_t vocab, uint32_t npos) {
     TWD_HIP(hipMalloc(&d->sums, 2 * TWD_MAX_ROWS * sizeof(float)));
     TWD_HIP(hipMalloc(&d->seg_d, static_cast<size_t>(2) * TWD_MAX_ROWS * (kSegMax + 1) * sizeof(double)));
     TWD_HIP(hipMalloc(&d->seg_rec, static_cast<size_t>(2) * TWD_MAX_ROWS * kSegMax * sizeof(SegRec)));
+    TWD_HIP(hipMalloc(&d->seg_head, static_cast<size_t>(2) * TWD_MAX_ROWS * sizeof(SegHead)));
     TWD_HIP(hipMalloc(&d->live, TWD_MAX_ROWS * sizeof(uint32_t)));
+    if (!d->side) {  // kept across growth: freed with the selector
+        TWD_HIP(hipStreamCreateWithFlags(&d->side, hipStreamNonBlocking));
+        TWD_HIP(hipEventCreateWithFlags(&d->fork, hipEventDisableTiming));
+        TWD_HIP(hipEventCreateWithFlags(&d->join, hipEventDisableTiming));
+    }
     return TWD_OK;
 }
 
@@ -1020,8 +1077,24 @@ void draft_scratch_free(DraftScratch* d) {
     if (d->sums) (void)hipFree(d->sums);
     if (d->seg_d) (void)hipFree(d->seg_d);
     if (d->seg_rec) (void)hipFree(d->seg_rec);
+    if (d->seg_head) (void)hipFree(d->seg_head);
     if (d->live) (void)hipFree(d->live);
+    const DraftScratch keep = *d;
     *d = DraftScratch{};
+    d->side = keep.side;
+    d->fork = keep.fork;
+    d->join = keep.join;
+}
+
+void draft_side_free(DraftScratch* d) {
+    if (d->side) {
+        (void)hipStreamSynchronize(d->side);
+        (void)hipStreamDestroy(d->side);
+    }
+    if (d->fork) (void)hipEventDestroy(d->fork);
+    if (d->join) (void)hipEventDestroy(d->join);
+    d->side = nullptr;
+    d->fork = d->join = nullptr;
 }
 
 }  // namespace twd
@@ -1056,21 +1129,24 @@ TWD_API int twd_sequential_sum(const float* terms, uint32_t n, float thr, float*
     static std::mutex mu;
     static double* seg_d = nullptr;
     static SegRec* seg_rec = nullptr;
+    static SegHead* seg_head = nullptr;
     {
         std::lock_guard<std::mutex> lock(mu);
         if (!seg_d) {
             TWD_HIP(hipMalloc(&seg_d, (kSegMax + 1) * sizeof(double)));
             TWD_HIP(hipMalloc(&seg_rec, kSegMax * sizeof(SegRec)));
+            TWD_HIP(hipMalloc(&seg_head, sizeof(SegHead)));
         }
     }
     const uint32_t nseg = seg_count(n);
     const SegSrcArray src{terms};
     seg_dsum_kernel<<<dim3(nseg + 1, 1), kSegThreads, 0, s>>>(src, n, seg_d);
-    if (nseg) seg_xfer_kernel<<<dim3(nseg, 1), kSegThreads, 0, s>>>(src, n, seg_d, seg_rec);
+    seg_xfer_kernel<<<dim3(nseg + 1, 1), kSegThreads, 0, s>>>(src, n, seg_d, seg_rec, thr, stop_out ? 1u : 0u,
+                                                              seg_head);
     if (stop_out)
-        seg_array_kernel<true><<<1, kRejThreads, 0, s>>>(terms, n, thr, seg_rec, sum_out, stop_out);
+        seg_array_kernel<true><<<1, kRejThreads, 0, s>>>(terms, n, thr, seg_rec, seg_head, sum_out, stop_out);
     else
-        seg_array_kernel<false><<<1, kRejThreads, 0, s>>>(terms, n, thr, seg_rec, sum_out, stop_out);
+        seg_array_kernel<false><<<1, kRejThreads, 0, s>>>(terms, n, thr, seg_rec, seg_head, sum_out, stop_out);
     TWD_HIP(hipGetLastError());
     return TWD_OK;
 }
@@ -1124,7 +1200,13 @@ int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab
                                n_drafts, result, s);
     if (vocab == 0) return fail(TWD_E_INVALID, "vocab must be > 0");
 
-    // target tokens for the positions without draft rows, the fallback and the bonus row
+    int rc = draft_scratch_reserve(&sel->draft, vocab, a.npos);
+    if (rc) return rc;
+    DraftScratch& ds = sel->draft;
+
+    // target tokens for the positions without draft rows, the fallback and the bonus row: the
+    // selection runs on the side stream, beside the draft chain below (which leaves most of
+    // the GPU idle), and joins it before draft_finish_kernel
     const uint32_t used = (rows > k) ? k + 1 : k;
     twd_row_params rp[TWD_MAX_ROWS + 1];
     for (uint32_t i = 0; i < used; ++i) {
@@ -1133,11 +1215,16 @@ int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab
         rp[i].history_len = 0;
         rp[i].uniform = twd_uniform_from_seed(twd_splitmix64(base_seed + i));
     }
-    int rc = launch_select(sel->scratch, const_cast<float*>(logits), vocab, used, row_stride, rp,
-                           nullptr, sel->scratch.verify_tokens, s);
-    if (rc) return rc;
+    TWD_HIP(hipEventRecord(ds.fork, s));
+    TWD_HIP(hipStreamWaitEvent(ds.side, ds.fork, 0));
+    rc = launch_select(sel->scratch, const_cast<float*>(logits), vocab, used, row_stride, rp, nullptr,
+                       sel->scratch.verify_tokens, ds.side);
+    TWD_HIP(hipEventRecord(ds.join, ds.side));
+    if (rc) {
+        (void)hipStreamWaitEvent(s, ds.join, 0);
+        return rc;
+    }
 
-    if ((rc = draft_scratch_reserve(&sel->draft, vocab, a.npos))) return rc;
     a.vocab = vocab;
     a.estride = (vocab + 15u) & ~15u;
     a.parts = (vocab + kDraftChunk - 1) / kDraftChunk;
@@ -1159,14 +1246,17 @@ int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab
     double* seg_d = sel->draft.seg_d;
     SegRec* seg_rec = static_cast<SegRec*>(sel->draft.seg_rec);
     const SegSrcSoftmax src_e{a.e, a.estride, a.flags};
+    SegHead* seg_head = static_cast<SegHead*>(ds.seg_head);
     seg_dsum_kernel<<<dim3(nseg + 1, 2 * a.npos), kSegThreads, 0, s>>>(src_e, vocab, seg_d);
-    if (nseg) seg_xfer_kernel<<<dim3(nseg, 2 * a.npos), kSegThreads, 0, s>>>(src_e, vocab, seg_d, seg_rec);
-    seg_sum_kernel<<<2 * a.npos, kRejThreads, 0, s>>>(a, seg_rec);
-    draft_ratio_kernel<<<1, 64, 0, s>>>(a, sel->draft.live);
-    const SegSrcResidual src_r{a.e, a.estride, a.sums, sel->draft.live};
+    seg_xfer_kernel<<<dim3(nseg + 1, 2 * a.npos), kSegThreads, 0, s>>>(src_e, vocab, seg_d, seg_rec, 0.0f, 0u,
+                                                                      seg_head);
+    seg_sum_kernel<<<2 * a.npos, kRejThreads, 0, s>>>(a, seg_rec, seg_head);
+    draft_ratio_kernel<<<1, 64, 0, s>>>(a, ds.live);
+    const SegSrcResidual src_r{a.e, a.estride, a.sums, ds.live};
     seg_dsum_kernel<<<dim3(nseg + 1, a.npos), kSegThreads, 0, s>>>(src_r, vocab, seg_d);
-    if (nseg) seg_xfer_kernel<<<dim3(nseg, a.npos), kSegThreads, 0, s>>>(src_r, vocab, seg_d, seg_rec);
-    seg_residual_kernel<<<a.npos, kRejThreads, 0, s>>>(a, sel->draft.live, seg_rec);
+    seg_xfer_kernel<<<dim3(nseg + 1, a.npos), kSegThreads, 0, s>>>(src_r, vocab, seg_d, seg_rec, 0.0f, 0u, seg_head);
+    seg_residual_kernel<<<a.npos, kRejThreads, 0, s>>>(a, ds.live, seg_rec, seg_head);
+    TWD_HIP(hipStreamWaitEvent(s, ds.join, 0));  // the selector's tokens
     draft_finish_kernel<<<1, 64, 0, s>>>(sel->scratch.verify_tokens, used, drafts, n_drafts, has,
                                          a.rej, result);
     TWD_HIP(hipGetLastError());
