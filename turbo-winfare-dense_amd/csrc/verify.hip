@@ -75,12 +75,17 @@ __global__ __launch_bounds__(kDraftThreads) void draft_max_kernel(DraftArgs a) {
     const uint32_t r = blockIdx.y;
     const float* l = draft_row(a, r);
     const uint32_t base = blockIdx.x * kDraftChunk + threadIdx.x;
+    // every load issued before any is used (indices past the row clamped to its last entry and
+    // their values ignored), so the block waits for memory once
+    float xs[kDraftPer];
+#pragma unroll
+    for (int it = 0; it < kDraftPer; ++it) xs[it] = l[min(base + it * kDraftThreads, a.vocab - 1u)];
     float m = -1e9f;
 #pragma unroll
     for (int it = 0; it < kDraftPer; ++it) {
         const uint32_t j = base + it * kDraftThreads;
         if (j < a.vocab) {
-            const float x = l[j] / a.temp;
+            const float x = xs[it] / a.temp;
             if (x > m) m = x;  // NaN never wins, as in the reference's '>' scan
         }
     }
@@ -107,6 +112,10 @@ __global__ __launch_bounds__(kDraftThreads) void draft_exp_kernel(DraftArgs a) {
     // maxima are requested at once, one per thread, then reduced over the block: none is NaN,
     // so the order of the comparisons does not matter.
     __shared__ float red[kDraftThreads / 64];
+    const uint32_t base = blockIdx.x * kDraftChunk + threadIdx.x;
+    float xs[kDraftPer];  // the row's entries requested first, as in draft_max_kernel
+#pragma unroll
+    for (int it = 0; it < kDraftPer; ++it) xs[it] = l[min(base + it * kDraftThreads, a.vocab - 1u)];
     float mx = -1e9f;
     for (uint32_t p = threadIdx.x; p < a.parts; p += kDraftThreads) {
         const float y = a.part[r * a.parts + p];
@@ -118,14 +127,13 @@ __global__ __launch_bounds__(kDraftThreads) void draft_exp_kernel(DraftArgs a) {
     mx = red[0];
 #pragma unroll
     for (int w = 1; w < kDraftThreads / 64; ++w) mx = red[w] > mx ? red[w] : mx;
-    const uint32_t base = blockIdx.x * kDraftChunk + threadIdx.x;
     bool nan = false;
     float* e = a.e + static_cast<size_t>(r) * a.estride;
 #pragma unroll
     for (int it = 0; it < kDraftPer; ++it) {
         const uint32_t j = base + it * kDraftThreads;
         if (j < a.vocab) {
-            const float x = l[j] / a.temp;
+            const float x = xs[it] / a.temp;
             const float v = expf_libm<true>(x - mx);  // std::exp(float) of speculator.cpp:23
             nan |= (v != v);
             e[j] = v;
@@ -514,6 +522,7 @@ constexpr int kSegThreads = kSegLen / 4;             // 4 terms per thread in se
 constexpr int kSegWaves = kSegThreads / 64;
 constexpr uint32_t kSegMax = (1u << 19) / kSegLen;  // segments per row (vocab <= 2048 + 2^19)
 static_assert(kSegLen % 256 == 0 && kSegPer % 4 == 0, "whole waves, 16-byte lane loads");
+static_assert(kSegHead % kSegThreads == 0 && kSegMax % kSegThreads == 0, "whole per-thread strides");
 
 __host__ __device__ inline uint32_t seg_count(uint32_t n) {
     return n > kSegHead ? (n - kSegHead + kSegLen - 1) / kSegLen : 0u;
@@ -581,8 +590,21 @@ __global__ __launch_bounds__(kSegThreads) void seg_dsum_kernel(Src src, uint32_t
     const uint32_t nseg = seg_count(n);
     const uint32_t lo = b == 0 ? 0u : kSegHead + (b - 1) * kSegLen;
     const uint32_t hi = b == 0 ? min(n, kSegHead) : min(n, lo + kSegLen);
+    // every term requested before any is added (indices clamped into the row, values past hi
+    // dropped): one memory wait per block
+    constexpr int kPer = kSegHead / kSegThreads;
+    float v[kPer];
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+        const uint32_t j = lo + threadIdx.x + q * kSegThreads;
+        v[q] = (b == 0 || q < kSegLen / kSegThreads) ? src.term(row, min(j, n - 1u)) : 0.0f;
+    }
     double t = 0.0;
-    for (uint32_t j = lo + threadIdx.x; j < hi; j += kSegThreads) t += static_cast<double>(src.term(row, j));
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+        const uint32_t j = lo + threadIdx.x + q * kSegThreads;
+        t += j < hi ? static_cast<double>(v[q]) : 0.0;
+    }
     t = seg_block_sum(t, red);
     if (threadIdx.x == 0) d[static_cast<size_t>(row) * (nseg + 1) + b] = t;
 }
@@ -600,7 +622,15 @@ __global__ __launch_bounds__(kSegThreads) void seg_xfer_kernel(Src src, uint32_t
     if (!src.active(row)) return;  // the whole block
     if (blockIdx.x == 0) {
         const uint32_t nh = min(n, kSegHead);
-        for (uint32_t j = threadIdx.x; j < kSegHead; j += kSegThreads) hterm[j] = j < nh ? src.term(row, j) : 0.0f;
+        constexpr int kPer = kSegHead / kSegThreads;
+        float v[kPer];  // all loads first
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) v[q] = src.term(row, min(threadIdx.x + q * kSegThreads, n - 1u));
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const uint32_t j = threadIdx.x + q * kSegThreads;
+            hterm[j] = j < nh ? v[q] : 0.0f;
+        }
         __syncthreads();
         if (threadIdx.x < 64) {  // wave 0, every lane the same: the in-order loop itself
             float S = 0.0f;
@@ -624,8 +654,12 @@ __global__ __launch_bounds__(kSegThreads) void seg_xfer_kernel(Src src, uint32_t
     const uint32_t nseg = seg_count(n);
     const double* dr = d + static_cast<size_t>(row) * (nseg + 1);
     // D: the head's and the earlier segments' double sums
+    double dv[kSegMax / kSegThreads];  // all loads first; entries past s read dr[s], dropped
+#pragma unroll
+    for (int q = 0; q < kSegMax / kSegThreads; ++q) dv[q] = dr[min(threadIdx.x + q * kSegThreads, s)];
     double t = 0.0;
-    for (uint32_t i = threadIdx.x; i <= s; i += kSegThreads) t += dr[i];
+#pragma unroll
+    for (int q = 0; q < kSegMax / kSegThreads; ++q) t += threadIdx.x + q * kSegThreads <= s ? dv[q] : 0.0;
     const double D = seg_block_sum(t, red);
     int ex = 0;
     const double m = frexp(D, &ex);  // D = m * 2^ex, m in [0.5, 1)
@@ -635,10 +669,13 @@ __global__ __launch_bounds__(kSegThreads) void seg_xfer_kernel(Src src, uint32_t
     // this thread's four terms, in order, for both candidates
     const uint32_t k0 = kSegHead + s * kSegLen;
     Xfer f0 = xfer_id(), f1 = xfer_id();
+    float av[4];  // all loads first
+#pragma unroll
+    for (int q = 0; q < 4; ++q) av[q] = src.term(row, min(k0 + threadIdx.x * 4 + q, n - 1u));
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const uint32_t j = k0 + threadIdx.x * 4 + q;
-        const float a = (j < n && j < k0 + kSegLen) ? src.term(row, j) : 0.0f;
+        const float a = j < n ? av[q] : 0.0f;  // j < k0 + kSegLen always: 4 terms per thread
         uint32_t kk, kd;
         split_term(a, E0, kk, kd);
         f0 = xfer_then(f0, term_xfer(kk, kd));
