@@ -8,16 +8,17 @@
 // sequential float sums are reproduced bit for bit, so the device recomputes them exactly
 // (block_seq_sum and the segmented form below) instead of summing in a tree.
 //
-// Kernels, all on the caller's stream:
+// Kernels, on the caller's stream:
 //   draft_max_kernel     grid (parts, 2P): per row, partial maxima of l / T (T = 1 when <= 0)
-//   draft_exp_kernel     grid (parts, 2P): e = expf(l / T - max) to scratch, NaN flags
-//   seg_dsum_kernel, seg_xfer_kernel, seg_sum_kernel: each softmax's sequential sum
-//   draft_ratio_kernel   the ratio tests
-//   seg_dsum_kernel, seg_xfer_kernel, seg_residual_kernel: each rejected position's residual
-//                        sum and draw
+//   draft_exp_kernel     grid (parts, 2P): e = expf(l / T - max) to scratch, NaN flags, and the
+//                        double sums of the exact sums' head and segments
+//   seg_xfer_kernel, seg_sum_kernel: each softmax's sequential sum
+//   seg_ratio_dsum_kernel  the ratio tests, and each rejected position's segment double sums
+//   seg_xfer_kernel, seg_residual_kernel: each rejected position's residual sum and draw
 //   draft_finish_kernel  one thread: the accept chain over all positions, bonus, result
-// where P is the number of positions with a draft row; the target tokens of the other
-// positions, of the fallback and of the bonus row come from the selector (launch_select).
+// where P is the number of positions with a draft row. The target tokens of the other
+// positions, of the fallback and of the bonus row come from the selector (launch_select), run
+// on a side stream beside these launches and joined before draft_finish_kernel.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -44,6 +45,25 @@ constexpr int kRejPer = 16;          // terms per thread per window
 constexpr uint32_t kRejWin = kRejThreads * kRejPer;
 constexpr uint32_t kNoEvent = 0xFFFFFFFFu;
 
+// Segments of the exact sums (the segmented form below): the first kSegHead terms of a row are
+// summed serially, the rest in segments of kSegLen.
+constexpr uint32_t kSegHead = 2048;
+constexpr uint32_t kSegLen = 512;                    // terms per segment after the head
+constexpr int kSegPer = kSegLen / 64;                // terms per lane when one wave sums a segment
+constexpr int kSegThreads = kSegLen / 4;             // 4 terms per thread in seg_xfer_kernel
+constexpr int kSegWaves = kSegThreads / 64;
+constexpr uint32_t kSegMax = (1u << 19) / kSegLen;  // segments per row (vocab <= 2048 + 2^19)
+static_assert(kSegLen % 256 == 0 && kSegPer % 4 == 0, "whole waves, 16-byte lane loads");
+static_assert(kSegHead % kSegThreads == 0 && kSegMax % kSegThreads == 0, "whole per-thread strides");
+// draft_exp_kernel's blocks also form the segments' double sums: block 0 covers the head,
+// block c >= 1 the segments 4 (c - 1) .. 4 (c - 1) + 3
+static_assert(kDraftChunk == kSegHead && kDraftChunk % kSegLen == 0 && kSegLen % kDraftThreads == 0,
+              "a draft chunk is the head or whole segments");
+
+__host__ __device__ inline uint32_t seg_count(uint32_t n) {
+    return n > kSegHead ? (n - kSegHead + kSegLen - 1) / kSegLen : 0u;
+}
+
 struct DraftPos {
     const float* target;  // row of vocab logits
     const float* draft;
@@ -62,6 +82,7 @@ struct DraftArgs {
     float* e;                     // [2P][vocab] expf(l / T - max)
     uint32_t* flags;              // [2P] bit 0: a NaN term
     float* sums;                  // [2P] compute_softmax sums
+    double* seg_d;                // [2P][segments + 1] double sums of the head and each segment
     uint32_t* rej;                // [64][4] {accepted, token, fallback, valid}
     DraftPos pos[TWD_MAX_ROWS];
 };
@@ -129,6 +150,8 @@ __global__ __launch_bounds__(kDraftThreads) void draft_exp_kernel(DraftArgs a) {
     for (int w = 1; w < kDraftThreads / 64; ++w) mx = red[w] > mx ? red[w] : mx;
     bool nan = false;
     float* e = a.e + static_cast<size_t>(r) * a.estride;
+    constexpr int kSegsPerChunk = kDraftChunk / kSegLen;
+    double ds[kSegsPerChunk] = {};  // this thread's share of each segment's double sum
 #pragma unroll
     for (int it = 0; it < kDraftPer; ++it) {
         const uint32_t j = base + it * kDraftThreads;
@@ -137,10 +160,36 @@ __global__ __launch_bounds__(kDraftThreads) void draft_exp_kernel(DraftArgs a) {
             const float v = expf_libm<true>(x - mx);  // std::exp(float) of speculator.cpp:23
             nan |= (v != v);
             e[j] = v;
+            ds[it * kDraftThreads / kSegLen] += static_cast<double>(v);
         }
+    }
+    // the segments' double sums, which only predict binades (any order will do)
+    __shared__ double dsw[kDraftThreads / 64][kSegsPerChunk];
+#pragma unroll
+    for (int k = 0; k < kSegsPerChunk; ++k) {
+        const double w = wave_reduce(ds[k], 0.0, [](double u, double v) { return u + v; });
+        if ((threadIdx.x & 63) == 0) dsw[threadIdx.x >> 6][k] = w;
     }
     if (__syncthreads_or(nan) && threadIdx.x == 0)
         __hip_atomic_fetch_or(a.flags + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x < kSegsPerChunk) {
+        const uint32_t k = threadIdx.x, nseg = seg_count(a.vocab);
+        double t = 0.0;
+#pragma unroll
+        for (int w = 0; w < kDraftThreads / 64; ++w) t += dsw[w][k];
+        double* d = a.seg_d + static_cast<size_t>(r) * (nseg + 1);
+        if (blockIdx.x == 0) {  // the head: the four parts together
+            double h = 0.0;
+#pragma unroll
+            for (int q = 0; q < kSegsPerChunk; ++q)
+#pragma unroll
+                for (int w = 0; w < kDraftThreads / 64; ++w) h += dsw[w][q];
+            if (k == 0) d[0] = h;
+        } else {
+            const uint32_t sg = (blockIdx.x - 1) * kSegsPerChunk + k;
+            if (sg < nseg) d[1 + sg] = t;
+        }
+    }
 }
 
 // ---- exact sequential fp32 summation ---------------------------------------------------------
@@ -501,32 +550,24 @@ __device__ __forceinline__ void load_row(const float* row, uint32_t j0, float (&
 //
 // block_seq_sum runs one row on one CU. Here a row's terms after the serial head are cut into
 // segments of kSegLen, and three launches sum them exactly:
-//   seg_dsum_kernel  (segment x row blocks): each segment's sum in double, and the head's;
+//   double sums      (segment x row blocks): each segment's sum in double, and the head's
+//                    (seg_dsum_kernel; for the softmax rows draft_exp_kernel forms them, for
+//                    the residual seg_ratio_dsum_kernel);
 //   seg_xfer_kernel  (segment x row blocks): the double prefix D before the segment predicts the
 //                    binade of the fp32 running sum there. For that binade and its nearer
 //                    neighbour the segment's terms become transfer functions (as in a window of
-//                    block_seq_sum) and their ordered composition is the segment's record;
-//   a chain kernel   (one block per row): the serial head with block_seq_sum, then a walk by one
-//                    thread over the records: when the exact sum S at a segment start lies in one
-//                    of the record's two binades, and the composed increment keeps it there (and
-//                    below a stop threshold), S jumps to the segment's end in a few instructions;
-//                    otherwise (a binade change, a wrong prediction, the stop) the whole block
-//                    sums that one segment exactly with block_seq_sum, and the walk resumes.
+//                    block_seq_sum) and their ordered composition is the segment's record. An
+//                    extra block per row adds the head serially;
+//   a chain kernel   (one block per row): from the head's sum, wave 0 walks the records 64 at
+//                    a time: when the exact sum S at a segment start lies in one of the record's
+//                    two binades, and the composed increment keeps it there (and below a stop
+//                    threshold), S jumps to the segment's end; otherwise (a binade change, a
+//                    wrong prediction, the stop) the wave sums that one segment exactly with
+//                    wave_seg_sum, and the walk resumes.
 // A prediction only decides which transfer functions are ready; the walk checks every record
 // against the exact S, so a wrong prediction costs one exact segment, never a wrong sum. No
 // block waits on another: the launches are ordered on the stream.
-constexpr uint32_t kSegHead = kSerialUntil;  // terms summed serially at the start
-constexpr uint32_t kSegLen = 512;                    // terms per segment after the head
-constexpr int kSegPer = kSegLen / 64;                // terms per lane when one wave sums a segment
-constexpr int kSegThreads = kSegLen / 4;             // 4 terms per thread in seg_xfer_kernel
-constexpr int kSegWaves = kSegThreads / 64;
-constexpr uint32_t kSegMax = (1u << 19) / kSegLen;  // segments per row (vocab <= 2048 + 2^19)
-static_assert(kSegLen % 256 == 0 && kSegPer % 4 == 0, "whole waves, 16-byte lane loads");
-static_assert(kSegHead % kSegThreads == 0 && kSegMax % kSegThreads == 0, "whole per-thread strides");
-
-__host__ __device__ inline uint32_t seg_count(uint32_t n) {
-    return n > kSegHead ? (n - kSegHead + kSegLen - 1) / kSegLen : 0u;
-}
+static_assert(kSegHead == kSerialUntil, "the head is the serial start");
 
 struct SegRec {
     int E[2];   // the two candidate binades (exponents of S's leading bit; -126: below 2^-125)
@@ -581,12 +622,10 @@ __device__ __forceinline__ double seg_block_sum(double v, double* red) {
     return t;
 }
 
-// grid (1 + segments, rows): block 0 the head [0, kSegHead), block s the segment s - 1
+// Block b of row `row`: b = 0 the head [0, kSegHead), b = s + 1 the segment s
 template <class Src>
-__global__ __launch_bounds__(kSegThreads) void seg_dsum_kernel(Src src, uint32_t n, double* d) {
-    __shared__ double red[kSegWaves];
-    const uint32_t row = blockIdx.y, b = blockIdx.x;
-    if (!src.active(row)) return;  // the whole block
+__device__ __forceinline__ void seg_dsum_block(const Src& src, uint32_t row, uint32_t b, uint32_t n, double* d,
+                                               double* red) {
     const uint32_t nseg = seg_count(n);
     const uint32_t lo = b == 0 ? 0u : kSegHead + (b - 1) * kSegLen;
     const uint32_t hi = b == 0 ? min(n, kSegHead) : min(n, lo + kSegLen);
@@ -607,6 +646,15 @@ __global__ __launch_bounds__(kSegThreads) void seg_dsum_kernel(Src src, uint32_t
     }
     t = seg_block_sum(t, red);
     if (threadIdx.x == 0) d[static_cast<size_t>(row) * (nseg + 1) + b] = t;
+}
+
+// grid (1 + segments, rows): block 0 the head, block s + 1 the segment s
+template <class Src>
+__global__ __launch_bounds__(kSegThreads) void seg_dsum_kernel(Src src, uint32_t n, double* d) {
+    __shared__ double red[kSegWaves];
+    const uint32_t row = blockIdx.y;
+    if (!src.active(row)) return;  // the whole block
+    seg_dsum_block(src, row, blockIdx.x, n, d, red);
 }
 
 // grid (1 + segments, rows): block 0 the serial head's sum (and its stop, with want_stop) into
@@ -911,11 +959,8 @@ __global__ __launch_bounds__(kRejThreads) void seg_sum_kernel(DraftArgs a, const
     if (threadIdx.x == 0) a.sums[r] = s;
 }
 
-// The ratio test of each position with draft probabilities (speculator.cpp:83-92): an accepted
-// draft is final; a rejected one is marked for the residual draw.
-__global__ void draft_ratio_kernel(DraftArgs a, uint32_t* live) {
-    const uint32_t pi = blockIdx.x * blockDim.x + threadIdx.x;
-    if (pi >= a.npos) return;
+// The ratio test of position pi (speculator.cpp:83-92); *dt_out receives the draft token.
+__device__ __forceinline__ bool draft_accepts(const DraftArgs& a, uint32_t pi, uint32_t* dt_out) {
     const DraftPos& P = a.pos[pi];
     const uint32_t V = a.vocab;
     const float* et = a.e + static_cast<size_t>(2 * pi) * a.estride;
@@ -927,16 +972,32 @@ __global__ void draft_ratio_kernel(DraftArgs a, uint32_t* live) {
     const float p_val = dt < V ? et[dt] * inv_p : 0.0f;
     const float q_val = dt < V ? ed[dt] * inv_q : 0.0f;
     const float r = (q_val > 1e-12f) ? (p_val / q_val) : 1.0f;
-    uint32_t* out = a.rej + P.position * 4;
-    if (P.u1 <= r) {
-        out[0] = 1u;
-        out[1] = dt;
-        out[2] = 0u;
-        out[3] = 1u;
-        live[pi] = 0u;
-    } else {
-        live[pi] = 1u;
+    *dt_out = dt;
+    return P.u1 <= r;
+}
+
+// The residual's double segment sums, grid (1 + segments, P), each block first repeating its
+// position's ratio test (every block gets the same answer): an accepted draft is final (block 0
+// records it) and the position's blocks stop; a rejected one is marked live for the residual
+// draw (speculator.cpp:94-116).
+__global__ __launch_bounds__(kSegThreads) void seg_ratio_dsum_kernel(DraftArgs a, uint32_t* live, double* d) {
+    __shared__ double red[kSegWaves];
+    const uint32_t pi = blockIdx.y;
+    uint32_t dt = 0;
+    const bool accepted = draft_accepts(a, pi, &dt);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        if (accepted) {
+            uint32_t* out = a.rej + a.pos[pi].position * 4;
+            out[0] = 1u;
+            out[1] = dt;
+            out[2] = 0u;
+            out[3] = 1u;
+        }
+        live[pi] = accepted ? 0u : 1u;
     }
+    if (accepted) return;  // the whole block
+    const SegSrcResidual src{a.e, a.estride, a.sums, live};  // terms only: live is not read here
+    seg_dsum_block(src, pi, blockIdx.x, a.vocab, d, red);
 }
 
 // The residual (p - q)+ of a rejected position (speculator.cpp:94-116): its sum, then the first
@@ -1272,6 +1333,7 @@ int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab
     a.flags = sel->draft.flags;
     a.rej = sel->draft.rej;
     a.sums = sel->draft.sums;
+    a.seg_d = sel->draft.seg_d;
     sel->draft.last_npos = a.npos;
     for (uint32_t i = 0; i < a.npos; ++i) sel->draft.last_pos[i] = a.pos[i].position;
     const dim3 grid(a.parts, 2 * a.npos);
@@ -1284,13 +1346,11 @@ int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab
     SegRec* seg_rec = static_cast<SegRec*>(sel->draft.seg_rec);
     const SegSrcSoftmax src_e{a.e, a.estride, a.flags};
     SegHead* seg_head = static_cast<SegHead*>(ds.seg_head);
-    seg_dsum_kernel<<<dim3(nseg + 1, 2 * a.npos), kSegThreads, 0, s>>>(src_e, vocab, seg_d);
     seg_xfer_kernel<<<dim3(nseg + 1, 2 * a.npos), kSegThreads, 0, s>>>(src_e, vocab, seg_d, seg_rec, 0.0f, 0u,
                                                                       seg_head);
     seg_sum_kernel<<<2 * a.npos, kRejThreads, 0, s>>>(a, seg_rec, seg_head);
-    draft_ratio_kernel<<<1, 64, 0, s>>>(a, ds.live);
+    seg_ratio_dsum_kernel<<<dim3(nseg + 1, a.npos), kSegThreads, 0, s>>>(a, ds.live, seg_d);
     const SegSrcResidual src_r{a.e, a.estride, a.sums, ds.live};
-    seg_dsum_kernel<<<dim3(nseg + 1, a.npos), kSegThreads, 0, s>>>(src_r, vocab, seg_d);
     seg_xfer_kernel<<<dim3(nseg + 1, a.npos), kSegThreads, 0, s>>>(src_r, vocab, seg_d, seg_rec, 0.0f, 0u, seg_head);
     seg_residual_kernel<<<a.npos, kRejThreads, 0, s>>>(a, ds.live, seg_rec, seg_head);
     TWD_HIP(hipStreamWaitEvent(s, ds.join, 0));  // the selector's tokens
