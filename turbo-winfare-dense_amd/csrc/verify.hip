@@ -264,6 +264,22 @@ __device__ __forceinline__ Xfer xfer_wave_scan(Xfer v) {
     return v;
 }
 
+// Inclusive scan of the lanes' increments under saturating addition, lane order, by the DPP
+// steps of xfer_wave_scan (lanes outside a step's source row take 0).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t inc_dpp(uint32_t x) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, ROW_MASK, 0xF, false));
+}
+__device__ __forceinline__ uint32_t inc_wave_scan(uint32_t v) {
+    v = sat_add(inc_dpp<kDppRowShr + 1, 0xF>(v), v);
+    v = sat_add(inc_dpp<kDppRowShr + 2, 0xF>(v), v);
+    v = sat_add(inc_dpp<kDppRowShr + 4, 0xF>(v), v);
+    v = sat_add(inc_dpp<kDppRowShr + 8, 0xF>(v), v);
+    v = sat_add(inc_dpp<kDppRowBcast15, 0xA>(v), v);
+    v = sat_add(inc_dpp<kDppRowBcast31, 0xC>(v), v);
+    return v;
+}
+
 __device__ __forceinline__ Xfer xfer_shfl(const Xfer& x, int src) {
     return Xfer{static_cast<uint32_t>(__shfl(x.inc0, src)), static_cast<uint32_t>(__shfl(x.inc1, src)),
                 static_cast<uint32_t>(__shfl(x.out, src))};
@@ -789,17 +805,36 @@ __device__ float wave_seg_sum(Load load, uint32_t n, uint32_t k0, uint32_t k1, f
             Tu = t <= 0.0 ? 0u : (t >= 4294967295.0 ? 0xFFFFFFFFu : static_cast<uint32_t>(t));
         }
         uint32_t kk[kSegPer], kd[kSegPer];
-        Xfer t = xfer_id();
+        bool tie = false;
 #pragma unroll
         for (int q = 0; q < kSegPer; ++q) {
             split_term(j0 + q >= kc ? a[q] : 0.0f, E, kk[q], kd[q]);
-            t = xfer_then(t, term_xfer(kk[q], kd[q]));
+            tie = tie || kd[q] == 2u;
         }
-        const Xfer incl = xfer_wave_scan(t);
-        Xfer ex = xfer_shfl_up(incl, 1);
-        if (lane == 0) ex = xfer_id();
-        uint32_t R = sat_add(B, p0 ? ex.inc1 : ex.inc0);
-        uint32_t par = (ex.out >> p0) & 1u;
+        uint32_t R, Rend, par = 0;  // R: this lane's start; Rend: its end (lane 63: the wave's)
+        if (__ballot(tie) == 0) {
+            // no exact half-way case in this pass: every increment is k + kind whatever the
+            // parity, so a saturating prefix sum of the increments stands in for the scan of
+            // transfer functions, at about half its cost
+            uint32_t tot = 0;
+#pragma unroll
+            for (int q = 0; q < kSegPer; ++q) tot = sat_add(tot, kk[q] + kd[q]);
+            const uint32_t incl = inc_wave_scan(tot);
+            uint32_t ex = static_cast<uint32_t>(__shfl_up(incl, 1));
+            if (lane == 0) ex = 0u;
+            R = sat_add(B, ex);
+            Rend = sat_add(B, incl);
+        } else {
+            Xfer t = xfer_id();
+#pragma unroll
+            for (int q = 0; q < kSegPer; ++q) t = xfer_then(t, term_xfer(kk[q], kd[q]));
+            const Xfer incl = xfer_wave_scan(t);
+            Xfer ex = xfer_shfl_up(incl, 1);
+            if (lane == 0) ex = xfer_id();
+            R = sat_add(B, p0 ? ex.inc1 : ex.inc0);
+            par = (ex.out >> p0) & 1u;
+            Rend = sat_add(B, p0 ? incl.inc1 : incl.inc0);
+        }
         uint32_t ev = kNoEvent, R_before = R;
         bool live = R < kL;
 #pragma unroll
@@ -821,8 +856,7 @@ __device__ float wave_seg_sum(Load load, uint32_t n, uint32_t k0, uint32_t k1, f
         }
         // the earliest event is the lowest lane's (lanes hold increasing indices)
         const uint64_t m = __ballot(ev != kNoEvent);
-        if (m == 0) {  // no event: lane 63's inclusive transfer gives the segment's end
-            const uint32_t Rend = sat_add(B, p0 ? incl.inc1 : incl.inc0);
+        if (m == 0) {  // no event: lane 63's end is the segment's
             S = ldexpf(static_cast<float>(__shfl(Rend, 63)), E - 23);
             break;
         }
