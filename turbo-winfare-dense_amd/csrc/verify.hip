@@ -804,27 +804,35 @@ __device__ float wave_seg_sum(Load load, uint32_t n, uint32_t k0, uint32_t k1, f
             const double t = ceil(ldexp(static_cast<double>(thr), 23 - E));
             Tu = t <= 0.0 ? 0u : (t >= 4294967295.0 ? 0xFFFFFFFFu : static_cast<uint32_t>(t));
         }
+        // Each term in units of u = 2^(E - 23): x = a / u is exact (a power-of-two scaling of a
+        // value with at most 24 significant bits; an x that underflows is far below 1/2 and
+        // one that overflows saturates), and so is x - floor(x). The pass is tie-free when no
+        // x lies exactly half-way between integers; then every increment is rint(x), whatever
+        // the parity of S / u.
         uint32_t kk[kSegPer], kd[kSegPer];
         bool tie = false;
 #pragma unroll
         for (int q = 0; q < kSegPer; ++q) {
-            split_term(j0 + q >= kc ? a[q] : 0.0f, E, kk[q], kd[q]);
-            tie = tie || kd[q] == 2u;
+            const float x = ldexpf(j0 + q >= kc ? a[q] : 0.0f, 23 - E);
+            tie = tie || (x - floorf(x) == 0.5f);
+            kk[q] = static_cast<uint32_t>(fminf(rintf(x), 0x1p30f));  // saturated at kSat
+            kd[q] = 0u;
         }
         uint32_t R, Rend, par = 0;  // R: this lane's start; Rend: its end (lane 63: the wave's)
         if (__ballot(tie) == 0) {
-            // no exact half-way case in this pass: every increment is k + kind whatever the
-            // parity, so a saturating prefix sum of the increments stands in for the scan of
-            // transfer functions, at about half its cost
+            // no exact half-way case in this pass: a saturating prefix sum of the increments
+            // stands in for the scan of transfer functions, at about half its cost
             uint32_t tot = 0;
 #pragma unroll
-            for (int q = 0; q < kSegPer; ++q) tot = sat_add(tot, kk[q] + kd[q]);
+            for (int q = 0; q < kSegPer; ++q) tot = sat_add(tot, kk[q]);
             const uint32_t incl = inc_wave_scan(tot);
             uint32_t ex = static_cast<uint32_t>(__shfl_up(incl, 1));
             if (lane == 0) ex = 0u;
             R = sat_add(B, ex);
             Rend = sat_add(B, incl);
         } else {
+#pragma unroll
+            for (int q = 0; q < kSegPer; ++q) split_term(j0 + q >= kc ? a[q] : 0.0f, E, kk[q], kd[q]);
             Xfer t = xfer_id();
 #pragma unroll
             for (int q = 0; q < kSegPer; ++q) t = xfer_then(t, term_xfer(kk[q], kd[q]));
