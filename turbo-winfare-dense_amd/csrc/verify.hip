@@ -280,6 +280,12 @@ __device__ __forceinline__ uint32_t inc_wave_scan(uint32_t v) {
     return v;
 }
 
+// Lane l's value, for a wave-uniform l: a register read, where a shuffle is an LDS round trip.
+__device__ __forceinline__ uint32_t lane_u32(uint32_t v, int l) {
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), l));
+}
+__device__ __forceinline__ float lane_f32(float v, int l) { return __uint_as_float(lane_u32(__float_as_uint(v), l)); }
+
 __device__ __forceinline__ Xfer xfer_shfl(const Xfer& x, int src) {
     return Xfer{static_cast<uint32_t>(__shfl(x.inc0, src)), static_cast<uint32_t>(__shfl(x.inc1, src)),
                 static_cast<uint32_t>(__shfl(x.out, src))};
@@ -865,14 +871,14 @@ __device__ float wave_seg_sum(Load load, uint32_t n, uint32_t k0, uint32_t k1, f
         // the earliest event is the lowest lane's (lanes hold increasing indices)
         const uint64_t m = __ballot(ev != kNoEvent);
         if (m == 0) {  // no event: lane 63's end is the segment's
-            S = ldexpf(static_cast<float>(__shfl(Rend, 63)), E - 23);
+            S = ldexpf(static_cast<float>(lane_u32(Rend, 63)), E - 23);
             break;
         }
         const int owner = __ffsll(static_cast<long long>(m)) - 1;
-        const uint32_t e = __shfl(ev, owner);
+        const uint32_t e = lane_u32(ev, owner);
         const uint32_t j = e >> 1;
         if (e & 1u) {  // reaches thr, no binade change before it
-            S = ldexpf(static_cast<float>(__shfl(R, owner)), E - 23);
+            S = ldexpf(static_cast<float>(lane_u32(R, owner)), E - 23);
             stop = j;
             break;
         }
@@ -880,8 +886,8 @@ __device__ float wave_seg_sum(Load load, uint32_t n, uint32_t k0, uint32_t k1, f
         float aj = 0.0f;
 #pragma unroll
         for (int q = 0; q < kSegPer; ++q) aj = (j0 + q == j) ? a[q] : aj;
-        aj = __shfl(aj, owner);
-        const float s_new = ldexpf(static_cast<float>(__shfl(R_before, owner)), E - 23) + aj;
+        aj = lane_f32(aj, owner);
+        const float s_new = ldexpf(static_cast<float>(lane_u32(R_before, owner)), E - 23) + aj;
         S = s_new;
         if (want_stop && s_new >= thr) {
             stop = j;
@@ -934,18 +940,33 @@ __device__ float seg_chain(Load load, Term term, uint32_t n, float S, float thr,
                     c = R.E[0] == E ? 0 : (R.E[1] == E ? 1 : -1);
                     if (c >= 0) f = R.f[c];
                 }
-                const Xfer incl = xfer_wave_scan(f);
-                Xfer excl = xfer_shfl_up(incl, 1);
-                if (lane == 0) excl = xfer_id();
-                const uint32_t b0 = B + (p0 ? excl.inc1 : excl.inc0);  // < 2^24 up to the first bad lane
-                const uint32_t b1 = B + (p0 ? incl.inc1 : incl.inc0);
+                // b0, b1: S / u at the lane's segment start and end (< 2^24 up to the first bad
+                // lane). A record is parity-free when its segment holds no exact half-way
+                // term: the same increment for either parity of S / u. With every record
+                // parity-free a saturating prefix sum of the increments stands in for the scan
+                // of transfer functions.
+                const bool pfree = f.inc0 == f.inc1 && f.out == ((f.inc0 & 1u) ? 1u : 2u);
+                uint32_t b0, b1;
+                if (__ballot(!pfree) == 0) {
+                    const uint32_t incl = inc_wave_scan(f.inc0);
+                    uint32_t excl = static_cast<uint32_t>(__shfl_up(incl, 1));
+                    if (lane == 0) excl = 0u;
+                    b0 = B + excl;
+                    b1 = B + incl;
+                } else {
+                    const Xfer incl = xfer_wave_scan(f);
+                    Xfer excl = xfer_shfl_up(incl, 1);
+                    if (lane == 0) excl = xfer_id();
+                    b0 = B + (p0 ? excl.inc1 : excl.inc0);
+                    b1 = B + (p0 ? incl.inc1 : incl.inc0);
+                }
                 const float Se = ldexpf(static_cast<float>(b1), E - 23);
                 const bool good = c >= 0 && b1 < kL && !(want_stop && Se >= thr);
                 const uint64_t bad = __ballot(!good);
                 const uint32_t first = bad ? static_cast<uint32_t>(__ffsll(static_cast<long long>(bad)) - 1) : 64u;
                 // every lane up to the first bad one starts where the records before it end
                 if (static_cast<uint32_t>(lane) <= first && idx < nseg) ch.start[idx] = ldexpf(static_cast<float>(b0), E - 23);
-                if (first > 0) S = __shfl(Se, static_cast<int>(first) - 1);
+                if (first > 0) S = lane_f32(Se, static_cast<int>(first) - 1);
                 t += first;
                 if (first < 64 || t >= nseg) break;
             }
