@@ -825,7 +825,8 @@ __device__ float wave_seg_sum(Load load, uint32_t n, uint32_t k0, uint32_t k1, f
             kd[q] = 0u;
         }
         uint32_t R, Rend, par = 0;  // R: this lane's start; Rend: its end (lane 63: the wave's)
-        if (__ballot(tie) == 0) {
+        const bool fast = __ballot(tie) == 0;
+        if (fast) {
             // no exact half-way case in this pass: a saturating prefix sum of the increments
             // stands in for the scan of transfer functions, at about half its cost
             uint32_t tot = 0;
@@ -851,22 +852,42 @@ __device__ float wave_seg_sum(Load load, uint32_t n, uint32_t k0, uint32_t k1, f
         }
         uint32_t ev = kNoEvent, R_before = R;
         bool live = R < kL;
+        if (fast) {
+            // the replay with parity-free increments. The terms outside [kc, k1) are zeros: one
+            // can neither leave the binade nor be the first to reach thr (S < thr at a pass's
+            // start), so they need no range test here.
 #pragma unroll
-        for (int q = 0; q < kSegPer; ++q) {
-            const uint32_t j = j0 + q;
-            const uint32_t d = term_inc(kk[q], kd[q], par);
-            const bool go = live && j >= kc && j < k1;
-            const bool cross = go && (R + d >= kL);
-            const bool adv = go && !cross;
-            if (cross) {
-                ev = 2 * j;
-                R_before = R;
+            for (int q = 0; q < kSegPer; ++q) {
+                const uint32_t j = j0 + q, d = kk[q];
+                const bool cross = live && (R + d >= kL);
+                if (cross) {
+                    ev = 2 * j;
+                    R_before = R;
+                }
+                const bool adv = live && !cross;
+                R = adv ? R + d : R;
+                const bool hit = adv && R >= Tu;
+                if (hit) ev = 2 * j + 1;
+                live = adv && !hit;
             }
-            R = adv ? R + d : R;
-            par = adv ? ((par + d) & 1u) : par;
-            const bool hit = adv && R >= Tu;
-            if (hit) ev = 2 * j + 1;
-            live = live && !cross && !hit;
+        } else {
+#pragma unroll
+            for (int q = 0; q < kSegPer; ++q) {
+                const uint32_t j = j0 + q;
+                const uint32_t d = term_inc(kk[q], kd[q], par);
+                const bool go = live && j >= kc && j < k1;
+                const bool cross = go && (R + d >= kL);
+                const bool adv = go && !cross;
+                if (cross) {
+                    ev = 2 * j;
+                    R_before = R;
+                }
+                R = adv ? R + d : R;
+                par = adv ? ((par + d) & 1u) : par;
+                const bool hit = adv && R >= Tu;
+                if (hit) ev = 2 * j + 1;
+                live = live && !cross && !hit;
+            }
         }
         // the earliest event is the lowest lane's (lanes hold increasing indices)
         const uint64_t m = __ballot(ev != kNoEvent);
