@@ -815,23 +815,36 @@ __device__ float wave_seg_sum(Load load, uint32_t n, uint32_t k0, uint32_t k1, f
         // one that overflows saturates), and so is x - floor(x). The pass is tie-free when no
         // x lies exactly half-way between integers; then every increment is rint(x), whatever
         // the parity of S / u.
-        uint32_t kk[kSegPer], kd[kSegPer];
-        bool tie = false;
+        // The same for the next binade up (units 2u), where the sum goes at a crossing: k2 and
+        // its prefix sums let the pass finish the segment after the crossing term itself.
+        uint32_t kk[kSegPer], kd[kSegPer], k2[kSegPer];
+        bool tie = false, tie2 = false;
 #pragma unroll
         for (int q = 0; q < kSegPer; ++q) {
-            const float x = ldexpf(j0 + q >= kc ? a[q] : 0.0f, 23 - E);
+            const float aq = j0 + q >= kc ? a[q] : 0.0f;
+            const float x = ldexpf(aq, 23 - E), x2 = ldexpf(aq, 22 - E);
             tie = tie || (x - floorf(x) == 0.5f);
+            tie2 = tie2 || (x2 - floorf(x2) == 0.5f);
             kk[q] = static_cast<uint32_t>(fminf(rintf(x), 0x1p30f));  // saturated at kSat
+            k2[q] = static_cast<uint32_t>(fminf(rintf(x2), 0x1p30f));
             kd[q] = 0u;
         }
         uint32_t R, Rend, par = 0;  // R: this lane's start; Rend: its end (lane 63: the wave's)
+        uint32_t incl2 = 0u, total2 = kSat;
         const bool fast = __ballot(tie) == 0;
         if (fast) {
             // no exact half-way case in this pass: a saturating prefix sum of the increments
             // stands in for the scan of transfer functions, at about half its cost
-            uint32_t tot = 0;
+            uint32_t tot = 0, tot2 = 0;
 #pragma unroll
-            for (int q = 0; q < kSegPer; ++q) tot = sat_add(tot, kk[q]);
+            for (int q = 0; q < kSegPer; ++q) {
+                tot = sat_add(tot, kk[q]);
+                tot2 = sat_add(tot2, k2[q]);
+            }
+            if (__ballot(tie2) == 0) {
+                incl2 = inc_wave_scan(tot2);
+                total2 = lane_u32(incl2, 63);  // below kSat: every prefix of it is exact
+            }
             const uint32_t incl = inc_wave_scan(tot);
             uint32_t ex = static_cast<uint32_t>(__shfl_up(incl, 1));
             if (lane == 0) ex = 0u;
@@ -916,6 +929,31 @@ __device__ float wave_seg_sum(Load load, uint32_t n, uint32_t k0, uint32_t k1, f
         }
         kc = j + 1;
         if (kc >= k1) break;
+        if (total2 < kSat) {
+            // S is now in binade E + 1 (checked): with no exact half-way term there and no
+            // saturation, the terms after j add sum2 = (the owner lane's terms after j) + (the
+            // lanes after it) units of 2u. If that stays in the binade and below thr, the
+            // segment ends here; otherwise the next pass takes it from kc.
+            const uint32_t sb2 = __float_as_uint(S), sf2 = sb2 >> 23;
+            const int E2 = sf2 ? static_cast<int>(sf2) - 127 : -126;
+            if (E2 == E + 1) {
+                const uint32_t B2 = sf2 ? ((sb2 & 0x7FFFFFu) | 0x800000u) : sb2;
+                uint32_t mine = 0u;
+#pragma unroll
+                for (int q = 0; q < kSegPer; ++q) mine += j0 + q > j ? k2[q] : 0u;
+                const uint32_t sum2 = lane_u32(mine, owner) + (total2 - lane_u32(incl2, owner));
+                const uint32_t Rend2 = B2 + sum2;  // B2 < 2^24, sum2 < 2^30
+                uint32_t Tu2 = 0xFFFFFFFFu;
+                if (want_stop) {
+                    const double t2 = ceil(ldexp(static_cast<double>(thr), 23 - E2));
+                    Tu2 = t2 <= 0.0 ? 0u : (t2 >= 4294967295.0 ? 0xFFFFFFFFu : static_cast<uint32_t>(t2));
+                }
+                if (Rend2 < kL && Rend2 < Tu2) {
+                    S = ldexpf(static_cast<float>(Rend2), E2 - 23);
+                    break;
+                }
+            }
+        }
     }
     if (want_stop) *stop_at = stop;
     return S;
