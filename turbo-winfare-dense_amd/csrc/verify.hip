@@ -47,7 +47,7 @@ constexpr uint32_t kNoEvent = 0xFFFFFFFFu;
 
 // Segments of the exact sums (the segmented form below): the first kSegHead terms of a row are
 // summed serially, the rest in segments of kSegLen.
-constexpr uint32_t kSegHead = 2048;
+constexpr uint32_t kSegHead = 2048;                   // a multiple of kSegLen, <= kDraftChunk
 constexpr uint32_t kSegLen = 512;                    // terms per segment after the head
 constexpr int kSegPer = kSegLen / 64;                // terms per lane when one wave sums a segment
 constexpr int kSegThreads = kSegLen / 4;             // 4 terms per thread in seg_xfer_kernel
@@ -55,10 +55,12 @@ constexpr int kSegWaves = kSegThreads / 64;
 constexpr uint32_t kSegMax = (1u << 19) / kSegLen;  // segments per row (vocab <= 2048 + 2^19)
 static_assert(kSegLen % 256 == 0 && kSegPer % 4 == 0, "whole waves, 16-byte lane loads");
 static_assert(kSegHead % kSegThreads == 0 && kSegMax % kSegThreads == 0, "whole per-thread strides");
-// draft_exp_kernel's blocks also form the segments' double sums: block 0 covers the head,
-// block c >= 1 the segments 4 (c - 1) .. 4 (c - 1) + 3
-static_assert(kDraftChunk == kSegHead && kDraftChunk % kSegLen == 0 && kSegLen % kDraftThreads == 0,
-              "a draft chunk is the head or whole segments");
+// draft_exp_kernel's blocks also form the double sums of the head and the segments: a block's
+// kDraftChunk entries are kDraftChunk / kSegLen whole parts of kSegLen, the first
+// kSegHead / kSegLen parts of the row being the head's
+static_assert(kSegHead % kSegLen == 0 && kSegHead <= kDraftChunk && kDraftChunk % kSegLen == 0 &&
+                  kSegLen % kDraftThreads == 0,
+              "a draft chunk holds whole parts of the head or of segments");
 
 __host__ __device__ inline uint32_t seg_count(uint32_t n) {
     return n > kSegHead ? (n - kSegHead + kSegLen - 1) / kSegLen : 0u;
@@ -173,22 +175,22 @@ __global__ __launch_bounds__(kDraftThreads) void draft_exp_kernel(DraftArgs a) {
     if (__syncthreads_or(nan) && threadIdx.x == 0)
         __hip_atomic_fetch_or(a.flags + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (threadIdx.x < kSegsPerChunk) {
+        constexpr uint32_t kHeadParts = kSegHead / kSegLen;
         const uint32_t k = threadIdx.x, nseg = seg_count(a.vocab);
+        const uint32_t g = blockIdx.x * kSegsPerChunk + k;  // the part of the row
         double t = 0.0;
 #pragma unroll
         for (int w = 0; w < kDraftThreads / 64; ++w) t += dsw[w][k];
         double* d = a.seg_d + static_cast<size_t>(r) * (nseg + 1);
-        if (blockIdx.x == 0) {  // the head: the four parts together
+        if (blockIdx.x == 0 && k == 0) {  // the head: its parts together
             double h = 0.0;
 #pragma unroll
-            for (int q = 0; q < kSegsPerChunk; ++q)
+            for (uint32_t q = 0; q < kHeadParts; ++q)
 #pragma unroll
                 for (int w = 0; w < kDraftThreads / 64; ++w) h += dsw[w][q];
-            if (k == 0) d[0] = h;
-        } else {
-            const uint32_t sg = (blockIdx.x - 1) * kSegsPerChunk + k;
-            if (sg < nseg) d[1 + sg] = t;
+            d[0] = h;
         }
+        if (g >= kHeadParts && g - kHeadParts < nseg) d[1 + g - kHeadParts] = t;
     }
 }
 
@@ -589,7 +591,7 @@ __device__ __forceinline__ void load_row(const float* row, uint32_t j0, float (&
 // A prediction only decides which transfer functions are ready; the walk checks every record
 // against the exact S, so a wrong prediction costs one exact segment, never a wrong sum. No
 // block waits on another: the launches are ordered on the stream.
-static_assert(kSegHead == kSerialUntil, "the head is the serial start");
+static_assert(kSegHead <= kSerialUntil, "block_seq_sum adds a head in order");
 
 struct SegRec {
     int E[2];   // the two candidate binades (exponents of S's leading bit; -126: below 2^-125)
@@ -1343,7 +1345,7 @@ TWD_API int twd_sequential_sum(const float* terms, uint32_t n, float thr, float*
     if (!terms || !sum_out) return fail(TWD_E_INVALID, "null terms or sum_out");
     if (n == 0) return fail(TWD_E_INVALID, "n must be > 0");
     if ((reinterpret_cast<uintptr_t>(terms) & 15u) != 0) return fail(TWD_E_INVALID, "terms must be 16-byte aligned");
-    if (seg_count(n) > kSegMax) return fail(TWD_E_INVALID, "n above 2048 + 524288");
+    if (seg_count(n) > kSegMax) return fail(TWD_E_INVALID, "n above the segmented sums' limit (2^19 after the head)");
     const hipStream_t s = static_cast<hipStream_t>(stream);
     // one row's segment scratch, allocated on the first call and kept for the process
     static std::mutex mu;
