@@ -86,7 +86,9 @@ def _random_case(rng, vocab):
     return rows, drs, drafts, T, (1.0 if k == 0 else 0.9), k, int(rng.integers(0, 2**63))
 
 
-@pytest.mark.parametrize("vocab", [3000, 50000, V])
+# 1000: the serial head alone (no segment); 2049: one one-term segment; 3000 and 50000: a last
+# segment and a last exp block cut short; V: the config-4 rows
+@pytest.mark.parametrize("vocab", [1000, 2049, 3000, 50000, V])
 def test_verify_draft_random_vs_oracle(env, oracle, vocab):
     rng = np.random.default_rng(vocab)
     n_rej = n_sums = 0
