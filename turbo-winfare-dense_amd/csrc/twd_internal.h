@@ -281,6 +281,8 @@ struct DraftScratch {
     void* seg_rec = nullptr;   // [2 * TWD_MAX_ROWS][segments] segment records
     void* seg_head = nullptr;  // [2 * TWD_MAX_ROWS] the serial heads' sums
     uint32_t* live = nullptr;  // [TWD_MAX_ROWS] 1: the position's draft was rejected
+    uint64_t* fin_ctr = nullptr;  // [2] the residual launch's arrival counter (epoch-armed)
+    uint32_t fin_epoch = 0;       // the last call's epoch
     hipStream_t side = nullptr;  // twd_verify_draft's selection runs here, beside the draft chain
     hipEvent_t fork = nullptr, join = nullptr;
     size_t e_capacity = 0;

@@ -15,10 +15,10 @@
 //   seg_xfer_kernel, seg_sum_kernel: each softmax's sequential sum
 //   seg_ratio_dsum_kernel  the ratio tests, and each rejected position's segment double sums
 //   seg_xfer_kernel, seg_residual_kernel: each rejected position's residual sum and draw
-//   draft_finish_kernel  one thread: the accept chain over all positions, bonus, result
+//   (seg_residual_kernel's last block: the accept chain over all positions, bonus, result)
 // where P is the number of positions with a draft row. The target tokens of the other
 // positions, of the fallback and of the bonus row come from the selector (launch_select), run
-// on a side stream beside these launches and joined before draft_finish_kernel.
+// on a side stream beside these launches and joined before seg_residual_kernel.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -1127,12 +1127,70 @@ __global__ __launch_bounds__(kSegThreads) void seg_ratio_dsum_kernel(DraftArgs a
 // The residual (p - q)+ of a rejected position (speculator.cpp:94-116): its sum, then the first
 // index whose prefix reaches u2 * sum, found in the segment where the recorded starts straddle
 // it. One block per position; accepted positions return at once.
+__device__ void draft_finish_body(const uint32_t* row_tokens, uint32_t rows, const uint32_t* drafts, uint32_t nd,
+                                  uint64_t has_draft, const uint32_t* rej, twd_verify_result* v);
+
+__device__ __forceinline__ void seg_residual_block(const DraftArgs& a, uint32_t pi, const SegRec* rec,
+                                                   const SegHead* heads, SeqShared& sh, ChainShared& ch);
+
+struct DraftFinish {  // the accept chain's inputs: the residual launch's last block runs it
+    const uint32_t* row_tokens;  // the selector's tokens (joined before the launch)
+    uint32_t rows;
+    const uint32_t* drafts;
+    uint32_t nd;
+    uint64_t has_draft;
+    twd_verify_result* v;
+    unsigned long long* ctr;     // [2] arrival counter {arrivals << 32 | epoch} and its fallback
+    uint32_t epoch, next_epoch;  // this call's epoch (never 0) and the next call's
+};
+
+// Counts the calling block in (one thread). True in the last of the nb blocks to arrive. The
+// counter is armed with this call's epoch by the previous call's last block; when it is not
+// (the first call, a call that did not finish, a write from outside), the blocks count in on
+// the fallback word by compare-and-swap with the epoch attached, and every failed swap means
+// another block counted itself in, so that loop ends after at most nb tries.
+__device__ bool last_to_arrive(unsigned long long* ctr, uint32_t epoch, uint32_t next_epoch, uint32_t nb) {
+    const unsigned long long ep = epoch;
+    const unsigned long long old = __hip_atomic_fetch_add(ctr, 1ull << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bool last;
+    if ((old & 0xFFFFFFFFull) == ep && (old >> 32) < nb) {
+        last = (old >> 32) == nb - 1;
+    } else {
+        unsigned long long* c2 = ctr + 1;
+        unsigned long long cur = __hip_atomic_load(c2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), want;
+        do {
+            want = ((cur & 0xFFFFFFFFull) == ep) ? cur + (1ull << 32) : (ep | (1ull << 32));
+        } while (!__hip_atomic_compare_exchange_strong(c2, &cur, want, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT));
+        last = (want >> 32) == nb;
+    }
+    if (last)  // every block of this launch has added to ctr[0] by now: arm it for the next call
+        __hip_atomic_exchange(ctr, static_cast<unsigned long long>(next_epoch), __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+    return last;
+}
+
 __global__ __launch_bounds__(kRejThreads) void seg_residual_kernel(DraftArgs a, const uint32_t* live,
-                                                                   const SegRec* rec, const SegHead* heads) {
+                                                                   const SegRec* rec, const SegHead* heads,
+                                                                   DraftFinish f) {
     __shared__ SeqShared sh;
     __shared__ ChainShared ch;
     const uint32_t pi = blockIdx.x;
-    if (!live[pi]) return;  // the whole block
+    if (live[pi]) seg_residual_block(a, pi, rec, heads, sh, ch);  // block-uniform
+    // count in, the position's outcome (written above, or by seg_ratio_dsum_kernel) published
+    // first; the last block reads every outcome after an acquiring fence
+    if (threadIdx.x == 0) {
+        __threadfence();
+        if (last_to_arrive(f.ctr, f.epoch, f.next_epoch, gridDim.x)) {
+            __threadfence();
+            draft_finish_body(f.row_tokens, f.rows, f.drafts, f.nd, f.has_draft, a.rej, f.v);
+        }
+    }
+}
+
+// A rejected position's residual sum and draw (the body of seg_residual_kernel).
+__device__ __forceinline__ void seg_residual_block(const DraftArgs& a, uint32_t pi, const SegRec* rec,
+                                                   const SegHead* heads, SeqShared& sh, ChainShared& ch) {
     const DraftPos& P = a.pos[pi];
     const uint32_t V = a.vocab;
     const float* et = a.e + static_cast<size_t>(2 * pi) * a.estride;
@@ -1215,10 +1273,8 @@ __global__ __launch_bounds__(kRejThreads) void seg_array_kernel(const float* x, 
 // The accept chain of speculator.cpp:53-146 over per-position outcomes: rej[i] for positions
 // with draft rows (has_draft bit i), the selector's sampled token row_tok[i] otherwise, for the
 // fallback, and for the bonus row k.
-__global__ void draft_finish_kernel(const uint32_t* row_tokens, uint32_t rows, const uint32_t* drafts,
-                                    uint32_t nd, uint64_t has_draft, const uint32_t* rej,
-                                    twd_verify_result* v) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+__device__ void draft_finish_body(const uint32_t* row_tokens, uint32_t rows, const uint32_t* drafts, uint32_t nd,
+                                  uint64_t has_draft, const uint32_t* rej, twd_verify_result* v) {
     uint32_t n = 0, acc = 0, bonus = 0, sampled = 0;
     bool bad = false;
     const uint32_t k = nd < rows ? nd : rows;
@@ -1283,6 +1339,8 @@ int draft_scratch_reserve(DraftScratch* d, uint32_t vocab, uint32_t npos) {
     TWD_HIP(hipMalloc(&d->seg_rec, static_cast<size_t>(2) * TWD_MAX_ROWS * kSegMax * sizeof(SegRec)));
     TWD_HIP(hipMalloc(&d->seg_head, static_cast<size_t>(2) * TWD_MAX_ROWS * sizeof(SegHead)));
     TWD_HIP(hipMalloc(&d->live, TWD_MAX_ROWS * sizeof(uint32_t)));
+    TWD_HIP(hipMalloc(&d->fin_ctr, 2 * sizeof(uint64_t)));
+    TWD_HIP(hipMemset(d->fin_ctr, 0, 2 * sizeof(uint64_t)));  // epoch 0 is never a call's
     if (!d->side) {  // kept across growth: freed with the selector
         TWD_HIP(hipStreamCreateWithFlags(&d->side, hipStreamNonBlocking));
         TWD_HIP(hipEventCreateWithFlags(&d->fork, hipEventDisableTiming));
@@ -1301,6 +1359,7 @@ void draft_scratch_free(DraftScratch* d) {
     if (d->seg_rec) (void)hipFree(d->seg_rec);
     if (d->seg_head) (void)hipFree(d->seg_head);
     if (d->live) (void)hipFree(d->live);
+    if (d->fin_ctr) (void)hipFree(d->fin_ctr);
     const DraftScratch keep = *d;
     *d = DraftScratch{};
     d->side = keep.side;
@@ -1428,7 +1487,7 @@ int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab
 
     // target tokens for the positions without draft rows, the fallback and the bonus row: the
     // selection runs on the side stream, beside the draft chain below (which leaves most of
-    // the GPU idle), and joins it before draft_finish_kernel
+    // the GPU idle), and joins it before seg_residual_kernel, whose last block reads them
     const uint32_t used = (rows > k) ? k + 1 : k;
     twd_row_params rp[TWD_MAX_ROWS + 1];
     for (uint32_t i = 0; i < used; ++i) {
@@ -1476,10 +1535,12 @@ int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab
     seg_ratio_dsum_kernel<<<dim3(nseg + 1, a.npos), kSegThreads, 0, s>>>(a, ds.live, seg_d);
     const SegSrcResidual src_r{a.e, a.estride, a.sums, ds.live};
     seg_xfer_kernel<<<dim3(nseg + 1, a.npos), kSegThreads, 0, s>>>(src_r, vocab, seg_d, seg_rec, 0.0f, 0u, seg_head);
-    seg_residual_kernel<<<a.npos, kRejThreads, 0, s>>>(a, ds.live, seg_rec, seg_head);
-    TWD_HIP(hipStreamWaitEvent(s, ds.join, 0));  // the selector's tokens
-    draft_finish_kernel<<<1, 64, 0, s>>>(sel->scratch.verify_tokens, used, drafts, n_drafts, has,
-                                         a.rej, result);
+    TWD_HIP(hipStreamWaitEvent(s, ds.join, 0));  // the selector's tokens, read by the finish
+    ds.fin_epoch = ds.fin_epoch % 0x7FFFFFFFu + 1u;
+    const DraftFinish fin{sel->scratch.verify_tokens, used, drafts, n_drafts, has, result,
+                          reinterpret_cast<unsigned long long*>(ds.fin_ctr), ds.fin_epoch,
+                          ds.fin_epoch % 0x7FFFFFFFu + 1u};
+    seg_residual_kernel<<<a.npos, kRejThreads, 0, s>>>(a, ds.live, seg_rec, seg_head, fin);
     TWD_HIP(hipGetLastError());
     return TWD_OK;
 }
