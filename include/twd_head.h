@@ -365,6 +365,13 @@ TWD_API int twd_verify_draft(twd_selector* sel, const float* logits, uint32_t vo
 TWD_API int twd_sequential_sum(const float* terms, uint32_t n, float thr, float* sum_out,
                                uint32_t* stop_out, void* stream);
 
+/* No counterpart in the reference: the device address of the selector's draft-verify finish
+ * counter, for diagnostics and tests (NULL before the first twd_verify_draft call that had
+ * draft rows): the uint64 counter {arrivals << 32 | epoch}, then the uint64 fallback counter.
+ * The residual launch's blocks count in on it and its last block runs the accept chain; each
+ * call arms it for the next, and a call that finds it not armed for itself (a call that did not
+ * finish, a write from outside) counts in on the fallback word instead. */
+TWD_API void* twd_selector_verify_state(const twd_selector* sel);
 /* No counterpart in the reference: the fp32 softmax sums (compute_softmax, speculator.cpp:22-26)
  * of the last twd_verify_draft call on this selector that ran the rejection branch, for
  * diagnostics and tests. *n receives the number of positions that had draft rows; for each,

@@ -86,6 +86,47 @@ def _random_case(rng, vocab):
     return rows, drs, drafts, T, (1.0 if k == 0 else 0.9), k, int(rng.integers(0, 2**63))
 
 
+def test_verify_draft_after_finish_counter_left_stale(env, oracle):
+    # a plain host copy writes the residual launch's arrival counter (what a call that stopped
+    # part-way would leave, and arbitrary values); the next calls must still finish their
+    # accept chain in the right block, with the oracle's outcome
+    import ctypes
+    torch, dev, t, sel = env
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    hip.hipMemcpy.restype = ctypes.c_int
+    rng = np.random.default_rng(404)
+    cases = []
+    for _ in range(3):  # every position with a draft row, so that each call has the residual launch
+        rows, drs, dr, T, p, k, base = _random_case(rng, 5000)
+        drs = [d if d is not None else (0.5 * rows[min(i, len(rows) - 1)]).astype(np.float32)
+               for i, d in enumerate(drs)]
+        cases.append((rows, drs, dr, T, p, k, base))
+    wants = [oracle.verify_draft(dr, rows, drs, T, p, k, 1.0, base)
+             for rows, drs, dr, T, p, k, base in cases]
+    for w in wants:
+        w.pop("diag")
+    for (rows, drs, dr, T, p, k, base), w in zip(cases, wants):  # arms the counter
+        assert same(run_device(env, rows, drs, dr, T, p, k, 1.0, base), w)
+    state = t.twd.lib.twd_selector_verify_state(sel.handle)
+    assert state
+    cur = ctypes.c_uint64()
+    assert hip.hipMemcpy(ctypes.byref(cur), state, 8, 2) == 0
+    nxt = cur.value & 0xFFFFFFFF
+    assert cur.value >> 32 == 0 and nxt > 0  # armed for the next call's epoch
+    # a call of the previous epoch that stopped after two blocks, another epoch's count, all ones,
+    # and zero
+    for garbage in ((2 << 32) | (nxt - 1), (5 << 32) | (nxt + 77), 0xFFFFFFFFFFFFFFFF, 0):
+        torch.cuda.synchronize()
+        g = ctypes.c_uint64(garbage)
+        assert hip.hipMemcpy(state, ctypes.byref(g), 8, 1) == 0
+        for (rows, drs, dr, T, p, k, base), w in zip(cases, wants):  # that call and the next ones
+            got = run_device(env, rows, drs, dr, T, p, k, 1.0, base)
+            assert same(got, w), (hex(garbage), got, w)
+    assert hip.hipMemcpy(ctypes.byref(cur), state, 8, 2) == 0
+    assert cur.value >> 32 == 0 and cur.value & 0xFFFFFFFF != 0  # armed again
+
+
 # 1000: the serial head alone (no segment); 2049: one one-term segment; 3000 and 50000: a last
 # segment and a last exp block cut short; V: the config-4 rows
 @pytest.mark.parametrize("vocab", [1000, 2049, 3000, 50000, V])

@@ -1384,6 +1384,10 @@ using namespace twd;
 
 extern "C" {
 
+TWD_API void* twd_selector_verify_state(const twd_selector* sel) {
+    return sel ? static_cast<void*>(sel->draft.fin_ctr) : nullptr;
+}
+
 TWD_API int twd_verify_draft_sums(const twd_selector* sel, float* sums, uint32_t* positions,
                                   uint32_t capacity, uint32_t* n) {
     clear_error();

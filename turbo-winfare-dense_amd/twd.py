@@ -144,6 +144,7 @@ _SIGS = {
                                    C.POINTER(RowParams), _u64, _vp, _u32, _vp, _vp]),
     "twd_rejection_uniforms": (None, [_u64, C.POINTER(_f32), C.POINTER(_f32)]),
     "twd_verify_draft_sums": (C.c_int, [_vp, C.POINTER(_f32), C.POINTER(_u32), _u32, C.POINTER(_u32)]),
+    "twd_selector_verify_state": (_vp, [_vp]),
     "twd_probe_expf": (C.c_int, [_vp, _vp, _u64, _vp]),
     "twd_splitmix64": (_u64, [_u64]),
     "twd_seed_for": (_u64, [C.c_int, _u64, C.c_int]),
