@@ -681,26 +681,29 @@ __global__ __launch_bounds__(kSegThreads) void seg_dsum_kernel(Src src, uint32_t
     seg_dsum_block(src, row, blockIdx.x, n, d, red);
 }
 
-// grid (1 + segments, rows): block 0 the serial head's sum (and its stop, with want_stop) into
-// head[row]; block 1 + s the record of segment s. The head runs here, beside the records, so
-// that the chain kernel starts at the walk.
+// seg_xfer_kernel's shape: one wave per segment, kXferSegs segments per block, no barrier
+constexpr int kXferThreads = 256;
+constexpr uint32_t kXferSegs = kXferThreads / 64;
+__host__ __device__ inline uint32_t xfer_blocks(uint32_t n) { return 1u + (seg_count(n) + kXferSegs - 1u) / kXferSegs; }
+
+// grid (xfer_blocks(n), rows): block 0 the serial head's sum (and its stop, with want_stop) into
+// head[row]; in block b >= 1, wave w the record of segment (b - 1) kXferSegs + w. The head runs
+// here, beside the records, so that the chain kernel starts at the walk.
 template <class Src>
-__global__ __launch_bounds__(kSegThreads) void seg_xfer_kernel(Src src, uint32_t n, const double* d, SegRec* rec,
-                                                               float thr, uint32_t want_stop, SegHead* head) {
-    __shared__ double red[kSegWaves];
-    __shared__ Xfer wt[2][kSegWaves];
+__global__ __launch_bounds__(kXferThreads) void seg_xfer_kernel(Src src, uint32_t n, const double* d, SegRec* rec,
+                                                                float thr, uint32_t want_stop, SegHead* head) {
     __shared__ float hterm[kSegHead];
     const uint32_t row = blockIdx.y;
     if (!src.active(row)) return;  // the whole block
     if (blockIdx.x == 0) {
         const uint32_t nh = min(n, kSegHead);
-        constexpr int kPer = kSegHead / kSegThreads;
+        constexpr int kPer = kSegHead / kXferThreads;
         float v[kPer];  // all loads first
 #pragma unroll
-        for (int q = 0; q < kPer; ++q) v[q] = src.term(row, min(threadIdx.x + q * kSegThreads, n - 1u));
+        for (int q = 0; q < kPer; ++q) v[q] = src.term(row, min(threadIdx.x + q * kXferThreads, n - 1u));
 #pragma unroll
         for (int q = 0; q < kPer; ++q) {
-            const uint32_t j = threadIdx.x + q * kSegThreads;
+            const uint32_t j = threadIdx.x + q * kXferThreads;
             hterm[j] = j < nh ? v[q] : 0.0f;
         }
         __syncthreads();
@@ -722,57 +725,49 @@ __global__ __launch_bounds__(kSegThreads) void seg_xfer_kernel(Src src, uint32_t
         }
         return;
     }
-    const uint32_t s = blockIdx.x - 1;
+    const int lane = threadIdx.x & 63;
     const uint32_t nseg = seg_count(n);
+    const uint32_t s = (blockIdx.x - 1) * kXferSegs + (threadIdx.x >> 6);
+    if (s >= nseg) return;  // the whole wave; nothing below waits on another wave
     const double* dr = d + static_cast<size_t>(row) * (nseg + 1);
-    // D: the head's and the earlier segments' double sums
-    double dv[kSegMax / kSegThreads];  // all loads first; entries past s read dr[s], dropped
+    // D: the head's and the earlier segments' double sums (entries past s read dr[s], dropped)
+    constexpr int kDq = kSegMax / 64;
+    double dv[kDq];
 #pragma unroll
-    for (int q = 0; q < kSegMax / kSegThreads; ++q) dv[q] = dr[min(threadIdx.x + q * kSegThreads, s)];
+    for (int q = 0; q < kDq; ++q) dv[q] = dr[min(static_cast<uint32_t>(lane + q * 64), s)];
     double t = 0.0;
 #pragma unroll
-    for (int q = 0; q < kSegMax / kSegThreads; ++q) t += threadIdx.x + q * kSegThreads <= s ? dv[q] : 0.0;
-    const double D = seg_block_sum(t, red);
+    for (int q = 0; q < kDq; ++q) t += static_cast<uint32_t>(lane + q * 64) <= s ? dv[q] : 0.0;
+    const double D = wave_reduce(t, 0.0, [](double x, double y) { return x + y; });
     int ex = 0;
     const double m = frexp(D, &ex);  // D = m * 2^ex, m in [0.5, 1)
     const bool low = D < 0x1p-125;
     const int E0 = low ? -126 : ex - 1;
     const int E1 = low ? -125 : max(-126, m < 0.75 ? ex - 2 : ex);
-    // this thread's four terms, in order, for both candidates
-    const uint32_t k0 = kSegHead + s * kSegLen;
+    // this lane's kSegPer terms, in order, for both candidates; then the ordered composition
+    // over the lanes
+    const uint32_t j0 = kSegHead + s * kSegLen + static_cast<uint32_t>(lane) * kSegPer;
+    float av[kSegPer];  // all loads first
+#pragma unroll
+    for (int q = 0; q < kSegPer; ++q) av[q] = src.term(row, min(j0 + q, n - 1u));
     Xfer f0 = xfer_id(), f1 = xfer_id();
-    float av[4];  // all loads first
 #pragma unroll
-    for (int q = 0; q < 4; ++q) av[q] = src.term(row, min(k0 + threadIdx.x * 4 + q, n - 1u));
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const uint32_t j = k0 + threadIdx.x * 4 + q;
-        const float a = j < n ? av[q] : 0.0f;  // j < k0 + kSegLen always: 4 terms per thread
+    for (int q = 0; q < kSegPer; ++q) {
+        const float a = j0 + q < n ? av[q] : 0.0f;
         uint32_t kk, kd;
         split_term(a, E0, kk, kd);
         f0 = xfer_then(f0, term_xfer(kk, kd));
         split_term(a, E1, kk, kd);
         f1 = xfer_then(f1, term_xfer(kk, kd));
     }
-    // ordered composition: wave scans, then the four wave totals in order
     f0 = xfer_wave_scan(f0);
     f1 = xfer_wave_scan(f1);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (lane == 63) {
-        wt[0][wave] = f0;
-        wt[1][wave] = f1;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
         SegRec r;
         r.E[0] = E0;
         r.E[1] = E1;
-        r.f[0] = wt[0][0];
-        r.f[1] = wt[1][0];
-        for (int w = 1; w < kSegWaves; ++w) {
-            r.f[0] = xfer_then(r.f[0], wt[0][w]);
-            r.f[1] = xfer_then(r.f[1], wt[1][w]);
-        }
+        r.f[0] = f0;
+        r.f[1] = f1;
         rec[static_cast<size_t>(row) * kSegMax + s] = r;
     }
 }
@@ -1426,8 +1421,8 @@ TWD_API int twd_sequential_sum(const float* terms, uint32_t n, float thr, float*
     const uint32_t nseg = seg_count(n);
     const SegSrcArray src{terms};
     seg_dsum_kernel<<<dim3(nseg + 1, 1), kSegThreads, 0, s>>>(src, n, seg_d);
-    seg_xfer_kernel<<<dim3(nseg + 1, 1), kSegThreads, 0, s>>>(src, n, seg_d, seg_rec, thr, stop_out ? 1u : 0u,
-                                                              seg_head);
+    seg_xfer_kernel<<<dim3(xfer_blocks(n), 1), kXferThreads, 0, s>>>(src, n, seg_d, seg_rec, thr,
+                                                                     stop_out ? 1u : 0u, seg_head);
     if (stop_out)
         seg_array_kernel<true><<<1, kRejThreads, 0, s>>>(terms, n, thr, seg_rec, seg_head, sum_out, stop_out);
     else
@@ -1533,12 +1528,13 @@ int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab
     SegRec* seg_rec = static_cast<SegRec*>(sel->draft.seg_rec);
     const SegSrcSoftmax src_e{a.e, a.estride, a.flags};
     SegHead* seg_head = static_cast<SegHead*>(ds.seg_head);
-    seg_xfer_kernel<<<dim3(nseg + 1, 2 * a.npos), kSegThreads, 0, s>>>(src_e, vocab, seg_d, seg_rec, 0.0f, 0u,
-                                                                      seg_head);
+    seg_xfer_kernel<<<dim3(xfer_blocks(vocab), 2 * a.npos), kXferThreads, 0, s>>>(src_e, vocab, seg_d, seg_rec,
+                                                                                 0.0f, 0u, seg_head);
     seg_sum_kernel<<<2 * a.npos, kRejThreads, 0, s>>>(a, seg_rec, seg_head);
     seg_ratio_dsum_kernel<<<dim3(nseg + 1, a.npos), kSegThreads, 0, s>>>(a, ds.live, seg_d);
     const SegSrcResidual src_r{a.e, a.estride, a.sums, ds.live};
-    seg_xfer_kernel<<<dim3(nseg + 1, a.npos), kSegThreads, 0, s>>>(src_r, vocab, seg_d, seg_rec, 0.0f, 0u, seg_head);
+    seg_xfer_kernel<<<dim3(xfer_blocks(vocab), a.npos), kXferThreads, 0, s>>>(src_r, vocab, seg_d, seg_rec, 0.0f, 0u,
+                                                                             seg_head);
     TWD_HIP(hipStreamWaitEvent(s, ds.join, 0));  // the selector's tokens, read by the finish
     ds.fin_epoch = ds.fin_epoch % 0x7FFFFFFFu + 1u;
     const DraftFinish fin{sel->scratch.verify_tokens, used, drafts, n_drafts, has, result,
