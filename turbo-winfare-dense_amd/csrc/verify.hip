@@ -50,11 +50,9 @@ constexpr uint32_t kNoEvent = 0xFFFFFFFFu;
 constexpr uint32_t kSegHead = 2048;                   // a multiple of kSegLen, <= kDraftChunk
 constexpr uint32_t kSegLen = 512;                    // terms per segment after the head
 constexpr int kSegPer = kSegLen / 64;                // terms per lane when one wave sums a segment
-constexpr int kSegThreads = kSegLen / 4;             // 4 terms per thread in seg_xfer_kernel
-constexpr int kSegWaves = kSegThreads / 64;
 constexpr uint32_t kSegMax = (1u << 19) / kSegLen;  // segments per row (vocab <= 2048 + 2^19)
 static_assert(kSegLen % 256 == 0 && kSegPer % 4 == 0, "whole waves, 16-byte lane loads");
-static_assert(kSegHead % kSegThreads == 0 && kSegMax % kSegThreads == 0, "whole per-thread strides");
+static_assert(kSegMax % 64 == 0, "whole lane strides over the segment double sums");
 // draft_exp_kernel's blocks also form the double sums of the head and the segments: a block's
 // kDraftChunk entries are kDraftChunk / kSegLen whole parts of kSegLen, the first
 // kSegHead / kSegLen parts of the row being the head's
@@ -633,58 +631,62 @@ struct SegSrcResidual {  // (p - q)+ of a rejected position (draft_reject_kernel
     }
 };
 
-// sum of one double per thread over a kSegThreads block (any order: the value only predicts)
-__device__ __forceinline__ double seg_block_sum(double v, double* red) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    double t = red[0];
-#pragma unroll
-    for (int w = 1; w < kSegWaves; ++w) t += red[w];
-    __syncthreads();
-    return t;
-}
+// The segment kernels' shape: one wave per segment, kXferSegs segments per block, no barrier
+// (block 0 of a row takes the head)
+constexpr int kXferThreads = 256;
+constexpr uint32_t kXferSegs = kXferThreads / 64;
+__host__ __device__ inline uint32_t xfer_blocks(uint32_t n) { return 1u + (seg_count(n) + kXferSegs - 1u) / kXferSegs; }
+static_assert(kSegLen == 64 * kSegPer && kSegHead % kXferThreads == 0, "a wave per segment, whole head strides");
 
-// Block b of row `row`: b = 0 the head [0, kSegHead), b = s + 1 the segment s
+// Block b of row `row` (kXferThreads threads): b = 0 the head's double sum into d[row][0]; in
+// block b >= 1, wave w segment s = (b - 1) kXferSegs + w into d[row][1 + s]. Every term is
+// requested before any is added (indices clamped into the row, values past its end dropped).
 template <class Src>
 __device__ __forceinline__ void seg_dsum_block(const Src& src, uint32_t row, uint32_t b, uint32_t n, double* d,
                                                double* red) {
     const uint32_t nseg = seg_count(n);
-    const uint32_t lo = b == 0 ? 0u : kSegHead + (b - 1) * kSegLen;
-    const uint32_t hi = b == 0 ? min(n, kSegHead) : min(n, lo + kSegLen);
-    // every term requested before any is added (indices clamped into the row, values past hi
-    // dropped): one memory wait per block
-    constexpr int kPer = kSegHead / kSegThreads;
-    float v[kPer];
+    const int lane = threadIdx.x & 63;
+    double* dr = d + static_cast<size_t>(row) * (nseg + 1);
+    if (b == 0) {
+        const uint32_t nh = min(n, kSegHead);
+        constexpr int kPer = kSegHead / kXferThreads;
+        float v[kPer];
 #pragma unroll
-    for (int q = 0; q < kPer; ++q) {
-        const uint32_t j = lo + threadIdx.x + q * kSegThreads;
-        v[q] = (b == 0 || q < kSegLen / kSegThreads) ? src.term(row, min(j, n - 1u)) : 0.0f;
+        for (int q = 0; q < kPer; ++q) v[q] = src.term(row, min(threadIdx.x + q * kXferThreads, n - 1u));
+        double t = 0.0;
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) t += threadIdx.x + q * kXferThreads < nh ? static_cast<double>(v[q]) : 0.0;
+        t = wave_reduce(t, 0.0, [](double x, double y) { return x + y; });
+        if (lane == 0) red[threadIdx.x >> 6] = t;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            double h = red[0];
+            for (uint32_t w = 1; w < kXferSegs; ++w) h += red[w];
+            dr[0] = h;
+        }
+        return;
     }
+    const uint32_t s = (b - 1) * kXferSegs + (threadIdx.x >> 6);
+    if (s >= nseg) return;  // the whole wave
+    const uint32_t j0 = kSegHead + s * kSegLen + static_cast<uint32_t>(lane) * kSegPer;
+    float v[kSegPer];
+#pragma unroll
+    for (int q = 0; q < kSegPer; ++q) v[q] = src.term(row, min(j0 + q, n - 1u));
     double t = 0.0;
 #pragma unroll
-    for (int q = 0; q < kPer; ++q) {
-        const uint32_t j = lo + threadIdx.x + q * kSegThreads;
-        t += j < hi ? static_cast<double>(v[q]) : 0.0;
-    }
-    t = seg_block_sum(t, red);
-    if (threadIdx.x == 0) d[static_cast<size_t>(row) * (nseg + 1) + b] = t;
+    for (int q = 0; q < kSegPer; ++q) t += j0 + q < n ? static_cast<double>(v[q]) : 0.0;
+    t = wave_reduce(t, 0.0, [](double x, double y) { return x + y; });
+    if (lane == 0) dr[1 + s] = t;
 }
 
-// grid (1 + segments, rows): block 0 the head, block s + 1 the segment s
+// grid (xfer_blocks(n), rows): the head's and the segments' double sums
 template <class Src>
-__global__ __launch_bounds__(kSegThreads) void seg_dsum_kernel(Src src, uint32_t n, double* d) {
-    __shared__ double red[kSegWaves];
+__global__ __launch_bounds__(kXferThreads) void seg_dsum_kernel(Src src, uint32_t n, double* d) {
+    __shared__ double red[kXferSegs];
     const uint32_t row = blockIdx.y;
     if (!src.active(row)) return;  // the whole block
     seg_dsum_block(src, row, blockIdx.x, n, d, red);
 }
-
-// seg_xfer_kernel's shape: one wave per segment, kXferSegs segments per block, no barrier
-constexpr int kXferThreads = 256;
-constexpr uint32_t kXferSegs = kXferThreads / 64;
-__host__ __device__ inline uint32_t xfer_blocks(uint32_t n) { return 1u + (seg_count(n) + kXferSegs - 1u) / kXferSegs; }
 
 // grid (xfer_blocks(n), rows): block 0 the serial head's sum (and its stop, with want_stop) into
 // head[row]; in block b >= 1, wave w the record of segment (b - 1) kXferSegs + w. The head runs
@@ -1095,12 +1097,12 @@ __device__ __forceinline__ bool draft_accepts(const DraftArgs& a, uint32_t pi, u
     return P.u1 <= r;
 }
 
-// The residual's double segment sums, grid (1 + segments, P), each block first repeating its
+// The residual's double segment sums, grid (xfer_blocks(V), P), each block first repeating its
 // position's ratio test (every block gets the same answer): an accepted draft is final (block 0
 // records it) and the position's blocks stop; a rejected one is marked live for the residual
 // draw (speculator.cpp:94-116).
-__global__ __launch_bounds__(kSegThreads) void seg_ratio_dsum_kernel(DraftArgs a, uint32_t* live, double* d) {
-    __shared__ double red[kSegWaves];
+__global__ __launch_bounds__(kXferThreads) void seg_ratio_dsum_kernel(DraftArgs a, uint32_t* live, double* d) {
+    __shared__ double red[kXferSegs];
     const uint32_t pi = blockIdx.y;
     uint32_t dt = 0;
     const bool accepted = draft_accepts(a, pi, &dt);
@@ -1420,7 +1422,7 @@ TWD_API int twd_sequential_sum(const float* terms, uint32_t n, float thr, float*
     }
     const uint32_t nseg = seg_count(n);
     const SegSrcArray src{terms};
-    seg_dsum_kernel<<<dim3(nseg + 1, 1), kSegThreads, 0, s>>>(src, n, seg_d);
+    seg_dsum_kernel<<<dim3(xfer_blocks(n), 1), kXferThreads, 0, s>>>(src, n, seg_d);
     seg_xfer_kernel<<<dim3(xfer_blocks(n), 1), kXferThreads, 0, s>>>(src, n, seg_d, seg_rec, thr,
                                                                      stop_out ? 1u : 0u, seg_head);
     if (stop_out)
@@ -1531,7 +1533,7 @@ int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab
     seg_xfer_kernel<<<dim3(xfer_blocks(vocab), 2 * a.npos), kXferThreads, 0, s>>>(src_e, vocab, seg_d, seg_rec,
                                                                                  0.0f, 0u, seg_head);
     seg_sum_kernel<<<2 * a.npos, kRejThreads, 0, s>>>(a, seg_rec, seg_head);
-    seg_ratio_dsum_kernel<<<dim3(nseg + 1, a.npos), kSegThreads, 0, s>>>(a, ds.live, seg_d);
+    seg_ratio_dsum_kernel<<<dim3(xfer_blocks(vocab), a.npos), kXferThreads, 0, s>>>(a, ds.live, seg_d);
     const SegSrcResidual src_r{a.e, a.estride, a.sums, ds.live};
     seg_xfer_kernel<<<dim3(xfer_blocks(vocab), a.npos), kXferThreads, 0, s>>>(src_r, vocab, seg_d, seg_rec, 0.0f, 0u,
                                                                              seg_head);
