@@ -1057,9 +1057,9 @@ template <typename Load, typename Term>
 __device__ float seg_row_sum(Load load, Term term, uint32_t n, const SegRec* rec, const SegHead* hd, float thr,
                              uint32_t* stop_at, SeqShared& sh, ChainShared& ch) {
     const uint32_t nseg = seg_count(n);
+    const SegHead h = *hd;  // the same value in every thread; requested with the records
     for (uint32_t i = threadIdx.x; i < nseg; i += blockDim.x) ch.rec[i] = rec[i];
     __syncthreads();
-    const SegHead h = *hd;  // the same value in every thread
     if (stop_at && h.stop < min(n, kSegHead)) {
         *stop_at = h.stop;
         return h.S;
