@@ -572,14 +572,14 @@ __device__ __forceinline__ void load_row(const float* row, uint32_t j0, float (&
 //
 // block_seq_sum runs one row on one CU. Here a row's terms after the serial head are cut into
 // segments of kSegLen, and three launches sum them exactly:
-//   double sums      (segment x row blocks): each segment's sum in double, and the head's
+//   double sums      (a wave per segment): each segment's sum in double, and the head's
 //                    (seg_dsum_kernel; for the softmax rows draft_exp_kernel forms them, for
 //                    the residual seg_ratio_dsum_kernel);
-//   seg_xfer_kernel  (segment x row blocks): the double prefix D before the segment predicts the
+//   seg_xfer_kernel  (a wave per segment): the double prefix D before the segment predicts the
 //                    binade of the fp32 running sum there. For that binade and its nearer
 //                    neighbour the segment's terms become transfer functions (as in a window of
-//                    block_seq_sum) and their ordered composition is the segment's record. An
-//                    extra block per row adds the head serially;
+//                    block_seq_sum) and their ordered composition is the segment's record.
+//                    Block 0 of each row adds the head serially;
 //   a chain kernel   (one block per row): from the head's sum, wave 0 walks the records 64 at
 //                    a time: when the exact sum S at a segment start lies in one of the record's
 //                    two binades, and the composed increment keeps it there (and below a stop
