@@ -346,7 +346,9 @@ TWD_API int twd_verify(twd_selector* sel, const float* logits, uint32_t vocab, u
  * (twd_rejection_uniforms). NULL entries, positions >= n_draft_rows and greedy params
  * (temperature <= 0 and repetition_penalty == 1) sample-and-compare as twd_verify does. The
  * first call with draft rows allocates 8 * vocab bytes of scratch per such position on the
- * selector (kept, and grown when a later call needs more). */
+ * selector (kept, and grown when a later call needs more), and one side stream (default
+ * priority) with two events: the target rows' selection runs there, forked from `stream` and
+ * joined back into it before the call's last launch, so `stream` orders all of the call's work. */
 TWD_API int twd_verify_draft(twd_selector* sel, const float* logits, uint32_t vocab, uint32_t rows,
                              uint64_t row_stride, const float* const* draft_rows,
                              uint32_t n_draft_rows, const twd_row_params* params,
