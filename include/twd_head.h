@@ -135,13 +135,20 @@ TWD_API int twd_head_verify_greedy(twd_head* head, const uint16_t* hidden_bf16, 
  * first change of stream waits for the device once; after that each call records an event
  * and a call on another stream waits for it). A head is driven by one host thread at a time.
  * Each launch counts its blocks in under its own epoch, and its last block arms the counter for
- * the next launch; a launch that finds the counter not armed for it (a launch that did not
- * finish, a write from outside) counts in on a fallback word instead, so a count left behind
+ * the next launch. A launch repeated with the same arguments (a captured graph replayed) counts
+ * in on a replay slot armed by its previous replay, and a launch that finds neither armed for it
+ * (the first replay, a write from outside) counts in on a fallback word, so a count left behind
  * never decides which block finishes.
  *
+ * Stream capture: the head's calls (and a selector's) may be captured into a HIP graph on any
+ * stream; a captured call waits for nothing and records nothing. Replays of such a graph share
+ * the object's state with its other calls, so the caller orders them against those calls (one
+ * stream, or its own events), as it orders the replays themselves.
+ *
  * No counterpart in the reference: the device address of that state, for diagnostics and
- * tests: 64 per-row uint64 maxima, then the uint64 counter {arrivals << 32 | epoch}, then the
- * uint64 fallback counter. */
+ * tests: 64 per-row uint64 maxima, then the arrival counter's six uint64 words
+ * {arrivals << 32 | epoch}: the word armed for the next launch, four replay slots and the
+ * fallback word. */
 TWD_API void* twd_head_finish_state(const twd_head* head);
 
 /* ---- the same passes with the final RMSNorm as their prologue --------------------------------
@@ -318,7 +325,7 @@ TWD_API int twd_select(twd_selector* sel, float* logits, uint32_t vocab, uint32_
 /* twd_select without a selector, allocating nothing: no counterpart in the reference. It is for
  * callers that cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). The selection scratch is a fixed device array of
- * 4,252,176 bytes per GPU, kept for the life of the process: at most 64 rows of at most 262144
+ * 4,252,208 bytes per GPU, kept for the life of the process: at most 64 rows of at most 262144
  * entries per call (TWD_E_INVALID beyond). Every call on one GPU uses that GPU's one array, so
  * calls that overlap on a GPU (other streams, other threads) race: order them. The first call on
  * each device looks the array's address up there. Results are those of twd_select. */
@@ -369,10 +376,10 @@ TWD_API int twd_sequential_sum(const float* terms, uint32_t n, float thr, float*
 
 /* No counterpart in the reference: the device address of the selector's draft-verify finish
  * counter, for diagnostics and tests (NULL before the first twd_verify_draft call that had
- * draft rows): the uint64 counter {arrivals << 32 | epoch}, then the uint64 fallback counter.
- * The residual launch's blocks count in on it and its last block runs the accept chain; each
- * call arms it for the next, and a call that finds it not armed for itself (a call that did not
- * finish, a write from outside) counts in on the fallback word instead. */
+ * draft rows): the six uint64 words {arrivals << 32 | epoch} of its arrival counter (the word
+ * armed for the next call, four replay slots, the fallback word). The residual launch's blocks
+ * count in on it and its last block runs the accept chain; each call arms it for the next, and a
+ * call that finds it not armed for itself (a write from outside) counts in on another word. */
 TWD_API void* twd_selector_verify_state(const twd_selector* sel);
 /* No counterpart in the reference: the fp32 softmax sums (compute_softmax, speculator.cpp:22-26)
  * of the last twd_verify_draft call on this selector that ran the rejection branch, for
@@ -411,6 +418,10 @@ TWD_API int twd_probe_read_bandwidth(const void* buf, uint64_t bytes, uint32_t w
  * (glibc's expf method, bit-exact with the x86-64 host library) of x[i], for tests. Device
  * buffers of n floats; asynchronous on `stream`. */
 TWD_API int twd_probe_expf(const float* x, float* out, uint64_t n, void* stream);
+/* No counterpart in the reference: out[i] = the device exp(double) the sampled shortlist uses for
+ * its terms exp(l - max) and exp((l - max) / T) (glibc's exp method, bit-exact with the x86-64
+ * host library) of x[i], for tests. Device buffers of n doubles; asynchronous on `stream`. */
+TWD_API int twd_probe_exp(const double* x, double* out, uint64_t n, void* stream);
 /* Bytes of the reference layout for a V x d head with 64-wide groups. */
 TWD_API uint64_t twd_head_bytes(uint32_t vocab, uint32_t d_model, uint32_t group_size);
 

@@ -1,7 +1,7 @@
 /*
  * CPU oracle: scalar restatement of the reference's token-selection path.
  *
- * TEST INFRASTRUCTURE ONLY (see oracle.h). Built with -O2 -ffp-contract=off so every float
+ * TEST INFRASTRUCTURE ONLY (see oracle.h). Built with -O3 -ffp-contract=off so every float
  * expression is evaluated exactly as written, in the order written.
  *
  * What pins each function (tests/test_oracle.py):
@@ -349,6 +349,11 @@ void or_rejection_uniforms(uint64_t step_seed, float* u1, float* u2) {
     or_mt64_seed(&g, step_seed);
     *u1 = or_canonical_float(or_mt64_next(&g));
     *u2 = or_canonical_float(or_mt64_next(&g));
+}
+
+/* sampling.cpp:114,145,157: std::exp(double) is the C library's exp */
+void or_exp(const double* x, double* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = exp(x[i]);
 }
 
 /* speculator.cpp:23: std::exp(float) is the C library's expf */

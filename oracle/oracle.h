@@ -135,6 +135,9 @@ int or_verify_draft(const uint32_t* drafts, size_t n_drafts, const float* const*
 /* out[i] = expf(x[i]) of the host C library: std::exp(float) as compute_softmax calls it
  * (speculator.cpp:23). */
 void or_expf(const float* x, float* out, size_t n);
+/* out[i] = exp(x[i]) of the host C library: std::exp(double) as sample_token calls it
+ * (sampling.cpp:114,145,157) */
+void or_exp(const double* x, double* out, size_t n);
 
 /* Scalar INT4 g64 LM head (cpu_reference.cpp:643-665): fp32 sequential dot over c, then
  * softcap*tanhf(sum/softcap) when softcap > 0. W is [V][d/8] u32, S/B are [V][d/G] bf16 bits,

@@ -80,6 +80,8 @@ def _load():
     lib.or_splitmix64.restype = C.c_uint64
     lib.or_expf.argtypes = [_f32p, _f32p, C.c_size_t]
     lib.or_expf.restype = None
+    lib.or_exp.argtypes = [_f64p, _f64p, C.c_size_t]
+    lib.or_exp.restype = None
     lib.or_splitmix64.argtypes = [C.c_uint64]
     lib.or_seed_for.restype = C.c_uint64
     lib.or_seed_for.argtypes = [C.c_int, C.c_uint64, C.c_int]
@@ -273,6 +275,14 @@ def expf(x) -> np.ndarray:
     xs = _f32(x).copy()
     out = np.empty_like(xs)
     lib().or_expf(xs, out, xs.size)
+    return out
+
+
+def exp(x) -> np.ndarray:
+    """The host C library's exp(double), elementwise (std::exp(double) of sampling.cpp)."""
+    xs = np.ascontiguousarray(x, np.float64)
+    out = np.empty_like(xs)
+    lib().or_exp(xs, out, xs.size)
     return out
 
 

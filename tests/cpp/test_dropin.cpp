@@ -2,6 +2,7 @@
 // libtwd_head.so on the GPU, with the assertions of the reference's own tests:
 // tests/test_sampling.cpp:92-265 and tests/test_speculative.cpp:29-77.
 // Prints one line per block and exits nonzero on the first failure.
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -22,6 +23,52 @@ using namespace g4dense;
             std::exit(1);                                                    \
         }                                                                    \
     } while (0)
+
+// sample_token restated with a full sort of the row (the shortlist is its first want entries),
+// sequential double sums and the host's exp: the expectation for top_k above 256.
+static uint32_t full_sort_sample(const std::vector<float>& lg, const SamplingParams& p, uint64_t seed) {
+    const uint32_t V = static_cast<uint32_t>(lg.size());
+    std::vector<uint32_t> order(V);
+    for (uint32_t i = 0; i < V; ++i) order[i] = i;
+    std::sort(order.begin(), order.end(),
+              [&](uint32_t a, uint32_t b) { return lg[a] != lg[b] ? lg[a] > lg[b] : a < b; });
+    float mx = lg[0];
+    for (float x : lg) mx = x > mx ? x : mx;
+    double total = 0.0;
+    for (float x : lg) total += std::exp(static_cast<double>(x) - mx);
+    const size_t want = p.top_k > 0 ? std::min<size_t>(static_cast<size_t>(p.top_k), V) : std::min<size_t>(256, V);
+    size_t cut = want;
+    if (p.top_p < 1.0f) {
+        double run = 0.0;
+        for (size_t i = 0; i < want; ++i) {
+            run += std::exp(static_cast<double>(lg[order[i]]) - mx) / total;
+            if (run >= static_cast<double>(p.top_p)) {
+                cut = i + 1;
+                break;
+            }
+        }
+    }
+    if (p.top_k > 0) cut = std::min(cut, static_cast<size_t>(p.top_k));
+    cut = std::max<size_t>(cut, 1);
+    std::vector<double> q(cut);
+    double denom = 0.0;
+    for (size_t i = 0; i < cut; ++i) {
+        q[i] = std::exp((static_cast<double>(lg[order[i]]) - mx) / p.temperature);
+        denom += q[i];
+    }
+    uint64_t s = seed;  // one xorshift64* step, the top 24 bits as a fraction of 2^24
+    s ^= s >> 12;
+    s ^= s << 25;
+    s ^= s >> 27;
+    const float u = static_cast<float>(((s * 0x2545F4914F6CDD1DULL) >> 40) & 0xFFFFFFu) / 16777216.0f;
+    const double r = static_cast<double>(u) * denom;
+    double acc = 0.0;
+    for (size_t i = 0; i < cut; ++i) {
+        acc += q[i];
+        if (acc >= r) return order[i];
+    }
+    return order[cut - 1];
+}
 
 static bool rejects(const SamplingParams& p) {
     try {
@@ -113,6 +160,28 @@ int main() {
         CHECK(a == b);
     }
     std::puts("determinism ok");
+
+    // top_k above 256: sample_token takes any top_k (want = min(top_k, V), sampling.cpp:122-124);
+    // only validate_sampling bounds it. Ids at V = 262144 against the full-sort restatement.
+    {
+        const uint32_t V = 262144;
+        std::mt19937 rng(20261202);
+        std::normal_distribution<float> nd(0.0f, 4.0f);
+        std::vector<float> lg(V);
+        for (auto& x : lg) x = nd(rng);
+        const SamplingParams cases[] = {{0.8f, 0.95f, 1000, 1.0f, true, 11},
+                                        {1.2f, 1.0f, 1000, 1.0f, true, 12},
+                                        {0.7f, 0.99f, 4096, 1.0f, true, 13},
+                                        {1.0f, 1.0f, 300000, 1.0f, true, 14}};
+        for (const auto& p : cases) {
+            CHECK(rejects(p));
+            for (int i = 0; i < 4; ++i) {
+                const uint64_t seed = seed_for(p, i);
+                CHECK(sample_token(lg.data(), V, p, seed) == full_sort_sample(lg, p, seed));
+            }
+        }
+    }
+    std::puts("top_k above 256 ok");
 
     {
         SpeculativeCoordinator spec;

@@ -48,7 +48,7 @@ struct HeadArgs {
     // greedy finish: running per-row maxima (zero between launches), the arrival counter
     // {epoch, count} and this launch's epoch, and where the last block puts its results
     uint64_t* gbest;    // [TWD_MAX_ROWS]
-    uint64_t* gctr;     // [2]: the armed counter, then the fallback counter
+    uint64_t* gctr;     // [kArriveWords]: grid_arrive's counter
     uint32_t epoch, next_epoch;
     uint32_t* tokens;
     const uint32_t* drafts;
@@ -201,13 +201,9 @@ using EpiShared = EpiSharedT<kHeadWaves>;
 // stores, so no device-scope fence is needed: on this part such a fence writes back the XCD's
 // L2 and, paid by each of ~1000 blocks, costs more than the streaming pass itself.
 //
-// Arrivals are counted in gctr[0] = {arrivals (high 32 bits), epoch (low 32 bits)}: every
-// launch carries its own epoch, and the last block of each launch leaves the counter armed for
-// the next one, {0, next epoch}. A block adds 1 to the high half, which never carries into the
-// epoch, so every block of a launch sees the same epoch there. When it is not this launch's
-// (the first launch on a fresh state, a launch that did not finish, a write from outside), the
-// blocks count themselves in on gctr[1] instead, by compare-and-swap with the epoch attached,
-// and the last one re-arms gctr[0]; only that case pays for contended retries.
+// Arrivals are counted by grid_arrive on gctr (an epoch per launch, armed by the previous
+// launch's last block; replays of a captured launch count in on a replay slot, and only a launch
+// that finds neither armed for it pays for contended compare-and-swap retries).
 // tot[j][mt][i] holds row r = (tile0 + j) * 16 + lane % 16 of MFMA row 16 mt + 4 (lane / 16) + i,
 // which carries h row m = (16 mt + 4 (lane / 16) + i) / MS when i is a multiple of MS (MS > 1:
 // the rows are spread over the MFMA rows, see head_small_kernel); other entries are not outputs.
@@ -287,28 +283,7 @@ __device__ __forceinline__ void grid_finish(const HeadArgs& a, EpiSharedT<NW>& s
     }
     __syncthreads();
     if (tid == 0) {
-        unsigned long long* ctr = reinterpret_cast<unsigned long long*>(a.gctr);
-        const unsigned long long ep = a.epoch;
-        const unsigned long long old = __hip_atomic_fetch_add(ctr, 1ull << 32, __ATOMIC_RELAXED,
-                                                              __HIP_MEMORY_SCOPE_AGENT);
-        bool last;
-        if ((old & 0xFFFFFFFFull) == ep && (old >> 32) < nb) {
-            last = (old >> 32) == nb - 1;
-        } else {
-            // not armed for this launch: count in on the fallback word; every failed exchange
-            // means another block counted itself in, so the loop ends after at most nb tries
-            unsigned long long* c2 = ctr + 1;
-            unsigned long long cur = __hip_atomic_load(c2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), want;
-            do {
-                want = ((cur & 0xFFFFFFFFull) == ep) ? cur + (1ull << 32) : (ep | (1ull << 32));
-            } while (!__hip_atomic_compare_exchange_strong(c2, &cur, want, __ATOMIC_RELAXED,
-                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-            last = (want >> 32) == nb;
-        }
-        // every block of this launch has added to gctr[0] by now: arm it for the next launch
-        if (last)
-            __hip_atomic_exchange(ctr, static_cast<unsigned long long>(a.next_epoch), __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = grid_arrive(reinterpret_cast<unsigned long long*>(a.gctr), nb, a.epoch, a.next_epoch);
         se.last = last;
     }
     __syncthreads();
@@ -1476,7 +1451,7 @@ struct twd_head {
     // [TWD_MAX_ROWS] per-row maxima (zero between launches), the arrival counter, and the
     // repack's flag
     uint64_t* gbest = nullptr;
-    uint32_t epoch = 0;           // of the last launch; 0 is never used
+    uint32_t epoch = kFirstEpoch - 1;  // of the last launch; the next is epoch_after(epoch)
     StreamOrder order;            // calls on several streams share gbest, hp/hx and sel
     u32x4_t* hp = nullptr;        // prepared h in A-fragment order for M > 8 (prep_hidden_kernel)
     u32x4_t* hx = nullptr;        // its bias A-fragment entries
@@ -1555,9 +1530,6 @@ int enable_small_kernels(uint32_t d) {
     return TWD_OK;
 }
 
-// Epochs run through 1 .. 2^31 - 1 and repeat; 0 never arms the counter.
-uint32_t epoch_after(uint32_t e) { return e % 0x7FFFFFFFu + 1u; }
-
 int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
     twd_head* h = new twd_head();
     h->vocab = vocab;
@@ -1567,11 +1539,12 @@ int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
     h->nunits = d / kChunkK;
     h->tiled_bytes = static_cast<uint64_t>(h->ntiles) * h->nunits * kUnitBytes;
     hipError_t e = hipMalloc(&h->tiled, h->tiled_bytes);
-    // gbest: per-row maxima, the two arrival counters, and the repack's bad-scale flag; the
+    // gbest: per-row maxima, the arrival counter's words, and the repack's bad-scale flag; the
     // counter starts armed for the first launch's epoch
-    const uint64_t armed = epoch_after(0);
-    if (e == hipSuccess) e = hipMalloc(&h->gbest, sizeof(uint64_t) * (TWD_MAX_ROWS + 3));
-    if (e == hipSuccess) e = hipMemset(h->gbest, 0, sizeof(uint64_t) * (TWD_MAX_ROWS + 3));
+    const uint64_t armed = kFirstEpoch;
+    constexpr size_t kWords = TWD_MAX_ROWS + kArriveWords + 1;
+    if (e == hipSuccess) e = hipMalloc(&h->gbest, sizeof(uint64_t) * kWords);
+    if (e == hipSuccess) e = hipMemset(h->gbest, 0, sizeof(uint64_t) * kWords);
     if (e == hipSuccess) e = hipMemcpy(h->gbest + TWD_MAX_ROWS, &armed, sizeof(armed), hipMemcpyHostToDevice);
     // hp / hx: room past the last chunk and super-unit (each stage copies the next one
     // unconditionally)
@@ -1596,7 +1569,7 @@ int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
     return TWD_OK;
 }
 
-uint32_t* repack_flag(twd_head* h) { return reinterpret_cast<uint32_t*>(h->gbest + TWD_MAX_ROWS + 2); }
+uint32_t* repack_flag(twd_head* h) { return reinterpret_cast<uint32_t*>(h->gbest + TWD_MAX_ROWS + kArriveWords); }
 
 int head_repack(twd_head* h, const uint8_t* wsb_dev, hipStream_t stream) {
     const uint64_t w_bytes = static_cast<uint64_t>(h->vocab) * (h->d / 8) * 4;
@@ -1758,8 +1731,6 @@ int launch_head_sample(twd_head* h, const uint16_t* hidden, const float* x, cons
         a.hist_off[m] = live ? params[m].history_offset : 0u;
         a.hist_len[m] = live ? params[m].history_len : 0u;
         if (!live) continue;
-        if (params[m].temperature > 0.0f && params[m].top_k > static_cast<int32_t>(TWD_MAX_WANT))
-            return fail(TWD_E_UNSUPPORTED, "top_k > 256 is not supported on the device path (validate_sampling rejects it)");
         if (params[m].repetition_penalty != 1.0f && params[m].history_len > 0 && !history)
             return fail(TWD_E_INVALID, "null history with a non-empty history_len");
     }
@@ -1774,7 +1745,8 @@ int launch_head_sample(twd_head* h, const uint16_t* hidden, const float* x, cons
     }
     TWD_HIP(hipGetLastError());
     static_assert(kRTS * kTileRows == kSampleWaveRows, "a wave of the sample pass owns 64 rows");
-    return launch_sample_merge(h->stats, grid * kNWS4, logits, h->vocab, rows, params, tokens, stream);
+    return launch_sample_merge(h->stats, grid * kNWS4, logits, h->vocab, rows, params, tokens, h->sel->scratch.lng,
+                               stream);
 }
 
 // Runs one call's launches with the head's cross-stream ordering around them.

@@ -28,7 +28,15 @@ int hip_fail(hipError_t e, const char* what) {
     return TWD_E_HIP;
 }
 
+// Under stream capture nothing runs: the calls become graph nodes, replayed later in an order
+// only the caller knows, so the caller orders the replays against the object's other calls. A
+// captured call waits for nothing (a device-wide wait, or a wait on an event recorded outside
+// the capture, would invalidate the capture), records nothing, and leaves the object's stream
+// where it was.
 int order_before(StreamOrder& o, hipStream_t s) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    TWD_HIP(hipStreamIsCapturing(s, &cap));
+    if (cap != hipStreamCaptureStatusNone) return TWD_OK;
     if (!o.used) {
         o.used = true;
         o.last = s;
@@ -49,7 +57,10 @@ int order_before(StreamOrder& o, hipStream_t s) {
 }
 
 int order_after(StreamOrder& o, hipStream_t s) {
-    if (o.multi) TWD_HIP(hipEventRecord(o.ev, s));
+    if (!o.multi) return TWD_OK;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    TWD_HIP(hipStreamIsCapturing(s, &cap));
+    if (cap == hipStreamCaptureStatusNone) TWD_HIP(hipEventRecord(o.ev, s));
     return TWD_OK;
 }
 

@@ -6,6 +6,7 @@
 
 #include <algorithm>
 
+#include "exp_libm.h"
 #include "expf_libm.h"
 #include "twd_internal.h"
 
@@ -48,6 +49,12 @@ __global__ void expf_probe_kernel(const float* __restrict__ x, float* __restrict
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
         out[i] = expf_libm<true>(x[i]);
+}
+
+__global__ void exp_probe_kernel(const double* __restrict__ x, double* __restrict__ out, uint64_t n) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = exp_libm(x[i]);
 }
 
 }  // namespace
@@ -102,6 +109,16 @@ TWD_API int twd_probe_expf(const float* x, float* out, uint64_t n, void* stream)
     if (!x || !out) return fail(TWD_E_INVALID, "null x or out");
     const uint64_t blocks = std::min<uint64_t>((n + 255) / 256, 1u << 16);
     expf_probe_kernel<<<static_cast<uint32_t>(blocks), 256, 0, static_cast<hipStream_t>(stream)>>>(x, out, n);
+    TWD_HIP(hipGetLastError());
+    return TWD_OK;
+}
+
+TWD_API int twd_probe_exp(const double* x, double* out, uint64_t n, void* stream) {
+    clear_error();
+    if (n == 0) return TWD_OK;
+    if (!x || !out) return fail(TWD_E_INVALID, "null x or out");
+    const uint64_t blocks = std::min<uint64_t>((n + 255) / 256, 1u << 16);
+    exp_probe_kernel<<<static_cast<uint32_t>(blocks), 256, 0, static_cast<hipStream_t>(stream)>>>(x, out, n);
     TWD_HIP(hipGetLastError());
     return TWD_OK;
 }

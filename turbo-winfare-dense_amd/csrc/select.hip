@@ -22,6 +22,7 @@
 #include <cstring>
 #include <mutex>
 
+#include "exp_libm.h"
 #include "twd_internal.h"
 
 namespace twd {
@@ -62,7 +63,7 @@ struct SelectBufs {
     uint64_t* part_key;
     uint64_t* cand;
     uint64_t* gbest;  // one-pass greedy: per-row best ranks, zero between launches
-    uint64_t* gctr;   // its arrival counter {arrivals (high 32 bits), epoch} and fallback word
+    uint64_t* gctr;   // its arrival counter, kArriveWords words (grid_arrive)
 };
 
 // Shared memory: what every block needs (reductions, the row's shortlist and its sums)...
@@ -407,8 +408,8 @@ __device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, 
     const double td = static_cast<double>(p.temperature);
     if (static_cast<uint32_t>(tid) < want) {
         const double l = static_cast<double>(rank_value(c.sorted[tid]));
-        c.e[tid] = exp(l - mx) / total;
-        c.q[tid] = exp((l - mx) / td);
+        c.e[tid] = exp_libm(l - mx) / total;
+        c.q[tid] = exp_libm((l - mx) / td);
     }
     __syncthreads();
     if (tid >= 64) return 0;
@@ -490,9 +491,8 @@ __device__ __forceinline__ void finish_row(SelCommon& c, uint32_t want, const tw
 // the tokens. The protocol is the head's grid finish (device-scope atomics only, no fence):
 // a returning atomic is performed at the memory-side coherence point before it returns, and
 // the block waits for that return before it counts in, so every maximum precedes its
-// block's arrival. The counter holds {arrivals, epoch}; its last block arms it for the next
-// launch, and a launch that finds it armed for another epoch counts in on the fallback word
-// by compare-and-swap.
+// block's arrival. The count is grid_arrive's (an epoch per launch, replay slots for captured
+// launches).
 __device__ __forceinline__ void select_greedy_finish(const SelectArgs& args, const SelectBufs& b, uint32_t row,
                                                      uint64_t k, SelCommon& c) {
     const int tid = threadIdx.x;
@@ -502,27 +502,7 @@ __device__ __forceinline__ void select_greedy_finish(const SelectArgs& args, con
                                                                __HIP_MEMORY_SCOPE_AGENT);
         c.red64[0] = seen;  // waits for the return: the maximum is performed before the count
         const uint32_t nb = gridDim.x * gridDim.y;
-        unsigned long long* ctr = reinterpret_cast<unsigned long long*>(b.gctr);
-        const unsigned long long ep = args.epoch;
-        const unsigned long long old = __hip_atomic_fetch_add(ctr, 1ull << 32, __ATOMIC_RELAXED,
-                                                              __HIP_MEMORY_SCOPE_AGENT);
-        bool last;
-        if ((old & 0xFFFFFFFFull) == ep && (old >> 32) < nb) {
-            last = (old >> 32) == nb - 1;
-        } else {
-            // not armed for this launch: every failed exchange means another block counted
-            // itself in, so the loop ends after at most nb tries
-            unsigned long long* c2 = ctr + 1;
-            unsigned long long cur = __hip_atomic_load(c2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), want;
-            do {
-                want = ((cur & 0xFFFFFFFFull) == ep) ? cur + (1ull << 32) : (ep | (1ull << 32));
-            } while (!__hip_atomic_compare_exchange_strong(c2, &cur, want, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                           __HIP_MEMORY_SCOPE_AGENT));
-            last = (want >> 32) == nb;
-        }
-        if (last)  // every block of this launch has added to ctr[0] by now
-            __hip_atomic_exchange(ctr, static_cast<unsigned long long>(args.next_epoch), __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = grid_arrive(reinterpret_cast<unsigned long long*>(b.gctr), nb, args.epoch, args.next_epoch);
         c.misc[7] = last ? 1u : 0u;
     }
     __syncthreads();
@@ -640,6 +620,8 @@ void select_slice_kernel(SelectArgs args_by_value, SelectBufs b) {
         return;
     }
 
+    // a shortlist longer than kMaxWant: the long path finishes the row from its wave records
+    if (p.top_k > static_cast<int32_t>(kMaxWant) && b.vocab > kMaxWant) return;
     // ---- sampled: slice statistics, sampling.cpp:109-118 ----
     // Any NaN makes the row degenerate, so the max only has to be right for NaN-free rows.
     uint32_t nan_seen = 0;
@@ -728,6 +710,7 @@ __global__ __launch_bounds__(kMergeThreads) void select_merge_kernel(SelectArgs 
     }
     const uint32_t want_row = (p.top_k > 0) ? min(static_cast<uint32_t>(p.top_k), b.vocab)
                                             : min(kMaxWant, b.vocab);
+    if (want_row > kMaxWant) return;  // the long path finishes the row
     for (uint32_t i = tid; i < kReps * kBins; i += NT) sh.t.hist[i] = 0;  // for block_top
     // Wave 0: global max and NaN flag over the slices, the row sum
     // sum_q part_sum[q] * exp(part_max[q] - max), and where each slice's ranks go.
@@ -828,6 +811,113 @@ constexpr uint32_t kSmPer = kSampleMaxWaves / kSmThreads;  // wave records per t
 constexpr uint32_t kSmCap = 2048;     // survivors kept in LDS
 constexpr uint32_t kSmMaxCand = 2048; // candidate waves listed in LDS
 
+// A sampled row's statistics from its wave records, and b*: the row max, the sum of
+// exp(l - max) over the row, the binning of wave maxima by distance from the row max
+// (block_top's monotone bins) and the first bin b* at which `want` wave maxima have been
+// counted. Every top-`want` entry lies in a bin <= b*, in a wave whose maximum is in a bin
+// <= b*. One block of kSmThreads threads; thread tid holds records tid + kSmThreads q in key /
+// wsum (0 / 0.0 past the row's records) and receives their maxima in wm. t.hist must be zero
+// and c.exp2_tbl loaded, both published by the barriers inside. `degenerate` (the same in every
+// thread, which then return together) marks a row whose total is NaN or not > 0
+// (sampling.cpp:116-118). Every caller runs this code, so rows finished by different kernels
+// see the same max and total.
+struct RecStats {
+    float gm;
+    double total;
+    float scale;   // bins per unit of distance from gm
+    bool binned;   // false: every value in bin 0
+    uint32_t bstar;
+    bool degenerate;
+};
+
+__device__ __forceinline__ uint32_t rec_bin(const RecStats& r, float x) {
+    if (!r.binned) return 0u;
+    const float dist = (r.gm - x) * r.scale;
+    return dist < static_cast<float>(kBins - 2) ? static_cast<uint32_t>(dist) : kBins - 2;
+}
+
+__device__ __forceinline__ RecStats records_stats(const uint64_t (&key)[kSmPer], const double (&wsum)[kSmPer],
+                                                  float (&wm)[kSmPer], uint32_t want, TopScratch& t,
+                                                  SelCommon& c) {
+    constexpr int NT = kSmThreads;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    RecStats rs{};
+    uint32_t flag = 0;
+    float gm = -INFINITY, mn = INFINITY;
+#pragma unroll
+    for (uint32_t q = 0; q < kSmPer; ++q) {
+        wm[q] = key[q] != 0 ? rank_value(key[q]) : -INFINITY;
+        if (wsum[q] != wsum[q]) flag = 1;
+        gm = fmaxf(gm, wm[q]);
+        if (key[q] != 0 && __builtin_isfinite(wm[q])) mn = fminf(mn, wm[q]);
+    }
+    block_stats<NT>(flag, gm, mn, c);  // NaN seen, row max, smallest finite wave max
+    rs.gm = gm;
+    if (flag != 0) {  // a NaN term makes the total NaN
+        rs.degenerate = true;
+        return rs;
+    }
+    double part = 0.0;
+#pragma unroll
+    for (uint32_t q = 0; q < kSmPer; ++q)
+        if (key[q] != 0 && wsum[q] != 0.0) {
+            // exp_core is exp_for_sum's value on [-700, 0] without its special cases
+            const double x = static_cast<double>(wm[q]) - static_cast<double>(gm);
+            part += wsum[q] * (x >= -700.0 ? exp_core(x, c.exp2_tbl) : exp_for_sum(x, c.exp2_tbl));
+        }
+    // the waves' partial sums cross the histogram's barrier below (block_sum_f64's order)
+    part = wave_reduce(part, 0.0, [](double u, double v) { return u + v; });
+    if (lane == 0) c.redd[wave] = part;
+
+    // ---- b*: bins of distance from the row max (block_top's binning), 8 replicas
+    const float span = gm - mn;
+    rs.binned = __builtin_isfinite(gm) && __builtin_isfinite(mn) && span > 0.0f;
+    rs.scale = rs.binned ? static_cast<float>(kBins - 1) / (span < kBinRange ? span : kBinRange) : 0.0f;
+#pragma unroll
+    for (uint32_t q = 0; q < kSmPer; ++q)
+        if (key[q] != 0) atomicAdd(&t.hist[rec_bin(rs, wm[q]) * kReps + (lane & (kReps - 1))], 1u);
+    __syncthreads();
+    double total = 0.0;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) total += c.redd[w];
+    rs.total = total;
+    if (!(total > 0.0)) {  // every thread sums the same values
+        rs.degenerate = true;
+        return rs;
+    }
+    if (wave == 0) {  // lane l owns bins 4l .. 4l + 3
+        uint32_t cc[4], tsum = 0;
+        const u32x4* h4 = reinterpret_cast<const u32x4*>(t.hist) + lane * (4 * kReps / 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const u32x4 x = h4[2 * j], y = h4[2 * j + 1];
+            cc[j] = x.x + x.y + x.z + x.w + y.x + y.y + y.z + y.w;
+            tsum += cc[j];
+        }
+        uint32_t incl = tsum;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint32_t y = __shfl_up(incl, off);
+            if (lane >= off) incl += y;
+        }
+        uint32_t before = incl - tsum;
+        if (lane == 63) c.misc[0] = kBins - 1;  // fewer maxima than want: every bin
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (before < want && want <= before + cc[j]) c.misc[0] = 4 * lane + j;
+            before += cc[j];
+        }
+        if (lane == 0) {
+            c.misc[3] = 0;  // candidate waves
+            c.misc[4] = 0;  // survivors
+        }
+    }
+    __syncthreads();
+    rs.bstar = c.misc[0];
+    return rs;
+}
+
 struct SampleMergeBufs {
     const float* logits;  // [rows][stride], penalised
     uint64_t stride;
@@ -882,85 +972,19 @@ __global__ __launch_bounds__(kSmThreads) void select_sample_merge_kernel(SelectA
         if (tid == 0) b.tokens[row] = rank_index(k);
         return;
     }
-    float wm[kSmPer];
-    uint32_t flag = 0;
-    float gm = -INFINITY, mn = INFINITY;
-#pragma unroll
-    for (uint32_t q = 0; q < kSmPer; ++q) {
-        wm[q] = key[q] != 0 ? rank_value(key[q]) : -INFINITY;
-        if (wsum[q] != wsum[q]) flag = 1;
-        gm = fmaxf(gm, wm[q]);
-        if (key[q] != 0 && __builtin_isfinite(wm[q])) mn = fminf(mn, wm[q]);
-    }
-    block_stats<NT>(flag, gm, mn, sh.c);  // NaN seen, row max, smallest finite wave max
-    if (flag != 0) {  // sampling.cpp:116-118: a NaN term makes the total NaN
-        if (tid == 0) b.tokens[row] = TWD_TOKEN_DEGENERATE;
-        return;
-    }
-    double part = 0.0;
-#pragma unroll
-    for (uint32_t q = 0; q < kSmPer; ++q)
-        if (key[q] != 0 && wsum[q] != 0.0) {
-            // exp_core is exp_for_sum's value on [-700, 0] without its special cases
-            const double x = static_cast<double>(wm[q]) - static_cast<double>(gm);
-            part += wsum[q] * (x >= -700.0 ? exp_core(x, sh.c.exp2_tbl) : exp_for_sum(x, sh.c.exp2_tbl));
-        }
-    // the waves' partial sums cross the histogram's barrier below (block_sum_f64's order)
-    part = wave_reduce(part, 0.0, [](double u, double v) { return u + v; });
-    if (lane == 0) sh.c.redd[wave] = part;
     const uint32_t want = (p.top_k > 0) ? min(static_cast<uint32_t>(p.top_k), b.vocab)
                                         : min(kMaxWant, b.vocab);
-
-    // ---- b*: bins of distance from the row max (block_top's binning), 8 replicas
-    const float span = gm - mn;
-    const bool binned = __builtin_isfinite(gm) && __builtin_isfinite(mn) && span > 0.0f;
-    const float scale = binned ? static_cast<float>(kBins - 1) / (span < kBinRange ? span : kBinRange) : 0.0f;
-    auto bin_of = [&](float x) -> uint32_t {
-        if (!binned) return 0u;
-        const float dist = (gm - x) * scale;
-        return dist < static_cast<float>(kBins - 2) ? static_cast<uint32_t>(dist) : kBins - 2;
-    };
-#pragma unroll
-    for (uint32_t q = 0; q < kSmPer; ++q)
-        if (key[q] != 0) atomicAdd(&sh.t.hist[bin_of(wm[q]) * kReps + (lane & (kReps - 1))], 1u);
-    __syncthreads();
-    double total = 0.0;
-#pragma unroll
-    for (int w = 0; w < NT / 64; ++w) total += sh.c.redd[w];
-    if (!(total > 0.0)) {  // sampling.cpp:116-118 (uniform: every thread sums the same values)
+    if (want > kMaxWant) return;  // a longer shortlist: the long path finishes the row
+    float wm[kSmPer];
+    const RecStats rs = records_stats(key, wsum, wm, want, sh.t, sh.c);
+    if (rs.degenerate) {  // sampling.cpp:116-118
         if (tid == 0) b.tokens[row] = TWD_TOKEN_DEGENERATE;
         return;
     }
-    if (wave == 0) {  // lane l owns bins 4l .. 4l + 3
-        uint32_t cc[4], tsum = 0;
-        const u32x4* h4 = reinterpret_cast<const u32x4*>(sh.t.hist) + lane * (4 * kReps / 4);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const u32x4 x = h4[2 * j], y = h4[2 * j + 1];
-            cc[j] = x.x + x.y + x.z + x.w + y.x + y.y + y.z + y.w;
-            tsum += cc[j];
-        }
-        uint32_t incl = tsum;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const uint32_t y = __shfl_up(incl, off);
-            if (lane >= off) incl += y;
-        }
-        uint32_t before = incl - tsum;
-        if (lane == 63) sh.c.misc[0] = kBins - 1;  // fewer maxima than want: every bin
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (before < want && want <= before + cc[j]) sh.c.misc[0] = 4 * lane + j;
-            before += cc[j];
-        }
-        if (lane == 0) {
-            sh.c.misc[3] = 0;  // candidate waves
-            sh.c.misc[4] = 0;  // survivors
-        }
-    }
-    __syncthreads();
-    const uint32_t bstar = sh.c.misc[0];
+    const float gm = rs.gm;
+    const double total = rs.total;
+    const uint32_t bstar = rs.bstar;
+    auto bin_of = [&](float x) -> uint32_t { return rec_bin(rs, x); };
     // the candidate waves, in any order
 #pragma unroll
     for (uint32_t q = 0; q < kSmPer; ++q) {
@@ -1072,6 +1096,329 @@ __global__ __launch_bounds__(kSmThreads) void select_sample_merge_kernel(SelectA
     }
     const uint32_t tok = finish_sampled(sh.c, want, p, gm, total);
     if (tid == 0) b.tokens[row] = tok;
+}
+
+// ---- shortlists longer than 256: top_k > 256 -------------------------------------------------------
+//
+// sample_token takes any top_k: its shortlist is the top want = min(top_k, V) entries in the
+// order (value desc, index asc), and steps 5-7 run over all of them (sampling.cpp:120-168).
+// Rows with temperature > 0 and want > 256 are finished here, from the penalised logits and the
+// same wave records as the shorter rows (so the same row max and total):
+//   * long_gather_kernel, one block per row: records_stats, then every entry of a candidate wave
+//     (maximum in a bin <= b*) that lies in a bin <= b*, into the row's sort buffer in any
+//     order. Every top-`want` entry is among them. The buffer is padded with zero ranks (below
+//     every real rank) to a power of two, its sort length;
+//   * a bitonic sort of each buffer into descending order: long_sort_tile_kernel sorts tiles of
+//     kSortTile ranks in LDS (alternating directions); each longer stage k runs its cross-tile
+//     steps (long_sort_step_kernel, one launch per step) and then its in-tile steps
+//     (long_sort_merge_kernel). The launches cover the longest possible buffer; a block past its
+//     row's sort length, or of a stage longer than it, returns at once;
+//   * long_finish_kernel, one block per row: steps 5-7 over the sorted ranks, kFinTile at a
+//     time. The block forms the terms exp(l - max) / total and exp((l - max) / T) in LDS with the
+//     reference's expressions; the two running sums then go in reference order on two lanes of
+//     wave 0 (finish_sampled's loop), and the running sums of the temperature weights are kept in
+//     memory. After the cut (top-p, then top-k), r = u * denom and the draw is the first running
+//     sum >= r: the running sums never decrease, so a search over the tiles' last sums, then
+//     over one tile, finds it.
+constexpr int kLongThreads = 1024;
+constexpr uint32_t kSortTile = 8192;  // ranks sorted in LDS by one block (64 KB)
+constexpr int kStepThreads = 256;
+constexpr uint32_t kFinTile = 2048;   // shortlist entries per tile of the finish
+
+struct LongArgs {
+    uint32_t n;                          // long rows in the launch
+    uint32_t row[TWD_MAX_ROWS + 1];      // each one's row in the call
+    twd_row_params p[TWD_MAX_ROWS + 1];  // and its parameters
+};
+
+struct LongBufs {
+    const float* logits;  // [rows][stride], penalised
+    uint64_t stride;
+    uint32_t vocab;
+    uint32_t waves;       // records per row
+    SampleStats st;       // [row][waves]
+    uint64_t npad;        // sort buffer per long row: a power of two >= vocab
+    uint64_t* keys;       // [n][npad]
+    double* pre;          // [n][npad] running sums of the temperature weights
+    uint32_t* len;        // [n] sort length (0: the row is already finished)
+    float* gmax;          // [n]
+    double* total;        // [n]
+    uint32_t* tokens;
+};
+
+struct LongGatherShared {
+    uint32_t cwave[kSampleMaxWaves];
+    TopScratch t;
+    SelCommon c;
+};
+
+// The long-path kernels read LongArgs (the first kernel argument) through the kernarg segment
+// pointer: indexing the by-value argument with blockIdx would copy it to scratch memory.
+#if __HIP_DEVICE_COMPILE__
+#define TWD_LONG_ARGS(byval) \
+    (*reinterpret_cast<const LongArgs*>(__builtin_amdgcn_kernarg_segment_ptr()))
+#else
+#define TWD_LONG_ARGS(byval) (byval)
+#endif
+
+__global__ __launch_bounds__(kLongThreads) void long_gather_kernel(LongArgs args_by_value, LongBufs b) {
+    constexpr int NT = kLongThreads;
+    static_assert(NT == kSmThreads, "records_stats' block");
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    LongGatherShared& sh = *reinterpret_cast<LongGatherShared*>(smem_raw);
+    const LongArgs& args = TWD_LONG_ARGS(args_by_value);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const uint32_t j = blockIdx.x;
+    const uint32_t row = args.row[j];
+    const twd_row_params p = args.p[j];
+    const uint32_t W = b.waves;
+    const size_t o = static_cast<size_t>(row) * W;
+    const float* lg = b.logits + static_cast<size_t>(row) * b.stride;
+    uint64_t* keys = b.keys + static_cast<size_t>(j) * b.npad;
+
+    if (tid < 64) sh.c.exp2_tbl[tid] = kExp2Table[tid];
+    uint64_t key[kSmPer];
+    double wsum[kSmPer];
+#pragma unroll
+    for (uint32_t q = 0; q < kSmPer; ++q) {
+        const uint32_t i = tid + NT * q;
+        key[q] = i < W ? b.st.key[o + i] : 0ull;
+        wsum[q] = i < W ? b.st.sum[o + i] : 0.0;
+    }
+    for (uint32_t i = tid; i < kReps * kBins; i += NT) sh.t.hist[i] = 0;
+    const uint32_t want = min(static_cast<uint32_t>(p.top_k), b.vocab);
+    float wm[kSmPer];
+    const RecStats rs = records_stats(key, wsum, wm, want, sh.t, sh.c);
+    if (rs.degenerate) {  // sampling.cpp:116-118
+        if (tid == 0) {
+            b.tokens[row] = TWD_TOKEN_DEGENERATE;
+            b.len[j] = 0;
+        }
+        return;
+    }
+    // the candidate waves, in any order (at most W <= kSampleMaxWaves)
+#pragma unroll
+    for (uint32_t q = 0; q < kSmPer; ++q) {
+        const uint32_t i = tid + NT * q;
+        const bool is_cand = key[q] != 0 && rec_bin(rs, wm[q]) <= rs.bstar;
+        const uint64_t mask = __ballot(is_cand);
+        if (mask != 0) {
+            const int leader = __ffsll(static_cast<long long>(mask)) - 1;
+            uint32_t base = 0;
+            if (lane == leader) base = atomicAdd(&sh.c.misc[3], static_cast<uint32_t>(__popcll(mask)));
+            base = __builtin_amdgcn_readlane(base, leader);
+            if (is_cand) {
+                const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+                sh.cwave[base + below] = i;
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t nent = sh.c.misc[3] * kSampleWaveRows;
+    // the survivors into the sort buffer, eight loads requested at a time
+    constexpr uint32_t kBatch = 8;
+    const uint32_t per = (nent + NT - 1) / NT;
+    for (uint32_t i0 = 0; i0 < per; i0 += kBatch) {
+        float v[kBatch];
+        uint32_t r[kBatch];
+#pragma unroll
+        for (uint32_t q = 0; q < kBatch; ++q) {
+            const uint32_t f = (i0 + q) * NT + static_cast<uint32_t>(tid);
+            r[q] = 0xFFFFFFFFu;
+            v[q] = 0.0f;
+            if (i0 + q < per && f < nent) {
+                const uint32_t rr = sh.cwave[f / kSampleWaveRows] * kSampleWaveRows + f % kSampleWaveRows;
+                if (rr < b.vocab) {
+                    r[q] = rr;
+                    v[q] = lg[rr];
+                }
+            }
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < kBatch; ++q) {
+            const bool keep = r[q] != 0xFFFFFFFFu && rec_bin(rs, v[q]) <= rs.bstar;
+            wave_put(keep, keep ? rank_key(v[q], r[q]) : 0ull, &sh.c.misc[4], keys, static_cast<uint32_t>(b.npad));
+        }
+    }
+    __syncthreads();
+    const uint32_t n = sh.c.misc[4];
+    uint32_t len = 1;
+    while (len < n) len <<= 1;
+    for (uint32_t i = n + tid; i < len; i += NT) keys[i] = 0ull;
+    if (tid == 0) {
+        b.len[j] = len;
+        b.gmax[j] = rs.gm;
+        b.total[j] = rs.total;
+    }
+}
+
+// One compare-exchange of the bitonic network over a row's buffer (global positions): the pair
+// (i, i | jj) in stage k is put in descending order when bit k of i is clear, ascending when it
+// is set, so the last stage (k = length) leaves the whole buffer descending.
+__device__ __forceinline__ void bitonic_pair(uint64_t& a, uint64_t& c, uint64_t gi, uint64_t k) {
+    const bool desc = (gi & k) == 0;
+    if (desc ? a < c : a > c) {
+        const uint64_t t = a;
+        a = c;
+        c = t;
+    }
+}
+
+// steps jj = j0, j0 / 2, .., 1 of stage k on the LDS tile s of `t` ranks starting at global base
+__device__ __forceinline__ void bitonic_tile_steps(uint64_t* s, uint32_t t, uint64_t base, uint64_t k, uint32_t j0) {
+    for (uint32_t jj = j0; jj > 0; jj >>= 1) {
+        for (uint32_t q = threadIdx.x; q < t / 2; q += blockDim.x) {
+            const uint32_t i = ((q & ~(jj - 1)) << 1) | (q & (jj - 1));
+            uint64_t a = s[i], c = s[i | jj];
+            bitonic_pair(a, c, base + i, k);
+            s[i] = a;
+            s[i | jj] = c;
+        }
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(kLongThreads) void long_sort_tile_kernel(LongBufs b, uint32_t tile) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    uint64_t* s = reinterpret_cast<uint64_t*>(smem_raw);
+    const uint32_t j = blockIdx.y;
+    const uint32_t len = b.len[j];
+    const uint64_t base = static_cast<uint64_t>(blockIdx.x) * tile;
+    if (base >= len) return;  // the whole block
+    const uint32_t t = min(tile, len);  // both powers of two
+    uint64_t* keys = b.keys + static_cast<size_t>(j) * b.npad + base;
+    for (uint32_t i = threadIdx.x; i < t; i += blockDim.x) s[i] = keys[i];
+    __syncthreads();
+    for (uint32_t k = 2; k <= t; k <<= 1) bitonic_tile_steps(s, t, base, k, k >> 1);
+    for (uint32_t i = threadIdx.x; i < t; i += blockDim.x) keys[i] = s[i];
+}
+
+__global__ __launch_bounds__(kStepThreads) void long_sort_step_kernel(LongBufs b, uint32_t k, uint32_t jj) {
+    const uint32_t j = blockIdx.y;
+    const uint32_t len = b.len[j];
+    const uint64_t q = static_cast<uint64_t>(blockIdx.x) * kStepThreads + threadIdx.x;
+    if (k > len || 2 * q >= len) return;
+    const uint64_t i = ((q & ~static_cast<uint64_t>(jj - 1)) << 1) | (q & (jj - 1));
+    uint64_t* keys = b.keys + static_cast<size_t>(j) * b.npad;
+    uint64_t a = keys[i], c = keys[i | jj];
+    bitonic_pair(a, c, i, k);
+    keys[i] = a;
+    keys[i | jj] = c;
+}
+
+__global__ __launch_bounds__(kLongThreads) void long_sort_merge_kernel(LongBufs b, uint32_t tile, uint32_t k) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    uint64_t* s = reinterpret_cast<uint64_t*>(smem_raw);
+    const uint32_t j = blockIdx.y;
+    const uint32_t len = b.len[j];
+    const uint64_t base = static_cast<uint64_t>(blockIdx.x) * tile;
+    if (k > len || base >= len) return;  // the whole block; here len >= k > tile
+    uint64_t* keys = b.keys + static_cast<size_t>(j) * b.npad + base;
+    for (uint32_t i = threadIdx.x; i < tile; i += blockDim.x) s[i] = keys[i];
+    __syncthreads();
+    bitonic_tile_steps(s, tile, base, k, tile >> 1);
+    for (uint32_t i = threadIdx.x; i < tile; i += blockDim.x) keys[i] = s[i];
+}
+
+struct LongFinishShared {
+    double e[kFinTile];  // exp(l - max) / total, then lane 1's running sums
+    double q[kFinTile];  // exp((l - max) / T), then lane 0's running sums
+    uint32_t misc[4];
+    uint32_t best;
+};
+
+__global__ __launch_bounds__(kLongThreads) void long_finish_kernel(LongArgs args_by_value, LongBufs b) {
+    constexpr int NT = kLongThreads;
+    __shared__ LongFinishShared sh;
+    const LongArgs& args = TWD_LONG_ARGS(args_by_value);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t j = blockIdx.x;
+    if (b.len[j] == 0) return;  // degenerate: long_gather_kernel wrote its token
+    const uint32_t row = args.row[j];
+    const twd_row_params p = args.p[j];
+    const uint64_t* keys = b.keys + static_cast<size_t>(j) * b.npad;
+    double* pre = b.pre + static_cast<size_t>(j) * b.npad;
+    const uint32_t want = min(static_cast<uint32_t>(p.top_k), b.vocab);
+    const double mx = static_cast<double>(b.gmax[j]);
+    const double total = b.total[j];
+    const double td = static_cast<double>(p.temperature);
+    const bool topp = p.top_p < 1.0f;
+    const double pp = static_cast<double>(p.top_p);
+    constexpr uint32_t kChunk = 16;
+    double run = 0.0;  // wave 0: lane 0's sum of the weights, lane 1's top-p sum
+    uint32_t cut = want;
+    if (tid == 0) sh.misc[0] = 0;
+    for (uint32_t t0 = 0; t0 < want; t0 += kFinTile) {
+        const uint32_t cnt = min(kFinTile, want - t0);
+        // steps 5 and 7's terms, as sampling.cpp:145 and :157 form them
+        for (uint32_t i = tid; i < cnt; i += NT) {
+            const double l = static_cast<double>(rank_value(keys[t0 + i]));
+            sh.q[i] = exp_libm((l - mx) / td);
+            if (topp) sh.e[i] = exp_libm(l - mx) / total;
+        }
+        __syncthreads();
+        if (wave == 0 && lane < 2) {
+            // lane 0 reads q and stores its running sums over q; lane 1 does the same over e
+            // (over q when top-p is off: its sums are then never used)
+            double* src = (lane == 0 || !topp) ? sh.q : sh.e;
+            double x[kChunk];
+#pragma unroll
+            for (uint32_t jj = 0; jj < kChunk; ++jj) x[jj] = src[min(jj, cnt - 1)];
+            for (uint32_t i0 = 0; i0 < cnt; i0 += kChunk) {
+                double xn[kChunk], pr[kChunk];
+                if (i0 + kChunk < cnt) {
+#pragma unroll
+                    for (uint32_t jj = 0; jj < kChunk; ++jj) xn[jj] = src[min(i0 + kChunk + jj, cnt - 1)];
+                }
+#pragma unroll
+                for (uint32_t jj = 0; jj < kChunk; ++jj) {
+                    run += x[jj];
+                    pr[jj] = run;
+                }
+                uint32_t hit = 0;
+#pragma unroll
+                for (uint32_t jj = 0; jj < kChunk; ++jj) {
+                    src[i0 + jj] = pr[jj];  // i0 + jj < cnt rounded up to kChunk <= kFinTile
+                    hit |= (pr[jj] >= pp ? 1u : 0u) << jj;
+                }
+                uint32_t h1 = __builtin_amdgcn_readlane(hit, 1);
+                h1 &= cnt - i0 >= kChunk ? 0xFFFFu : ((1u << (cnt - i0)) - 1u);
+                if (topp && h1 != 0) {  // lane 0's sums cover the cut
+                    if (lane == 0) sh.misc[0] = t0 + i0 + static_cast<uint32_t>(__builtin_ctz(h1)) + 1;
+                    break;
+                }
+#pragma unroll
+                for (uint32_t jj = 0; jj < kChunk; ++jj) x[jj] = xn[jj];
+            }
+        }
+        __syncthreads();
+        const uint32_t c = sh.misc[0];  // the cut, once the top-p sum has reached p
+        const uint32_t keep = c != 0 ? c - t0 : cnt;
+        for (uint32_t i = tid; i < keep; i += NT) pre[t0 + i] = sh.q[i];
+        if (c != 0) {
+            cut = c;
+            break;
+        }
+        __syncthreads();  // the next tile's terms overwrite sh
+    }
+    if (p.top_k > 0 && cut > static_cast<uint32_t>(p.top_k)) cut = static_cast<uint32_t>(p.top_k);
+    if (cut < 1) cut = 1;
+    if (tid == 0) sh.best = cut - 1;  // the reference's fallback: the last survivor
+    __syncthreads();                  // also publishes pre (block scope)
+    const double r = static_cast<double>(p.uniform) * pre[cut - 1];  // r = u * denom
+    // the first tile whose last running sum (within the cut) reaches r, then its first entry
+    const uint32_t ntiles = (cut + kFinTile - 1) / kFinTile;
+    if (tid == 0) sh.misc[1] = ntiles - 1;
+    __syncthreads();
+    for (uint32_t t = tid; t < ntiles; t += NT)
+        if (pre[min((t + 1) * kFinTile, cut) - 1] >= r) atomicMin(&sh.misc[1], t);
+    __syncthreads();
+    const uint32_t t0 = sh.misc[1] * kFinTile, t1 = min(t0 + kFinTile, cut);
+    for (uint32_t i = t0 + tid; i < t1; i += NT)
+        if (pre[i] >= r) atomicMin(&sh.best, i);
+    __syncthreads();
+    if (tid == 0) b.tokens[row] = rank_index(keys[sh.best]);
 }
 
 // ---- the wave-record path for logits that are already in memory ---------------------------------
@@ -1348,8 +1695,9 @@ constexpr size_t kStaticOffMax = kStaticOffKey + 8 * kStaticSlots;    // float [
 constexpr size_t kStaticOffFlag = kStaticOffMax + 4 * kStaticSlots;   // uint32 [slots]
 constexpr size_t kStaticOffCount = kStaticOffFlag + 4 * kStaticSlots; // uint32 [slots]
 constexpr size_t kStaticOffCand = kStaticOffCount + 4 * kStaticSlots; // uint64 [slots][kMaxWant]
-constexpr size_t kStaticOffGbest = kStaticOffCand + 8 * kStaticSlots * kMaxWant;  // uint64 [rows + 2]
-constexpr size_t kStaticBytes = kStaticOffGbest + 8 * (kStaticRows + 2);  // 4,252,176 B
+constexpr size_t kStaticOffGbest = kStaticOffCand + 8 * kStaticSlots * kMaxWant;  // uint64 [rows + kArriveWords]
+constexpr size_t kStaticBytes = kStaticOffGbest + 8 * (kStaticRows + kArriveWords);  // 4,252,208 B
+static_assert(kStaticBytes == 4252208, "the size twd_head.h states");
 static_assert(kStaticOffCand % 256 == 0, "candidate array alignment");
 
 static __device__ __align__(256) unsigned char scratch[kStaticBytes];
@@ -1389,8 +1737,8 @@ int static_scratch(SelectScratch* out) {
     s.part_flag = reinterpret_cast<uint32_t*>(b + kStaticOffFlag);
     s.part_count = reinterpret_cast<uint32_t*>(b + kStaticOffCount);
     s.cand = reinterpret_cast<uint64_t*>(b + kStaticOffCand);
-    // zero at load: the first one-pass greedy launch finds its counter unarmed and counts in on
-    // the fallback word, then arms it for the next
+    // zero at load: the first one-pass greedy launch on a GPU finds the counter unarmed and
+    // counts in on the fallback word, then arms it for the next
     s.gbest = reinterpret_cast<uint64_t*>(b + kStaticOffGbest);
     s.gctr = s.gbest + kStaticRows;
     s.epoch = &g_static_epoch[dev];
@@ -1418,11 +1766,14 @@ int scratch_alloc(SelectScratch* s, uint32_t max_vocab, uint32_t max_rows) {
     const size_t nw = static_cast<size_t>(max_rows) * s->wave_cap;
     if (e == hipSuccess) e = hipMalloc(&s->wkey, nw * sizeof(uint64_t));
     if (e == hipSuccess) e = hipMalloc(&s->wsum, nw * sizeof(double));
-    if (e == hipSuccess) e = hipMalloc(&s->gbest, (max_rows + 2) * sizeof(uint64_t));
-    if (e == hipSuccess) e = hipMemset(s->gbest, 0, (max_rows + 2) * sizeof(uint64_t));
+    if (e == hipSuccess) e = hipMalloc(&s->gbest, (max_rows + kArriveWords) * sizeof(uint64_t));
+    if (e == hipSuccess) e = hipMemset(s->gbest, 0, (max_rows + kArriveWords) * sizeof(uint64_t));
+    const uint64_t armed = kFirstEpoch;  // the counter starts armed for the first launch
+    if (e == hipSuccess) e = hipMemcpy(s->gbest + max_rows, &armed, sizeof(armed), hipMemcpyHostToDevice);
     if (e == hipSuccess) {
         s->gctr = s->gbest + max_rows;
-        s->epoch = new uint32_t(0);
+        s->epoch = new uint32_t(kFirstEpoch - 1);
+        s->lng = new LongScratch();
     }
     if (e != hipSuccess) {
         scratch_free(s);
@@ -1443,7 +1794,95 @@ void scratch_free(SelectScratch* s) {
     (void)hipFree(s->wsum);
     (void)hipFree(s->gbest);
     delete s->epoch;
+    if (s->lng) {
+        long_free(s->lng);
+        delete s->lng;
+    }
     *s = SelectScratch{};
+}
+
+void long_free(LongScratch* l) {
+    (void)hipFree(l->keys);
+    (void)hipFree(l->pre);
+    (void)hipFree(l->len);
+    (void)hipFree(l->gmax);
+    (void)hipFree(l->total);
+    *l = LongScratch{};
+}
+
+namespace {
+int long_reserve(LongScratch* l, uint32_t rows, uint64_t npad) {
+    if (l->keys && l->rows_cap >= rows && l->npad_cap >= npad) return TWD_OK;
+    const uint32_t r = std::max(rows, l->rows_cap);
+    const uint64_t n = std::max(npad, l->npad_cap);
+    long_free(l);  // waits for the device (hipFree) before the old buffers go
+    const size_t m = static_cast<size_t>(r) * n;
+    hipError_t e = hipSuccess;
+    if (e == hipSuccess) e = hipMalloc(&l->keys, m * sizeof(uint64_t));
+    if (e == hipSuccess) e = hipMalloc(&l->pre, m * sizeof(double));
+    if (e == hipSuccess) e = hipMalloc(&l->len, r * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&l->gmax, r * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&l->total, r * sizeof(double));
+    if (e != hipSuccess) {
+        long_free(l);
+        return hip_fail(e, "allocating the long-shortlist scratch");
+    }
+    l->rows_cap = r;
+    l->npad_cap = n;
+    return TWD_OK;
+}
+}  // namespace
+
+int launch_long(LongScratch* lng, const SampleStats& st, uint32_t waves, const float* logits, uint64_t stride,
+                uint32_t vocab, uint32_t rows, const twd_row_params* params, uint32_t* tokens,
+                hipStream_t stream) {
+    LongArgs a{};
+    for (uint32_t r = 0; r < rows; ++r) {
+        if (!long_row(params[r], vocab)) continue;
+        a.row[a.n] = r;
+        a.p[a.n] = params[r];
+        ++a.n;
+    }
+    if (a.n == 0) return TWD_OK;
+    if (!lng) return fail(TWD_E_INVALID, "top_k > 256 needs a selector's scratch (twd_select)");
+    if (waves == 0 || waves > kSampleMaxWaves) return fail(TWD_E_INVALID, "long shortlist: wave records out of range");
+    uint64_t npad = 1;
+    while (npad < vocab) npad <<= 1;
+    int rc = long_reserve(lng, a.n, npad);
+    if (rc) return rc;
+    LongBufs b{};
+    b.logits = logits;
+    b.stride = stride;
+    b.vocab = vocab;
+    b.waves = waves;
+    b.st = st;
+    b.npad = npad;
+    b.keys = lng->keys;
+    b.pre = lng->pre;
+    b.len = lng->len;
+    b.gmax = lng->gmax;
+    b.total = lng->total;
+    b.tokens = tokens;
+    long_gather_kernel<<<a.n, kLongThreads, sizeof(LongGatherShared), stream>>>(a, b);
+    TWD_HIP(hipGetLastError());
+    const uint32_t tile = static_cast<uint32_t>(std::min<uint64_t>(npad, kSortTile));
+    const size_t tile_bytes = static_cast<size_t>(tile) * sizeof(uint64_t);
+    const uint32_t ntile = static_cast<uint32_t>(npad / tile);
+    long_sort_tile_kernel<<<dim3(ntile, a.n), kLongThreads, tile_bytes, stream>>>(b, tile);
+    TWD_HIP(hipGetLastError());
+    for (uint64_t k = 2ull * tile; k <= npad; k <<= 1) {
+        for (uint64_t jj = k >> 1; jj >= tile; jj >>= 1) {
+            long_sort_step_kernel<<<dim3(static_cast<uint32_t>(npad / 2 / kStepThreads), a.n), kStepThreads, 0,
+                                    stream>>>(b, static_cast<uint32_t>(k), static_cast<uint32_t>(jj));
+            TWD_HIP(hipGetLastError());
+        }
+        long_sort_merge_kernel<<<dim3(ntile, a.n), kLongThreads, tile_bytes, stream>>>(b, tile,
+                                                                                       static_cast<uint32_t>(k));
+        TWD_HIP(hipGetLastError());
+    }
+    long_finish_kernel<<<a.n, kLongThreads, 0, stream>>>(a, b);
+    TWD_HIP(hipGetLastError());
+    return TWD_OK;
 }
 
 // Lets the selection kernels use the LDS they need (no memory is allocated).
@@ -1462,6 +1901,18 @@ int enable_select_kernels() {
             err = hipFuncSetAttribute(reinterpret_cast<const void*>(select_sample_merge_kernel),
                                       hipFuncAttributeMaxDynamicSharedMemorySize,
                                       static_cast<int>(sizeof(SampleMergeShared)));
+        if (err == hipSuccess)
+            err = hipFuncSetAttribute(reinterpret_cast<const void*>(long_gather_kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      static_cast<int>(sizeof(LongGatherShared)));
+        if (err == hipSuccess)
+            err = hipFuncSetAttribute(reinterpret_cast<const void*>(long_sort_tile_kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      static_cast<int>(kSortTile * sizeof(uint64_t)));
+        if (err == hipSuccess)
+            err = hipFuncSetAttribute(reinterpret_cast<const void*>(long_sort_merge_kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      static_cast<int>(kSortTile * sizeof(uint64_t)));
     });
     if (err != hipSuccess) return hip_fail(err, "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
     return TWD_OK;
@@ -1481,18 +1932,21 @@ int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_
     a.rows = rows;
     a.parts = parts;
     a.penalty_only = penalty_only ? 1u : 0u;
+    bool any_long = false;
     for (uint32_t r = 0; r < rows; ++r) {
         const twd_row_params& p = params[r];
-        if (p.temperature > 0.0f && p.top_k > static_cast<int32_t>(kMaxWant))
-            return fail(TWD_E_UNSUPPORTED, "top_k > 256 is not supported on the device path (validate_sampling rejects it)");
         if (p.repetition_penalty != 1.0f && p.history_len > 0 && !history)
             return fail(TWD_E_INVALID, "null history with a non-empty history_len");
         a.p[r] = p;
+        any_long |= !penalty_only && long_row(p, vocab);
     }
+    const uint32_t waves = (vocab + kSampleWaveRows - 1) / kSampleWaveRows;
+    const bool have_records = s.wkey != nullptr && waves <= s.wave_cap && waves <= kSampleMaxWaves;
+    if (any_long && (!s.lng || !have_records))
+        return fail(TWD_E_INVALID, "top_k > 256 needs a selector's scratch (twd_select, not twd_select_noalloc)");
     // sampled rows with short histories: the wave-record path (penalty pass, per-64-entry
     // statistics, then the one-block-per-row merge that reads only the candidate waves)
-    const uint32_t waves = (vocab + kSampleWaveRows - 1) / kSampleWaveRows;
-    bool records = !penalty_only && s.wkey != nullptr && waves <= s.wave_cap && waves <= kSampleMaxWaves;
+    bool records = !penalty_only && have_records;
     bool any_sampled = false, any_penalty = false;
     for (uint32_t r = 0; r < rows; ++r) {
         const twd_row_params& p = params[r];
@@ -1524,7 +1978,7 @@ int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_
         mb.tokens = tokens;
         select_sample_merge_kernel<<<rows, kSmThreads, sizeof(SampleMergeShared), stream>>>(a, mb);
         TWD_HIP(hipGetLastError());
-        return TWD_OK;
+        return launch_long(s.lng, st, waves, logits, stride, vocab, rows, params, tokens, stream);
     }
     SelectBufs b{};
     b.logits = logits;
@@ -1540,10 +1994,10 @@ int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_
     b.cand = s.cand;
     // every row greedy: the slice blocks finish the rows (one launch instead of two)
     if (!penalty_only && !any_sampled && parts > 1 && s.gbest && s.gctr && s.epoch) {
-        *s.epoch = *s.epoch % 0x7FFFFFFFu + 1u;  // 1 .. 2^31 - 1, never 0
+        *s.epoch = epoch_after(*s.epoch);  // 1 .. 2^31 - 1, never 0
         a.one_pass = 1;
         a.epoch = *s.epoch;
-        a.next_epoch = *s.epoch % 0x7FFFFFFFu + 1u;
+        a.next_epoch = epoch_after(*s.epoch);
         b.gbest = s.gbest;
         b.gctr = s.gctr;
     }
@@ -1553,12 +2007,20 @@ int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_
         select_merge_kernel<<<rows, kMergeThreads, sizeof(MergeShared), stream>>>(a, b);
         TWD_HIP(hipGetLastError());
     }
+    if (any_long) {  // their wave records from the penalised logits, then the long path
+        const SampleStats st{s.wkey, s.wsum};
+        WaveStatsBufs wb{logits, stride, vocab, waves,
+                         (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && (stride & 3) == 0 ? 1u : 0u, st};
+        wave_stats_kernel<1><<<dim3((vocab + kWsEntries - 1) / kWsEntries, rows), kWsThreads, 0, stream>>>(wb);
+        TWD_HIP(hipGetLastError());
+        return launch_long(s.lng, st, waves, logits, stride, vocab, rows, params, tokens, stream);
+    }
     return TWD_OK;
 }
 
 int launch_sample_merge(const SampleStats& st, uint32_t waves, const float* logits, uint32_t vocab,
                         uint32_t rows, const twd_row_params* params, uint32_t* tokens,
-                        hipStream_t stream) {
+                        LongScratch* lng, hipStream_t stream) {
     if (waves == 0 || waves > kSampleMaxWaves) return fail(TWD_E_INVALID, "sample merge: head waves out of range");
     if (rows == 0 || rows > TWD_MAX_ROWS) return fail(TWD_E_INVALID, "sample merge: rows out of range");
     int rc = enable_select_kernels();
@@ -1576,7 +2038,7 @@ int launch_sample_merge(const SampleStats& st, uint32_t waves, const float* logi
     b.tokens = tokens;
     select_sample_merge_kernel<<<rows, kSmThreads, sizeof(SampleMergeShared), stream>>>(a, b);
     TWD_HIP(hipGetLastError());
-    return TWD_OK;
+    return launch_long(lng, st, waves, logits, vocab, vocab, rows, params, tokens, stream);
 }
 
 int launch_verify_compare(const uint32_t* row_tokens, uint32_t rows, const uint32_t* drafts,

@@ -198,6 +198,75 @@ __device__ __forceinline__ double exp_core(double x, const double* tbl) {
     return __builtin_bit_cast(double, tb) * p;
 }
 
+// ---- which block of a launch arrives last ----------------------------------------------------
+//
+// Launches whose last block finishes the work (the head's greedy finish, the one-pass greedy
+// selection, the draft verify's accept chain) count their blocks in on an arrival counter of
+// kArriveWords uint64 words, each {arrivals (high 32 bits), epoch (low 32 bits)}. The host gives
+// every launch an epoch (1 .. 2^31 - 1, never 0) and the next one's; a block adds 1 to the high
+// half of a word, which never carries into the epoch, so every block of a launch sees the same
+// epoch in a word until the launch's last block rewrites it.
+//   * word 0, the eager word: armed {0, epoch} for the launch by the previous launch's last
+//     block (or at allocation for the first). Every launch of a host thread's call sequence
+//     finishes on it with one atomic add per block.
+//   * words 1 .. kArriveSlots, the replay slots: a launch repeated with frozen arguments (a
+//     captured graph replayed) carries an epoch that word 0 is no longer armed for. It counts in
+//     on slot (epoch % kArriveSlots), which the previous launch of the same arguments armed with
+//     its epoch; its last block re-arms the slot and takes this launch's adds back out of word 0,
+//     leaving word 0 armed for the next eager launch.
+//   * the last word, the fallback: a launch that finds neither armed for it (the first replay of
+//     a captured launch, another capture's epoch in the slot, a count written from outside) counts
+//     in by compare-and-swap with its epoch attached, starting afresh over any other epoch or a
+//     count that already reached nb. Every failed swap means another block counted itself in, so
+//     that loop ends after at most nb tries. Its last block arms word 0 for the next launch and
+//     the slot for this launch's arguments.
+// Every block of a launch takes the same word: the words' epochs do not change until all nb
+// blocks have counted in, and a word's count is 0 when it is armed. Exactly one block returns
+// true, after every other block of the launch has counted in.
+constexpr uint32_t kArriveSlots = 4;
+constexpr uint32_t kArriveWords = 2 + kArriveSlots;
+
+// First epoch of a counter; allocation arms word 0 with it.
+constexpr uint32_t kFirstEpoch = 1;
+inline uint32_t epoch_after(uint32_t e) { return e % 0x7FFFFFFFu + 1u; }
+
+__device__ __forceinline__ bool grid_arrive(unsigned long long* ctr, uint32_t nb, uint32_t epoch,
+                                            uint32_t next_epoch) {
+    constexpr unsigned long long kOne = 1ull << 32, kLo = 0xFFFFFFFFull;
+    const unsigned long long ep = epoch;
+    const unsigned long long o0 = __hip_atomic_fetch_add(ctr, kOne, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((o0 & kLo) == ep && (o0 >> 32) < nb) {
+        const bool last = (o0 >> 32) == nb - 1;
+        if (last)
+            __hip_atomic_exchange(ctr, static_cast<unsigned long long>(next_epoch), __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+        return last;
+    }
+    unsigned long long* slot = ctr + 1 + epoch % kArriveSlots;
+    const unsigned long long o1 = __hip_atomic_fetch_add(slot, kOne, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((o1 & kLo) == ep && (o1 >> 32) < nb) {
+        const bool last = (o1 >> 32) == nb - 1;
+        if (last) {  // every block has added to word 0 and the slot by now
+            __hip_atomic_exchange(ctr, o0 & kLo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_exchange(slot, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return last;
+    }
+    unsigned long long* fb = ctr + 1 + kArriveSlots;
+    unsigned long long cur = __hip_atomic_load(fb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), want;
+    do {
+        want = ((cur & kLo) == ep && (cur >> 32) < nb) ? cur + kOne : (ep | kOne);
+    } while (!__hip_atomic_compare_exchange_strong(fb, &cur, want, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT));
+    const bool last = (want >> 32) == nb;
+    if (last) {  // every block has added to word 0 and the slot by now
+        __hip_atomic_exchange(ctr, static_cast<unsigned long long>(next_epoch), __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_exchange(slot, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return last;
+}
+
 // bf16 bit patterns <-> float
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
@@ -241,10 +310,36 @@ struct SampleStats {
 constexpr uint32_t kSampleMaxWaves = 8192;  // waves a fused sample pass may have
 constexpr uint32_t kSampleWaveRows = 64;    // vocabulary rows per wave
 
-// Enqueues the merge after a sample-mode head pass over `rows` rows (params: host array).
+// Sort and finish buffers of the rows whose shortlist is longer than kMaxWant (top_k > 256),
+// grown on demand by the calls that have such rows.
+struct LongScratch {
+    uint64_t* keys = nullptr;  // [rows][npad] ranks to sort
+    double* pre = nullptr;     // [rows][npad] running sums of the temperature weights
+    uint32_t* len = nullptr;   // [rows] sort length
+    float* gmax = nullptr;     // [rows] row max
+    double* total = nullptr;   // [rows] sum of exp(l - max)
+    uint32_t rows_cap = 0;
+    uint64_t npad_cap = 0;
+};
+void long_free(LongScratch* l);
+
+// True for a row that the long path finishes: temperature > 0 and min(top_k, vocab) > kMaxWant.
+inline bool long_row(const twd_row_params& p, uint32_t vocab) {
+    return p.temperature > 0.0f && p.top_k > static_cast<int32_t>(kMaxWant) && vocab > kMaxWant;
+}
+
+// Enqueues the long path for those of `rows` rows that need it, after their penalised logits
+// and wave records (`waves` per row, row stride of the records) are in place. `lng` may be
+// null only when no row needs it.
+int launch_long(LongScratch* lng, const SampleStats& st, uint32_t waves, const float* logits, uint64_t stride,
+                uint32_t vocab, uint32_t rows, const twd_row_params* params, uint32_t* tokens,
+                hipStream_t stream);
+
+// Enqueues the merge after a sample-mode head pass over `rows` rows (params: host array), and
+// the long path for rows with top_k > 256 (lng: their scratch).
 int launch_sample_merge(const SampleStats& st, uint32_t waves, const float* logits, uint32_t vocab,
                         uint32_t rows, const twd_row_params* params, uint32_t* tokens,
-                        hipStream_t stream);
+                        LongScratch* lng, hipStream_t stream);
 
 // ---- device scratch shared by the launch helpers ------------------------------------------------------
 struct SelectScratch {
@@ -263,8 +358,9 @@ struct SelectScratch {
     // one-pass greedy launches: per-row best ranks (zero between launches), the arrival counter
     // {arrivals, epoch} and its fallback word, and the host's epoch of the last such launch
     uint64_t* gbest = nullptr;          // [max_rows]
-    uint64_t* gctr = nullptr;           // [2]
+    uint64_t* gctr = nullptr;           // [kArriveWords]
     uint32_t* epoch = nullptr;          // host memory
+    LongScratch* lng = nullptr;         // rows with top_k > 256 (null: not supported)
 };
 
 int scratch_alloc(SelectScratch* s, uint32_t max_vocab, uint32_t max_rows);

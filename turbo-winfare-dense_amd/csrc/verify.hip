@@ -1137,35 +1137,9 @@ struct DraftFinish {  // the accept chain's inputs: the residual launch's last b
     uint32_t nd;
     uint64_t has_draft;
     twd_verify_result* v;
-    unsigned long long* ctr;     // [2] arrival counter {arrivals << 32 | epoch} and its fallback
+    unsigned long long* ctr;     // [kArriveWords] grid_arrive's arrival counter
     uint32_t epoch, next_epoch;  // this call's epoch (never 0) and the next call's
 };
-
-// Counts the calling block in (one thread). True in the last of the nb blocks to arrive. The
-// counter is armed with this call's epoch by the previous call's last block; when it is not
-// (the first call, a call that did not finish, a write from outside), the blocks count in on
-// the fallback word by compare-and-swap with the epoch attached, and every failed swap means
-// another block counted itself in, so that loop ends after at most nb tries.
-__device__ bool last_to_arrive(unsigned long long* ctr, uint32_t epoch, uint32_t next_epoch, uint32_t nb) {
-    const unsigned long long ep = epoch;
-    const unsigned long long old = __hip_atomic_fetch_add(ctr, 1ull << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    bool last;
-    if ((old & 0xFFFFFFFFull) == ep && (old >> 32) < nb) {
-        last = (old >> 32) == nb - 1;
-    } else {
-        unsigned long long* c2 = ctr + 1;
-        unsigned long long cur = __hip_atomic_load(c2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), want;
-        do {
-            want = ((cur & 0xFFFFFFFFull) == ep) ? cur + (1ull << 32) : (ep | (1ull << 32));
-        } while (!__hip_atomic_compare_exchange_strong(c2, &cur, want, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                       __HIP_MEMORY_SCOPE_AGENT));
-        last = (want >> 32) == nb;
-    }
-    if (last)  // every block of this launch has added to ctr[0] by now: arm it for the next call
-        __hip_atomic_exchange(ctr, static_cast<unsigned long long>(next_epoch), __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
-    return last;
-}
 
 __global__ __launch_bounds__(kRejThreads) void seg_residual_kernel(DraftArgs a, const uint32_t* live,
                                                                    const SegRec* rec, const SegHead* heads,
@@ -1178,7 +1152,7 @@ __global__ __launch_bounds__(kRejThreads) void seg_residual_kernel(DraftArgs a, 
     // first; the last block reads every outcome after an acquiring fence
     if (threadIdx.x == 0) {
         __threadfence();
-        if (last_to_arrive(f.ctr, f.epoch, f.next_epoch, gridDim.x)) {
+        if (grid_arrive(f.ctr, gridDim.x, f.epoch, f.next_epoch)) {
             __threadfence();
             draft_finish_body(f.row_tokens, f.rows, f.drafts, f.nd, f.has_draft, a.rej, f.v);
         }
@@ -1322,27 +1296,39 @@ __device__ void draft_finish_body(const uint32_t* row_tokens, uint32_t rows, con
 int draft_scratch_reserve(DraftScratch* d, uint32_t vocab, uint32_t npos) {
     const uint32_t parts = (vocab + kDraftChunk - 1) / kDraftChunk;
     const size_t need_e = static_cast<size_t>(2) * npos * ((vocab + 15u) & ~15u);
-    if (d->e && d->side && d->e_capacity >= need_e && d->part_capacity >= static_cast<size_t>(2) * npos * parts)
-        return TWD_OK;
+    const size_t need_part = static_cast<size_t>(2) * npos * parts;
+    // the capacities are set only once every buffer exists, so a call after a failed one never
+    // finds a partial set
+    if (d->e_capacity >= need_e && d->part_capacity >= need_part && d->side) return TWD_OK;
     draft_scratch_free(d);  // grows: later calls with as many positions reuse it
-    TWD_HIP(hipMalloc(&d->e, need_e * sizeof(float)));
-    d->e_capacity = need_e;
-    TWD_HIP(hipMalloc(&d->part, static_cast<size_t>(2) * npos * parts * sizeof(float)));
-    d->part_capacity = static_cast<size_t>(2) * npos * parts;
-    TWD_HIP(hipMalloc(&d->flags, 2 * TWD_MAX_ROWS * sizeof(uint32_t)));
-    TWD_HIP(hipMalloc(&d->rej, 4 * TWD_MAX_ROWS * sizeof(uint32_t)));
-    TWD_HIP(hipMalloc(&d->sums, 2 * TWD_MAX_ROWS * sizeof(float)));
-    TWD_HIP(hipMalloc(&d->seg_d, static_cast<size_t>(2) * TWD_MAX_ROWS * (kSegMax + 1) * sizeof(double)));
-    TWD_HIP(hipMalloc(&d->seg_rec, static_cast<size_t>(2) * TWD_MAX_ROWS * kSegMax * sizeof(SegRec)));
-    TWD_HIP(hipMalloc(&d->seg_head, static_cast<size_t>(2) * TWD_MAX_ROWS * sizeof(SegHead)));
-    TWD_HIP(hipMalloc(&d->live, TWD_MAX_ROWS * sizeof(uint32_t)));
-    TWD_HIP(hipMalloc(&d->fin_ctr, 2 * sizeof(uint64_t)));
-    TWD_HIP(hipMemset(d->fin_ctr, 0, 2 * sizeof(uint64_t)));  // epoch 0 is never a call's
-    if (!d->side) {  // kept across growth: freed with the selector
-        TWD_HIP(hipStreamCreateWithFlags(&d->side, hipStreamNonBlocking));
-        TWD_HIP(hipEventCreateWithFlags(&d->fork, hipEventDisableTiming));
-        TWD_HIP(hipEventCreateWithFlags(&d->join, hipEventDisableTiming));
+    hipError_t e = hipSuccess;
+    if (e == hipSuccess) e = hipMalloc(&d->e, need_e * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&d->part, need_part * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&d->flags, 2 * TWD_MAX_ROWS * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&d->rej, 4 * TWD_MAX_ROWS * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&d->sums, 2 * TWD_MAX_ROWS * sizeof(float));
+    if (e == hipSuccess)
+        e = hipMalloc(&d->seg_d, static_cast<size_t>(2) * TWD_MAX_ROWS * (kSegMax + 1) * sizeof(double));
+    if (e == hipSuccess) e = hipMalloc(&d->seg_rec, static_cast<size_t>(2) * TWD_MAX_ROWS * kSegMax * sizeof(SegRec));
+    if (e == hipSuccess) e = hipMalloc(&d->seg_head, static_cast<size_t>(2) * TWD_MAX_ROWS * sizeof(SegHead));
+    if (e == hipSuccess) e = hipMalloc(&d->live, TWD_MAX_ROWS * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&d->fin_ctr, kArriveWords * sizeof(uint64_t));
+    if (e == hipSuccess) e = hipMemset(d->fin_ctr, 0, kArriveWords * sizeof(uint64_t));
+    const uint64_t armed = kFirstEpoch;  // the counter starts armed for the first call
+    if (e == hipSuccess) e = hipMemcpy(d->fin_ctr, &armed, sizeof(armed), hipMemcpyHostToDevice);
+    if (e == hipSuccess && !d->side) {  // kept across growth: freed with the selector
+        e = hipStreamCreateWithFlags(&d->side, hipStreamNonBlocking);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&d->fork, hipEventDisableTiming);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&d->join, hipEventDisableTiming);
+        if (e != hipSuccess) draft_side_free(d);
     }
+    if (e != hipSuccess) {
+        draft_scratch_free(d);
+        return hip_fail(e, "allocating the draft verify's scratch");
+    }
+    d->fin_epoch = kFirstEpoch - 1;
+    d->e_capacity = need_e;
+    d->part_capacity = need_part;
     return TWD_OK;
 }
 
@@ -1538,10 +1524,10 @@ int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab
     seg_xfer_kernel<<<dim3(xfer_blocks(vocab), a.npos), kXferThreads, 0, s>>>(src_r, vocab, seg_d, seg_rec, 0.0f, 0u,
                                                                              seg_head);
     TWD_HIP(hipStreamWaitEvent(s, ds.join, 0));  // the selector's tokens, read by the finish
-    ds.fin_epoch = ds.fin_epoch % 0x7FFFFFFFu + 1u;
+    ds.fin_epoch = epoch_after(ds.fin_epoch);
     const DraftFinish fin{sel->scratch.verify_tokens, used, drafts, n_drafts, has, result,
                           reinterpret_cast<unsigned long long*>(ds.fin_ctr), ds.fin_epoch,
-                          ds.fin_epoch % 0x7FFFFFFFu + 1u};
+                          epoch_after(ds.fin_epoch)};
     seg_residual_kernel<<<a.npos, kRejThreads, 0, s>>>(a, ds.live, seg_rec, seg_head, fin);
     TWD_HIP(hipGetLastError());
     return TWD_OK;

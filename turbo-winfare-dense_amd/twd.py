@@ -146,6 +146,7 @@ _SIGS = {
     "twd_verify_draft_sums": (C.c_int, [_vp, C.POINTER(_f32), C.POINTER(_u32), _u32, C.POINTER(_u32)]),
     "twd_selector_verify_state": (_vp, [_vp]),
     "twd_probe_expf": (C.c_int, [_vp, _vp, _u64, _vp]),
+    "twd_probe_exp": (C.c_int, [_vp, _vp, _u64, _vp]),
     "twd_splitmix64": (_u64, [_u64]),
     "twd_seed_for": (_u64, [C.c_int, _u64, C.c_int]),
     "twd_uniform_from_seed": (_f32, [_u64]),
@@ -329,6 +330,15 @@ def probe_expf(x, out=None, stream=None):
     if out is None:
         out = torch.empty_like(x)
     _check(lib.twd_probe_expf(_ptr(x), _ptr(out), x.numel(), _stream(stream)))
+    return out
+
+
+def probe_exp(x, out=None, stream=None):
+    """The sampled shortlist's device exp(double) over a float64 device tensor (twd_probe_exp)."""
+    import torch
+    if out is None:
+        out = torch.empty_like(x)
+    _check(lib.twd_probe_exp(_ptr(x), _ptr(out), x.numel(), _stream(stream)))
     return out
 
 
