@@ -90,6 +90,13 @@ def launch_percentiles(torch, n, step_fn):
     return {f"launch_us_p{q}": float(np.percentile(us, q)) for q in (10, 50, 90)}
 
 
+def under_profiler() -> bool:
+    """True when a profiler's library is preloaded into this process (rocprofv3 sets these):
+    its child processes would initialise the GPU too, so no amd-smi child is started then."""
+    env = " ".join(os.environ.get(k, "") for k in ("LD_PRELOAD", "ROCP_TOOL_LIBRARIES", "HSA_TOOLS_LIB"))
+    return "rocprof" in env
+
+
 def power_during(torch, seconds, step_fn):
     """Runs step_fn back to back for `seconds` (after the timed regions, outside every one of
     them) while `amd-smi metric -p -c`, started as a child process, samples the socket power
@@ -99,7 +106,7 @@ def power_during(torch, seconds, step_fn):
     import subprocess
     import threading
     exe = shutil.which("amd-smi")
-    if not exe:
+    if not exe or under_profiler():
         return None
     samples, stop = [], threading.Event()
 
@@ -272,8 +279,8 @@ def main():
     ap.add_argument("--configs", default="1,2,3,4,5")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-power", action="store_true",
-                    help="skip the amd-smi power sampling (needed under a profiler whose preloaded "
-                         "library initialises the GPU in child processes as well)")
+                    help="skip the amd-smi power sampling (skipped anyway when a profiler's library "
+                         "is preloaded: it would initialise the GPU in the child processes too)")
     ap.add_argument("--cpu-rows", type=int, default=3,
                     help="full rows of config 2 in the CPU baseline (each about 1.7 s; the other "
                          "configs add about 15 s)")
@@ -412,7 +419,19 @@ def main():
     if 4 in cfgs:
         log("config 4: M=5 verify")
         hp4 = hidden_pool(torch, dev, 64, 5, 4)
-        drafts = torch.from_numpy(np.random.default_rng(4).integers(0, V, (64, 4)).astype(np.int32)).to(dev)
+        # the drafts as BASELINE config 4 draws them: position by position, the target row's
+        # argmax with probability 0.6, otherwise a random id (the argmax from a greedy pass over
+        # the same rows, outside the timed region)
+        tgt = torch.empty(64, 5, dtype=torch.int32, device=dev)
+        for c in range(64):
+            head.greedy(hp4[c], tokens=tgt[c], stream=stream)
+        tgt_np = tgt.cpu().numpy()
+        drng = np.random.default_rng(4)
+        dr = np.empty((64, 4), np.int32)
+        for c in range(64):
+            for i in range(4):
+                dr[c, i] = tgt_np[c, i] if drng.random() < 0.6 else drng.integers(0, V)
+        drafts = torch.from_numpy(dr).to(dev)
         res4 = torch.zeros(twd.twd.VERIFY_WORDS, dtype=torch.int32, device=dev)
         work[4] = (hp4[0].cpu().numpy().view(np.uint16), drafts[0].cpu().numpy().view(np.uint32))
 
@@ -424,6 +443,14 @@ def main():
         k4 = r_s / n4
         results[4] = {"rows_per_s": 5 * n4 / r_s, "ms_per_step": k4 * 1e3,
                       "kernel_us_mean": k4 * 1e6, "hbm_frac": algorithmic_bytes(5) / k4 / PEAK_HBM}
+        # the accepted counts of the 64 verify cases the steps cycle through (device results)
+        acc = []
+        for c in range(64):
+            step4(c)
+            acc.append(int(twd.decode_verify(res4)["num_accepted"]))
+        results[4]["mean_accepted"] = float(np.mean(acc))
+        results[4]["accepted_histogram"] = [acc.count(a) for a in range(5)]
+        results[4]["drafts"] = "target argmax with p=0.6 per position, else a random id (64 cases)"
 
         # the same 5 rows verified with draft logits (rejection sampling, speculator.cpp:71-122):
         # the head's logits plus 4 synthetic draft rows, T=0.8, k=40, p=0.9
