@@ -258,6 +258,20 @@ def cpu_baseline(host, work: dict, rows2: int):
             "configs": per}
 
 
+def cpp_verify_timing():
+    """Runs tests/cpp/verify_timing (built by __graft_entry__.build) as a child process on the
+    config-4 shape; its JSON line, or None when the program is not built."""
+    import subprocess
+    exe = os.path.join(ROOT, "tests", "cpp", "verify_timing")
+    if not os.path.exists(exe):
+        return None
+    try:
+        out = subprocess.run([exe, "400"], capture_output=True, text=True, timeout=120, check=True).stdout
+        return json.loads(out.strip().splitlines()[-1])
+    except (subprocess.SubprocessError, ValueError, IndexError, OSError):
+        return None
+
+
 def measured_traffic():
     """HBM bytes per launch of the config-2 kernel from the committed PMC summary
     (FETCH_SIZE and WRITE_SIZE passes, calibrated on a 1 GiB copy), or None."""
@@ -463,13 +477,18 @@ def main():
         sel4 = twd.Selector(V, 5)
         p4 = twd.RowParams(0.8, 0.9, 40, 1.0, 0.0, CAP, 0, 0)
 
+        dviews = [drafts[c] for c in range(64)]
+
         def step4d(i):
-            sel4.verify_draft(lg4, drows, p4, 1000 + i, drafts[i % 64], result=res4,
+            sel4.verify_draft(lg4, drows, p4, 1000 + i, dviews[i % 64], result=res4,
                               stream=stream)
 
         nd = max(20, args.steps // 20)
         r_d = time_loop(torch, nd, 5, step4d)
         results[4]["draft_logits_verify_us"] = r_d / nd * 1e6
+        # the same verify issued from C++ (tests/cpp/verify_timing, its own process): GPU time
+        # back to back and alone, and the host time to issue one call, without the Python wrapper
+        results[4]["draft_logits_verify_cpp"] = cpp_verify_timing()
 
     # ---- config 5: M=64 rows, each with own T/k/p, rp 1.1 over its own 2048-id history ---------
     if 5 in cfgs:

@@ -294,3 +294,23 @@ def test_device_expf_matches_host(env, oracle):
         both_nan = np.isnan(got) & np.isnan(want)
         bad = (got.view(np.uint32) != want.view(np.uint32)) & ~both_nan
         assert not bad.any(), (int(bad.sum()), x[bad][:5], got[bad][:5], want[bad][:5])
+
+
+@pytest.mark.parametrize("k", [40, 600])
+def test_verify_draft_bonus_and_fallback_tokens(env, oracle, k):
+    # the target rows' sampled tokens (rows without draft logits, the bonus row, the fallback)
+    # come from the selection run inside the draft chain's launches (k = 40) or from the
+    # selector's own launches on the side stream (k = 600, a shortlist longer than 256); both
+    # against the oracle, with every draft accepted so that the bonus row is drawn
+    rng = np.random.default_rng(1000 + k)
+    for case in range(6):
+        K = 4
+        rows = [(rng.standard_normal(V) * rng.uniform(1.0, 4.0)).astype(np.float32) for _ in range(K + 1)]
+        drs = [rows[i].copy() if i != 2 or case % 2 else None for i in range(K)]  # p == q: r = 1
+        want_tok = [oracle.sample_token(rows[i], 0.9, 0.95, k, seed=oracle.splitmix64(77 + i)) for i in range(K + 1)]
+        drafts = [want_tok[i] for i in range(K)]
+        got = run_device(env, rows, drs, drafts, 0.9, 0.95, k, 1.0, 77)
+        want = oracle.verify_draft(drafts, rows, drs, 0.9, 0.95, k, 1.0, 77)
+        want.pop("diag")
+        assert same(got, want), (case, got, want)
+        assert got["num_accepted"] == K and got["bonus_token"] == want_tok[K], (case, got)

@@ -22,12 +22,10 @@
 #include <cstring>
 #include <mutex>
 
-#include "exp_libm.h"
-#include "twd_internal.h"
+#include "select_core.h"
 
 namespace twd {
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kSliceThreads = 512;     // two slice blocks share a CU
 constexpr int kSelPerThread = 16;
@@ -35,11 +33,6 @@ constexpr uint32_t kSlice = kSliceThreads * kSelPerThread;  // vocabulary entrie
 constexpr uint32_t kMaxParts = 64;    // vocab <= 64 * 8192 = 524288
 constexpr int kMergeThreads = 256;
 constexpr int kMergePerThread = kMaxParts * kMaxWant / kMergeThreads;  // 64
-constexpr int kMaxWaves = 16;
-constexpr uint32_t kBins = 256;         // distance-from-max bins of block_top
-constexpr uint32_t kReps = 8;           // histogram replicas: lane l counts into replica l % 8
-constexpr uint32_t kGatherMax = 512;    // boundary-bin entries ranked directly
-constexpr float kBinRange = 64.0f;      // widest span of values the bins resolve
 
 struct SelectArgs {
     uint32_t rows;
@@ -66,30 +59,6 @@ struct SelectBufs {
     uint64_t* gctr;   // its arrival counter, kArriveWords words (grid_arrive)
 };
 
-// Shared memory: what every block needs (reductions, the row's shortlist and its sums)...
-struct SelCommon {
-    uint32_t misc[8];
-    uint64_t red64[kMaxWaves];
-    double redd[kMaxWaves];
-    float redf[kMaxWaves];
-    float redf2[kMaxWaves];
-    uint32_t redu[kMaxWaves];
-    uint64_t top[kMaxWant];     // selected ranks
-    uint64_t sorted[kMaxWant];  // the same, in descending order
-    double e[kMaxWant];         // exp(l - max) / total
-    double q[kMaxWant];         // exp((l - max) / T), then the running sum
-    double exp2_tbl[64];        // 2^(j/64), for the row sum's exponentials
-    float gmax;
-    double total;
-    uint32_t flag;
-};
-
-// ... block_top's work space ...
-struct TopScratch {
-    uint32_t hist[kReps * kBins];  // radix digit histogram / replicated bin histogram [bin][rep]
-    uint64_t gath[kGatherMax];     // the boundary bin's ranks
-};
-
 // ... and per kernel: the slice kernel's penalty counts, then a copy of its values for the
 // radix fallback, one entry per thread and slot so neither needs a barrier to hand over (two
 // slice blocks fit on a CU); the merge kernel keeps every slice's ranks.
@@ -108,368 +77,6 @@ struct MergeShared {
     TopScratch t;
     SelCommon c;
 };
-
-template <int NT>
-__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, SelCommon& c) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    v = wave_max_u64(v);
-    if (lane == 0) c.red64[wave] = v;
-    __syncthreads();
-    uint64_t r = c.red64[0];
-    for (int w = 1; w < NT / 64; ++w) r = c.red64[w] > r ? c.red64[w] : r;
-    __syncthreads();
-    return r;
-}
-
-template <int NT>
-__device__ __forceinline__ double block_sum_f64(double v, SelCommon& c) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    v = wave_reduce(v, 0.0, [](double a, double b) { return a + b; });
-    if (lane == 0) c.redd[wave] = v;
-    __syncthreads();
-    double r = 0.0;
-    for (int w = 0; w < NT / 64; ++w) r += c.redd[w];
-    __syncthreads();
-    return r;
-}
-
-// One exchange for three block reductions: OR of the NaN flags, max and min (NaN-ignoring).
-template <int NT>
-__device__ __forceinline__ void block_stats(uint32_t& flag, float& mx, float& mn, SelCommon& c) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    flag = wave_reduce(flag, 0u, [](uint32_t a, uint32_t b) { return a | b; });
-    mx = wave_reduce(mx, -INFINITY, [](float a, float b) { return fmaxf(a, b); });
-    mn = wave_reduce(mn, INFINITY, [](float a, float b) { return fminf(a, b); });
-    if (lane == 0) {
-        c.redu[wave] = flag;
-        c.redf[wave] = mx;
-        c.redf2[wave] = mn;
-    }
-    __syncthreads();
-    flag = 0;
-    mx = -INFINITY;
-    mn = INFINITY;
-    for (int w = 0; w < NT / 64; ++w) {
-        flag |= c.redu[w];
-        mx = fmaxf(mx, c.redf[w]);
-        mn = fminf(mn, c.redf2[w]);
-    }
-    __syncthreads();
-}
-
-// The smallest rank T with exactly `want` of the block's ranks >= T (ranks are distinct; rank
-// 0 marks an empty slot and is never selected while want <= number of real ranks). Radix
-// descent over 8-bit digits from the top, stopping once a digit bin is taken whole.
-// PER = 0: `per` entries per thread with a loop that is not unrolled (entries read from memory).
-template <int NT, int PER, typename KeyAt>
-__device__ __forceinline__ uint64_t block_select(KeyAt key_at, int per, uint32_t want, uint32_t* hist,
-                                                 SelCommon& c) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    uint64_t prefix = 0, mask = 0;
-    uint32_t need = want;
-    for (int shift = 56; shift >= 0; shift -= 8) {
-        for (int i = tid; i < 256; i += NT) hist[i] = 0;
-        __syncthreads();
-        auto count = [&](int e) {
-            const uint64_t k = key_at(e);
-            if (k != 0 && (k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
-        };
-        if constexpr (PER > 0) {
-#pragma unroll
-            for (int e = 0; e < PER; ++e) {
-                if (e >= per) break;
-                count(e);
-            }
-        } else {
-            for (int e = 0; e < per; ++e) count(e);
-        }
-        __syncthreads();
-        if (wave == 0) {
-            uint32_t cc[4];
-            uint32_t t = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                cc[j] = hist[4 * lane + j];
-                t += cc[j];
-            }
-            uint32_t x = t;  // inclusive suffix sum over lanes >= lane
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const uint32_t y = __shfl_down(x, off);
-                if (lane + off < 64) x += y;
-            }
-            uint32_t above = x - t;
-#pragma unroll
-            for (int j = 3; j >= 0; --j) {
-                if (above < need && need <= above + cc[j]) {
-                    c.misc[0] = 4 * lane + j;
-                    c.misc[1] = above;
-                    c.misc[2] = cc[j];
-                }
-                above += cc[j];
-            }
-        }
-        __syncthreads();
-        const uint32_t d = c.misc[0], above = c.misc[1], cnt = c.misc[2];
-        need -= above;
-        prefix |= static_cast<uint64_t>(d) << shift;
-        mask |= 255ull << shift;
-        if (cnt == need) break;
-    }
-    return prefix;
-}
-
-// Appends k (where pred holds) to dst through the shared counter, one atomic per wave: the
-// wave's slots are reserved by its first active lane and handed out in lane order. Slots at
-// or beyond cap are dropped (a guard: callers reserve exactly what they need).
-__device__ __forceinline__ void wave_put(bool pred, uint64_t k, uint32_t* counter, uint64_t* dst,
-                                         uint32_t cap) {
-    const uint64_t mask = __ballot(pred);
-    if (mask == 0) return;
-    const int lane = threadIdx.x & 63;
-    const int leader = __ffsll(static_cast<long long>(mask)) - 1;
-    uint32_t base = 0;
-    if (lane == leader) base = atomicAdd(counter, static_cast<uint32_t>(__popcll(mask)));
-    base = __builtin_amdgcn_readlane(base, leader);
-    if (pred) {
-        const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
-                                                          __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
-        if (base + below < cap) dst[base + below] = k;
-    }
-}
-
-// The block's top-`want` ranks (value desc, index asc), appended to out[0..want) in no
-// particular order; every thread returns once out is complete, with c.misc[4] holding how
-// many were found (want, unless fewer entries carry a rank). Entry e < per (per <= PER, the
-// same in every thread) of the calling thread has value val_at(e) and rank key_at(e) (0 = no
-// entry); slow_key(e) gives the same rank for the radix fallback, from memory the compiler
-// cannot keep in registers across its passes. mx / mn are the largest and smallest finite
-// values among the entries. ts.hist must be zero on entry (cleared behind an earlier barrier).
-//
-// bin(v) = floor((mx - v) * 255 / min(mx - mn, kBinRange)), capped at 254, is monotone in v,
-// so every entry of a bin nearer than the boundary bin bt outranks every entry of bt, which
-// outranks every farther one. The boundary bin's entries are ranked against each other.
-template <int NT, int PER, typename ValAt, typename KeyAt, typename SlowVal, typename SlowKey>
-__device__ __forceinline__ void block_top(ValAt val_at, KeyAt key_at, SlowVal slow_val, SlowKey slow_key,
-                                          int per, float mx, float mn, uint32_t want, uint64_t* out,
-                                          TopScratch& ts, SelCommon& c) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const float span = mx - mn;
-    // 0: take every entry; 1: rank the gathered boundary bin; 2: radix inside the boundary bin;
-    // 3: radix over the whole block
-    int mode = 3;
-    uint32_t bt = kBins, above = 0, nbt = 0;
-    float scale = 0.0f;
-    auto bin_of_value = [&](float x) -> uint32_t {
-        const float dist = (mx - x) * scale;
-        return dist < static_cast<float>(kBins - 2) ? static_cast<uint32_t>(dist) : kBins - 2;
-    };
-    // each entry's bin, computed once: 8 bits per entry, 0xFF for entries without a rank
-    uint32_t bins[(PER + 3) / 4];
-#pragma unroll
-    for (int j = 0; j < (PER + 3) / 4; ++j) bins[j] = 0;
-    auto bin_at = [&](int e) -> uint32_t { return (bins[e / 4] >> (8 * (e % 4))) & 0xFFu; };
-    if (__builtin_isfinite(mx) && __builtin_isfinite(mn) && span > 0.0f) {
-        scale = static_cast<float>(kBins - 1) / (span < kBinRange ? span : kBinRange);
-        const uint32_t rep = lane & (kReps - 1);
-#pragma unroll
-        for (int e = 0; e < PER; ++e) {
-            if (e >= per) break;
-            if (key_at(e) != 0) {
-                const uint32_t b = bin_of_value(val_at(e));
-                atomicAdd(&ts.hist[b * kReps + rep], 1u);
-                bins[e / 4] |= b << (8 * (e % 4));
-            } else {
-                bins[e / 4] |= 0xFFu << (8 * (e % 4));  // no rank: never gathered or taken
-            }
-        }
-        __syncthreads();
-        if (wave == 0) {  // lane l owns bins 4l .. 4l+3: their replicas are 32 consecutive words
-            uint32_t cc[4], t = 0;
-            const u32x4* h4 = reinterpret_cast<const u32x4*>(ts.hist) + lane * (4 * kReps / 4);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const u32x4 a = h4[2 * j], b2 = h4[2 * j + 1];
-                cc[j] = a.x + a.y + a.z + a.w + b2.x + b2.y + b2.z + b2.w;
-                t += cc[j];
-            }
-            uint32_t x = t;  // inclusive prefix sum over lanes <= lane
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const uint32_t y = __shfl_up(x, off);
-                if (lane >= off) x += y;
-            }
-            uint32_t before = x - t;
-            if (lane == 63) {
-                c.misc[0] = kBins;  // no boundary: fewer ranked entries than want
-                c.misc[3] = 0;
-            }
-            __builtin_amdgcn_wave_barrier();
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                if (before < want && want <= before + cc[j]) {
-                    c.misc[0] = 4 * lane + j;
-                    c.misc[1] = before;
-                    c.misc[2] = cc[j];
-                }
-                before += cc[j];
-            }
-        }
-        __syncthreads();
-        bt = c.misc[0];
-        above = c.misc[1];
-        nbt = c.misc[2];
-        mode = (bt == kBins) ? 0 : (nbt <= kGatherMax ? 1 : 2);
-    }
-
-    uint64_t thr = 0;
-    if (mode == 1) {
-#pragma unroll
-        for (int e = 0; e < PER; ++e) {
-            if (e >= per) break;
-            const bool in_bt = bin_at(e) == bt;
-            wave_put(in_bt, in_bt ? key_at(e) : 0ull, &c.misc[3], ts.gath, kGatherMax);
-        }
-    } else if (mode == 2) {
-        auto key_in_bin = [&](int e) -> uint64_t {
-            return bin_of_value(slow_val(e)) == bt ? slow_key(e) : 0ull;
-        };
-        thr = block_select<NT, PER>(key_in_bin, per, want - above, ts.hist, c);
-    } else if (mode == 3) {
-        thr = block_select<NT, PER>(slow_key, per, want, ts.hist, c);
-    }
-    if (tid == 0) c.misc[4] = 0;
-    __syncthreads();
-    // every entry that is taken whole, then (mode 1) the boundary bin's top `want - above`;
-    // exactly `want` ranks are written
-    if (mode == 0 || mode == 1) {
-#pragma unroll
-        for (int e = 0; e < PER; ++e) {
-            if (e >= per) break;
-            const bool take = bin_at(e) < (mode == 0 ? kBins - 1 : bt);  // 0xFF: no rank
-            wave_put(take, take ? key_at(e) : 0ull, &c.misc[4], out, want);
-        }
-    } else {
-        for (int e = 0; e < per; ++e) {
-            const uint64_t k = slow_key(e);
-            bool take = k != 0;
-            if (take && mode == 3) take = k >= thr;
-            if (take && mode == 2) {
-                const uint32_t b = bin_of_value(slow_val(e));
-                take = b < bt || (b == bt && k >= thr);
-            }
-            wave_put(take, k, &c.misc[4], out, want);
-        }
-    }
-    if (mode == 1) {
-        const uint32_t need = want - above;
-        for (uint32_t i0 = 0; i0 < nbt; i0 += NT) {  // the same trip count in every thread
-            const uint32_t i = i0 + tid;
-            uint64_t k = 0;
-            uint32_t higher = need;
-            if (i < nbt) {
-                k = ts.gath[i];
-                higher = 0;
-                for (uint32_t j = 0; j < nbt; ++j) higher += ts.gath[j] > k ? 1u : 0u;
-            }
-            wave_put(higher < need, k, &c.misc[4], out, want);
-        }
-    }
-    __syncthreads();
-}
-
-// c.sorted[0..n) = c.top[0..n) in descending order (ranks are distinct): each entry's
-// position is the number of entries above it.
-__device__ __forceinline__ void block_sort_desc(SelCommon& c, uint32_t n) {
-    const int tid = threadIdx.x;
-    if (static_cast<uint32_t>(tid) < n) {
-        const uint64_t k = c.top[tid];
-        uint32_t higher = 0;
-        for (uint32_t j = 0; j < n; ++j) higher += c.top[j] > k ? 1u : 0u;
-        c.sorted[higher] = k;
-    }
-    __syncthreads();
-}
-
-// Steps 5-7 of sample_token on the sorted shortlist c.sorted[0..want) (sampling.cpp:139-168).
-// Every thread i < want computes its two terms as the reference does: e_i = exp(l_i - max) /
-// total (top-p, at T = 1) and q_i = exp((l_i - max) / T). The two sequential double sums then run
-// in reference order on two lanes of wave 0, one v_add per term for both: lane 0 forms the
-// running sums acc_i of q (stored back), lane 1 the top-p running sum, kChunk terms at a time,
-// until lane 1's sum reaches p (the cut). denom is acc at the cut (the additions of the
-// reference's denom loop), and the draw -- the first i < cut with acc_i >= u * denom, else
-// cut - 1 -- is a ballot over the stored sums in wave 0. Needs want <= blockDim.x. gmax and total
-// are the row's maximum and sum of exponentials, the same in every thread. The id is returned to
-// the threads of wave 0 (callers store it from thread 0).
-__device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, const twd_row_params& p,
-                                                   float gmax, double total) {
-    const int tid = threadIdx.x, lane = tid & 63;
-    const double mx = static_cast<double>(gmax);
-    const double td = static_cast<double>(p.temperature);
-    if (static_cast<uint32_t>(tid) < want) {
-        const double l = static_cast<double>(rank_value(c.sorted[tid]));
-        c.e[tid] = exp_libm(l - mx) / total;
-        c.q[tid] = exp_libm((l - mx) / td);
-    }
-    __syncthreads();
-    if (tid >= 64) return 0;
-    constexpr uint32_t kChunk = 16;
-    const bool topp = p.top_p < 1.0f;
-    const double pp = static_cast<double>(p.top_p);
-    uint32_t cut = want;
-    if (lane < 2) {
-        // lane 0 reads q and stores its running sums over q; lane 1 reads e and stores its own
-        // (unused) over e, so that no store needs a branch
-        double* src = lane == 0 ? c.q : c.e;
-        double run = 0.0;
-        double x[kChunk];
-#pragma unroll
-        for (uint32_t j = 0; j < kChunk; ++j) x[j] = src[min(j, want - 1)];
-        for (uint32_t i0 = 0; i0 < want; i0 += kChunk) {
-            // the next chunk's terms are read before this chunk's sums are stored: they lie at
-            // i0 + kChunk or later (want - 1 >= i0 + kChunk when there is a next chunk)
-            double xn[kChunk], pre[kChunk];
-            if (i0 + kChunk < want) {
-#pragma unroll
-                for (uint32_t j = 0; j < kChunk; ++j) xn[j] = src[min(i0 + kChunk + j, want - 1)];
-            }
-#pragma unroll
-            for (uint32_t j = 0; j < kChunk; ++j) {
-                run += x[j];
-                pre[j] = run;
-            }
-            uint32_t hit = 0;
-#pragma unroll
-            for (uint32_t j = 0; j < kChunk; ++j) {
-                src[i0 + j] = pre[j];  // i0 + j < want rounded up to kChunk <= kMaxWant
-                hit |= (pre[j] >= pp ? 1u : 0u) << j;
-            }
-            // lane 1's sums decide; entries past want repeat the last term and never count
-            uint32_t h1 = __builtin_amdgcn_readlane(hit, 1);
-            h1 &= want - i0 >= kChunk ? 0xFFFFu : ((1u << (want - i0)) - 1u);
-            if (topp && h1 != 0) {  // lane 0's sums cover the cut
-                cut = i0 + static_cast<uint32_t>(__builtin_ctz(h1)) + 1;
-                break;
-            }
-#pragma unroll
-            for (uint32_t j = 0; j < kChunk; ++j) x[j] = xn[j];
-        }
-    }
-    cut = __builtin_amdgcn_readfirstlane(cut);
-    if (p.top_k > 0 && cut > static_cast<uint32_t>(p.top_k)) cut = static_cast<uint32_t>(p.top_k);
-    if (cut < 1) cut = 1;
-    const double r = static_cast<double>(p.uniform) * c.q[cut - 1];  // r = u * denom
-    uint32_t pick = cut - 1;  // the reference's fallback: the last survivor
-    for (uint32_t i0 = 0; i0 < cut; i0 += 64) {
-        const uint32_t i = i0 + static_cast<uint32_t>(lane);
-        const uint64_t m = __ballot(i < cut && c.q[min(i, cut - 1)] >= r);
-        if (m != 0) {
-            pick = i0 + static_cast<uint32_t>(__ffsll(static_cast<long long>(m)) - 1);
-            break;
-        }
-    }
-    return rank_index(c.sorted[pick]);
-}
 
 // After c.top[0..want) holds the row's shortlist and c.gmax/total/flag its statistics:
 // the degenerate check of sampling.cpp:116-118, the shortlist sort, and steps 5-7.
@@ -789,154 +396,10 @@ __global__ __launch_bounds__(kMergeThreads) void select_merge_kernel(SelectArgs 
     finish_row(sh.c, want_row, p, b.tokens + row);
 }
 
-// ---- after the head's sample mode: one block per row ---------------------------------------------
-//
-// The head's waves have applied the penalty (the logits hold the penalised rows) and published
-// per wave {best rank, sum exp(v - best value) in double, NaN when a NaN was seen}, one record
-// per 64 vocabulary rows. This kernel finishes sample_token (sampling.cpp:92-169) per row:
-//   * greedy rows take the best rank over the waves;
-//   * the row max and the rescaled sum of exponentials come from the records (a NaN sum makes
-//     the row degenerate, as the reference's NaN total does);
-//   * the shortlist only needs the waves that can hold a top-`want` entry. The wave maxima are
-//     binned by distance from the row max (256 bins, monotone in the value) and b* is the first
-//     bin at which `want` maxima have been counted: `want` entries lie in bins <= b*, so the
-//     want-th largest entry X does too, every top-`want` entry is in a bin <= b*, and it lives in
-//     a wave whose maximum is in a bin <= b*. Only those waves' rows are read, and only entries
-//     in bins <= b* are kept;
-//   * the survivors are ranked exactly (by counting when they fit one per thread, else by
-//     block_top; by a radix select over the candidate waves' rows in memory if they overflow
-//     the LDS list), then steps 5-7 run on one wave from registers.
-constexpr int kSmThreads = 1024;
-constexpr uint32_t kSmPer = kSampleMaxWaves / kSmThreads;  // wave records per thread
-constexpr uint32_t kSmCap = 2048;     // survivors kept in LDS
-constexpr uint32_t kSmMaxCand = 2048; // candidate waves listed in LDS
-
-// A sampled row's statistics from its wave records, and b*: the row max, the sum of
-// exp(l - max) over the row, the binning of wave maxima by distance from the row max
-// (block_top's monotone bins) and the first bin b* at which `want` wave maxima have been
-// counted. Every top-`want` entry lies in a bin <= b*, in a wave whose maximum is in a bin
-// <= b*. One block of kSmThreads threads; thread tid holds records tid + kSmThreads q in key /
-// wsum (0 / 0.0 past the row's records) and receives their maxima in wm. t.hist must be zero
-// and c.exp2_tbl loaded, both published by the barriers inside. `degenerate` (the same in every
-// thread, which then return together) marks a row whose total is NaN or not > 0
-// (sampling.cpp:116-118). Every caller runs this code, so rows finished by different kernels
-// see the same max and total.
-struct RecStats {
-    float gm;
-    double total;
-    float scale;   // bins per unit of distance from gm
-    bool binned;   // false: every value in bin 0
-    uint32_t bstar;
-    bool degenerate;
-};
-
-__device__ __forceinline__ uint32_t rec_bin(const RecStats& r, float x) {
-    if (!r.binned) return 0u;
-    const float dist = (r.gm - x) * r.scale;
-    return dist < static_cast<float>(kBins - 2) ? static_cast<uint32_t>(dist) : kBins - 2;
-}
-
-__device__ __forceinline__ RecStats records_stats(const uint64_t (&key)[kSmPer], const double (&wsum)[kSmPer],
-                                                  float (&wm)[kSmPer], uint32_t want, TopScratch& t,
-                                                  SelCommon& c) {
-    constexpr int NT = kSmThreads;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    RecStats rs{};
-    uint32_t flag = 0;
-    float gm = -INFINITY, mn = INFINITY;
-#pragma unroll
-    for (uint32_t q = 0; q < kSmPer; ++q) {
-        wm[q] = key[q] != 0 ? rank_value(key[q]) : -INFINITY;
-        if (wsum[q] != wsum[q]) flag = 1;
-        gm = fmaxf(gm, wm[q]);
-        if (key[q] != 0 && __builtin_isfinite(wm[q])) mn = fminf(mn, wm[q]);
-    }
-    block_stats<NT>(flag, gm, mn, c);  // NaN seen, row max, smallest finite wave max
-    rs.gm = gm;
-    if (flag != 0) {  // a NaN term makes the total NaN
-        rs.degenerate = true;
-        return rs;
-    }
-    double part = 0.0;
-#pragma unroll
-    for (uint32_t q = 0; q < kSmPer; ++q)
-        if (key[q] != 0 && wsum[q] != 0.0) {
-            // exp_core is exp_for_sum's value on [-700, 0] without its special cases
-            const double x = static_cast<double>(wm[q]) - static_cast<double>(gm);
-            part += wsum[q] * (x >= -700.0 ? exp_core(x, c.exp2_tbl) : exp_for_sum(x, c.exp2_tbl));
-        }
-    // the waves' partial sums cross the histogram's barrier below (block_sum_f64's order)
-    part = wave_reduce(part, 0.0, [](double u, double v) { return u + v; });
-    if (lane == 0) c.redd[wave] = part;
-
-    // ---- b*: bins of distance from the row max (block_top's binning), 8 replicas
-    const float span = gm - mn;
-    rs.binned = __builtin_isfinite(gm) && __builtin_isfinite(mn) && span > 0.0f;
-    rs.scale = rs.binned ? static_cast<float>(kBins - 1) / (span < kBinRange ? span : kBinRange) : 0.0f;
-#pragma unroll
-    for (uint32_t q = 0; q < kSmPer; ++q)
-        if (key[q] != 0) atomicAdd(&t.hist[rec_bin(rs, wm[q]) * kReps + (lane & (kReps - 1))], 1u);
-    __syncthreads();
-    double total = 0.0;
-#pragma unroll
-    for (int w = 0; w < NT / 64; ++w) total += c.redd[w];
-    rs.total = total;
-    if (!(total > 0.0)) {  // every thread sums the same values
-        rs.degenerate = true;
-        return rs;
-    }
-    if (wave == 0) {  // lane l owns bins 4l .. 4l + 3
-        uint32_t cc[4], tsum = 0;
-        const u32x4* h4 = reinterpret_cast<const u32x4*>(t.hist) + lane * (4 * kReps / 4);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const u32x4 x = h4[2 * j], y = h4[2 * j + 1];
-            cc[j] = x.x + x.y + x.z + x.w + y.x + y.y + y.z + y.w;
-            tsum += cc[j];
-        }
-        uint32_t incl = tsum;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const uint32_t y = __shfl_up(incl, off);
-            if (lane >= off) incl += y;
-        }
-        uint32_t before = incl - tsum;
-        if (lane == 63) c.misc[0] = kBins - 1;  // fewer maxima than want: every bin
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (before < want && want <= before + cc[j]) c.misc[0] = 4 * lane + j;
-            before += cc[j];
-        }
-        if (lane == 0) {
-            c.misc[3] = 0;  // candidate waves
-            c.misc[4] = 0;  // survivors
-        }
-    }
-    __syncthreads();
-    rs.bstar = c.misc[0];
-    return rs;
-}
-
-struct SampleMergeBufs {
-    const float* logits;  // [rows][stride], penalised
-    uint64_t stride;
-    uint32_t vocab;
-    uint32_t waves;       // head waves (records per row)
-    SampleStats st;
-    uint32_t* tokens;
-};
-
-struct SampleMergeShared {
-    uint32_t cwave[kSmMaxCand];  // the candidate waves
-    uint64_t cand[kSmCap];       // surviving ranks
-    TopScratch t;
-    SelCommon c;
-};
-
+// ---- after the head's sample mode (or the wave-record pass): one block per row --------------------
+// sample_merge_row (select_core.h) finishes each row from its per-64-entry records.
 __global__ __launch_bounds__(kSmThreads) void select_sample_merge_kernel(SelectArgs args_by_value,
                                                                          SampleMergeBufs b) {
-    constexpr int NT = kSmThreads;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     SampleMergeShared& sh = *reinterpret_cast<SampleMergeShared*>(smem_raw);
 #if __HIP_DEVICE_COMPILE__
@@ -945,157 +408,8 @@ __global__ __launch_bounds__(kSmThreads) void select_sample_merge_kernel(SelectA
 #else
     const SelectArgs& args = args_by_value;
 #endif
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t row = blockIdx.x;
-    const twd_row_params p = args.p[row];
-    const uint32_t W = b.waves;
-    const size_t o = static_cast<size_t>(row) * W;
-    const float* lg = b.logits + static_cast<size_t>(row) * b.stride;
-
-    // the exp2 table first, so that its load overlaps the records' (the first barrier publishes it)
-    if (tid < 64) sh.c.exp2_tbl[tid] = kExp2Table[tid];
-    // ---- the wave records, one round trip: thread tid holds waves tid + NT * q
-    uint64_t key[kSmPer];
-    double wsum[kSmPer];
-#pragma unroll
-    for (uint32_t q = 0; q < kSmPer; ++q) {
-        const uint32_t i = tid + NT * q;
-        key[q] = i < W ? b.st.key[o + i] : 0ull;
-        wsum[q] = i < W ? b.st.sum[o + i] : 0.0;
-    }
-    for (uint32_t i = tid; i < kReps * kBins; i += NT) sh.t.hist[i] = 0;
-    if (!(p.temperature > 0.0f)) {  // greedy: the best rank over the waves
-        uint64_t k = 0;
-#pragma unroll
-        for (uint32_t q = 0; q < kSmPer; ++q) k = key[q] > k ? key[q] : k;
-        k = block_max_u64<NT>(k, sh.c);
-        if (tid == 0) b.tokens[row] = rank_index(k);
-        return;
-    }
-    const uint32_t want = (p.top_k > 0) ? min(static_cast<uint32_t>(p.top_k), b.vocab)
-                                        : min(kMaxWant, b.vocab);
-    if (want > kMaxWant) return;  // a longer shortlist: the long path finishes the row
-    float wm[kSmPer];
-    const RecStats rs = records_stats(key, wsum, wm, want, sh.t, sh.c);
-    if (rs.degenerate) {  // sampling.cpp:116-118
-        if (tid == 0) b.tokens[row] = TWD_TOKEN_DEGENERATE;
-        return;
-    }
-    const float gm = rs.gm;
-    const double total = rs.total;
-    const uint32_t bstar = rs.bstar;
-    auto bin_of = [&](float x) -> uint32_t { return rec_bin(rs, x); };
-    // the candidate waves, in any order
-#pragma unroll
-    for (uint32_t q = 0; q < kSmPer; ++q) {
-        const uint32_t i = tid + NT * q;
-        const bool is_cand = key[q] != 0 && bin_of(wm[q]) <= bstar;
-        const uint64_t mask = __ballot(is_cand);
-        if (mask != 0) {
-            const int leader = __ffsll(static_cast<long long>(mask)) - 1;
-            uint32_t base = 0;
-            if (lane == leader) base = atomicAdd(&sh.c.misc[3], static_cast<uint32_t>(__popcll(mask)));
-            base = __builtin_amdgcn_readlane(base, leader);
-            if (is_cand) {
-                const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
-                                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
-                if (base + below < kSmMaxCand) sh.cwave[base + below] = i;
-            }
-        }
-    }
-    __syncthreads();
-    const uint32_t ncw = sh.c.misc[3];
-    if (ncw > kSmMaxCand) {
-        // a candidate list this long only comes from values that barely bin (huge ties): the
-        // two-launch path's kernels are not reachable from here, so rank over every wave
-        if (tid == 0) sh.c.misc[3] = 0;
-        __syncthreads();
-    }
-    const bool all_waves = ncw > kSmMaxCand;
-    const uint32_t nent = all_waves ? W * kSampleWaveRows : ncw * kSampleWaveRows;  // entries to scan
-    auto entry_row = [&](uint32_t f) -> uint32_t {  // row of entry f of the candidate waves
-        const uint32_t w = all_waves ? f / kSampleWaveRows : sh.cwave[f / kSampleWaveRows];
-        return w * kSampleWaveRows + f % kSampleWaveRows;
-    };
-
-    // ---- survivors: entries in bins <= b* of the candidate waves, kGatherBatch loads at a time
-    float smn = INFINITY;
-    constexpr uint32_t kGatherBatch = 8;
-    const uint32_t per = (nent + NT - 1) / NT;
-    for (uint32_t i0 = 0; i0 < per; i0 += kGatherBatch) {
-        float v[kGatherBatch];
-        uint32_t r[kGatherBatch];
-#pragma unroll
-        for (uint32_t q = 0; q < kGatherBatch; ++q) {
-            const uint32_t f = (i0 + q) * NT + static_cast<uint32_t>(tid);
-            r[q] = 0xFFFFFFFFu;
-            v[q] = 0.0f;
-            if (i0 + q < per && f < nent) {
-                const uint32_t rr = entry_row(f);
-                if (rr < b.vocab) {
-                    r[q] = rr;
-                    v[q] = lg[rr];
-                }
-            }
-        }
-#pragma unroll
-        for (uint32_t q = 0; q < kGatherBatch; ++q) {
-            const bool keep = r[q] != 0xFFFFFFFFu && bin_of(v[q]) <= bstar;
-            if (keep && __builtin_isfinite(v[q])) smn = fminf(smn, v[q]);
-            wave_put(keep, keep ? rank_key(v[q], r[q]) : 0ull, &sh.c.misc[4], sh.cand, kSmCap);
-        }
-    }
-    __syncthreads();                  // the survivors are listed
-    const uint32_t n = sh.c.misc[4];  // may exceed kSmCap: then only counted
-    if (n > static_cast<uint32_t>(NT)) {  // block_top needs the survivors' smallest finite value
-        uint32_t no_flag = 0;
-        float no_max = -INFINITY;
-        block_stats<NT>(no_flag, no_max, smn, sh.c);
-    }
-
-    // ---- the shortlist, sorted (value desc, index asc)
-    if (n <= static_cast<uint32_t>(NT)) {
-        if (static_cast<uint32_t>(tid) < n) {
-            const uint64_t k = sh.cand[tid];
-            uint32_t higher = 0;
-#pragma unroll 8
-            for (uint32_t j = 0; j < n; ++j) higher += sh.cand[j] > k ? 1u : 0u;
-            if (higher < want) sh.c.sorted[higher] = k;
-        }
-        __syncthreads();
-    } else if (n <= kSmCap) {
-        auto merge_key = [&](int e) -> uint64_t {
-            const uint32_t f = tid + NT * e;
-            return f < n ? sh.cand[f] : 0ull;
-        };
-        auto merge_val = [&](int e) -> float { return rank_value(merge_key(e)); };
-        for (uint32_t i = tid; i < kReps * kBins; i += NT) sh.t.hist[i] = 0;
-        __syncthreads();
-        block_top<NT, kSmCap / NT>(merge_val, merge_key, merge_val, merge_key, static_cast<int>((n + NT - 1) / NT),
-                                   gm, smn, want, sh.c.top, sh.t, sh.c);
-        block_sort_desc(sh.c, want);
-    } else {
-        // overflow (heavy ties): a radix select over the candidate waves' rows in memory
-        auto cand_key = [&](int e) -> uint64_t {
-            const uint32_t f = static_cast<uint32_t>(e) * NT + static_cast<uint32_t>(tid);
-            if (f >= nent) return 0ull;
-            const uint32_t rr = entry_row(f);
-            if (rr >= b.vocab) return 0ull;
-            const float x = lg[rr];
-            return bin_of(x) <= bstar ? rank_key(x, rr) : 0ull;
-        };
-        const uint64_t thr = block_select<NT, 0>(cand_key, static_cast<int>(per), want, sh.t.hist, sh.c);
-        if (tid == 0) sh.c.misc[4] = 0;
-        __syncthreads();
-        for (uint32_t e = 0; e < per; ++e) {
-            const uint64_t k = cand_key(static_cast<int>(e));
-            wave_put(k != 0 && k >= thr, k, &sh.c.misc[4], sh.c.top, want);
-        }
-        __syncthreads();
-        block_sort_desc(sh.c, want);
-    }
-    const uint32_t tok = finish_sampled(sh.c, want, p, gm, total);
-    if (tid == 0) b.tokens[row] = tok;
+    sample_merge_row(args.p[row], row, b, sh);
 }
 
 // ---- shortlists longer than 256: top_k > 256 -------------------------------------------------------
@@ -1518,123 +832,14 @@ __global__ __launch_bounds__(kPhThreads) void penalty_hash_kernel(SelectArgs arg
     }
 }
 
-constexpr int kWsThreads = 256;
-constexpr uint32_t kWsEntries = kWsThreads * 8;         // entries of one batch of a block
-
-struct WaveStatsBufs {
-    const float* logits;
-    uint64_t stride;
-    uint32_t vocab;
-    uint32_t waves;  // records per row, ceil(vocab / 64)
-    uint32_t vec;    // rows 16-byte aligned: 16 B loads
-    SampleStats st;
-};
-
 // NB 8-entry batches per lane. One: many short blocks, so that later blocks' loads overlap
 // earlier blocks' arithmetic (with four, every wave requested all its loads first, and the pass
 // ran as a load phase, then an arithmetic phase).
 template <uint32_t NB>
 __global__ __launch_bounds__(kWsThreads) __attribute__((amdgpu_waves_per_eu(8)))
 void wave_stats_kernel(WaveStatsBufs b) {
-    constexpr uint32_t kWsBatches = NB;
-    constexpr uint32_t kWsBlockEntries = kWsEntries * NB;
     __shared__ double tbl[64];
-    const int tid = threadIdx.x, lane = tid & 63;
-    if (tid < 64) tbl[tid] = kExp2Table[tid];
-    const uint32_t row = blockIdx.y;
-    const float* lg = b.logits + static_cast<size_t>(row) * b.stride;
-    // batch k of this lane: entries e0 + 8 * 256 * k .. + 7; all loads requested at once
-    const uint32_t e0 = blockIdx.x * kWsBlockEntries + static_cast<uint32_t>(tid) * 8;
-    float v[kWsBatches][8];
-#pragma unroll
-    for (uint32_t k = 0; k < kWsBatches; ++k) {
-        const uint32_t e = e0 + kWsEntries * k;
-        if (b.vec && e + 8 <= b.vocab) {
-            const float4 x0 = *reinterpret_cast<const float4*>(lg + e);
-            const float4 x1 = *reinterpret_cast<const float4*>(lg + e + 4);
-            v[k][0] = x0.x; v[k][1] = x0.y; v[k][2] = x0.z; v[k][3] = x0.w;
-            v[k][4] = x1.x; v[k][5] = x1.y; v[k][6] = x1.z; v[k][7] = x1.w;
-        } else {
-#pragma unroll
-            for (int q = 0; q < 8; ++q) v[k][q] = e + q < b.vocab ? lg[e + q] : -INFINITY;
-        }
-    }
-    __syncthreads();
-#pragma unroll
-    for (uint32_t k = 0; k < kWsBatches; ++k) {
-        const uint32_t e = e0 + kWsEntries * k;
-        // common case, decided per wave: every entry of the wave finite and live, and every
-        // exp argument v - (record best) in [-700, 0]. The lane's best rank is its largest value
-        // at its lowest index (equal values, -0 and +0 included, rank by index), and exp_core
-        // needs no special cases.
-        float hi = v[k][0], lo = v[k][0];
-        bool ok = e + 8 <= b.vocab;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            ok &= __builtin_isfinite(v[k][q]);
-            hi = fmaxf(hi, v[k][q]);
-            lo = fminf(lo, v[k][q]);
-        }
-        if (__ballot(!ok) == 0) {
-            uint32_t qi = 7;
-#pragma unroll
-            for (int q = 6; q >= 0; --q) qi = v[k][q] == hi ? static_cast<uint32_t>(q) : qi;
-            uint64_t best = rank_key(hi, e + qi);
-#pragma unroll
-            for (int m = 1; m < 8; m <<= 1) {
-                const uint64_t o = shfl_xor_u64(best, m);
-                best = o > best ? o : best;
-            }
-            const float wm = rank_value(best);
-            if (__ballot(lo < wm - 700.0f) == 0) {
-                const double dwm = static_cast<double>(wm);
-                double sum = 0.0;
-#pragma unroll
-                for (int q = 0; q < 8; ++q) sum += exp_core(static_cast<double>(v[k][q]) - dwm, tbl);
-#pragma unroll
-                for (int m = 1; m < 8; m <<= 1) sum += __shfl_xor(sum, m);
-                const uint32_t w = e / kSampleWaveRows;
-                if ((lane & 7) == 0) {
-                    const size_t o = static_cast<size_t>(row) * b.waves + w;
-                    b.st.key[o] = best;
-                    b.st.sum[o] = sum;
-                }
-                continue;
-            }
-        }
-        // entries past the vocabulary hold -inf and no rank: they add nothing
-        uint64_t best = 0;
-        uint32_t nan = 0;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const uint64_t key = e + q < b.vocab ? rank_key(v[k][q], e + q) : 0ull;
-            best = key > best ? key : best;
-            nan |= v[k][q] != v[k][q] ? 1u : 0u;
-        }
-        // the record's 64 entries are the 8 lanes with the same lane >> 3
-#pragma unroll
-        for (int m = 1; m < 8; m <<= 1) {
-            const uint64_t o = shfl_xor_u64(best, m);
-            best = o > best ? o : best;
-            nan |= __shfl_xor(nan, m);
-        }
-        // a record of -inf entries only (best value -inf, or no entry) adds nothing
-        const float wm = best != 0 ? rank_value(best) : -INFINITY;
-        const double dwm = wm != -INFINITY ? static_cast<double>(wm) : 0.0;
-        double sum = 0.0;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) sum += exp_for_sum(static_cast<double>(v[k][q]) - dwm, tbl);
-        if (wm == -INFINITY) sum = 0.0;
-#pragma unroll
-        for (int m = 1; m < 8; m <<= 1) sum += __shfl_xor(sum, m);
-        if (nan) sum = __builtin_nan("");
-        const uint32_t w = e / kSampleWaveRows;
-        if ((lane & 7) == 0 && w < b.waves) {
-            const size_t o = static_cast<size_t>(row) * b.waves + w;
-            b.st.key[o] = best;
-            b.st.sum[o] = sum;
-        }
-    }
+    wave_records_block<NB>(b, blockIdx.x, blockIdx.y, tbl);
 }
 
 __global__ void verify_compare_kernel(const uint32_t* row_tokens, uint32_t rows,

@@ -17,8 +17,12 @@
 //   seg_xfer_kernel, seg_residual_kernel: each rejected position's residual sum and draw
 //   (seg_residual_kernel's last block: the accept chain over all positions, bonus, result)
 // where P is the number of positions with a draft row. The target tokens of the other
-// positions, of the fallback and of the bonus row come from the selector (launch_select), run
-// on a side stream beside these launches and joined before seg_residual_kernel.
+// positions, of the fallback and of the bonus row come from the selection code of select.hip,
+// run inside two of these launches: draft_max_kernel's extra grid rows write the target rows'
+// wave records (wave_records_block) and seg_sum_kernel's extra blocks merge them
+// (sample_merge_row), so the selection adds no launch and no stream synchronisation. Target rows
+// with shortlists longer than 256 take the selector's own launches (launch_select) on a side
+// stream instead, joined before seg_residual_kernel.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -27,6 +31,7 @@
 #include <mutex>
 
 #include "expf_libm.h"
+#include "select_core.h"
 #include "twd_internal.h"
 
 // Every float expression in this file rounds each operation on its own: hipcc would otherwise
@@ -88,12 +93,30 @@ struct DraftArgs {
 };
 
 
+// The target rows' selection inside the draft chain's launches (rows 0 .. nsel - 1 of the
+// target logits, all with the parameters `base` and their own uniforms): records by
+// draft_max_kernel's grid rows 2P .. 2P + nsel - 1, the merges by seg_sum_kernel's blocks
+// 2P .. 2P + nsel - 1. nsel = 0: the selection runs elsewhere.
+struct DraftSelect {
+    uint32_t nsel;
+    twd_row_params base;
+    float u[TWD_MAX_ROWS + 1];
+    WaveStatsBufs wb;     // the target rows' records
+    SampleMergeBufs mb;   // and their merge, tokens into the selector's verify tokens
+};
+
 __device__ __forceinline__ const float* draft_row(const DraftArgs& a, uint32_t r) {
     return (r & 1) ? a.pos[r >> 1].draft : a.pos[r >> 1].target;
 }
 
-__global__ __launch_bounds__(kDraftThreads) void draft_max_kernel(DraftArgs a) {
+__global__ __launch_bounds__(kDraftThreads) void draft_max_kernel(DraftArgs a, DraftSelect sel) {
+    static_assert(kDraftThreads == kWsThreads && kDraftChunk == kWsEntries, "a record block per draft chunk");
     const uint32_t r = blockIdx.y;
+    if (r >= 2 * a.npos) {  // the whole block: the target row's records over this chunk
+        __shared__ double tbl[64];
+        wave_records_block<1>(sel.wb, blockIdx.x, r - 2 * a.npos, tbl);
+        return;
+    }
     const float* l = draft_row(a, r);
     const uint32_t base = blockIdx.x * kDraftChunk + threadIdx.x;
     // every load issued before any is used (indices past the row clamped to its last entry and
@@ -1068,10 +1091,29 @@ __device__ float seg_row_sum(Load load, Term term, uint32_t n, const SegRec* rec
 }
 
 // The softmax sums of the e rows: one block per row.
-__global__ __launch_bounds__(kRejThreads) void seg_sum_kernel(DraftArgs a, const SegRec* rec, const SegHead* heads) {
-    __shared__ SeqShared sh;
-    __shared__ ChainShared ch;
+// LDS of seg_sum_kernel: a softmax row's chain, or a target row's merge
+union SumOrMergeShared {
+    struct {
+        SeqShared sh;
+        ChainShared ch;
+    } seg;
+    SampleMergeShared sm;
+};
+
+__global__ __launch_bounds__(kRejThreads) void seg_sum_kernel(DraftArgs a, const SegRec* rec, const SegHead* heads,
+                                                              DraftSelect sel) {
+    static_assert(kRejThreads == kSmThreads, "a merge block is a chain block");
+    __shared__ SumOrMergeShared u;
     const uint32_t r = blockIdx.x;
+    if (r >= 2 * a.npos) {  // the whole block: sample_token of target row r - 2P from its records
+        const uint32_t row = r - 2 * a.npos;
+        twd_row_params p = sel.base;
+        p.uniform = sel.u[row];
+        sample_merge_row(p, row, sel.mb, u.sm);
+        return;
+    }
+    SeqShared& sh = u.seg.sh;
+    ChainShared& ch = u.seg.ch;
     const float* e = a.e + static_cast<size_t>(r) * a.estride;
     float s = __uint_as_float(0x7FC00000u);
     if (!(a.flags[r] & 1u))
@@ -1472,9 +1514,8 @@ int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab
     if (rc) return rc;
     DraftScratch& ds = sel->draft;
 
-    // target tokens for the positions without draft rows, the fallback and the bonus row: the
-    // selection runs on the side stream, beside the draft chain below (which leaves most of
-    // the GPU idle), and joins it before seg_residual_kernel, whose last block reads them
+    // target tokens for the positions without draft rows, the fallback and the bonus row, read
+    // by seg_residual_kernel's last block: sample_token of the target rows 0 .. used - 1
     const uint32_t used = (rows > k) ? k + 1 : k;
     twd_row_params rp[TWD_MAX_ROWS + 1];
     for (uint32_t i = 0; i < used; ++i) {
@@ -1483,14 +1524,34 @@ int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab
         rp[i].history_len = 0;
         rp[i].uniform = twd_uniform_from_seed(twd_splitmix64(base_seed + i));
     }
-    TWD_HIP(hipEventRecord(ds.fork, s));
-    TWD_HIP(hipStreamWaitEvent(ds.side, ds.fork, 0));
-    rc = launch_select(sel->scratch, const_cast<float*>(logits), vocab, used, row_stride, rp, nullptr,
-                       sel->scratch.verify_tokens, ds.side);
-    TWD_HIP(hipEventRecord(ds.join, ds.side));
-    if (rc) {
-        (void)hipStreamWaitEvent(s, ds.join, 0);
-        return rc;
+    // Inside the draft chain's launches (records in draft_max_kernel's grid, merges in
+    // seg_sum_kernel's) when the selector holds the rows' records and no shortlist is longer
+    // than 256; otherwise the selector's launches run on the side stream beside the chain and
+    // join it before seg_residual_kernel.
+    const SelectScratch& ss = sel->scratch;
+    const uint32_t waves = (vocab + kSampleWaveRows - 1) / kSampleWaveRows;
+    bool fused = ss.wkey != nullptr && waves <= ss.wave_cap && waves <= kSampleMaxWaves;
+    for (uint32_t i = 0; i < used; ++i) fused = fused && !long_row(rp[i], vocab);
+    DraftSelect dsel{};
+    if (fused) {
+        const SampleStats st{ss.wkey, ss.wsum};
+        dsel.nsel = used;
+        dsel.base = rp[0];
+        for (uint32_t i = 0; i < used; ++i) dsel.u[i] = rp[i].uniform;
+        dsel.wb = WaveStatsBufs{logits, row_stride, vocab, waves,
+                                (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && (row_stride & 3) == 0 ? 1u : 0u,
+                                st};
+        dsel.mb = SampleMergeBufs{logits, row_stride, vocab, waves, st, ss.verify_tokens};
+    } else {
+        TWD_HIP(hipEventRecord(ds.fork, s));
+        TWD_HIP(hipStreamWaitEvent(ds.side, ds.fork, 0));
+        rc = launch_select(sel->scratch, const_cast<float*>(logits), vocab, used, row_stride, rp, nullptr,
+                           sel->scratch.verify_tokens, ds.side);
+        TWD_HIP(hipEventRecord(ds.join, ds.side));
+        if (rc) {
+            (void)hipStreamWaitEvent(s, ds.join, 0);
+            return rc;
+        }
     }
 
     a.vocab = vocab;
@@ -1507,7 +1568,7 @@ int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab
     sel->draft.last_npos = a.npos;
     for (uint32_t i = 0; i < a.npos; ++i) sel->draft.last_pos[i] = a.pos[i].position;
     const dim3 grid(a.parts, 2 * a.npos);
-    draft_max_kernel<<<grid, kDraftThreads, 0, s>>>(a);
+    draft_max_kernel<<<dim3(a.parts, 2 * a.npos + dsel.nsel), kDraftThreads, 0, s>>>(a, dsel);
     draft_exp_kernel<<<grid, kDraftThreads, 0, s>>>(a);
     // the softmax sums, then the ratio tests, then the residual draws of rejected positions,
     // each exact sum through the segmented pipeline
@@ -1518,12 +1579,12 @@ int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab
     SegHead* seg_head = static_cast<SegHead*>(ds.seg_head);
     seg_xfer_kernel<<<dim3(xfer_blocks(vocab), 2 * a.npos), kXferThreads, 0, s>>>(src_e, vocab, seg_d, seg_rec,
                                                                                  0.0f, 0u, seg_head);
-    seg_sum_kernel<<<2 * a.npos, kRejThreads, 0, s>>>(a, seg_rec, seg_head);
+    seg_sum_kernel<<<2 * a.npos + dsel.nsel, kRejThreads, 0, s>>>(a, seg_rec, seg_head, dsel);
     seg_ratio_dsum_kernel<<<dim3(xfer_blocks(vocab), a.npos), kXferThreads, 0, s>>>(a, ds.live, seg_d);
     const SegSrcResidual src_r{a.e, a.estride, a.sums, ds.live};
     seg_xfer_kernel<<<dim3(xfer_blocks(vocab), a.npos), kXferThreads, 0, s>>>(src_r, vocab, seg_d, seg_rec, 0.0f, 0u,
                                                                              seg_head);
-    TWD_HIP(hipStreamWaitEvent(s, ds.join, 0));  // the selector's tokens, read by the finish
+    if (!fused) TWD_HIP(hipStreamWaitEvent(s, ds.join, 0));  // the selector's tokens, read by the finish
     ds.fin_epoch = epoch_after(ds.fin_epoch);
     const DraftFinish fin{sel->scratch.verify_tokens, used, drafts, n_drafts, has, result,
                           reinterpret_cast<unsigned long long*>(ds.fin_ctr), ds.fin_epoch,

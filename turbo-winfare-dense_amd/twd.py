@@ -250,6 +250,7 @@ class Selector:
         _check(lib.twd_selector_create(max_vocab, max_rows, C.byref(h)))
         self.handle = h
         self.max_vocab = max_vocab
+        self._draft_ptrs = None  # (addresses, ctypes array) of the last verify_draft's draft rows
 
     def close(self):
         if self.handle:
@@ -304,22 +305,27 @@ class Selector:
                      result=None, stream=None):
         """evaluate_verification with draft logits (speculator.cpp:34-153): draft_rows[i] is a
         float32 device row of position i's draft logits, or None."""
-        import torch
         rows, vocab = logits.shape
         if result is None:
+            import torch
             result = torch.zeros(VERIFY_WORDS, dtype=torch.int32, device=logits.device)
         if logits.stride(1) != 1:
             raise ValueError("logit rows must be contiguous")
-        for r in draft_rows:
-            if r is not None and (r.numel() != vocab or not r.is_contiguous()):
-                raise ValueError("each draft row must be a contiguous row of vocab floats")
+        # the pointer array of the last list of draft rows is kept, so repeated calls with the
+        # same rows only compare their addresses
+        key = tuple(0 if r is None else r.data_ptr() for r in draft_rows)
+        cached = self._draft_ptrs
+        if cached is None or cached[0] != key:
+            for r in draft_rows:
+                if r is not None and (r.numel() != vocab or not r.is_contiguous()):
+                    raise ValueError("each draft row must be a contiguous row of vocab floats")
+            cached = (key, (_vp * max(1, len(key)))(*[k or None for k in key]))
+            self._draft_ptrs = cached
         stride = logits.stride(0) if rows > 1 else vocab
-        ptrs = (_vp * max(1, len(draft_rows)))(*[None if r is None else r.data_ptr()
-                                                  for r in draft_rows])
-        _check(lib.twd_verify_draft(self.handle, _ptr(logits), vocab, rows, stride, ptrs,
-                                    len(draft_rows), C.byref(params),
+        _check(lib.twd_verify_draft(self.handle, logits.data_ptr(), vocab, rows, stride, cached[1],
+                                    len(key), C.byref(params),
                                     base_seed & 0xFFFFFFFFFFFFFFFF, _ptr(drafts),
-                                    0 if drafts is None else drafts.numel(), _ptr(result),
+                                    0 if drafts is None else drafts.numel(), result.data_ptr(),
                                     _stream(stream)))
         return result
 
