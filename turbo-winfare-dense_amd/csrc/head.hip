@@ -1129,20 +1129,29 @@ __device__ __forceinline__ void head_epilogue32(const HeadArgs& a, f32x16_t (&to
             }
     }
     if (MODE == kModeLogits) return;
-    // rows sharing m are the 32 lanes with the same lane / 32
+    // The rows sharing m are the 32 lanes with the same lane / 32, and each lane holds NM * 16
+    // maxima (index j = 16 mt + v, padded to 32 with zero keys). A transposed butterfly reduces
+    // all of them at once: at the step over lane bit b, the lanes with that bit set keep the
+    // upper half of their indices and send the lower half to their partner, which keeps the
+    // lower half, so each step halves the values per lane. After five steps lane l holds the
+    // maximum of index j = l % 32 over its 32 lanes: 31 exchanges instead of 32 x 5.
+    uint64_t k[32];
 #pragma unroll
-    for (int mt = 0; mt < NM; ++mt)
+    for (int j = 0; j < 32; ++j) k[j] = j < NM * 16 ? best[j / 16 % NM][j % 16] : 0ull;
+    static_for<5>([&](auto st) {
+        constexpr int kHalf = 16 >> decltype(st)::value;  // values kept after this step
+        const bool up = (lane & kHalf) != 0;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            uint64_t k = best[mt][v];
-#pragma unroll
-            for (int msk = 1; msk < 32; msk <<= 1) {
-                const uint64_t o = shfl_xor_u64(k, msk);
-                k = o > k ? o : k;
-            }
-            const uint32_t m = 32 * mt + 8 * (v >> 2) + mb + (v & 3);
-            if ((lane & 31) == 0 && m < TWD_MAX_ROWS) se.red[wave][m] = k;
+        for (int i = 0; i < kHalf; ++i) {
+            const uint64_t send = up ? k[i] : k[i + kHalf];
+            const uint64_t keep = up ? k[i + kHalf] : k[i];
+            const uint64_t o = shfl_xor_u64(send, kHalf);
+            k[i] = o > keep ? o : keep;
         }
+    });
+    const uint32_t j = lane & 31;
+    const uint32_t m = 32 * (j / 16) + 8 * ((j % 16) >> 2) + mb + (j & 3);
+    if (j < NM * 16 && m < TWD_MAX_ROWS) se.red[wave][m] = k[0];
     grid_finish<NW>(a, se);
 }
 
@@ -1181,7 +1190,9 @@ void head_wide32_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_
     __shared__ u32x4_t sX[2][kXA];
     __shared__ u32x4_t sWn[NW][2][NP][2][64];
     __shared__ uint32_t sWs[NW][2][NP][64];
-    __shared__ EpiSharedT<NW> se;
+    // the greedy finish's shared state lives in the h staging, dead once the stream has ended:
+    // a block stays within the LDS that lets two share a CU
+    static_assert(sizeof(EpiSharedT<NW>) <= sizeof(sH), "the finish's state fits the h staging");
 
     const int lane = threadIdx.x & 63;
     const uint32_t wave = wave_id();
@@ -1362,7 +1373,7 @@ void head_wide32_kernel(HeadArgs a, const u32x4_t* __restrict__ hp, const u32x4_
     }
     __builtin_amdgcn_s_waitcnt(kWaitVm0);  // the last (unused) DMAs land before LDS is reused
     __syncthreads();
-    head_epilogue32<NP, NM, MODE, NW>(a, tot, T0, se);
+    head_epilogue32<NP, NM, MODE, NW>(a, tot, T0, *reinterpret_cast<EpiSharedT<NW>*>(&sH[0][0]));
 }
 
 // ---- layout repack: reference [W|S|B] -> units ----------------------------------------------
