@@ -1,6 +1,6 @@
-"""The fused sample pass of the LM head (rows <= 4): softcap and repetition penalty in the head's
-epilogue, per-block selection statistics, then one merge launch that reads only the blocks able
-to hold a top-`want` entry; and head.sample past 4 rows (logits pass, then the selection over the
+"""The fused sample pass of the LM head (rows <= 8): softcap and repetition penalty in the head's
+epilogue, per-wave selection statistics, then one merge launch that reads only the blocks able
+to hold a top-`want` entry; and head.sample past 8 rows (logits pass, then the selection over the
 logits in memory). Every token is compared bit-exactly with the oracle's
 apply_repetition_penalty + sample_token (sampling.cpp:74-169) on the GPU's own raw logits, and
 the penalised rows bit for bit. The cases reach every branch of the merge: survivors ranked by
@@ -71,6 +71,13 @@ PARAM_SETS = [  # (T, p, k, rp): top-256 shortlists, tiny and full k, greedy wit
     [(1.0, 1.0, 0, 1.0), (0.0, 1.0, 0, 1.3)],
     [(0.8, 0.95, 256, 1.2), (1.5, 0.5, 1, 1.0), (0.3, 0.99, 7, 0.8)],
     [(0.9, 0.97, 100, 1.1), (2.0, 1.0, 0, 1.05), (0.0, 1.0, 0, 1.0), (0.6, 0.8, 64, 1.4)],
+    # 5..8 rows: rows two apart in the MFMA's rows, two per lane in the epilogue
+    [(0.7, 0.9, 40, 1.1), (0.0, 1.0, 0, 1.2), (1.2, 0.95, 100, 0.9), (0.5, 0.8, 20, 1.0),
+     (0.9, 0.97, 256, 1.1)],
+    [(0.7, 0.9, 40, 1.1)] * 6,
+    [(0.8, 0.9, 300, 1.1), (1.0, 1.0, 0, 1.0), (0.6, 0.85, 50, 1.3), (0.0, 1.0, 0, 1.0),
+     (1.1, 0.99, 3, 1.05), (0.7, 0.5, 1000, 1.1), (0.4, 0.9, 64, 0.8)],
+    [(0.5 + 0.1 * m, 0.8 + 0.02 * m, 20 + 10 * m, 1.1) for m in range(8)],
 ]
 
 
@@ -134,9 +141,10 @@ def test_fused_ties_at_the_top(env, oracle):
 
 
 @pytest.mark.parametrize("V", [300, 1000, 5000])
-def test_fused_small_vocabularies(env, oracle, V):
+@pytest.mark.parametrize("M", [2, 6])
+def test_fused_small_vocabularies(env, oracle, V, M):
     # few head blocks: every block is a candidate (counting for 300, binned top for 1000, radix
-    # for 5000 survivors)
+    # for 5000 survivors); 2 rows (four apart) and 6 (two apart, 16-wave blocks)
     torch, dev, t = env
     d = 256
     W, S, B = oracle.gen_lm_head(730 + V, V, d)
@@ -144,18 +152,22 @@ def test_fused_small_vocabularies(env, oracle, V):
     rng = np.random.default_rng(V)
     hist = rng.integers(0, V + 10, 300).astype(np.uint32)
     params = [t.RowParams(0.7, 0.9, 40, 1.1, 0.3, CAP, 0, 300), t.RowParams(1.0, 1.0, 0, 1.0, 0.8, CAP, 0, 0)]
-    run_and_check(env, oracle, head, hidden_bf16(731, 2, d), params, hist, f"V={V}")
+    params += [t.RowParams(0.6 + 0.1 * m, 0.9, 30 + m, 1.2 if m % 2 else 1.0, 0.1 + 0.2 * m, CAP, 50 * m, 100)
+               for m in range(M - 2)]
+    run_and_check(env, oracle, head, hidden_bf16(731 + M, M, d), params, hist, f"V={V} M={M}")
     head.close()
 
 
-def test_fused_degenerate_row(env, oracle, full_head):
-    # a NaN hidden row gives NaN logits: that row is degenerate, the other samples normally
+@pytest.mark.parametrize("M", [2, 7])
+def test_fused_degenerate_row(env, oracle, full_head, M):
+    # a NaN hidden row gives NaN logits: that row is degenerate, the others sample normally
     torch, dev, t = env
-    hb = hidden_bf16(740, 2, D)
+    hb = hidden_bf16(740 + M, M, D)
     hb[1, 100] = 0x7FC0
-    params = [t.RowParams(0.7, 0.9, 40, 1.0, 0.5, CAP, 0, 0), t.RowParams(0.7, 0.9, 40, 1.0, 0.5, CAP, 0, 0)]
-    tok = run_and_check(env, oracle, full_head, hb, params, np.zeros(0, np.uint32), "nan row")
-    assert tok[1] == t.TOKEN_DEGENERATE and tok[0] != t.TOKEN_DEGENERATE
+    params = [t.RowParams(0.7, 0.9, 40, 1.0, 0.5, CAP, 0, 0)] * M
+    tok = run_and_check(env, oracle, full_head, hb, params, np.zeros(0, np.uint32), f"nan row M={M}")
+    assert tok[1] == t.TOKEN_DEGENERATE
+    assert all(tok[m] != t.TOKEN_DEGENERATE for m in range(M) if m != 1)
 
 
 @pytest.mark.parametrize("M", [9, 20, 40, 64])

@@ -28,11 +28,11 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
-// greedy: also the grid-wide rank maximum; sample (M <= 4, resident-h kernel only): the
-// repetition penalty in place and each block's selection statistics
+// greedy: also the grid-wide rank maximum; sample (M <= 8, resident-h kernel only): the
+// repetition penalty in place and each wave's selection statistics
 enum HeadMode { kModeLogits = 0, kModeGreedy = 1, kModeSample = 2 };
 
-constexpr uint32_t kSampleRows = 4;  // rows of the sample mode
+constexpr uint32_t kSampleRows = 8;  // rows of the sample mode: four apart up to 4, two apart up to 8
 
 constexpr int kHeadThreads = 256;
 constexpr int kHeadWaves = 4;
@@ -300,8 +300,9 @@ __device__ __forceinline__ void grid_finish(const HeadArgs& a, EpiSharedT<NW>& s
     if (tid == 0 && a.vres) verify_bookkeeping(se.tok, a.M, a.drafts, a.n_drafts, a.vres);
 }
 
-// Sample mode of the resident-h kernel with rows spread four apart (MS = 4: row m's outputs are
-// accumulator entry 0 of lanes 16m .. 16m + 15). Per live entry: the softcap, then
+// Sample mode of the resident-h kernel. With rows spread four apart (MS = 4, M <= 4) row m's
+// outputs are accumulator entry 0 of lanes 16m .. 16m + 15; two apart (MS = 2, M <= 8) rows 2g
+// and 2g + 1 are entries 0 and 2 of lanes 16g .. 16g + 15. Per live entry: the softcap, then
 // apply_repetition_penalty (sampling.cpp:74-90) with the entry's occurrence count from the
 // block's LDS counts, one occurrence at a time (divide or multiply, then clamp), then the store.
 // Each wave then publishes, per row, the statistics of its 64 vocabulary rows that
@@ -309,63 +310,78 @@ __device__ __forceinline__ void grid_finish(const HeadArgs& a, EpiSharedT<NW>& s
 // exp(v - that value) in double, NaN when the wave saw a NaN (the row is then degenerate, as a
 // NaN makes the reference's total NaN) -- with no barrier and no cross-wave step. tbl holds
 // 2^(j/64), j < 64, for exp_for_sum.
-template <int RT, int NW>
+template <int RT, int NW, int MS>
 __device__ __forceinline__ void head_epilogue_sample(const HeadArgs& a, f32x4_t (&tot)[RT][1],
                                                      uint32_t tile0, uint32_t block_row0,
-                                                     const uint32_t* cnt, const double* tbl) {
+                                                     const uint32_t* cnt, const double* tbl,
+                                                     const float* prm) {
     constexpr uint32_t kRowsPerBlock = NW * RT * kTileRows;
     const int lane = threadIdx.x & 63;
-    const uint32_t m = lane >> 4;
-    const bool mlive = m < a.M;
-    const uint32_t mm = mlive ? m : 0u;
-    const float rp = a.rp[mm], lim = a.clamp[mm];
-    float v[RT];
-    uint64_t best = 0;
-    uint32_t nan = 0;
 #pragma unroll
-    for (int j = 0; j < RT; ++j) {
-        const uint32_t r = (tile0 + j) * kTileRows + (lane & 15);
-        const bool live = mlive && r < a.vocab;
-        float x = tot[j][0][0];
-        if (a.softcap > 0.0f) x = a.softcap * tanhf(x / a.softcap);
-        if (live && rp != 1.0f) {
-            const uint32_t n = cnt[mm * kRowsPerBlock + (r - block_row0)];
-            for (uint32_t t = 0; t < n; ++t) {
-                x = (x > 0.0f) ? (x / rp) : (x * rp);
-                if (lim > 0.0f) x = (x < -lim) ? -lim : ((lim < x) ? lim : x);
+    for (int e = 0; e < 4 / MS; ++e) {  // entry MS * e: h row (4 (lane / 16) + MS * e) / MS
+        const uint32_t m = (4 * (lane >> 4) + MS * e) / MS;
+        const bool mlive = m < a.M;
+        const uint32_t mm = mlive ? m : 0u;
+        const float rp = prm[mm], lim = prm[kSampleRows + mm];
+        float v[RT];
+        uint64_t best = 0;
+        uint32_t nan = 0;
+#pragma unroll
+        for (int j = 0; j < RT; ++j) {
+            const uint32_t r = (tile0 + j) * kTileRows + (lane & 15);
+            const bool live = mlive && r < a.vocab;
+            float x = tot[j][0][MS * e];
+            if (a.softcap > 0.0f) x = a.softcap * tanhf(x / a.softcap);
+            if (live && rp != 1.0f) {
+                const uint32_t n = cnt[mm * kRowsPerBlock + (r - block_row0)];
+                for (uint32_t t = 0; t < n; ++t) {
+                    x = (x > 0.0f) ? (x / rp) : (x * rp);
+                    if (lim > 0.0f) x = (x < -lim) ? -lim : ((lim < x) ? lim : x);
+                }
+            }
+            if (live) {
+                a.logits[static_cast<size_t>(m) * a.vocab + r] = x;
+                const uint64_t k = rank_key(x, r);
+                best = k > best ? k : best;
+                if (x != x) nan = 1;
+            }
+            v[j] = live ? x : -INFINITY;
+        }
+        // the 16 lanes of a row
+#pragma unroll
+        for (int msk = 1; msk < 16; msk <<= 1) {
+            const uint64_t o = shfl_xor_u64(best, msk);
+            best = o > best ? o : best;
+            nan |= __shfl_xor(nan, msk);
+        }
+        // the wave's largest value (exact: the best rank's value, -0 read as +0); a wave of -inf
+        // entries adds nothing to the row's sum
+        const float wm = best != 0 ? rank_value(best) : -INFINITY;
+        double sum = 0.0;
+        if (wm != -INFINITY) {
+            const double dwm = static_cast<double>(wm);
+            // exp_core where every argument of the lane is finite and in [-700, 0]: the value
+            // exp_for_sum gives there, without its special cases
+            bool core = true;
+#pragma unroll
+            for (int j = 0; j < RT; ++j)
+                core = core && __builtin_isfinite(v[j]) && static_cast<double>(v[j]) - dwm >= -700.0;
+            if (core) {
+#pragma unroll
+                for (int j = 0; j < RT; ++j) sum += exp_core(static_cast<double>(v[j]) - dwm, tbl);
+            } else {
+#pragma unroll
+                for (int j = 0; j < RT; ++j) sum += exp_for_sum(static_cast<double>(v[j]) - dwm, tbl);
             }
         }
-        if (live) {
-            a.logits[static_cast<size_t>(m) * a.vocab + r] = x;
-            const uint64_t k = rank_key(x, r);
-            best = k > best ? k : best;
-            if (x != x) nan = 1;
+#pragma unroll
+        for (int msk = 1; msk < 16; msk <<= 1) sum += __shfl_xor(sum, msk);
+        if (nan) sum = __builtin_nan("");
+        if ((lane & 15) == 0 && mlive) {
+            const size_t o = static_cast<size_t>(m) * (gridDim.x * NW) + blockIdx.x * NW + (threadIdx.x >> 6);
+            a.stats.key[o] = best;
+            a.stats.sum[o] = sum;
         }
-        v[j] = live ? x : -INFINITY;
-    }
-    // the 16 lanes of a row
-#pragma unroll
-    for (int msk = 1; msk < 16; msk <<= 1) {
-        const uint64_t o = shfl_xor_u64(best, msk);
-        best = o > best ? o : best;
-        nan |= __shfl_xor(nan, msk);
-    }
-    // the wave's largest value (exact: the best rank's value, -0 read as +0); a wave of -inf
-    // entries adds nothing to the row's sum
-    const float wm = best != 0 ? rank_value(best) : -INFINITY;
-    double sum = 0.0;
-    if (wm != -INFINITY) {
-        const double dwm = static_cast<double>(wm);
-#pragma unroll
-        for (int j = 0; j < RT; ++j) sum += exp_for_sum(static_cast<double>(v[j]) - dwm, tbl);
-    }
-#pragma unroll
-    for (int msk = 1; msk < 16; msk <<= 1) sum += __shfl_xor(sum, msk);
-    if (nan) sum = __builtin_nan("");
-    if ((lane & 15) == 0 && mlive) {
-        const size_t o = static_cast<size_t>(m) * (gridDim.x * NW) + blockIdx.x * NW + (threadIdx.x >> 6);
-        a.stats.key[o] = best;
-        a.stats.sum[o] = sum;
     }
 }
 
@@ -484,14 +500,22 @@ __global__ __launch_bounds__(NW * 64) void head_small_kernel(HeadArgs a) {
     const uint32_t last = a.nunits - 1;
     u32x4_t wq[PF][RT];
     u32x2_t sq[PF][RT];
-    // sample mode: occurrence counts of the block's rows in each row's history
+    // sample mode: occurrence counts of the block's rows in each row's history (16 / MS rows)
     constexpr uint32_t kRowsPerBlock = NW * RT * kTileRows;
-    __shared__ uint32_t cnt[MODE == kModeSample ? kSampleRows * kRowsPerBlock : 1];
+    constexpr uint32_t kCntRows = 16 / MS;
+    __shared__ uint32_t cnt[MODE == kModeSample ? kCntRows * kRowsPerBlock : 1];
     __shared__ double exp2_tbl[MODE == kModeSample ? 64 : 1];
+    // the rows' penalty factors and clamps, read per lane in the epilogue: staged here, where the
+    // load overlaps the ring fill, instead of a memory round trip at the end of every block
+    __shared__ float prm[MODE == kModeSample ? 2 * kSampleRows : 1];
     const uint32_t block_row0 = blockIdx.x * kRowsPerBlock;
     if constexpr (MODE == kModeSample) {
-        for (uint32_t i = tid; i < kSampleRows * kRowsPerBlock; i += NT) cnt[i] = 0;
+        for (uint32_t i = tid; i < kCntRows * kRowsPerBlock; i += NT) cnt[i] = 0;
         if (tid < 64) exp2_tbl[tid] = kExp2Table[tid];
+        if (tid < static_cast<int>(kSampleRows)) {
+            prm[tid] = a.rp[tid];
+            prm[kSampleRows + tid] = a.clamp[tid];
+        }
     }
     // sample mode: the history's first batch (kHistBatch ids per thread of the first row with a
     // penalty) is requested first, so that its round trip overlaps the ring fill and the staging
@@ -747,8 +771,7 @@ __global__ __launch_bounds__(NW * 64) void head_small_kernel(HeadArgs a) {
         for (int j = 0; j < RT; ++j) tot[j][0][0] = (tot[j][0][0] + tot[j][0][1]) * rms;
     }
     if constexpr (MODE == kModeSample) {
-        static_assert(MS == 4, "the sample mode takes rows spread four apart (M <= 4)");
-        head_epilogue_sample<RT, NW>(a, tot, tile0, block_row0, cnt, exp2_tbl);
+        head_epilogue_sample<RT, NW, MS>(a, tot, tile0, block_row0, cnt, exp2_tbl, prm);
     } else {
         head_epilogue<1, 4, RT, MODE, NW, MS>(a, tot, tile0, se);
     }
@@ -1468,8 +1491,9 @@ struct twd_head {
     u32x4_t* hx = nullptr;        // its bias A-fragment entries
     twd_selector* sel = nullptr;
     uint16_t* norm_w = nullptr;   // final RMSNorm weight, when loaded from a container
-    SampleStats stats{};          // per-wave statistics of the fused sample pass (M <= 4)
-    uint32_t sample_blocks = 0;   // its head blocks (0: no fused sample pass for this head)
+    SampleStats stats{};          // per-wave statistics of the fused sample pass (M <= 8)
+    uint32_t sample_blocks = 0;   // its head blocks for M <= 4 (0: no fused sample pass)
+    uint32_t sample_blocks8 = 0;  // for 5 <= M <= 8 (0: none, e.g. h and the counts exceed LDS)
 };
 
 namespace {
@@ -1484,6 +1508,9 @@ constexpr int kRTS = 4, kPFS = 2;
 constexpr int kNWS4 = 8, kNWS8 = 16;
 constexpr size_t kLdsBytes = 160 * 1024;
 constexpr uint32_t kSmallMaxRows = 8;
+// static LDS of the 16-wave sample mode (its occurrence counts, 8 rows x 1,024 block rows, and
+// the exp table), beside the dynamic h staging
+constexpr size_t kSample8StaticLds = kSampleRows * kNWS8 * kRTS * kTileRows * 4 + 64 * 8 + 1024;
 
 uint32_t blocks_for(uint32_t ntiles, int rt, int nw = kHeadWaves) {
     const uint32_t per = nw * rt;
@@ -1534,9 +1561,12 @@ int enable_small_kernels(uint32_t d) {
     if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS, kPFS, kNWS4, kModeGreedy, true>, bytes8);
     if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS, kPFS, kNWS8, kModeLogits, true>, bytes8);
     if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS, kPFS, kNWS8, kModeGreedy, true>, bytes8);
-    // the fused sample pass (M <= 4), with and without the RMSNorm prologue
+    // the fused sample pass (M <= 4), with and without the RMSNorm prologue, and 5 <= M <= 8
+    // where its counts fit beside h
     if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS, kPFS, kNWS4, kModeSample>, bytes4);
     if (e == hipSuccess) e = allow_smem(head_small_kernel<4, kRTS, kPFS, kNWS4, kModeSample, true>, bytes8);
+    if (e == hipSuccess && bytes8 + kSample8StaticLds <= kLdsBytes)
+        e = allow_smem(head_small_kernel<2, kRTS, kPFS, kNWS8, kModeSample>, bytes8);
     if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
     return TWD_OK;
 }
@@ -1561,10 +1591,15 @@ int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
     // unconditionally)
     if (e == hipSuccess) e = hipMalloc(&h->hp, sizeof(u32x4_t) * (h->nunits + 3) * 4 * 4 * 64);
     if (e == hipSuccess) e = hipMalloc(&h->hx, sizeof(u32x4_t) * (super_units(h->nunits) + 1) * 4 * 64);
-    const uint32_t sb = blocks_for(h->ntiles, kRTS, kNWS4);
-    if (sb * kNWS4 <= kSampleMaxWaves) {
+    // the fused sample pass's wave records: rows <= 4 on 8-wave blocks, 5..8 on 16-wave blocks
+    // (the two grids' wave counts differ by less than a block); the 16-wave form also needs its
+    // occurrence counts beside h in LDS
+    const uint32_t sb = blocks_for(h->ntiles, kRTS, kNWS4), sb8 = blocks_for(h->ntiles, kRTS, kNWS8);
+    const uint32_t waves = std::max(sb * kNWS4, sb8 * kNWS8);
+    if (waves <= kSampleMaxWaves) {
         h->sample_blocks = sb;
-        const size_t n = static_cast<size_t>(kSampleRows) * sb * kNWS4;
+        if (small_smem_bytes<kPFS>(kSampleRows, d) + kSample8StaticLds <= kLdsBytes) h->sample_blocks8 = sb8;
+        const size_t n = static_cast<size_t>(kSampleRows) * waves;
         if (e == hipSuccess) e = hipMalloc(&h->stats.key, n * sizeof(uint64_t));
         if (e == hipSuccess) e = hipMalloc(&h->stats.sum, n * sizeof(double));
     }
@@ -1703,13 +1738,15 @@ int launch_head_rmsnorm(twd_head* h, const float* x, const uint16_t* norm_w, flo
 }
 
 // The fused sample pass: the resident-h kernel in sample mode (softcap, penalty from LDS
-// occurrence counts, logits store, per-block statistics), then select_sample_merge_kernel. Used
-// for rows <= 4 when the head's block count allows it and the rows' histories (where the
-// penalty applies) hold at most kSampleMaxHistory ids together: every head block scans them.
+// occurrence counts, logits store, per-wave statistics), then select_sample_merge_kernel. Used
+// for rows <= 8 (rows <= 4 with the RMSNorm prologue) when the head's wave count allows it, the
+// 16-wave form's counts fit beside h, and the rows' histories (where the penalty applies) hold
+// at most kSampleMaxHistory ids together: every head block scans them.
 constexpr uint32_t kSampleMaxHistory = 16384;
 
-bool sample_fusable(const twd_head* h, uint32_t rows, const twd_row_params* params) {
+bool sample_fusable(const twd_head* h, uint32_t rows, const twd_row_params* params, bool norm) {
     if (rows == 0 || rows > kSampleRows || h->sample_blocks == 0) return false;
+    if (rows > 4 && (norm || h->sample_blocks8 == 0)) return false;  // the RMSNorm form: rows <= 4
     uint64_t ids = 0;
     for (uint32_t m = 0; m < rows; ++m)
         if (params[m].repetition_penalty != 1.0f) ids += params[m].history_len;
@@ -1746,17 +1783,24 @@ int launch_head_sample(twd_head* h, const uint16_t* hidden, const float* x, cons
             return fail(TWD_E_INVALID, "null history with a non-empty history_len");
     }
     a.stats = h->stats;
-    const uint32_t grid = h->sample_blocks;
+    uint32_t waves = 0;
     if (x) {
         const size_t bytes = small_smem_bytes<kPFS>(2 * rows, h->d);
-        head_small_kernel<4, kRTS, kPFS, kNWS4, kModeSample, true><<<grid, kNWS4 * 64, bytes, stream>>>(a);
-    } else {
-        head_small_kernel<4, kRTS, kPFS, kNWS4, kModeSample><<<grid, kNWS4 * 64, small_smem_bytes<kPFS>(rows, h->d),
-                                                             stream>>>(a);
+        head_small_kernel<4, kRTS, kPFS, kNWS4, kModeSample, true>
+            <<<h->sample_blocks, kNWS4 * 64, bytes, stream>>>(a);
+        waves = h->sample_blocks * kNWS4;
+    } else if (rows <= 4) {
+        head_small_kernel<4, kRTS, kPFS, kNWS4, kModeSample>
+            <<<h->sample_blocks, kNWS4 * 64, small_smem_bytes<kPFS>(rows, h->d), stream>>>(a);
+        waves = h->sample_blocks * kNWS4;
+    } else {  // rows two apart in the MFMA's rows, one 16-wave block per CU
+        head_small_kernel<2, kRTS, kPFS, kNWS8, kModeSample>
+            <<<h->sample_blocks8, kNWS8 * 64, small_smem_bytes<kPFS>(rows, h->d), stream>>>(a);
+        waves = h->sample_blocks8 * kNWS8;
     }
     TWD_HIP(hipGetLastError());
     static_assert(kRTS * kTileRows == kSampleWaveRows, "a wave of the sample pass owns 64 rows");
-    return launch_sample_merge(h->stats, grid * kNWS4, logits, h->vocab, rows, params, tokens, h->sel->scratch.lng,
+    return launch_sample_merge(h->stats, waves, logits, h->vocab, rows, params, tokens, h->sel->scratch.lng,
                                stream);
 }
 
@@ -1909,7 +1953,7 @@ TWD_API int twd_head_sample(twd_head* h, const uint16_t* hidden, uint32_t rows,
     clear_error();
     if (!logits || !tokens || !params) return fail(TWD_E_INVALID, "null logits, tokens or params");
     return ordered(h, stream, [&](hipStream_t s) {
-        if (sample_fusable(h, rows, params)) {
+        if (sample_fusable(h, rows, params, false)) {
             if (!hidden || !aligned16(hidden))
                 return fail(TWD_E_INVALID, "hidden must be a 16-byte aligned device pointer");
             return launch_head_sample(h, hidden, nullptr, nullptr, 0.0f, rows, params, history, logits,
@@ -1963,7 +2007,7 @@ TWD_API int twd_head_sample_rmsnorm(twd_head* h, const float* x, const uint16_t*
     clear_error();
     if (!logits || !tokens || !params) return fail(TWD_E_INVALID, "null logits, tokens or params");
     return ordered(h, stream, [&](hipStream_t s) {
-        if (sample_fusable(h, rows, params)) {
+        if (sample_fusable(h, rows, params, true)) {
             if (!x || !aligned16(x)) return fail(TWD_E_INVALID, "x must be a 16-byte aligned device pointer");
             if (!norm_w || !aligned16(norm_w))
                 return fail(TWD_E_INVALID, "norm_weight must be a 16-byte aligned device pointer");
