@@ -131,41 +131,64 @@ uint32_t thr_units(float thr, int E) {
 struct SegRec {
     int E[2];
     Xfer f[2];
+    // crossing data (seg_xfer_kernel writes it where the double sums predict a binade change in
+    // the segment): bit 0 present, bit 1 + c: candidate c's terms hold no exact half-way case;
+    // lane_inc[c][l] the increments of lanes 0..l in candidate c's units (inclusive, saturating)
+    uint32_t xl = 0;
+    uint32_t lane_inc[2][W] = {};
 };
 
 struct Stats {
     long exact_segments = 0, passes = 0, tie_passes = 0, walk_steps = 0, mispredicted = 0;
+    long crossings = 0, crossings_finished = 0;
 };
 
 // seg_xfer_kernel, wave w's segment s: the double prefix D predicts the binade of the running
 // sum at the segment start; the segment's transfer functions for that binade and its nearer
 // neighbour, composed in order
-SegRec make_record(const std::vector<float>& t, uint32_t n, uint32_t s, double D) {
+SegRec make_record(const std::vector<float>& t, uint32_t n, uint32_t s, double D, double Dend) {
     int ex = 0;
     const double m = std::frexp(D, &ex);
     const bool low = D < 0x1p-125;
     const int E0 = low ? -126 : ex - 1;
     const int E1 = low ? -125 : std::max(-126, m < 0.75 ? ex - 2 : ex);
     Lanes<Xfer> f0, f1;
+    Lanes<bool> tie0, tie1;
     for (int lane = 0; lane < W; ++lane) {
         const uint32_t j0 = kSegHead + s * kSegLen + static_cast<uint32_t>(lane) * kSegPer;
         Xfer a0 = xfer_id(), a1 = xfer_id();
+        tie0[lane] = tie1[lane] = false;
         for (int q = 0; q < kSegPer; ++q) {
             const float a = j0 + q < n ? t[j0 + q] : 0.0f;
             uint32_t kk, kd;
             split_term(a, E0, kk, kd);
             a0 = xfer_then(a0, term_xfer(kk, kd));
+            tie0[lane] = tie0[lane] || kd == 2u;
             split_term(a, E1, kk, kd);
             a1 = xfer_then(a1, term_xfer(kk, kd));
+            tie1[lane] = tie1[lane] || kd == 2u;
         }
         f0[lane] = a0;
         f1[lane] = a1;
     }
+    const Lanes<Xfer> s0 = xfer_scan(f0), s1 = xfer_scan(f1);
     SegRec r;
     r.E[0] = E0;
     r.E[1] = E1;
-    r.f[0] = xfer_scan(f0)[W - 1];  // lane 63's inclusive scan
-    r.f[1] = xfer_scan(f1)[W - 1];
+    r.f[0] = s0[W - 1];  // lane 63's inclusive scan
+    r.f[1] = s1[W - 1];
+    // a predicted crossing: the double sums before and after the segment, widened by 2^-10,
+    // lie in different binades
+    int e_lo = 0, e_hi = 0;
+    (void)std::frexp(D * (1.0 - 0x1p-10), &e_lo);
+    (void)std::frexp(Dend * (1.0 + 0x1p-10), &e_hi);
+    if (e_lo != e_hi) {
+        r.xl = 1u | (ballot(tie0) == 0 ? 2u : 0u) | (ballot(tie1) == 0 ? 4u : 0u);
+        for (int lane = 0; lane < W; ++lane) {
+            r.lane_inc[0][lane] = s0[lane].inc0;
+            r.lane_inc[1][lane] = s1[lane].inc0;
+        }
+    }
     return r;
 }
 
@@ -359,6 +382,50 @@ float wave_seg_sum(const std::vector<float>& t, uint32_t n, uint32_t k0, uint32_
     return S;
 }
 
+// The walk's crossing shortcut for segment [k0, k1) (seg_chain, no stop threshold): when the
+// segment carries crossing data for S's binade E and for E + 1, both free of exact half-way
+// terms, the lanes' increments in units of E locate the lane c where S leaves E; S before that
+// lane is exact, the lane's terms are added with fp32 adds in order (the reference's own
+// operations), and, when S has then reached E + 1, the later lanes' increments in units of E + 1
+// give the segment's end unless it leaves E + 1 as well. Returns false (S untouched) when the
+// data does not apply; otherwise S holds the sum after the segment (the rest of the segment
+// summed exactly by wave_seg_sum where the shortcut stops short).
+bool crossing(const std::vector<float>& t, const SegRec& R, uint32_t k0, uint32_t k1, uint32_t n, float& S,
+              Stats& st) {
+    if (!(R.xl & 1u)) return false;
+    uint32_t B;
+    const int E = binade(S, B);
+    const int ce = R.E[0] == E ? 0 : (R.E[1] == E ? 1 : -1);
+    if (ce < 0 || R.E[1 - ce] != E + 1 || !((R.xl >> (1 + ce)) & 1u) || !((R.xl >> (2 - ce)) & 1u)) return false;
+    Lanes<bool> over;
+    for (int lane = 0; lane < W; ++lane) over[lane] = B + R.lane_inc[ce][lane] >= kL;
+    const int c = ffs64(ballot(over));
+    if (c < 0) return false;  // no lane leaves E: the walk's own test found another reason
+    ++st.crossings;
+    const uint32_t ex = c > 0 ? R.lane_inc[ce][c - 1] : 0u;
+    MODEL_ASSERT(B + ex < kL, "the sum before the crossing lane stays in its binade");
+    float s = std::ldexp(static_cast<float>(B + ex), E - 23);
+    const uint32_t jc = k0 + static_cast<uint32_t>(c) * kSegPer;
+    for (int q = 0; q < kSegPer; ++q) {
+        const uint32_t j = jc + static_cast<uint32_t>(q);
+        s += (j < k1 && j < n) ? t[j] : 0.0f;
+    }
+    uint32_t B2;
+    const int E2 = binade(s, B2);
+    const uint32_t tot1 = R.lane_inc[1 - ce][W - 1], pre1 = R.lane_inc[1 - ce][c];
+    if (E2 == E + 1 && tot1 < kSat && B2 + (tot1 - pre1) < kL) {
+        S = std::ldexp(static_cast<float>(B2 + (tot1 - pre1)), E2 - 23);
+        ++st.crossings_finished;
+        return true;
+    }
+    S = s;
+    if (jc + kSegPer < k1) {
+        uint32_t at = k1;
+        S = wave_seg_sum(t, n, jc + kSegPer, k1, S, 0.0f, false, &at, st);
+    }
+    return true;
+}
+
 // seg_chain: the walk over the records from the head's sum S, 64 records per step
 float seg_chain(const std::vector<float>& t, uint32_t n, const std::vector<SegRec>& rec, float S, float thr,
                 uint32_t* stop_at, std::vector<float>& start, Stats& st) {
@@ -439,6 +506,10 @@ float seg_chain(const std::vector<float>& t, uint32_t n, const std::vector<SegRe
         if (t_seg >= nseg) break;
         const uint32_t k0 = kSegHead + t_seg * kSegLen, k1 = std::min(n, k0 + kSegLen);
         uint32_t at = k1;
+        if (!want_stop && crossing(t, rec[t_seg], k0, k1, n, S, st)) {
+            ++t_seg;
+            continue;
+        }
         S = wave_seg_sum(t, n, k0, k1, S, thr, want_stop, &at, st);
         if (want_stop && at < k1) {
             stop = at;
@@ -472,7 +543,7 @@ RowResult engine(const std::vector<float>& t, uint32_t n, float thr, bool want_s
     double D = 0.0;
     for (uint32_t s = 0; s < nseg; ++s) {
         D += d[s];
-        rec[s] = make_record(t, n, s, D);
+        rec[s] = make_record(t, n, s, D, D + d[s + 1]);
     }
     // the serial head, staged in LDS (kSegHead entries)
     std::vector<float> hterm(kSegHead, 0.0f);
@@ -652,6 +723,8 @@ int main(int argc, char** argv) {
     for (int k = 0; k < 6; ++k) std::printf("%-18s %ld rows\n", names[k], checked[k]);
     std::printf("exact segments %ld (passes %ld, with a tie %ld), walk steps %ld, record lookups outside both binades %ld\n",
                 st.exact_segments, st.passes, st.tie_passes, st.walk_steps, st.mispredicted);
+    std::printf("crossings resolved from the crossing data %ld (finished without a pass %ld)\n", st.crossings,
+                st.crossings_finished);
     std::printf("mismatches %ld\n", bad);
     if (bad == 0) std::puts("MODEL OK");
     return bad == 0 ? 0 : 1;

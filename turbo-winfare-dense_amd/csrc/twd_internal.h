@@ -376,6 +376,7 @@ struct DraftScratch {
     double* seg_d = nullptr;   // [2 * TWD_MAX_ROWS][segments + 1] double sums of the exact-sum pipeline
     void* seg_rec = nullptr;   // [2 * TWD_MAX_ROWS][segments] segment records
     void* seg_head = nullptr;  // [2 * TWD_MAX_ROWS] the serial heads' sums
+    uint32_t* xin = nullptr;   // [2 positions][segments][128] the segments' crossing data
     uint32_t* live = nullptr;  // [TWD_MAX_ROWS] 1: the position's draft was rejected
     uint64_t* fin_ctr = nullptr;  // [2] the residual launch's arrival counter (epoch-armed)
     uint32_t fin_epoch = 0;       // the last call's epoch
@@ -383,6 +384,7 @@ struct DraftScratch {
     hipEvent_t fork = nullptr, join = nullptr;
     size_t e_capacity = 0;
     size_t part_capacity = 0;
+    size_t x_capacity = 0;
     uint32_t last_npos = 0;               // positions of the last call with draft rows
     uint32_t last_pos[TWD_MAX_ROWS] = {};
 };

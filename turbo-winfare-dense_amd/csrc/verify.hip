@@ -88,6 +88,7 @@ struct DraftArgs {
     uint32_t* flags;              // [2P] bit 0: a NaN term
     float* sums;                  // [2P] compute_softmax sums
     double* seg_d;                // [2P][segments + 1] double sums of the head and each segment
+    uint32_t* xin;                // [2P][kSegMax][2][64] the segments' crossing data
     uint32_t* rej;                // [64][4] {accepted, token, fallback, valid}
     DraftPos pos[TWD_MAX_ROWS];
 };
@@ -617,7 +618,13 @@ static_assert(kSegHead <= kSerialUntil, "block_seq_sum adds a head in order");
 struct SegRec {
     int E[2];   // the two candidate binades (exponents of S's leading bit; -126: below 2^-125)
     Xfer f[2];  // the segment's composed transfer functions in units of 2^(E - 23)
+    // crossing data, written where the double sums predict a binade change inside the segment:
+    // bit 0 present; bit 1 + c: candidate c's terms hold no exact half-way case. The data itself
+    // (kXinWords per segment): per candidate c and lane l, the increments of lanes 0 .. l in c's
+    // units (the lanes' inclusive scan, saturating)
+    uint32_t xl;
 };
+constexpr uint32_t kXinWords = 2 * 64;
 
 struct SegHead {  // the serial head's sum; with a stop, the first index whose prefix reaches thr
     float S;
@@ -716,7 +723,8 @@ __global__ __launch_bounds__(kXferThreads) void seg_dsum_kernel(Src src, uint32_
 // here, beside the records, so that the chain kernel starts at the walk.
 template <class Src>
 __global__ __launch_bounds__(kXferThreads) void seg_xfer_kernel(Src src, uint32_t n, const double* d, SegRec* rec,
-                                                                float thr, uint32_t want_stop, SegHead* head) {
+                                                                float thr, uint32_t want_stop, SegHead* head,
+                                                                uint32_t* xin) {
     __shared__ float hterm[kSegHead];
     const uint32_t row = blockIdx.y;
     if (!src.active(row)) return;  // the whole block
@@ -760,6 +768,7 @@ __global__ __launch_bounds__(kXferThreads) void seg_xfer_kernel(Src src, uint32_
     double dv[kDq];
 #pragma unroll
     for (int q = 0; q < kDq; ++q) dv[q] = dr[min(static_cast<uint32_t>(lane + q * 64), s)];
+    const double dseg = dr[1 + s];  // this segment's own double sum
     double t = 0.0;
 #pragma unroll
     for (int q = 0; q < kDq; ++q) t += static_cast<uint32_t>(lane + q * 64) <= s ? dv[q] : 0.0;
@@ -776,23 +785,39 @@ __global__ __launch_bounds__(kXferThreads) void seg_xfer_kernel(Src src, uint32_
 #pragma unroll
     for (int q = 0; q < kSegPer; ++q) av[q] = src.term(row, min(j0 + q, n - 1u));
     Xfer f0 = xfer_id(), f1 = xfer_id();
+    bool tie0 = false, tie1 = false;
 #pragma unroll
     for (int q = 0; q < kSegPer; ++q) {
         const float a = j0 + q < n ? av[q] : 0.0f;
         uint32_t kk, kd;
         split_term(a, E0, kk, kd);
         f0 = xfer_then(f0, term_xfer(kk, kd));
+        tie0 = tie0 || kd == 2u;
         split_term(a, E1, kk, kd);
         f1 = xfer_then(f1, term_xfer(kk, kd));
+        tie1 = tie1 || kd == 2u;
     }
     f0 = xfer_wave_scan(f0);
     f1 = xfer_wave_scan(f1);
+    // the crossing data, where the double sums before and after the segment (widened by 2^-10)
+    // lie in different binades: the walk finds the lane that leaves S's binade from it
+    int e_lo = 0, e_hi = 0;
+    (void)frexp(D * (1.0 - 0x1p-10), &e_lo);
+    (void)frexp((D + dseg) * (1.0 + 0x1p-10), &e_hi);
+    uint32_t xl = 0u;
+    if (xin && e_lo != e_hi) {
+        xl = 1u | (__ballot(tie0) == 0 ? 2u : 0u) | (__ballot(tie1) == 0 ? 4u : 0u);
+        uint32_t* x = xin + (static_cast<size_t>(row) * kSegMax + s) * kXinWords;
+        x[lane] = f0.inc0;
+        x[64 + lane] = f1.inc0;
+    }
     if (lane == 63) {
         SegRec r;
         r.E[0] = E0;
         r.E[1] = E1;
         r.f[0] = f0;
         r.f[1] = f1;
+        r.xl = xl;
         rec[static_cast<size_t>(row) * kSegMax + s] = r;
     }
 }
@@ -981,6 +1006,62 @@ __device__ float wave_seg_sum(Load load, uint32_t n, uint32_t k0, uint32_t k1, f
     return S;
 }
 
+// The walk's crossing shortcut for segment [k0, k1) (one wave, no stop threshold). When the
+// segment carries crossing data for S's binade E and for E + 1, both free of exact half-way
+// terms, each lane's increments in units of E locate the lane c where S leaves E: the sum
+// before lane c is exact (integer increments inside one binade); lane c's terms are added one
+// by one with fp32 adds, the reference's own operations; and when S has then reached E + 1, the
+// later lanes' increments in units of E + 1 give the segment's end unless it leaves E + 1 too.
+// Where the shortcut stops short, wave_seg_sum sums the rest of the segment exactly. Returns
+// false, with S untouched, when the data does not apply; otherwise S is the sum after the
+// segment. x: the segment's kXinWords crossing words. Every lane returns the same values.
+template <typename Load>
+__device__ bool seg_crossing(Load load, uint32_t n, const SegRec& R, const uint32_t* x, uint32_t k0, uint32_t k1,
+                             float& S) {
+    if (!(R.xl & 1u)) return false;
+    const int lane = threadIdx.x & 63;
+    const uint32_t sb = __float_as_uint(S), sf = sb >> 23;
+    const int E = sf ? static_cast<int>(sf) - 127 : -126;
+    const uint32_t B = sf ? ((sb & 0x7FFFFFu) | 0x800000u) : sb;
+    const int ce = R.E[0] == E ? 0 : (R.E[1] == E ? 1 : -1);
+    if (ce < 0 || R.E[1 - ce] != E + 1 || !((R.xl >> (1 + ce)) & 1u) || !((R.xl >> (2 - ce)) & 1u)) return false;
+    // the lanes' increments in both binades and the lane's terms: one round trip
+    const uint32_t incE = x[ce * 64 + lane], incE1 = x[(1 - ce) * 64 + lane];
+    const uint32_t j0 = k0 + static_cast<uint32_t>(lane) * kSegPer;
+    float a[kSegPer];
+    if (j0 < ((n + 15u) & ~15u)) {  // rows are padded to 16 floats: the whole load is inside
+        load(j0, a);
+    } else {
+#pragma unroll
+        for (int q = 0; q < kSegPer; ++q) a[q] = 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < kSegPer; ++q)
+        if (j0 + q >= k1) a[q] = 0.0f;
+    const uint64_t over = __ballot(B + incE >= kL);  // B < 2^24, incE <= 2^30: no wrap
+    if (over == 0) return false;  // no lane leaves E: the walk stopped here for another reason
+    const int c = __ffsll(static_cast<long long>(over)) - 1;
+    const uint32_t ex = c > 0 ? lane_u32(incE, c - 1) : 0u;  // < 2^24 - B: S stays in E
+    float sc = ldexpf(static_cast<float>(B + ex), E - 23);
+#pragma unroll
+    for (int q = 0; q < kSegPer; ++q) sc = sc + lane_f32(a[q], c);
+    const uint32_t sb2 = __float_as_uint(sc), sf2 = sb2 >> 23;
+    const int E2 = sf2 ? static_cast<int>(sf2) - 127 : -126;
+    const uint32_t B2 = sf2 ? ((sb2 & 0x7FFFFFu) | 0x800000u) : sb2;
+    const uint32_t tot1 = lane_u32(incE1, 63), pre1 = lane_u32(incE1, c);
+    if (E2 == E + 1 && tot1 < kSat && B2 + (tot1 - pre1) < kL) {
+        S = ldexpf(static_cast<float>(B2 + (tot1 - pre1)), E2 - 23);
+        return true;
+    }
+    S = sc;
+    const uint32_t jn = k0 + static_cast<uint32_t>(c + 1) * kSegPer;
+    if (jn < k1) {
+        uint32_t at = k1;
+        S = wave_seg_sum(load, n, jn, k1, S, 0.0f, false, &at);
+    }
+    return true;
+}
+
 struct ChainShared {
     SegRec rec[kSegMax];
     float start[kSegMax + 1];  // the exact sum at each segment start, then the row's sum
@@ -994,7 +1075,7 @@ struct ChainShared {
 // every t the chain passes.
 template <typename Load, typename Term>
 __device__ float seg_chain(Load load, Term term, uint32_t n, float S, float thr, uint32_t* stop_at,
-                           SeqShared& sh, ChainShared& ch) {
+                           const uint32_t* xr, SeqShared& sh, ChainShared& ch) {
     (void)term;
     (void)sh;
     const uint32_t nseg = seg_count(n);
@@ -1052,8 +1133,12 @@ __device__ float seg_chain(Load load, Term term, uint32_t n, float S, float thr,
                 if (first < 64 || t >= nseg) break;
             }
             if (t >= nseg) break;
-            // segment t exactly, from S
+            // segment t exactly, from S: by its crossing data where that applies
             const uint32_t k0 = kSegHead + t * kSegLen, k1 = min(n, k0 + kSegLen);
+            if (!want_stop && xr && seg_crossing(load, n, ch.rec[t], xr + static_cast<size_t>(t) * kXinWords, k0, k1, S)) {
+                ++t;
+                continue;
+            }
             uint32_t at = k1;
             S = wave_seg_sum(load, n, k0, k1, S, thr, want_stop, &at);
             if (want_stop && at < k1) {
@@ -1078,7 +1163,7 @@ __device__ float seg_chain(Load load, Term term, uint32_t n, float S, float thr,
 // The chain of one row: its records into LDS, the head's sum from seg_xfer_kernel, the walk.
 template <typename Load, typename Term>
 __device__ float seg_row_sum(Load load, Term term, uint32_t n, const SegRec* rec, const SegHead* hd, float thr,
-                             uint32_t* stop_at, SeqShared& sh, ChainShared& ch) {
+                             uint32_t* stop_at, const uint32_t* xr, SeqShared& sh, ChainShared& ch) {
     const uint32_t nseg = seg_count(n);
     const SegHead h = *hd;  // the same value in every thread; requested with the records
     for (uint32_t i = threadIdx.x; i < nseg; i += blockDim.x) ch.rec[i] = rec[i];
@@ -1087,7 +1172,7 @@ __device__ float seg_row_sum(Load load, Term term, uint32_t n, const SegRec* rec
         *stop_at = h.stop;
         return h.S;
     }
-    return seg_chain(load, term, n, h.S, thr, stop_at, sh, ch);
+    return seg_chain(load, term, n, h.S, thr, stop_at, xr, sh, ch);
 }
 
 // The softmax sums of the e rows: one block per row.
@@ -1118,7 +1203,8 @@ __global__ __launch_bounds__(kRejThreads) void seg_sum_kernel(DraftArgs a, const
     float s = __uint_as_float(0x7FC00000u);
     if (!(a.flags[r] & 1u))
         s = seg_row_sum([&](uint32_t j0, auto& v) { load_row(e, j0, v); }, [&](uint32_t j) { return e[j]; },
-                        a.vocab, rec + static_cast<size_t>(r) * kSegMax, heads + r, 0.0f, nullptr, sh, ch);
+                        a.vocab, rec + static_cast<size_t>(r) * kSegMax, heads + r, 0.0f, nullptr,
+                        a.xin + static_cast<size_t>(r) * kSegMax * kXinWords, sh, ch);
     if (threadIdx.x == 0) a.sums[r] = s;
 }
 
@@ -1226,7 +1312,8 @@ __device__ __forceinline__ void seg_residual_block(const DraftArgs& a, uint32_t 
         for (int q = 0; q < PER; ++q) v[q] = diff1(v[q], w[q]);
     };
     const SegRec* rr = rec + static_cast<size_t>(pi) * kSegMax;
-    const float sum_diff = seg_row_sum(load_diff, diff, V, rr, heads + pi, 0.0f, nullptr, sh, ch);
+    const float sum_diff = seg_row_sum(load_diff, diff, V, rr, heads + pi, 0.0f, nullptr,
+                                       a.xin + static_cast<size_t>(pi) * kSegMax * kXinWords, sh, ch);
     uint32_t corr = 0, fallback = 0;
     if (sum_diff > 1e-9f) {
         const float r_val = P.u2 * sum_diff;
@@ -1271,12 +1358,13 @@ __device__ __forceinline__ void seg_residual_block(const DraftArgs& a, uint32_t 
 template <bool STOP>
 __global__ __launch_bounds__(kRejThreads) void seg_array_kernel(const float* x, uint32_t n, float thr,
                                                                 const SegRec* rec, const SegHead* hd,
-                                                                float* sum_out, uint32_t* stop_out) {
+                                                                const uint32_t* xin, float* sum_out,
+                                                                uint32_t* stop_out) {
     __shared__ SeqShared sh;
     __shared__ ChainShared ch;
     uint32_t stop = n;
     const float s = seg_row_sum([&](uint32_t j0, auto& v) { load_row(x, j0, v); }, [&](uint32_t j) { return x[j]; },
-                                n, rec, hd, thr, STOP ? &stop : nullptr, sh, ch);
+                                n, rec, hd, thr, STOP ? &stop : nullptr, xin, sh, ch);
     if (threadIdx.x == 0) {
         *sum_out = s;
         if (STOP) *stop_out = stop;
@@ -1339,13 +1427,16 @@ int draft_scratch_reserve(DraftScratch* d, uint32_t vocab, uint32_t npos) {
     const uint32_t parts = (vocab + kDraftChunk - 1) / kDraftChunk;
     const size_t need_e = static_cast<size_t>(2) * npos * ((vocab + 15u) & ~15u);
     const size_t need_part = static_cast<size_t>(2) * npos * parts;
+    const size_t need_x = static_cast<size_t>(2) * npos * kSegMax * kXinWords;
     // the capacities are set only once every buffer exists, so a call after a failed one never
     // finds a partial set
-    if (d->e_capacity >= need_e && d->part_capacity >= need_part && d->side) return TWD_OK;
+    if (d->e_capacity >= need_e && d->part_capacity >= need_part && d->x_capacity >= need_x && d->side)
+        return TWD_OK;
     draft_scratch_free(d);  // grows: later calls with as many positions reuse it
     hipError_t e = hipSuccess;
     if (e == hipSuccess) e = hipMalloc(&d->e, need_e * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&d->part, need_part * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&d->xin, need_x * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMalloc(&d->flags, 2 * TWD_MAX_ROWS * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMalloc(&d->rej, 4 * TWD_MAX_ROWS * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMalloc(&d->sums, 2 * TWD_MAX_ROWS * sizeof(float));
@@ -1371,12 +1462,14 @@ int draft_scratch_reserve(DraftScratch* d, uint32_t vocab, uint32_t npos) {
     d->fin_epoch = kFirstEpoch - 1;
     d->e_capacity = need_e;
     d->part_capacity = need_part;
+    d->x_capacity = need_x;
     return TWD_OK;
 }
 
 void draft_scratch_free(DraftScratch* d) {
     if (d->e) (void)hipFree(d->e);
     if (d->part) (void)hipFree(d->part);
+    if (d->xin) (void)hipFree(d->xin);
     if (d->flags) (void)hipFree(d->flags);
     if (d->rej) (void)hipFree(d->rej);
     if (d->sums) (void)hipFree(d->sums);
@@ -1440,23 +1533,25 @@ TWD_API int twd_sequential_sum(const float* terms, uint32_t n, float thr, float*
     static double* seg_d = nullptr;
     static SegRec* seg_rec = nullptr;
     static SegHead* seg_head = nullptr;
+    static uint32_t* xin = nullptr;
     {
         std::lock_guard<std::mutex> lock(mu);
-        if (!seg_d) {
-            TWD_HIP(hipMalloc(&seg_d, (kSegMax + 1) * sizeof(double)));
-            TWD_HIP(hipMalloc(&seg_rec, kSegMax * sizeof(SegRec)));
-            TWD_HIP(hipMalloc(&seg_head, sizeof(SegHead)));
+        if (!xin) {
+            if (!seg_d) TWD_HIP(hipMalloc(&seg_d, (kSegMax + 1) * sizeof(double)));
+            if (!seg_rec) TWD_HIP(hipMalloc(&seg_rec, kSegMax * sizeof(SegRec)));
+            if (!seg_head) TWD_HIP(hipMalloc(&seg_head, sizeof(SegHead)));
+            TWD_HIP(hipMalloc(&xin, static_cast<size_t>(kSegMax) * kXinWords * sizeof(uint32_t)));
         }
     }
     const uint32_t nseg = seg_count(n);
     const SegSrcArray src{terms};
     seg_dsum_kernel<<<dim3(xfer_blocks(n), 1), kXferThreads, 0, s>>>(src, n, seg_d);
     seg_xfer_kernel<<<dim3(xfer_blocks(n), 1), kXferThreads, 0, s>>>(src, n, seg_d, seg_rec, thr,
-                                                                     stop_out ? 1u : 0u, seg_head);
+                                                                     stop_out ? 1u : 0u, seg_head, xin);
     if (stop_out)
-        seg_array_kernel<true><<<1, kRejThreads, 0, s>>>(terms, n, thr, seg_rec, seg_head, sum_out, stop_out);
+        seg_array_kernel<true><<<1, kRejThreads, 0, s>>>(terms, n, thr, seg_rec, seg_head, xin, sum_out, stop_out);
     else
-        seg_array_kernel<false><<<1, kRejThreads, 0, s>>>(terms, n, thr, seg_rec, seg_head, sum_out, stop_out);
+        seg_array_kernel<false><<<1, kRejThreads, 0, s>>>(terms, n, thr, seg_rec, seg_head, xin, sum_out, stop_out);
     TWD_HIP(hipGetLastError());
     return TWD_OK;
 }
@@ -1565,6 +1660,7 @@ int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab
     a.rej = sel->draft.rej;
     a.sums = sel->draft.sums;
     a.seg_d = sel->draft.seg_d;
+    a.xin = sel->draft.xin;
     sel->draft.last_npos = a.npos;
     for (uint32_t i = 0; i < a.npos; ++i) sel->draft.last_pos[i] = a.pos[i].position;
     const dim3 grid(a.parts, 2 * a.npos);
@@ -1578,12 +1674,12 @@ int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab
     const SegSrcSoftmax src_e{a.e, a.estride, a.flags};
     SegHead* seg_head = static_cast<SegHead*>(ds.seg_head);
     seg_xfer_kernel<<<dim3(xfer_blocks(vocab), 2 * a.npos), kXferThreads, 0, s>>>(src_e, vocab, seg_d, seg_rec,
-                                                                                 0.0f, 0u, seg_head);
+                                                                                 0.0f, 0u, seg_head, a.xin);
     seg_sum_kernel<<<2 * a.npos + dsel.nsel, kRejThreads, 0, s>>>(a, seg_rec, seg_head, dsel);
     seg_ratio_dsum_kernel<<<dim3(xfer_blocks(vocab), a.npos), kXferThreads, 0, s>>>(a, ds.live, seg_d);
     const SegSrcResidual src_r{a.e, a.estride, a.sums, ds.live};
     seg_xfer_kernel<<<dim3(xfer_blocks(vocab), a.npos), kXferThreads, 0, s>>>(src_r, vocab, seg_d, seg_rec, 0.0f, 0u,
-                                                                             seg_head);
+                                                                             seg_head, a.xin);
     if (!fused) TWD_HIP(hipStreamWaitEvent(s, ds.join, 0));  // the selector's tokens, read by the finish
     ds.fin_epoch = epoch_after(ds.fin_epoch);
     const DraftFinish fin{sel->scratch.verify_tokens, used, drafts, n_drafts, has, result,
