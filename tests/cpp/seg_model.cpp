@@ -1,5 +1,6 @@
 // A CPU model of the draft verify's exact sequential-sum engine (turbo-winfare-dense_amd/csrc/
-// verify.hip: seg_xfer_kernel, seg_chain, wave_seg_sum, seg_residual_block's search), over a
+// verify.hip: seg_xfer_kernel with its crossing data, seg_chain with seg_crossing, wave_seg_sum,
+// seg_residual_block's search), over a
 // simulated 64-lane wave, statement for statement with the device code. The engine reproduces
 // `float s = 0; for (j = 0; j < n; ++j) s += t[j];` bit for bit (the sums of compute_softmax and
 // of the residual draw, src/speculator.cpp:22-26,104-116); this program checks it against that

@@ -1,5 +1,6 @@
 """The CPU model of the draft verify's exact sequential-sum engine (tests/cpp/seg_model.cpp):
-the segment records, the walk, the one-wave exact segments and the residual draw's search,
+the segment records with their crossing data, the walk and its crossing shortcut, the one-wave
+exact segments and the residual draw's search,
 transliterated from turbo-winfare-dense_amd/csrc/verify.hip over a simulated 64-lane wave.
 1,600 rows of six kinds (softmax terms, residual terms, exact half-way ties, powers of two,
 terms near 0.5, zeros with tiny and sparse big terms), 1,000 to 300,000 terms, each summed

@@ -1014,10 +1014,11 @@ __device__ float wave_seg_sum(Load load, uint32_t n, uint32_t k0, uint32_t k1, f
 // later lanes' increments in units of E + 1 give the segment's end unless it leaves E + 1 too.
 // Where the shortcut stops short, wave_seg_sum sums the rest of the segment exactly. Returns
 // false, with S untouched, when the data does not apply; otherwise S is the sum after the
-// segment. x: the segment's kXinWords crossing words. Every lane returns the same values.
+// segment. x: the segment's kXinWords crossing words; xw and xt, when not null, the same words
+// and the segment's terms (zeros past its end) staged in LDS. Every lane returns the same values.
 template <typename Load>
-__device__ bool seg_crossing(Load load, uint32_t n, const SegRec& R, const uint32_t* x, uint32_t k0, uint32_t k1,
-                             float& S) {
+__device__ bool seg_crossing(Load load, uint32_t n, const SegRec& R, const uint32_t* x, const uint32_t* xw,
+                             const float* xt, uint32_t k0, uint32_t k1, float& S) {
     if (!(R.xl & 1u)) return false;
     const int lane = threadIdx.x & 63;
     const uint32_t sb = __float_as_uint(S), sf = sb >> 23;
@@ -1025,19 +1026,29 @@ __device__ bool seg_crossing(Load load, uint32_t n, const SegRec& R, const uint3
     const uint32_t B = sf ? ((sb & 0x7FFFFFu) | 0x800000u) : sb;
     const int ce = R.E[0] == E ? 0 : (R.E[1] == E ? 1 : -1);
     if (ce < 0 || R.E[1 - ce] != E + 1 || !((R.xl >> (1 + ce)) & 1u) || !((R.xl >> (2 - ce)) & 1u)) return false;
-    // the lanes' increments in both binades and the lane's terms: one round trip
-    const uint32_t incE = x[ce * 64 + lane], incE1 = x[(1 - ce) * 64 + lane];
+    // the lanes' increments in both binades and the lane's terms: from LDS when staged, else
+    // one round trip
     const uint32_t j0 = k0 + static_cast<uint32_t>(lane) * kSegPer;
+    uint32_t incE, incE1;
     float a[kSegPer];
-    if (j0 < ((n + 15u) & ~15u)) {  // rows are padded to 16 floats: the whole load is inside
-        load(j0, a);
+    if (xw) {
+        incE = xw[ce * 64 + lane];
+        incE1 = xw[(1 - ce) * 64 + lane];
+#pragma unroll
+        for (int q = 0; q < kSegPer; ++q) a[q] = xt[lane * kSegPer + q];
     } else {
+        incE = x[ce * 64 + lane];
+        incE1 = x[(1 - ce) * 64 + lane];
+        if (j0 < ((n + 15u) & ~15u)) {  // rows are padded to 16 floats: the whole load is inside
+            load(j0, a);
+        } else {
 #pragma unroll
-        for (int q = 0; q < kSegPer; ++q) a[q] = 0.0f;
+            for (int q = 0; q < kSegPer; ++q) a[q] = 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < kSegPer; ++q)
+            if (j0 + q >= k1) a[q] = 0.0f;
     }
-#pragma unroll
-    for (int q = 0; q < kSegPer; ++q)
-        if (j0 + q >= k1) a[q] = 0.0f;
     const uint64_t over = __ballot(B + incE >= kL);  // B < 2^24, incE <= 2^30: no wrap
     if (over == 0) return false;  // no lane leaves E: the walk stopped here for another reason
     const int c = __ffsll(static_cast<long long>(over)) - 1;
@@ -1062,11 +1073,18 @@ __device__ bool seg_crossing(Load load, uint32_t n, const SegRec& R, const uint3
     return true;
 }
 
+constexpr uint32_t kXSlots = 16;         // crossing segments staged in LDS per row
+constexpr uint32_t kNoSlot = 0xFFFFFFFFu;
 struct ChainShared {
     SegRec rec[kSegMax];
     float start[kSegMax + 1];  // the exact sum at each segment start, then the row's sum
     float S;
     uint32_t s;
+    // the first kXSlots segments with crossing data, staged while wave 0 walks: xslot[t] is the
+    // slot of segment t, stored (release) once the slot holds its words and terms
+    uint32_t xslot[kSegMax];
+    uint32_t xw[kXSlots][kXinWords];
+    float xt[kXSlots][kSegLen];
 };
 
 // The walk and the exact segments after the head: S is the sum of terms [0, kSegHead) on entry.
@@ -1135,9 +1153,14 @@ __device__ float seg_chain(Load load, Term term, uint32_t n, float S, float thr,
             if (t >= nseg) break;
             // segment t exactly, from S: by its crossing data where that applies
             const uint32_t k0 = kSegHead + t * kSegLen, k1 = min(n, k0 + kSegLen);
-            if (!want_stop && xr && seg_crossing(load, n, ch.rec[t], xr + static_cast<size_t>(t) * kXinWords, k0, k1, S)) {
-                ++t;
-                continue;
+            if (!want_stop && xr) {
+                const uint32_t sl = __hip_atomic_load(&ch.xslot[t], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                const bool staged = sl < kXSlots;
+                if (seg_crossing(load, n, ch.rec[t], xr + static_cast<size_t>(t) * kXinWords,
+                                 staged ? ch.xw[sl] : nullptr, staged ? ch.xt[sl] : nullptr, k0, k1, S)) {
+                    ++t;
+                    continue;
+                }
             }
             uint32_t at = k1;
             S = wave_seg_sum(load, n, k0, k1, S, thr, want_stop, &at);
@@ -1166,11 +1189,54 @@ __device__ float seg_row_sum(Load load, Term term, uint32_t n, const SegRec* rec
                              uint32_t* stop_at, const uint32_t* xr, SeqShared& sh, ChainShared& ch) {
     const uint32_t nseg = seg_count(n);
     const SegHead h = *hd;  // the same value in every thread; requested with the records
-    for (uint32_t i = threadIdx.x; i < nseg; i += blockDim.x) ch.rec[i] = rec[i];
+    for (uint32_t i = threadIdx.x; i < nseg; i += blockDim.x) {
+        ch.rec[i] = rec[i];
+        ch.xslot[i] = kNoSlot;
+    }
     __syncthreads();
     if (stop_at && h.stop < min(n, kSegHead)) {
         *stop_at = h.stop;
         return h.S;
+    }
+    if (!stop_at && xr && threadIdx.x >= 64) {
+        // waves 1 .. stage the first kXSlots segments with crossing data, in segment order, slot
+        // q by wave 1 + q % (waves - 1): the words and the terms into LDS, then (release) the
+        // slot number into xslot, which the walk reads (acquire) at a crossing. Nothing waits:
+        // a crossing the walk reaches before its slot is published goes to memory instead.
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        const uint32_t stagers = blockDim.x / 64 - 1;
+        uint32_t q = 0;
+        for (uint32_t base = 0; base < nseg && q < kXSlots; base += 64) {
+            const uint32_t i = base + static_cast<uint32_t>(lane);
+            const uint64_t cm = __ballot(i < nseg && (ch.rec[i].xl & 1u));
+            uint64_t m = cm;
+            while (m != 0 && q < kXSlots) {
+                const int b = __ffsll(static_cast<long long>(m)) - 1;
+                m &= m - 1;
+                const uint32_t t = base + static_cast<uint32_t>(b);
+                if (q % stagers == static_cast<uint32_t>(wave - 1)) {
+                    const uint32_t* x = xr + static_cast<size_t>(t) * kXinWords;
+                    const uint32_t k0 = kSegHead + t * kSegLen, k1 = min(n, k0 + kSegLen);
+                    const uint32_t j0 = k0 + static_cast<uint32_t>(lane) * kSegPer;
+                    const uint32_t w0 = x[lane], w1 = x[64 + lane];
+                    float a[kSegPer];
+                    if (j0 < ((n + 15u) & ~15u)) {
+                        load(j0, a);
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < kSegPer; ++r) a[r] = 0.0f;
+                    }
+                    ch.xw[q][lane] = w0;
+                    ch.xw[q][64 + lane] = w1;
+#pragma unroll
+                    for (int r = 0; r < kSegPer; ++r) ch.xt[q][lane * kSegPer + r] = j0 + r < k1 ? a[r] : 0.0f;
+                    __builtin_amdgcn_wave_barrier();
+                    if (lane == 0)
+                        __hip_atomic_store(&ch.xslot[t], q, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                }
+                ++q;
+            }
+        }
     }
     return seg_chain(load, term, n, h.S, thr, stop_at, xr, sh, ch);
 }
@@ -1622,7 +1688,8 @@ int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab
     // Inside the draft chain's launches (records in draft_max_kernel's grid, merges in
     // seg_sum_kernel's) when the selector holds the rows' records and no shortlist is longer
     // than 256; otherwise the selector's launches run on the side stream beside the chain and
-    // join it before seg_residual_kernel.
+    // join it before seg_residual_kernel. (A fork and a join cost more host time per call than
+    // the merges take on the GPU.)
     const SelectScratch& ss = sel->scratch;
     const uint32_t waves = (vocab + kSampleWaveRows - 1) / kSampleWaveRows;
     bool fused = ss.wkey != nullptr && waves <= ss.wave_cap && waves <= kSampleMaxWaves;
