@@ -32,8 +32,8 @@ struct SelCommon {
     uint32_t redu[kMaxWaves];
     uint64_t top[kMaxWant];     // selected ranks
     uint64_t sorted[kMaxWant];  // the same, in descending order
-    double e[kMaxWant];         // exp(l - max) / total
-    double q[kMaxWant];         // exp((l - max) / T), then the running sum
+    alignas(16) double e[kMaxWant];  // exp(l - max) / total
+    alignas(16) double q[kMaxWant];  // exp((l - max) / T), then the running sum
     double exp2_tbl[64];        // 2^(j/64), for the row sum's exponentials
     float gmax;
     double total;
@@ -330,27 +330,36 @@ __device__ __forceinline__ void block_sort_desc(SelCommon& c, uint32_t n) {
 
 // Steps 5-7 of sample_token on the sorted shortlist c.sorted[0..want) (sampling.cpp:139-168).
 // Every thread i < want computes its two terms as the reference does: e_i = exp(l_i - max) /
-// total (top-p, at T = 1) and q_i = exp((l_i - max) / T). The two sequential double sums then run
-// in reference order on two lanes of wave 0, one v_add per term for both: lane 0 forms the
+// total (top-p, at T = 1) and q_i = exp((l_i - max) / T); threads want .. want rounded up to
+// kChunk write zeros, which leave a running sum unchanged. The two sequential double sums then
+// run in reference order on two lanes of wave 0, one v_add per term for both: lane 0 forms the
 // running sums acc_i of q (stored back), lane 1 the top-p running sum, kChunk terms at a time,
-// until lane 1's sum reaches p (the cut). denom is acc at the cut (the additions of the
-// reference's denom loop), and the draw -- the first i < cut with acc_i >= u * denom, else
-// cut - 1 -- is a ballot over the stored sums in wave 0. Needs want <= blockDim.x. gmax and total
-// are the row's maximum and sum of exponentials, the same in every thread. The id is returned to
-// the threads of wave 0 (callers store it from thread 0).
+// until lane 1's sum reaches p (the cut). The sums of non-negative terms never decrease, so a
+// chunk holds the cut exactly when its last sum reaches p: one compare per chunk, then the
+// chunk's own compares find the term. Both lanes issue every instruction of a full wave, so
+// the loop is held to the sums' adds, 16-byte LDS accesses and that one compare. denom is acc
+// at the cut (the additions of the reference's denom loop), and the draw -- the first i < cut
+// with acc_i >= u * denom, else cut - 1 -- is a ballot over the stored sums in wave 0. Needs
+// want <= blockDim.x and c.e, c.q 16-byte aligned. gmax and total are the row's maximum and sum
+// of exponentials, the same in every thread. The id is returned to the threads of wave 0
+// (callers store it from thread 0).
 __device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, const twd_row_params& p,
                                                    float gmax, double total) {
     const int tid = threadIdx.x, lane = tid & 63;
     const double mx = static_cast<double>(gmax);
     const double td = static_cast<double>(p.temperature);
+    constexpr uint32_t kChunk = 16;
+    const uint32_t padded = (want + kChunk - 1) & ~(kChunk - 1);  // <= kMaxWant
     if (static_cast<uint32_t>(tid) < want) {
         const double l = static_cast<double>(rank_value(c.sorted[tid]));
         c.e[tid] = exp_libm(l - mx) / total;
         c.q[tid] = exp_libm((l - mx) / td);
+    } else if (static_cast<uint32_t>(tid) < padded) {
+        c.e[tid] = 0.0;
+        c.q[tid] = 0.0;
     }
     __syncthreads();
     if (tid >= 64) return 0;
-    constexpr uint32_t kChunk = 16;
     const bool topp = p.top_p < 1.0f;
     const double pp = static_cast<double>(p.top_p);
     uint32_t cut = want;
@@ -359,37 +368,44 @@ __device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, 
         // (unused) over e, so that no store needs a branch
         double* src = lane == 0 ? c.q : c.e;
         double run = 0.0;
-        double x[kChunk];
+        auto load = [&](double (&x)[kChunk], uint32_t i0) {
+            const double2* s2 = reinterpret_cast<const double2*>(src + i0);
 #pragma unroll
-        for (uint32_t j = 0; j < kChunk; ++j) x[j] = src[min(j, want - 1)];
-        for (uint32_t i0 = 0; i0 < want; i0 += kChunk) {
-            // the next chunk's terms are read before this chunk's sums are stored: they lie at
-            // i0 + kChunk or later (want - 1 >= i0 + kChunk when there is a next chunk)
-            double xn[kChunk], pre[kChunk];
-            if (i0 + kChunk < want) {
-#pragma unroll
-                for (uint32_t j = 0; j < kChunk; ++j) xn[j] = src[min(i0 + kChunk + j, want - 1)];
+            for (uint32_t j = 0; j < kChunk / 2; ++j) {
+                const double2 v = s2[j];
+                x[2 * j] = v.x;
+                x[2 * j + 1] = v.y;
             }
+        };
+        // the running sums of chunk i0, stored over its terms; true when it holds the cut
+        auto step = [&](const double (&x)[kChunk], uint32_t i0) -> bool {
+            double pre[kChunk];
 #pragma unroll
             for (uint32_t j = 0; j < kChunk; ++j) {
                 run += x[j];
                 pre[j] = run;
             }
+            double2* d2 = reinterpret_cast<double2*>(src + i0);
+#pragma unroll
+            for (uint32_t j = 0; j < kChunk / 2; ++j) d2[j] = make_double2(pre[2 * j], pre[2 * j + 1]);
+            // lane 1's sums decide; past want they repeat the sum at want - 1
+            if (!topp || __builtin_amdgcn_readlane(pre[kChunk - 1] >= pp ? 1u : 0u, 1) == 0) return false;
             uint32_t hit = 0;
 #pragma unroll
-            for (uint32_t j = 0; j < kChunk; ++j) {
-                src[i0 + j] = pre[j];  // i0 + j < want rounded up to kChunk <= kMaxWant
-                hit |= (pre[j] >= pp ? 1u : 0u) << j;
-            }
-            // lane 1's sums decide; entries past want repeat the last term and never count
-            uint32_t h1 = __builtin_amdgcn_readlane(hit, 1);
-            h1 &= want - i0 >= kChunk ? 0xFFFFu : ((1u << (want - i0)) - 1u);
-            if (topp && h1 != 0) {  // lane 0's sums cover the cut
-                cut = i0 + static_cast<uint32_t>(__builtin_ctz(h1)) + 1;
-                break;
-            }
-#pragma unroll
-            for (uint32_t j = 0; j < kChunk; ++j) x[j] = xn[j];
+            for (uint32_t j = 0; j < kChunk; ++j) hit |= (pre[j] >= pp ? 1u : 0u) << j;
+            const uint32_t h1 = __builtin_amdgcn_readlane(hit, 1);
+            cut = i0 + static_cast<uint32_t>(__builtin_ctz(h1)) + 1;  // h1 != 0: its top bit is set
+            return true;
+        };
+        // two chunks in flight: the next chunk's terms are read before this chunk's sums are
+        // stored (it lies at i0 + kChunk, below padded when i0 + kChunk < want)
+        double xa[kChunk], xb[kChunk];
+        load(xa, 0);
+        for (uint32_t i0 = 0; i0 < want; i0 += 2 * kChunk) {
+            if (i0 + kChunk < want) load(xb, i0 + kChunk);
+            if (step(xa, i0) || i0 + kChunk >= want) break;
+            if (i0 + 2 * kChunk < want) load(xa, i0 + 2 * kChunk);
+            if (step(xb, i0 + kChunk)) break;
         }
     }
     cut = __builtin_amdgcn_readfirstlane(cut);
