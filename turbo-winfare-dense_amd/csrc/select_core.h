@@ -175,6 +175,35 @@ __device__ __forceinline__ void wave_put(bool pred, uint64_t k, uint32_t* counte
     }
 }
 
+// wave_put for N items per lane: one atomic reserves the wave's slots for all N, handed out in
+// (item, lane) order.
+template <uint32_t N, typename T>
+__device__ __forceinline__ void wave_put_n(const bool (&pred)[N], const T (&k)[N], uint32_t* counter, T* dst,
+                                           uint32_t cap) {
+    uint64_t mask[N];
+    uint32_t total = 0;
+#pragma unroll
+    for (uint32_t q = 0; q < N; ++q) {
+        mask[q] = __ballot(pred[q]);
+        total += static_cast<uint32_t>(__popcll(mask[q]));
+    }
+    if (total == 0) return;
+    const int lane = threadIdx.x & 63;
+    const int leader = __ffsll(static_cast<long long>(__ballot(true))) - 1;
+    uint32_t base = 0;
+    if (lane == leader) base = atomicAdd(counter, total);
+    base = __builtin_amdgcn_readlane(base, leader);
+#pragma unroll
+    for (uint32_t q = 0; q < N; ++q) {
+        if (pred[q]) {
+            const uint32_t at = base + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask[q] >> 32),
+                                                                 __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask[q]), 0u));
+            if (at < cap) dst[at] = k[q];
+        }
+        base += static_cast<uint32_t>(__popcll(mask[q]));
+    }
+}
+
 // The block's top-`want` ranks (value desc, index asc), appended to out[0..want) in no
 // particular order; every thread returns once out is complete, with c.misc[4] holding how
 // many were found (want, unless fewer entries carry a rank). Entry e < per (per <= PER, the
@@ -230,12 +259,7 @@ __device__ __forceinline__ void block_top(ValAt val_at, KeyAt key_at, SlowVal sl
                 cc[j] = a.x + a.y + a.z + a.w + b2.x + b2.y + b2.z + b2.w;
                 t += cc[j];
             }
-            uint32_t x = t;  // inclusive prefix sum over lanes <= lane
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const uint32_t y = __shfl_up(x, off);
-                if (lane >= off) x += y;
-            }
+            const uint32_t x = wave_incl_scan_u32(t);  // over lanes <= lane
             uint32_t before = x - t;
             if (lane == 63) {
                 c.misc[0] = kBins;  // no boundary: fewer ranked entries than want
@@ -456,7 +480,10 @@ constexpr uint32_t kSmMaxCand = 2048; // candidate waves listed in LDS
 // and c.exp2_tbl loaded, both published by the barriers inside. `degenerate` (the same in every
 // thread, which then return together) marks a row whose total is NaN or not > 0
 // (sampling.cpp:116-118). Every caller runs this code, so rows finished by different kernels
-// see the same max and total.
+// see the same max and total. With kTotal false the total is left to the caller (records_part,
+// then the waves' sums in order after a barrier of its own), and a row max that is not finite
+// marks the row degenerate here: the reference's total is then NaN (+inf - +inf, or -inf -
+// -inf, in every term), and with a finite max it is at least exp(0) = 1.
 struct RecStats {
     float gm;
     double total;
@@ -472,6 +499,23 @@ __device__ __forceinline__ uint32_t rec_bin(const RecStats& r, float x) {
     return dist < static_cast<float>(kBins - 2) ? static_cast<uint32_t>(dist) : kBins - 2;
 }
 
+// The calling wave's share of the row's sum of exp(l - max): its records' sums rescaled to the
+// row max gm, summed in the thread's record order and then over the wave (wave_reduce's
+// tree); the waves' shares summed in wave order give the row total.
+__device__ __forceinline__ double records_part(const uint64_t (&key)[kSmPer], const double (&wsum)[kSmPer],
+                                               const float (&wm)[kSmPer], float gm, const double* tbl) {
+    double part = 0.0;
+#pragma unroll
+    for (uint32_t q = 0; q < kSmPer; ++q)
+        if (key[q] != 0 && wsum[q] != 0.0) {
+            // exp_core is exp_for_sum's value on [-700, 0] without its special cases
+            const double x = static_cast<double>(wm[q]) - static_cast<double>(gm);
+            part += wsum[q] * (x >= -700.0 ? exp_core(x, tbl) : exp_for_sum(x, tbl));
+        }
+    return wave_reduce(part, 0.0, [](double u, double v) { return u + v; });
+}
+
+template <bool kTotal = true>
 __device__ __forceinline__ RecStats records_stats(const uint64_t (&key)[kSmPer], const double (&wsum)[kSmPer],
                                                   float (&wm)[kSmPer], uint32_t want, TopScratch& t,
                                                   SelCommon& c) {
@@ -489,21 +533,15 @@ __device__ __forceinline__ RecStats records_stats(const uint64_t (&key)[kSmPer],
     }
     block_stats<NT>(flag, gm, mn, c);  // NaN seen, row max, smallest finite wave max
     rs.gm = gm;
-    if (flag != 0) {  // a NaN term makes the total NaN
+    if (flag != 0 || (!kTotal && !__builtin_isfinite(gm))) {  // a NaN term makes the total NaN
         rs.degenerate = true;
         return rs;
     }
-    double part = 0.0;
-#pragma unroll
-    for (uint32_t q = 0; q < kSmPer; ++q)
-        if (key[q] != 0 && wsum[q] != 0.0) {
-            // exp_core is exp_for_sum's value on [-700, 0] without its special cases
-            const double x = static_cast<double>(wm[q]) - static_cast<double>(gm);
-            part += wsum[q] * (x >= -700.0 ? exp_core(x, c.exp2_tbl) : exp_for_sum(x, c.exp2_tbl));
-        }
-    // the waves' partial sums cross the histogram's barrier below (block_sum_f64's order)
-    part = wave_reduce(part, 0.0, [](double u, double v) { return u + v; });
-    if (lane == 0) c.redd[wave] = part;
+    if constexpr (kTotal) {
+        // the waves' partial sums cross the histogram's barrier below (block_sum_f64's order)
+        const double part = records_part(key, wsum, wm, gm, c.exp2_tbl);
+        if (lane == 0) c.redd[wave] = part;
+    }
 
     // ---- b*: bins of distance from the row max (block_top's binning), 8 replicas
     const float span = gm - mn;
@@ -513,13 +551,15 @@ __device__ __forceinline__ RecStats records_stats(const uint64_t (&key)[kSmPer],
     for (uint32_t q = 0; q < kSmPer; ++q)
         if (key[q] != 0) atomicAdd(&t.hist[rec_bin(rs, wm[q]) * kReps + (lane & (kReps - 1))], 1u);
     __syncthreads();
-    double total = 0.0;
+    if constexpr (kTotal) {
+        double total = 0.0;
 #pragma unroll
-    for (int w = 0; w < NT / 64; ++w) total += c.redd[w];
-    rs.total = total;
-    if (!(total > 0.0)) {  // every thread sums the same values
-        rs.degenerate = true;
-        return rs;
+        for (int w = 0; w < NT / 64; ++w) total += c.redd[w];
+        rs.total = total;
+        if (!(total > 0.0)) {  // every thread sums the same values
+            rs.degenerate = true;
+            return rs;
+        }
     }
     if (wave == 0) {  // lane l owns bins 4l .. 4l + 3
         uint32_t cc[4], tsum = 0;
@@ -530,13 +570,7 @@ __device__ __forceinline__ RecStats records_stats(const uint64_t (&key)[kSmPer],
             cc[j] = x.x + x.y + x.z + x.w + y.x + y.y + y.z + y.w;
             tsum += cc[j];
         }
-        uint32_t incl = tsum;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const uint32_t y = __shfl_up(incl, off);
-            if (lane >= off) incl += y;
-        }
-        uint32_t before = incl - tsum;
+        uint32_t before = wave_incl_scan_u32(tsum) - tsum;
         if (lane == 63) c.misc[0] = kBins - 1;  // fewer maxima than want: every bin
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -565,7 +599,8 @@ struct SampleMergeBufs {
 
 struct SampleMergeShared {
     uint32_t cwave[kSmMaxCand];  // the candidate waves
-    uint64_t cand[kSmCap];       // surviving ranks
+    alignas(16) uint64_t cand[kSmCap];  // surviving ranks
+    uint64_t warm[32];           // sink of the loads that bring exp_libm's table into the caches
     TopScratch t;
     SelCommon c;
 };
@@ -592,6 +627,9 @@ __device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32
         key[q] = i < W ? b.st.key[o + i] : 0ull;
         wsum[q] = i < W ? b.st.sum[o + i] : 0.0;
     }
+    // one load per 64-byte line of exp_libm's table, in flight with the records': the finish's
+    // exponentials then find it in the caches
+    if (tid < 32) sh.warm[tid] = kExpTab[8 * tid];
     for (uint32_t i = tid; i < kReps * kBins; i += NT) sh.t.hist[i] = 0;
     if (!(p.temperature > 0.0f)) {  // greedy: the best rank over the waves
         uint64_t k = 0;
@@ -605,32 +643,24 @@ __device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32
                                         : min(kMaxWant, b.vocab);
     if (want > kMaxWant) return;  // a longer shortlist: the long path finishes the row
     float wm[kSmPer];
-    const RecStats rs = records_stats(key, wsum, wm, want, sh.t, sh.c);
+    const RecStats rs = records_stats<false>(key, wsum, wm, want, sh.t, sh.c);
     if (rs.degenerate) {  // sampling.cpp:116-118
         if (tid == 0) b.tokens[row] = TWD_TOKEN_DEGENERATE;
         return;
     }
     const float gm = rs.gm;
-    const double total = rs.total;
     const uint32_t bstar = rs.bstar;
     auto bin_of = [&](float x) -> uint32_t { return rec_bin(rs, x); };
     // the candidate waves, in any order
+    {
+        bool is_cand[kSmPer];
+        uint32_t wid[kSmPer];
 #pragma unroll
-    for (uint32_t q = 0; q < kSmPer; ++q) {
-        const uint32_t i = tid + NT * q;
-        const bool is_cand = key[q] != 0 && bin_of(wm[q]) <= bstar;
-        const uint64_t mask = __ballot(is_cand);
-        if (mask != 0) {
-            const int leader = __ffsll(static_cast<long long>(mask)) - 1;
-            uint32_t base = 0;
-            if (lane == leader) base = atomicAdd(&sh.c.misc[3], static_cast<uint32_t>(__popcll(mask)));
-            base = __builtin_amdgcn_readlane(base, leader);
-            if (is_cand) {
-                const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
-                                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
-                if (base + below < kSmMaxCand) sh.cwave[base + below] = i;
-            }
+        for (uint32_t q = 0; q < kSmPer; ++q) {
+            is_cand[q] = key[q] != 0 && bin_of(wm[q]) <= bstar;
+            wid[q] = tid + NT * q;
         }
+        wave_put_n(is_cand, wid, &sh.c.misc[3], sh.cwave, kSmMaxCand);
     }
     __syncthreads();
     const uint32_t ncw = sh.c.misc[3];
@@ -651,30 +681,57 @@ __device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32
     float smn = INFINITY;
     constexpr uint32_t kGatherBatch = 8;
     const uint32_t per = (nent + NT - 1) / NT;
-    for (uint32_t i0 = 0; i0 < per; i0 += kGatherBatch) {
-        float v[kGatherBatch];
-        uint32_t r[kGatherBatch];
+    float v[kGatherBatch];
+    uint32_t r[kGatherBatch];
+    // the batch's list reads first, then its loads back to back (an entry past the list or the
+    // vocabulary loads entry 0 and is dropped)
+    auto issue = [&](uint32_t i0) {
+        uint32_t w[kGatherBatch];
 #pragma unroll
         for (uint32_t q = 0; q < kGatherBatch; ++q) {
             const uint32_t f = (i0 + q) * NT + static_cast<uint32_t>(tid);
-            r[q] = 0xFFFFFFFFu;
-            v[q] = 0.0f;
-            if (i0 + q < per && f < nent) {
-                const uint32_t rr = entry_row(f);
-                if (rr < b.vocab) {
-                    r[q] = rr;
-                    v[q] = lg[rr];
-                }
-            }
+            const uint32_t slot = min(f / kSampleWaveRows, kSmMaxCand - 1);
+            w[q] = all_waves ? f / kSampleWaveRows : sh.cwave[slot];
         }
 #pragma unroll
         for (uint32_t q = 0; q < kGatherBatch; ++q) {
-            const bool keep = r[q] != 0xFFFFFFFFu && bin_of(v[q]) <= bstar;
-            if (keep && __builtin_isfinite(v[q])) smn = fminf(smn, v[q]);
-            wave_put(keep, keep ? rank_key(v[q], r[q]) : 0ull, &sh.c.misc[4], sh.cand, kSmCap);
+            const uint32_t f = (i0 + q) * NT + static_cast<uint32_t>(tid);
+            const uint32_t rr = w[q] * kSampleWaveRows + f % kSampleWaveRows;
+            const bool ok = i0 + q < per && f < nent && rr < b.vocab;
+            r[q] = ok ? rr : 0xFFFFFFFFu;
+            v[q] = lg[ok ? rr : 0u];
         }
+    };
+    auto consume = [&]() {
+        bool keep[kGatherBatch];
+        uint64_t kk[kGatherBatch];
+#pragma unroll
+        for (uint32_t q = 0; q < kGatherBatch; ++q) {
+            keep[q] = r[q] != 0xFFFFFFFFu && bin_of(v[q]) <= bstar;
+            if (keep[q] && __builtin_isfinite(v[q])) smn = fminf(smn, v[q]);
+            kk[q] = keep[q] ? rank_key(v[q], r[q]) : 0ull;
+        }
+        wave_put_n(keep, kk, &sh.c.misc[4], sh.cand, kSmCap);
+    };
+    issue(0);
+    // the row total's terms while the first loads are in flight (the empty asm keeps the loads
+    // ahead of them); the barrier below publishes the waves' shares
+    __asm__ volatile("" ::: "memory");
+    const double part = records_part(key, wsum, wm, gm, sh.c.exp2_tbl);
+    if (lane == 0) sh.c.redd[wave] = part;
+    consume();
+    for (uint32_t i0 = kGatherBatch; i0 < per; i0 += kGatherBatch) {
+        issue(i0);
+        consume();
     }
     __syncthreads();                  // the survivors are listed
+    double total = 0.0;               // block_sum_f64's order
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) total += sh.c.redd[w];
+    if (!(total > 0.0)) {  // sampling.cpp:116-118; every thread sums the same values
+        if (tid == 0) b.tokens[row] = TWD_TOKEN_DEGENERATE;
+        return;
+    }
     const uint32_t n = sh.c.misc[4];  // may exceed kSmCap: then only counted
     if (n > static_cast<uint32_t>(NT)) {  // block_top needs the survivors' smallest finite value
         uint32_t no_flag = 0;
@@ -683,7 +740,23 @@ __device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32
     }
 
     // ---- the shortlist, sorted (value desc, index asc)
-    if (n <= static_cast<uint32_t>(NT)) {
+    if (n <= static_cast<uint32_t>(NT / 4)) {
+        // four lanes per survivor, each counting the larger ranks over every fourth pair of the
+        // list (pair reads may take the slot at n, past the survivors: it is not counted)
+        const uint32_t sv = static_cast<uint32_t>(tid) >> 2, part = static_cast<uint32_t>(tid) & 3;
+        const uint64_t k = sv < n ? sh.cand[sv] : 0ull;
+        const ulonglong2* c2 = reinterpret_cast<const ulonglong2*>(sh.cand);
+        uint32_t higher = 0;
+        for (uint32_t pi = part; 2 * pi < n; pi += 4) {
+            const ulonglong2 x = c2[pi];
+            higher += x.x > k ? 1u : 0u;
+            higher += (2 * pi + 1 < n && x.y > k) ? 1u : 0u;
+        }
+        higher += dpp_move<0xB1>(0u, higher);  // quad_perm [1,0,3,2]
+        higher += dpp_move<0x4E>(0u, higher);  // quad_perm [2,3,0,1]
+        if (sv < n && part == 0 && higher < want) sh.c.sorted[higher] = k;
+        __syncthreads();
+    } else if (n <= static_cast<uint32_t>(NT)) {
         if (static_cast<uint32_t>(tid) < n) {
             const uint64_t k = sh.cand[tid];
             uint32_t higher = 0;

@@ -122,6 +122,20 @@ __device__ __forceinline__ T wave_reduce(T v, T ident, Op op) {
     return readlane63(v);
 }
 
+// Inclusive prefix sum over the lanes of a full wave (every lane active): row_shr:1, 2, 4, 8
+// inside each row of 16 lanes (lanes without a source add 0), then row_bcast:15 adds row 0's
+// total to row 1 and row 2's to row 3, and row_bcast:31 adds rows 0-1's total to rows 2 and 3.
+// Register moves only, where a shuffle is an LDS round trip per step.
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t x) {
+    x += dpp_move<0x111>(0u, x);
+    x += dpp_move<0x112>(0u, x);
+    x += dpp_move<0x114>(0u, x);
+    x += dpp_move<0x118>(0u, x);
+    x += dpp_move<0x142, 0xA>(0u, x);
+    x += dpp_move<0x143, 0xC>(0u, x);
+    return x;
+}
+
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return wave_reduce(v, uint64_t{0}, [](uint64_t a, uint64_t b) { return a > b ? a : b; });
 }
