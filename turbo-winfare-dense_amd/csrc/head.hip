@@ -381,6 +381,7 @@ __device__ __forceinline__ void head_epilogue_sample(const HeadArgs& a, f32x4_t 
             const size_t o = static_cast<size_t>(m) * (gridDim.x * NW) + blockIdx.x * NW + (threadIdx.x >> 6);
             a.stats.key[o] = best;
             a.stats.sum[o] = sum;
+            a.stats.max[o] = nan ? __builtin_nanf("") : wm;
         }
     }
 }
@@ -1602,6 +1603,7 @@ int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
         const size_t n = static_cast<size_t>(kSampleRows) * waves;
         if (e == hipSuccess) e = hipMalloc(&h->stats.key, n * sizeof(uint64_t));
         if (e == hipSuccess) e = hipMalloc(&h->stats.sum, n * sizeof(double));
+        if (e == hipSuccess) e = hipMalloc(&h->stats.max, n * sizeof(float));
     }
     if (e != hipSuccess) {
         twd_head_destroy(h);
@@ -1900,6 +1902,7 @@ TWD_API void twd_head_destroy(twd_head* h) {
     if (h->norm_w) (void)hipFree(h->norm_w);
     if (h->stats.key) (void)hipFree(h->stats.key);
     if (h->stats.sum) (void)hipFree(h->stats.sum);
+    if (h->stats.max) (void)hipFree(h->stats.max);
     order_release(h->order);
     delete h;
 }

@@ -502,7 +502,15 @@ __global__ __launch_bounds__(kLongThreads) void long_gather_kernel(LongArgs args
     for (uint32_t i = tid; i < kReps * kBins; i += NT) sh.t.hist[i] = 0;
     const uint32_t want = min(static_cast<uint32_t>(p.top_k), b.vocab);
     float wm[kSmPer];
-    const RecStats rs = records_stats(key, wsum, wm, want, sh.t, sh.c);
+    bool live[kSmPer];
+    uint32_t nan = 0;
+#pragma unroll
+    for (uint32_t q = 0; q < kSmPer; ++q) {
+        live[q] = key[q] != 0;
+        wm[q] = live[q] ? rank_value(key[q]) : -INFINITY;
+        nan |= wsum[q] != wsum[q] ? 1u : 0u;
+    }
+    const RecStats rs = records_stats(live, wm, nan, wsum, want, sh.t, sh.c);
     if (rs.degenerate) {  // sampling.cpp:116-118
         if (tid == 0) {
             b.tokens[row] = TWD_TOKEN_DEGENERATE;
@@ -971,6 +979,7 @@ int scratch_alloc(SelectScratch* s, uint32_t max_vocab, uint32_t max_rows) {
     const size_t nw = static_cast<size_t>(max_rows) * s->wave_cap;
     if (e == hipSuccess) e = hipMalloc(&s->wkey, nw * sizeof(uint64_t));
     if (e == hipSuccess) e = hipMalloc(&s->wsum, nw * sizeof(double));
+    if (e == hipSuccess) e = hipMalloc(&s->wmax, nw * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&s->gbest, (max_rows + kArriveWords) * sizeof(uint64_t));
     if (e == hipSuccess) e = hipMemset(s->gbest, 0, (max_rows + kArriveWords) * sizeof(uint64_t));
     const uint64_t armed = kFirstEpoch;  // the counter starts armed for the first launch
@@ -997,6 +1006,7 @@ void scratch_free(SelectScratch* s) {
     (void)hipFree(s->verify_tokens);
     (void)hipFree(s->wkey);
     (void)hipFree(s->wsum);
+    (void)hipFree(s->wmax);
     (void)hipFree(s->gbest);
     delete s->epoch;
     if (s->lng) {
@@ -1169,7 +1179,7 @@ int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_
             penalty_hash_kernel<<<rows, kPhThreads, 0, stream>>>(a, pb);
             TWD_HIP(hipGetLastError());
         }
-        const SampleStats st{s.wkey, s.wsum};
+        const SampleStats st{s.wkey, s.wsum, s.wmax};
         WaveStatsBufs wb{logits, stride, vocab, waves,
                          (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && (stride & 3) == 0 ? 1u : 0u, st};
         wave_stats_kernel<1><<<dim3((vocab + kWsEntries - 1) / kWsEntries, rows), kWsThreads, 0, stream>>>(wb);
@@ -1213,7 +1223,7 @@ int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_
         TWD_HIP(hipGetLastError());
     }
     if (any_long) {  // their wave records from the penalised logits, then the long path
-        const SampleStats st{s.wkey, s.wsum};
+        const SampleStats st{s.wkey, s.wsum, s.wmax};
         WaveStatsBufs wb{logits, stride, vocab, waves,
                          (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && (stride & 3) == 0 ? 1u : 0u, st};
         wave_stats_kernel<1><<<dim3((vocab + kWsEntries - 1) / kWsEntries, rows), kWsThreads, 0, stream>>>(wb);

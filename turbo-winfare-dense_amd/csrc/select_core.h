@@ -501,13 +501,14 @@ __device__ __forceinline__ uint32_t rec_bin(const RecStats& r, float x) {
 
 // The calling wave's share of the row's sum of exp(l - max): its records' sums rescaled to the
 // row max gm, summed in the thread's record order and then over the wave (wave_reduce's
-// tree); the waves' shares summed in wave order give the row total.
-__device__ __forceinline__ double records_part(const uint64_t (&key)[kSmPer], const double (&wsum)[kSmPer],
-                                               const float (&wm)[kSmPer], float gm, const double* tbl) {
+// tree); the waves' shares summed in wave order give the row total. A record adds nothing when
+// its sum is 0 (no live entry, every entry -inf, or past the row's records).
+__device__ __forceinline__ double records_part(const double (&wsum)[kSmPer], const float (&wm)[kSmPer], float gm,
+                                               const double* tbl) {
     double part = 0.0;
 #pragma unroll
     for (uint32_t q = 0; q < kSmPer; ++q)
-        if (key[q] != 0 && wsum[q] != 0.0) {
+        if (wsum[q] != 0.0) {
             // exp_core is exp_for_sum's value on [-700, 0] without its special cases
             const double x = static_cast<double>(wm[q]) - static_cast<double>(gm);
             part += wsum[q] * (x >= -700.0 ? exp_core(x, tbl) : exp_for_sum(x, tbl));
@@ -515,21 +516,20 @@ __device__ __forceinline__ double records_part(const uint64_t (&key)[kSmPer], co
     return wave_reduce(part, 0.0, [](double u, double v) { return u + v; });
 }
 
+// The records as records_stats takes them: live[q] for a record that counts among the row's
+// wave maxima, wm[q] its maximum (-inf otherwise), and `flag` set when a record saw a NaN.
 template <bool kTotal = true>
-__device__ __forceinline__ RecStats records_stats(const uint64_t (&key)[kSmPer], const double (&wsum)[kSmPer],
-                                                  float (&wm)[kSmPer], uint32_t want, TopScratch& t,
-                                                  SelCommon& c) {
+__device__ __forceinline__ RecStats records_stats(const bool (&live)[kSmPer], const float (&wm)[kSmPer],
+                                                  uint32_t flag, const double (&wsum)[kSmPer], uint32_t want,
+                                                  TopScratch& t, SelCommon& c) {
     constexpr int NT = kSmThreads;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     RecStats rs{};
-    uint32_t flag = 0;
     float gm = -INFINITY, mn = INFINITY;
 #pragma unroll
     for (uint32_t q = 0; q < kSmPer; ++q) {
-        wm[q] = key[q] != 0 ? rank_value(key[q]) : -INFINITY;
-        if (wsum[q] != wsum[q]) flag = 1;
         gm = fmaxf(gm, wm[q]);
-        if (key[q] != 0 && __builtin_isfinite(wm[q])) mn = fminf(mn, wm[q]);
+        if (live[q] && __builtin_isfinite(wm[q])) mn = fminf(mn, wm[q]);
     }
     block_stats<NT>(flag, gm, mn, c);  // NaN seen, row max, smallest finite wave max
     rs.gm = gm;
@@ -539,7 +539,7 @@ __device__ __forceinline__ RecStats records_stats(const uint64_t (&key)[kSmPer],
     }
     if constexpr (kTotal) {
         // the waves' partial sums cross the histogram's barrier below (block_sum_f64's order)
-        const double part = records_part(key, wsum, wm, gm, c.exp2_tbl);
+        const double part = records_part(wsum, wm, gm, c.exp2_tbl);
         if (lane == 0) c.redd[wave] = part;
     }
 
@@ -549,7 +549,7 @@ __device__ __forceinline__ RecStats records_stats(const uint64_t (&key)[kSmPer],
     rs.scale = rs.binned ? static_cast<float>(kBins - 1) / (span < kBinRange ? span : kBinRange) : 0.0f;
 #pragma unroll
     for (uint32_t q = 0; q < kSmPer; ++q)
-        if (key[q] != 0) atomicAdd(&t.hist[rec_bin(rs, wm[q]) * kReps + (lane & (kReps - 1))], 1u);
+        if (live[q]) atomicAdd(&t.hist[rec_bin(rs, wm[q]) * kReps + (lane & (kReps - 1))], 1u);
     __syncthreads();
     if constexpr (kTotal) {
         double total = 0.0;
@@ -618,20 +618,14 @@ __device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32
 
     // the exp2 table first, so that its load overlaps the records' (the first barrier publishes it)
     if (tid < 64) sh.c.exp2_tbl[tid] = kExp2Table[tid];
-    // ---- the wave records, one round trip: thread tid holds waves tid + NT * q
-    uint64_t key[kSmPer];
-    double wsum[kSmPer];
-#pragma unroll
-    for (uint32_t q = 0; q < kSmPer; ++q) {
-        const uint32_t i = tid + NT * q;
-        key[q] = i < W ? b.st.key[o + i] : 0ull;
-        wsum[q] = i < W ? b.st.sum[o + i] : 0.0;
-    }
-    // one load per 64-byte line of exp_libm's table, in flight with the records': the finish's
-    // exponentials then find it in the caches
-    if (tid < 32) sh.warm[tid] = kExpTab[8 * tid];
-    for (uint32_t i = tid; i < kReps * kBins; i += NT) sh.t.hist[i] = 0;
+    // ---- the wave records: thread tid holds waves tid + NT * q
     if (!(p.temperature > 0.0f)) {  // greedy: the best rank over the waves
+        uint64_t key[kSmPer];
+#pragma unroll
+        for (uint32_t q = 0; q < kSmPer; ++q) {
+            const uint32_t i = tid + NT * q;
+            key[q] = i < W ? b.st.key[o + i] : 0ull;
+        }
         uint64_t k = 0;
 #pragma unroll
         for (uint32_t q = 0; q < kSmPer; ++q) k = key[q] > k ? key[q] : k;
@@ -642,8 +636,33 @@ __device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32
     const uint32_t want = (p.top_k > 0) ? min(static_cast<uint32_t>(p.top_k), b.vocab)
                                         : min(kMaxWant, b.vocab);
     if (want > kMaxWant) return;  // a longer shortlist: the long path finishes the row
+    // Sampled: the records' maxima first (4 bytes each: the row max, the bins and the
+    // candidates need nothing else), then their sums, which arrive while the maxima are binned
+    // and are first used by the row total. A record of the grid whose waves had no live entry
+    // counts as a -inf maximum: -inf maxima land in the last bin, which every entry's bin is at
+    // most, so they change neither b* nor the survivors, and their rows are past the vocabulary.
     float wm[kSmPer];
-    const RecStats rs = records_stats<false>(key, wsum, wm, want, sh.t, sh.c);
+    double wsum[kSmPer];
+    bool live[kSmPer];
+#pragma unroll
+    for (uint32_t q = 0; q < kSmPer; ++q) {
+        const uint32_t i = tid + NT * q;
+        live[q] = i < W;
+        wm[q] = live[q] ? b.st.max[o + i] : -INFINITY;
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < kSmPer; ++q) {
+        const uint32_t i = tid + NT * q;
+        wsum[q] = i < W ? b.st.sum[o + i] : 0.0;
+    }
+    // one load per 64-byte line of exp_libm's table, in flight with the records': the finish's
+    // exponentials then find it in the caches
+    if (tid < 32) sh.warm[tid] = kExpTab[8 * tid];
+    for (uint32_t i = tid; i < kReps * kBins; i += NT) sh.t.hist[i] = 0;
+    uint32_t nan = 0;
+#pragma unroll
+    for (uint32_t q = 0; q < kSmPer; ++q) nan |= wm[q] != wm[q] ? 1u : 0u;
+    const RecStats rs = records_stats<false>(live, wm, nan, wsum, want, sh.t, sh.c);
     if (rs.degenerate) {  // sampling.cpp:116-118
         if (tid == 0) b.tokens[row] = TWD_TOKEN_DEGENERATE;
         return;
@@ -657,7 +676,7 @@ __device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32
         uint32_t wid[kSmPer];
 #pragma unroll
         for (uint32_t q = 0; q < kSmPer; ++q) {
-            is_cand[q] = key[q] != 0 && bin_of(wm[q]) <= bstar;
+            is_cand[q] = live[q] && bin_of(wm[q]) <= bstar;
             wid[q] = tid + NT * q;
         }
         wave_put_n(is_cand, wid, &sh.c.misc[3], sh.cwave, kSmMaxCand);
@@ -717,7 +736,7 @@ __device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32
     // the row total's terms while the first loads are in flight (the empty asm keeps the loads
     // ahead of them); the barrier below publishes the waves' shares
     __asm__ volatile("" ::: "memory");
-    const double part = records_part(key, wsum, wm, gm, sh.c.exp2_tbl);
+    const double part = records_part(wsum, wm, gm, sh.c.exp2_tbl);
     if (lane == 0) sh.c.redd[wave] = part;
     consume();
     for (uint32_t i0 = kGatherBatch; i0 < per; i0 += kGatherBatch) {
@@ -884,6 +903,7 @@ __device__ __forceinline__ void wave_records_block(const WaveStatsBufs& b, uint3
                     const size_t o = static_cast<size_t>(row) * b.waves + w;
                     b.st.key[o] = best;
                     b.st.sum[o] = sum;
+                    b.st.max[o] = wm;
                 }
                 continue;
             }
@@ -919,6 +939,7 @@ __device__ __forceinline__ void wave_records_block(const WaveStatsBufs& b, uint3
             const size_t o = static_cast<size_t>(row) * b.waves + w;
             b.st.key[o] = best;
             b.st.sum[o] = sum;
+            b.st.max[o] = nan ? __builtin_nanf("") : wm;
         }
     }
 }

@@ -320,6 +320,8 @@ void order_release(StreamOrder& o);
 struct SampleStats {
     uint64_t* key;  // best rank (value desc, index asc) of the wave's rows (0: none live)
     double* sum;    // sum of exp(v - best value) over them in double; NaN when a NaN was seen
+    float* max;     // the best rank's value (-inf: none live, or every one -inf); NaN when a NaN
+                    // was seen. The merge of a sampled row reads these 4 bytes per record first.
 };
 constexpr uint32_t kSampleMaxWaves = 8192;  // waves a fused sample pass may have
 constexpr uint32_t kSampleWaveRows = 64;    // vocabulary rows per wave
@@ -369,6 +371,7 @@ struct SelectScratch {
     uint32_t wave_cap = 0;              // wave records per row (0: no wave-record path)
     uint64_t* wkey = nullptr;           // [rows][wave_cap] best rank per 64 entries
     double* wsum = nullptr;             // [rows][wave_cap] sum of exp(v - best value)
+    float* wmax = nullptr;              // [rows][wave_cap] best value (NaN: a NaN seen)
     // one-pass greedy launches: per-row best ranks (zero between launches), the arrival counter
     // {arrivals, epoch} and its fallback word, and the host's epoch of the last such launch
     uint64_t* gbest = nullptr;          // [max_rows]
