@@ -71,7 +71,9 @@ __device__ __forceinline__ double block_sum_f64(double v, SelCommon& c) {
 }
 
 // One exchange for three block reductions: OR of the NaN flags, max and min (NaN-ignoring).
-template <int NT>
+// kReuse false: the caller passes another barrier before c.redu/redf/redf2 are written again,
+// so the trailing barrier that protects them is left out.
+template <int NT, bool kReuse = true>
 __device__ __forceinline__ void block_stats(uint32_t& flag, float& mx, float& mn, SelCommon& c) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     flag = wave_reduce(flag, 0u, [](uint32_t a, uint32_t b) { return a | b; });
@@ -91,7 +93,7 @@ __device__ __forceinline__ void block_stats(uint32_t& flag, float& mx, float& mn
         mx = fmaxf(mx, c.redf[w]);
         mn = fminf(mn, c.redf2[w]);
     }
-    __syncthreads();
+    if constexpr (kReuse) __syncthreads();
 }
 
 // The smallest rank T with exactly `want` of the block's ranks >= T (ranks are distinct; rank
@@ -367,22 +369,43 @@ __device__ __forceinline__ void block_sort_desc(SelCommon& c, uint32_t n) {
 // want <= blockDim.x and c.e, c.q 16-byte aligned. gmax and total are the row's maximum and sum
 // of exponentials, the same in every thread. The id is returned to the threads of wave 0
 // (callers store it from thread 0).
-__device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, const twd_row_params& p,
-                                                   float gmax, double total) {
-    const int tid = threadIdx.x, lane = tid & 63;
+constexpr uint32_t kFinishChunk = 16;  // terms per step of the sequential sums
+
+// The two terms of shortlist entry i (rank k) as the reference forms them (sampling.cpp:145,157).
+__device__ __forceinline__ void shortlist_terms(SelCommon& c, uint32_t i, uint64_t k, float gmax, double total,
+                                                const twd_row_params& p) {
     const double mx = static_cast<double>(gmax);
-    const double td = static_cast<double>(p.temperature);
-    constexpr uint32_t kChunk = 16;
-    const uint32_t padded = (want + kChunk - 1) & ~(kChunk - 1);  // <= kMaxWant
-    if (static_cast<uint32_t>(tid) < want) {
-        const double l = static_cast<double>(rank_value(c.sorted[tid]));
-        c.e[tid] = exp_libm(l - mx) / total;
-        c.q[tid] = exp_libm((l - mx) / td);
-    } else if (static_cast<uint32_t>(tid) < padded) {
+    const double l = static_cast<double>(rank_value(k));
+    c.e[i] = exp_libm(l - mx) / total;
+    c.q[i] = exp_libm((l - mx) / static_cast<double>(p.temperature));
+}
+
+// Zero terms past the shortlist, up to the sums' next whole chunk: they leave a running sum
+// unchanged.
+__device__ __forceinline__ void shortlist_pad(SelCommon& c, uint32_t want) {
+    const uint32_t tid = threadIdx.x;
+    const uint32_t padded = (want + kFinishChunk - 1) & ~(kFinishChunk - 1);  // <= kMaxWant
+    if (tid >= want && tid < padded) {
         c.e[tid] = 0.0;
         c.q[tid] = 0.0;
     }
+}
+
+__device__ __forceinline__ uint32_t finish_sums(SelCommon& c, uint32_t want, const twd_row_params& p);
+
+__device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, const twd_row_params& p,
+                                                   float gmax, double total) {
+    const uint32_t tid = threadIdx.x;
+    if (tid < want) shortlist_terms(c, tid, c.sorted[tid], gmax, total, p);
+    shortlist_pad(c, want);
     __syncthreads();
+    return finish_sums(c, want, p);
+}
+
+// Steps 5-7 after the terms c.e[0..want), c.q[0..want) (zero-padded) have been published.
+__device__ __forceinline__ uint32_t finish_sums(SelCommon& c, uint32_t want, const twd_row_params& p) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    constexpr uint32_t kChunk = kFinishChunk;
     if (tid >= 64) return 0;
     const bool topp = p.top_p < 1.0f;
     const double pp = static_cast<double>(p.top_p);
@@ -531,7 +554,9 @@ __device__ __forceinline__ RecStats records_stats(const bool (&live)[kSmPer], co
         gm = fmaxf(gm, wm[q]);
         if (live[q] && __builtin_isfinite(wm[q])) mn = fminf(mn, wm[q]);
     }
-    block_stats<NT>(flag, gm, mn, c);  // NaN seen, row max, smallest finite wave max
+    // NaN seen, row max, smallest finite wave max; the histogram's barrier below comes before
+    // any reuse of the exchange
+    block_stats<NT, false>(flag, gm, mn, c);
     rs.gm = gm;
     if (flag != 0 || (!kTotal && !__builtin_isfinite(gm))) {  // a NaN term makes the total NaN
         rs.degenerate = true;
@@ -773,8 +798,17 @@ __device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32
         }
         higher += dpp_move<0xB1>(0u, higher);  // quad_perm [1,0,3,2]
         higher += dpp_move<0x4E>(0u, higher);  // quad_perm [2,3,0,1]
-        if (sv < n && part == 0 && higher < want) sh.c.sorted[higher] = k;
+        // the survivor's place in the shortlist, and there its two terms: steps 5-7 then need
+        // only the sums, after one barrier
+        if (sv < n && part == 0 && higher < want) {
+            sh.c.sorted[higher] = k;
+            shortlist_terms(sh.c, higher, k, gm, total, p);
+        }
+        shortlist_pad(sh.c, want);
         __syncthreads();
+        const uint32_t tok = finish_sums(sh.c, want, p);
+        if (tid == 0) b.tokens[row] = tok;
+        return;
     } else if (n <= static_cast<uint32_t>(NT)) {
         if (static_cast<uint32_t>(tid) < n) {
             const uint64_t k = sh.cand[tid];
