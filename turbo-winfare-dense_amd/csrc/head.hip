@@ -324,7 +324,7 @@ __device__ __forceinline__ void head_epilogue_sample(const HeadArgs& a, f32x4_t 
         const uint32_t mm = mlive ? m : 0u;
         const float rp = prm[mm], lim = prm[kSampleRows + mm];
         float v[RT];
-        uint64_t best = 0;
+        uint64_t best = 0, second = 0;
         uint32_t nan = 0;
 #pragma unroll
         for (int j = 0; j < RT; ++j) {
@@ -341,19 +341,20 @@ __device__ __forceinline__ void head_epilogue_sample(const HeadArgs& a, f32x4_t 
             }
             if (live) {
                 a.logits[static_cast<size_t>(m) * a.vocab + r] = x;
-                const uint64_t k = rank_key(x, r);
-                best = k > best ? k : best;
+                top2_insert(best, second, rank_key(x, r));
                 if (x != x) nan = 1;
             }
             v[j] = live ? x : -INFINITY;
         }
-        // the 16 lanes of a row
-#pragma unroll
-        for (int msk = 1; msk < 16; msk <<= 1) {
-            const uint64_t o = shfl_xor_u64(best, msk);
-            best = o > best ? o : best;
-            nan |= __shfl_xor(nan, msk);
-        }
+        // the 16 lanes of a row, one DPP row: its two best ranks and the NaN flag
+        top2_step<0xB1>(best, second);
+        top2_step<0x4E>(best, second);
+        top2_step<0x141>(best, second);
+        top2_step<0x140>(best, second);
+        nan |= dpp_move<0xB1>(nan, nan);
+        nan |= dpp_move<0x4E>(nan, nan);
+        nan |= dpp_move<0x141>(nan, nan);
+        nan |= dpp_move<0x140>(nan, nan);
         // the wave's largest value (exact: the best rank's value, -0 read as +0); a wave of -inf
         // entries adds nothing to the row's sum
         const float wm = best != 0 ? rank_value(best) : -INFINITY;
@@ -382,6 +383,7 @@ __device__ __forceinline__ void head_epilogue_sample(const HeadArgs& a, f32x4_t 
             a.stats.key[o] = best;
             a.stats.sum[o] = sum;
             a.stats.max[o] = nan ? __builtin_nanf("") : wm;
+            a.stats.aux[o] = record_aux(best, second);
         }
     }
 }
@@ -1604,6 +1606,7 @@ int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
         if (e == hipSuccess) e = hipMalloc(&h->stats.key, n * sizeof(uint64_t));
         if (e == hipSuccess) e = hipMalloc(&h->stats.sum, n * sizeof(double));
         if (e == hipSuccess) e = hipMalloc(&h->stats.max, n * sizeof(float));
+        if (e == hipSuccess) e = hipMalloc(&h->stats.aux, n * sizeof(uint32_t));
     }
     if (e != hipSuccess) {
         twd_head_destroy(h);
@@ -1903,6 +1906,7 @@ TWD_API void twd_head_destroy(twd_head* h) {
     if (h->stats.key) (void)hipFree(h->stats.key);
     if (h->stats.sum) (void)hipFree(h->stats.sum);
     if (h->stats.max) (void)hipFree(h->stats.max);
+    if (h->stats.aux) (void)hipFree(h->stats.aux);
     order_release(h->order);
     delete h;
 }

@@ -980,6 +980,7 @@ int scratch_alloc(SelectScratch* s, uint32_t max_vocab, uint32_t max_rows) {
     if (e == hipSuccess) e = hipMalloc(&s->wkey, nw * sizeof(uint64_t));
     if (e == hipSuccess) e = hipMalloc(&s->wsum, nw * sizeof(double));
     if (e == hipSuccess) e = hipMalloc(&s->wmax, nw * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&s->waux, nw * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMalloc(&s->gbest, (max_rows + kArriveWords) * sizeof(uint64_t));
     if (e == hipSuccess) e = hipMemset(s->gbest, 0, (max_rows + kArriveWords) * sizeof(uint64_t));
     const uint64_t armed = kFirstEpoch;  // the counter starts armed for the first launch
@@ -1007,6 +1008,7 @@ void scratch_free(SelectScratch* s) {
     (void)hipFree(s->wkey);
     (void)hipFree(s->wsum);
     (void)hipFree(s->wmax);
+    (void)hipFree(s->waux);
     (void)hipFree(s->gbest);
     delete s->epoch;
     if (s->lng) {
@@ -1179,7 +1181,7 @@ int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_
             penalty_hash_kernel<<<rows, kPhThreads, 0, stream>>>(a, pb);
             TWD_HIP(hipGetLastError());
         }
-        const SampleStats st{s.wkey, s.wsum, s.wmax};
+        const SampleStats st{s.wkey, s.wsum, s.wmax, s.waux};
         WaveStatsBufs wb{logits, stride, vocab, waves,
                          (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && (stride & 3) == 0 ? 1u : 0u, st};
         wave_stats_kernel<1><<<dim3((vocab + kWsEntries - 1) / kWsEntries, rows), kWsThreads, 0, stream>>>(wb);
@@ -1223,7 +1225,7 @@ int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_
         TWD_HIP(hipGetLastError());
     }
     if (any_long) {  // their wave records from the penalised logits, then the long path
-        const SampleStats st{s.wkey, s.wsum, s.wmax};
+        const SampleStats st{s.wkey, s.wsum, s.wmax, s.waux};
         WaveStatsBufs wb{logits, stride, vocab, waves,
                          (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && (stride & 3) == 0 ? 1u : 0u, st};
         wave_stats_kernel<1><<<dim3((vocab + kWsEntries - 1) / kWsEntries, rows), kWsThreads, 0, stream>>>(wb);

@@ -177,6 +177,37 @@ __device__ __forceinline__ void wave_put(bool pred, uint64_t k, uint32_t* counte
     }
 }
 
+// wave_put_n for pairs: item q goes to dst[at] and its companion to dst2[at], one slot for both.
+template <uint32_t N, typename T, typename U>
+__device__ __forceinline__ void wave_put_n2(const bool (&pred)[N], const T (&k)[N], const U (&k2)[N],
+                                            uint32_t* counter, T* dst, U* dst2, uint32_t cap) {
+    uint64_t mask[N];
+    uint32_t total = 0;
+#pragma unroll
+    for (uint32_t q = 0; q < N; ++q) {
+        mask[q] = __ballot(pred[q]);
+        total += static_cast<uint32_t>(__popcll(mask[q]));
+    }
+    if (total == 0) return;
+    const int lane = threadIdx.x & 63;
+    const int leader = __ffsll(static_cast<long long>(__ballot(true))) - 1;
+    uint32_t base = 0;
+    if (lane == leader) base = atomicAdd(counter, total);
+    base = __builtin_amdgcn_readlane(base, leader);
+#pragma unroll
+    for (uint32_t q = 0; q < N; ++q) {
+        if (pred[q]) {
+            const uint32_t at = base + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask[q] >> 32),
+                                                                 __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask[q]), 0u));
+            if (at < cap) {
+                dst[at] = k[q];
+                dst2[at] = k2[q];
+            }
+        }
+        base += static_cast<uint32_t>(__popcll(mask[q]));
+    }
+}
+
 // wave_put for N items per lane: one atomic reserves the wave's slots for all N, handed out in
 // (item, lane) order.
 template <uint32_t N, typename T>
@@ -604,8 +635,9 @@ __device__ __forceinline__ RecStats records_stats(const bool (&live)[kSmPer], co
             before += cc[j];
         }
         if (lane == 0) {
-            c.misc[3] = 0;  // candidate waves
+            c.misc[3] = 0;  // candidate waves read whole
             c.misc[4] = 0;  // survivors
+            c.misc[5] = 0;  // candidate waves with one survivor
         }
     }
     __syncthreads();
@@ -623,7 +655,8 @@ struct SampleMergeBufs {
 };
 
 struct SampleMergeShared {
-    uint32_t cwave[kSmMaxCand];  // the candidate waves
+    uint32_t cwave[kSmMaxCand];   // the candidate waves read whole
+    uint16_t cwave1[kSmMaxCand];  // the candidate waves whose one survivor is their best rank
     alignas(16) uint64_t cand[kSmCap];  // surviving ranks
     uint64_t warm[32];           // sink of the loads that bring exp_libm's table into the caches
     TopScratch t;
@@ -669,11 +702,13 @@ __device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32
     float wm[kSmPer];
     double wsum[kSmPer];
     bool live[kSmPer];
+    uint32_t aux[kSmPer];
 #pragma unroll
     for (uint32_t q = 0; q < kSmPer; ++q) {
         const uint32_t i = tid + NT * q;
         live[q] = i < W;
         wm[q] = live[q] ? b.st.max[o + i] : -INFINITY;
+        aux[q] = live[q] ? b.st.aux[o + i] : 0u;
     }
 #pragma unroll
     for (uint32_t q = 0; q < kSmPer; ++q) {
@@ -695,34 +730,51 @@ __device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32
     const float gm = rs.gm;
     const uint32_t bstar = rs.bstar;
     auto bin_of = [&](float x) -> uint32_t { return rec_bin(rs, x); };
-    // the candidate waves, in any order
+    // The candidate waves, in any order. A record's entries other than its best two ranks rank
+    // below its second, so they lie in bins at least the second's (the bins are monotone): a
+    // candidate whose second (rounded up, which can only lower its bin) lies past b* holds one
+    // survivor, its best rank, rebuilt here from the record's maximum and row; the others are
+    // read whole below. Most rows of a short shortlist then read no logits at all.
+    float smn = INFINITY;  // the survivors' smallest finite value
     {
-        bool is_cand[kSmPer];
+        bool whole[kSmPer], one[kSmPer];
         uint32_t wid[kSmPer];
+        uint16_t wid1[kSmPer];
+        uint64_t bk[kSmPer];
 #pragma unroll
         for (uint32_t q = 0; q < kSmPer; ++q) {
-            is_cand[q] = live[q] && bin_of(wm[q]) <= bstar;
-            wid[q] = tid + NT * q;
+            const uint32_t w = tid + NT * q;
+            const bool cand = live[q] && bin_of(wm[q]) <= bstar;
+            whole[q] = cand && bin_of(fminf(aux_second(aux[q]), gm)) <= bstar;
+            one[q] = cand && !whole[q];
+            wid[q] = w;
+            wid1[q] = static_cast<uint16_t>(w);  // w < kSampleMaxWaves
+            bk[q] = rank_key(wm[q], w * kSampleWaveRows + (aux[q] & 63u));
+            if (one[q] && __builtin_isfinite(wm[q])) smn = fminf(smn, wm[q]);
         }
-        wave_put_n(is_cand, wid, &sh.c.misc[3], sh.cwave, kSmMaxCand);
+        wave_put_n(whole, wid, &sh.c.misc[3], sh.cwave, kSmMaxCand);
+        // the one-survivor waves' best ranks are the first survivors; cwave1[i] is cand[i]'s wave
+        wave_put_n2(one, bk, wid1, &sh.c.misc[5], sh.cand, sh.cwave1, kSmMaxCand);
     }
     __syncthreads();
-    const uint32_t ncw = sh.c.misc[3];
-    if (ncw > kSmMaxCand) {
-        // a candidate list this long only comes from values that barely bin (huge ties): the
-        // two-launch path's kernels are not reachable from here, so rank over every wave
-        if (tid == 0) sh.c.misc[3] = 0;
-        __syncthreads();
-    }
-    const bool all_waves = ncw > kSmMaxCand;
+    const uint32_t ncw = sh.c.misc[3], ncw1 = sh.c.misc[5];
+    // a candidate list this long only comes from values that barely bin (huge ties): the
+    // two-launch path's kernels are not reachable from here, so rank over every wave, its
+    // survivors listed afresh (each best rank is read again with the rest of its wave)
+    const bool all_waves = ncw + ncw1 > kSmMaxCand;
+    if (all_waves) smn = INFINITY;
+    // the gathered survivors follow the best ranks already listed (counted in misc[4] from 0)
+    const uint32_t first = all_waves ? 0u : ncw1;
     const uint32_t nent = all_waves ? W * kSampleWaveRows : ncw * kSampleWaveRows;  // entries to scan
-    auto entry_row = [&](uint32_t f) -> uint32_t {  // row of entry f of the candidate waves
-        const uint32_t w = all_waves ? f / kSampleWaveRows : sh.cwave[f / kSampleWaveRows];
+    // every candidate wave's entries, for the overflow path: the whole ones, then the others
+    const uint32_t nent_all = all_waves ? nent : (ncw + ncw1) * kSampleWaveRows;
+    auto entry_row = [&](uint32_t f) -> uint32_t {
+        const uint32_t s = f / kSampleWaveRows;
+        const uint32_t w = all_waves ? s : (s < ncw ? sh.cwave[s] : static_cast<uint32_t>(sh.cwave1[s - ncw]));
         return w * kSampleWaveRows + f % kSampleWaveRows;
     };
 
-    // ---- survivors: entries in bins <= b* of the candidate waves, kGatherBatch loads at a time
-    float smn = INFINITY;
+    // ---- survivors: entries in bins <= b* of the waves read whole, kGatherBatch loads at a time
     constexpr uint32_t kGatherBatch = 8;
     const uint32_t per = (nent + NT - 1) / NT;
     float v[kGatherBatch];
@@ -755,15 +807,15 @@ __device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32
             if (keep[q] && __builtin_isfinite(v[q])) smn = fminf(smn, v[q]);
             kk[q] = keep[q] ? rank_key(v[q], r[q]) : 0ull;
         }
-        wave_put_n(keep, kk, &sh.c.misc[4], sh.cand, kSmCap);
+        wave_put_n(keep, kk, &sh.c.misc[4], sh.cand + first, kSmCap - first);
     };
-    issue(0);
+    if (per > 0) issue(0);  // per is the same in every thread
     // the row total's terms while the first loads are in flight (the empty asm keeps the loads
     // ahead of them); the barrier below publishes the waves' shares
     __asm__ volatile("" ::: "memory");
     const double part = records_part(wsum, wm, gm, sh.c.exp2_tbl);
     if (lane == 0) sh.c.redd[wave] = part;
-    consume();
+    if (per > 0) consume();
     for (uint32_t i0 = kGatherBatch; i0 < per; i0 += kGatherBatch) {
         issue(i0);
         consume();
@@ -776,7 +828,7 @@ __device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32
         if (tid == 0) b.tokens[row] = TWD_TOKEN_DEGENERATE;
         return;
     }
-    const uint32_t n = sh.c.misc[4];  // may exceed kSmCap: then only counted
+    const uint32_t n = first + sh.c.misc[4];  // may exceed kSmCap: then only counted
     if (n > static_cast<uint32_t>(NT)) {  // block_top needs the survivors' smallest finite value
         uint32_t no_flag = 0;
         float no_max = -INFINITY;
@@ -830,19 +882,20 @@ __device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32
                                    gm, smn, want, sh.c.top, sh.t, sh.c);
         block_sort_desc(sh.c, want);
     } else {
-        // overflow (heavy ties): a radix select over the candidate waves' rows in memory
+        // overflow (heavy ties): a radix select over every candidate wave's rows in memory
+        const uint32_t per_all = (nent_all + NT - 1) / NT;
         auto cand_key = [&](int e) -> uint64_t {
             const uint32_t f = static_cast<uint32_t>(e) * NT + static_cast<uint32_t>(tid);
-            if (f >= nent) return 0ull;
+            if (f >= nent_all) return 0ull;
             const uint32_t rr = entry_row(f);
             if (rr >= b.vocab) return 0ull;
             const float x = lg[rr];
             return bin_of(x) <= bstar ? rank_key(x, rr) : 0ull;
         };
-        const uint64_t thr = block_select<NT, 0>(cand_key, static_cast<int>(per), want, sh.t.hist, sh.c);
+        const uint64_t thr = block_select<NT, 0>(cand_key, static_cast<int>(per_all), want, sh.t.hist, sh.c);
         if (tid == 0) sh.c.misc[4] = 0;
         __syncthreads();
-        for (uint32_t e = 0; e < per; ++e) {
+        for (uint32_t e = 0; e < per_all; ++e) {
             const uint64_t k = cand_key(static_cast<int>(e));
             wave_put(k != 0 && k >= thr, k, &sh.c.misc[4], sh.c.top, want);
         }
@@ -918,12 +971,19 @@ __device__ __forceinline__ void wave_records_block(const WaveStatsBufs& b, uint3
             uint32_t qi = 7;
 #pragma unroll
             for (int q = 6; q >= 0; --q) qi = v[k][q] == hi ? static_cast<uint32_t>(q) : qi;
-            uint64_t best = rank_key(hi, e + qi);
+            // the lane's second: the largest of its other values, at the lowest such index
+            float h2 = -INFINITY;
 #pragma unroll
-            for (int m = 1; m < 8; m <<= 1) {
-                const uint64_t o = shfl_xor_u64(best, m);
-                best = o > best ? o : best;
-            }
+            for (int q = 0; q < 8; ++q) h2 = static_cast<uint32_t>(q) != qi ? fmaxf(h2, v[k][q]) : h2;
+            uint32_t q2 = 7;
+#pragma unroll
+            for (int q = 6; q >= 0; --q)
+                q2 = (static_cast<uint32_t>(q) != qi && v[k][q] == h2) ? static_cast<uint32_t>(q) : q2;
+            uint64_t best = rank_key(hi, e + qi), second = rank_key(h2, e + q2);
+            // the record's 64 entries are the 8 lanes with the same lane >> 3
+            top2_step<0xB1>(best, second);
+            top2_step<0x4E>(best, second);
+            top2_step<0x141>(best, second);
             const float wm = rank_value(best);
             if (__ballot(lo < wm - 700.0f) == 0) {
                 const double dwm = static_cast<double>(wm);
@@ -938,26 +998,26 @@ __device__ __forceinline__ void wave_records_block(const WaveStatsBufs& b, uint3
                     b.st.key[o] = best;
                     b.st.sum[o] = sum;
                     b.st.max[o] = wm;
+                    b.st.aux[o] = record_aux(best, second);
                 }
                 continue;
             }
         }
         // entries past the vocabulary hold -inf and no rank: they add nothing
-        uint64_t best = 0;
+        uint64_t best = 0, second = 0;
         uint32_t nan = 0;
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            const uint64_t key = e + q < b.vocab ? rank_key(v[k][q], e + q) : 0ull;
-            best = key > best ? key : best;
+            top2_insert(best, second, e + q < b.vocab ? rank_key(v[k][q], e + q) : 0ull);
             nan |= v[k][q] != v[k][q] ? 1u : 0u;
         }
         // the record's 64 entries are the 8 lanes with the same lane >> 3
-#pragma unroll
-        for (int m = 1; m < 8; m <<= 1) {
-            const uint64_t o = shfl_xor_u64(best, m);
-            best = o > best ? o : best;
-            nan |= __shfl_xor(nan, m);
-        }
+        top2_step<0xB1>(best, second);
+        top2_step<0x4E>(best, second);
+        top2_step<0x141>(best, second);
+        nan |= dpp_move<0xB1>(nan, nan);
+        nan |= dpp_move<0x4E>(nan, nan);
+        nan |= dpp_move<0x141>(nan, nan);
         // a record of -inf entries only (best value -inf, or no entry) adds nothing
         const float wm = best != 0 ? rank_value(best) : -INFINITY;
         const double dwm = wm != -INFINITY ? static_cast<double>(wm) : 0.0;
@@ -974,6 +1034,7 @@ __device__ __forceinline__ void wave_records_block(const WaveStatsBufs& b, uint3
             b.st.key[o] = best;
             b.st.sum[o] = sum;
             b.st.max[o] = nan ? __builtin_nanf("") : wm;
+            b.st.aux[o] = record_aux(best, second);
         }
     }
 }

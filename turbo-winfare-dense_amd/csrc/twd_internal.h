@@ -93,6 +93,45 @@ __device__ __forceinline__ T dpp_move(T old, T v) {
     }
 }
 
+// The two largest of a set of distinct ranks (0 stands for none). Merging another such pair
+// keeps the larger first, and as second the larger of the smaller first and the larger second.
+__device__ __forceinline__ void top2_merge(uint64_t& b1, uint64_t& b2, uint64_t o1, uint64_t o2) {
+    const uint64_t lo = b1 < o1 ? b1 : o1;
+    const uint64_t hi2 = b2 > o2 ? b2 : o2;
+    b1 = b1 > o1 ? b1 : o1;
+    b2 = lo > hi2 ? lo : hi2;
+}
+
+__device__ __forceinline__ void top2_insert(uint64_t& b1, uint64_t& b2, uint64_t k) { top2_merge(b1, b2, k, 0ull); }
+
+// One exchange of a top-two reduction inside a DPP row, every lane active: CTRL pairs the lanes
+// (quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror, row_mirror), and both lanes of a pair
+// end with the pair's merge (the pairs hold disjoint ranks).
+template <int CTRL>
+__device__ __forceinline__ void top2_step(uint64_t& b1, uint64_t& b2) {
+    const uint64_t o1 = dpp_move<CTRL>(b1, b1), o2 = dpp_move<CTRL>(b2, b2);
+    top2_merge(b1, b2, o1, o2);
+}
+
+// A record's second word: the best rank's row within the record's 64 (bits 0-5), and the
+// second-best rank's value rounded up to bf16 (bits 16-31; -inf when there is none). Rounding up
+// keeps the merge's test conservative: a second value whose bin lies past b* rounds to one that
+// does too only when the exact one does.
+__device__ __forceinline__ uint32_t record_aux(uint64_t best, uint64_t second) {
+    uint32_t up = 0xFF80u;  // -inf
+    if (second != 0) {
+        const float v = rank_value(second);
+        const uint32_t b = __float_as_uint(v);
+        const uint32_t t = b >> 16;  // truncation: toward zero
+        // toward +inf: a positive value with bits below the bf16 cut goes up one bf16 step
+        up = (v > 0.0f && (b & 0xFFFFu) != 0) ? t + 1 : t;
+        if (v != v) up = 0x7FC0u;
+    }
+    return (up << 16) | (rank_index(best) & 63u);
+}
+
+__device__ __forceinline__ float aux_second(uint32_t aux) { return __uint_as_float(aux & 0xFFFF0000u); }
+
 template <typename T>
 __device__ __forceinline__ T readlane63(T v) {
     if constexpr (sizeof(T) == 4) {
@@ -322,6 +361,7 @@ struct SampleStats {
     double* sum;    // sum of exp(v - best value) over them in double; NaN when a NaN was seen
     float* max;     // the best rank's value (-inf: none live, or every one -inf); NaN when a NaN
                     // was seen. The merge of a sampled row reads these 4 bytes per record first.
+    uint32_t* aux;  // record_aux of the best two ranks, read with max
 };
 constexpr uint32_t kSampleMaxWaves = 8192;  // waves a fused sample pass may have
 constexpr uint32_t kSampleWaveRows = 64;    // vocabulary rows per wave
@@ -372,6 +412,7 @@ struct SelectScratch {
     uint64_t* wkey = nullptr;           // [rows][wave_cap] best rank per 64 entries
     double* wsum = nullptr;             // [rows][wave_cap] sum of exp(v - best value)
     float* wmax = nullptr;              // [rows][wave_cap] best value (NaN: a NaN seen)
+    uint32_t* waux = nullptr;           // [rows][wave_cap] record_aux
     // one-pass greedy launches: per-row best ranks (zero between launches), the arrival counter
     // {arrivals, epoch} and its fallback word, and the host's epoch of the last such launch
     uint64_t* gbest = nullptr;          // [max_rows]
