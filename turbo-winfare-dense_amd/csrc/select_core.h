@@ -557,11 +557,12 @@ __device__ __forceinline__ uint32_t rec_bin(const RecStats& r, float x) {
 // row max gm, summed in the thread's record order and then over the wave (wave_reduce's
 // tree); the waves' shares summed in wave order give the row total. A record adds nothing when
 // its sum is 0 (no live entry, every entry -inf, or past the row's records).
-__device__ __forceinline__ double records_part(const double (&wsum)[kSmPer], const float (&wm)[kSmPer], float gm,
+template <uint32_t PER = kSmPer>
+__device__ __forceinline__ double records_part(const double (&wsum)[PER], const float (&wm)[PER], float gm,
                                                const double* tbl) {
     double part = 0.0;
 #pragma unroll
-    for (uint32_t q = 0; q < kSmPer; ++q)
+    for (uint32_t q = 0; q < PER; ++q)
         if (wsum[q] != 0.0) {
             // exp_core is exp_for_sum's value on [-700, 0] without its special cases
             const double x = static_cast<double>(wm[q]) - static_cast<double>(gm);
@@ -572,16 +573,16 @@ __device__ __forceinline__ double records_part(const double (&wsum)[kSmPer], con
 
 // The records as records_stats takes them: live[q] for a record that counts among the row's
 // wave maxima, wm[q] its maximum (-inf otherwise), and `flag` set when a record saw a NaN.
-template <bool kTotal = true>
-__device__ __forceinline__ RecStats records_stats(const bool (&live)[kSmPer], const float (&wm)[kSmPer],
-                                                  uint32_t flag, const double (&wsum)[kSmPer], uint32_t want,
+template <bool kTotal = true, uint32_t PER = kSmPer>
+__device__ __forceinline__ RecStats records_stats(const bool (&live)[PER], const float (&wm)[PER],
+                                                  uint32_t flag, const double (&wsum)[PER], uint32_t want,
                                                   TopScratch& t, SelCommon& c) {
     constexpr int NT = kSmThreads;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     RecStats rs{};
     float gm = -INFINITY, mn = INFINITY;
 #pragma unroll
-    for (uint32_t q = 0; q < kSmPer; ++q) {
+    for (uint32_t q = 0; q < PER; ++q) {
         gm = fmaxf(gm, wm[q]);
         if (live[q] && __builtin_isfinite(wm[q])) mn = fminf(mn, wm[q]);
     }
@@ -595,7 +596,7 @@ __device__ __forceinline__ RecStats records_stats(const bool (&live)[kSmPer], co
     }
     if constexpr (kTotal) {
         // the waves' partial sums cross the histogram's barrier below (block_sum_f64's order)
-        const double part = records_part(wsum, wm, gm, c.exp2_tbl);
+        const double part = records_part<PER>(wsum, wm, gm, c.exp2_tbl);
         if (lane == 0) c.redd[wave] = part;
     }
 
@@ -604,7 +605,7 @@ __device__ __forceinline__ RecStats records_stats(const bool (&live)[kSmPer], co
     rs.binned = __builtin_isfinite(gm) && __builtin_isfinite(mn) && span > 0.0f;
     rs.scale = rs.binned ? static_cast<float>(kBins - 1) / (span < kBinRange ? span : kBinRange) : 0.0f;
 #pragma unroll
-    for (uint32_t q = 0; q < kSmPer; ++q)
+    for (uint32_t q = 0; q < PER; ++q)
         if (live[q]) atomicAdd(&t.hist[rec_bin(rs, wm[q]) * kReps + (lane & (kReps - 1))], 1u);
     __syncthreads();
     if constexpr (kTotal) {
@@ -666,8 +667,9 @@ struct SampleMergeShared {
 // One row of the merge after the wave records (select_sample_merge_kernel's block, kSmThreads
 // threads): sample_token of row `row` with parameters p from its records and its penalised
 // logits (see the kernel's comment). Every thread of the block calls it.
-__device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32_t row, const SampleMergeBufs& b,
-                                                 SampleMergeShared& sh) {
+template <uint32_t PER>
+__device__ __forceinline__ void sample_merge_row_per(const twd_row_params& p, uint32_t row, const SampleMergeBufs& b,
+                                                     SampleMergeShared& sh) {
     constexpr int NT = kSmThreads;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t W = b.waves;
@@ -678,15 +680,15 @@ __device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32
     if (tid < 64) sh.c.exp2_tbl[tid] = kExp2Table[tid];
     // ---- the wave records: thread tid holds waves tid + NT * q
     if (!(p.temperature > 0.0f)) {  // greedy: the best rank over the waves
-        uint64_t key[kSmPer];
+        uint64_t key[PER];
 #pragma unroll
-        for (uint32_t q = 0; q < kSmPer; ++q) {
+        for (uint32_t q = 0; q < PER; ++q) {
             const uint32_t i = tid + NT * q;
             key[q] = i < W ? b.st.key[o + i] : 0ull;
         }
         uint64_t k = 0;
 #pragma unroll
-        for (uint32_t q = 0; q < kSmPer; ++q) k = key[q] > k ? key[q] : k;
+        for (uint32_t q = 0; q < PER; ++q) k = key[q] > k ? key[q] : k;
         k = block_max_u64<NT>(k, sh.c);
         if (tid == 0) b.tokens[row] = rank_index(k);
         return;
@@ -699,19 +701,19 @@ __device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32
     // and are first used by the row total. A record of the grid whose waves had no live entry
     // counts as a -inf maximum: -inf maxima land in the last bin, which every entry's bin is at
     // most, so they change neither b* nor the survivors, and their rows are past the vocabulary.
-    float wm[kSmPer];
-    double wsum[kSmPer];
-    bool live[kSmPer];
-    uint32_t aux[kSmPer];
+    float wm[PER];
+    double wsum[PER];
+    bool live[PER];
+    uint32_t aux[PER];
 #pragma unroll
-    for (uint32_t q = 0; q < kSmPer; ++q) {
+    for (uint32_t q = 0; q < PER; ++q) {
         const uint32_t i = tid + NT * q;
         live[q] = i < W;
         wm[q] = live[q] ? b.st.max[o + i] : -INFINITY;
         aux[q] = live[q] ? b.st.aux[o + i] : 0u;
     }
 #pragma unroll
-    for (uint32_t q = 0; q < kSmPer; ++q) {
+    for (uint32_t q = 0; q < PER; ++q) {
         const uint32_t i = tid + NT * q;
         wsum[q] = i < W ? b.st.sum[o + i] : 0.0;
     }
@@ -721,8 +723,8 @@ __device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32
     for (uint32_t i = tid; i < kReps * kBins; i += NT) sh.t.hist[i] = 0;
     uint32_t nan = 0;
 #pragma unroll
-    for (uint32_t q = 0; q < kSmPer; ++q) nan |= wm[q] != wm[q] ? 1u : 0u;
-    const RecStats rs = records_stats<false>(live, wm, nan, wsum, want, sh.t, sh.c);
+    for (uint32_t q = 0; q < PER; ++q) nan |= wm[q] != wm[q] ? 1u : 0u;
+    const RecStats rs = records_stats<false, PER>(live, wm, nan, wsum, want, sh.t, sh.c);
     if (rs.degenerate) {  // sampling.cpp:116-118
         if (tid == 0) b.tokens[row] = TWD_TOKEN_DEGENERATE;
         return;
@@ -737,12 +739,12 @@ __device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32
     // read whole below. Most rows of a short shortlist then read no logits at all.
     float smn = INFINITY;  // the survivors' smallest finite value
     {
-        bool whole[kSmPer], one[kSmPer];
-        uint32_t wid[kSmPer];
-        uint16_t wid1[kSmPer];
-        uint64_t bk[kSmPer];
+        bool whole[PER], one[PER];
+        uint32_t wid[PER];
+        uint16_t wid1[PER];
+        uint64_t bk[PER];
 #pragma unroll
-        for (uint32_t q = 0; q < kSmPer; ++q) {
+        for (uint32_t q = 0; q < PER; ++q) {
             const uint32_t w = tid + NT * q;
             const bool cand = live[q] && bin_of(wm[q]) <= bstar;
             whole[q] = cand && bin_of(fminf(aux_second(aux[q]), gm)) <= bstar;
@@ -813,7 +815,7 @@ __device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32
     // the row total's terms while the first loads are in flight (the empty asm keeps the loads
     // ahead of them); the barrier below publishes the waves' shares
     __asm__ volatile("" ::: "memory");
-    const double part = records_part(wsum, wm, gm, sh.c.exp2_tbl);
+    const double part = records_part<PER>(wsum, wm, gm, sh.c.exp2_tbl);
     if (lane == 0) sh.c.redd[wave] = part;
     if (per > 0) consume();
     for (uint32_t i0 = kGatherBatch; i0 < per; i0 += kGatherBatch) {
@@ -906,6 +908,15 @@ __device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32
     if (tid == 0) b.tokens[row] = tok;
 }
 
+// One row of the merge: the records per thread sized to the row's record count, so that rows of
+// at most 4,096 records (V <= 262,144) run no code for records that do not exist.
+__device__ __forceinline__ void sample_merge_row(const twd_row_params& p, uint32_t row, const SampleMergeBufs& b,
+                                                 SampleMergeShared& sh) {
+    if (b.waves <= kSmThreads * (kSmPer / 2))
+        sample_merge_row_per<kSmPer / 2>(p, row, b, sh);
+    else
+        sample_merge_row_per<kSmPer>(p, row, b, sh);
+}
 
 // ---- the wave records of logits in memory ------------------------------------------------------------
 //
