@@ -360,7 +360,9 @@ __device__ __forceinline__ void head_epilogue_sample(const HeadArgs& a, f32x4_t 
         const float wm = best != 0 ? rank_value(best) : -INFINITY;
         double sum = 0.0;
         if (wm != -INFINITY) {
-            const double dwm = static_cast<double>(wm);
+            // the sum's reference: the fixed one (the cap, above every value) or the wave's max
+            const bool fixed = a.stats.ref == a.stats.ref;
+            const double dwm = static_cast<double>(fixed ? a.stats.ref : wm);
             // exp_core where every argument of the lane is finite and in [-700, 0]: the value
             // exp_for_sum gives there, without its special cases
             bool core = true;
@@ -1608,6 +1610,7 @@ int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
         if (e == hipSuccess) e = hipMalloc(&h->stats.max, n * sizeof(float));
         if (e == hipSuccess) e = hipMalloc(&h->stats.aux, n * sizeof(uint32_t));
     }
+    h->stats.ref = (softcap > 0.0f && softcap <= kFixedRefMaxCap) ? softcap : __builtin_nanf("");
     if (e != hipSuccess) {
         twd_head_destroy(h);
         return hip_fail(e, "allocating the LM head");

@@ -510,7 +510,7 @@ __global__ __launch_bounds__(kLongThreads) void long_gather_kernel(LongArgs args
         wm[q] = live[q] ? rank_value(key[q]) : -INFINITY;
         nan |= wsum[q] != wsum[q] ? 1u : 0u;
     }
-    const RecStats rs = records_stats(live, wm, nan, wsum, want, sh.t, sh.c);
+    const RecStats rs = records_stats(live, wm, nan, wsum, b.st.ref, want, sh.t, sh.c);
     if (rs.degenerate) {  // sampling.cpp:116-118
         if (tid == 0) {
             b.tokens[row] = TWD_TOKEN_DEGENERATE;
@@ -1181,7 +1181,7 @@ int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_
             penalty_hash_kernel<<<rows, kPhThreads, 0, stream>>>(a, pb);
             TWD_HIP(hipGetLastError());
         }
-        const SampleStats st{s.wkey, s.wsum, s.wmax, s.waux};
+        const SampleStats st{s.wkey, s.wsum, s.wmax, s.waux, __builtin_nanf("")};
         WaveStatsBufs wb{logits, stride, vocab, waves,
                          (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && (stride & 3) == 0 ? 1u : 0u, st};
         wave_stats_kernel<1><<<dim3((vocab + kWsEntries - 1) / kWsEntries, rows), kWsThreads, 0, stream>>>(wb);
@@ -1225,7 +1225,7 @@ int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_
         TWD_HIP(hipGetLastError());
     }
     if (any_long) {  // their wave records from the penalised logits, then the long path
-        const SampleStats st{s.wkey, s.wsum, s.wmax, s.waux};
+        const SampleStats st{s.wkey, s.wsum, s.wmax, s.waux, __builtin_nanf("")};
         WaveStatsBufs wb{logits, stride, vocab, waves,
                          (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && (stride & 3) == 0 ? 1u : 0u, st};
         wave_stats_kernel<1><<<dim3((vocab + kWsEntries - 1) / kWsEntries, rows), kWsThreads, 0, stream>>>(wb);

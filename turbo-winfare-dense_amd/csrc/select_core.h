@@ -556,11 +556,19 @@ __device__ __forceinline__ uint32_t rec_bin(const RecStats& r, float x) {
 // The calling wave's share of the row's sum of exp(l - max): its records' sums rescaled to the
 // row max gm, summed in the thread's record order and then over the wave (wave_reduce's
 // tree); the waves' shares summed in wave order give the row total. A record adds nothing when
-// its sum is 0 (no live entry, every entry -inf, or past the row's records).
+// its sum is 0 (no live entry, every entry -inf, or past the row's records). With a fixed
+// reference ref (finite; every record's sum is of exp(v - ref)) the share is the records' sums,
+// times exp(ref - gm) once.
 template <uint32_t PER = kSmPer>
 __device__ __forceinline__ double records_part(const double (&wsum)[PER], const float (&wm)[PER], float gm,
-                                               const double* tbl) {
+                                               float ref, const double* tbl) {
     double part = 0.0;
+    if (ref == ref) {
+#pragma unroll
+        for (uint32_t q = 0; q < PER; ++q) part += wsum[q];
+        part = wave_reduce(part, 0.0, [](double u, double v) { return u + v; });
+        return part * exp_for_sum(static_cast<double>(ref) - static_cast<double>(gm), tbl);
+    }
 #pragma unroll
     for (uint32_t q = 0; q < PER; ++q)
         if (wsum[q] != 0.0) {
@@ -575,7 +583,7 @@ __device__ __forceinline__ double records_part(const double (&wsum)[PER], const 
 // wave maxima, wm[q] its maximum (-inf otherwise), and `flag` set when a record saw a NaN.
 template <bool kTotal = true, uint32_t PER = kSmPer>
 __device__ __forceinline__ RecStats records_stats(const bool (&live)[PER], const float (&wm)[PER],
-                                                  uint32_t flag, const double (&wsum)[PER], uint32_t want,
+                                                  uint32_t flag, const double (&wsum)[PER], float ref, uint32_t want,
                                                   TopScratch& t, SelCommon& c) {
     constexpr int NT = kSmThreads;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -596,7 +604,7 @@ __device__ __forceinline__ RecStats records_stats(const bool (&live)[PER], const
     }
     if constexpr (kTotal) {
         // the waves' partial sums cross the histogram's barrier below (block_sum_f64's order)
-        const double part = records_part<PER>(wsum, wm, gm, c.exp2_tbl);
+        const double part = records_part<PER>(wsum, wm, gm, ref, c.exp2_tbl);
         if (lane == 0) c.redd[wave] = part;
     }
 
@@ -724,7 +732,7 @@ __device__ __forceinline__ void sample_merge_row_per(const twd_row_params& p, ui
     uint32_t nan = 0;
 #pragma unroll
     for (uint32_t q = 0; q < PER; ++q) nan |= wm[q] != wm[q] ? 1u : 0u;
-    const RecStats rs = records_stats<false, PER>(live, wm, nan, wsum, want, sh.t, sh.c);
+    const RecStats rs = records_stats<false, PER>(live, wm, nan, wsum, b.st.ref, want, sh.t, sh.c);
     if (rs.degenerate) {  // sampling.cpp:116-118
         if (tid == 0) b.tokens[row] = TWD_TOKEN_DEGENERATE;
         return;
@@ -815,7 +823,7 @@ __device__ __forceinline__ void sample_merge_row_per(const twd_row_params& p, ui
     // the row total's terms while the first loads are in flight (the empty asm keeps the loads
     // ahead of them); the barrier below publishes the waves' shares
     __asm__ volatile("" ::: "memory");
-    const double part = records_part<PER>(wsum, wm, gm, sh.c.exp2_tbl);
+    const double part = records_part<PER>(wsum, wm, gm, b.st.ref, sh.c.exp2_tbl);
     if (lane == 0) sh.c.redd[wave] = part;
     if (per > 0) consume();
     for (uint32_t i0 = kGatherBatch; i0 < per; i0 += kGatherBatch) {

@@ -362,7 +362,12 @@ struct SampleStats {
     float* max;     // the best rank's value (-inf: none live, or every one -inf); NaN when a NaN
                     // was seen. The merge of a sampled row reads these 4 bytes per record first.
     uint32_t* aux;  // record_aux of the best two ranks, read with max
+    // sum holds the sum of exp(v - ref) instead when ref is finite: the head's sample mode with
+    // a softcap 0 < cap <= kFixedRefMaxCap, whose values all lie in [-cap, cap], takes ref = cap,
+    // so the row total is one exponential times the sum of the records' sums
+    float ref;
 };
+constexpr float kFixedRefMaxCap = 300.0f;  // exp(v - cap) >= exp(-600) stays a normal double
 constexpr uint32_t kSampleMaxWaves = 8192;  // waves a fused sample pass may have
 constexpr uint32_t kSampleWaveRows = 64;    // vocabulary rows per wave
 

@@ -1696,7 +1696,7 @@ int verify_draft_launches(twd_selector* sel, const float* logits, uint32_t vocab
     for (uint32_t i = 0; i < used; ++i) fused = fused && !long_row(rp[i], vocab);
     DraftSelect dsel{};
     if (fused) {
-        const SampleStats st{ss.wkey, ss.wsum, ss.wmax, ss.waux};
+        const SampleStats st{ss.wkey, ss.wsum, ss.wmax, ss.waux, __builtin_nanf("")};
         dsel.nsel = used;
         dsel.base = rp[0];
         for (uint32_t i = 0; i < used; ++i) dsel.u[i] = rp[i].uniform;
