@@ -11,26 +11,33 @@ sys.path.insert(0, ROOT)
 # Sampled-row parity margins: every oracle.sample_token made by a GPU test is the expectation of a
 # device row, so its cut margin |run - p| and draw margin |acc - r| are kept and summarised in
 # one line at the end of the run (the summary survives -q).
-_MARGINS = {"rows": 0, "cut": math.inf, "draw": math.inf, "under": 0}
+_MARGINS = {"rows": 0, "cut": math.inf, "draw": math.inf, "under": 0, "ties": 0}
 _IN_GPU_TEST = [False]
+_TIE_TEST = [False]  # a test whose rows put a prefix exactly on its threshold on purpose
 _TIGHT = 1e-12
 
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
     config.addinivalue_line("markers", "slow: takes more than a few seconds on the CPU")
+    config.addinivalue_line("markers", "ties: rows built with zero cut or draw margin on purpose")
 
 
 def pytest_runtest_setup(item):
     _IN_GPU_TEST[0] = item.get_closest_marker("gpu") is not None
+    _TIE_TEST[0] = item.get_closest_marker("ties") is not None
 
 
 def pytest_runtest_teardown(item):
     _IN_GPU_TEST[0] = False
+    _TIE_TEST[0] = False
 
 
 def _record(dg):
     if not _IN_GPU_TEST[0]:
+        return
+    if _TIE_TEST[0]:
+        _MARGINS["ties"] += 1
         return
     _MARGINS["rows"] += 1
     _MARGINS["cut"] = min(_MARGINS["cut"], dg["cut_margin"])
@@ -45,7 +52,8 @@ def pytest_terminal_summary(terminalreporter):
     terminalreporter.write_line(
         f"sampled-row margins: {_MARGINS['rows']} device rows checked against the oracle; smallest cut "
         f"margin {_MARGINS['cut']:.3e}, smallest draw margin {_MARGINS['draw']:.3e}; rows with a "
-        f"margin under {_TIGHT:g}: {_MARGINS['under']}")
+        f"margin under {_TIGHT:g}: {_MARGINS['under']}; rows built with a zero margin on purpose (and "
+        f"checked the same way): {_MARGINS['ties']}")
 
 
 @pytest.fixture(scope="session")

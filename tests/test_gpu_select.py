@@ -390,3 +390,41 @@ def test_plus_inf_rows(env, oracle, n):
     assert np.isfinite(want_pen).all()
     assert np.array_equal(pen[0].view(np.uint32), want_pen.view(np.uint32))
     assert int(tok[0]) == oracle.sample_token(want_pen, 0.8, 0.95, 64, u=0.37)
+
+
+@pytest.mark.ties
+@pytest.mark.parametrize("case", ["cut_on_p", "draw_on_r", "cut_and_draw", "near_tie"])
+def test_prefix_sums_that_land_on_their_threshold(env, oracle, case):
+    # Steps 5-7 decide by prefix sums compared with p (the top-p cut) and with u * denom (the
+    # draw). Rows built so that a prefix equals its threshold exactly (or lies within a few ulp
+    # of it) leave no margin between the reference's running sums and any other order of
+    # additions, so the device must decide them with the reference's additions.
+    torch, dev, t, sel = env
+    n = 4096
+    rows, params = [], []
+    for s in range(8):
+        row = np.full(n, -np.inf, np.float32)
+        if case == "cut_on_p":
+            # two equal maxima hold the whole mass: e = (1/2, 1/2), p = 1/2 exactly
+            row[[17 + s, 900 + s]] = 0.0
+            params.append(rp(t, 0.9, 0.5, 0, 0.25 + 0.0625 * s))
+        elif case == "draw_on_r":
+            # q = (1, 1), denom 2, u = 1/2: u * denom equals the first running sum
+            row[[5 + s, 2000 + s]] = 1.5
+            params.append(rp(t, 1.0, 1.0, 2, 0.5))
+        elif case == "cut_and_draw":
+            # four equal maxima: running sums 1/4, 1/2, 3/4 of the mass; p = 3/4, u = 2/3
+            row[[3 + s, 300 + s, 1000 + s, 3000 + s]] = -2.0
+            params.append(rp(t, 1.0, 0.75, 0, 2.0 / 3.0))
+        else:
+            # many near-equal values whose running sum passes p within a few ulp
+            rng = np.random.default_rng(100 + s)
+            idx = rng.choice(n, 64, replace=False)
+            row[idx] = np.float32(0.0) + rng.integers(0, 3, 64).astype(np.float32) * np.float32(2 ** -23)
+            params.append(rp(t, 0.8, 0.5, 0, float(np.float32(0.5))))
+        rows.append(row)
+    rows = np.stack(rows)
+    tok, _ = select_rows(env, rows, params)
+    for i in range(len(rows)):
+        p = params[i]
+        assert int(tok[i]) == oracle.sample_token(rows[i], p.temperature, p.top_p, p.top_k, u=p.uniform), (case, i)

@@ -423,6 +423,7 @@ __device__ __forceinline__ void shortlist_pad(SelCommon& c, uint32_t want) {
 }
 
 __device__ __forceinline__ uint32_t finish_sums(SelCommon& c, uint32_t want, const twd_row_params& p);
+__device__ __forceinline__ uint32_t finish_sums_exact(SelCommon& c, uint32_t want, const twd_row_params& p);
 
 __device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, const twd_row_params& p,
                                                    float gmax, double total) {
@@ -434,7 +435,101 @@ __device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, 
 }
 
 // Steps 5-7 after the terms c.e[0..want), c.q[0..want) (zero-padded) have been published.
+//
+// First on wave 0 by parallel prefix sums: lane l sums terms 4l .. 4l + 3 in order (one term per
+// lane for shortlists of up to 64), a wave scan adds the lanes' totals, so every prefix is formed
+// by at most ten additions of non-negative terms, against up to 255 in the reference's running sum: the two differ by less than 3e-14 of
+// the prefix. Each decision of steps 5-7 compares a prefix with a threshold (the top-p cut: the
+// first running sum >= p; the draw: the first running sum of q >= u * the sum at the cut), and
+// the prefixes never decrease, so a decision is the reference's whenever the prefixes on both
+// sides of it lie further than kSumTol (relative) from its threshold. Otherwise (a prefix that
+// close, e.g. an exact tie) finish_sums_exact repeats steps 5-7 with the reference's additions.
+constexpr double kSumTol = 0x1p-36;
+
+// TPL terms per lane of wave 0: lane l holds terms TPL l .. TPL l + TPL - 1 and their running
+// sums (TPL = 1 for shortlists of up to 64 terms: each prefix is then the scan's own value).
+template <uint32_t TPL>
+__device__ __forceinline__ uint32_t finish_sums_par(SelCommon& c, uint32_t want, const twd_row_params& p) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t padded = (want + kFinishChunk - 1) & ~(kFinishChunk - 1);  // <= 64 * TPL
+    const uint32_t i0 = TPL * static_cast<uint32_t>(lane);
+    double pe[TPL], pq[TPL];
+#pragma unroll
+    for (uint32_t j = 0; j < TPL; ++j) pe[j] = pq[j] = 0.0;
+    if (i0 < padded) {  // padded is a multiple of 16: the lane's terms all lie below it
+#pragma unroll
+        for (uint32_t j = 0; j < TPL; ++j) {
+            pe[j] = c.e[i0 + j];
+            pq[j] = c.q[i0 + j];
+        }
+    }
+#pragma unroll
+    for (uint32_t j = 1; j < TPL; ++j) {
+        pe[j] = pe[j - 1] + pe[j];
+        pq[j] = pq[j - 1] + pq[j];
+    }
+    const double se = wave_incl_scan_f64(pe[TPL - 1]), sq = wave_incl_scan_f64(pq[TPL - 1]);
+    if constexpr (TPL == 1) {
+        pe[0] = se;
+        pq[0] = sq;
+    } else {
+        // the lanes below: wave_shr:1 (lane 0 takes 0)
+        const double xe = dpp_move<0x138>(0.0, se), xq = dpp_move<0x138>(0.0, sq);
+#pragma unroll
+        for (uint32_t j = 0; j < TPL; ++j) {
+            pe[j] = xe + pe[j];
+            pq[j] = xq + pq[j];
+        }
+    }
+    auto at = [&](const double (&a)[TPL], uint32_t i) {
+        double v = a[0];
+#pragma unroll
+        for (uint32_t j = 1; j < TPL; ++j) v = (i % TPL) == j ? a[j] : v;
+        return readlane_f64(v, static_cast<int>(i / TPL));
+    };
+    // the first index i < lim whose prefix reaches x, as (found, i)
+    auto first = [&](const double (&a)[TPL], uint32_t lim, double x, uint32_t& i) -> bool {
+        uint32_t hit = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < TPL; ++j) hit |= (i0 + j < lim && a[j] >= x ? 1u : 0u) << j;
+        const uint64_t lanes = __ballot(hit != 0);
+        if (lanes == 0) return false;
+        const int L = __ffsll(static_cast<long long>(lanes)) - 1;
+        i = TPL * static_cast<uint32_t>(L) +
+            static_cast<uint32_t>(__builtin_ctz(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(hit), L))));
+        return true;
+    };
+    bool ok = true;
+    uint32_t cut = want;
+    if (p.top_p < 1.0f) {
+        const double pp = static_cast<double>(p.top_p);
+        uint32_t i = 0;
+        if (first(pe, want, pp, i)) {
+            cut = i + 1;
+            ok = at(pe, i) >= pp * (1.0 + kSumTol) && (i == 0 || at(pe, i - 1) < pp * (1.0 - kSumTol));
+        } else {
+            ok = at(pe, want - 1) < pp * (1.0 - kSumTol);
+        }
+    }
+    if (p.top_k > 0 && cut > static_cast<uint32_t>(p.top_k)) cut = static_cast<uint32_t>(p.top_k);
+    if (cut < 1) cut = 1;
+    const double r = static_cast<double>(p.uniform) * at(pq, cut - 1);
+    uint32_t pick = cut - 1;
+    if (first(pq, cut, r, pick))
+        ok = ok && at(pq, pick) >= r * (1.0 + kSumTol) && (pick == 0 || at(pq, pick - 1) < r * (1.0 - kSumTol));
+    else
+        ok = false;
+    if (ok) return rank_index(c.sorted[pick]);
+    return finish_sums_exact(c, want, p);
+}
+
 __device__ __forceinline__ uint32_t finish_sums(SelCommon& c, uint32_t want, const twd_row_params& p) {
+    if (threadIdx.x >= 64) return 0;
+    return want <= 64 ? finish_sums_par<1>(c, want, p) : finish_sums_par<4>(c, want, p);
+}
+
+// Steps 5-7 with the reference's running sums: lanes 0 and 1 of wave 0 (every lane of it calls).
+__device__ __forceinline__ uint32_t finish_sums_exact(SelCommon& c, uint32_t want, const twd_row_params& p) {
     const int tid = threadIdx.x, lane = tid & 63;
     constexpr uint32_t kChunk = kFinishChunk;
     if (tid >= 64) return 0;

@@ -175,6 +175,24 @@ __device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t x) {
     return x;
 }
 
+// The same inclusive prefix sum of doubles (each lane's value formed by at most six additions).
+__device__ __forceinline__ double wave_incl_scan_f64(double x) {
+    x += dpp_move<0x111>(0.0, x);
+    x += dpp_move<0x112>(0.0, x);
+    x += dpp_move<0x114>(0.0, x);
+    x += dpp_move<0x118>(0.0, x);
+    x += dpp_move<0x142, 0xA>(0.0, x);
+    x += dpp_move<0x143, 0xC>(0.0, x);
+    return x;
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+    const uint64_t x = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(x)), l));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(x >> 32)), l));
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return wave_reduce(v, uint64_t{0}, [](uint64_t a, uint64_t b) { return a > b ? a : b; });
 }
