@@ -843,12 +843,17 @@ __global__ __launch_bounds__(kPhThreads) void penalty_hash_kernel(SelectArgs arg
 // NB 8-entry batches per lane. One: many short blocks, so that later blocks' loads overlap
 // earlier blocks' arithmetic (with four, every wave requested all its loads first, and the pass
 // ran as a load phase, then an arithmetic phase).
-template <uint32_t NB>
+template <uint32_t NB, bool AUX>
 __global__ __launch_bounds__(kWsThreads) __attribute__((amdgpu_waves_per_eu(8)))
 void wave_stats_kernel(WaveStatsBufs b) {
     __shared__ double tbl[64];
-    wave_records_block<NB>(b, blockIdx.x, blockIdx.y, tbl);
+    wave_records_block<NB, AUX>(b, blockIdx.x, blockIdx.y, tbl);
 }
+
+// Rows up to which the record pass also forms the record words: its blocks are then few and
+// short of work, and the words spare most merges their gather; past it the words cost the
+// pass more than the merges save (64 rows: 25.0 against 20.9 us for the pass).
+constexpr uint32_t kAuxMaxRows = 8;
 
 __global__ void verify_compare_kernel(const uint32_t* row_tokens, uint32_t rows,
                                       const uint32_t* drafts, uint32_t nd,
@@ -1181,10 +1186,15 @@ int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_
             penalty_hash_kernel<<<rows, kPhThreads, 0, stream>>>(a, pb);
             TWD_HIP(hipGetLastError());
         }
-        const SampleStats st{s.wkey, s.wsum, s.wmax, s.waux, __builtin_nanf("")};
+        const bool aux = rows <= kAuxMaxRows;
+        const SampleStats st{s.wkey, s.wsum, s.wmax, aux ? s.waux : nullptr, __builtin_nanf("")};
         WaveStatsBufs wb{logits, stride, vocab, waves,
                          (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && (stride & 3) == 0 ? 1u : 0u, st};
-        wave_stats_kernel<1><<<dim3((vocab + kWsEntries - 1) / kWsEntries, rows), kWsThreads, 0, stream>>>(wb);
+        const dim3 grid((vocab + kWsEntries - 1) / kWsEntries, rows);
+        if (aux)
+            wave_stats_kernel<1, true><<<grid, kWsThreads, 0, stream>>>(wb);
+        else
+            wave_stats_kernel<1, false><<<grid, kWsThreads, 0, stream>>>(wb);
         TWD_HIP(hipGetLastError());
         SampleMergeBufs mb{};
         mb.logits = logits;
@@ -1225,10 +1235,10 @@ int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_
         TWD_HIP(hipGetLastError());
     }
     if (any_long) {  // their wave records from the penalised logits, then the long path
-        const SampleStats st{s.wkey, s.wsum, s.wmax, s.waux, __builtin_nanf("")};
+        const SampleStats st{s.wkey, s.wsum, s.wmax, nullptr, __builtin_nanf("")};  // no merge reads words
         WaveStatsBufs wb{logits, stride, vocab, waves,
                          (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && (stride & 3) == 0 ? 1u : 0u, st};
-        wave_stats_kernel<1><<<dim3((vocab + kWsEntries - 1) / kWsEntries, rows), kWsThreads, 0, stream>>>(wb);
+        wave_stats_kernel<1, false><<<dim3((vocab + kWsEntries - 1) / kWsEntries, rows), kWsThreads, 0, stream>>>(wb);
         TWD_HIP(hipGetLastError());
         return launch_long(s.lng, st, waves, logits, stride, vocab, rows, params, tokens, stream);
     }

@@ -808,12 +808,13 @@ __device__ __forceinline__ void sample_merge_row_per(const twd_row_params& p, ui
     double wsum[PER];
     bool live[PER];
     uint32_t aux[PER];
+    const bool have_aux = b.st.aux != nullptr;  // the records' words (else every candidate is read)
 #pragma unroll
     for (uint32_t q = 0; q < PER; ++q) {
         const uint32_t i = tid + NT * q;
         live[q] = i < W;
         wm[q] = live[q] ? b.st.max[o + i] : -INFINITY;
-        aux[q] = live[q] ? b.st.aux[o + i] : 0u;
+        aux[q] = (live[q] && have_aux) ? b.st.aux[o + i] : 0u;
     }
 #pragma unroll
     for (uint32_t q = 0; q < PER; ++q) {
@@ -850,7 +851,7 @@ __device__ __forceinline__ void sample_merge_row_per(const twd_row_params& p, ui
         for (uint32_t q = 0; q < PER; ++q) {
             const uint32_t w = tid + NT * q;
             const bool cand = live[q] && bin_of(wm[q]) <= bstar;
-            whole[q] = cand && bin_of(fminf(aux_second(aux[q]), gm)) <= bstar;
+            whole[q] = cand && (!have_aux || bin_of(fminf(aux_second(aux[q]), gm)) <= bstar);
             one[q] = cand && !whole[q];
             wid[q] = w;
             wid1[q] = static_cast<uint16_t>(w);  // w < kSampleMaxWaves
@@ -1041,7 +1042,9 @@ struct WaveStatsBufs {
 // The records of one block of kWsThreads threads: row `row`, its NB * kWsEntries entries from
 // chunk * NB * kWsEntries. tbl: 64 doubles of LDS for the exp table (loaded here, published by
 // the barrier below). Every thread of the block calls it.
-template <uint32_t NB>
+// AUX: also the record word (record_aux); without it the merge reads every candidate wave whole
+// (b.st.aux is then null), which costs many-row launches less than forming the words.
+template <uint32_t NB, bool AUX = true>
 __device__ __forceinline__ void wave_records_block(const WaveStatsBufs& b, uint32_t chunk, uint32_t row,
                                                    double* tbl) {
     constexpr uint32_t kWsBatches = NB;
@@ -1085,19 +1088,29 @@ __device__ __forceinline__ void wave_records_block(const WaveStatsBufs& b, uint3
             uint32_t qi = 7;
 #pragma unroll
             for (int q = 6; q >= 0; --q) qi = v[k][q] == hi ? static_cast<uint32_t>(q) : qi;
-            // the lane's second: the largest of its other values, at the lowest such index
+            // the lane's second value: the largest of its other entries (hi again if it repeats)
             float h2 = -INFINITY;
+            if constexpr (AUX) {
 #pragma unroll
-            for (int q = 0; q < 8; ++q) h2 = static_cast<uint32_t>(q) != qi ? fmaxf(h2, v[k][q]) : h2;
-            uint32_t q2 = 7;
-#pragma unroll
-            for (int q = 6; q >= 0; --q)
-                q2 = (static_cast<uint32_t>(q) != qi && v[k][q] == h2) ? static_cast<uint32_t>(q) : q2;
-            uint64_t best = rank_key(hi, e + qi), second = rank_key(h2, e + q2);
-            // the record's 64 entries are the 8 lanes with the same lane >> 3
-            top2_step<0xB1>(best, second);
-            top2_step<0x4E>(best, second);
-            top2_step<0x141>(best, second);
+                for (int q = 0; q < 8; ++q) h2 = static_cast<uint32_t>(q) != qi ? fmaxf(h2, v[k][q]) : h2;
+            }
+            uint64_t best = rank_key(hi, e + qi);
+            float h1 = hi;
+            // the record's 64 entries are the 8 lanes with the same lane >> 3: the best rank, and
+            // the two largest values (a value held twice counts twice)
+            auto step = [&](auto ctrl) {
+                constexpr int C = decltype(ctrl)::value;
+                const uint64_t ob = dpp_move<C>(best, best);
+                best = ob > best ? ob : best;
+                if constexpr (AUX) {
+                    const float o1 = dpp_move<C>(h1, h1), o2 = dpp_move<C>(h2, h2);
+                    h2 = fmaxf(fminf(h1, o1), fmaxf(h2, o2));
+                    h1 = fmaxf(h1, o1);
+                }
+            };
+            step(std::integral_constant<int, 0xB1>{});
+            step(std::integral_constant<int, 0x4E>{});
+            step(std::integral_constant<int, 0x141>{});
             const float wm = rank_value(best);
             if (__ballot(lo < wm - 700.0f) == 0) {
                 const double dwm = static_cast<double>(wm);
@@ -1112,7 +1125,7 @@ __device__ __forceinline__ void wave_records_block(const WaveStatsBufs& b, uint3
                     b.st.key[o] = best;
                     b.st.sum[o] = sum;
                     b.st.max[o] = wm;
-                    b.st.aux[o] = record_aux(best, second);
+                    if constexpr (AUX) b.st.aux[o] = record_aux_value(best, h2);
                 }
                 continue;
             }
@@ -1148,7 +1161,7 @@ __device__ __forceinline__ void wave_records_block(const WaveStatsBufs& b, uint3
             b.st.key[o] = best;
             b.st.sum[o] = sum;
             b.st.max[o] = nan ? __builtin_nanf("") : wm;
-            b.st.aux[o] = record_aux(best, second);
+            if constexpr (AUX) b.st.aux[o] = record_aux(best, second);
         }
     }
 }

@@ -117,17 +117,18 @@ __device__ __forceinline__ void top2_step(uint64_t& b1, uint64_t& b2) {
 // second-best rank's value rounded up to bf16 (bits 16-31; -inf when there is none). Rounding up
 // keeps the merge's test conservative: a second value whose bin lies past b* rounds to one that
 // does too only when the exact one does.
-__device__ __forceinline__ uint32_t record_aux(uint64_t best, uint64_t second) {
-    uint32_t up = 0xFF80u;  // -inf
-    if (second != 0) {
-        const float v = rank_value(second);
-        const uint32_t b = __float_as_uint(v);
-        const uint32_t t = b >> 16;  // truncation: toward zero
-        // toward +inf: a positive value with bits below the bf16 cut goes up one bf16 step
-        up = (v > 0.0f && (b & 0xFFFFu) != 0) ? t + 1 : t;
-        if (v != v) up = 0x7FC0u;
-    }
+// second: the second-best value (-inf when there is none).
+__device__ __forceinline__ uint32_t record_aux_value(uint64_t best, float second) {
+    const uint32_t b = __float_as_uint(second + 0.0f);  // -0 as +0
+    const uint32_t t = b >> 16;                        // truncation: toward zero
+    // toward +inf: a positive value with bits below the bf16 cut goes up one bf16 step
+    uint32_t up = (second > 0.0f && (b & 0xFFFFu) != 0) ? t + 1 : t;
+    if (second != second) up = 0x7FC0u;
     return (up << 16) | (rank_index(best) & 63u);
+}
+
+__device__ __forceinline__ uint32_t record_aux(uint64_t best, uint64_t second) {
+    return record_aux_value(best, second != 0 ? rank_value(second) : -INFINITY);
 }
 
 __device__ __forceinline__ float aux_second(uint32_t aux) { return __uint_as_float(aux & 0xFFFF0000u); }
