@@ -191,3 +191,32 @@ def test_sample_rows_past_the_fused_pass(env, oracle, M):
     hist = np.concatenate(hists)
     run_and_check(env, oracle, head, hidden_bf16(760 + M, M, d), params, hist, f"M={M}")
     head.close()
+
+
+@pytest.mark.parametrize("M", [2, 6])
+def test_fused_penalty_past_the_softcap(env, oracle, M):
+    # The fused pass sums each record against a fixed bound of the row's values when it has one
+    # (the softcap, or the penalty's clamp); a penalty without a clamp, or below 1, can take
+    # values far past the softcap (v / rp^n grows, v * rp^n falls), where that bound would
+    # overflow or underflow exp: such rows are summed against each wave's max. Histories repeat
+    # a few ids hundreds of times, so their penalised values reach ~1e6 in magnitude.
+    torch, dev, t = env
+    V, d = 1000, 256
+    W, S, B = oracle.gen_lm_head(770 + M, V, d)
+    head = t.LMHead(torch.from_numpy(wsb_bytes(W, S, B)).to(dev), V, d, CAP)
+    rng = np.random.default_rng(77 + M)
+    hist = np.concatenate([np.repeat(rng.integers(0, V, 4).astype(np.uint32), 150),
+                           rng.integers(0, V, 400).astype(np.uint32)])
+    n = len(hist)
+    cases = [
+        (0.7, 0.9, 40, 0.95, 0.0),   # rp < 1, no clamp: values grow by 0.95^-150 ~ 2,200x
+        (1.0, 0.95, 100, 1.1, 0.0),  # rp > 1, no clamp: negative values fall by 1.1^150 ~ 1.6e6x
+        (0.8, 0.9, 64, 0.9, 500.0),  # a clamp at 499.95: past the bound the fixed form allows
+        (0.7, 0.9, 40, 1.2, CAP),    # a clamp at the softcap: the fixed reference applies
+        (1.2, 1.0, 0, 0.8, 10.0),    # a clamp below the softcap: the softcap bounds the row
+        (0.0, 1.0, 0, 0.9, 0.0),     # greedy, grown values
+    ]
+    params = [t.RowParams(T, p, k, rp, float(rng.uniform()), cap, 0, n)
+              for T, p, k, rp, cap in (cases[m % len(cases)] for m in range(M))]
+    run_and_check(env, oracle, head, hidden_bf16(780 + M, M, d), params, hist, f"past the cap M={M}")
+    head.close()

@@ -67,6 +67,7 @@ struct HeadArgs {
     const uint32_t* history;
     uint32_t hist_off[kSampleRows], hist_len[kSampleRows];
     float rp[kSampleRows], clamp[kSampleRows];
+    float ref[kSampleRows];  // fixed_ref of each row (NaN: its records are summed against each wave's max)
     SampleStats stats;
 };
 
@@ -322,7 +323,7 @@ __device__ __forceinline__ void head_epilogue_sample(const HeadArgs& a, f32x4_t 
         const uint32_t m = (4 * (lane >> 4) + MS * e) / MS;
         const bool mlive = m < a.M;
         const uint32_t mm = mlive ? m : 0u;
-        const float rp = prm[mm], lim = prm[kSampleRows + mm];
+        const float rp = prm[mm], lim = prm[kSampleRows + mm], ref = prm[2 * kSampleRows + mm];
         float v[RT];
         uint64_t best = 0, second = 0;
         uint32_t nan = 0;
@@ -360,9 +361,8 @@ __device__ __forceinline__ void head_epilogue_sample(const HeadArgs& a, f32x4_t 
         const float wm = best != 0 ? rank_value(best) : -INFINITY;
         double sum = 0.0;
         if (wm != -INFINITY) {
-            // the sum's reference: the fixed one (the cap, above every value) or the wave's max
-            const bool fixed = a.stats.ref == a.stats.ref;
-            const double dwm = static_cast<double>(fixed ? a.stats.ref : wm);
+            // the sum's reference: the row's fixed one (a bound of every value) or the wave's max
+            const double dwm = static_cast<double>(ref == ref ? ref : wm);
             // exp_core where every argument of the lane is finite and in [-700, 0]: the value
             // exp_for_sum gives there, without its special cases
             bool core = true;
@@ -512,7 +512,7 @@ __global__ __launch_bounds__(NW * 64) void head_small_kernel(HeadArgs a) {
     __shared__ double exp2_tbl[MODE == kModeSample ? 64 : 1];
     // the rows' penalty factors and clamps, read per lane in the epilogue: staged here, where the
     // load overlaps the ring fill, instead of a memory round trip at the end of every block
-    __shared__ float prm[MODE == kModeSample ? 2 * kSampleRows : 1];
+    __shared__ float prm[MODE == kModeSample ? 3 * kSampleRows : 1];
     const uint32_t block_row0 = blockIdx.x * kRowsPerBlock;
     if constexpr (MODE == kModeSample) {
         for (uint32_t i = tid; i < kCntRows * kRowsPerBlock; i += NT) cnt[i] = 0;
@@ -520,6 +520,7 @@ __global__ __launch_bounds__(NW * 64) void head_small_kernel(HeadArgs a) {
         if (tid < static_cast<int>(kSampleRows)) {
             prm[tid] = a.rp[tid];
             prm[kSampleRows + tid] = a.clamp[tid];
+            prm[2 * kSampleRows + tid] = a.ref[tid];
         }
     }
     // sample mode: the history's first batch (kHistBatch ids per thread of the first row with a
@@ -1610,7 +1611,7 @@ int head_alloc(uint32_t vocab, uint32_t d, float softcap, twd_head** out) {
         if (e == hipSuccess) e = hipMalloc(&h->stats.max, n * sizeof(float));
         if (e == hipSuccess) e = hipMalloc(&h->stats.aux, n * sizeof(uint32_t));
     }
-    h->stats.ref = (softcap > 0.0f && softcap <= kFixedRefMaxCap) ? softcap : __builtin_nanf("");
+    h->stats.cap = softcap > 0.0f ? softcap : __builtin_nanf("");
     if (e != hipSuccess) {
         twd_head_destroy(h);
         return hip_fail(e, "allocating the LM head");
@@ -1786,6 +1787,7 @@ int launch_head_sample(twd_head* h, const uint16_t* hidden, const float* x, cons
         a.clamp[m] = (live && params[m].softcap > 0.0f) ? params[m].softcap * 0.9999f : 0.0f;
         a.hist_off[m] = live ? params[m].history_offset : 0u;
         a.hist_len[m] = live ? params[m].history_len : 0u;
+        a.ref[m] = live ? fixed_ref(h->stats.cap, params[m]) : __builtin_nanf("");
         if (!live) continue;
         if (params[m].repetition_penalty != 1.0f && params[m].history_len > 0 && !history)
             return fail(TWD_E_INVALID, "null history with a non-empty history_len");

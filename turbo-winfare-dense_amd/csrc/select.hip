@@ -510,7 +510,7 @@ __global__ __launch_bounds__(kLongThreads) void long_gather_kernel(LongArgs args
         wm[q] = live[q] ? rank_value(key[q]) : -INFINITY;
         nan |= wsum[q] != wsum[q] ? 1u : 0u;
     }
-    const RecStats rs = records_stats(live, wm, nan, wsum, b.st.ref, want, sh.t, sh.c);
+    const RecStats rs = records_stats(live, wm, nan, wsum, fixed_ref(b.st.cap, p), want, sh.t, sh.c);
     if (rs.degenerate) {  // sampling.cpp:116-118
         if (tid == 0) {
             b.tokens[row] = TWD_TOKEN_DEGENERATE;
@@ -1187,7 +1187,7 @@ int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_
             TWD_HIP(hipGetLastError());
         }
         const bool aux = rows <= kAuxMaxRows;
-        const SampleStats st{s.wkey, s.wsum, s.wmax, aux ? s.waux : nullptr, __builtin_nanf("")};
+        const SampleStats st{s.wkey, s.wsum, s.wmax, aux ? s.waux : nullptr, __builtin_nanf("")};  // no cap
         WaveStatsBufs wb{logits, stride, vocab, waves,
                          (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && (stride & 3) == 0 ? 1u : 0u, st};
         const dim3 grid((vocab + kWsEntries - 1) / kWsEntries, rows);

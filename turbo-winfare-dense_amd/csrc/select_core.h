@@ -809,6 +809,7 @@ __device__ __forceinline__ void sample_merge_row_per(const twd_row_params& p, ui
     bool live[PER];
     uint32_t aux[PER];
     const bool have_aux = b.st.aux != nullptr;  // the records' words (else every candidate is read)
+    const float ref = fixed_ref(b.st.cap, p);    // the records' sums' reference (NaN: each wave's max)
 #pragma unroll
     for (uint32_t q = 0; q < PER; ++q) {
         const uint32_t i = tid + NT * q;
@@ -828,7 +829,7 @@ __device__ __forceinline__ void sample_merge_row_per(const twd_row_params& p, ui
     uint32_t nan = 0;
 #pragma unroll
     for (uint32_t q = 0; q < PER; ++q) nan |= wm[q] != wm[q] ? 1u : 0u;
-    const RecStats rs = records_stats<false, PER>(live, wm, nan, wsum, b.st.ref, want, sh.t, sh.c);
+    const RecStats rs = records_stats<false, PER>(live, wm, nan, wsum, ref, want, sh.t, sh.c);
     if (rs.degenerate) {  // sampling.cpp:116-118
         if (tid == 0) b.tokens[row] = TWD_TOKEN_DEGENERATE;
         return;
@@ -919,7 +920,7 @@ __device__ __forceinline__ void sample_merge_row_per(const twd_row_params& p, ui
     // the row total's terms while the first loads are in flight (the empty asm keeps the loads
     // ahead of them); the barrier below publishes the waves' shares
     __asm__ volatile("" ::: "memory");
-    const double part = records_part<PER>(wsum, wm, gm, b.st.ref, sh.c.exp2_tbl);
+    const double part = records_part<PER>(wsum, wm, gm, ref, sh.c.exp2_tbl);
     if (lane == 0) sh.c.redd[wave] = part;
     if (per > 0) consume();
     for (uint32_t i0 = kGatherBatch; i0 < per; i0 += kGatherBatch) {

@@ -381,12 +381,29 @@ struct SampleStats {
     float* max;     // the best rank's value (-inf: none live, or every one -inf); NaN when a NaN
                     // was seen. The merge of a sampled row reads these 4 bytes per record first.
     uint32_t* aux;  // record_aux of the best two ranks, read with max
-    // sum holds the sum of exp(v - ref) instead when ref is finite: the head's sample mode with
-    // a softcap 0 < cap <= kFixedRefMaxCap, whose values all lie in [-cap, cap], takes ref = cap,
-    // so the row total is one exponential times the sum of the records' sums
-    float ref;
+    // The head's softcap when its records were formed by the head's sample mode, NaN otherwise.
+    // For a row whose values fixed_ref bounds (finite result), sum holds the sum of exp(v - ref)
+    // against that fixed reference instead of the wave's max, so the row total is one
+    // exponential times the sum of the records' sums.
+    float cap;
 };
-constexpr float kFixedRefMaxCap = 300.0f;  // exp(v - cap) >= exp(-600) stays a normal double
+
+// The fixed reference of a head row's record sums: a bound C >= |v| of every value the row can
+// hold after the softcap (|cap tanh(x / cap)| <= cap) and the repetition penalty (whose clamp
+// bounds the entries it changes by the row's softcap * 0.9999; without a clamp they are not
+// bounded), when C <= kFixedRefMaxCap, so that exp(v - C) >= exp(-2 C) stays a normal double;
+// NaN otherwise (the records are then summed against each wave's max).
+constexpr float kFixedRefMaxCap = 300.0f;
+__host__ __device__ inline float fixed_ref(float cap, const twd_row_params& p) {
+    if (!(cap > 0.0f)) return __builtin_nanf("");
+    float c = cap;
+    if (p.repetition_penalty != 1.0f && p.history_len != 0) {
+        if (!(p.softcap > 0.0f)) return __builtin_nanf("");
+        const float lim = p.softcap * 0.9999f;
+        c = lim > c ? lim : c;
+    }
+    return c <= kFixedRefMaxCap ? c : __builtin_nanf("");
+}
 constexpr uint32_t kSampleMaxWaves = 8192;  // waves a fused sample pass may have
 constexpr uint32_t kSampleWaveRows = 64;    // vocabulary rows per wave
 
