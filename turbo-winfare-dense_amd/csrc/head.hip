@@ -248,17 +248,22 @@ __device__ __forceinline__ void head_epilogue(const HeadArgs& a, f32x4_t (&tot)[
     }
     if (MODE == kModeLogits) return;
 
-    // rows sharing m are the 16 lanes with the same lane >> 4
+    // rows sharing m are the 16 lanes with the same lane >> 4, one DPP row: quad_perm [1,0,3,2]
+    // and [2,3,0,1], row_half_mirror, row_mirror (register moves, where a shuffle is an LDS
+    // round trip at the end of every wave)
 #pragma unroll
     for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
         for (int i = 0; i < NI; i += MS) {
             uint64_t k = best[mt][i];
-#pragma unroll
-            for (int msk = 1; msk < 16; msk <<= 1) {
-                const uint64_t o = shfl_xor_u64(k, msk);
+            auto step = [&](auto ctrl) {
+                const uint64_t o = dpp_move<decltype(ctrl)::value>(k, k);
                 k = o > k ? o : k;
-            }
+            };
+            step(std::integral_constant<int, 0xB1>{});
+            step(std::integral_constant<int, 0x4E>{});
+            step(std::integral_constant<int, 0x141>{});
+            step(std::integral_constant<int, 0x140>{});
             const uint32_t m = (mt * 16 + 4 * (lane >> 4) + i) / MS;
             if ((lane & 15) == 0 && m < TWD_MAX_ROWS) se.red[wave][m] = k;
         }
