@@ -285,6 +285,50 @@ def measured_traffic():
     return None, None
 
 
+def rows_sweep(torch, dev, twd, rounds: int = 3, n: int = 200):
+    """The head's time by rows, and the fused sample pass against the two-pass form, each the
+    median over `rounds` interleaved rounds of `n` back-to-back calls on one stream."""
+    log("rows sweep: head by M, fused sample pass against logits + selector")
+    wsb = torch.empty(HEAD_BYTES, dtype=torch.uint8, device=dev)
+    twd.generate_head(wsb, V, D, SEED)
+    head = twd.LMHead(wsb, V, D, CAP)
+    sel = twd.Selector(V, 64)
+    stream = torch.cuda.current_stream().cuda_stream
+    hp = hidden_pool(torch, dev, 8, 64, 7)
+    lg = torch.empty(64, V, dtype=torch.float32, device=dev)
+    tk = torch.empty(64, dtype=torch.int32, device=dev)
+    rng = np.random.default_rng(77)
+    hist = torch.from_numpy(rng.integers(0, V, 8 * 2048, dtype=np.int64).astype(np.int32)).to(dev)
+    # config 3's chain parameters (T = 0.7, k = 40, p = 0.9, rp 1.1) on every row, over 2,048
+    # history ids per row: eight such rows stay within the fused pass's 16,384 ids
+    prm = [twd.RowParams(0.7, 0.9, 40, 1.1, float(rng.uniform()), CAP, 2048 * m, 2048)
+           for m in range(8)]
+    cases = {}
+    for m in (1, 2, 3, 4, 5, 8, 16, 32, 48, 64):
+        cases[f"logits_M{m}"] = (lambda mm: lambda i: head.logits(hp[i % 8, :mm], out=lg[:mm],
+                                                                  stream=stream))(m)
+        cases[f"greedy_M{m}"] = (lambda mm: lambda i: head.greedy(hp[i % 8, :mm], tokens=tk[:mm],
+                                                                  stream=stream))(m)
+    for m in (1, 4, 5, 6, 8):
+        cases[f"sample_fused_M{m}"] = (lambda mm: lambda i: head.sample(
+            hp[i % 8, :mm], prm[:mm], history=hist, logits=lg[:mm], tokens=tk[:mm],
+            stream=stream))(m)
+
+        def two_pass(i, mm=m):
+            head.logits(hp[i % 8, :mm], out=lg[:mm], stream=stream)
+            sel.select(lg[:mm], prm[:mm], history=hist, tokens=tk[:mm], stream=stream)
+        cases[f"logits_then_select_M{m}"] = two_pass
+    got = {k: [] for k in cases}
+    for _ in range(rounds):
+        for k, fn in cases.items():
+            got[k].append(time_loop(torch, n, 10, fn, min_warm_s=0.02) / n * 1e6)
+    sel.close()
+    print(json.dumps({"rows_sweep_us": {k: round(float(np.median(v)), 2) for k, v in got.items()},
+                      "rounds": rounds, "calls_per_round": n,
+                      "note": "back-to-back calls on one stream, median over interleaved rounds; "
+                              "sample rows: rp 1.1 over 2048 ids each, T 0.7, k 40, p 0.9"}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -300,6 +344,10 @@ def main():
                          "configs add about 15 s)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (FETCH_SIZE/WRITE_SIZE calibration)")
+    ap.add_argument("--rows-sweep", action="store_true",
+                    help="only time the head by rows (logits and greedy, M = 1..64) and the fused "
+                         "sample pass against the logits pass + selector (M = 1, 4..8), back to "
+                         "back in interleaved rounds; prints one JSON line of its own")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -323,6 +371,9 @@ def main():
 
     sys.path.insert(0, ROOT)
     twd = importlib.import_module("turbo-winfare-dense_amd")
+    if args.rows_sweep:
+        rows_sweep(torch, dev, twd)
+        return
     cfgs = {int(c) for c in args.configs.split(",") if c}
     cfgs.add(2)
     work = {}  # each config's inputs, for the CPU baseline
