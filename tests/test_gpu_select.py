@@ -1,7 +1,8 @@
 """GPU parity of the selection kernel (repetition penalty, greedy, top-p -> top-k -> temperature
 draw, verify) against the reference's golden ids and the CPU oracle. Token ids and penalised
 logits are compared bit-exactly. For sampled draws the oracle's cut and draw margins are
-printed: a mismatch could only come from libm/summation-order differences within that margin."""
+recorded for the run's summary line; a decision within the summation's rounding of its
+threshold is taken with the reference's own additions and row total, so none may differ."""
 import hashlib
 import os
 import subprocess
@@ -428,3 +429,38 @@ def test_prefix_sums_that_land_on_their_threshold(env, oracle, case):
     for i in range(len(rows)):
         p = params[i]
         assert int(tok[i]) == oracle.sample_token(rows[i], p.temperature, p.top_p, p.top_k, u=p.uniform), (case, i)
+
+
+@pytest.mark.ties
+def test_cut_within_the_totals_rounding(env, oracle):
+    # The reference's row total adds the vocab exponentials in index order, and terms under half
+    # an ulp of the running total are dropped: two equal maxima first and a tail of exp(-36.05)
+    # ~ 2.19e-16 each leave it exactly 2.0, while any tree of partial sums keeps ~5.7e-11 of the
+    # tail. At p = 1/2 the first prefix then equals p in the reference (cut 1, token 0 whatever
+    # the draw) and lies 2.9e-11 below it with a tree total (cut 2, token 1 for u > 1/2). Such a
+    # cut is decided with the reference's own total. Rows through the wave-record path, the
+    # long path (top_k > 256) and the slice path (a penalty over more ids than the hash takes),
+    # with rows whose cut has a wide margin beside them.
+    torch, dev, t, sel = env
+    row = np.full(V, np.float32(-36.05), np.float32)
+    row[:2] = 0.0
+    rng = np.random.default_rng(71)
+    hist = rng.integers(2, V, 5000).astype(np.uint32)  # tail ids only: the maxima stay as they are
+    # one launch per path: a penalty over more ids than the hash takes sends the whole launch
+    # through the slice kernels
+    launches = [
+        [("records", rp(t, 1.0, 0.5, 0, 0.75), 0),
+         ("records k40", rp(t, 1.0, 0.5, 40, 0.999), 0),
+         ("records wide margin", rp(t, 1.0, 0.4, 0, 0.75), 0),
+         ("long k300", rp(t, 1.0, 0.5, 300, 0.75), 0),
+         ("long k300 wide margin", rp(t, 1.0, 0.6, 300, 0.75), 1)],
+        [("slice", rp(t, 1.0, 0.5, 0, 0.75, rep=1.5, off=0, n=len(hist)), 0),
+         ("slice wide margin", rp(t, 1.0, 0.6, 0, 0.75, rep=1.5, off=0, n=len(hist)), 1)],
+    ]
+    for cases in launches:
+        rows = np.tile(row, (len(cases), 1))
+        tok, pen = select_rows(env, rows, [c[1] for c in cases], history=hist)
+        for i, (name, p, expect) in enumerate(cases):
+            want = oracle.sample_token(pen[i], p.temperature, p.top_p, p.top_k, u=p.uniform)
+            assert want == expect, name
+            assert int(tok[i]) == want, name

@@ -533,3 +533,26 @@ def test_gen_lm_head_formula(oracle):
     # the rows are a pure function of the global row index
     W2, S2, B2 = oracle.gen_lm_head(seed, rows + row0, d)
     assert np.array_equal(W2[row0:], W) and np.array_equal(S2[row0:], S)
+
+
+def _absorbed_tail_row(n=262144):
+    # two equal maxima first, then a tail whose terms exp(-36.05) ~ 2.19e-16 each lie under half
+    # an ulp of the running total 2.0 (2^-52 ~ 2.22e-16): the reference's in-order total drops
+    # every one of them and stays exactly 2.0, while any tree of partial sums keeps ~5.7e-11 of
+    # them. With p = 1/2 the first prefix, 1/total, is then exactly p in the reference.
+    row = np.full(n, np.float32(-36.05), np.float32)
+    row[:2] = 0.0
+    return row
+
+
+def test_absorbed_tail_total(oracle, reference):
+    row = _absorbed_tail_row()
+    terms = np.exp(row.astype(np.float64) - 0.0)
+    assert np.cumsum(terms)[-1] == 2.0                    # in index order: every tail term drops
+    assert np.sum(terms) - 2.0 > 5e-11                    # pairwise: the tail's mass survives
+    # cut = 1 at p = 1/2, so the token is the first maximum whatever the draw; a total with the
+    # tail's mass would put the cut at 2 and draw index 1 for u > 1/2
+    for u in (0.25, 0.75, 0.999):
+        assert oracle.sample_token(row, 1.0, 0.5, 0, u=u) == 0
+    seed = next(s for s in range(1, 1000) if oracle.uniform_from_seed(s) > 0.5)
+    assert reference.sample_token(row, 1.0, 0.5, 0, seed) == 0

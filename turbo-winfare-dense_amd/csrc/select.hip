@@ -81,14 +81,14 @@ struct MergeShared {
 // After c.top[0..want) holds the row's shortlist and c.gmax/total/flag its statistics:
 // the degenerate check of sampling.cpp:116-118, the shortlist sort, and steps 5-7.
 __device__ __forceinline__ void finish_row(SelCommon& c, uint32_t want, const twd_row_params& p,
-                           uint32_t* token_out) {
+                           uint32_t* token_out, const float* row_logits, uint32_t vocab) {
     const int tid = threadIdx.x;
     if (c.flag != 0 || !(c.total > 0.0)) {
         if (tid == 0) *token_out = TWD_TOKEN_DEGENERATE;
         return;
     }
     block_sort_desc(c, want);
-    const uint32_t tok = finish_sampled(c, want, p, c.gmax, c.total);
+    const uint32_t tok = finish_sampled(c, want, p, c.total, RowSrc{row_logits, vocab, c.gmax});
     if (tid == 0) *token_out = tok;
 }
 
@@ -287,7 +287,7 @@ void select_slice_kernel(SelectArgs args_by_value, SelectBufs b) {
         sh.c.flag = nan_seen;
     }
     __syncthreads();
-    finish_row(sh.c, want_row, p, b.tokens + row);
+    finish_row(sh.c, want_row, p, b.tokens + row, b.logits + static_cast<size_t>(row) * b.stride, b.vocab);
 }
 
 // Second launch when a row spans several slices: global max, the rescaled sum of exponentials,
@@ -393,7 +393,7 @@ __global__ __launch_bounds__(kMergeThreads) void select_merge_kernel(SelectArgs 
     const int per = static_cast<int>((n_cand + NT - 1) / NT);
     block_top<NT, kMergePerThread>(merge_val, merge_key, merge_val, merge_key, per, gm, cmn, want_row,
                                    sh.c.top, sh.t, sh.c);
-    finish_row(sh.c, want_row, p, b.tokens + row);
+    finish_row(sh.c, want_row, p, b.tokens + row, b.logits + static_cast<size_t>(row) * b.stride, b.vocab);
 }
 
 // ---- after the head's sample mode (or the wave-record pass): one block per row --------------------
@@ -646,6 +646,8 @@ __global__ __launch_bounds__(kLongThreads) void long_sort_merge_kernel(LongBufs 
 struct LongFinishShared {
     double e[kFinTile];  // exp(l - max) / total, then lane 1's running sums
     double q[kFinTile];  // exp((l - max) / T), then lane 0's running sums
+    double base;         // lane 1's running sum before the tile
+    double total;        // the reference's row total, when the cut takes it
     uint32_t misc[4];
     uint32_t best;
 };
@@ -663,66 +665,94 @@ __global__ __launch_bounds__(kLongThreads) void long_finish_kernel(LongArgs args
     double* pre = b.pre + static_cast<size_t>(j) * b.npad;
     const uint32_t want = min(static_cast<uint32_t>(p.top_k), b.vocab);
     const double mx = static_cast<double>(b.gmax[j]);
-    const double total = b.total[j];
+    double total = b.total[j];
     const double td = static_cast<double>(p.temperature);
     const bool topp = p.top_p < 1.0f;
     const double pp = static_cast<double>(p.top_p);
     constexpr uint32_t kChunk = 16;
-    double run = 0.0;  // wave 0: lane 0's sum of the weights, lane 1's top-p sum
     uint32_t cut = want;
-    if (tid == 0) sh.misc[0] = 0;
-    for (uint32_t t0 = 0; t0 < want; t0 += kFinTile) {
-        const uint32_t cnt = min(kFinTile, want - t0);
-        // steps 5 and 7's terms, as sampling.cpp:145 and :157 form them
-        for (uint32_t i = tid; i < cnt; i += NT) {
-            const double l = static_cast<double>(rank_value(keys[t0 + i]));
-            sh.q[i] = exp_libm((l - mx) / td);
-            if (topp) sh.e[i] = exp_libm(l - mx) / total;
-        }
-        __syncthreads();
-        if (wave == 0 && lane < 2) {
-            // lane 0 reads q and stores its running sums over q; lane 1 does the same over e
-            // (over q when top-p is off: its sums are then never used)
-            double* src = (lane == 0 || !topp) ? sh.q : sh.e;
-            double x[kChunk];
-#pragma unroll
-            for (uint32_t jj = 0; jj < kChunk; ++jj) x[jj] = src[min(jj, cnt - 1)];
-            for (uint32_t i0 = 0; i0 < cnt; i0 += kChunk) {
-                double xn[kChunk], pr[kChunk];
-                if (i0 + kChunk < cnt) {
-#pragma unroll
-                    for (uint32_t jj = 0; jj < kChunk; ++jj) xn[jj] = src[min(i0 + kChunk + jj, cnt - 1)];
-                }
-#pragma unroll
-                for (uint32_t jj = 0; jj < kChunk; ++jj) {
-                    run += x[jj];
-                    pr[jj] = run;
-                }
-                uint32_t hit = 0;
-#pragma unroll
-                for (uint32_t jj = 0; jj < kChunk; ++jj) {
-                    src[i0 + jj] = pr[jj];  // i0 + jj < cnt rounded up to kChunk <= kFinTile
-                    hit |= (pr[jj] >= pp ? 1u : 0u) << jj;
-                }
-                uint32_t h1 = __builtin_amdgcn_readlane(hit, 1);
-                h1 &= cnt - i0 >= kChunk ? 0xFFFFu : ((1u << (cnt - i0)) - 1u);
-                if (topp && h1 != 0) {  // lane 0's sums cover the cut
-                    if (lane == 0) sh.misc[0] = t0 + i0 + static_cast<uint32_t>(__builtin_ctz(h1)) + 1;
-                    break;
-                }
-#pragma unroll
-                for (uint32_t jj = 0; jj < kChunk; ++jj) x[jj] = xn[jj];
+    // a second pass with the reference's own row total when the first pass's cut lies within
+    // total_tol of p (see finish_sums_exact)
+    for (int pass = 0;; ++pass) {
+        double run = 0.0;  // wave 0: lane 0's sum of the weights, lane 1's top-p sum
+        uint32_t tl = 0;   // the last tile's first entry
+        cut = want;
+        if (tid == 0) sh.misc[0] = 0;
+        for (uint32_t t0 = 0; t0 < want; t0 += kFinTile) {
+            tl = t0;
+            const uint32_t cnt = min(kFinTile, want - t0);
+            // steps 5 and 7's terms, as sampling.cpp:145 and :157 form them
+            for (uint32_t i = tid; i < cnt; i += NT) {
+                const double l = static_cast<double>(rank_value(keys[t0 + i]));
+                sh.q[i] = exp_libm((l - mx) / td);
+                if (topp) sh.e[i] = exp_libm(l - mx) / total;
             }
+            __syncthreads();
+            if (wave == 0 && lane < 2) {
+                // lane 0 reads q and stores its running sums over q; lane 1 does the same over e
+                // (over q when top-p is off: its sums are then never used)
+                double* src = (lane == 0 || !topp) ? sh.q : sh.e;
+                if (lane == 1) sh.base = run;  // the top-p sum before the tile
+                double x[kChunk];
+#pragma unroll
+                for (uint32_t jj = 0; jj < kChunk; ++jj) x[jj] = src[min(jj, cnt - 1)];
+                for (uint32_t i0 = 0; i0 < cnt; i0 += kChunk) {
+                    double xn[kChunk], pr[kChunk];
+                    if (i0 + kChunk < cnt) {
+#pragma unroll
+                        for (uint32_t jj = 0; jj < kChunk; ++jj) xn[jj] = src[min(i0 + kChunk + jj, cnt - 1)];
+                    }
+#pragma unroll
+                    for (uint32_t jj = 0; jj < kChunk; ++jj) {
+                        run += x[jj];
+                        pr[jj] = run;
+                    }
+                    uint32_t hit = 0;
+#pragma unroll
+                    for (uint32_t jj = 0; jj < kChunk; ++jj) {
+                        src[i0 + jj] = pr[jj];  // i0 + jj < cnt rounded up to kChunk <= kFinTile
+                        hit |= (pr[jj] >= pp ? 1u : 0u) << jj;
+                    }
+                    uint32_t h1 = __builtin_amdgcn_readlane(hit, 1);
+                    h1 &= cnt - i0 >= kChunk ? 0xFFFFu : ((1u << (cnt - i0)) - 1u);
+                    if (topp && h1 != 0) {  // lane 0's sums cover the cut
+                        if (lane == 0) sh.misc[0] = t0 + i0 + static_cast<uint32_t>(__builtin_ctz(h1)) + 1;
+                        break;
+                    }
+#pragma unroll
+                    for (uint32_t jj = 0; jj < kChunk; ++jj) x[jj] = xn[jj];
+                }
+            }
+            __syncthreads();
+            const uint32_t c = sh.misc[0];  // the cut, once the top-p sum has reached p
+            const uint32_t keep = c != 0 ? c - t0 : cnt;
+            for (uint32_t i = tid; i < keep; i += NT) pre[t0 + i] = sh.q[i];
+            if (c != 0) {
+                cut = c;
+                break;
+            }
+            __syncthreads();  // the next tile's terms overwrite sh
+        }
+        if (!topp || pass > 0) break;
+        // the last tile's top-p sums are in sh.e: the one at the cut (at want - 1 when there is
+        // none) and the one before it decide
+        if (tid == 0) {
+            const double tc = total_tol(b.vocab);
+            const double hi = sh.e[cut - 1 - tl];
+            const double lo = cut >= 2 ? (cut - 2 >= tl ? sh.e[cut - 2 - tl] : sh.base) : 0.0;
+            const bool near = (hi >= pp * (1.0 - tc) && hi <= pp * (1.0 + tc)) ||
+                              (cut >= 2 && lo >= pp * (1.0 - tc) && lo <= pp * (1.0 + tc));
+            sh.misc[2] = near ? 1u : 0u;
         }
         __syncthreads();
-        const uint32_t c = sh.misc[0];  // the cut, once the top-p sum has reached p
-        const uint32_t keep = c != 0 ? c - t0 : cnt;
-        for (uint32_t i = tid; i < keep; i += NT) pre[t0 + i] = sh.q[i];
-        if (c != 0) {
-            cut = c;
-            break;
+        if (sh.misc[2] == 0) break;
+        if (wave == 0) {
+            const double t = exact_row_total(RowSrc{b.logits + static_cast<size_t>(row) * b.stride, b.vocab,
+                                                    b.gmax[j]}, sh.e);
+            if (lane == 0) sh.total = t;
         }
-        __syncthreads();  // the next tile's terms overwrite sh
+        __syncthreads();
+        total = sh.total;
     }
     if (p.top_k > 0 && cut > static_cast<uint32_t>(p.top_k)) cut = static_cast<uint32_t>(p.top_k);
     if (cut < 1) cut = 1;

@@ -422,16 +422,66 @@ __device__ __forceinline__ void shortlist_pad(SelCommon& c, uint32_t want) {
     }
 }
 
-__device__ __forceinline__ uint32_t finish_sums(SelCommon& c, uint32_t want, const twd_row_params& p);
-__device__ __forceinline__ uint32_t finish_sums_exact(SelCommon& c, uint32_t want, const twd_row_params& p);
+// The row a shortlist was taken from: its (penalised) logits and maximum, for the reference's
+// own row total when a top-p cut lies within that total's rounding of p.
+struct RowSrc {
+    const float* logits;
+    uint32_t vocab;
+    float gmax;
+};
+
+// How far (relative) a top-p prefix formed with this build's row total may lie from the
+// reference's. The reference adds the row's vocab exponentials one after another, and a
+// recursive sum of n non-negative terms lies within (n - 1) 2^-53 of their exact sum (terms
+// under half an ulp of the running sum are dropped, so the bound is reached on rows with long
+// tails); this build's total (partial sums at most a few dozen additions deep, rescaled once or
+// twice, table exponentials within 2 ulp) within 256 2^-53, and the prefixes' own additions (at
+// most 256 per prefix, each term one division) within 512 2^-53. Doubled, with room to spare,
+// for the margin the decisions keep.
+__device__ __forceinline__ double total_tol(uint32_t vocab) {
+    return static_cast<double>(vocab + 2048u) * 0x1p-52;
+}
+
+// The reference's row total (sampling.cpp:113-115): exp((double)l - max) over the row in index
+// order, each term glibc's exp, added one after another. Wave 0 only (every lane calls): the
+// lanes form 256 terms at a time into stage[0..256), lane 0 adds them in order. Milliseconds at
+// V = 262,144: taken only for a top-p cut within total_tol of p.
+__device__ __forceinline__ double exact_row_total(const RowSrc& src, double* stage) {
+    const int lane = threadIdx.x & 63;
+    const double mx = static_cast<double>(src.gmax);
+    double run = 0.0;
+    for (uint32_t i0 = 0; i0 < src.vocab; i0 += 256) {
+#pragma unroll 1
+        for (uint32_t j = 0; j < 4; ++j) {
+            const uint32_t i = i0 + 64 * j + static_cast<uint32_t>(lane);
+            stage[64 * j + lane] = i < src.vocab ? exp_libm(static_cast<double>(src.logits[i]) - mx) : 0.0;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane == 0) {
+            const uint32_t n = min(256u, src.vocab - i0);
+            for (uint32_t k = 0; k < n; ++k) run += stage[k];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    return readlane_f64(run, 0);
+}
+
+__device__ __forceinline__ uint32_t finish_sums(SelCommon& c, uint32_t want, const twd_row_params& p,
+                                                const RowSrc& src);
+__device__ __noinline__ uint32_t finish_sums_exact(SelCommon& c, uint32_t want, const twd_row_params& p,
+                                                      const RowSrc& src);
 
 __device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, const twd_row_params& p,
-                                                   float gmax, double total) {
+                                                   double total, const RowSrc& src) {
     const uint32_t tid = threadIdx.x;
-    if (tid < want) shortlist_terms(c, tid, c.sorted[tid], gmax, total, p);
+    if (tid < want) shortlist_terms(c, tid, c.sorted[tid], src.gmax, total, p);
     shortlist_pad(c, want);
     __syncthreads();
-    return finish_sums(c, want, p);
+    return finish_sums(c, want, p, src);
 }
 
 // Steps 5-7 after the terms c.e[0..want), c.q[0..want) (zero-padded) have been published.
@@ -442,14 +492,17 @@ __device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, 
 // the prefix. Each decision of steps 5-7 compares a prefix with a threshold (the top-p cut: the
 // first running sum >= p; the draw: the first running sum of q >= u * the sum at the cut), and
 // the prefixes never decrease, so a decision is the reference's whenever the prefixes on both
-// sides of it lie further than kSumTol (relative) from its threshold. Otherwise (a prefix that
-// close, e.g. an exact tie) finish_sums_exact repeats steps 5-7 with the reference's additions.
+// sides of it lie further than kSumTol (relative) from its threshold, and for the top-p cut
+// further than kSumTol + total_tol, since its terms are divided by this build's row total.
+// Otherwise (a prefix that close, e.g. an exact tie) finish_sums_exact repeats steps 5-7 with the
+// reference's additions.
 constexpr double kSumTol = 0x1p-36;
 
 // TPL terms per lane of wave 0: lane l holds terms TPL l .. TPL l + TPL - 1 and their running
 // sums (TPL = 1 for shortlists of up to 64 terms: each prefix is then the scan's own value).
 template <uint32_t TPL>
-__device__ __forceinline__ uint32_t finish_sums_par(SelCommon& c, uint32_t want, const twd_row_params& p) {
+__device__ __forceinline__ uint32_t finish_sums_par(SelCommon& c, uint32_t want, const twd_row_params& p,
+                                                    const RowSrc& src) {
     const int lane = threadIdx.x & 63;
     const uint32_t padded = (want + kFinishChunk - 1) & ~(kFinishChunk - 1);  // <= 64 * TPL
     const uint32_t i0 = TPL * static_cast<uint32_t>(lane);
@@ -503,12 +556,13 @@ __device__ __forceinline__ uint32_t finish_sums_par(SelCommon& c, uint32_t want,
     uint32_t cut = want;
     if (p.top_p < 1.0f) {
         const double pp = static_cast<double>(p.top_p);
+        const double tc = kSumTol + total_tol(src.vocab);
         uint32_t i = 0;
         if (first(pe, want, pp, i)) {
             cut = i + 1;
-            ok = at(pe, i) >= pp * (1.0 + kSumTol) && (i == 0 || at(pe, i - 1) < pp * (1.0 - kSumTol));
+            ok = at(pe, i) >= pp * (1.0 + tc) && (i == 0 || at(pe, i - 1) < pp * (1.0 - tc));
         } else {
-            ok = at(pe, want - 1) < pp * (1.0 - kSumTol);
+            ok = at(pe, want - 1) < pp * (1.0 - tc);
         }
     }
     if (p.top_k > 0 && cut > static_cast<uint32_t>(p.top_k)) cut = static_cast<uint32_t>(p.top_k);
@@ -520,68 +574,93 @@ __device__ __forceinline__ uint32_t finish_sums_par(SelCommon& c, uint32_t want,
     else
         ok = false;
     if (ok) return rank_index(c.sorted[pick]);
-    return finish_sums_exact(c, want, p);
+    return finish_sums_exact(c, want, p, src);
 }
 
-__device__ __forceinline__ uint32_t finish_sums(SelCommon& c, uint32_t want, const twd_row_params& p) {
+__device__ __forceinline__ uint32_t finish_sums(SelCommon& c, uint32_t want, const twd_row_params& p,
+                                                const RowSrc& src) {
     if (threadIdx.x >= 64) return 0;
-    return want <= 64 ? finish_sums_par<1>(c, want, p) : finish_sums_par<4>(c, want, p);
+    return want <= 64 ? finish_sums_par<1>(c, want, p, src) : finish_sums_par<4>(c, want, p, src);
 }
 
 // Steps 5-7 with the reference's running sums: lanes 0 and 1 of wave 0 (every lane of it calls).
-__device__ __forceinline__ uint32_t finish_sums_exact(SelCommon& c, uint32_t want, const twd_row_params& p) {
+// When a prefix on either side of the top-p cut lies within total_tol of p, the terms are formed
+// again with the reference's own row total (exact_row_total) and the sums repeated.
+__device__ __noinline__ uint32_t finish_sums_exact(SelCommon& c, uint32_t want, const twd_row_params& p,
+                                                      const RowSrc& src) {
     const int tid = threadIdx.x, lane = tid & 63;
     constexpr uint32_t kChunk = kFinishChunk;
     if (tid >= 64) return 0;
     const bool topp = p.top_p < 1.0f;
     const double pp = static_cast<double>(p.top_p);
     uint32_t cut = want;
-    if (lane < 2) {
-        // lane 0 reads q and stores its running sums over q; lane 1 reads e and stores its own
-        // (unused) over e, so that no store needs a branch
-        double* src = lane == 0 ? c.q : c.e;
-        double run = 0.0;
-        auto load = [&](double (&x)[kChunk], uint32_t i0) {
-            const double2* s2 = reinterpret_cast<const double2*>(src + i0);
+    for (int pass = 0;; ++pass) {
+        cut = want;
+        if (lane < 2) {
+            // lane 0 reads q and stores its running sums over q; lane 1 reads e and stores its own
+            // over e, so that no store needs a branch
+            double* srcv = lane == 0 ? c.q : c.e;
+            double run = 0.0;
+            auto load = [&](double (&x)[kChunk], uint32_t i0) {
+                const double2* s2 = reinterpret_cast<const double2*>(srcv + i0);
 #pragma unroll
-            for (uint32_t j = 0; j < kChunk / 2; ++j) {
-                const double2 v = s2[j];
-                x[2 * j] = v.x;
-                x[2 * j + 1] = v.y;
+                for (uint32_t j = 0; j < kChunk / 2; ++j) {
+                    const double2 v = s2[j];
+                    x[2 * j] = v.x;
+                    x[2 * j + 1] = v.y;
+                }
+            };
+            // the running sums of chunk i0, stored over its terms; true when it holds the cut
+            auto step = [&](const double (&x)[kChunk], uint32_t i0) -> bool {
+                double pre[kChunk];
+#pragma unroll
+                for (uint32_t j = 0; j < kChunk; ++j) {
+                    run += x[j];
+                    pre[j] = run;
+                }
+                double2* d2 = reinterpret_cast<double2*>(srcv + i0);
+#pragma unroll
+                for (uint32_t j = 0; j < kChunk / 2; ++j) d2[j] = make_double2(pre[2 * j], pre[2 * j + 1]);
+                // lane 1's sums decide; past want they repeat the sum at want - 1
+                if (!topp || __builtin_amdgcn_readlane(pre[kChunk - 1] >= pp ? 1u : 0u, 1) == 0) return false;
+                uint32_t hit = 0;
+#pragma unroll
+                for (uint32_t j = 0; j < kChunk; ++j) hit |= (pre[j] >= pp ? 1u : 0u) << j;
+                const uint32_t h1 = __builtin_amdgcn_readlane(hit, 1);
+                cut = i0 + static_cast<uint32_t>(__builtin_ctz(h1)) + 1;  // h1 != 0: its top bit is set
+                return true;
+            };
+            // two chunks in flight: the next chunk's terms are read before this chunk's sums are
+            // stored (it lies at i0 + kChunk, below padded when i0 + kChunk < want)
+            double xa[kChunk], xb[kChunk];
+            load(xa, 0);
+            for (uint32_t i0 = 0; i0 < want; i0 += 2 * kChunk) {
+                if (i0 + kChunk < want) load(xb, i0 + kChunk);
+                if (step(xa, i0) || i0 + kChunk >= want) break;
+                if (i0 + 2 * kChunk < want) load(xa, i0 + 2 * kChunk);
+                if (step(xb, i0 + kChunk)) break;
             }
-        };
-        // the running sums of chunk i0, stored over its terms; true when it holds the cut
-        auto step = [&](const double (&x)[kChunk], uint32_t i0) -> bool {
-            double pre[kChunk];
-#pragma unroll
-            for (uint32_t j = 0; j < kChunk; ++j) {
-                run += x[j];
-                pre[j] = run;
-            }
-            double2* d2 = reinterpret_cast<double2*>(src + i0);
-#pragma unroll
-            for (uint32_t j = 0; j < kChunk / 2; ++j) d2[j] = make_double2(pre[2 * j], pre[2 * j + 1]);
-            // lane 1's sums decide; past want they repeat the sum at want - 1
-            if (!topp || __builtin_amdgcn_readlane(pre[kChunk - 1] >= pp ? 1u : 0u, 1) == 0) return false;
-            uint32_t hit = 0;
-#pragma unroll
-            for (uint32_t j = 0; j < kChunk; ++j) hit |= (pre[j] >= pp ? 1u : 0u) << j;
-            const uint32_t h1 = __builtin_amdgcn_readlane(hit, 1);
-            cut = i0 + static_cast<uint32_t>(__builtin_ctz(h1)) + 1;  // h1 != 0: its top bit is set
-            return true;
-        };
-        // two chunks in flight: the next chunk's terms are read before this chunk's sums are
-        // stored (it lies at i0 + kChunk, below padded when i0 + kChunk < want)
-        double xa[kChunk], xb[kChunk];
-        load(xa, 0);
-        for (uint32_t i0 = 0; i0 < want; i0 += 2 * kChunk) {
-            if (i0 + kChunk < want) load(xb, i0 + kChunk);
-            if (step(xa, i0) || i0 + kChunk >= want) break;
-            if (i0 + 2 * kChunk < want) load(xa, i0 + 2 * kChunk);
-            if (step(xb, i0 + kChunk)) break;
         }
+        cut = __builtin_amdgcn_readfirstlane(cut);
+        if (!topp || pass > 0 || !src.logits) break;
+        // c.e holds the top-p running sums up to the cut (all of them when there is none): the
+        // one at the cut and the one before it decide
+        const double tc = total_tol(src.vocab);
+        const double hi = c.e[cut - 1], lo = cut >= 2 ? c.e[cut - 2] : 0.0;
+        const bool near = (hi >= pp * (1.0 - tc) && hi <= pp * (1.0 + tc)) ||
+                          (cut >= 2 && lo >= pp * (1.0 - tc) && lo <= pp * (1.0 + tc));
+        if (!near) break;
+        const double total = exact_row_total(src, c.e);
+        for (uint32_t i = static_cast<uint32_t>(lane); i < want; i += 64)
+            shortlist_terms(c, i, c.sorted[i], src.gmax, total, p);
+        for (uint32_t i = want + static_cast<uint32_t>(lane); i < ((want + kChunk - 1) & ~(kChunk - 1)); i += 64) {
+            c.e[i] = 0.0;
+            c.q[i] = 0.0;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    cut = __builtin_amdgcn_readfirstlane(cut);
     if (p.top_k > 0 && cut > static_cast<uint32_t>(p.top_k)) cut = static_cast<uint32_t>(p.top_k);
     if (cut < 1) cut = 1;
     const double r = static_cast<double>(p.uniform) * c.q[cut - 1];  // r = u * denom
@@ -965,7 +1044,7 @@ __device__ __forceinline__ void sample_merge_row_per(const twd_row_params& p, ui
         }
         shortlist_pad(sh.c, want);
         __syncthreads();
-        const uint32_t tok = finish_sums(sh.c, want, p);
+        const uint32_t tok = finish_sums(sh.c, want, p, RowSrc{lg, b.vocab, gm});
         if (tid == 0) b.tokens[row] = tok;
         return;
     } else if (n <= static_cast<uint32_t>(NT)) {
@@ -1009,7 +1088,7 @@ __device__ __forceinline__ void sample_merge_row_per(const twd_row_params& p, ui
         __syncthreads();
         block_sort_desc(sh.c, want);
     }
-    const uint32_t tok = finish_sampled(sh.c, want, p, gm, total);
+    const uint32_t tok = finish_sampled(sh.c, want, p, total, RowSrc{lg, b.vocab, gm});
     if (tid == 0) b.tokens[row] = tok;
 }
 
