@@ -71,37 +71,43 @@ struct HeadArgs {
     SampleStats stats;
 };
 
-// speculator.cpp:46-69 and :138-150, greedy branch, over per-row target tokens tok[0..rows).
+// speculator.cpp:46-69 and :138-150, greedy branch, over per-row target tokens tok[0..rows)
+// (in LDS). Called by every lane of wave 0: lane i reads draft i, so the drafts cost one memory
+// round trip, and a ballot finds the first mismatch. The reference's loop accepts drafts while
+// they equal the target tokens and then emits the target token at the first mismatch (or, with
+// every draft accepted and a row past them, that row's token as the bonus), so the emitted
+// tokens are tok[0..n). n <= rows <= 64 (a bonus needs rows > the accepted count).
 __device__ void verify_bookkeeping(const uint32_t* tok, uint32_t rows, const uint32_t* drafts,
                                    uint32_t nd, twd_verify_result* v) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t k = (nd != 0 && rows != 0) ? (nd < rows ? nd : rows) : 0u;  // <= 64
+    const bool live = lane < k;
+    const uint32_t d = live ? drafts[lane] : 0u;
+    const uint32_t t = live ? tok[lane] : 0u;
+    const uint64_t miss = __ballot(live && d != t);
     uint32_t n = 0, acc = 0, bonus = 0, sampled = 0;
-    if (nd != 0 && rows != 0) {
-        const uint32_t k = nd < rows ? nd : rows;
-        bool rejected = false;
-        for (uint32_t i = 0; i < k; ++i) {
-            const uint32_t t = tok[i];
-            if (drafts[i] == t) {
-                v->tokens[n++] = t;
-                ++acc;
-            } else {
-                bonus = t;
-                sampled = 1;
-                v->tokens[n++] = t;
-                rejected = true;
-                break;
-            }
-        }
-        if (!rejected && rows > k) {
+    if (miss != 0) {
+        acc = static_cast<uint32_t>(__ffsll(static_cast<long long>(miss)) - 1);
+        n = acc + 1;
+        bonus = tok[acc];
+        sampled = 1;
+    } else if (k != 0) {
+        acc = k;
+        n = k;
+        if (rows > k) {
             bonus = tok[k];
             sampled = 1;
-            v->tokens[n++] = bonus;
+            n = k + 1;
         }
     }
-    v->n_tokens = n;
-    v->num_accepted = acc;
-    v->total_drafted = nd;
-    v->bonus_token_sampled = sampled;
-    v->bonus_token = bonus;
+    if (lane < n) v->tokens[lane] = tok[lane];
+    if (lane == 0) {
+        v->n_tokens = n;
+        v->num_accepted = acc;
+        v->total_drafted = nd;
+        v->bonus_token_sampled = sampled;
+        v->bonus_token = bonus;
+    }
 }
 
 __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
@@ -303,7 +309,7 @@ __device__ __forceinline__ void grid_finish(const HeadArgs& a, EpiSharedT<NW>& s
         if (a.tokens) a.tokens[tid] = t;
     }
     __syncthreads();
-    if (tid == 0 && a.vres) verify_bookkeeping(se.tok, a.M, a.drafts, a.n_drafts, a.vres);
+    if (tid < 64 && a.vres) verify_bookkeeping(se.tok, a.M, a.drafts, a.n_drafts, a.vres);
 }
 
 // Sample mode of the resident-h kernel. With rows spread four apart (MS = 4, M <= 4) row m's
