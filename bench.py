@@ -351,7 +351,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the sharded design is described in DESIGN.md)", file=sys.stderr)
+              "(the vocabulary-sharded form across GPUs is a design, not built)", file=sys.stderr)
         sys.exit(2)
 
     import torch

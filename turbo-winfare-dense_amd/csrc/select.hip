@@ -734,13 +734,13 @@ __global__ __launch_bounds__(kLongThreads) void long_finish_kernel(LongArgs args
             __syncthreads();  // the next tile's terms overwrite sh
         }
         if (!topp || pass > 0) break;
-        // the last tile's top-p sums are in sh.e: the one at the cut (at want - 1 when there is
-        // none) and the one before it decide
+        // the last tile's top-p sums are in sh.e: the one at the cut (when it reached p) and the
+        // one before it decide (as in finish_sums_exact)
         if (tid == 0) {
             const double tc = total_tol(b.vocab);
             const double hi = sh.e[cut - 1 - tl];
             const double lo = cut >= 2 ? (cut - 2 >= tl ? sh.e[cut - 2 - tl] : sh.base) : 0.0;
-            const bool near = (hi >= pp * (1.0 - tc) && hi <= pp * (1.0 + tc)) ||
+            const bool near = (hi >= pp && hi <= pp * (1.0 + tc)) ||
                               (cut >= 2 && lo >= pp * (1.0 - tc) && lo <= pp * (1.0 + tc));
             sh.misc[2] = near ? 1u : 0u;
         }

@@ -644,10 +644,11 @@ __device__ __noinline__ uint32_t finish_sums_exact(SelCommon& c, uint32_t want, 
         cut = __builtin_amdgcn_readfirstlane(cut);
         if (!topp || pass > 0 || !src.logits) break;
         // c.e holds the top-p running sums up to the cut (all of them when there is none): the
-        // one at the cut and the one before it decide
+        // one at the cut (when it reached p; a last sum below p gives the same cut, want, either
+        // way) and the one before it decide
         const double tc = total_tol(src.vocab);
         const double hi = c.e[cut - 1], lo = cut >= 2 ? c.e[cut - 2] : 0.0;
-        const bool near = (hi >= pp * (1.0 - tc) && hi <= pp * (1.0 + tc)) ||
+        const bool near = (hi >= pp && hi <= pp * (1.0 + tc)) ||
                           (cut >= 2 && lo >= pp * (1.0 - tc) && lo <= pp * (1.0 + tc));
         if (!near) break;
         const double total = exact_row_total(src, c.e);
