@@ -556,3 +556,32 @@ def test_absorbed_tail_total(oracle, reference):
         assert oracle.sample_token(row, 1.0, 0.5, 0, u=u) == 0
     seed = next(s for s in range(1, 1000) if oracle.uniform_from_seed(s) > 0.5)
     assert reference.sample_token(row, 1.0, 0.5, 0, seed) == 0
+
+
+def test_row_total_rounding_bound():
+    # The device keeps a top-p cut away from p by (V + 2048) * 2^-52 (relative) unless it forms the
+    # reference's own total; that allowance rests on the in-order double sum of V non-negative
+    # terms lying within (V - 1) * 2^-53 of any other order's sum (each term of which is within a
+    # few dozen roundings of exact). Rows built to approach the bound (tails just under half an
+    # ulp of the running total, which the in-order sum drops) and ordinary rows.
+    rng = np.random.default_rng(5)
+    n = 262144
+    rows = []
+    for tail in (-36.05, -36.5, -38.0, -40.0):
+        r = np.full(n, np.float32(tail), np.float32)
+        r[:2] = 0.0
+        rows.append(r)
+    rows.append(rng.standard_normal(n).astype(np.float32) * 3)
+    rows.append(np.sort(rng.standard_normal(n).astype(np.float32) * 5)[::-1].copy())
+    worst = 0.0
+    for r in rows:
+        terms = np.exp(r.astype(np.float64) - float(r.max()))
+        seq = np.cumsum(terms)[-1]                                # the reference's order
+        blocked = np.sum(np.sum(terms.reshape(-1, 64), axis=1))   # per-64 records, then a tree
+        pairwise = np.sum(terms)
+        for other in (blocked, pairwise):
+            rel = abs(other - seq) / seq
+            worst = max(worst, rel / ((n - 1) * 2.0 ** -53))
+            assert rel <= (n + 2048) * 2.0 ** -53
+    # the tail rows reach a large part of the bound: it is not a loose estimate
+    assert worst > 0.25
