@@ -473,7 +473,7 @@ __device__ __forceinline__ double exact_row_total(const RowSrc& src, double* sta
 __device__ __forceinline__ uint32_t finish_sums(SelCommon& c, uint32_t want, const twd_row_params& p,
                                                 const RowSrc& src);
 __device__ __noinline__ uint32_t finish_sums_exact(SelCommon& c, uint32_t want, const twd_row_params& p,
-                                                      const RowSrc& src);
+                                                   const RowSrc& src);
 
 __device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, const twd_row_params& p,
                                                    double total, const RowSrc& src) {
@@ -587,7 +587,7 @@ __device__ __forceinline__ uint32_t finish_sums(SelCommon& c, uint32_t want, con
 // When a prefix on either side of the top-p cut lies within total_tol of p, the terms are formed
 // again with the reference's own row total (exact_row_total) and the sums repeated.
 __device__ __noinline__ uint32_t finish_sums_exact(SelCommon& c, uint32_t want, const twd_row_params& p,
-                                                      const RowSrc& src) {
+                                                   const RowSrc& src) {
     const int tid = threadIdx.x, lane = tid & 63;
     constexpr uint32_t kChunk = kFinishChunk;
     if (tid >= 64) return 0;
