@@ -444,24 +444,57 @@ __device__ __forceinline__ double total_tol(uint32_t vocab) {
 
 // The reference's row total (sampling.cpp:113-115): exp((double)l - max) over the row in index
 // order, each term glibc's exp, added one after another. Wave 0 only (every lane calls): the
-// lanes form 256 terms at a time into stage[0..256), lane 0 adds them in order. Milliseconds at
-// V = 262,144: taken only for a top-p cut within total_tol of p.
+// lanes form kTotStep terms at a time into stage[0..kTotStep), with the next step's logits
+// already requested, and lane 0 adds them in order, 16 LDS reads ahead of its additions. About
+// 3.6 ms at V = 262,144 (the additions are one dependent chain): taken only for a top-p cut
+// within total_tol of p.
+constexpr uint32_t kTotStep = 512;
 __device__ __forceinline__ double exact_row_total(const RowSrc& src, double* stage) {
+    constexpr uint32_t kPer = kTotStep / 64;
     const int lane = threadIdx.x & 63;
     const double mx = static_cast<double>(src.gmax);
-    double run = 0.0;
-    for (uint32_t i0 = 0; i0 < src.vocab; i0 += 256) {
-#pragma unroll 1
-        for (uint32_t j = 0; j < 4; ++j) {
+    auto fetch = [&](float (&x)[kPer], uint32_t i0) {
+#pragma unroll
+        for (uint32_t j = 0; j < kPer; ++j) {
             const uint32_t i = i0 + 64 * j + static_cast<uint32_t>(lane);
-            stage[64 * j + lane] = i < src.vocab ? exp_libm(static_cast<double>(src.logits[i]) - mx) : 0.0;
+            x[j] = src.logits[i < src.vocab ? i : src.vocab - 1];
+        }
+    };
+    float xn[kPer];
+    fetch(xn, 0);
+    double run = 0.0;
+    for (uint32_t i0 = 0; i0 < src.vocab; i0 += kTotStep) {
+        float x[kPer];
+#pragma unroll
+        for (uint32_t j = 0; j < kPer; ++j) x[j] = xn[j];
+        if (i0 + kTotStep < src.vocab) fetch(xn, i0 + kTotStep);
+#pragma unroll
+        for (uint32_t j = 0; j < kPer; ++j) {
+            const uint32_t i = i0 + 64 * j + static_cast<uint32_t>(lane);
+            stage[64 * j + lane] = i < src.vocab ? exp_libm(static_cast<double>(x[j]) - mx) : 0.0;
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         if (lane == 0) {
-            const uint32_t n = min(256u, src.vocab - i0);
-            for (uint32_t k = 0; k < n; ++k) run += stage[k];
+            // all kTotStep in order (past the row they are +0, which leaves a sum >= +0
+            // unchanged), 16 at a time, the next 16 requested before these are added
+            double a[16], b[16];
+#pragma unroll
+            for (uint32_t j = 0; j < 16; ++j) a[j] = stage[j];
+#pragma unroll 1
+            for (uint32_t k = 0; k < kTotStep; k += 32) {
+#pragma unroll
+                for (uint32_t j = 0; j < 16; ++j) b[j] = stage[k + 16 + j];
+#pragma unroll
+                for (uint32_t j = 0; j < 16; ++j) run += a[j];
+                if (k + 32 < kTotStep) {
+#pragma unroll
+                    for (uint32_t j = 0; j < 16; ++j) a[j] = stage[k + 32 + j];
+                }
+#pragma unroll
+                for (uint32_t j = 0; j < 16; ++j) run += b[j];
+            }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -651,6 +684,9 @@ __device__ __noinline__ uint32_t finish_sums_exact(SelCommon& c, uint32_t want, 
         const bool near = (hi >= pp && hi <= pp * (1.0 + tc)) ||
                           (cut >= 2 && lo >= pp * (1.0 - tc) && lo <= pp * (1.0 + tc));
         if (!near) break;
+        // c.e and c.q, adjacent, stage the terms (both are formed again below)
+        static_assert(offsetof(SelCommon, q) == offsetof(SelCommon, e) + sizeof(SelCommon::e) &&
+                          2 * kMaxWant >= kTotStep, "the exact total's stage spans e and q");
         const double total = exact_row_total(src, c.e);
         for (uint32_t i = static_cast<uint32_t>(lane); i < want; i += 64)
             shortlist_terms(c, i, c.sorted[i], src.gmax, total, p);
