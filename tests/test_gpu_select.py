@@ -464,3 +464,30 @@ def test_cut_within_the_totals_rounding(env, oracle):
             want = oracle.sample_token(pen[i], p.temperature, p.top_p, p.top_k, u=p.uniform)
             assert want == expect, name
             assert int(tok[i]) == want, name
+
+
+def test_masked_vocabulary(env, oracle):
+    # A vocabulary masked to one value (-inf, or a large negative number) with fewer allowed
+    # tokens than the shortlist: the shortlist is filled by ties of the masked value. Where both
+    # of a masked entry's terms underflow to 0 it can be neither cut nor drawn, and the row is
+    # finished from the allowed tokens alone; at T = 50 the masked terms do not underflow and the
+    # ties go through the radix select.
+    torch, dev, t, sel = env
+    rng = np.random.default_rng(21)
+    cases = []
+    for fill in (-np.inf, -1e4, -1e30):
+        for allowed in (1, 10, 300):
+            row = np.full(V, np.float32(fill), np.float32)
+            idx = rng.choice(V, allowed, replace=False)
+            row[idx] = (rng.standard_normal(allowed) * 2).astype(np.float32)
+            for T, p, k in ((0.8, 0.9, 0), (0.8, 1.0, 0), (0.8, 0.9, 40), (1.3, 0.95, 256)):
+                cases.append((row, rp(t, T, p, k, float(rng.uniform()))))
+    row = np.full(V, np.float32(-1e4), np.float32)
+    row[rng.choice(V, 10, replace=False)] = 1.0
+    cases.append((row, rp(t, 50.0, 1.0, 0, 0.99)))  # masked q = exp(-200): drawable
+    for start in range(0, len(cases), 16):
+        chunk = cases[start:start + 16]
+        tok, _ = select_rows(env, np.stack([c[0] for c in chunk]), [c[1] for c in chunk])
+        for i, (row, p) in enumerate(chunk):
+            want = oracle.sample_token(row, p.temperature, p.top_p, p.top_k, u=p.uniform)
+            assert int(tok[i]) == want, (start + i, p.temperature, p.top_p, p.top_k)

@@ -88,7 +88,7 @@ __device__ __forceinline__ void finish_row(SelCommon& c, uint32_t want, const tw
         return;
     }
     block_sort_desc(c, want);
-    const uint32_t tok = finish_sampled(c, want, p, c.total, RowSrc{row_logits, vocab, c.gmax});
+    const uint32_t tok = finish_sampled(c, want, p, c.total, RowSrc{row_logits, vocab, c.gmax, want});
     if (tid == 0) *token_out = tok;
 }
 
@@ -748,7 +748,7 @@ __global__ __launch_bounds__(kLongThreads) void long_finish_kernel(LongArgs args
         if (sh.misc[2] == 0) break;
         if (wave == 0) {
             const double t = exact_row_total(RowSrc{b.logits + static_cast<size_t>(row) * b.stride, b.vocab,
-                                                    b.gmax[j]}, sh.e);
+                                                    b.gmax[j], 0u}, sh.e);
             if (lane == 0) sh.total = t;
         }
         __syncthreads();

@@ -109,18 +109,42 @@ __device__ __forceinline__ uint64_t block_select(KeyAt key_at, int per, uint32_t
     for (int shift = 56; shift >= 0; shift -= 8) {
         for (int i = tid; i < 256; i += NT) hist[i] = 0;
         __syncthreads();
-        auto count = [&](int e) {
-            const uint64_t k = key_at(e);
-            if (k != 0 && (k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+        // keys read from memory (the merge's overflow over whole candidate waves, where heavy
+        // ties are the usual cause): one wave's keys into the digit histogram, and where every
+        // counted key of the wave has the same digit, one atomic adds them all. Every lane of
+        // the wave calls.
+        auto count_key = [&](uint64_t k) {
+            const bool live = k != 0 && (k & mask) == prefix;
+            const uint32_t dg = static_cast<uint32_t>(k >> shift) & 255u;
+            const uint64_t m = __ballot(live);
+            if (m == 0) return;
+            const int first = __ffsll(static_cast<long long>(m)) - 1;
+            const uint32_t d0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(dg), first));
+            if (__ballot(live && dg == d0) == m) {
+                if (lane == first) atomicAdd(&hist[d0], static_cast<uint32_t>(__popcll(m)));
+            } else if (live) {
+                atomicAdd(&hist[dg], 1u);
+            }
         };
-        if constexpr (PER > 0) {
+        if constexpr (PER > 0) {  // keys in registers: a plain atomic per key
 #pragma unroll
             for (int e = 0; e < PER; ++e) {
                 if (e >= per) break;
-                count(e);
+                const uint64_t k = key_at(e);
+                if (k != 0 && (k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
             }
         } else {
-            for (int e = 0; e < per; ++e) count(e);
+            // eight keys requested before any is counted: key_at may read memory
+            constexpr int kB = 8;
+            int e = 0;
+            for (; e + kB <= per; e += kB) {
+                uint64_t kk[kB];
+#pragma unroll
+                for (int j = 0; j < kB; ++j) kk[j] = key_at(e + j);
+#pragma unroll
+                for (int j = 0; j < kB; ++j) count_key(kk[j]);
+            }
+            for (; e < per; ++e) count_key(key_at(e));
         }
         __syncthreads();
         if (wave == 0) {
@@ -428,6 +452,7 @@ struct RowSrc {
     const float* logits;
     uint32_t vocab;
     float gmax;
+    uint32_t nterms;  // the shortlist entries known by rank (c.sorted); the rest have zero terms
 };
 
 // How far (relative) a top-p prefix formed with this build's row total may lie from the
@@ -508,10 +533,17 @@ __device__ __forceinline__ uint32_t finish_sums(SelCommon& c, uint32_t want, con
 __device__ __noinline__ uint32_t finish_sums_exact(SelCommon& c, uint32_t want, const twd_row_params& p,
                                                    const RowSrc& src);
 
+// src.nterms <= want: only c.sorted[0..nterms) is known; the shortlist's other entries are ones
+// whose two terms are 0 (they can be neither cut nor drawn), so zero terms stand in for them.
 __device__ __forceinline__ uint32_t finish_sampled(SelCommon& c, uint32_t want, const twd_row_params& p,
                                                    double total, const RowSrc& src) {
     const uint32_t tid = threadIdx.x;
-    if (tid < want) shortlist_terms(c, tid, c.sorted[tid], src.gmax, total, p);
+    if (tid < src.nterms) {
+        shortlist_terms(c, tid, c.sorted[tid], src.gmax, total, p);
+    } else if (tid < want) {
+        c.e[tid] = 0.0;
+        c.q[tid] = 0.0;
+    }
     shortlist_pad(c, want);
     __syncthreads();
     return finish_sums(c, want, p, src);
@@ -688,8 +720,14 @@ __device__ __noinline__ uint32_t finish_sums_exact(SelCommon& c, uint32_t want, 
         static_assert(offsetof(SelCommon, q) == offsetof(SelCommon, e) + sizeof(SelCommon::e) &&
                           2 * kMaxWant >= kTotStep, "the exact total's stage spans e and q");
         const double total = exact_row_total(src, c.e);
-        for (uint32_t i = static_cast<uint32_t>(lane); i < want; i += 64)
-            shortlist_terms(c, i, c.sorted[i], src.gmax, total, p);
+        for (uint32_t i = static_cast<uint32_t>(lane); i < want; i += 64) {
+            if (i < src.nterms) {
+                shortlist_terms(c, i, c.sorted[i], src.gmax, total, p);
+            } else {
+                c.e[i] = 0.0;
+                c.q[i] = 0.0;
+            }
+        }
         for (uint32_t i = want + static_cast<uint32_t>(lane); i < ((want + kChunk - 1) & ~(kChunk - 1)); i += 64) {
             c.e[i] = 0.0;
             c.q[i] = 0.0;
@@ -756,7 +794,18 @@ struct RecStats {
     bool binned;   // false: every value in bin 0
     uint32_t bstar;
     bool degenerate;
+    double dead;   // a record whose maximum lies further than this below gm holds no live entry
 };
+
+// sampling.cpp:145,157: an entry l with l - max below -746 and (l - max) / T below -746 has both
+// terms 0 (exp(x) = 0 below -745.14): it adds nothing to any running sum and is never drawn
+// (the draw's threshold u * denom lies below denom), so which such entries fill a shortlist
+// cannot change the token. The distance below the row max past which an entry is so, for a row
+// at temperature T > 0.
+__device__ __forceinline__ double dead_distance(const twd_row_params& p) {
+    const double t = static_cast<double>(p.temperature);
+    return -746.0 * (t > 1.0 ? t : 1.0);
+}
 
 __device__ __forceinline__ uint32_t rec_bin(const RecStats& r, float x) {
     if (!r.binned) return 0u;
@@ -793,9 +842,11 @@ __device__ __forceinline__ double records_part(const double (&wsum)[PER], const 
 // The records as records_stats takes them: live[q] for a record that counts among the row's
 // wave maxima, wm[q] its maximum (-inf otherwise), and `flag` set when a record saw a NaN.
 template <bool kTotal = true, uint32_t PER = kSmPer>
+// dead: records whose maximum lies further below the row max than this (dead_distance; -inf:
+// none) are left out of the bins, so that b* and the candidates are those of the live entries.
 __device__ __forceinline__ RecStats records_stats(const bool (&live)[PER], const float (&wm)[PER],
                                                   uint32_t flag, const double (&wsum)[PER], float ref, uint32_t want,
-                                                  TopScratch& t, SelCommon& c) {
+                                                  TopScratch& t, SelCommon& c, double dead = -INFINITY) {
     constexpr int NT = kSmThreads;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     RecStats rs{};
@@ -823,9 +874,11 @@ __device__ __forceinline__ RecStats records_stats(const bool (&live)[PER], const
     const float span = gm - mn;
     rs.binned = __builtin_isfinite(gm) && __builtin_isfinite(mn) && span > 0.0f;
     rs.scale = rs.binned ? static_cast<float>(kBins - 1) / (span < kBinRange ? span : kBinRange) : 0.0f;
+    rs.dead = dead;
 #pragma unroll
     for (uint32_t q = 0; q < PER; ++q)
-        if (live[q]) atomicAdd(&t.hist[rec_bin(rs, wm[q]) * kReps + (lane & (kReps - 1))], 1u);
+        if (live[q] && !(static_cast<double>(wm[q]) - static_cast<double>(gm) < dead))
+            atomicAdd(&t.hist[rec_bin(rs, wm[q]) * kReps + (lane & (kReps - 1))], 1u);
     __syncthreads();
     if constexpr (kTotal) {
         double total = 0.0;
@@ -945,7 +998,7 @@ __device__ __forceinline__ void sample_merge_row_per(const twd_row_params& p, ui
     uint32_t nan = 0;
 #pragma unroll
     for (uint32_t q = 0; q < PER; ++q) nan |= wm[q] != wm[q] ? 1u : 0u;
-    const RecStats rs = records_stats<false, PER>(live, wm, nan, wsum, ref, want, sh.t, sh.c);
+    const RecStats rs = records_stats<false, PER>(live, wm, nan, wsum, ref, want, sh.t, sh.c, dead_distance(p));
     if (rs.degenerate) {  // sampling.cpp:116-118
         if (tid == 0) b.tokens[row] = TWD_TOKEN_DEGENERATE;
         return;
@@ -967,7 +1020,8 @@ __device__ __forceinline__ void sample_merge_row_per(const twd_row_params& p, ui
 #pragma unroll
         for (uint32_t q = 0; q < PER; ++q) {
             const uint32_t w = tid + NT * q;
-            const bool cand = live[q] && bin_of(wm[q]) <= bstar;
+            const bool cand = live[q] && bin_of(wm[q]) <= bstar &&
+                              !(static_cast<double>(wm[q]) - static_cast<double>(gm) < rs.dead);
             whole[q] = cand && (!have_aux || bin_of(fminf(aux_second(aux[q]), gm)) <= bstar);
             one[q] = cand && !whole[q];
             wid[q] = w;
@@ -1079,9 +1133,15 @@ __device__ __forceinline__ void sample_merge_row_per(const twd_row_params& p, ui
             sh.c.sorted[higher] = k;
             shortlist_terms(sh.c, higher, k, gm, total, p);
         }
+        // fewer survivors than want only when the rest of the row is dead (dead_distance): zero
+        // terms stand in for the dead entries that fill the reference's shortlist
+        if (static_cast<uint32_t>(tid) >= n && static_cast<uint32_t>(tid) < want) {
+            sh.c.e[tid] = 0.0;
+            sh.c.q[tid] = 0.0;
+        }
         shortlist_pad(sh.c, want);
         __syncthreads();
-        const uint32_t tok = finish_sums(sh.c, want, p, RowSrc{lg, b.vocab, gm});
+        const uint32_t tok = finish_sums(sh.c, want, p, RowSrc{lg, b.vocab, gm, min(n, want)});
         if (tid == 0) b.tokens[row] = tok;
         return;
     } else if (n <= static_cast<uint32_t>(NT)) {
@@ -1107,25 +1167,71 @@ __device__ __forceinline__ void sample_merge_row_per(const twd_row_params& p, ui
     } else {
         // overflow (heavy ties): a radix select over every candidate wave's rows in memory
         const uint32_t per_all = (nent_all + NT - 1) / NT;
+        // branch-free, so that a batch's loads issue back to back: an index past the list or
+        // the row reads a valid entry and is dropped
         auto cand_key = [&](int e) -> uint64_t {
             const uint32_t f = static_cast<uint32_t>(e) * NT + static_cast<uint32_t>(tid);
-            if (f >= nent_all) return 0ull;
-            const uint32_t rr = entry_row(f);
-            if (rr >= b.vocab) return 0ull;
-            const float x = lg[rr];
-            return bin_of(x) <= bstar ? rank_key(x, rr) : 0ull;
+            const uint32_t rr = entry_row(f < nent_all ? f : nent_all - 1);
+            const float x = lg[rr < b.vocab ? rr : b.vocab - 1];
+            return (f < nent_all && rr < b.vocab && bin_of(x) <= bstar) ? rank_key(x, rr) : 0ull;
         };
+        // Entries whose two terms, exp(l - max) and exp((l - max) / T), are both 0 can be neither
+        // cut nor drawn (sampling.cpp:145,157: they add 0 to every running sum, and the draw's
+        // threshold u * denom lies below denom). Which value is live is monotone in the value, so
+        // when fewer than want entries are live they are the shortlist's first entries and zero
+        // terms the rest, whichever tied entries fill it: a vocabulary masked to one value (-inf
+        // or a large negative number) then needs one pass over the candidates, not a radix select
+        // through every digit of the ties.
+        {
+            const double td = static_cast<double>(p.temperature), dgm = static_cast<double>(gm);
+            auto live_key = [&](uint32_t e) -> uint64_t {
+                const uint64_t k = cand_key(static_cast<int>(e));
+                if (k == 0) return 0ull;
+                const double d = static_cast<double>(rank_value(k)) - dgm;  // exp(x) = 0 below -745.14
+                return (d >= -746.0 || d / td >= -746.0) ? k : 0ull;
+            };
+            if (tid == 0) sh.c.misc[4] = 0;
+            __syncthreads();
+            uint32_t e = 0;
+            for (; e + 8 <= per_all; e += 8) {  // eight rows requested before any is kept
+                uint64_t kk[8];
+#pragma unroll
+                for (uint32_t j = 0; j < 8; ++j) kk[j] = live_key(e + j);
+#pragma unroll
+                for (uint32_t j = 0; j < 8; ++j) wave_put(kk[j] != 0, kk[j], &sh.c.misc[4], sh.c.top, want);
+            }
+            for (; e < per_all; ++e) {
+                const uint64_t k = live_key(e);
+                wave_put(k != 0, k, &sh.c.misc[4], sh.c.top, want);
+            }
+            __syncthreads();
+            const uint32_t nlive = sh.c.misc[4];  // every live entry counted, at most want kept
+            if (nlive < want) {
+                block_sort_desc(sh.c, nlive);
+                const uint32_t tok = finish_sampled(sh.c, want, p, total, RowSrc{lg, b.vocab, gm, nlive});
+                if (tid == 0) b.tokens[row] = tok;
+                return;
+            }
+        }
         const uint64_t thr = block_select<NT, 0>(cand_key, static_cast<int>(per_all), want, sh.t.hist, sh.c);
         if (tid == 0) sh.c.misc[4] = 0;
         __syncthreads();
-        for (uint32_t e = 0; e < per_all; ++e) {
+        uint32_t e = 0;
+        for (; e + 8 <= per_all; e += 8) {  // eight rows requested before any is kept
+            uint64_t kk[8];
+#pragma unroll
+            for (uint32_t j = 0; j < 8; ++j) kk[j] = cand_key(static_cast<int>(e + j));
+#pragma unroll
+            for (uint32_t j = 0; j < 8; ++j) wave_put(kk[j] != 0 && kk[j] >= thr, kk[j], &sh.c.misc[4], sh.c.top, want);
+        }
+        for (; e < per_all; ++e) {
             const uint64_t k = cand_key(static_cast<int>(e));
             wave_put(k != 0 && k >= thr, k, &sh.c.misc[4], sh.c.top, want);
         }
         __syncthreads();
         block_sort_desc(sh.c, want);
     }
-    const uint32_t tok = finish_sampled(sh.c, want, p, total, RowSrc{lg, b.vocab, gm});
+    const uint32_t tok = finish_sampled(sh.c, want, p, total, RowSrc{lg, b.vocab, gm, want});
     if (tid == 0) b.tokens[row] = tok;
 }
 
