@@ -491,3 +491,27 @@ def test_masked_vocabulary(env, oracle):
         for i, (row, p) in enumerate(chunk):
             want = oracle.sample_token(row, p.temperature, p.top_p, p.top_k, u=p.uniform)
             assert int(tok[i]) == want, (start + i, p.temperature, p.top_p, p.top_k)
+
+
+def test_nan_temperature_samples(env, oracle):
+    # sampling.cpp:97: only temperature <= 0 is greedy. A NaN temperature samples with NaN
+    # weights, and the token is the cut's last survivor; short, long (top_k > 256) and masked
+    # rows, through the wave-record path, and a masked row at an infinite temperature
+    torch, dev, t, sel = env
+    rng = np.random.default_rng(33)
+    nan = float("nan")
+    rows, params = [], []
+    for p, k in ((1.0, 0), (0.9, 40), (0.95, 0), (1.0, 300), (0.9, 1000)):
+        rows.append((rng.standard_normal(V) * 3).astype(np.float32))
+        params.append(rp(t, nan, p, k, float(rng.uniform())))
+    masked = np.full(V, -np.inf, np.float32)
+    masked[rng.choice(V, 10, replace=False)] = rng.standard_normal(10).astype(np.float32)
+    rows.append(masked)
+    params.append(rp(t, nan, 1.0, 0, 0.5))
+    # an infinite temperature: the -inf entries' weights are exp(-inf / inf) = NaN
+    rows.append(masked)
+    params.append(rp(t, float("inf"), 1.0, 0, 0.5))
+    tok, _ = select_rows(env, np.stack(rows), params)
+    for i, p in enumerate(params):
+        want = oracle.sample_token(rows[i], p.temperature, p.top_p, p.top_k, u=p.uniform)
+        assert int(tok[i]) == want, (i, p.top_p, p.top_k)

@@ -585,3 +585,19 @@ def test_row_total_rounding_bound():
             assert rel <= (n + 2048) * 2.0 ** -53
     # the tail rows reach a large part of the bound: it is not a loose estimate
     assert worst > 0.25
+
+
+def test_nan_temperature_samples(oracle, reference):
+    # sampling.cpp:97 takes the greedy branch only for temperature <= 0: a NaN temperature
+    # samples, every weight exp((l - max) / T) is NaN, no running sum reaches u * denom, and the
+    # token is the cut's last survivor (sampling.cpp:168)
+    rng = np.random.default_rng(8)
+    for trial in range(12):
+        n = int(rng.integers(50, 3000))
+        lg = (rng.standard_normal(n) * 3).astype(np.float32)
+        p = float(rng.choice([1.0, 0.9, 0.5]))
+        k = int(rng.choice([0, 1, 5, 40, 300]))
+        seed = int(rng.integers(0, 2**63))
+        got = oracle.sample_token(lg, float("nan"), p, k, seed=seed)
+        assert got == reference.sample_token(lg, float("nan"), p, k, seed)
+        assert got != int(np.argmax(lg)) or k == 1 or p == 0.5

@@ -205,7 +205,7 @@ void select_slice_kernel(SelectArgs args_by_value, SelectBufs b) {
         const uint32_t i = lo + tid + NT * e;
         return i < hi ? rank_key(v[e], i) : 0ull;
     };
-    const bool greedy = !(p.temperature > 0.0f);
+    const bool greedy = p.temperature <= 0.0f;  // sampling.cpp:97: a NaN temperature samples
     if (greedy) {
         // ---- sampling.cpp:97-104 ----
         uint64_t k = 0;
@@ -308,7 +308,7 @@ __global__ __launch_bounds__(kMergeThreads) void select_merge_kernel(SelectArgs 
     const twd_row_params p = args.p[row];
     const size_t o = static_cast<size_t>(row) * parts;
 
-    if (!(p.temperature > 0.0f)) {  // greedy: the best rank over the slices
+    if (p.temperature <= 0.0f) {  // greedy: the best rank over the slices
         if (tid < 64) {
             const uint64_t m = wave_max_u64(static_cast<uint32_t>(lane) < parts ? b.part_key[o + lane] : 0ull);
             if (tid == 0) b.tokens[row] = rank_index(m);
@@ -1202,7 +1202,7 @@ int launch_select(const SelectScratch& s, float* logits, uint32_t vocab, uint32_
     bool any_sampled = false, any_penalty = false;
     for (uint32_t r = 0; r < rows; ++r) {
         const twd_row_params& p = params[r];
-        any_sampled |= p.temperature > 0.0f;
+        any_sampled |= !(p.temperature <= 0.0f);
         if (p.repetition_penalty != 1.0f && p.history_len > 0) {
             any_penalty = true;
             records &= p.history_len <= kHashMaxIds;

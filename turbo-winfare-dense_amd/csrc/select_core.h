@@ -802,8 +802,11 @@ struct RecStats {
 // (the draw's threshold u * denom lies below denom), so which such entries fill a shortlist
 // cannot change the token. The distance below the row max past which an entry is so, for a row
 // at temperature T > 0.
+// A NaN or infinite temperature has none: its weights can be NaN (every one, or those of -inf
+// entries), and then the draw falls back to the cut's last survivor, whose identity matters.
 __device__ __forceinline__ double dead_distance(const twd_row_params& p) {
     const double t = static_cast<double>(p.temperature);
+    if (!(t < INFINITY)) return -INFINITY;
     return -746.0 * (t > 1.0 ? t : 1.0);
 }
 
@@ -951,7 +954,7 @@ __device__ __forceinline__ void sample_merge_row_per(const twd_row_params& p, ui
     // the exp2 table first, so that its load overlaps the records' (the first barrier publishes it)
     if (tid < 64) sh.c.exp2_tbl[tid] = kExp2Table[tid];
     // ---- the wave records: thread tid holds waves tid + NT * q
-    if (!(p.temperature > 0.0f)) {  // greedy: the best rank over the waves
+    if (p.temperature <= 0.0f) {  // greedy (sampling.cpp:97; a NaN temperature samples): the best rank over the waves
         uint64_t key[PER];
 #pragma unroll
         for (uint32_t q = 0; q < PER; ++q) {
@@ -1183,12 +1186,11 @@ __device__ __forceinline__ void sample_merge_row_per(const twd_row_params& p, ui
         // or a large negative number) then needs one pass over the candidates, not a radix select
         // through every digit of the ties.
         {
-            const double td = static_cast<double>(p.temperature), dgm = static_cast<double>(gm);
+            const double dead = dead_distance(p), dgm = static_cast<double>(gm);
             auto live_key = [&](uint32_t e) -> uint64_t {
                 const uint64_t k = cand_key(static_cast<int>(e));
                 if (k == 0) return 0ull;
-                const double d = static_cast<double>(rank_value(k)) - dgm;  // exp(x) = 0 below -745.14
-                return (d >= -746.0 || d / td >= -746.0) ? k : 0ull;
+                return static_cast<double>(rank_value(k)) - dgm < dead ? 0ull : k;
             };
             if (tid == 0) sh.c.misc[4] = 0;
             __syncthreads();

@@ -422,7 +422,7 @@ void long_free(LongScratch* l);
 
 // True for a row that the long path finishes: temperature > 0 and min(top_k, vocab) > kMaxWant.
 inline bool long_row(const twd_row_params& p, uint32_t vocab) {
-    return p.temperature > 0.0f && p.top_k > static_cast<int32_t>(kMaxWant) && vocab > kMaxWant;
+    return !(p.temperature <= 0.0f) && p.top_k > static_cast<int32_t>(kMaxWant) && vocab > kMaxWant;
 }
 
 // Enqueues the long path for those of `rows` rows that need it, after their penalised logits
